@@ -1,0 +1,61 @@
+/*
+ * mingru_hip.h -- C ABI of libmingru_hip.so, the MI355X (gfx950) kernels behind
+ * the MINGRU_SCAN seam of mingru_amd.
+ *
+ * Conventions (every entry point):
+ *   - pointers are device pointers to contiguous row-major fp32 (bf16 where
+ *     stated) tensors; sizes are int64 element counts;
+ *   - `ws`/`ws_bytes` is a caller-provided device workspace of at least the
+ *     size returned by the matching *_workspace_bytes query; its contents on
+ *     entry are irrelevant (the call clears what it needs);
+ *   - work is enqueued asynchronously on `stream`; nothing allocates, throws or
+ *     synchronises;
+ *   - the return value is a status: 0 ok, 1 invalid argument / outside the
+ *     envelope, 2 kernel launch failed, 3 workspace too small.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (chris-santiago/minGRU, paths relative to the repository root).
+ */
+#ifndef MINGRU_HIP_H
+#define MINGRU_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* mg_stream_t; /* == hipStream_t */
+
+/* ---- linear_scan: h_t = a_t h_{t-1} + b_t, (B, T, D) ------------------------
+ * Replaces linear_scan_fwd / linear_scan_bwd
+ * (src/mingru/triton_scans.py:1318-1334, 1392-1417; kernels :703-751, :962-1036)
+ * behind SCAN_IMPLS["linear_scan"] (src/mingru/triton_scans.py:2449-2465). */
+size_t mg_linear_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
+/* a, b -> A (running product), Bc (zero-start solution). */
+int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int64_t B, int64_t T,
+                       int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
+/* Grads gA, gB of (A, Bc) -> da, db.  A, Bc are the forward outputs. */
+int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
+                       const float* gA, const float* gB, float* da, float* db, int64_t B,
+                       int64_t T, int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
+
+/* ---- parallel_scan_log: log-space inputs, (B, T, D) and (B, T+1, D) ---------
+ * Replaces parallel_scan_log_fwd (src/mingru/triton_scans.py:1336-1357, kernel
+ * :754-821) and its eager-recompute backward (:1489-1552) behind
+ * SCAN_IMPLS["parallel_scan_log"] (:2467-2490). */
+size_t mg_log_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
+/* lc = log a (B,T,D), lv = [log h0, log b] (B,T+1,D) -> h (B,T,D). */
+int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,
+                    void* ws, size_t ws_bytes, mg_stream_t stream);
+/* h = forward output, gh = dL/dh -> dlc (B,T,D), dlv (B,T+1,D). */
+int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* gh, float* dlc,
+                    float* dlv, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    mg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINGRU_HIP_H */

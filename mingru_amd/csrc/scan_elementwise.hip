@@ -1,0 +1,676 @@
+// Elementwise (diagonal) scans: linear_scan and parallel_scan_log, fwd + bwd.
+//
+// Recurrence per column: h_t = a_t h_{t-1} + b_t.
+//   linear_scan       (reference src/mingru/min_gru.py:1454-1510): outputs the
+//                     running product A_t and the zero-start solution Bc_t.
+//   parallel_scan_log (reference src/mingru/min_gru.py:755-807): a = exp(lc),
+//                     b = exp(lv[t+1]), h_{-1} = exp(lv[0]); all terms positive,
+//                     so the linear-space fp32 recurrence has no cancellation.
+//
+// Work decomposition (one pass over HBM, decoupled look-back):
+//   * a lane group is (batch row, tile of 64*VEC consecutive columns); each
+//     thread owns VEC consecutive columns, so a wave's loads/stores along D
+//     are contiguous (1 KiB per row for VEC=4);
+//   * a workgroup of WAVES waves owns a chunk of WAVES*TSUB time steps; wave w
+//     owns TSUB consecutive steps and keeps all its inputs in registers;
+//   * per thread: local affine aggregate -> LDS combine across waves ->
+//     look-back over earlier chunks (wave 0) -> final recompute from the carry
+//     and streaming stores.
+// The backward is the same machinery run in reverse time order over the
+// adjoint recurrence y_t = a_t (g_t + y_{t+1}); forward values needed for the
+// gradient (A_{t-1}, Bc_{t-1} or h_{t-1}) are recomputed from one saved
+// forward output per thread sub-chunk boundary.
+#include "mg_common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int EW_WAVES = 4;
+constexpr int EW_TSUB_FWD = 16;
+constexpr int EW_TSUB_BWD = 8;
+
+// Affine map y -> p*y + l (NL independent offsets sharing one slope).
+template <int NL>
+struct Aff {
+  float p;
+  float l[NL];
+};
+
+template <int NL>
+__device__ __forceinline__ Aff<NL> aff_identity() {
+  Aff<NL> r;
+  r.p = 1.f;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) r.l[i] = 0.f;
+  return r;
+}
+
+// outer o inner: apply `inner` first, then `outer`.
+template <int NL>
+__device__ __forceinline__ Aff<NL> aff_compose(const Aff<NL>& inner, const Aff<NL>& outer) {
+  Aff<NL> r;
+  r.p = outer.p * inner.p;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) r.l[i] = fmaf(outer.p, inner.l[i], outer.l[i]);
+  return r;
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(float (&dst)[VEC], const float* __restrict__ src) {
+  if constexpr (VEC == 4) {
+    float4 v = *reinterpret_cast<const float4*>(src);
+    dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) dst[i] = src[i];
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(float* __restrict__ dst, const float (&src)[VEC]) {
+  if constexpr (VEC == 4) {
+    *reinterpret_cast<float4*>(dst) = make_float4(src[0], src[1], src[2], src[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) dst[i] = src[i];
+  }
+}
+
+struct EwGeom {
+  int64_t T, D;
+  int n_tiles, n_lg, n_chunks;
+};
+
+// Look-back storage: [lg][chunk][field][TILE] floats, TILE = 64*VEC.
+template <int NL, int VEC>
+__device__ __forceinline__ void lb_store(float* base, const EwGeom& g, int lg, int c, int lane,
+                                         const Aff<NL> (&x)[VEC]) {
+  constexpr int TILE = MG_WAVE * VEC;
+  float* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
+  float tmp[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) tmp[v] = x[v].p;
+  store_vec<VEC>(p, tmp);
+#pragma unroll
+  for (int f = 0; f < NL; ++f) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) tmp[v] = x[v].l[f];
+    store_vec<VEC>(p + (f + 1) * TILE, tmp);
+  }
+}
+
+template <int NL, int VEC>
+__device__ __forceinline__ void lb_load(const float* base, const EwGeom& g, int lg, int c,
+                                        int lane, Aff<NL> (&x)[VEC]) {
+  constexpr int TILE = MG_WAVE * VEC;
+  const float* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
+  float tmp[VEC];
+  load_vec<VEC>(tmp, p);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) x[v].p = tmp[v];
+#pragma unroll
+  for (int f = 0; f < NL; ++f) {
+    load_vec<VEC>(tmp, p + (f + 1) * TILE);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v].l[f] = tmp[v];
+  }
+}
+
+// Intra-workgroup combine + decoupled look-back.  On return `carry` holds, for
+// this thread's columns, the composition of everything before (forward) or
+// after (REVERSE) this thread's sub-chunk.  `seed` is the map applied at the
+// sequence start (forward) or end (reverse).
+template <int NL, int VEC, int WAVES, bool REVERSE>
+__device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL> (&seed)[VEC],
+                                         const EwGeom& g, int lg, int c, unsigned* header,
+                                         unsigned* flags, float* agg_data, float* incl_data,
+                                         Aff<NL> (&carry)[VEC]) {
+  constexpr int TILE = MG_WAVE * VEC;
+  constexpr int NF = NL + 1;
+  __shared__ float s_agg[WAVES][NF][TILE];
+  __shared__ float s_carry[NF][TILE];
+  const int lane = threadIdx.x & (MG_WAVE - 1);
+  const int w = threadIdx.x / MG_WAVE;
+
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    s_agg[w][0][lane * VEC + v] = loc[v].p;
+#pragma unroll
+    for (int f = 0; f < NL; ++f) s_agg[w][f + 1][lane * VEC + v] = loc[v].l[f];
+  }
+  __syncthreads();
+
+  auto wave_agg = [&](int j, int v) {
+    Aff<NL> r;
+    r.p = s_agg[j][0][lane * VEC + v];
+#pragma unroll
+    for (int f = 0; f < NL; ++f) r.l[f] = s_agg[j][f + 1][lane * VEC + v];
+    return r;
+  };
+
+  // Exclusive prefix of this wave inside the workgroup.
+  Aff<NL> ew[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    ew[v] = aff_identity<NL>();
+    if (!REVERSE) {
+      for (int j = 0; j < w; ++j) ew[v] = aff_compose(ew[v], wave_agg(j, v));
+    } else {
+      for (int j = WAVES - 1; j > w; --j) ew[v] = aff_compose(ew[v], wave_agg(j, v));
+    }
+  }
+
+  if (w == 0) {
+    Aff<NL> G[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      G[v] = aff_identity<NL>();
+      if (!REVERSE) {
+        for (int j = 0; j < WAVES; ++j) G[v] = aff_compose(G[v], wave_agg(j, v));
+      } else {
+        for (int j = WAVES - 1; j >= 0; --j) G[v] = aff_compose(G[v], wave_agg(j, v));
+      }
+    }
+    const int first = REVERSE ? g.n_chunks - 1 : 0;
+    const int dir = REVERSE ? 1 : -1;  // step towards predecessors
+    Aff<NL> E[VEC];
+    if (c == first) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) E[v] = seed[v];
+    } else {
+      lb_store<NL, VEC>(agg_data, g, lg, c, lane, G);
+      mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_AGG);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) E[v] = aff_identity<NL>();
+      for (int j = c + dir;; j += dir) {
+        unsigned f = mg_wait_flag(&flags[lg * g.n_chunks + j], header);
+        if (f == MG_FLAG_NONE) break;  // spin limit: error already recorded
+        Aff<NL> X[VEC];
+        lb_load<NL, VEC>(f == MG_FLAG_INCL ? incl_data : agg_data, g, lg, j, lane, X);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
+        if (f == MG_FLAG_INCL) break;
+        if (j == first) break;  // defensive: the first chunk always publishes INCL
+      }
+    }
+    Aff<NL> I[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) I[v] = aff_compose(E[v], G[v]);
+    lb_store<NL, VEC>(incl_data, g, lg, c, lane, I);
+    mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_INCL);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      s_carry[0][lane * VEC + v] = E[v].p;
+#pragma unroll
+      for (int f = 0; f < NL; ++f) s_carry[f + 1][lane * VEC + v] = E[v].l[f];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    Aff<NL> C;
+    C.p = s_carry[0][lane * VEC + v];
+#pragma unroll
+    for (int f = 0; f < NL; ++f) C.l[f] = s_carry[f + 1][lane * VEC + v];
+    carry[v] = aff_compose(C, ew[v]);
+  }
+}
+
+struct EwThread {
+  int lane, w, c, lg, bb;
+  int64_t col;
+  bool col_ok;
+};
+
+template <int VEC, int TSUB, int WAVES, bool REVERSE>
+__device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header) {
+  EwThread th;
+  unsigned ticket = mg_take_ticket(header);
+  th.lane = threadIdx.x & (MG_WAVE - 1);
+  th.w = threadIdx.x / MG_WAVE;
+  int k = (int)(ticket / (unsigned)g.n_lg);
+  th.lg = (int)(ticket - (unsigned)k * (unsigned)g.n_lg);
+  th.c = REVERSE ? g.n_chunks - 1 - k : k;
+  th.bb = th.lg / g.n_tiles;
+  int tile = th.lg - th.bb * g.n_tiles;
+  th.col = (int64_t)tile * (MG_WAVE * VEC) + th.lane * VEC;
+  th.col_ok = th.col < g.D;
+  return th;
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  LOG=false: x0=a, x1=b -> out0=A, out1=Bc.
+//           LOG=true : x0=lc (B,T,D), x1=lv (B,T+1,D) -> out0=h.
+// ---------------------------------------------------------------------------
+template <int VEC, int TSUB, int WAVES, bool LOG>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
+    const float* __restrict__ x0, const float* __restrict__ x1, float* __restrict__ out0,
+    float* __restrict__ out1, EwGeom g, unsigned* header, unsigned* flags, float* agg_data,
+    float* incl_data) {
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  float av[TSUB][VEC], bv[TSUB][VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      load_vec<VEC>(av[s], x0 + (th.bb * T + t) * D + th.col);
+      if (LOG) {
+        load_vec<VEC>(bv[s], x1 + (th.bb * (T + 1) + t + 1) * D + th.col);
+      } else {
+        load_vec<VEC>(bv[s], x1 + (th.bb * T + t) * D + th.col);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = LOG ? 0.f : 1.f;  // exp(0) = 1 below
+        bv[s][v] = LOG ? -INFINITY : 0.f;
+      }
+    }
+  }
+  if (LOG) {
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = expf(av[s][v]);
+        bv[s][v] = expf(bv[s][v]);
+      }
+  }
+
+  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    loc[v] = aff_identity<1>();
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
+      loc[v].p *= av[s][v];
+    }
+    seed[v] = aff_identity<1>();
+  }
+  if (LOG && th.c == 0 && th.w == 0) {
+    float h0[VEC];
+    if (th.col_ok) {
+      load_vec<VEC>(h0, x1 + (th.bb * (T + 1)) * D + th.col);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) h0[v] = -INFINITY;
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) seed[v].l[0] = expf(h0[v]);
+  }
+  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+                                 carry);
+
+  float P[VEC], L[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    P[v] = carry[v].p;
+    L[v] = carry[v].l[0];
+  }
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      L[v] = fmaf(av[s][v], L[v], bv[s][v]);
+      P[v] *= av[s][v];
+    }
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      if (LOG) {
+        store_vec<VEC>(out0 + off, L);
+      } else {
+        store_vec<VEC>(out0 + off, P);
+        store_vec<VEC>(out1 + off, L);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward of linear_scan.  Inputs a, b, saved A, Bc and grads gA, gB;
+// outputs da, db.  Adjoint: x_t = g_t + a_{t+1} x_{t+1} for both streams;
+// da_t = xA_t A_{t-1} + xB_t Bc_{t-1}, db_t = xB_t.
+// ---------------------------------------------------------------------------
+template <int VEC, int TSUB, int WAVES>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ A,
+    const float* __restrict__ Bc, const float* __restrict__ gA, const float* __restrict__ gB,
+    float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header, unsigned* flags,
+    float* agg_data, float* incl_data) {
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  float av[TSUB][VEC], bv[TSUB][VEC], xa[TSUB][VEC], xb[TSUB][VEC];
+  float Ap[VEC], Bp[VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      load_vec<VEC>(av[s], a + off);
+      load_vec<VEC>(bv[s], b + off);
+      load_vec<VEC>(xa[s], gA + off);
+      load_vec<VEC>(xb[s], gB + off);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = 1.f;
+        bv[s][v] = 0.f;
+        xa[s][v] = 0.f;
+        xb[s][v] = 0.f;
+      }
+    }
+  }
+  if (th.col_ok && t0 > 0 && t0 <= T) {
+    const int64_t off = (th.bb * T + t0 - 1) * D + th.col;
+    load_vec<VEC>(Ap, A + off);
+    load_vec<VEC>(Bp, Bc + off);
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      Ap[v] = 1.f;
+      Bp[v] = 0.f;
+    }
+  }
+
+  Aff<2> loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    loc[v] = aff_identity<2>();
+#pragma unroll
+    for (int s = TSUB - 1; s >= 0; --s) {
+      const float al = av[s][v];
+      loc[v].l[0] = al * (xa[s][v] + loc[v].l[0]);
+      loc[v].l[1] = al * (xb[s][v] + loc[v].l[1]);
+      loc[v].p *= al;
+    }
+    seed[v] = aff_identity<2>();
+  }
+  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+                                carry);
+
+  float ya[VEC], yb[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    ya[v] = carry[v].l[0];
+    yb[v] = carry[v].l[1];
+  }
+#pragma unroll
+  for (int s = TSUB - 1; s >= 0; --s) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      xa[s][v] += ya[v];
+      xb[s][v] += yb[v];
+      ya[v] = av[s][v] * xa[s][v];
+      yb[v] = av[s][v] * xb[s][v];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float d_a[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      d_a[v] = fmaf(xa[s][v], Ap[v], xb[s][v] * Bp[v]);
+      Bp[v] = fmaf(av[s][v], Bp[v], bv[s][v]);
+      Ap[v] *= av[s][v];
+    }
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      store_vec<VEC>(da + off, d_a);
+      store_vec<VEC>(db + off, xb[s]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward of parallel_scan_log.  Inputs lc, lv, saved h, grad gh; outputs
+// dlc (B,T,D) and dlv (B,T+1,D).
+//   x_t = gh_t + a_{t+1} x_{t+1};  dlc_t = x_t a_t h_{t-1};  dlv_{t+1} = x_t b_t;
+//   dlv_0 = a_0 x_0 h_{-1}.
+// ---------------------------------------------------------------------------
+template <int VEC, int TSUB, int WAVES>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
+    const float* __restrict__ lc, const float* __restrict__ lv, const float* __restrict__ h,
+    const float* __restrict__ gh, float* __restrict__ dlc, float* __restrict__ dlv, EwGeom g,
+    unsigned* header, unsigned* flags, float* agg_data, float* incl_data) {
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  float av[TSUB][VEC], bv[TSUB][VEC], x[TSUB][VEC];
+  float hp[VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      load_vec<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
+      load_vec<VEC>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+      load_vec<VEC>(x[s], gh + (th.bb * T + t) * D + th.col);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = 0.f;
+        bv[s][v] = -INFINITY;
+        x[s][v] = 0.f;
+      }
+    }
+  }
+  const bool first_sub = (t0 == 0);
+  if (th.col_ok && t0 <= T) {
+    if (first_sub) {
+      load_vec<VEC>(hp, lv + (th.bb * (T + 1)) * D + th.col);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) hp[v] = expf(hp[v]);
+    } else {
+      load_vec<VEC>(hp, h + (th.bb * T + t0 - 1) * D + th.col);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) hp[v] = 0.f;
+  }
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      av[s][v] = expf(av[s][v]);
+      bv[s][v] = expf(bv[s][v]);
+    }
+
+  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    loc[v] = aff_identity<1>();
+#pragma unroll
+    for (int s = TSUB - 1; s >= 0; --s) {
+      loc[v].l[0] = av[s][v] * (x[s][v] + loc[v].l[0]);
+      loc[v].p *= av[s][v];
+    }
+    seed[v] = aff_identity<1>();
+  }
+  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+                                carry);
+
+  float y[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
+#pragma unroll
+  for (int s = TSUB - 1; s >= 0; --s) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      x[s][v] += y[v];
+      y[v] = av[s][v] * x[s][v];
+    }
+  }
+  if (first_sub && th.col_ok) {
+    float d0[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) d0[v] = y[v] * hp[v];
+    store_vec<VEC>(dlv + (th.bb * (T + 1)) * D + th.col, d0);
+  }
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float d_c[VEC], d_v[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      d_c[v] = x[s][v] * av[s][v] * hp[v];
+      d_v[v] = x[s][v] * bv[s][v];
+      hp[v] = fmaf(av[s][v], hp[v], bv[s][v]);
+    }
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      store_vec<VEC>(dlc + (th.bb * T + t) * D + th.col, d_c);
+      store_vec<VEC>(dlv + (th.bb * (T + 1) + t + 1) * D + th.col, d_v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+struct EwPlan {
+  EwGeom g;
+  int vec;
+  int tsub;
+  size_t flag_words;  // header + flags, in 32-bit words
+  size_t agg_off, incl_off, total;
+};
+
+EwPlan ew_plan(int64_t B, int64_t T, int64_t D, int vec, int tsub, int nl) {
+  EwPlan p;
+  p.vec = vec;
+  p.tsub = tsub;
+  p.g.T = T;
+  p.g.D = D;
+  const int tile = MG_WAVE * vec;
+  p.g.n_tiles = (int)((D + tile - 1) / tile);
+  p.g.n_lg = (int)(B * p.g.n_tiles);
+  const int64_t cl = (int64_t)EW_WAVES * tsub;
+  p.g.n_chunks = (int)((T + cl - 1) / cl);
+  const size_t n = (size_t)p.g.n_lg * p.g.n_chunks;
+  p.flag_words = MG_HEADER_BYTES / 4 + mg_align_up(n, 64);
+  const size_t data_bytes = n * (size_t)(nl + 1) * tile * sizeof(float);
+  p.agg_off = p.flag_words * 4;
+  p.incl_off = p.agg_off + mg_align_up(data_bytes, 256);
+  p.total = p.incl_off + mg_align_up(data_bytes, 256);
+  return p;
+}
+
+bool is_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool geometry_ok(int64_t B, int64_t T, int64_t D) {
+  if (B <= 0 || T <= 0 || D <= 0) return false;
+  // Ticket space and look-back indices are 32-bit.
+  const int64_t tiles = (D + MG_WAVE - 1) / MG_WAVE;
+  const int64_t lgs = B * tiles;
+  const int64_t chunks = (T + EW_WAVES - 1) / EW_WAVES;
+  return lgs < (1ll << 30) && chunks < (1ll << 30) && lgs * chunks < (1ll << 31);
+}
+
+template <typename Kernel, typename... Args>
+int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... args) {
+  int rc = mg_clear(ws, p.flag_words, stream);
+  if (rc != MG_OK) return rc;
+  unsigned* header = (unsigned*)ws;
+  unsigned* flags = header + MG_HEADER_BYTES / 4;
+  float* agg = (float*)((char*)ws + p.agg_off);
+  float* incl = (float*)((char*)ws + p.incl_off);
+  const unsigned grid = (unsigned)p.g.n_lg * (unsigned)p.g.n_chunks;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(MG_WAVE * EW_WAVES), 0, stream, args..., p.g, header,
+                     flags, agg, incl);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
+  size_t m = 0;
+  for (int vec : {1, 4}) {
+    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_FWD, 1).total);
+    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_BWD, 2).total);
+  }
+  return m;
+}
+
+}  // namespace
+
+__global__ void mg_clear_kernel(unsigned* p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+extern "C" {
+
+size_t mg_linear_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
+  return ew_ws_bytes(B, T, D);
+}
+
+size_t mg_log_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
+  return ew_ws_bytes(B, T, D);
+}
+
+int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int64_t B, int64_t T,
+                       int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!a || !b || !A || !Bc || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
+                  is_aligned16(Bc);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  if (v4)
+    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES, false>, p, ws, stream, a, b, A, Bc);
+  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES, false>, p, ws, stream, a, b, A, Bc);
+}
+
+int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
+                       const float* gA, const float* gB, float* da, float* db, int64_t B,
+                       int64_t T, int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!a || !b || !A || !Bc || !gA || !gB || !da || !db || !ws || !geometry_ok(B, T, D))
+    return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
+                  is_aligned16(Bc) && is_aligned16(gA) && is_aligned16(gB) &&
+                  is_aligned16(da) && is_aligned16(db);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, 2);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  if (v4)
+    return ew_launch(linear_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, a, b, A, Bc, gA,
+                     gB, da, db);
+  return ew_launch(linear_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, a, b, A, Bc, gA,
+                   gB, da, db);
+}
+
+int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,
+                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!lc || !lv || !h || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  float* none = nullptr;
+  if (v4)
+    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES, true>, p, ws, stream, lc, lv, h,
+                     none);
+  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES, true>, p, ws, stream, lc, lv, h, none);
+}
+
+int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* gh, float* dlc,
+                    float* dlv, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    hipStream_t stream) {
+  if (!lc || !lv || !h || !gh || !dlc || !dlv || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h) &&
+                  is_aligned16(gh) && is_aligned16(dlc) && is_aligned16(dlv);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  if (v4)
+    return ew_launch(log_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, lc, lv, h, gh, dlc,
+                     dlv);
+  return ew_launch(log_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, lc, lv, h, gh, dlc,
+                   dlv);
+}
+
+}  // extern "C"

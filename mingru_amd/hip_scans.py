@@ -1,0 +1,245 @@
+"""HIP backend for the ``MINGRU_SCAN`` seam (replaces the reference's ``triton_scans``).
+
+Backend contract (reference ``src/mingru/triton_scans.py:166-177, 460,
+2403-2590``), kept name for name so the seam in :mod:`mingru_amd.min_gru`
+and code written against the reference work unchanged:
+
+* ``available() -> True | str`` -- ``True`` when a gfx950 GPU is visible and
+  ``libmingru_hip.so`` loads; otherwise the reason.
+* ``ScanFallback`` -- the one exception a decline raises (out-of-envelope
+  shape or dtype, launch failure).  The seam turns it into a warn-once eager
+  fallback under ``auto`` and a ``RuntimeError`` under the forcing mode.
+* ``SCAN_IMPLS[name](*args)`` -- same signature and return as the eager scan
+  ``name``, differentiable through ``torch.autograd.Function`` wrappers whose
+  forward and backward are single C-ABI calls.
+* ``angle_scan_impl`` and ``delta_scan_impl`` -- module fast paths for
+  ``RotationMinGRU``/``GivensMinGRU`` and ``DeltaMinGRU``.
+
+Launches are asynchronous on torch's current stream; outputs and workspaces
+come from torch's caching allocator on the input's device.  Double backward
+is not supported (``once_differentiable``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch.autograd.function import once_differentiable
+
+__all__ = ["available", "ScanFallback", "SCAN_IMPLS", "angle_scan_impl", "delta_scan_impl"]
+
+
+class ScanFallback(Exception):
+    """The HIP path declines this call; the seam falls back to eager (or raises)."""
+
+
+# Block sizes the matrix kernels are compiled for (k x k transitions, k x v
+# injections).  Same set as the reference's envelope
+# (``src/mingru/triton_scans.py:183``) minus k = 16, whose 256-float block
+# product does not fit one thread's registers.
+_AFFINE_K = frozenset({1, 2, 4, 8})
+_AFFINE_V = frozenset({1, 2, 4, 8, 16})
+
+# Angle-fused kernel: block sizes and rotation-count limit.
+_ANGLE_K = frozenset({2, 4, 8})
+_ANGLE_MAX_ROT = 64
+
+# DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``):
+# d_k = d_v in this set, chunk_size <= 64, nh * chunk_size <= 64.
+_DELTA_DK = frozenset({16, 32, 64})
+_DELTA_MAX_CHUNK = 64
+_DELTA_MAX_MICROSTEPS = 64
+
+_SUPPORTED_ARCH = "gfx950"
+
+
+def _lib():
+    from . import _native
+
+    return _native.load()
+
+
+_avail_cache: dict = {}
+
+
+def available() -> bool | str:
+    """``True`` if the HIP kernels can run in this process, else the reason."""
+    if not torch.cuda.is_available():
+        return "CUDA/HIP device not available"
+    if torch.version.hip is None:
+        return "torch is not a ROCm build"
+    try:
+        _lib()
+    except (ImportError, OSError) as exc:
+        return f"HIP library not loadable: {exc}"
+    dev = torch.cuda.current_device()
+    arch = _avail_cache.get(dev)
+    if arch is None:
+        arch = torch.cuda.get_device_properties(dev).gcnArchName.split(":")[0]
+        _avail_cache[dev] = arch
+    if arch != _SUPPORTED_ARCH:
+        return f"HIP kernels are built for {_SUPPORTED_ARCH} (device is {arch})"
+    return True
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _call(fn_name: str, *args) -> None:
+    from . import _native
+
+    rc = getattr(_lib(), fn_name)(*args)
+    _native.check(rc, fn_name)
+
+
+def _as_f32(*ts: torch.Tensor):
+    """Contiguous fp32 views of the inputs (half types are upcast; fp64 declines)."""
+    out = []
+    for t in ts:
+        if t.dtype == torch.float64:
+            raise ScanFallback("HIP scans compute in fp32; float64 inputs stay on the eager path")
+        if not t.dtype.is_floating_point:
+            raise ScanFallback(f"HIP scans need floating-point inputs (got {t.dtype})")
+        out.append(t.to(torch.float32).contiguous())
+    return out
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ScanFallback("HIP scans need GPU tensors")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ScanFallback("HIP scan inputs live on different devices")
+
+
+def _funnel(what: str, fn, *args):
+    """Run ``fn`` and turn any launch-side failure into ``ScanFallback``."""
+    try:
+        return fn(*args)
+    except ScanFallback:
+        raise
+    except Exception as exc:  # noqa: BLE001 - every launch failure becomes a decline
+        raise ScanFallback(f"{what} HIP kernel failed: {exc}") from exc
+
+
+# ---------------------------------------------------------------------------
+# linear_scan
+# ---------------------------------------------------------------------------
+
+
+class _LinearScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b):
+        out_dtype = a.dtype
+        a32, b32 = _as_f32(a, b)
+        Bn, T, D = a32.shape
+        A = torch.empty_like(a32)
+        Bc = torch.empty_like(a32)
+        ws = _workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        _call("mg_linear_scan_fwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), Bn, T, D,
+              _ptr(ws), ws.numel(), _stream(a32))
+        ctx.save_for_backward(a32, b32, A, Bc)
+        ctx.out_dtype = out_dtype
+        if out_dtype != torch.float32:
+            return A.to(out_dtype), Bc.to(out_dtype)
+        return A, Bc
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gA, gB):
+        a32, b32, A, Bc = ctx.saved_tensors
+        Bn, T, D = a32.shape
+        gA32, gB32 = _as_f32(gA, gB)
+        da = torch.empty_like(a32)
+        db = torch.empty_like(a32)
+        ws = _workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        _call("mg_linear_scan_bwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), _ptr(gA32),
+              _ptr(gB32), _ptr(da), _ptr(db), Bn, T, D, _ptr(ws), ws.numel(), _stream(a32))
+        return da.to(ctx.out_dtype), db.to(ctx.out_dtype)
+
+
+def _linear_scan_impl(a: torch.Tensor, b: torch.Tensor):
+    """``SCAN_IMPLS['linear_scan']``: same contract as the eager ``linear_scan``."""
+    if a.ndim != 3 or b.ndim != 3 or a.shape != b.shape:
+        raise ScanFallback(
+            f"linear_scan (a={tuple(a.shape)}, b={tuple(b.shape)}) outside the HIP envelope: "
+            "need matching (B, T, D) a and b"
+        )
+    _same_device(a, b)
+    if a.numel() == 0:
+        return a.new_empty(a.shape), b.new_empty(b.shape)
+    return _funnel("linear_scan", _LinearScanFn.apply, a, b)
+
+
+# ---------------------------------------------------------------------------
+# parallel_scan_log
+# ---------------------------------------------------------------------------
+
+
+class _LogScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, log_coeffs, log_values):
+        out_dtype = log_coeffs.dtype
+        lc, lv = _as_f32(log_coeffs, log_values)
+        Bn, T, D = lc.shape
+        h = torch.empty_like(lc)
+        ws = _workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        _call("mg_log_scan_fwd", _ptr(lc), _ptr(lv), _ptr(h), Bn, T, D, _ptr(ws), ws.numel(),
+              _stream(lc))
+        ctx.save_for_backward(lc, lv, h)
+        ctx.out_dtype = out_dtype
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        lc, lv, h = ctx.saved_tensors
+        Bn, T, D = lc.shape
+        (gh32,) = _as_f32(gh)
+        dlc = torch.empty_like(lc)
+        dlv = torch.empty_like(lv)
+        ws = _workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        _call("mg_log_scan_bwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(gh32), _ptr(dlc), _ptr(dlv),
+              Bn, T, D, _ptr(ws), ws.numel(), _stream(lc))
+        return dlc.to(ctx.out_dtype), dlv.to(ctx.out_dtype)
+
+
+def _parallel_scan_log_impl(log_coeffs: torch.Tensor, log_values: torch.Tensor):
+    """``SCAN_IMPLS['parallel_scan_log']``: same contract as the eager op."""
+    if (
+        log_coeffs.ndim != 3
+        or log_values.ndim != 3
+        or log_values.shape
+        != (log_coeffs.shape[0], log_coeffs.shape[1] + 1, log_coeffs.shape[2])
+    ):
+        raise ScanFallback(
+            f"parallel_scan_log (log_coeffs={tuple(log_coeffs.shape)}, "
+            f"log_values={tuple(log_values.shape)}) outside the HIP envelope: need (B, T, D) "
+            "log_coeffs and (B, T+1, D) log_values"
+        )
+    _same_device(log_coeffs, log_values)
+    if log_coeffs.numel() == 0:
+        return log_coeffs.new_empty(log_coeffs.shape)
+    return _funnel("parallel_scan_log", _LogScanFn.apply, log_coeffs, log_values)
+
+
+SCAN_IMPLS: dict = {
+    "parallel_scan_log": _parallel_scan_log_impl,
+    "linear_scan": _linear_scan_impl,
+}
