@@ -54,6 +54,22 @@ int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const floa
                     float* dlv, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
                     mg_stream_t stream);
 
+/* ---- matrix_scan / matrix_affine_scan: k x k blocks, (B, T, n, k, k) -------
+ * Replaces affine_scan_fwd / affine_scan_bwd (src/mingru/triton_scans.py:
+ * 1293-1316, 1359-1390; kernels :630-700, :824-959) behind
+ * SCAN_IMPLS["matrix_scan"] / ["matrix_affine_scan"] (:2492-2563).
+ * k in {1,2,4,8}, v in {1,2,4,8,16}; pointers 16-byte aligned. */
+size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v);
+/* A (B,T,n,k,k), Bm (B,T,n,k,v) -> Abar = A_t..A_1, Bbar (zero-start solution). */
+int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,
+                       int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
+                       mg_stream_t stream);
+/* Grads of (Abar, Bbar) -> dA, dBm.  Abar, Bbar are the forward outputs. */
+int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const float* Bbar,
+                       const float* gAbar, const float* gBbar, float* dA, float* dBm, int64_t B,
+                       int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
+                       mg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,14 +27,11 @@ __all__ = [*_min_gru_all, "__version__"]
 
 
 def __getattr__(name: str) -> object:
-    if name in _BACKEND_EXPORTS:
-        from . import hip_scans
+    if name in _BACKEND_EXPORTS or name == "hip_scans":
+        import importlib
 
-        return getattr(hip_scans, name)
-    if name == "hip_scans":
-        from . import hip_scans
-
-        return hip_scans
+        backend = importlib.import_module(f"{__name__}.hip_scans")
+        return backend if name == "hip_scans" else getattr(backend, name)
     raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
 
 

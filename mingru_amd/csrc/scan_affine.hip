@@ -1,0 +1,716 @@
+// Block-matrix affine scans: matrix_scan (k=2, v=1) and matrix_affine_scan
+// (k in {1,2,4,8}, v in {1,2,4,8,16}), fwd + bwd.
+//
+// Recurrence per plane (reference src/mingru/min_gru.py:1513-1655):
+//   Abar_t = A_t Abar_{t-1},  Bbar_t = A_t Bbar_{t-1} + B_t,  Abar_0 = I, Bbar_0 = 0.
+// Adjoint (reference kernel src/mingru/triton_scans.py:824-959 derives the same):
+//   X_t = G_t + A_{t+1}^T X_{t+1}       (for both the Abar and Bbar streams)
+//   dA_t = XA_t Abar_{t-1}^T + XB_t Bbar_{t-1}^T,   dB_t = XB_t.
+//
+// One thread owns one plane (b, i) and keeps the k x k block product in
+// registers.  Planes of one (b, t) are contiguous in memory, so a wave reads
+// 64 consecutive planes per time step (1 KiB for k = 2).  Time is split into
+// chunks of WAVES*TSUB steps per workgroup; chunks are chained with the same
+// decoupled look-back as the elementwise scans, carrying the affine map
+// (P, L): S -> P S + L of each chunk.  Inside a workgroup the waves combine
+// their sub-chunk maps through one LDS buffer in time order.
+//
+// For k <= 2 every input of the thread's sub-chunk stays in registers between
+// the aggregate pass and the final pass (one HBM read).  For k >= 4 the
+// register file cannot hold them: inputs are re-read for the final pass and
+// the backward reads the saved forward outputs Abar_{t-1}, Bbar_{t-1}.
+#include "mg_common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int AF_WAVES = 4;
+
+template <int K>
+constexpr int af_tsub() {
+  return K == 1 ? 16 : (K == 2 ? 8 : 8);
+}
+
+template <int K>
+constexpr bool af_hold() {
+  return K <= 2;
+}
+
+// Affine map on K x W matrices: S -> P S + L.
+template <int K, int W>
+struct AffM {
+  float P[K][K];
+  float L[K][W];
+};
+
+template <int K, int W>
+__device__ __forceinline__ void affm_identity(AffM<K, W>& r) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) r.P[i][j] = (i == j) ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < W; ++j) r.L[i][j] = 0.f;
+  }
+}
+
+// r = outer o inner (apply inner first).  r may alias neither argument.
+template <int K, int W>
+__device__ __forceinline__ void affm_compose(const AffM<K, W>& inner, const AffM<K, W>& outer,
+                                             AffM<K, W>& r) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int m = 0; m < K; ++m) acc = fmaf(outer.P[i][m], inner.P[m][j], acc);
+      r.P[i][j] = acc;
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      float acc = outer.L[i][j];
+#pragma unroll
+      for (int m = 0; m < K; ++m) acc = fmaf(outer.P[i][m], inner.L[m][j], acc);
+      r.L[i][j] = acc;
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void ld(float* dst, const float* __restrict__ src) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      float4 v = *reinterpret_cast<const float4*>(src + i);
+      dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+    }
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      float2 v = *reinterpret_cast<const float2*>(src + i);
+      dst[i] = v.x; dst[i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = src[i];
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void st(float* __restrict__ dst, const float* src) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<float4*>(dst + i) = make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]);
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2)
+      *reinterpret_cast<float2*>(dst + i) = make_float2(src[i], src[i + 1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = src[i];
+  }
+}
+
+struct AfGeom {
+  int64_t T, n;
+  int n_tiles, n_lg, n_chunks;
+};
+
+// Look-back storage: [lg][chunk][field][64] floats.
+template <int K, int W>
+__device__ __forceinline__ void af_lb_store(float* base, const AfGeom& g, int lg, int c, int lane,
+                                            const AffM<K, W>& x) {
+  constexpr int NF = K * K + K * W;
+  float* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
+  const float* f = &x.P[0][0];
+#pragma unroll
+  for (int i = 0; i < K * K; ++i) p[i * MG_WAVE] = f[i];
+  const float* l = &x.L[0][0];
+#pragma unroll
+  for (int i = 0; i < K * W; ++i) p[(K * K + i) * MG_WAVE] = l[i];
+}
+
+template <int K, int W>
+__device__ __forceinline__ void af_lb_load(const float* base, const AfGeom& g, int lg, int c,
+                                           int lane, AffM<K, W>& x) {
+  constexpr int NF = K * K + K * W;
+  const float* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
+  float* f = &x.P[0][0];
+#pragma unroll
+  for (int i = 0; i < K * K; ++i) f[i] = p[i * MG_WAVE];
+  float* l = &x.L[0][0];
+#pragma unroll
+  for (int i = 0; i < K * W; ++i) l[i] = p[(K * K + i) * MG_WAVE];
+}
+
+template <int K, int W>
+__device__ __forceinline__ void lds_put(float* s, int lane, const AffM<K, W>& x) {
+  const float* f = &x.P[0][0];
+#pragma unroll
+  for (int i = 0; i < K * K; ++i) s[i * MG_WAVE + lane] = f[i];
+  const float* l = &x.L[0][0];
+#pragma unroll
+  for (int i = 0; i < K * W; ++i) s[(K * K + i) * MG_WAVE + lane] = l[i];
+}
+
+template <int K, int W>
+__device__ __forceinline__ void lds_get(const float* s, int lane, AffM<K, W>& x) {
+  float* f = &x.P[0][0];
+#pragma unroll
+  for (int i = 0; i < K * K; ++i) f[i] = s[i * MG_WAVE + lane];
+  float* l = &x.L[0][0];
+#pragma unroll
+  for (int i = 0; i < K * W; ++i) l[i] = s[(K * K + i) * MG_WAVE + lane];
+}
+
+// Chained intra-workgroup scan + decoupled look-back.  `loc` is this thread's
+// sub-chunk map; on return `carry` is the map of everything before
+// (forward) / after (REVERSE) the thread's sub-chunk, including the seed
+// (identity: Abar_0 = I, Bbar_0 = 0 forward; Y_T = 0 reverse).
+template <int K, int W, int WAVES, bool REVERSE>
+__device__ void af_carry(const AffM<K, W>& loc, const AfGeom& g, int lg, int c,
+                         unsigned* header, unsigned* flags, float* agg_data, float* incl_data,
+                         AffM<K, W>& carry) {
+  constexpr int NF = K * K + K * W;
+  __shared__ float s_buf[NF * MG_WAVE];
+  const int lane = threadIdx.x & (MG_WAVE - 1);
+  const int w = threadIdx.x / MG_WAVE;
+  AffM<K, W> ew, tmp;
+  affm_identity(ew);
+  // Waves in time order: forward 0..W-1, reverse W-1..0.
+  for (int step = 0; step < WAVES; ++step) {
+    const int j = REVERSE ? WAVES - 1 - step : step;
+    if (w == j) {
+      if (step > 0) lds_get(s_buf, lane, ew);
+      affm_compose(ew, loc, tmp);
+      lds_put(s_buf, lane, tmp);
+    }
+    __syncthreads();
+  }
+  // s_buf now holds the workgroup aggregate G.
+  if (w == 0) {
+    AffM<K, W> G, E, X, acc;
+    lds_get(s_buf, lane, G);
+    const int first = REVERSE ? g.n_chunks - 1 : 0;
+    const int dir = REVERSE ? 1 : -1;
+    affm_identity(E);
+    if (c != first) {
+      af_lb_store(agg_data, g, lg, c, lane, G);
+      mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_AGG);
+      for (int j = c + dir;; j += dir) {
+        unsigned f = mg_wait_flag(&flags[lg * g.n_chunks + j], header);
+        if (f == MG_FLAG_NONE) break;
+        af_lb_load(f == MG_FLAG_INCL ? incl_data : agg_data, g, lg, j, lane, X);
+        affm_compose(X, E, acc);
+        E = acc;
+        if (f == MG_FLAG_INCL || j == first) break;
+      }
+    }
+    affm_compose(E, G, acc);
+    af_lb_store(incl_data, g, lg, c, lane, acc);
+    mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_INCL);
+    lds_put(s_buf, lane, E);
+  }
+  __syncthreads();
+  AffM<K, W> C;
+  lds_get(s_buf, lane, C);
+  affm_compose(C, ew, carry);
+}
+
+struct AfThread {
+  int lane, w, c, lg, bb;
+  int64_t plane;
+  bool ok;
+};
+
+template <bool REVERSE>
+__device__ __forceinline__ AfThread af_thread(const AfGeom& g, unsigned* header) {
+  AfThread th;
+  unsigned ticket = mg_take_ticket(header);
+  th.lane = threadIdx.x & (MG_WAVE - 1);
+  th.w = threadIdx.x / MG_WAVE;
+  int kk = (int)(ticket / (unsigned)g.n_lg);
+  th.lg = (int)(ticket - (unsigned)kk * (unsigned)g.n_lg);
+  th.c = REVERSE ? g.n_chunks - 1 - kk : kk;
+  th.bb = th.lg / g.n_tiles;
+  const int tile = th.lg - th.bb * g.n_tiles;
+  th.plane = (int64_t)tile * MG_WAVE + th.lane;
+  th.ok = th.plane < g.n;
+  return th;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <int K, int V, int TSUB, int WAVES>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
+    const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ Abar,
+    float* __restrict__ Bbar, AfGeom g, unsigned* header, unsigned* flags, float* agg_data,
+    float* incl_data) {
+  constexpr bool HOLD = af_hold<K>();
+  constexpr int HS = HOLD ? TSUB : 1;
+  AfThread th = af_thread<false>(g, header);
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, n = g.n;
+  auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
+  auto offB = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * V); };
+
+  float ha[HS][K * K], hb[HS][K * V];
+  auto fetch = [&](int s, float* a, float* b) {
+    const int64_t t = t0 + s;
+    if (th.ok && t < T) {
+      ld<K * K>(a, A + offA(t));
+      ld<K * V>(b, Bm + offB(t));
+    } else {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) a[i] = (i / K == i % K) ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) b[i] = 0.f;
+    }
+  };
+  if constexpr (HOLD) {
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) fetch(s, ha[s], hb[s]);
+  }
+
+  // Local aggregate: S -> A_t S + B_t composed over the sub-chunk.
+  AffM<K, V> loc, carry;
+  affm_identity(loc);
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float a[K * K], b[K * V];
+    if constexpr (HOLD) {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) a[i] = ha[s][i];
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) b[i] = hb[s][i];
+    } else {
+      fetch(s, a, b);
+    }
+    AffM<K, V> nx;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(a[i * K + m], loc.P[m][j], acc);
+        nx.P[i][j] = acc;
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float acc = b[i * V + j];
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(a[i * K + m], loc.L[m][j], acc);
+        nx.L[i][j] = acc;
+      }
+    }
+    loc = nx;
+  }
+  af_carry<K, V, WAVES, false>(loc, g, th.lg, th.c, header, flags, agg_data, incl_data, carry);
+
+  // Final pass from the carry-in (Abar_{t0-1}, Bbar_{t0-1}).
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float a[K * K], b[K * V];
+    if constexpr (HOLD) {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) a[i] = ha[s][i];
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) b[i] = hb[s][i];
+    } else {
+      fetch(s, a, b);
+    }
+    AffM<K, V> nx;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(a[i * K + m], carry.P[m][j], acc);
+        nx.P[i][j] = acc;
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float acc = b[i * V + j];
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(a[i * K + m], carry.L[m][j], acc);
+        nx.L[i][j] = acc;
+      }
+    }
+    carry = nx;
+    const int64_t t = t0 + s;
+    if (th.ok && t < T) {
+      st<K * K>(Abar + offA(t), &carry.P[0][0]);
+      st<K * V>(Bbar + offB(t), &carry.L[0][0]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+template <int K, int V, int TSUB, int WAVES>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
+    const float* __restrict__ A, const float* __restrict__ Bm, const float* __restrict__ Abar,
+    const float* __restrict__ Bbar, const float* __restrict__ GA, const float* __restrict__ GB,
+    float* __restrict__ dA, float* __restrict__ dB, AfGeom g, unsigned* header,
+    unsigned* flags, float* agg_data, float* incl_data) {
+  constexpr bool HOLD = af_hold<K>();
+  constexpr int HS = HOLD ? TSUB : 1;
+  constexpr int W = K + V;  // adjoint state: [XA | XB]
+  AfThread th = af_thread<true>(g, header);
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, n = g.n;
+  auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
+  auto offB = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * V); };
+
+  float ha[HS][K * K], hb[HS][K * V], hga[HS][K * K], hgb[HS][K * V];
+  auto fetch = [&](int s, float* a, float* b, float* ga, float* gb, bool need_b) {
+    const int64_t t = t0 + s;
+    if (th.ok && t < T) {
+      ld<K * K>(a, A + offA(t));
+      if (need_b) ld<K * V>(b, Bm + offB(t));
+      ld<K * K>(ga, GA + offA(t));
+      ld<K * V>(gb, GB + offB(t));
+    } else {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) {
+        a[i] = (i / K == i % K) ? 1.f : 0.f;
+        ga[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) {
+        b[i] = 0.f;
+        gb[i] = 0.f;
+      }
+    }
+  };
+  if constexpr (HOLD) {
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) fetch(s, ha[s], hb[s], hga[s], hgb[s], true);
+  }
+
+  // Local reverse aggregate: Y -> A_t^T (G_t + Y), composed from the end.
+  AffM<K, W> loc, carry;
+  affm_identity(loc);
+#pragma unroll
+  for (int s = TSUB - 1; s >= 0; --s) {
+    float a[K * K], b[K * V], ga[K * K], gb[K * V];
+    if constexpr (HOLD) {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) { a[i] = ha[s][i]; ga[i] = hga[s][i]; }
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) { b[i] = hb[s][i]; gb[i] = hgb[s][i]; }
+    } else {
+      fetch(s, a, b, ga, gb, false);
+    }
+    AffM<K, W> nx;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], loc.P[m][j], acc);
+        nx.P[i][j] = acc;
+      }
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < K; ++m) {
+          const float gmj = j < K ? ga[m * K + j] : gb[m * V + (j - K)];
+          acc = fmaf(a[m * K + i], gmj + loc.L[m][j], acc);
+        }
+        nx.L[i][j] = acc;
+      }
+    }
+    loc = nx;
+  }
+  af_carry<K, W, WAVES, true>(loc, g, th.lg, th.c, header, flags, agg_data, incl_data, carry);
+
+  // Y entering the sub-chunk from the right (Y_T = 0 seed applied).
+  float Y[K][W];
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+#pragma unroll
+    for (int j = 0; j < W; ++j) Y[i][j] = carry.L[i][j];
+
+  if constexpr (HOLD) {
+    // Reverse sweep: X_t = G_t + Y; Y <- A_t^T X_t; keep X_t in place of G_t.
+#pragma unroll
+    for (int s = TSUB - 1; s >= 0; --s) {
+      float X[K][W];
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+          X[i][j] = (j < K ? hga[s][i * K + j] : hgb[s][i * V + (j - K)]) + Y[i][j];
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][m * K + i], X[m][j], acc);
+          Y[i][j] = acc;
+        }
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          if (j < K) hga[s][i * K + j] = X[i][j];
+          else hgb[s][i * V + (j - K)] = X[i][j];
+        }
+    }
+    // Forward sweep: recompute (Abar_{t-1}, Bbar_{t-1}) from the saved boundary.
+    float Sa[K * K], Sb[K * V];
+    if (th.ok && t0 > 0 && t0 <= T) {
+      ld<K * K>(Sa, Abar + offA(t0 - 1));
+      ld<K * V>(Sb, Bbar + offB(t0 - 1));
+    } else {
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      float d[K * K];
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(hga[s][i * K + m], Sa[j * K + m], acc);
+#pragma unroll
+          for (int m = 0; m < V; ++m) acc = fmaf(hgb[s][i * V + m], Sb[j * V + m], acc);
+          d[i * K + j] = acc;
+        }
+      float na[K * K], nb[K * V];
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sa[m * K + j], acc);
+          na[i * K + j] = acc;
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          float acc = hb[s][i * V + j];
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sb[m * V + j], acc);
+          nb[i * V + j] = acc;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < K * K; ++i) Sa[i] = na[i];
+#pragma unroll
+      for (int i = 0; i < K * V; ++i) Sb[i] = nb[i];
+      const int64_t t = t0 + s;
+      if (th.ok && t < T) {
+        st<K * K>(dA + offA(t), d);
+        st<K * V>(dB + offB(t), hgb[s]);
+      }
+    }
+  } else {
+    // Single reverse sweep reading the saved forward outputs.
+    for (int s = TSUB - 1; s >= 0; --s) {
+      const int64_t t = t0 + s;
+      if (!(th.ok && t < T)) continue;
+      float a[K * K], ga[K * K], gb[K * V], b_unused[1];
+      (void)b_unused;
+      ld<K * K>(a, A + offA(t));
+      ld<K * K>(ga, GA + offA(t));
+      ld<K * V>(gb, GB + offB(t));
+      float Sa[K * K], Sb[K * V];
+      if (t > 0) {
+        ld<K * K>(Sa, Abar + offA(t - 1));
+        ld<K * V>(Sb, Bbar + offB(t - 1));
+      } else {
+#pragma unroll
+        for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
+#pragma unroll
+        for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
+      }
+      float X[K][W];
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+          X[i][j] = (j < K ? ga[i * K + j] : gb[i * V + (j - K)]) + Y[i][j];
+      float d[K * K], xb[K * V];
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(X[i][m], Sa[j * K + m], acc);
+#pragma unroll
+          for (int m = 0; m < V; ++m) acc = fmaf(X[i][K + m], Sb[j * V + m], acc);
+          d[i * K + j] = acc;
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) xb[i * V + j] = X[i][K + j];
+      }
+      st<K * K>(dA + offA(t), d);
+      st<K * V>(dB + offB(t), xb);
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], X[m][j], acc);
+          Y[i][j] = acc;
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------
+struct AfPlan {
+  AfGeom g;
+  size_t flag_words, agg_off, incl_off, total;
+};
+
+AfPlan af_plan(int64_t B, int64_t T, int64_t n, int k, int v, int tsub, int nf) {
+  AfPlan p;
+  p.g.T = T;
+  p.g.n = n;
+  p.g.n_tiles = (int)((n + MG_WAVE - 1) / MG_WAVE);
+  p.g.n_lg = (int)(B * p.g.n_tiles);
+  const int64_t cl = (int64_t)AF_WAVES * tsub;
+  p.g.n_chunks = (int)((T + cl - 1) / cl);
+  const size_t cnt = (size_t)p.g.n_lg * p.g.n_chunks;
+  p.flag_words = MG_HEADER_BYTES / 4 + mg_align_up(cnt, 64);
+  const size_t data = cnt * (size_t)nf * MG_WAVE * sizeof(float);
+  p.agg_off = p.flag_words * 4;
+  p.incl_off = p.agg_off + mg_align_up(data, 256);
+  p.total = p.incl_off + mg_align_up(data, 256);
+  (void)k;
+  (void)v;
+  return p;
+}
+
+int tsub_for(int k) { return k == 1 ? af_tsub<1>() : k == 2 ? af_tsub<2>() : k == 4 ? af_tsub<4>() : af_tsub<8>(); }
+
+bool kv_ok(int k, int v) {
+  return (k == 1 || k == 2 || k == 4 || k == 8) &&
+         (v == 1 || v == 2 || v == 4 || v == 8 || v == 16);
+}
+
+bool af_geometry_ok(int64_t B, int64_t T, int64_t n) {
+  if (B <= 0 || T <= 0 || n <= 0) return false;
+  const int64_t lgs = B * ((n + MG_WAVE - 1) / MG_WAVE);
+  const int64_t chunks = (T + AF_WAVES - 1) / AF_WAVES;
+  return lgs * chunks < (1ll << 24);
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int K, int V>
+int af_launch_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B, int64_t T,
+                  int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
+  constexpr int TS = af_tsub<K>();
+  AfPlan p = af_plan(B, T, n, K, V, TS, K * K + K * V);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  int rc = mg_clear(ws, p.flag_words, stream);
+  if (rc != MG_OK) return rc;
+  unsigned* header = (unsigned*)ws;
+  hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, AF_WAVES>),
+                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
+                     stream, A, Bm, Abar, Bbar, p.g, header, header + MG_HEADER_BYTES / 4,
+                     (float*)((char*)ws + p.agg_off), (float*)((char*)ws + p.incl_off));
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+template <int K, int V>
+int af_launch_bwd(const float* A, const float* Bm, const float* Abar, const float* Bbar,
+                  const float* GA, const float* GB, float* dA, float* dB, int64_t B, int64_t T,
+                  int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
+  constexpr int TS = af_tsub<K>();
+  AfPlan p = af_plan(B, T, n, K, V, TS, K * K + K * (K + V));
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  int rc = mg_clear(ws, p.flag_words, stream);
+  if (rc != MG_OK) return rc;
+  unsigned* header = (unsigned*)ws;
+  hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, AF_WAVES>),
+                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
+                     stream, A, Bm, Abar, Bbar, GA, GB, dA, dB, p.g, header,
+                     header + MG_HEADER_BYTES / 4, (float*)((char*)ws + p.agg_off),
+                     (float*)((char*)ws + p.incl_off));
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+#define MG_AF_DISPATCH(FN, ...)                                    \
+  switch (k * 100 + v) {                                           \
+    case 101: return FN<1, 1>(__VA_ARGS__);                        \
+    case 102: return FN<1, 2>(__VA_ARGS__);                        \
+    case 104: return FN<1, 4>(__VA_ARGS__);                        \
+    case 108: return FN<1, 8>(__VA_ARGS__);                        \
+    case 116: return FN<1, 16>(__VA_ARGS__);                       \
+    case 201: return FN<2, 1>(__VA_ARGS__);                        \
+    case 202: return FN<2, 2>(__VA_ARGS__);                        \
+    case 204: return FN<2, 4>(__VA_ARGS__);                        \
+    case 208: return FN<2, 8>(__VA_ARGS__);                        \
+    case 216: return FN<2, 16>(__VA_ARGS__);                       \
+    case 401: return FN<4, 1>(__VA_ARGS__);                        \
+    case 402: return FN<4, 2>(__VA_ARGS__);                        \
+    case 404: return FN<4, 4>(__VA_ARGS__);                        \
+    case 408: return FN<4, 8>(__VA_ARGS__);                        \
+    case 416: return FN<4, 16>(__VA_ARGS__);                       \
+    case 801: return FN<8, 1>(__VA_ARGS__);                        \
+    case 802: return FN<8, 2>(__VA_ARGS__);                        \
+    case 804: return FN<8, 4>(__VA_ARGS__);                        \
+    case 808: return FN<8, 8>(__VA_ARGS__);                        \
+    case 816: return FN<8, 16>(__VA_ARGS__);                       \
+    default: return MG_ERR_ARG;                                    \
+  }
+
+}  // namespace
+
+extern "C" {
+
+size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v) {
+  if (!kv_ok(k, v) || B <= 0 || T <= 0 || n <= 0) return 256;
+  const int ts = tsub_for(k);
+  return std::max(af_plan(B, T, n, k, v, ts, k * k + k * v).total,
+                  af_plan(B, T, n, k, v, ts, k * k + k * (k + v)).total);
+}
+
+int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,
+                       int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
+                       hipStream_t stream) {
+  if (!A || !Bm || !Abar || !Bbar || !ws || !kv_ok(k, v) || !af_geometry_ok(B, T, n))
+    return MG_ERR_ARG;
+  if (!al16(A) || !al16(Bm) || !al16(Abar) || !al16(Bbar)) return MG_ERR_ARG;
+  MG_AF_DISPATCH(af_launch_fwd, A, Bm, Abar, Bbar, B, T, n, ws, ws_bytes, stream)
+}
+
+int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const float* Bbar,
+                       const float* gAbar, const float* gBbar, float* dA, float* dBm, int64_t B,
+                       int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
+                       hipStream_t stream) {
+  if (!A || !Bm || !Abar || !Bbar || !gAbar || !gBbar || !dA || !dBm || !ws || !kv_ok(k, v) ||
+      !af_geometry_ok(B, T, n))
+    return MG_ERR_ARG;
+  if (!al16(A) || !al16(Bm) || !al16(Abar) || !al16(Bbar) || !al16(gAbar) || !al16(gBbar) ||
+      !al16(dA) || !al16(dBm))
+    return MG_ERR_ARG;
+  MG_AF_DISPATCH(af_launch_bwd, A, Bm, Abar, Bbar, gAbar, gBbar, dA, dBm, B, T, n, ws, ws_bytes,
+                 stream)
+}
+
+}  // extern "C"

@@ -115,7 +115,10 @@ def _as_f32(*ts: torch.Tensor):
             raise ScanFallback("HIP scans compute in fp32; float64 inputs stay on the eager path")
         if not t.dtype.is_floating_point:
             raise ScanFallback(f"HIP scans need floating-point inputs (got {t.dtype})")
-        out.append(t.to(torch.float32).contiguous())
+        t = t.to(torch.float32).contiguous()
+        if t.data_ptr() % 16:
+            t = t.clone()  # kernels use 16-byte vector accesses
+        out.append(t)
     return out
 
 
@@ -239,7 +242,98 @@ def _parallel_scan_log_impl(log_coeffs: torch.Tensor, log_values: torch.Tensor):
     return _funnel("parallel_scan_log", _LogScanFn.apply, log_coeffs, log_values)
 
 
+# ---------------------------------------------------------------------------
+# matrix_scan / matrix_affine_scan
+# ---------------------------------------------------------------------------
+
+
+class _AffineScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, A, Bm):
+        out_dtype = A.dtype
+        A32, B32 = _as_f32(A, Bm)
+        Bn, T, n, k, _ = A32.shape
+        v = B32.shape[-1]
+        Abar = torch.empty_like(A32)
+        Bbar = torch.empty_like(B32)
+        ws = _workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        _call("mg_affine_scan_fwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), Bn, T, n, k, v,
+              _ptr(ws), ws.numel(), _stream(A32))
+        ctx.save_for_backward(A32, B32, Abar, Bbar)
+        ctx.out_dtype = out_dtype
+        if out_dtype != torch.float32:
+            return Abar.to(out_dtype), Bbar.to(out_dtype)
+        return Abar, Bbar
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gAbar, gBbar):
+        A32, B32, Abar, Bbar = ctx.saved_tensors
+        Bn, T, n, k, _ = A32.shape
+        v = B32.shape[-1]
+        gA32, gB32 = _as_f32(gAbar, gBbar)
+        dA = torch.empty_like(A32)
+        dB = torch.empty_like(B32)
+        ws = _workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        _call("mg_affine_scan_bwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), _ptr(gA32),
+              _ptr(gB32), _ptr(dA), _ptr(dB), Bn, T, n, k, v, _ptr(ws), ws.numel(), _stream(A32))
+        return dA.to(ctx.out_dtype), dB.to(ctx.out_dtype)
+
+
+def _matrix_affine_scan_impl(A: torch.Tensor, Bm: torch.Tensor):
+    """``SCAN_IMPLS['matrix_affine_scan']``: generic k x k transitions, k x v injections."""
+    if A.ndim != 5 or Bm.ndim != 5:
+        raise ScanFallback(
+            f"matrix_affine_scan (A={tuple(A.shape)}, Bm={tuple(Bm.shape)}) outside the HIP "
+            "envelope: need 5-D (B, T, n, k, k) A and (B, T, n, k, v) Bm"
+        )
+    k = A.shape[-1]
+    v = Bm.shape[-1]
+    if (
+        k not in _AFFINE_K
+        or v not in _AFFINE_V
+        or A.shape[-2] != k
+        or Bm.shape[-2] != k
+        or A.shape[:3] != Bm.shape[:3]
+    ):
+        raise ScanFallback(
+            f"matrix_affine_scan (A={tuple(A.shape)}, Bm={tuple(Bm.shape)}) outside the HIP "
+            f"envelope: need k in {sorted(_AFFINE_K)}, v in {sorted(_AFFINE_V)}, a square A and "
+            "A/Bm sharing the (B, T, n) lane grid"
+        )
+    _same_device(A, Bm)
+    if A.numel() == 0:
+        return A.new_empty(A.shape), Bm.new_empty(Bm.shape)
+    return _funnel("matrix_affine_scan", _AffineScanFn.apply, A, Bm)
+
+
+def _matrix_scan_impl(M: torch.Tensor, b: torch.Tensor):
+    """``SCAN_IMPLS['matrix_scan']``: the k = 2, v = 1 case, ``b`` viewed as (..., 2, 1)."""
+    if (
+        M.ndim != 5
+        or b.ndim != 4
+        or tuple(M.shape[-2:]) != (2, 2)
+        or b.shape[-1] != 2
+        or M.shape[:3] != b.shape[:3]
+    ):
+        raise ScanFallback(
+            f"matrix_scan (M={tuple(M.shape)}, b={tuple(b.shape)}) outside the HIP envelope: "
+            "need (B, T, n, 2, 2) M and (B, T, n, 2) b sharing the (B, T, n) lane grid"
+        )
+    _same_device(M, b)
+    if M.numel() == 0:
+        return M.new_empty(M.shape), b.new_empty(b.shape)
+
+    def run():
+        Abar, Bbar = _AffineScanFn.apply(M, b.unsqueeze(-1))
+        return Abar, Bbar.squeeze(-1)
+
+    return _funnel("matrix_scan", run)
+
+
 SCAN_IMPLS: dict = {
     "parallel_scan_log": _parallel_scan_log_impl,
     "linear_scan": _linear_scan_impl,
+    "matrix_scan": _matrix_scan_impl,
+    "matrix_affine_scan": _matrix_affine_scan_impl,
 }
