@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark of the minGRU scan hot path on one MI355X.
+
+Metric: fwd+bwd tokens/s and achieved HBM TB/s (% of peak) per
+scan op.  The headline JSON line is workload C2 (``linear_scan`` fwd+bwd,
+B=16 T=4096 D=1024 fp32, BASELINE.json ``configs[1]``); the other workloads
+are reported under ``"ops"`` in the same line.
+
+A step is one forward + backward pass of the op through the public API
+(``torch.autograd.grad`` on the HIP autograd Function) over one batch of
+synthetic inputs already resident in HBM.  ``--warmup`` untimed steps, then
+exactly ``--steps`` timed steps between two ``torch.cuda.synchronize()``.
+Per-kernel device durations come from HIP events recorded around every C-ABI
+launch on the launch stream; achieved bandwidth = algorithmic bytes per launch
+/ that duration.  The CPU baseline times this package's eager path (the
+reference algorithm on CPU tensors, all host threads) on a bounded batch slice
+of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only C2,...]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+
+METRIC = "fwd+bwd tokens/s + achieved HBM TB/s (% of peak) per scan op, 1 MI355X"
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", type=str, default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def _traffic(name: str):
+    """HBM bytes per launch from the committed rocprof counter summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    return data.get(name)
+
+
+class Op:
+    """One benchmark workload: input builder, one fwd+bwd step, byte accounting."""
+
+    def __init__(self, key, workload, tokens, fwd_entry, bwd_entry, fwd_bytes, bwd_bytes):
+        self.key = key
+        self.workload = workload
+        self.tokens = tokens
+        self.fwd_entry = fwd_entry
+        self.bwd_entry = bwd_entry
+        self.fwd_bytes = fwd_bytes
+        self.bwd_bytes = bwd_bytes
+
+
+def build_ops(torch, wl):
+    ops = {}
+
+    # C2: linear_scan (headline)
+    c = wl.C2
+    N = c["B"] * c["T"] * c["D"]
+    ops["C2"] = Op("C2", "C2 SignedMinGRU linear_scan fwd+bwd", c["B"] * c["T"],
+                   "mg_linear_scan_fwd", "mg_linear_scan_bwd", 4 * N * 4, 6 * N * 4)
+    # C1: parallel_scan_log
+    c = wl.C1
+    N = c["B"] * c["T"] * c["D"]
+    N1 = c["B"] * (c["T"] + 1) * c["D"]
+    ops["C1"] = Op("C1", "C1 MinGRU parallel_scan_log fwd+bwd", c["B"] * c["T"],
+                   "mg_log_scan_fwd", "mg_log_scan_bwd", (2 * N + N1) * 4, (3 * N + 2 * N1) * 4)
+    # C3: 2x2 matrix_affine_scan and matrix_scan (b = 0)
+    c = wl.C3
+    P = c["B"] * c["T"] * c["n"]
+    ops["C3"] = Op("C3", "C3 RotationMinGRU 2x2 matrix_affine_scan fwd+bwd", c["B"] * c["T"],
+                   "mg_affine_scan_fwd", "mg_affine_scan_bwd", 12 * P * 4, 18 * P * 4)
+    ops["C3m"] = Op("C3m", "C3 matrix_scan (b=0) fwd+bwd", c["B"] * c["T"],
+                    "mg_affine_scan_fwd", "mg_affine_scan_bwd", 12 * P * 4, 18 * P * 4)
+    return ops
+
+
+def make_step(key, torch, wl, dev):
+    """Returns (step_fn, cpu_step_fn(batch_slice) or None)."""
+    import mingru_amd as mg
+
+    if key == "C2":
+        inp = wl.c2_inputs(**wl.C2)
+        a = inp["a"].to(dev).requires_grad_(True)
+        b = inp["b"].to(dev).requires_grad_(True)
+        gA, gB = inp["grad_A"].to(dev), inp["grad_Bc"].to(dev)
+
+        def step():
+            A, Bc = mg.linear_scan(a, b)
+            return torch.autograd.grad((A, Bc), (a, b), (gA, gB))
+
+        def cpu(bs):
+            ac = inp["a"][:bs].clone().requires_grad_(True)
+            bc = inp["b"][:bs].clone().requires_grad_(True)
+            A, Bc = mg.linear_scan(ac, bc)
+            torch.autograd.grad((A, Bc), (ac, bc), (inp["grad_A"][:bs], inp["grad_Bc"][:bs]))
+
+        return step, cpu, wl.C2["B"]
+    if key == "C1":
+        inp = wl.c1_inputs(**wl.C1)
+        lc = inp["log_coeffs"].to(dev).requires_grad_(True)
+        lv = inp["log_values"].to(dev).requires_grad_(True)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = mg.parallel_scan_log(lc, lv)
+            return torch.autograd.grad(h, (lc, lv), gh)
+
+        def cpu(bs):
+            lcc = inp["log_coeffs"][:bs].clone().requires_grad_(True)
+            lvc = inp["log_values"][:bs].clone().requires_grad_(True)
+            h = mg.parallel_scan_log(lcc, lvc)
+            torch.autograd.grad(h, (lcc, lvc), inp["grad_h"][:bs])
+
+        return step, cpu, wl.C1["B"]
+    if key in ("C3", "C3m"):
+        inp = wl.c3_inputs(**wl.C3)
+        A = inp["A"].to(dev).requires_grad_(True)
+        if key == "C3":
+            Bm = inp["Bm"].to(dev).requires_grad_(True)
+            gA, gB = inp["grad_Abar"].to(dev), inp["grad_Bbar"].to(dev)
+
+            def step():
+                Abar, Bbar = mg.matrix_affine_scan(A, Bm)
+                return torch.autograd.grad((Abar, Bbar), (A, Bm), (gA, gB))
+
+            def cpu(bs):
+                Ac = inp["A"][:bs].clone().requires_grad_(True)
+                Bc = inp["Bm"][:bs].clone().requires_grad_(True)
+                Abar, Bbar = mg.matrix_affine_scan(Ac, Bc)
+                torch.autograd.grad((Abar, Bbar), (Ac, Bc),
+                                    (inp["grad_Abar"][:bs], inp["grad_Bbar"][:bs]))
+        else:
+            b0 = torch.zeros(inp["Bm"].shape[:-1], device=dev).requires_grad_(True)
+            gA, gB = inp["grad_Abar"].to(dev), inp["grad_Bbar"][..., 0].to(dev)
+
+            def step():
+                Abar, Bc = mg.matrix_scan(A, b0)
+                return torch.autograd.grad((Abar, Bc), (A, b0), (gA, gB))
+
+            cpu = None
+        return step, cpu, wl.C3["B"]
+    raise KeyError(key)
+
+
+def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
+    step, cpu_step, B = make_step(op.key, torch, wl, dev)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with hip_scans.kernel_timer() as timer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
+    durs = timer.durations_ms()
+    kern = {}
+    for entry, nbytes in ((op.fwd_entry, op.fwd_bytes), (op.bwd_entry, op.bwd_bytes)):
+        d = durs.get(entry, [])
+        if not d:
+            continue
+        d = sorted(d)
+        avg = sum(d) / len(d)
+        kern[entry] = {
+            "avg_us": avg * 1e3,
+            "median_us": d[len(d) // 2] * 1e3,
+            "algorithmic_bytes": nbytes,
+            "achieved_GBs": nbytes / (avg * 1e-3) / 1e9,
+        }
+    total_bytes = op.fwd_bytes + op.bwd_bytes
+    res = {
+        "workload": op.workload,
+        "tokens_per_s": op.tokens / (ms * 1e-3),
+        "ms_per_step": ms,
+        "algorithmic_bytes": total_bytes,
+        "achieved_TBs": total_bytes / (ms * 1e-3) / 1e12,
+        "frac_of_hbm_peak": total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernels": kern,
+    }
+    return res, cpu_step, B
+
+
+def cpu_baseline(cpu_step, B_full, tokens_full, torch, budget_s=20.0):
+    """Time the eager CPU path on a batch slice; returns the baseline dict."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    os.environ["MINGRU_SCAN"] = "eager"
+    bs = 1
+    t0 = time.perf_counter()
+    cpu_step(bs)  # warm-up
+    warm = time.perf_counter() - t0
+    reps = max(1, min(3, int(budget_s / max(warm, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cpu_step(bs)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    tokens_slice = tokens_full * bs // B_full
+    return {
+        "value": tokens_slice / med,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"eager torch CPU fwd+bwd on batch slice {bs}/{B_full} of the same inputs "
+                  f"(1 warm-up, median of {reps}; min {tokens_slice / times[0]:.4g} tokens/s); "
+                  f"os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
+                          "(the scan path shards with no communication over batch and lanes; "
+                          "see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+
+    from mingru_amd import hip_scans
+    from mingru_amd import workloads as wl
+
+    status = hip_scans.available()
+    if status is not True:
+        raise SystemExit(f"HIP backend unavailable: {status}")
+    os.environ["MINGRU_SCAN"] = "hip"
+    dev = torch.device("cuda:0")
+    ops = build_ops(torch, wl)
+    order = ["C2", "C1", "C3", "C3m"]
+    if args.only:
+        order = [k for k in order if k in args.only.split(",")]
+    results = {}
+    cpu = None
+    for key in order:
+        if key not in ops:
+            continue
+        res, cpu_step, B = run_op(ops[key], torch, wl, dev, args.steps, args.warmup, hip_scans)
+        results[key] = res
+        print(f"# {key}: {res['tokens_per_s']:.4g} tok/s, {res['ms_per_step']:.3f} ms/step, "
+              f"{res['achieved_TBs']:.3f} TB/s ({100 * res['frac_of_hbm_peak']:.1f}% of peak)",
+              file=sys.stderr, flush=True)
+        for kname, kres in res["kernels"].items():
+            print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
+                  file=sys.stderr, flush=True)
+        if key == "C2" and cpu_step is not None and not args.no_cpu:
+            cpu = cpu_baseline(cpu_step, B, ops[key].tokens, torch)
+            os.environ["MINGRU_SCAN"] = "hip"
+        torch.cuda.empty_cache()
+
+    head = results.get("C2") or next(iter(results.values()))
+    head_key = "C2" if "C2" in results else next(iter(results))
+    op = ops[head_key]
+    # Dominant kernel: the one with the largest device time per step.
+    dom_name, dom = max(head["kernels"].items(), key=lambda kv: kv[1]["avg_us"])
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom_name,
+        "achieved": dom["achieved_GBs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": dom["achieved_GBs"] / HBM_PEAK_GBS,
+        "traffic": _traffic(f"{head_key}:{dom_name}"),
+    }
+    line = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
+        "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C3": wl.C3,
+                                               "C3m": wl.C3}.get(head_key, {})},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "achieved_TBs": head["achieved_TBs"],
+        "frac_of_hbm_peak": head["frac_of_hbm_peak"],
+        "ops": results,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

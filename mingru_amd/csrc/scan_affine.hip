@@ -119,31 +119,33 @@ struct AfGeom {
   int n_tiles, n_lg, n_chunks;
 };
 
-// Look-back storage: [lg][chunk][field][64] floats.
+// Look-back slots: [lg][chunk][field][64] tagged words.
 template <int K, int W>
-__device__ __forceinline__ void af_lb_store(float* base, const AfGeom& g, int lg, int c, int lane,
-                                            const AffM<K, W>& x) {
+__device__ __forceinline__ void af_lb_put(mg_slot_t* base, const AfGeom& g, int lg, int c,
+                                          int lane, const AffM<K, W>& x) {
   constexpr int NF = K * K + K * W;
-  float* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
+  mg_slot_t* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
   const float* f = &x.P[0][0];
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) p[i * MG_WAVE] = f[i];
+  for (int i = 0; i < K * K; ++i) mg_slot_put(p + i * MG_WAVE, f[i]);
   const float* l = &x.L[0][0];
 #pragma unroll
-  for (int i = 0; i < K * W; ++i) p[(K * K + i) * MG_WAVE] = l[i];
+  for (int i = 0; i < K * W; ++i) mg_slot_put(p + (K * K + i) * MG_WAVE, l[i]);
 }
 
 template <int K, int W>
-__device__ __forceinline__ void af_lb_load(const float* base, const AfGeom& g, int lg, int c,
-                                           int lane, AffM<K, W>& x) {
+__device__ __forceinline__ bool af_lb_try(const mg_slot_t* base, const AfGeom& g, int lg, int c,
+                                          int lane, AffM<K, W>& x) {
   constexpr int NF = K * K + K * W;
-  const float* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
+  const mg_slot_t* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
+  bool ok = true;
   float* f = &x.P[0][0];
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) f[i] = p[i * MG_WAVE];
+  for (int i = 0; i < K * K; ++i) ok &= mg_slot_get(p + i * MG_WAVE, f[i]);
   float* l = &x.L[0][0];
 #pragma unroll
-  for (int i = 0; i < K * W; ++i) l[i] = p[(K * K + i) * MG_WAVE];
+  for (int i = 0; i < K * W; ++i) ok &= mg_slot_get(p + (K * K + i) * MG_WAVE, l[i]);
+  return ok;
 }
 
 template <int K, int W>
@@ -172,7 +174,7 @@ __device__ __forceinline__ void lds_get(const float* s, int lane, AffM<K, W>& x)
 // (identity: Abar_0 = I, Bbar_0 = 0 forward; Y_T = 0 reverse).
 template <int K, int W, int WAVES, bool REVERSE>
 __device__ void af_carry(const AffM<K, W>& loc, const AfGeom& g, int lg, int c,
-                         unsigned* header, unsigned* flags, float* agg_data, float* incl_data,
+                         unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data,
                          AffM<K, W>& carry) {
   constexpr int NF = K * K + K * W;
   __shared__ float s_buf[NF * MG_WAVE];
@@ -198,20 +200,30 @@ __device__ void af_carry(const AffM<K, W>& loc, const AfGeom& g, int lg, int c,
     const int dir = REVERSE ? 1 : -1;
     affm_identity(E);
     if (c != first) {
-      af_lb_store(agg_data, g, lg, c, lane, G);
-      mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_AGG);
-      for (int j = c + dir;; j += dir) {
-        unsigned f = mg_wait_flag(&flags[lg * g.n_chunks + j], header);
-        if (f == MG_FLAG_NONE) break;
-        af_lb_load(f == MG_FLAG_INCL ? incl_data : agg_data, g, lg, j, lane, X);
-        affm_compose(X, E, acc);
-        E = acc;
-        if (f == MG_FLAG_INCL || j == first) break;
+      af_lb_put(agg_data, g, lg, c, lane, G);
+      int j = c + dir;
+      unsigned spins = 0;
+      bool done = false;
+      while (!done) {
+        bool have = af_lb_try(incl_data, g, lg, j, lane, X);
+        const bool incl = have;
+        if (!have && j != first) have = af_lb_try(agg_data, g, lg, j, lane, X);
+        if (have) {
+          affm_compose(X, E, acc);
+          E = acc;
+          if (incl) done = true;
+          else j += dir;
+        } else {
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins >= MG_SPIN_LIMIT) {
+            mg_count_error(header);
+            done = true;
+          }
+        }
       }
     }
     affm_compose(E, G, acc);
-    af_lb_store(incl_data, g, lg, c, lane, acc);
-    mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_INCL);
+    af_lb_put(incl_data, g, lg, c, lane, acc);
     lds_put(s_buf, lane, E);
   }
   __syncthreads();
@@ -248,8 +260,8 @@ __device__ __forceinline__ AfThread af_thread(const AfGeom& g, unsigned* header)
 template <int K, int V, int TSUB, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
     const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ Abar,
-    float* __restrict__ Bbar, AfGeom g, unsigned* header, unsigned* flags, float* agg_data,
-    float* incl_data) {
+    float* __restrict__ Bbar, AfGeom g, unsigned* header, mg_slot_t* agg_data,
+    mg_slot_t* incl_data) {
   constexpr bool HOLD = af_hold<K>();
   constexpr int HS = HOLD ? TSUB : 1;
   AfThread th = af_thread<false>(g, header);
@@ -310,7 +322,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
     }
     loc = nx;
   }
-  af_carry<K, V, WAVES, false>(loc, g, th.lg, th.c, header, flags, agg_data, incl_data, carry);
+  af_carry<K, V, WAVES, false>(loc, g, th.lg, th.c, header, agg_data, incl_data, carry);
 
   // Final pass from the carry-in (Abar_{t0-1}, Bbar_{t0-1}).
 #pragma unroll
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
     const float* __restrict__ A, const float* __restrict__ Bm, const float* __restrict__ Abar,
     const float* __restrict__ Bbar, const float* __restrict__ GA, const float* __restrict__ GB,
     float* __restrict__ dA, float* __restrict__ dB, AfGeom g, unsigned* header,
-    unsigned* flags, float* agg_data, float* incl_data) {
+    mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool HOLD = af_hold<K>();
   constexpr int HS = HOLD ? TSUB : 1;
   constexpr int W = K + V;  // adjoint state: [XA | XB]
@@ -432,7 +444,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
     }
     loc = nx;
   }
-  af_carry<K, W, WAVES, true>(loc, g, th.lg, th.c, header, flags, agg_data, incl_data, carry);
+  af_carry<K, W, WAVES, true>(loc, g, th.lg, th.c, header, agg_data, incl_data, carry);
 
   // Y entering the sub-chunk from the right (Y_T = 0 seed applied).
   float Y[K][W];
@@ -582,10 +594,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
 // ---------------------------------------------------------------------------
 struct AfPlan {
   AfGeom g;
-  size_t flag_words, agg_off, incl_off, total;
+  size_t agg_off, incl_off, total;
 };
 
-AfPlan af_plan(int64_t B, int64_t T, int64_t n, int k, int v, int tsub, int nf) {
+AfPlan af_plan(int64_t B, int64_t T, int64_t n, int tsub, int nf) {
   AfPlan p;
   p.g.T = T;
   p.g.n = n;
@@ -594,13 +606,10 @@ AfPlan af_plan(int64_t B, int64_t T, int64_t n, int k, int v, int tsub, int nf) 
   const int64_t cl = (int64_t)AF_WAVES * tsub;
   p.g.n_chunks = (int)((T + cl - 1) / cl);
   const size_t cnt = (size_t)p.g.n_lg * p.g.n_chunks;
-  p.flag_words = MG_HEADER_BYTES / 4 + mg_align_up(cnt, 64);
-  const size_t data = cnt * (size_t)nf * MG_WAVE * sizeof(float);
-  p.agg_off = p.flag_words * 4;
+  const size_t data = cnt * (size_t)nf * MG_WAVE * sizeof(mg_slot_t);
+  p.agg_off = MG_HEADER_BYTES;
   p.incl_off = p.agg_off + mg_align_up(data, 256);
   p.total = p.incl_off + mg_align_up(data, 256);
-  (void)k;
-  (void)v;
   return p;
 }
 
@@ -624,15 +633,15 @@ template <int K, int V>
 int af_launch_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B, int64_t T,
                   int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
   constexpr int TS = af_tsub<K>();
-  AfPlan p = af_plan(B, T, n, K, V, TS, K * K + K * V);
+  AfPlan p = af_plan(B, T, n, TS, K * K + K * V);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-  int rc = mg_clear(ws, p.flag_words, stream);
+  int rc = mg_clear(ws, p.total, stream);
   if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
   hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, AF_WAVES>),
                      dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
-                     stream, A, Bm, Abar, Bbar, p.g, header, header + MG_HEADER_BYTES / 4,
-                     (float*)((char*)ws + p.agg_off), (float*)((char*)ws + p.incl_off));
+                     stream, A, Bm, Abar, Bbar, p.g, header,
+                     (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
@@ -641,16 +650,15 @@ int af_launch_bwd(const float* A, const float* Bm, const float* Abar, const floa
                   const float* GA, const float* GB, float* dA, float* dB, int64_t B, int64_t T,
                   int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
   constexpr int TS = af_tsub<K>();
-  AfPlan p = af_plan(B, T, n, K, V, TS, K * K + K * (K + V));
+  AfPlan p = af_plan(B, T, n, TS, K * K + K * (K + V));
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-  int rc = mg_clear(ws, p.flag_words, stream);
+  int rc = mg_clear(ws, p.total, stream);
   if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
   hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, AF_WAVES>),
                      dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
                      stream, A, Bm, Abar, Bbar, GA, GB, dA, dB, p.g, header,
-                     header + MG_HEADER_BYTES / 4, (float*)((char*)ws + p.agg_off),
-                     (float*)((char*)ws + p.incl_off));
+                     (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
@@ -686,8 +694,8 @@ extern "C" {
 size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v) {
   if (!kv_ok(k, v) || B <= 0 || T <= 0 || n <= 0) return 256;
   const int ts = tsub_for(k);
-  return std::max(af_plan(B, T, n, k, v, ts, k * k + k * v).total,
-                  af_plan(B, T, n, k, v, ts, k * k + k * (k + v)).total);
+  return std::max(af_plan(B, T, n, ts, k * k + k * v).total,
+                  af_plan(B, T, n, ts, k * k + k * (k + v)).total);
 }
 
 int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,

@@ -26,8 +26,10 @@
 
 namespace {
 
-constexpr int EW_WAVES = 4;
+// Chunk = WAVES * TSUB time steps per workgroup.
+constexpr int EW_WAVES_FWD = 8;
 constexpr int EW_TSUB_FWD = 16;
+constexpr int EW_WAVES_BWD = 8;
 constexpr int EW_TSUB_BWD = 8;
 
 // Affine map y -> p*y + l (NL independent offsets sharing one slope).
@@ -82,39 +84,33 @@ struct EwGeom {
   int n_tiles, n_lg, n_chunks;
 };
 
-// Look-back storage: [lg][chunk][field][TILE] floats, TILE = 64*VEC.
+// Look-back slots: [lg][chunk][field][TILE] tagged words, TILE = 64*VEC.
 template <int NL, int VEC>
-__device__ __forceinline__ void lb_store(float* base, const EwGeom& g, int lg, int c, int lane,
-                                         const Aff<NL> (&x)[VEC]) {
+__device__ __forceinline__ void lb_put(mg_slot_t* base, const EwGeom& g, int lg, int c, int lane,
+                                       const Aff<NL> (&x)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
-  float* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
-  float tmp[VEC];
+  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) tmp[v] = x[v].p;
-  store_vec<VEC>(p, tmp);
+  for (int v = 0; v < VEC; ++v) {
+    mg_slot_put(p + v, x[v].p);
 #pragma unroll
-  for (int f = 0; f < NL; ++f) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) tmp[v] = x[v].l[f];
-    store_vec<VEC>(p + (f + 1) * TILE, tmp);
+    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v, x[v].l[f]);
   }
 }
 
 template <int NL, int VEC>
-__device__ __forceinline__ void lb_load(const float* base, const EwGeom& g, int lg, int c,
-                                        int lane, Aff<NL> (&x)[VEC]) {
+__device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, int lg, int c,
+                                       int lane, Aff<NL> (&x)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
-  const float* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
-  float tmp[VEC];
-  load_vec<VEC>(tmp, p);
+  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
+  bool ok = true;
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) x[v].p = tmp[v];
+  for (int v = 0; v < VEC; ++v) {
+    ok &= mg_slot_get(p + v, x[v].p);
 #pragma unroll
-  for (int f = 0; f < NL; ++f) {
-    load_vec<VEC>(tmp, p + (f + 1) * TILE);
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) x[v].l[f] = tmp[v];
+    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v, x[v].l[f]);
   }
+  return ok;
 }
 
 // Intra-workgroup combine + decoupled look-back.  On return `carry` holds, for
@@ -124,7 +120,7 @@ __device__ __forceinline__ void lb_load(const float* base, const EwGeom& g, int 
 template <int NL, int VEC, int WAVES, bool REVERSE>
 __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL> (&seed)[VEC],
                                          const EwGeom& g, int lg, int c, unsigned* header,
-                                         unsigned* flags, float* agg_data, float* incl_data,
+                                         mg_slot_t* agg_data, mg_slot_t* incl_data,
                                          Aff<NL> (&carry)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
   constexpr int NF = NL + 1;
@@ -179,26 +175,38 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
 #pragma unroll
       for (int v = 0; v < VEC; ++v) E[v] = seed[v];
     } else {
-      lb_store<NL, VEC>(agg_data, g, lg, c, lane, G);
-      mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_AGG);
+      lb_put<NL, VEC>(agg_data, g, lg, c, lane, G);
 #pragma unroll
       for (int v = 0; v < VEC; ++v) E[v] = aff_identity<NL>();
-      for (int j = c + dir;; j += dir) {
-        unsigned f = mg_wait_flag(&flags[lg * g.n_chunks + j], header);
-        if (f == MG_FLAG_NONE) break;  // spin limit: error already recorded
+      // Per-lane walk over predecessors: an inclusive prefix ends the walk, an
+      // aggregate is composed in and the walk continues; the first chunk only
+      // ever publishes its inclusive prefix.
+      int j = c + dir;
+      unsigned spins = 0;
+      bool done = false;
+      while (!done) {
         Aff<NL> X[VEC];
-        lb_load<NL, VEC>(f == MG_FLAG_INCL ? incl_data : agg_data, g, lg, j, lane, X);
+        if (lb_try<NL, VEC>(incl_data, g, lg, j, lane, X)) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
-        if (f == MG_FLAG_INCL) break;
-        if (j == first) break;  // defensive: the first chunk always publishes INCL
+          for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
+          done = true;
+        } else if (j != first && lb_try<NL, VEC>(agg_data, g, lg, j, lane, X)) {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
+          j += dir;
+        } else {
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins >= MG_SPIN_LIMIT) {
+            mg_count_error(header);
+            done = true;
+          }
+        }
       }
     }
     Aff<NL> I[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) I[v] = aff_compose(E[v], G[v]);
-    lb_store<NL, VEC>(incl_data, g, lg, c, lane, I);
-    mg_publish_flag(&flags[lg * g.n_chunks + c], MG_FLAG_INCL);
+    lb_put<NL, VEC>(incl_data, g, lg, c, lane, I);
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       s_carry[0][lane * VEC + v] = E[v].p;
@@ -246,8 +254,8 @@ __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header)
 template <int VEC, int TSUB, int WAVES, bool LOG>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     const float* __restrict__ x0, const float* __restrict__ x1, float* __restrict__ out0,
-    float* __restrict__ out1, EwGeom g, unsigned* header, unsigned* flags, float* agg_data,
-    float* incl_data) {
+    float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
+    mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -303,7 +311,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
 #pragma unroll
     for (int v = 0; v < VEC; ++v) seed[v].l[0] = expf(h0[v]);
   }
-  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
                                  carry);
 
   float P[VEC], L[VEC];
@@ -341,8 +349,8 @@ template <int VEC, int TSUB, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ A,
     const float* __restrict__ Bc, const float* __restrict__ gA, const float* __restrict__ gB,
-    float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header, unsigned* flags,
-    float* agg_data, float* incl_data) {
+    float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
+    mg_slot_t* agg_data, mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     }
     seed[v] = aff_identity<2>();
   }
-  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
                                 carry);
 
   float ya[VEC], yb[VEC];
@@ -440,7 +448,7 @@ template <int VEC, int TSUB, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     const float* __restrict__ lc, const float* __restrict__ lv, const float* __restrict__ h,
     const float* __restrict__ gh, float* __restrict__ dlc, float* __restrict__ dlv, EwGeom g,
-    unsigned* header, unsigned* flags, float* agg_data, float* incl_data) {
+    unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -495,7 +503,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, flags, agg_data, incl_data,
+  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
                                 carry);
 
   float y[VEC];
@@ -538,29 +546,25 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
 
 struct EwPlan {
   EwGeom g;
-  int vec;
-  int tsub;
-  size_t flag_words;  // header + flags, in 32-bit words
+  int waves;
   size_t agg_off, incl_off, total;
 };
 
-EwPlan ew_plan(int64_t B, int64_t T, int64_t D, int vec, int tsub, int nl) {
+EwPlan ew_plan(int64_t B, int64_t T, int64_t D, int vec, int tsub, int waves, int nl) {
   EwPlan p;
-  p.vec = vec;
-  p.tsub = tsub;
+  p.waves = waves;
   p.g.T = T;
   p.g.D = D;
   const int tile = MG_WAVE * vec;
   p.g.n_tiles = (int)((D + tile - 1) / tile);
   p.g.n_lg = (int)(B * p.g.n_tiles);
-  const int64_t cl = (int64_t)EW_WAVES * tsub;
+  const int64_t cl = (int64_t)waves * tsub;
   p.g.n_chunks = (int)((T + cl - 1) / cl);
   const size_t n = (size_t)p.g.n_lg * p.g.n_chunks;
-  p.flag_words = MG_HEADER_BYTES / 4 + mg_align_up(n, 64);
-  const size_t data_bytes = n * (size_t)(nl + 1) * tile * sizeof(float);
-  p.agg_off = p.flag_words * 4;
-  p.incl_off = p.agg_off + mg_align_up(data_bytes, 256);
-  p.total = p.incl_off + mg_align_up(data_bytes, 256);
+  const size_t slot_bytes = n * (size_t)(nl + 1) * tile * sizeof(mg_slot_t);
+  p.agg_off = MG_HEADER_BYTES;
+  p.incl_off = p.agg_off + mg_align_up(slot_bytes, 256);
+  p.total = p.incl_off + mg_align_up(slot_bytes, 256);
   return p;
 }
 
@@ -568,42 +572,41 @@ bool is_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 bool geometry_ok(int64_t B, int64_t T, int64_t D) {
   if (B <= 0 || T <= 0 || D <= 0) return false;
-  // Ticket space and look-back indices are 32-bit.
-  const int64_t tiles = (D + MG_WAVE - 1) / MG_WAVE;
-  const int64_t lgs = B * tiles;
-  const int64_t chunks = (T + EW_WAVES - 1) / EW_WAVES;
-  return lgs < (1ll << 30) && chunks < (1ll << 30) && lgs * chunks < (1ll << 31);
+  // Tickets, look-back indices and grid sizes stay well inside 32 bits.
+  const int64_t lgs = B * ((D + MG_WAVE - 1) / MG_WAVE);
+  const int64_t chunks = (T + 7) / 8;
+  return lgs * chunks < (1ll << 24);
 }
 
 template <typename Kernel, typename... Args>
 int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... args) {
-  int rc = mg_clear(ws, p.flag_words, stream);
+  int rc = mg_clear(ws, p.total, stream);
   if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
-  unsigned* flags = header + MG_HEADER_BYTES / 4;
-  float* agg = (float*)((char*)ws + p.agg_off);
-  float* incl = (float*)((char*)ws + p.incl_off);
+  mg_slot_t* agg = (mg_slot_t*)((char*)ws + p.agg_off);
+  mg_slot_t* incl = (mg_slot_t*)((char*)ws + p.incl_off);
   const unsigned grid = (unsigned)p.g.n_lg * (unsigned)p.g.n_chunks;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(MG_WAVE * EW_WAVES), 0, stream, args..., p.g, header,
-                     flags, agg, incl);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(MG_WAVE * p.waves), 0, stream, args..., p.g, header,
+                     agg, incl);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
 size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
   size_t m = 0;
   for (int vec : {1, 4}) {
-    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_FWD, 1).total);
-    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_BWD, 2).total);
+    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_FWD, EW_WAVES_FWD, 1).total);
+    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_BWD, EW_WAVES_BWD, 2).total);
   }
   return m;
 }
 
 }  // namespace
 
-__global__ void mg_clear_kernel(unsigned* p, size_t n) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+__global__ void mg_clear_kernel(uint4* p, size_t n16) {
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
        i += (size_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
+    p[i] = z;
 }
 
 extern "C" {
@@ -621,11 +624,11 @@ int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int6
   if (!a || !b || !A || !Bc || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
   const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
                   is_aligned16(Bc);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, 1);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   if (v4)
-    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES, false>, p, ws, stream, a, b, A, Bc);
-  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES, false>, p, ws, stream, a, b, A, Bc);
+    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a, b, A, Bc);
+  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a, b, A, Bc);
 }
 
 int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
@@ -636,12 +639,12 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
   const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
                   is_aligned16(Bc) && is_aligned16(gA) && is_aligned16(gB) &&
                   is_aligned16(da) && is_aligned16(db);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, 2);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, EW_WAVES_BWD, 2);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   if (v4)
-    return ew_launch(linear_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, a, b, A, Bc, gA,
+    return ew_launch(linear_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
                      gB, da, db);
-  return ew_launch(linear_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, a, b, A, Bc, gA,
+  return ew_launch(linear_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
                    gB, da, db);
 }
 
@@ -649,13 +652,13 @@ int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64
                     void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!lc || !lv || !h || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
   const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, 1);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   float* none = nullptr;
   if (v4)
-    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES, true>, p, ws, stream, lc, lv, h,
+    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES_FWD, true>, p, ws, stream, lc, lv, h,
                      none);
-  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES, true>, p, ws, stream, lc, lv, h, none);
+  return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES_FWD, true>, p, ws, stream, lc, lv, h, none);
 }
 
 int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* gh, float* dlc,
@@ -664,12 +667,12 @@ int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const floa
   if (!lc || !lv || !h || !gh || !dlc || !dlv || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
   const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h) &&
                   is_aligned16(gh) && is_aligned16(dlc) && is_aligned16(dlv);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, 1);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, EW_WAVES_BWD, 1);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   if (v4)
-    return ew_launch(log_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, lc, lv, h, gh, dlc,
+    return ew_launch(log_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, lc, lv, h, gh, dlc,
                      dlv);
-  return ew_launch(log_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES>, p, ws, stream, lc, lv, h, gh, dlc,
+  return ew_launch(log_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, lc, lv, h, gh, dlc,
                    dlv);
 }
 

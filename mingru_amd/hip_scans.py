@@ -100,10 +100,48 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+class kernel_timer:
+    """Context manager recording HIP events around every C-ABI launch.
+
+    Events are recorded on the stream each call is enqueued on (torch's current
+    stream), so ``records`` yields per-call device durations:
+    ``[(entry_point_name, start_event, stop_event), ...]``.  Used by the
+    benchmark; inactive otherwise.
+    """
+
+    active = None
+
+    def __init__(self):
+        self.records = []
+
+    def __enter__(self):
+        kernel_timer.active = self
+        return self
+
+    def __exit__(self, *exc):
+        kernel_timer.active = None
+        return False
+
+    def durations_ms(self):
+        out: dict = {}
+        for name, a, b in self.records:
+            out.setdefault(name, []).append(a.elapsed_time(b))
+        return out
+
+
 def _call(fn_name: str, *args) -> None:
     from . import _native
 
-    rc = getattr(_lib(), fn_name)(*args)
+    timer = kernel_timer.active
+    if timer is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        rc = getattr(_lib(), fn_name)(*args)
+        stop.record()
+        timer.records.append((fn_name, start, stop))
+    else:
+        rc = getattr(_lib(), fn_name)(*args)
     _native.check(rc, fn_name)
 
 
