@@ -92,6 +92,13 @@ def build_ops(torch, wl):
                    "mg_affine_scan_fwd", "mg_affine_scan_bwd", 12 * P * 4, 18 * P * 4)
     ops["C3m"] = Op("C3m", "C3 matrix_scan (b=0) fwd+bwd", c["B"] * c["T"],
                     "mg_affine_scan_fwd", "mg_affine_scan_bwd", 12 * P * 4, 18 * P * 4)
+    # C4: angle-fused Givens, 28 lexicographic rotations, decay
+    c = wl.C4
+    L = c["B"] * c["T"] * c["n"]
+    h0b = c["B"] * c["n"] * c["k"] * 4
+    ops["C4"] = Op("C4", "C4 GivensMinGRU angle-fused (28 lexicographic rotations) fwd+bwd",
+                   c["B"] * c["T"], "mg_angle_scan_fwd", "mg_angle_scan_bwd",
+                   180 * L + h0b, 328 * L + 2 * h0b)
     return ops
 
 
@@ -160,6 +167,23 @@ def make_step(key, torch, wl, dev):
 
             cpu = None
         return step, cpu, wl.C3["B"]
+    if key == "C4":
+        from mingru_amd import hip_scans
+
+        inp = wl.c4_inputs(**wl.C4)
+        th = inp["theta"].to(dev).requires_grad_(True)
+        gm = inp["gamma"].to(dev).requires_grad_(True)
+        bb = inp["b"].to(dev).requires_grad_(True)
+        h0 = inp["h0"].to(dev).requires_grad_(True)
+        sc = inp["scale"].to(dev)
+        meta = [inp[k].to(dev) for k in ("perm", "sgn", "p2p")]
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = hip_scans.angle_scan_impl(th, sc, gm, bb, h0, *meta, has_scale=0, has_decay=1)
+            return torch.autograd.grad(h, (th, gm, bb, h0), gh)
+
+        return step, None, wl.C4["B"]
     raise KeyError(key)
 
 
@@ -250,7 +274,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C1", "C3", "C3m"]
+    order = ["C2", "C1", "C3", "C3m", "C4"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -299,7 +323,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
         "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C3": wl.C3,
-                                               "C3m": wl.C3}.get(head_key, {})},
+                                               "C3m": wl.C3, "C4": wl.C4}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "achieved_TBs": head["achieved_TBs"],

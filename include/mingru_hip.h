@@ -70,6 +70,27 @@ int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const
                        int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
                        mg_stream_t stream);
 
+/* ---- angle-fused block-rotation scan (RotationMinGRU / GivensMinGRU) --------
+ * Replaces angle_scan_fwd / angle_scan_bwd (src/mingru/triton_scans.py:1579-1703;
+ * kernels :1039-1291) behind angle_scan_impl (:1743-1812).
+ * theta (B,T,n,NA) with NA angles per token, scale/gamma (B,T,n), b/h (B,T,n,k),
+ * h0 (B,n,k); k in {2,4,8}.  sched 0: brick-wall rounds (NA = rounds*k/2),
+ * sched 1: all pairs i<j in lexicographic order, one plane per round
+ * (rounds = k(k-1)/2 = NA).  flags bit 0: scale coordinate 1 by `scale`,
+ * bit 1: decay by `gamma`. */
+size_t mg_angle_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
+int mg_angle_scan_fwd(const float* theta, const float* scale, const float* gamma, const float* b,
+                      const float* h0, float* h, int64_t B, int64_t T, int64_t n, int k,
+                      int sched, int rounds, int flags, void* ws, size_t ws_bytes,
+                      mg_stream_t stream);
+/* h = forward output, gh = dL/dh -> dtheta, dscale, dgamma (written when the
+ * flag is set), db, dh0. */
+int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma, const float* h0,
+                      const float* h, const float* gh, float* dtheta, float* dscale,
+                      float* dgamma, float* db, float* dh0, int64_t B, int64_t T, int64_t n,
+                      int k, int sched, int rounds, int flags, void* ws, size_t ws_bytes,
+                      mg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

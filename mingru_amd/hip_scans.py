@@ -23,6 +23,7 @@ is not supported (``once_differentiable``).
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -367,6 +368,155 @@ def _matrix_scan_impl(M: torch.Tensor, b: torch.Tensor):
         return Abar, Bbar.squeeze(-1)
 
     return _funnel("matrix_scan", run)
+
+
+# ---------------------------------------------------------------------------
+# angle-fused rotation scan
+# ---------------------------------------------------------------------------
+
+_SCHED_BRICK = 0
+_SCHED_LEX = 1
+# id(perm) -> (weakref to perm, validity key, (sched, rounds)).  Tensors cannot be
+# dictionary keys by value (their == is elementwise), hence the identity key.
+_sched_cache: dict = {}
+
+
+def _brick_tables(k: int, R: int):
+    perm = torch.arange(k, dtype=torch.int64).repeat(R, 1)
+    sgn = torch.zeros(R, k, dtype=torch.float64)
+    p2p = torch.zeros(R, k, dtype=torch.int64)
+    for r in range(R):
+        for m in range(k // 2):
+            i = (r % 2 + 2 * m) % k
+            j = (i + 1) % k
+            perm[r, i], perm[r, j] = j, i
+            sgn[r, i], sgn[r, j] = -1.0, 1.0
+            p2p[r, i] = p2p[r, j] = m
+    return perm, sgn, p2p
+
+
+def _classify_schedule(perm, sgn, p2p, k: int, R: int, half: int):
+    """Map the plane metadata onto a compiled schedule: ``(sched, rounds)``.
+
+    Recognised: brick-wall rounds (even rounds pair (0,1),(2,3)...; odd rounds
+    (1,2),...,(k-1,0); ``half = k/2`` angles per round) and one-plane rounds
+    over all pairs i<j in lexicographic order (``half = 1``).  A position whose
+    partner is itself is untouched by its round.  Anything else declines.
+    """
+    key = (perm._version, sgn.data_ptr(), sgn._version, p2p.data_ptr(), p2p._version, k, R, half)
+    hit = _sched_cache.get(id(perm))
+    if hit is not None and hit[0]() is perm and hit[1] == key:
+        return hit[2]
+    pc = perm.detach().to("cpu", torch.int64)
+    sc = sgn.detach().to("cpu", torch.float64)
+    qc = p2p.detach().to("cpu", torch.int64)
+    result = None
+    if half == k // 2:
+        bp, bs, bq = _brick_tables(k, R)
+        if torch.equal(pc, bp) and torch.equal(sc, bs) and torch.equal(qc, bq):
+            result = (_SCHED_BRICK, R)
+    if result is None and half == 1 and R == k * (k - 1) // 2:
+        ok = True
+        r = 0
+        for i in range(k):
+            for j in range(i + 1, k):
+                exp = torch.arange(k)
+                exp[i], exp[j] = j, i
+                if not (torch.equal(pc[r], exp) and sc[r, i] == -1.0 and sc[r, j] == 1.0
+                        and qc[r, i] == 0 and qc[r, j] == 0):
+                    ok = False
+                r += 1
+        if ok:
+            result = (_SCHED_LEX, R)
+    if result is None:
+        raise ScanFallback(
+            "angle-fused HIP kernel supports brick-wall rounds and the lexicographic all-pairs "
+            "schedule; the given perm/sgn/p2p plane metadata is neither"
+        )
+    if len(_sched_cache) > 256:
+        for dead in [i for i, v in _sched_cache.items() if v[0]() is None]:
+            del _sched_cache[dead]
+    _sched_cache[id(perm)] = (weakref.ref(perm), key, result)
+    return result
+
+
+class _AngleScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, theta, scale, gamma, b, h0, sched, rounds, flags):
+        out_dtype = b.dtype
+        th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
+        Bn, T, n, k = b32.shape
+        h = torch.empty_like(b32)
+        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
+        _call("mg_angle_scan_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032), _ptr(h),
+              Bn, T, n, k, sched, rounds, flags, _ptr(ws), ws.numel(), _stream(b32))
+        ctx.save_for_backward(th, sc, gm, h032, h)
+        ctx.meta = (sched, rounds, flags, out_dtype, theta.dtype, scale.dtype, gamma.dtype,
+                    h0.dtype)
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        th, sc, gm, h032, h = ctx.saved_tensors
+        sched, rounds, flags, out_dtype, tdt, sdt, gdt, hdt = ctx.meta
+        Bn, T, n, k = h.shape
+        (gh32,) = _as_f32(gh)
+        dth = torch.empty_like(th)
+        need = ctx.needs_input_grad
+        # Grads of a disabled scale / decay channel are zero (never read by the kernel).
+        dsc = torch.zeros_like(sc) if (flags & 1 or need[1]) else None
+        dgm = torch.zeros_like(gm) if (flags & 2 or need[2]) else None
+        db = torch.empty_like(h)
+        dh0 = torch.empty_like(h032)
+        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
+        _call("mg_angle_scan_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h), _ptr(gh32),
+              _ptr(dth), _ptr(dsc), _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k, sched, rounds,
+              flags, _ptr(ws), ws.numel(), _stream(h))
+        return (dth.to(tdt), None if dsc is None else dsc.to(sdt),
+                None if dgm is None else dgm.to(gdt), db.to(out_dtype), dh0.to(hdt),
+                None, None, None)
+
+
+def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: int,
+                    has_decay: int):
+    """Envelope-checked angle-fused rotation scan; returns ``h`` ``(B, T, n, k)``.
+
+    Same contract as the reference entry point (``src/mingru/triton_scans.py:1743-1812``):
+    ``theta`` ``(B, T, n, R, half)``, ``scale``/``gamma`` ``(B, T, n)``, ``b``
+    ``(B, T, n, k)``, ``h0`` ``(B, n, k)``, ``perm``/``sgn``/``p2p`` ``(R, k)``.
+    """
+    if theta.ndim != 5 or b.ndim != 4:
+        raise ScanFallback(
+            f"angle-fused kernel (theta={tuple(theta.shape)}, b={tuple(b.shape)}) outside the "
+            "envelope: need 5-D (B, T, n, R, half) theta and 4-D (B, T, n, k) b"
+        )
+    Bn, T, n, R, half = theta.shape
+    k = b.shape[-1]
+    if (
+        k not in _ANGLE_K
+        or tuple(b.shape[:3]) != (Bn, T, n)
+        or tuple(scale.shape) != (Bn, T, n)
+        or tuple(gamma.shape) != (Bn, T, n)
+        or tuple(h0.shape) != (Bn, n, k)
+        or tuple(perm.shape) != (R, k)
+        or tuple(sgn.shape) != (R, k)
+        or tuple(p2p.shape) != (R, k)
+        or R > _ANGLE_MAX_ROT
+    ):
+        raise ScanFallback(
+            f"angle-fused kernel (theta={tuple(theta.shape)}, scale={tuple(scale.shape)}, "
+            f"gamma={tuple(gamma.shape)}, b={tuple(b.shape)}, h0={tuple(h0.shape)}, "
+            f"perm={tuple(perm.shape)}) outside the envelope: need k in {sorted(_ANGLE_K)}, "
+            f"R <= {_ANGLE_MAX_ROT} and shapes agreeing on (B, T, n, R, k)"
+        )
+    _same_device(theta, scale, gamma, b, h0)
+    sched, rounds = _classify_schedule(perm, sgn, p2p, k, R, half)
+    if T == 0:
+        return b.new_empty(b.shape)
+    flags = (1 if has_scale else 0) | (2 if has_decay else 0)
+    return _funnel("angle-fused", _AngleScanFn.apply, theta, scale, gamma, b, h0, sched, rounds,
+                   flags)
 
 
 SCAN_IMPLS: dict = {

@@ -1,0 +1,169 @@
+"""GPU parity: HIP angle-fused rotation scan vs the fp64 oracle, and the module paths.
+
+Bars: fp32 forward max abs err <= 1e-4, gradients <= 1e-3 against float64 on
+the C4 workload.  The synthetic stress cases include schedules without decay,
+where the state random-walks to |h| ~ 25 over the sequence; there the bar is
+scaled by max(1, max|ref| / 4), i.e. the same bar relative to the state size.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import mingru_amd as mg
+from mingru_amd import hip_scans
+from mingru_amd import workloads as wl
+from oracle import scans as orc
+
+FWD_TOL = 1e-4
+GRAD_TOL = 1e-3
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _force_hip(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+
+
+def _maxerr(x, ref):
+    return float(np.max(np.abs(x.detach().double().cpu().numpy() - ref))) if ref.size else 0.0
+
+
+def _brick_meta(k, R):
+    layer = mg.GivensMinGRU(4, k, block_size=k, rounds=R)
+    return layer._angle_plane_meta(torch.device("cpu"))
+
+
+def _inputs(B, T, n, k, R, half, seed, std=0.7):
+    g = torch.Generator().manual_seed(seed)
+    theta = std * torch.randn(B, T, n, R, half, generator=g)
+    scale = torch.tanh(torch.randn(B, T, n, generator=g))
+    gamma = torch.sigmoid(torch.randn(B, T, n, generator=g))
+    b = torch.randn(B, T, n, k, generator=g)
+    h0 = torch.randn(B, n, k, generator=g)
+    gh = torch.randn(B, T, n, k, generator=g)
+    return theta, scale, gamma, b, h0, gh
+
+
+def _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, hs, hd):
+    ts = [t.to(cuda).requires_grad_(True) for t in (theta, scale, gamma, b, h0)]
+    h = hip_scans.angle_scan_impl(*ts, perm.to(cuda), sgn.to(cuda), p2p.to(cuda),
+                                  has_scale=hs, has_decay=hd)
+    assert "AngleScanFn" in type(h.grad_fn).__name__
+    h.backward(gh.to(cuda))
+    torch.cuda.synchronize()
+    npy = [t.numpy() for t in (theta, scale, gamma, b, h0)]
+    ref = orc.angle_scan(*npy, perm.numpy(), sgn.numpy(), p2p.numpy(), hs, hd)
+    rgrads = orc.angle_scan_bwd(*npy, perm.numpy(), sgn.numpy(), p2p.numpy(), hs, hd, gh.numpy())
+    def bar(tol, r):
+        return tol * max(1.0, float(np.max(np.abs(r))) / 4.0)
+
+    assert _maxerr(h, ref) <= bar(FWD_TOL, ref)
+    names = ["theta", "scale", "gamma", "b", "h0"]
+    for name, t, r in zip(names, ts, rgrads):
+        if name == "scale" and not hs:
+            continue
+        if name == "gamma" and not hd:
+            continue
+        err = _maxerr(t.grad, r)
+        assert err <= bar(GRAD_TOL, r), f"d{name}: {err}"
+
+
+BRICK_CASES = [
+    # B, T, n, k, R, has_scale, has_decay
+    (2, 1, 3, 8, 3, 0, 0),
+    (2, 37, 5, 8, 3, 0, 1),
+    (2, 100, 70, 8, 3, 0, 0),
+    (1, 65, 9, 8, 2, 0, 1),
+    (2, 50, 33, 4, 3, 0, 1),
+    (2, 80, 40, 4, 1, 0, 0),
+    (2, 90, 65, 2, 1, 1, 0),
+    (2, 71, 12, 2, 1, 1, 1),
+    (1, 40, 7, 2, 3, 0, 1),
+]
+
+
+@pytest.mark.parametrize("case", BRICK_CASES)
+def test_brick_schedule_matches_oracle(cuda, case):
+    B, T, n, k, R, hs, hd = case
+    print(f"[gpu] angle brick case={case}", flush=True)
+    perm, sgn, p2p = _brick_meta(k, R)
+    theta, scale, gamma, b, h0, gh = _inputs(B, T, n, k, R, k // 2, seed=T * 13 + n + k)
+    _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, hs, hd)
+
+
+LEX_CASES = [(2, 33, 10, 8, 1), (1, 120, 64, 8, 1), (2, 45, 20, 4, 1), (2, 30, 66, 8, 0)]
+
+
+@pytest.mark.parametrize("case", LEX_CASES)
+def test_lexicographic_schedule_matches_oracle(cuda, case):
+    B, T, n, k, hd = case
+    print(f"[gpu] angle lex case={case}", flush=True)
+    perm, sgn, p2p = wl.lexicographic_schedule(k)
+    R = k * (k - 1) // 2
+    theta, scale, gamma, b, h0, gh = _inputs(B, T, n, k, R, 1, seed=7 * T + n, std=0.5)
+    _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, 0, hd)
+
+
+def test_c4_full_size(cuda):
+    print("[gpu] angle C4 full size", flush=True)
+    inp = wl.c4_inputs(**wl.C4)
+    keys = ("theta", "scale", "gamma", "b", "h0")
+    ts = [inp[k].to(cuda).requires_grad_(True) for k in keys]
+    h = hip_scans.angle_scan_impl(*ts, inp["perm"].to(cuda), inp["sgn"].to(cuda),
+                                  inp["p2p"].to(cuda), has_scale=0, has_decay=1)
+    h.backward(inp["grad_h"].to(cuda))
+    torch.cuda.synchronize()
+    for r in (0, wl.C4["B"] - 1):
+        sl = slice(r, r + 1)
+        npy = [inp[k][sl].numpy() for k in keys]
+        meta = (inp["perm"].numpy(), inp["sgn"].numpy(), inp["p2p"].numpy())
+        ref = orc.angle_scan(*npy, *meta, 0, 1)
+        rg = orc.angle_scan_bwd(*npy, *meta, 0, 1, inp["grad_h"][sl].numpy())
+        assert _maxerr(h[sl], ref) <= FWD_TOL
+        for name, t, g in zip(keys, ts, rg):
+            if name == "scale":
+                continue
+            assert _maxerr(t.grad[sl], g) <= GRAD_TOL, name
+
+
+def _module_parity(cuda, layer, T=64, B=3):
+    torch.manual_seed(0)
+    layer = layer.to(cuda)
+    x = torch.randn(B, T, layer.input_size, device=cuda)
+    os.environ["MINGRU_SCAN"] = "eager"
+    y_ref = layer(x)
+    y_ref.square().sum().backward()
+    g_ref = {n: p.grad.clone() for n, p in layer.named_parameters()}
+    layer.zero_grad()
+    os.environ["MINGRU_SCAN"] = "hip"
+    y = layer(x)
+    y.square().sum().backward()
+    assert (y - y_ref).abs().max().item() <= FWD_TOL * 10
+    for n, p in layer.named_parameters():
+        scale = max(1.0, g_ref[n].abs().max().item())
+        assert (p.grad - g_ref[n]).abs().max().item() <= 1e-3 * scale, n
+
+
+def test_givens_module_matches_eager(cuda):
+    _module_parity(cuda, mg.GivensMinGRU(16, 64))
+
+
+def test_givens_module_decay_matches_eager(cuda):
+    layer = mg.GivensMinGRU(16, 32, decay="learnable")
+    layer = layer.to(cuda)
+    torch.manual_seed(1)
+    x = torch.randn(2, 40, 16, device=cuda)
+    dt = torch.rand(2, 40, device=cuda)
+    os.environ["MINGRU_SCAN"] = "eager"
+    y_ref = layer(x, delta_t=dt)
+    os.environ["MINGRU_SCAN"] = "hip"
+    y = layer(x, delta_t=dt)
+    assert (y - y_ref).abs().max().item() <= 1e-4
+
+
+def test_rotation_module_matches_eager(cuda):
+    _module_parity(cuda, mg.RotationMinGRU(16, 32, snap=None))
