@@ -34,6 +34,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+MFMA_FP32_PEAK_TFLOPS = 157.3  # dense fp32 (the delta kernels' MFMA type)
 
 METRIC = "fwd+bwd tokens/s + achieved HBM TB/s (% of peak) per scan op, 1 MI355X"
 
@@ -59,9 +60,10 @@ def _traffic(name: str):
 
 
 class Op:
-    """One benchmark workload: input builder, one fwd+bwd step, byte accounting."""
+    """One benchmark workload: input builder, one fwd+bwd step, byte (or FLOP) accounting."""
 
-    def __init__(self, key, workload, tokens, fwd_entry, bwd_entry, fwd_bytes, bwd_bytes):
+    def __init__(self, key, workload, tokens, fwd_entry, bwd_entry, fwd_bytes, bwd_bytes,
+                 fwd_flops=None, bwd_flops=None):
         self.key = key
         self.workload = workload
         self.tokens = tokens
@@ -69,6 +71,8 @@ class Op:
         self.bwd_entry = bwd_entry
         self.fwd_bytes = fwd_bytes
         self.bwd_bytes = bwd_bytes
+        self.fwd_flops = fwd_flops
+        self.bwd_flops = bwd_flops
 
 
 def build_ops(torch, wl):
@@ -99,6 +103,17 @@ def build_ops(torch, wl):
     ops["C4"] = Op("C4", "C4 GivensMinGRU angle-fused (28 lexicographic rotations) fwd+bwd",
                    c["B"] * c["T"], "mg_angle_scan_fwd", "mg_angle_scan_bwd",
                    180 * L + h0b, 328 * L + 2 * h0b)
+    # C5: DeltaMinGRU chunked-WY, bf16 inputs.  FLOP floor: per (b, h) and chunk of
+    # C tokens, six C x C x d products and one triangular solve (C^3), i.e.
+    # 6 * 2 C^3 + C^3 = 13 C^3 at C = d = 64; the backward is counted as 2x the
+    # forward (fwd+bwd = 3x fwd), the convention of the reference's delta probe.
+    c = wl.C5
+    n_chunk = c["B"] * c["H"] * (c["T"] // c["chunk"])
+    f_fwd = 13 * c["chunk"] ** 3 * n_chunk
+    bt = c["B"] * c["H"] * c["T"] * c["d"] * 2  # one bf16 (B,H,T,d) tensor
+    ops["C5"] = Op("C5", "C5 DeltaMinGRU chunked-WY fwd+bwd (bf16 in, fp32 state)",
+                   c["B"] * c["T"], "mg_delta_fwd", "mg_delta_bwd",
+                   4 * bt + bt // c["d"], 7 * bt + 2 * bt // c["d"], f_fwd, 2 * f_fwd)
     return ops
 
 
@@ -184,7 +199,47 @@ def make_step(key, torch, wl, dev):
             return torch.autograd.grad(h, (th, gm, bb, h0), gh)
 
         return step, None, wl.C4["B"]
+    if key == "C5":
+        from mingru_amd import hip_scans
+
+        inp = wl.c5_inputs(**wl.C5)
+        xs = [inp[k].to(dev).requires_grad_(True) for k in ("Q", "K", "V", "beta", "H0")]
+        gy = inp["grad_y"].to(dev).to(torch.bfloat16)
+        gH = inp["grad_HT"].to(dev)
+        C = inp["chunk_size"]
+
+        def step():
+            y, HT = hip_scans.delta_scan_impl(*xs, chunk_size=C)
+            return torch.autograd.grad((y, HT), xs, (gy, gH))
+
+        return step, None, wl.C5["B"]
     raise KeyError(key)
+
+
+def delta_eager_gpu_ms(torch, wl, dev, reps=3):
+    """The eager chunked-WY loop (torch ops on the GPU, fp32 since the triangular
+    solve has no bf16 kernel) fwd+bwd at C5; returns the median ms per step."""
+    from mingru_amd.min_gru import delta_chunked_eager
+
+    inp = wl.c5_inputs(**wl.C5)
+    xs = [inp[k].to(dev).float().requires_grad_(True) for k in ("Q", "K", "V", "beta", "H0")]
+    gy = inp["grad_y"].to(dev).float().permute(0, 2, 1, 3)
+    gH = inp["grad_HT"].to(dev)
+
+    def step():
+        y, HT = delta_chunked_eager(*xs, inp["chunk_size"])
+        torch.autograd.grad((y, HT), xs, (gy, gH))
+
+    step()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
 
 
 def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
@@ -202,7 +257,8 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
     ms = (t1 - t0) * 1e3 / steps
     durs = timer.durations_ms()
     kern = {}
-    for entry, nbytes in ((op.fwd_entry, op.fwd_bytes), (op.bwd_entry, op.bwd_bytes)):
+    for entry, nbytes, nflops in ((op.fwd_entry, op.fwd_bytes, op.fwd_flops),
+                                  (op.bwd_entry, op.bwd_bytes, op.bwd_flops)):
         d = durs.get(entry, [])
         if not d:
             continue
@@ -214,6 +270,9 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
             "algorithmic_bytes": nbytes,
             "achieved_GBs": nbytes / (avg * 1e-3) / 1e9,
         }
+        if nflops is not None:
+            kern[entry]["algorithmic_flops"] = nflops
+            kern[entry]["achieved_TFLOPs"] = nflops / (avg * 1e-3) / 1e12
     total_bytes = op.fwd_bytes + op.bwd_bytes
     res = {
         "workload": op.workload,
@@ -224,6 +283,11 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
         "frac_of_hbm_peak": total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernels": kern,
     }
+    if op.fwd_flops is not None:
+        fl = op.fwd_flops + op.bwd_flops
+        res["algorithmic_flops"] = fl
+        res["achieved_TFLOPs"] = fl / (ms * 1e-3) / 1e12
+        res["frac_of_fp32_mfma_peak"] = res["achieved_TFLOPs"] / MFMA_FP32_PEAK_TFLOPS
     return res, cpu_step, B
 
 
@@ -274,7 +338,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C1", "C3", "C3m", "C4"]
+    order = ["C2", "C1", "C3", "C3m", "C4", "C5"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -290,6 +354,13 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
+        if key == "C5":
+            eg = delta_eager_gpu_ms(torch, wl, dev)
+            res["eager_gpu_ms_per_step"] = eg
+            res["speedup_vs_eager_gpu"] = eg / res["ms_per_step"]
+            print(f"#   eager GPU chunked-WY: {eg:.2f} ms/step "
+                  f"({res['speedup_vs_eager_gpu']:.1f}x slower than HIP)", file=sys.stderr,
+                  flush=True)
         if key == "C2" and cpu_step is not None and not args.no_cpu:
             cpu = cpu_baseline(cpu_step, B, ops[key].tokens, torch)
             os.environ["MINGRU_SCAN"] = "hip"
@@ -323,7 +394,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
         "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C3": wl.C3,
-                                               "C3m": wl.C3, "C4": wl.C4}.get(head_key, {})},
+                                               "C3m": wl.C3, "C4": wl.C4,
+                                               "C5": wl.C5}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "achieved_TBs": head["achieved_TBs"],

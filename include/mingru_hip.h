@@ -91,6 +91,32 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
                       int k, int sched, int rounds, int flags, void* ws, size_t ws_bytes,
                       mg_stream_t stream);
 
+/* ---- DeltaMinGRU chunked-WY delta rule ----------------------------------------
+ * Replaces the reference's three forward kernels (_delta_prepass_kernel,
+ * _delta_state_kernel, _delta_readout_kernel, src/mingru/triton_scans.py:
+ * 1859-2193, launched by _delta_forward_launch :2195-2322) and its torch
+ * backward (_delta_backward_torch :473-605, wired by _DeltaScanFn :2324-2401)
+ * behind delta_scan_impl (:2403-2447).
+ * Layouts: Q (B,H,T,dk), K (B,H,T,nh,dk), V (B,H,T,nh,dv), beta (B,H,T,nh),
+ * y (B,H,T,dv), all of element type `dtype` (0 = fp32, 1 = bf16);
+ * H0 / HT / dHT / dH0 (B,H,dk,dv) fp32.  Envelope: 1 <= dk, dv <= 64,
+ * chunk >= 1, nh * chunk <= 64.
+ * `Hbound` (mg_delta_state_bytes) receives the chunk-entry states and is
+ * read back by mg_delta_bwd; `ws` needs mg_delta_workspace_bytes. */
+size_t mg_delta_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
+                                int chunk);
+size_t mg_delta_state_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk);
+int mg_delta_fwd(const void* Q, const void* K, const void* V, const void* beta, const float* H0,
+                 void* y, float* HT, float* Hbound, int64_t B, int64_t H, int64_t T, int nh,
+                 int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
+                 mg_stream_t stream);
+/* dy (dtype), dHT -> dQ, dK, dV, dbeta (dtype) and dH0. */
+int mg_delta_bwd(const void* Q, const void* K, const void* V, const void* beta,
+                 const float* Hbound, const void* dy, const float* dHT, void* dQ, void* dK,
+                 void* dV, void* dbeta, float* dH0, int64_t B, int64_t H, int64_t T, int nh,
+                 int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
+                 mg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,13 +39,14 @@ _SIGNATURES = {
         _I32, [_P] * 11 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
     "mg_delta_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
+    "mg_delta_state_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
     "mg_delta_fwd": (
         _I32,
-        [_P] * 5 + [_P, _P, _P] + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        [_P] * 5 + [_P] * 3 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
     "mg_delta_bwd": (
         _I32,
-        [_P] * 8 + [_P] * 5 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        [_P] * 7 + [_P] * 5 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
 }
 

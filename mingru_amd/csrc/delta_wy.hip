@@ -1,0 +1,839 @@
+// DeltaMinGRU chunked-WY delta rule, forward and backward (gfx950, MFMA).
+//
+// Recurrence per head (reference src/mingru/min_gru.py:3103-3255, 3611-3688):
+// for every micro-step m (token-major, nh per token)
+//     H <- H - beta_m k_m (k_m^T H) + beta_m k_m v_m^T,       y_t = H_t^T q_t.
+// Chunked-WY form over a chunk of C tokens (M = nh C micro-rows), with Hc the
+// state entering the chunk:
+//     KK = K K^T,  L = strict_lower(KK) * beta_col,  Tm = I + L
+//     U  = Tm^-1 (V - K Hc) = U0 - W Hc,   U0 = Tm^-1 V,  W = Tm^-1 K
+//     P  = (Q K^T) * beta_col * read,  read[t][m] = (m < (t+1) nh)
+//     y  = Q Hc + P U,   H_next = Hc + K^T (beta_row * U).
+// Backward (reference src/mingru/triton_scans.py:473-605), with dHn the
+// gradient of the state leaving the chunk:
+//     G  = Tm^-T (P^T dy + beta_row * (K dHn)) = G0 + E dHn,
+//          G0 = Tm^-T P^T dy,  E = Tm^-T diag(beta) K
+//     dHc = dHn + Q^T dy - K^T G,   dV = G
+//     dQ = dy Hc^T + dS K,          dS = (dy U^T) * beta_col * read
+//     dK = dS^T Q + (beta_row U) dHn^T - G Hc^T + dKK K + dKK^T K,
+//          dKK = (-G U^T) * beta_col * strict
+//     dbeta_m = sum_j U[m][j] (K dHn)[m][j] + sum_t dP[t][m] S[t][m] read[t][m]
+//             + sum_i dT[i][m] KK[i][m] strict[i][m].
+//
+// Kernels (every matrix is zero-padded to 64 x 64; d_k, d_v <= 64, M <= 64):
+//   fwd_prep   grid (chunk, head): KK, blocked inverse Tm^-1, W, U0, P
+//   fwd_chain  grid (head * d_v slice): serial over chunks, H slice (64 x 16)
+//              resident; U = U0 - W H, y = Q H + P U, H += K^T (beta U);
+//              stores the chunk-entry states (saved for the backward)
+//   bwd_prep   grid (chunk, head): Tm^-1 again, U, P, E, G0, Q^T dy
+//   bwd_chain  grid (head * d_v slice): reverse serial pass, G = G0 + E dH,
+//              dH += Q^T dy - K^T G; stores G and the chunk-exit state grads
+//   bwd_grads  grid (chunk, head): dQ, dK, dV, dbeta from Hc, dHn, U, G.
+// The serial passes are split over d_v because both recurrences act on the
+// columns of H independently.  Products run on v_mfma_f32_16x16x4_f32 with
+// fp32 operands: the state, Tm^-1, U and every accumulation stay fp32 while
+// Q, K, V, beta (and y, dy and the input gradients) may be bf16 in HBM.
+#include "mg_common.h"
+
+#include <algorithm>
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int DN = 64;        // padded extent of every chunk matrix
+constexpr int LD = 65;        // LDS row stride (floats): conflict-free row and column reads
+constexpr int LDS16 = 17;     // LDS row stride of 16-column slices
+constexpr int NT = 256;       // threads per workgroup (4 waves)
+constexpr int SLICE = 16;     // d_v columns per chain workgroup
+constexpr int MAT = DN * DN;  // floats per padded chunk matrix in the workspace
+
+struct DwGeom {
+  int64_t T;   // tokens per head
+  int nh;      // micro-steps per token
+  int dk, dv;  // head dims
+  int C;       // tokens per chunk
+  int nc;      // chunks per head
+  int ns;      // d_v slices per head
+};
+
+// ---- element access: fp32 or bf16 (uint16_t storage, round-to-nearest-even) ----
+__device__ __forceinline__ float ldf(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float ldf(const uint16_t* p, int64_t i) {
+  return __uint_as_float((unsigned)p[i] << 16);
+}
+__device__ __forceinline__ uint16_t f2bf(float v) {
+  unsigned u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ void stf(float* p, int64_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void stf(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// acc += A (16 x KD) * B (KD x 16) with A[i][k] = a[i*ars + k*acs], B[k][j] = b[k*brs + j*bcs].
+// Lane group g = lane/16 supplies k in [g*KD/4, (g+1)*KD/4) over the KD/4 steps; any
+// bijection of k works as long as A and B agree, and this one keeps each lane's
+// k range contiguous.
+template <int KD>
+__device__ __forceinline__ floatx4 mma(floatx4 acc, const float* a, int ars, int acs,
+                                       const float* b, int brs, int bcs, float sa = 1.f) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < KD / 4; ++s) {
+    const int k = (KD / 4) * g + s;
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sa * a[r * ars + k * acs], b[k * brs + r * bcs],
+                                               acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// Accumulator layout: lane (g, r) holds rows 4g..4g+3 of column r.
+__device__ __forceinline__ void acc_store_lds(floatx4 acc, float* dst, int ld) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[(4 * g + i) * ld + r] = acc[i];
+}
+__device__ __forceinline__ floatx4 acc_load_lds(const float* src, int ld) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = src[(4 * g + i) * ld + r];
+  return acc;
+}
+// Padded 64 x 64 workspace matrices (row stride DN).
+__device__ __forceinline__ void acc_store_ws(floatx4 acc, float* dst) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[(4 * g + i) * DN + r] = acc[i];
+}
+__device__ __forceinline__ floatx4 acc_load_ws(const float* src) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = src[(4 * g + i) * DN + r];
+  return acc;
+}
+
+__device__ __forceinline__ float tof(float x) { return x; }
+__device__ __forceinline__ float tof(uint16_t x) { return __uint_as_float((unsigned)x << 16); }
+
+// Register staging of a rows x cols block (row stride ldg) of a row-major global
+// matrix, written later to a 64 x 64 LDS matrix (stride LD) with zeros outside
+// the block.  Each thread holds 16 elements; every load is issued before any LDS
+// store, and full-width, 16-byte aligned blocks move as 16-byte vectors.
+template <typename TI>
+struct Tile {
+  static constexpr int EPV = 16 / sizeof(TI);  // elements per 16-byte vector
+  static constexpr int NV = 16 / EPV;          // vectors per thread
+  static constexpr int VPR = DN / EPV;         // vectors per 64-element row
+  uint4 q[NV];
+  bool vec;
+
+  __device__ __forceinline__ void load(const TI* src, int rows, int cols, int64_t ldg) {
+    vec = cols == DN && ldg == DN && (((uintptr_t)src) & 15u) == 0;
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = threadIdx.x + v * NT;
+        const int row = idx / VPR, col = (idx % VPR) * EPV;
+        q[v] = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + col)
+                          : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+      TI* e = reinterpret_cast<TI*>(q);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        const int row = idx >> 6, col = idx & 63;
+        e[k] = (row < rows && col < cols) ? src[(int64_t)row * ldg + col] : TI(0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* s) const {
+    const TI* e = reinterpret_cast<const TI*>(q);
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = threadIdx.x + v * NT;
+        const int row = idx / VPR, col = (idx % VPR) * EPV;
+#pragma unroll
+        for (int x = 0; x < EPV; ++x) s[row * LD + col + x] = tof(e[v * EPV + x]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        s[(idx >> 6) * LD + (idx & 63)] = tof(e[k]);
+      }
+    }
+  }
+};
+
+// Chunk geometry of chunk c: first token, valid tokens, valid micro-rows.
+struct Chunk {
+  int64_t t0;
+  int Ct, M;
+};
+__device__ __forceinline__ Chunk chunk_of(const DwGeom& g, int c) {
+  Chunk ch;
+  ch.t0 = (int64_t)c * g.C;
+  ch.Ct = (int)min((int64_t)g.C, g.T - ch.t0);
+  ch.M = ch.Ct * g.nh;
+  return ch;
+}
+
+// ---------------------------------------------------------------------------
+// Tm^-1 for Tm = I + L, L strictly lower (64 x 64 in LDS), blocked in 16 x 16:
+// diagonal blocks by forward substitution (one wave each), then
+// T_ab = -T_aa L_ab T_bb for the two 16-blocks below the diagonal of each
+// 32 x 32 half, then the lower-left 32 x 32 block -T_22' L' T_11'.
+// sT receives the full lower-triangular inverse with zeroed upper blocks.
+// ---------------------------------------------------------------------------
+__device__ void unit_lower_inverse(const float* sL, float* sT, float* sY) {
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
+  {
+    // Diagonal block w: column r of X = (I + L_ww)^-1; lane group g keeps rows
+    // 4q + g, q = 0..3.  X[i][r] = delta_ir - sum_k L[i][k] X[k][r].
+    const int o = 16 * w;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float p = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p += sL[(o + i) * LD + o + 4 * q + g] * x[q];
+      p += __shfl_xor(p, 16);
+      p += __shfl_xor(p, 32);
+      const float xi = (i == r ? 1.f : 0.f) - p;
+      if ((i & 3) == g) x[i >> 2] = xi;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + o + r] = x[q];
+    // Zero the blocks right of the diagonal in block-row w.
+    for (int jb = w + 1; jb < 4; ++jb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + 16 * jb + r] = 0.f;
+  }
+  __syncthreads();
+  if (w < 2) {
+    // Blocks (1,0) and (3,2).
+    const int a = 2 * w + 1, b = 2 * w;
+    floatx4 y = mma<16>(zero4(), sL + 16 * a * LD + 16 * b, LD, 1, sT + 16 * b * LD + 16 * b, LD, 1);
+    floatx4 t = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(-sT[(16 * a + r) * LD + 16 * a + 4 * g + s], y[s], t,
+                                               0, 0, 0);
+    acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
+  }
+  __syncthreads();
+  {
+    // Lower-left 32 x 32: Y = L[32:64, 0:32] T[0:32, 0:32], then -T[32:64, 32:64] Y.
+    const int a = 2 + (w >> 1), b = w & 1;
+    floatx4 y = mma<32>(zero4(), sL + 16 * a * LD, LD, 1, sT + 16 * b, LD, 1);
+    acc_store_lds(y, sY + b * 32 * LDS16 + (a - 2) * 16 * LDS16, LDS16);
+    __syncthreads();
+    floatx4 t = mma<32>(zero4(), sT + 16 * a * LD + 32, LD, 1, sY + b * 32 * LDS16, LDS16, 1, -1.f);
+    acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
+  }
+  __syncthreads();
+}
+
+// L = strict_lower(K K^T) * beta_col into sL; wave w builds block-row w.
+__device__ __forceinline__ void build_L(const float* sK, const float* sb, float* sL) {
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 acc = zero4();
+    if (J <= w) acc = mma<64>(acc, sK + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * w + 4 * g + i, col = 16 * J + r;
+      sL[row * LD + col] = col < row ? acc[i] * sb[col] : 0.f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename TI>
+__global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, const TI* __restrict__ K,
+                                                  const TI* __restrict__ V, const TI* __restrict__ beta,
+                                                  float* __restrict__ Wo, float* __restrict__ U0o,
+                                                  float* __restrict__ Po, DwGeom g) {
+  __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD];
+  __shared__ float sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;  // first micro-row of the chunk
+  Tile<TI> tk, tv, tq;
+  tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+  tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+  tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
+  const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+  tk.store(sK);
+  tv.store(sV);
+  if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  __syncthreads();
+  build_L(sK, sb, sL);
+  __syncthreads();
+  unit_lower_inverse(sL, sT, sY);
+  // sL is free: Q goes there for P.
+  tq.store(sL);
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 wa = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
+    acc_store_ws(wa, Wo + mat + 16 * w * DN + 16 * J);
+    floatx4 ua = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sV + 16 * J, LD, 1);
+    acc_store_ws(ua, U0o + mat + 16 * w * DN + 16 * J);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 s = mma<64>(zero4(), sL + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
+      s[i] = (m < (t + 1) * g.nh) ? s[i] * sb[m] : 0.f;
+    }
+    acc_store_ws(s, Po + mat + 16 * w * DN + 16 * J);
+  }
+}
+
+// Loads 16 consecutive floats (a lane's A-fragment row segment for KD = 64).
+__device__ __forceinline__ void load16(float (&a)[16], const float* p) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float4 x = q[v];
+    a[4 * v] = x.x;
+    a[4 * v + 1] = x.y;
+    a[4 * v + 2] = x.z;
+    a[4 * v + 3] = x.w;
+  }
+}
+
+// acc += sign * A B with A's row segment held in registers (KD = 64) and B in LDS.
+__device__ __forceinline__ floatx4 mma_reg(floatx4 acc, const float (&a)[16], const float* b,
+                                           int brs, float sa) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sa * a[s], b[(16 * g + s) * brs + r], acc, 0, 0, 0);
+  return acc;
+}
+
+template <typename TI>
+__global__ __launch_bounds__(NT) void dw_fwd_chain(const TI* __restrict__ Q, const TI* __restrict__ K,
+                                                   const TI* __restrict__ beta,
+                                                   const float* __restrict__ H0,
+                                                   const float* __restrict__ Wm,
+                                                   const float* __restrict__ U0m,
+                                                   const float* __restrict__ Pm, TI* __restrict__ y,
+                                                   float* __restrict__ HT, float* __restrict__ Hb,
+                                                   DwGeom g) {
+  __shared__ float sK[2][DN * LD], sQ[2][DN * LD];
+  __shared__ float sb[2][DN];
+  __shared__ float sH[DN * LDS16], sU[DN * LDS16];
+  const int64_t bh = blockIdx.x / g.ns;
+  const int col0 = (blockIdx.x % g.ns) * SLICE;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  // H slice rows 16w..16w+15 (d_k), columns col0..col0+15 (d_v), accumulator layout.
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  // Operands of chunk c + 1 are fetched into registers while chunk c computes.
+  Tile<TI> tk, tq;
+  float bv, wa[16], pa[16];
+  floatx4 u0;
+  auto fetch = [&](int c) {
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
+    bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    load16(wa, Wm + mat + (16 * w + r) * DN + 16 * gg);
+    load16(pa, Pm + mat + (16 * w + r) * DN + 16 * gg);
+    u0 = acc_load_ws(U0m + mat + 16 * w * DN + col0);
+  };
+  fetch(0);
+  for (int c = 0; c < g.nc; ++c) {
+    const int buf = c & 1;
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    tk.store(sK[buf]);
+    tq.store(sQ[buf]);
+    if (threadIdx.x < DN) sb[buf][threadIdx.x] = bv;
+    float wc[16], pc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      wc[i] = wa[i];
+      pc[i] = pa[i];
+    }
+    floatx4 u = u0;
+    if (c + 1 < g.nc) fetch(c + 1);
+    acc_store_lds(h, sH + 16 * w * LDS16, LDS16);
+    acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
+    __syncthreads();
+    u = mma_reg(u, wc, sH, LDS16, -1.f);  // U = U0 - W H (rows 16w.. of the micro-steps)
+    acc_store_lds(u, sU + 16 * w * LDS16, LDS16);
+    floatx4 yy = mma<64>(zero4(), sQ[buf] + 16 * w * LD, LD, 1, sH, LDS16, 1);
+    __syncthreads();
+    yy = mma_reg(yy, pc, sU, LDS16, 1.f);  // + P U
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i;
+      if (t < ch.Ct && col < g.dv) stf(y, (bh * g.T + ch.t0 + t) * g.dv + col, yy[i]);
+    }
+    // H += K^T (beta U): A[i][m] = beta_m K[m][16w + i].
+    {
+      const float* kb = sK[buf];
+      const float* bb = sb[buf];
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int m = 16 * gg + s;
+        h = __builtin_amdgcn_mfma_f32_16x16x4f32(bb[m] * kb[m * LD + 16 * w + r],
+                                                 sU[m * LDS16 + r], h, 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) HT[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+template <typename TI>
+__global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, const TI* __restrict__ K,
+                                                  const TI* __restrict__ V, const TI* __restrict__ beta,
+                                                  const TI* __restrict__ dy,
+                                                  const float* __restrict__ Hb,
+                                                  float* __restrict__ Uo, float* __restrict__ Eo,
+                                                  float* __restrict__ G0o, float* __restrict__ QdYo,
+                                                  DwGeom g) {
+  __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD], sX[DN * LD];
+  __shared__ float sQ[DN * LD], sD[DN * LD];
+  __shared__ float sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  {
+    Tile<TI> tk, tv, tq, td;
+    Tile<float> th;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+    th.load(Hb + mat, g.dk, g.dv, DN);
+    tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + (bh * g.T + ch.t0) * g.dv, ch.Ct, g.dv, g.dv);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.store(sK);
+    tv.store(sV);
+    th.store(sX);
+    tq.store(sQ);
+    td.store(sD);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  }
+  __syncthreads();
+  build_L(sK, sb, sL);
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  // R = V - K Hc in place in sV (tile (w, J) read and written by wave w only).
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 acc = acc_load_lds(sV + 16 * w * LD + 16 * J, LD);
+    acc = mma<64>(acc, sK + 16 * w * LD, LD, 1, sX + 16 * J, LD, 1, -1.f);
+    acc_store_lds(acc, sV + 16 * w * LD + 16 * J, LD);
+  }
+  __syncthreads();
+  unit_lower_inverse(sL, sT, sY);
+  // U = Tm^-1 R; P = (Q K^T) * beta_col * read into sL (free now).
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 u = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sV + 16 * J, LD, 1);
+    acc_store_ws(u, Uo + mat + 16 * w * DN + 16 * J);
+    floatx4 s = mma<64>(zero4(), sQ + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
+      s[i] = (m < (t + 1) * g.nh) ? s[i] * sb[m] : 0.f;
+    }
+    acc_store_lds(s, sL + 16 * w * LD + 16 * J, LD);
+  }
+  __syncthreads();
+  // D1 = P^T dy into sX (Hc no longer needed); Q^T dy and E = Tm^-T diag(beta) K out.
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 d1 = mma<64>(zero4(), sL + 16 * w, 1, LD, sD + 16 * J, LD, 1);
+    acc_store_lds(d1, sX + 16 * w * LD + 16 * J, LD);
+    floatx4 qd = mma<64>(zero4(), sQ + 16 * w, 1, LD, sD + 16 * J, LD, 1);
+    acc_store_ws(qd, QdYo + mat + 16 * w * DN + 16 * J);
+  }
+  // sK := diag(beta) K for E, once every wave is done with the unscaled K.
+  __syncthreads();
+  for (int e = threadIdx.x; e < DN * DN; e += NT) {
+    const int i = e >> 6, j = e & 63;
+    sK[i * LD + j] *= sb[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 ea = mma<64>(zero4(), sT + 16 * w, 1, LD, sK + 16 * J, LD, 1);
+    acc_store_ws(ea, Eo + mat + 16 * w * DN + 16 * J);
+    floatx4 g0 = mma<64>(zero4(), sT + 16 * w, 1, LD, sX + 16 * J, LD, 1);
+    acc_store_ws(g0, G0o + mat + 16 * w * DN + 16 * J);
+  }
+}
+
+template <typename TI>
+__global__ __launch_bounds__(NT) void dw_bwd_chain(const TI* __restrict__ K,
+                                                   const float* __restrict__ dHT,
+                                                   const float* __restrict__ Em,
+                                                   const float* __restrict__ G0m,
+                                                   const float* __restrict__ QdYm,
+                                                   float* __restrict__ Gm, float* __restrict__ dHn,
+                                                   float* __restrict__ dH0, DwGeom g) {
+  __shared__ float sK[2][DN * LD];
+  __shared__ float sH[DN * LDS16], sG[DN * LDS16];
+  const int64_t bh = blockIdx.x / g.ns;
+  const int col0 = (blockIdx.x % g.ns) * SLICE;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  Tile<TI> tk;
+  float ea[16];
+  floatx4 g0, qd0;
+  auto fetch = [&](int c) {
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    tk.load(K + (bh * g.T + ch.t0) * g.nh * g.dk, ch.M, g.dk, g.dk);
+    load16(ea, Em + mat + (16 * w + r) * DN + 16 * gg);
+    g0 = acc_load_ws(G0m + mat + 16 * w * DN + col0);
+    qd0 = acc_load_ws(QdYm + mat + 16 * w * DN + col0);
+  };
+  fetch(g.nc - 1);
+  for (int c = g.nc - 1; c >= 0; --c) {
+    const int buf = c & 1;
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    tk.store(sK[buf]);
+    float ec[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ec[i] = ea[i];
+    floatx4 gacc = g0;
+    const floatx4 qd = qd0;
+    if (c > 0) fetch(c - 1);
+    acc_store_lds(h, sH + 16 * w * LDS16, LDS16);
+    acc_store_ws(h, dHn + mat + 16 * w * DN + col0);
+    __syncthreads();
+    gacc = mma_reg(gacc, ec, sH, LDS16, 1.f);  // G = G0 + E dH
+    acc_store_ws(gacc, Gm + mat + 16 * w * DN + col0);
+    acc_store_lds(gacc, sG + 16 * w * LDS16, LDS16);
+    __syncthreads();
+    // dH += Q^T dy - K^T G: A[i][m] = K[m][16w + i].
+    h += qd;
+    const float* kb = sK[buf];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int m = 16 * gg + s;
+      h = __builtin_amdgcn_mfma_f32_16x16x4f32(-kb[m * LD + 16 * w + r], sG[m * LDS16 + r], h, 0,
+                                               0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) dH0[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
+// Column sums of a tile (over the 4 rows of each lane and the 4 lane groups)
+// written to s[col]; every (slot, column) is written by exactly one lane, so the
+// final reduction order is fixed and the result bitwise reproducible.
+__device__ __forceinline__ void put_colsum(floatx4 v, float* s, int col) {
+  float p = v[0] + v[1] + v[2] + v[3];
+  p += __shfl_xor(p, 16);
+  p += __shfl_xor(p, 32);
+  if (lane_id() < 16) s[col] = p;
+}
+
+template <typename TI>
+__global__ __launch_bounds__(NT) void dw_bwd_grads(
+    const TI* __restrict__ Q, const TI* __restrict__ K, const TI* __restrict__ beta,
+    const TI* __restrict__ dy, const float* __restrict__ Hb, const float* __restrict__ dHn,
+    const float* __restrict__ Um, const float* __restrict__ Gm, TI* __restrict__ dQ,
+    TI* __restrict__ dK, TI* __restrict__ dV, TI* __restrict__ dbeta, DwGeom g) {
+  __shared__ float sK[DN * LD], sQ[DN * LD], sD[DN * LD], sU[DN * LD], sG[DN * LD],
+      sH[DN * LD], sX[DN * LD];
+  __shared__ float sb[DN];
+  // dbeta partials: [0..3] read-term column sums per wave, [4..7] strict-term
+  // column sums per wave, [8] row sums of U * (K dHn).
+  __shared__ float sdb[9][DN];
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  Tile<float> tn;  // dHn, stored once Hc is no longer needed
+  {
+    Tile<TI> tk, tq, td;
+    Tile<float> tu, tg, th;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
+    tu.load(Um + mat, ch.M, g.dv, DN);
+    tg.load(Gm + mat, ch.M, g.dv, DN);
+    th.load(Hb + mat, g.dk, g.dv, DN);
+    tn.load(dHn + mat, g.dk, g.dv, DN);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.store(sK);
+    tq.store(sQ);
+    td.store(sD);
+    tu.store(sU);
+    tg.store(sG);
+    th.store(sH);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  }
+  __syncthreads();
+  // S = Q K^T, dP = dy U^T (rows = tokens of block w, cols = micro-rows of block J).
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 s = mma<64>(zero4(), sQ + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+    floatx4 dp = mma<64>(zero4(), sD + 16 * w * LD, LD, 1, sU + 16 * J * LD, 1, LD);
+    floatx4 ds, db;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
+      const bool rd = m < (t + 1) * g.nh;
+      ds[i] = rd ? dp[i] * sb[m] : 0.f;
+      db[i] = rd ? dp[i] * s[i] : 0.f;
+    }
+    acc_store_lds(ds, sX + 16 * w * LD + 16 * J, LD);
+    put_colsum(db, sdb[w], 16 * J + r);
+  }
+  __syncthreads();
+  // dQ = dy Hc^T + dS K; dK (kept in registers) = dS^T Q - G Hc^T.
+  floatx4 dk[4];
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 q = mma<64>(zero4(), sD + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD);
+    q = mma<64>(q, sX + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i, d = 16 * J + r;
+      if (t < ch.Ct && d < g.dk) stf(dQ, (trow0 + t) * g.dk + d, q[i]);
+    }
+    floatx4 a = mma<64>(zero4(), sX + 16 * w, 1, LD, sQ + 16 * J, LD, 1);
+    dk[J] = mma<64>(a, sG + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD, -1.f);
+  }
+  __syncthreads();
+  // dT = -G U^T, KK = K K^T; dKK = dT * beta_col * strict into sX.  dHn into sH.
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 dt = mma<64>(zero4(), sG + 16 * w * LD, LD, 1, sU + 16 * J * LD, 1, LD, -1.f);
+    floatx4 kk = mma<64>(zero4(), sK + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+    floatx4 dkk, db;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * w + 4 * gg + i, j = 16 * J + r;
+      const bool st = j < m;
+      dkk[i] = st ? dt[i] * sb[j] : 0.f;
+      db[i] = st ? dt[i] * kk[i] : 0.f;
+    }
+    acc_store_lds(dkk, sX + 16 * w * LD + 16 * J, LD);
+    put_colsum(db, sdb[4 + w], 16 * J + r);
+  }
+  tn.store(sH);
+  __syncthreads();
+  // dK += dKK K + dKK^T K + (beta_row U) dHn^T; dbeta += rowsum(U * (K dHn)).
+  float rowp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    floatx4 a = mma<64>(dk[J], sX + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
+    a = mma<64>(a, sX + 16 * w, 1, LD, sK + 16 * J, LD, 1);
+    floatx4 bu = mma<64>(zero4(), sU + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD);
+    floatx4 x = mma<64>(zero4(), sK + 16 * w * LD, LD, 1, sH + 16 * J, LD, 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * w + 4 * gg + i, d = 16 * J + r;
+      a[i] += sb[m] * bu[i];
+      if (m < ch.M && d < g.dk) stf(dK, (row0 + m) * g.dk + d, a[i]);
+      // row sum over the 16 columns of this tile
+      float p = sU[m * LD + 16 * J + r] * x[i];
+      p += __shfl_xor(p, 1);
+      p += __shfl_xor(p, 2);
+      p += __shfl_xor(p, 4);
+      p += __shfl_xor(p, 8);
+      rowp[i] += p;
+    }
+  }
+  if (r == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sdb[8][16 * w + 4 * gg + i] = rowp[i];
+  }
+  // dV = G.
+  for (int e = threadIdx.x; e < DN * DN; e += NT) {
+    const int m = e >> 6, j = e & 63;
+    if (m < ch.M && j < g.dv) stf(dV, (row0 + m) * g.dv + j, sG[m * LD + j]);
+  }
+  __syncthreads();
+  if (threadIdx.x < ch.M) {
+    const int m = threadIdx.x;
+    float acc = sdb[8][m];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc += sdb[q][m];
+    stf(dbeta, row0 + m, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------
+bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk, DwGeom& g,
+             int64_t& BH) {
+  if (B <= 0 || H <= 0 || T <= 0 || nh <= 0 || chunk <= 0) return false;
+  if (dk <= 0 || dk > DN || dv <= 0 || dv > DN || (int64_t)nh * chunk > DN) return false;
+  BH = B * H;
+  g.T = T;
+  g.nh = nh;
+  g.dk = dk;
+  g.dv = dv;
+  g.C = chunk;
+  const int64_t nc = (T + chunk - 1) / chunk;
+  if (nc > 65535 || BH > 65535 || BH * ((dv + SLICE - 1) / SLICE) > (1ll << 31) - 1) return false;
+  g.nc = (int)nc;
+  g.ns = (dv + SLICE - 1) / SLICE;
+  return true;
+}
+
+size_t dw_mat_bytes(int64_t BH, const DwGeom& g) { return (size_t)BH * g.nc * MAT * sizeof(float); }
+
+template <typename TI>
+int dw_fwd(const void* Q, const void* K, const void* V, const void* beta, const float* H0, void* y,
+           float* HT, float* Hb, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
+           hipStream_t stream) {
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 3 * mb) return MG_ERR_WORKSPACE;
+  float* Wm = (float*)ws;
+  float* U0m = (float*)((char*)ws + mb);
+  float* Pm = (float*)((char*)ws + 2 * mb);
+  hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
+                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3((unsigned)(BH * g.ns)), dim3(NT), 0, stream,
+                     (const TI*)Q, (const TI*)K, (const TI*)beta, H0, Wm, U0m, Pm, (TI*)y, HT, Hb,
+                     g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+template <typename TI>
+int dw_bwd(const void* Q, const void* K, const void* V, const void* beta, const float* Hb,
+           const void* dy, const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
+           float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
+           hipStream_t stream) {
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 6 * mb) return MG_ERR_WORKSPACE;
+  float* Um = (float*)ws;
+  float* Em = (float*)((char*)ws + mb);
+  float* G0m = (float*)((char*)ws + 2 * mb);
+  float* QdYm = (float*)((char*)ws + 3 * mb);
+  float* Gm = (float*)((char*)ws + 4 * mb);
+  float* dHn = (float*)((char*)ws + 5 * mb);
+  hipLaunchKernelGGL(dw_bwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
+                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, (const TI*)dy, Hb,
+                     Um, Em, G0m, QdYm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3((unsigned)(BH * g.ns)), dim3(NT), 0, stream,
+                     (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dw_bwd_grads<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
+                     (const TI*)Q, (const TI*)K, (const TI*)beta, (const TI*)dy, Hb, dHn, Um, Gm,
+                     (TI*)dQ, (TI*)dK, (TI*)dV, (TI*)dbeta, g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+size_t mg_delta_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
+                                int chunk) {
+  DwGeom g;
+  int64_t BH;
+  if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return 256;
+  return 6 * dw_mat_bytes(BH, g);
+}
+
+size_t mg_delta_state_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk) {
+  DwGeom g;
+  int64_t BH;
+  if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return 0;
+  return dw_mat_bytes(BH, g);
+}
+
+int mg_delta_fwd(const void* Q, const void* K, const void* V, const void* beta, const float* H0,
+                 void* y, float* HT, float* Hbound, int64_t B, int64_t H, int64_t T, int nh, int dk,
+                 int dv, int chunk, int dtype, void* ws, size_t ws_bytes, hipStream_t stream) {
+  DwGeom g;
+  int64_t BH;
+  if (!Q || !K || !V || !beta || !H0 || !y || !HT || !Hbound || !ws) return MG_ERR_ARG;
+  if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
+  if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
+  if (dtype == 0)
+    return dw_fwd<float>(Q, K, V, beta, H0, y, HT, Hbound, BH, g, ws, ws_bytes, stream);
+  if (dtype == 1)
+    return dw_fwd<uint16_t>(Q, K, V, beta, H0, y, HT, Hbound, BH, g, ws, ws_bytes, stream);
+  return MG_ERR_ARG;
+}
+
+int mg_delta_bwd(const void* Q, const void* K, const void* V, const void* beta,
+                 const float* Hbound, const void* dy, const float* dHT, void* dQ, void* dK,
+                 void* dV, void* dbeta, float* dH0, int64_t B, int64_t H, int64_t T, int nh,
+                 int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
+                 hipStream_t stream) {
+  DwGeom g;
+  int64_t BH;
+  if (!Q || !K || !V || !beta || !Hbound || !dy || !dHT || !dQ || !dK || !dV || !dbeta || !dH0 ||
+      !ws)
+    return MG_ERR_ARG;
+  if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
+  if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
+  if (dtype == 0)
+    return dw_bwd<float>(Q, K, V, beta, Hbound, dy, dHT, dQ, dK, dV, dbeta, dH0, BH, g, ws,
+                         ws_bytes, stream);
+  if (dtype == 1)
+    return dw_bwd<uint16_t>(Q, K, V, beta, Hbound, dy, dHT, dQ, dK, dV, dbeta, dH0, BH, g, ws,
+                            ws_bytes, stream);
+  return MG_ERR_ARG;
+}
+
+}  // extern "C"

@@ -46,11 +46,13 @@ _AFFINE_V = frozenset({1, 2, 4, 8, 16})
 _ANGLE_K = frozenset({2, 4, 8})
 _ANGLE_MAX_ROT = 64
 
-# DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``):
-# d_k = d_v in this set, chunk_size <= 64, nh * chunk_size <= 64.
-_DELTA_DK = frozenset({16, 32, 64})
+# DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``).  The
+# kernels zero-pad every chunk matrix to 64 x 64, so any d_k, d_v up to 64 runs
+# (d_k need not equal d_v) and a chunk holds at most 64 micro-steps.
+_DELTA_MAX_DIM = 64
 _DELTA_MAX_CHUNK = 64
 _DELTA_MAX_MICROSTEPS = 64
+_DELTA_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 _SUPPORTED_ARCH = "gfx950"
 
@@ -517,6 +519,149 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
     flags = (1 if has_scale else 0) | (2 if has_decay else 0)
     return _funnel("angle-fused", _AngleScanFn.apply, theta, scale, gamma, b, h0, sched, rounds,
                    flags)
+
+
+# ---------------------------------------------------------------------------
+# DeltaMinGRU chunked-WY
+# ---------------------------------------------------------------------------
+
+
+def _delta_envelope_reason(*, is_cuda: bool, q_dtype, k_dtype, v_dtype, beta_dtype, h0_dtype,
+                           d_k: int, d_v: int, chunk_size: int, nh: int) -> str | None:
+    """Human-readable rejection reason, or ``None`` inside the envelope.
+
+    Works on plain descriptors so every branch is reachable from a CPU test
+    (reference ``src/mingru/triton_scans.py:335-389``); each violation yields a
+    distinct string.  Q, K, V and beta may be float32, bfloat16 or float16 (the
+    kernels read bf16 natively and compute in fp32; fp16 is upcast); H0 may be
+    any of those.  float64 stays on the eager path.
+    """
+    if not is_cuda:
+        return "DeltaMinGRU HIP kernel requires GPU tensors (got a non-GPU tensor)"
+    for name, dt in (("Q", q_dtype), ("K", k_dtype), ("V", v_dtype), ("beta", beta_dtype),
+                     ("H0", h0_dtype)):
+        if dt not in _DELTA_DTYPES:
+            return (f"DeltaMinGRU HIP kernel takes float32, bfloat16 or float16 inputs "
+                    f"(got {name} dtype {dt})")
+    if not 1 <= d_k <= _DELTA_MAX_DIM:
+        return f"DeltaMinGRU HIP kernel needs 1 <= d_k <= {_DELTA_MAX_DIM} (got d_k={d_k})"
+    if not 1 <= d_v <= _DELTA_MAX_DIM:
+        return f"DeltaMinGRU HIP kernel needs 1 <= d_v <= {_DELTA_MAX_DIM} (got d_v={d_v})"
+    if not 1 <= chunk_size <= _DELTA_MAX_CHUNK:
+        return (f"DeltaMinGRU HIP kernel chunk_size must be in [1, {_DELTA_MAX_CHUNK}] "
+                f"(got chunk_size={chunk_size})")
+    if nh * chunk_size > _DELTA_MAX_MICROSTEPS:
+        return (f"DeltaMinGRU HIP kernel requires nh * chunk_size <= {_DELTA_MAX_MICROSTEPS} "
+                f"(got nh={nh}, chunk_size={chunk_size}, product={nh * chunk_size})")
+    return None
+
+
+def _delta_validate_envelope(Q, K, V, beta, H0, chunk_size: int) -> None:
+    """Raise ``ScanFallback`` unless the kernel layouts are eligible
+    (reference ``src/mingru/triton_scans.py:392-452``)."""
+    if Q.ndim != 4 or K.ndim != 5 or V.ndim != 5 or beta.ndim != 4 or H0.ndim != 4:
+        raise ScanFallback(
+            "DeltaMinGRU HIP kernel needs 4-D Q (B, n_heads, T, d_k), 5-D K "
+            "(B, n_heads, T, nh, d_k), 5-D V (B, n_heads, T, nh, d_v), 4-D beta "
+            "(B, n_heads, T, nh) and 4-D H0 (B, n_heads, d_k, d_v); got ranks "
+            f"Q={Q.ndim}, K={K.ndim}, V={V.ndim}, beta={beta.ndim}, H0={H0.ndim}"
+        )
+    Bn, nhd, T, d_k = Q.shape
+    nh = K.shape[3]
+    d_v = V.shape[4]
+    if (
+        tuple(K.shape[:3]) != (Bn, nhd, T)
+        or K.shape[4] != d_k
+        or tuple(V.shape[:3]) != (Bn, nhd, T)
+        or V.shape[3] != nh
+        or tuple(beta.shape) != (Bn, nhd, T, nh)
+        or tuple(H0.shape) != (Bn, nhd, d_k, d_v)
+    ):
+        raise ScanFallback(
+            "DeltaMinGRU HIP kernel shapes disagree: from Q=(B, n_heads, T, d_k)="
+            f"{tuple(Q.shape)} expected K={(Bn, nhd, T, nh, d_k)}, V={(Bn, nhd, T, nh, d_v)}, "
+            f"beta={(Bn, nhd, T, nh)}, H0={(Bn, nhd, d_k, d_v)}; got K={tuple(K.shape)}, "
+            f"V={tuple(V.shape)}, beta={tuple(beta.shape)}, H0={tuple(H0.shape)}"
+        )
+    reason = _delta_envelope_reason(
+        is_cuda=Q.is_cuda and K.is_cuda and V.is_cuda and beta.is_cuda and H0.is_cuda,
+        q_dtype=Q.dtype, k_dtype=K.dtype, v_dtype=V.dtype, beta_dtype=beta.dtype,
+        h0_dtype=H0.dtype, d_k=d_k, d_v=d_v, chunk_size=chunk_size, nh=nh,
+    )
+    if reason is not None:
+        raise ScanFallback(reason)
+
+
+def _delta_compute_dtype(*ts):
+    """bf16 when Q, K, V and beta are all bf16 (read natively), else fp32."""
+    return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in ts) else torch.float32
+
+
+def _contig(t, dtype):
+    t = t.to(dtype).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class _DeltaScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, beta, H0, chunk_size):
+        cdt = _delta_compute_dtype(Q, K, V, beta)
+        q, k, v, bt = (_contig(t, cdt) for t in (Q, K, V, beta))
+        h0 = _contig(H0, torch.float32)
+        Bn, nhd, T, d_k = q.shape
+        nh = k.shape[3]
+        d_v = v.shape[4]
+        lib = _lib()
+        dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
+        y = torch.empty(Bn, nhd, T, d_v, dtype=cdt, device=q.device)
+        HT = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+        Hb = torch.empty(max(int(lib.mg_delta_state_bytes(*dims)), 16) // 4, dtype=torch.float32,
+                         device=q.device)
+        ws = _workspace(lib.mg_delta_workspace_bytes(*dims), q.device)
+        _call("mg_delta_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(h0), _ptr(y), _ptr(HT),
+              _ptr(Hb), *dims[:6], chunk_size, 1 if cdt == torch.bfloat16 else 0, _ptr(ws),
+              ws.numel(), _stream(q))
+        ctx.save_for_backward(q, k, v, bt, Hb)
+        ctx.meta = (chunk_size, cdt, Q.dtype, K.dtype, V.dtype, beta.dtype, H0.dtype)
+        return y.to(Q.dtype), HT.to(H0.dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gy, gHT):
+        q, k, v, bt, Hb = ctx.saved_tensors
+        chunk_size, cdt, qdt, kdt, vdt, bdt, hdt = ctx.meta
+        Bn, nhd, T, d_k = q.shape
+        nh = k.shape[3]
+        d_v = v.shape[4]
+        dy = (torch.zeros(Bn, nhd, T, d_v, dtype=cdt, device=q.device) if gy is None
+              else _contig(gy, cdt))
+        dHT = (torch.zeros(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+               if gHT is None else _contig(gHT, torch.float32))
+        dQ, dK, dV, dbeta = (torch.empty_like(t) for t in (q, k, v, bt))
+        dH0 = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+        dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
+        ws = _workspace(_lib().mg_delta_workspace_bytes(*dims), q.device)
+        _call("mg_delta_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(Hb), _ptr(dy), _ptr(dHT),
+              _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dbeta), _ptr(dH0), *dims[:6], chunk_size,
+              1 if cdt == torch.bfloat16 else 0, _ptr(ws), ws.numel(), _stream(q))
+        return dQ.to(qdt), dK.to(kdt), dV.to(vdt), dbeta.to(bdt), dH0.to(hdt), None
+
+
+def delta_scan_impl(Q, K, V, beta, H0, *, chunk_size: int):
+    """DeltaMinGRU chunked-WY forward on the kernel layouts; returns ``(y, H_T)``.
+
+    Same contract as the reference entry point
+    (``src/mingru/triton_scans.py:2403-2447``): ``Q`` ``(B, n_heads, T, d_k)``,
+    ``K`` ``(B, n_heads, T, nh, d_k)``, ``V`` ``(B, n_heads, T, nh, d_v)``,
+    ``beta`` ``(B, n_heads, T, nh)``, ``H0`` ``(B, n_heads, d_k, d_v)``; ``y``
+    ``(B, n_heads, T, d_v)`` in Q's dtype and ``H_T`` in H0's dtype.
+    Differentiable in all five tensors.
+    """
+    _delta_validate_envelope(Q, K, V, beta, H0, chunk_size)
+    if Q.shape[2] == 0:
+        return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
+    return _funnel("DeltaMinGRU chunked-WY", _DeltaScanFn.apply, Q, K, V, beta, H0,
+                   int(chunk_size))
 
 
 SCAN_IMPLS: dict = {
