@@ -1,0 +1,79 @@
+"""The C-ABI library: loads on a machine without a GPU, exports every entry point
+that ``include/*.h`` declares, and rejects invalid arguments on the host before
+any device call (status 1).  No kernel is launched here."""
+
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from mingru_amd import _native
+from mingru_amd import build as hip_build
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NULL = ctypes.c_void_p(0)
+
+
+def _declared():
+    names = []
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names += re.findall(r"^\s*(?:int|size_t)\s+(mg_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(hip_build.LIB_PATH):
+        hip_build.build()
+    return _native.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert len(names) >= 16
+    for fam in ("linear_scan", "log_scan", "affine_scan", "angle_scan", "delta"):
+        assert any(fam in n for n in names), fam
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in _declared() if getattr(lib, n, None) is None]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+
+
+def test_ctypes_table_matches_header(lib):
+    assert sorted(_native._SIGNATURES) == _declared()
+    assert sorted(_native.exported_names()) == _declared()
+
+
+def test_workspace_queries(lib):
+    assert lib.mg_linear_scan_workspace_bytes(16, 4096, 1024) >= 256
+    assert lib.mg_affine_scan_workspace_bytes(16, 4096, 256, 2, 1) >= 256
+    assert lib.mg_angle_scan_workspace_bytes(8, 2048, 64, 8) >= 256
+    # delta: six padded 64 x 64 fp32 matrices per (batch, head, chunk)
+    assert lib.mg_delta_workspace_bytes(8, 8, 8192, 1, 64, 64, 64) == 6 * 64 * 128 * 64 * 64 * 4
+    assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 64 * 128 * 64 * 64 * 4
+    # outside the envelope: the minimum / zero answer, never a crash
+    assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 16, 1) == 256
+    assert lib.mg_delta_state_bytes(1, 1, 8, 1, 65, 64, 8) == 0
+
+
+def test_invalid_arguments_are_rejected_on_the_host(lib):
+    one = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.mg_linear_scan_fwd(NULL, one, one, one, 1, 4, 4, one, 4096, NULL) == 1
+    assert lib.mg_linear_scan_fwd(one, one, one, one, 0, 4, 4, one, 4096, NULL) == 1
+    assert lib.mg_log_scan_fwd(one, one, NULL, 1, 4, 4, one, 4096, NULL) == 1
+    assert lib.mg_affine_scan_fwd(one, one, one, one, 1, 4, 4, 3, 1, one, 4096, NULL) == 1
+    assert lib.mg_angle_scan_fwd(one, one, one, one, one, one, 1, 4, 4, 6, 0, 3, 0, one, 4096,
+                                 NULL) == 1
+    # delta: d_k above 64, nh * chunk above 64, unknown dtype tag
+    assert lib.mg_delta_fwd(one, one, one, one, one, one, one, one, 1, 1, 8, 1, 65, 64, 8, 1,
+                            one, 1 << 20, NULL) == 1
+    assert lib.mg_delta_fwd(one, one, one, one, one, one, one, one, 1, 1, 8, 2, 64, 64, 33, 1,
+                            one, 1 << 20, NULL) == 1
+    assert lib.mg_delta_fwd(one, one, one, one, one, one, one, one, 1, 1, 8, 1, 64, 64, 8, 7,
+                            one, 1 << 20, NULL) == 1
+    assert lib.mg_delta_bwd(*([one] * 11), NULL, 1, 1, 8, 1, 64, 64, 8, 1, one, 1 << 20,
+                            NULL) == 1

@@ -1,0 +1,292 @@
+"""CPU-only contract tests for the ``MINGRU_SCAN`` seam and the HIP backend's
+envelope (reference behaviour: ``src/mingru/min_gru.py:85-668``,
+``src/mingru/triton_scans.py:166-177, 335-452``; the reference's own seam
+tests are ``tests/test_dispatch.py``).
+
+No GPU is touched: a stand-in object reports ``is_cuda = True`` to reach the
+GPU branches, the real backend then declines because no device is visible,
+and a fake backend module injected into ``sys.modules`` pins the value-level
+layout round trip of the DeltaMinGRU seam.
+"""
+
+import subprocess
+import sys
+import types
+import warnings
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import mingru_amd
+from mingru_amd import DeltaMinGRU, GivensMinGRU, hip_scans, linear_scan
+from mingru_amd import min_gru as mg
+
+BACKEND = "mingru_amd.hip_scans"
+
+
+class _FakeCudaTensor:
+    """Reports GPU residency; the seam reads only ``.is_cuda`` before the backend declines."""
+
+    is_cuda = True
+
+
+@pytest.fixture(autouse=True)
+def _isolate(monkeypatch):
+    monkeypatch.delenv("MINGRU_SCAN", raising=False)
+    for flag in ("_warned_scan_fallback", "_warned_angle_fallback", "_warned_delta_fallback",
+                 "_warned_delta_decay_fallback"):
+        monkeypatch.setattr(mg, flag, False)
+
+
+def _fresh_python(code: str) -> str:
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=300, cwd=mingru_amd.__path__[0] + "/..")
+    assert out.returncode == 0, out.stderr
+    return out.stdout.strip()
+
+
+# ---------------------------------------------------------------- modes
+
+
+def test_invalid_mode_raises_value_error(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "cuda")
+    a = torch.rand(1, 3, 2)
+    with pytest.raises(ValueError, match="MINGRU_SCAN"):
+        linear_scan(a, a)
+
+
+@pytest.mark.parametrize("mode", [None, "auto", "eager"])
+def test_cpu_paths_stay_eager_without_warning(monkeypatch, mode):
+    if mode:
+        monkeypatch.setenv("MINGRU_SCAN", mode)
+    a, b = torch.rand(2, 9, 3), torch.randn(2, 9, 3)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        A, Bc = linear_scan(a, b)
+    assert A.grad_fn is None or "LinearScanFn" not in type(A.grad_fn).__name__
+
+
+@pytest.mark.parametrize("mode", ["auto", "eager"])
+def test_cpu_never_imports_backend(mode):
+    """``import mingru_amd`` and CPU scans under auto/eager never load the backend."""
+    code = (
+        "import os, sys; os.environ['MINGRU_SCAN'] = %r\n"
+        "import torch, mingru_amd\n"
+        "a = torch.rand(1, 5, 4)\n"
+        "mingru_amd.linear_scan(a, a); mingru_amd.parallel_scan_log(a.log(), torch.zeros(1, 6, 4))\n"
+        "m = mingru_amd.DeltaMinGRU(4, 8, n_heads=2, chunk_size=2); m(torch.randn(1, 9, 4))\n"
+        "print(%r in sys.modules)" % (mode, BACKEND)
+    )
+    assert _fresh_python(code) == "False"
+
+
+def test_lazy_backend_names_resolve():
+    code = (
+        "import sys, mingru_amd\n"
+        "before = %r in sys.modules\n"
+        "fb = mingru_amd.ScanFallback\n"
+        "print(before, %r in sys.modules, fb.__name__, callable(mingru_amd.delta_scan_impl))"
+        % (BACKEND, BACKEND)
+    )
+    assert _fresh_python(code) == "False True ScanFallback True"
+
+
+@pytest.mark.parametrize("mode", ["hip", "triton"])
+def test_forcing_mode_raises_with_reason(monkeypatch, mode):
+    monkeypatch.setenv("MINGRU_SCAN", mode)
+    with pytest.raises(RuntimeError, match="device not available"):
+        mg._dispatch_scan("linear_scan", _FakeCudaTensor(), _FakeCudaTensor())
+
+
+def test_auto_gpu_fallback_warns_once_and_returns_none(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    with pytest.warns(UserWarning, match="fell back to the eager scan"):
+        assert mg._dispatch_scan("linear_scan", _FakeCudaTensor(), _FakeCudaTensor()) is None
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert mg._dispatch_scan("matrix_scan", _FakeCudaTensor(), _FakeCudaTensor()) is None
+
+
+def test_angle_and_delta_fallbacks_warn_independently(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    f = _FakeCudaTensor()
+    with pytest.warns(UserWarning, match="angle-fused"):
+        assert mg._dispatch_angle_scan(f, f, f, f, f, f, f, f, has_scale=0, has_decay=0) is None
+    with pytest.warns(UserWarning, match="DeltaMinGRU"):
+        assert mg._dispatch_delta_scan(f, [], [], [], f, chunk_size=4) is None
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert mg._dispatch_delta_scan(f, [], [], [], f, chunk_size=4) is None
+
+
+def test_delta_auto_region_gate(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    assert mg._delta_scan_should_try(True, T=128, chunk_size=64, d_k=64)
+    assert not mg._delta_scan_should_try(True, T=100, chunk_size=64, d_k=64)
+    assert not mg._delta_scan_should_try(True, T=4096, chunk_size=64, d_k=128)
+    assert not mg._delta_scan_should_try(False, T=4096, chunk_size=64, d_k=64)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    assert mg._delta_scan_should_try(True, T=3, chunk_size=64, d_k=128)
+    monkeypatch.setenv("MINGRU_SCAN", "eager")
+    assert not mg._delta_scan_should_try(True, T=4096, chunk_size=64, d_k=64)
+
+
+def test_delta_decay_guard(monkeypatch):
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with pytest.raises(RuntimeError, match="decay"):
+        mg._delta_decay_dispatch_guard(True)
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    with pytest.warns(UserWarning, match="decay"):
+        mg._delta_decay_dispatch_guard(True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        mg._delta_decay_dispatch_guard(True)
+        mg._delta_decay_dispatch_guard(False)
+
+
+# ---------------------------------------------------------------- backend envelope
+
+
+def test_backend_declines_without_gpu():
+    assert hip_scans.available() is not True
+    a = torch.rand(1, 4, 3)
+    with pytest.raises(hip_scans.ScanFallback):
+        hip_scans.SCAN_IMPLS["linear_scan"](a, a)
+
+
+_OK = dict(is_cuda=True, q_dtype=torch.bfloat16, k_dtype=torch.bfloat16, v_dtype=torch.bfloat16,
+           beta_dtype=torch.bfloat16, h0_dtype=torch.float32, d_k=64, d_v=64, chunk_size=64, nh=1)
+
+_VIOLATIONS = {
+    "non_gpu": dict(is_cuda=False),
+    "q": dict(q_dtype=torch.float64),
+    "k": dict(k_dtype=torch.int32),
+    "v": dict(v_dtype=torch.float64),
+    "beta": dict(beta_dtype=torch.float64),
+    "h0": dict(h0_dtype=torch.float64),
+    "dk": dict(d_k=65),
+    "dv": dict(d_v=0),
+    "chunk": dict(chunk_size=65),
+    "micro": dict(nh=2, chunk_size=33),
+}
+
+
+def test_delta_envelope_in_range_is_none():
+    assert hip_scans._delta_envelope_reason(**_OK) is None
+    assert hip_scans._delta_envelope_reason(**{**_OK, "d_k": 5, "d_v": 48, "nh": 4,
+                                               "chunk_size": 16}) is None
+
+
+def test_delta_envelope_reasons_are_distinct():
+    reasons = {}
+    for name, bad in _VIOLATIONS.items():
+        r = hip_scans._delta_envelope_reason(**{**_OK, **bad})
+        assert r is not None, name
+        reasons[name] = r
+    assert len(set(reasons.values())) == len(reasons)
+
+
+def test_delta_validate_envelope_shapes():
+    Q = torch.zeros(1, 2, 5, 4)
+    K = torch.zeros(1, 2, 5, 1, 4)
+    V = torch.zeros(1, 2, 5, 1, 3)
+    b = torch.zeros(1, 2, 5, 1)
+    H0 = torch.zeros(1, 2, 4, 3)
+    with pytest.raises(hip_scans.ScanFallback, match="ranks"):
+        hip_scans._delta_validate_envelope(Q[0], K, V, b, H0, 4)
+    with pytest.raises(hip_scans.ScanFallback, match="shapes disagree"):
+        hip_scans._delta_validate_envelope(Q, K, V, b, torch.zeros(1, 2, 3, 3), 4)
+    with pytest.raises(hip_scans.ScanFallback, match="GPU tensors"):
+        hip_scans._delta_validate_envelope(Q, K, V, b, H0, 4)
+
+
+def test_angle_schedule_classifier():
+    from mingru_amd import workloads as wl
+
+    perm, sgn, p2p = wl.lexicographic_schedule(8)
+    assert hip_scans._classify_schedule(perm, sgn, p2p, 8, 28, 1) == (hip_scans._SCHED_LEX, 28)
+    bp, bs, bq = hip_scans._brick_tables(8, 3)
+    assert hip_scans._classify_schedule(bp, bs, bq, 8, 3, 4) == (hip_scans._SCHED_BRICK, 3)
+    bad = perm.clone()
+    bad[0, 0], bad[0, 1] = 0, 1
+    with pytest.raises(hip_scans.ScanFallback, match="schedule"):
+        hip_scans._classify_schedule(bad, sgn, p2p, 8, 28, 1)
+
+
+# ---------------------------------------------------------------- delta layout round trip
+
+
+def test_delta_seam_layout_round_trip(monkeypatch):
+    """A fake backend sees the kernel layouts and its (B, H, T, d_v) output comes back as
+    (B, T, H, d_v): the whole module forward then equals the eager chunked forward."""
+    seen = {}
+
+    class FakeFallback(Exception):
+        pass
+
+    def fake_delta(Q, K, V, beta, H0, *, chunk_size):
+        seen["shapes"] = (tuple(Q.shape), tuple(K.shape), tuple(V.shape), tuple(beta.shape),
+                          tuple(H0.shape), chunk_size)
+        y, HT = mg.delta_chunked_eager(Q, K, V, beta, H0, chunk_size)
+        return y.permute(0, 2, 1, 3), HT
+
+    fake = types.ModuleType(BACKEND)
+    fake.ScanFallback = FakeFallback
+    fake.available = lambda: True
+    fake.SCAN_IMPLS = {}
+    fake.delta_scan_impl = fake_delta
+    monkeypatch.setitem(sys.modules, BACKEND, fake)
+    monkeypatch.setattr(mingru_amd, "hip_scans", fake, raising=False)
+
+    torch.manual_seed(3)
+    m = DeltaMinGRU(6, 12, n_heads=3, nh=2, chunk_size=5).double()
+    x = torch.randn(2, 13, 6, dtype=torch.float64)
+    monkeypatch.setenv("MINGRU_SCAN", "eager")
+    ref, Href = m(x, return_state=True)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    out, H = m(x, return_state=True)
+    assert seen["shapes"] == ((2, 3, 13, 4), (2, 3, 13, 2, 4), (2, 3, 13, 2, 4), (2, 3, 13, 2),
+                              (2, 3, 4, 4), 5)
+    torch.testing.assert_close(out, ref, rtol=0, atol=1e-12)
+    torch.testing.assert_close(H, Href, rtol=0, atol=1e-12)
+
+
+def test_angle_seam_reaches_backend(monkeypatch):
+    """GivensMinGRU's fused path hands (B, T, n, R, half) angles to the backend."""
+    seen = {}
+
+    class FakeFallback(Exception):
+        pass
+
+    def fake_angle(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale, has_decay):
+        seen["theta"] = tuple(theta.shape)
+        raise FakeFallback("declined by the fake backend")
+
+    fake = types.ModuleType(BACKEND)
+    fake.ScanFallback = FakeFallback
+    fake.available = lambda: True
+    fake.SCAN_IMPLS = {}
+    fake.angle_scan_impl = fake_angle
+    monkeypatch.setitem(sys.modules, BACKEND, fake)
+    monkeypatch.setattr(mingru_amd, "hip_scans", fake, raising=False)
+    m = GivensMinGRU(6, 16, block_size=8)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with pytest.raises(RuntimeError, match="declined by the fake backend"):
+        m(torch.randn(2, 7, 6))
+    assert seen["theta"][:3] == (2, 7, 2)
+
+
+def test_delta_module_forward_equals_step_recurrence():
+    """Eager chunked forward == token-by-token ``step`` (reference tests/test_mixers.py:350-363)."""
+    torch.manual_seed(1)
+    m = DeltaMinGRU(5, 8, n_heads=2, nh=2, chunk_size=3).double()
+    x = torch.randn(2, 10, 5, dtype=torch.float64)
+    y = m(x)
+    h = None
+    ys = []
+    for t in range(10):
+        yt, h = m.step(x[:, t], h)
+        ys.append(yt)
+    torch.testing.assert_close(y, torch.stack(ys, 1), rtol=0, atol=1e-12)
+    assert F.mse_loss(y, y).item() == 0.0
