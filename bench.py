@@ -46,17 +46,27 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", type=str, default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-eager", action="store_true",
+                    help="skip the eager-GPU delta comparison (used under rocprof counters)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also time a plain 1 GiB device copy (rocprof counter calibration)")
     return ap.parse_args()
 
 
 def _traffic(name: str):
-    """HBM bytes per launch from the committed rocprof counter summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
-        data = json.load(f)
-    return data.get(name)
+    """HBM bytes per C-ABI call (fetch + write) from the committed rocprof counter
+    summaries: lines ``traffic <workload>:<entry> <fetch bytes> <write bytes>`` in
+    ``profiles/*.md``; ``None`` when no summary covers ``name``."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"^traffic (\S+) (\d+) (\d+)\s*$", line)
+                if m and m.group(1) == name:
+                    return int(m.group(2)) + int(m.group(3))
+    return None
 
 
 class Op:
@@ -212,7 +222,16 @@ def make_step(key, torch, wl, dev):
             y, HT = hip_scans.delta_scan_impl(*xs, chunk_size=C)
             return torch.autograd.grad((y, HT), xs, (gy, gH))
 
-        return step, None, wl.C5["B"]
+        def cpu(bs):
+            from mingru_amd.min_gru import delta_chunked_eager
+
+            xc = [inp[k][:bs].float().clone().requires_grad_(True)
+                  for k in ("Q", "K", "V", "beta", "H0")]
+            y, HT = delta_chunked_eager(*xc, C)
+            torch.autograd.grad((y, HT), xc, (inp["grad_y"][:bs].permute(0, 2, 1, 3),
+                                              inp["grad_HT"][:bs]))
+
+        return step, cpu, wl.C5["B"]
     raise KeyError(key)
 
 
@@ -291,21 +310,35 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans):
     return res, cpu_step, B
 
 
-def cpu_baseline(cpu_step, B_full, tokens_full, torch, budget_s=20.0):
-    """Time the eager CPU path on a batch slice; returns the baseline dict."""
+def cpu_baseline(cpu_step, B_full, tokens_full, torch, budget_s=12.0):
+    """Time the eager CPU path (this package's restatement of the reference's eager
+    algorithm, run on CPU tensors with every host thread) on a batch slice of the
+    same inputs: the slice doubles until one step takes >= 1 s (or is the whole
+    batch), then 1 warm-up and up to 5 timed reps within ``budget_s``."""
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    prev = os.environ.get("MINGRU_SCAN")
     os.environ["MINGRU_SCAN"] = "eager"
-    bs = 1
-    t0 = time.perf_counter()
-    cpu_step(bs)  # warm-up
-    warm = time.perf_counter() - t0
-    reps = max(1, min(3, int(budget_s / max(warm, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        cpu_step(bs)
-        times.append(time.perf_counter() - t0)
+    try:
+        bs = 1
+        while True:
+            t0 = time.perf_counter()
+            cpu_step(bs)  # warm-up at this slice
+            warm = time.perf_counter() - t0
+            if warm >= 1.0 or bs >= B_full:
+                break
+            bs = min(B_full, 2 * bs)
+        reps = max(1, min(5, int(budget_s / max(warm, 1e-3))))
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            cpu_step(bs)
+            times.append(time.perf_counter() - t0)
+    finally:
+        if prev is None:
+            os.environ.pop("MINGRU_SCAN", None)
+        else:
+            os.environ["MINGRU_SCAN"] = prev
     times.sort()
     med = times[len(times) // 2]
     tokens_slice = tokens_full * bs // B_full
@@ -316,8 +349,40 @@ def cpu_baseline(cpu_step, B_full, tokens_full, torch, budget_s=20.0):
         "kind": "port",
         "sample": f"eager torch CPU fwd+bwd on batch slice {bs}/{B_full} of the same inputs "
                   f"(1 warm-up, median of {reps}; min {tokens_slice / times[0]:.4g} tokens/s); "
-                  f"os.cpu_count()={os.cpu_count()}, cpu={platform.processor() or platform.machine()}",
+                  f"os.cpu_count()={os.cpu_count()}, cpu={_cpu_model()}",
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def copy_probe(torch, dev, nbytes=1 << 30, reps=20):
+    """A plain device-to-device copy of ``nbytes``: the streaming ceiling of this
+    GPU, and the known-size kernel that calibrates rocprof's FETCH_SIZE /
+    WRITE_SIZE counters."""
+    src = torch.randn(nbytes // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / reps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": us,
+            "achieved_GBs": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
 def main():
@@ -354,17 +419,28 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
-        if key == "C5":
+        if key == "C5" and not args.no_eager:
             eg = delta_eager_gpu_ms(torch, wl, dev)
             res["eager_gpu_ms_per_step"] = eg
             res["speedup_vs_eager_gpu"] = eg / res["ms_per_step"]
             print(f"#   eager GPU chunked-WY: {eg:.2f} ms/step "
                   f"({res['speedup_vs_eager_gpu']:.1f}x slower than HIP)", file=sys.stderr,
                   flush=True)
-        if key == "C2" and cpu_step is not None and not args.no_cpu:
-            cpu = cpu_baseline(cpu_step, B, ops[key].tokens, torch)
-            os.environ["MINGRU_SCAN"] = "hip"
+        if cpu_step is not None and not args.no_cpu:
+            cb = cpu_baseline(cpu_step, B, ops[key].tokens, torch)
+            res["cpu_eager_tokens_per_s"] = cb["value"]
+            res["cpu_eager_sample"] = cb["sample"]
+            print(f"#   CPU eager ({cb['cores']} threads): {cb['value']:.4g} tok/s "
+                  f"({res['tokens_per_s'] / cb['value']:.0f}x slower than HIP)", file=sys.stderr,
+                  flush=True)
+            if key == "C2":
+                cpu = cb
         torch.cuda.empty_cache()
+    copy = None
+    if args.copy_probe:
+        copy = copy_probe(torch, dev)
+        print(f"# copy probe: {copy['achieved_GBs']:.0f} GB/s ({copy['avg_us']:.1f} us per "
+              "1 GiB copy)", file=sys.stderr, flush=True)
 
     head = results.get("C2") or next(iter(results.values()))
     head_key = "C2" if "C2" in results else next(iter(results))
@@ -402,6 +478,8 @@ def main():
         "frac_of_hbm_peak": head["frac_of_hbm_peak"],
         "ops": results,
     }
+    if copy is not None:
+        line["copy_probe"] = copy
     print(json.dumps(line))
 
 

@@ -140,3 +140,23 @@ def test_parallel_scan_log_beats_fp32_eager_accuracy(cuda):
     h_eager = parallel_scan_log(lc, lv)
     os.environ["MINGRU_SCAN"] = "hip"
     assert _maxerr(h, rh) <= _maxerr(h_eager, rh)
+
+
+def test_non_contiguous_inputs(cuda):
+    """Strided views (a transposed base tensor) give the same results as contiguous copies."""
+    print("[gpu] linear_scan / parallel_scan_log non-contiguous views", flush=True)
+    g = torch.Generator().manual_seed(99)
+    base_a = torch.tanh(torch.randn(2, 48, 130, generator=g)).to(cuda)  # (B, D, T)
+    base_b = torch.randn(2, 48, 130, generator=g).to(cuda)
+    a, b = base_a.transpose(1, 2), base_b.transpose(1, 2)  # (B, T, D), non-contiguous
+    assert not a.is_contiguous()
+    A, Bc = linear_scan(a, b)
+    A2, Bc2 = linear_scan(a.contiguous(), b.contiguous())
+    assert torch.equal(A, A2) and torch.equal(Bc, Bc2)
+    rA, rB = orc.linear_scan(a.double().cpu().numpy(), b.double().cpu().numpy())
+    assert _maxerr(A, rA) <= FWD_TOL and _maxerr(Bc, rB) <= FWD_TOL
+    lc = -torch.nn.functional.softplus(base_a).transpose(1, 2)
+    lv = torch.randn(2, 48, 131, generator=g).to(cuda).transpose(1, 2) * 0.1
+    h = parallel_scan_log(lc, lv)
+    rh = orc.parallel_scan_log(lc.double().cpu().numpy(), lv.double().cpu().numpy())
+    assert _maxerr(h, rh) <= FWD_TOL
