@@ -53,39 +53,58 @@ __device__ __forceinline__ void affm_compose(const AffM<K, W>& inner, const AffM
   }
 }
 
-template <int N>
+// Row loads/stores of N floats.  NT selects non-temporal accesses, used for
+// data a kernel touches exactly once (held inputs, every output).
+template <int N, bool NT = false>
 __device__ __forceinline__ void ld(float* dst, const float* __restrict__ src) {
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
-      float4 v = *reinterpret_cast<const float4*>(src + i);
+      const float4 v = NT ? mg_ld_stream4(src + i) : *reinterpret_cast<const float4*>(src + i);
       dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
     }
   } else if constexpr (N % 2 == 0) {
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
-      float2 v = *reinterpret_cast<const float2*>(src + i);
-      dst[i] = v.x; dst[i + 1] = v.y;
+      if constexpr (NT) {
+        dst[i] = mg_ld_stream(src + i);
+        dst[i + 1] = mg_ld_stream(src + i + 1);
+      } else {
+        float2 v = *reinterpret_cast<const float2*>(src + i);
+        dst[i] = v.x; dst[i + 1] = v.y;
+      }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) dst[i] = src[i];
+    for (int i = 0; i < N; ++i) dst[i] = NT ? mg_ld_stream(src + i) : src[i];
   }
 }
 
-template <int N>
+template <int N, bool NT = false>
 __device__ __forceinline__ void st(float* __restrict__ dst, const float* src) {
   if constexpr (N % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < N; i += 4)
-      *reinterpret_cast<float4*>(dst + i) = make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]);
+    for (int i = 0; i < N; i += 4) {
+      const float4 v = make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]);
+      if constexpr (NT) mg_st_stream4(dst + i, v);
+      else *reinterpret_cast<float4*>(dst + i) = v;
+    }
   } else if constexpr (N % 2 == 0) {
 #pragma unroll
-    for (int i = 0; i < N; i += 2)
-      *reinterpret_cast<float2*>(dst + i) = make_float2(src[i], src[i + 1]);
+    for (int i = 0; i < N; i += 2) {
+      if constexpr (NT) {
+        mg_st_stream(dst + i, src[i]);
+        mg_st_stream(dst + i + 1, src[i + 1]);
+      } else {
+        *reinterpret_cast<float2*>(dst + i) = make_float2(src[i], src[i + 1]);
+      }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) dst[i] = src[i];
+    for (int i = 0; i < N; ++i) {
+      if constexpr (NT) mg_st_stream(dst + i, src[i]);
+      else dst[i] = src[i];
+    }
   }
 }
 

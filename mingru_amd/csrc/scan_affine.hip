@@ -59,8 +59,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
   auto fetch = [&](int s, float* a, float* b) {
     const int64_t t = t0 + s;
     if (th.ok && t < T) {
-      ld<K * K>(a, A + offA(t));
-      ld<K * V>(b, Bm + offB(t));
+      ld<K * K, HOLD>(a, A + offA(t));
+      ld<K * V, HOLD>(b, Bm + offB(t));
     } else {
 #pragma unroll
       for (int i = 0; i < K * K; ++i) a[i] = (i / K == i % K) ? 1.f : 0.f;
@@ -144,8 +144,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
     carry = nx;
     const int64_t t = t0 + s;
     if (th.ok && t < T) {
-      st<K * K>(Abar + offA(t), &carry.P[0][0]);
-      st<K * V>(Bbar + offB(t), &carry.L[0][0]);
+      st<K * K, true>(Abar + offA(t), &carry.P[0][0]);
+      st<K * V, true>(Bbar + offB(t), &carry.L[0][0]);
     }
   }
 }
@@ -172,10 +172,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
   auto fetch = [&](int s, float* a, float* b, float* ga, float* gb, bool need_b) {
     const int64_t t = t0 + s;
     if (th.ok && t < T) {
-      ld<K * K>(a, A + offA(t));
-      if (need_b) ld<K * V>(b, Bm + offB(t));
-      ld<K * K>(ga, GA + offA(t));
-      ld<K * V>(gb, GB + offB(t));
+      ld<K * K, HOLD>(a, A + offA(t));
+      if (need_b) ld<K * V, HOLD>(b, Bm + offB(t));
+      ld<K * K, HOLD>(ga, GA + offA(t));
+      ld<K * V, HOLD>(gb, GB + offB(t));
     } else {
 #pragma unroll
       for (int i = 0; i < K * K; ++i) {
@@ -318,8 +318,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
       for (int i = 0; i < K * V; ++i) Sb[i] = nb[i];
       const int64_t t = t0 + s;
       if (th.ok && t < T) {
-        st<K * K>(dA + offA(t), d);
-        st<K * V>(dB + offB(t), hgb[s]);
+        st<K * K, true>(dA + offA(t), d);
+        st<K * V, true>(dB + offB(t), hgb[s]);
       }
     }
   } else {
@@ -363,8 +363,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
 #pragma unroll
         for (int j = 0; j < V; ++j) xb[i * V + j] = X[i][K + j];
       }
-      st<K * K>(dA + offA(t), d);
-      st<K * V>(dB + offB(t), xb);
+      st<K * K, true>(dA + offA(t), d);
+      st<K * V, true>(dB + offB(t), xb);
 #pragma unroll
       for (int i = 0; i < K; ++i)
 #pragma unroll

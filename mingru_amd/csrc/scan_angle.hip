@@ -323,7 +323,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, 
         v[i][0] += bt[i];
         bt[i] = v[i][0];
       }
-      st<K>(a.out + lane_tok * K, bt);
+      st<K, true>(a.out + lane_tok * K, bt);
     }
   }
 }
@@ -364,7 +364,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
           gr[r] = rot_grad<K, lex_first(K, r), lex_second(K, r)>(v, x, cs[r], sn[r]);
         },
         std::make_index_sequence<R>{});
-    st<R>(dth, gr);
+    st<R, true>(dth, gr);
   } else {
     constexpr int H = K / 2;
     for (int r = 0; r < rounds; ++r) {
@@ -404,7 +404,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
             },
             std::make_index_sequence<H>{});
       }
-      st<H>(dth + r * H, gr);
+      st<H, true>(dth + r * H, gr);
     }
   }
   if (HS) {
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_kernel(AnArgs a, 
         y[i][0] += gt[i];
         gt[i] = y[i][0];
       }
-      st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
+      st<K, true>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
       float dd = 0.f, dg = 0.f;
       token_grad<K, SCHED, HS, HD>(y, hp, a.theta + lane_tok * a.na, a.dtheta + lane_tok * a.na,
                                    a.rounds, d, gm, dd, dg);

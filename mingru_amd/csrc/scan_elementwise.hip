@@ -58,24 +58,25 @@ __device__ __forceinline__ Aff<NL> aff_compose(const Aff<NL>& inner, const Aff<N
   return r;
 }
 
+// Data streams are read and written once: non-temporal accesses.
 template <int VEC>
 __device__ __forceinline__ void load_vec(float (&dst)[VEC], const float* __restrict__ src) {
   if constexpr (VEC == 4) {
-    float4 v = *reinterpret_cast<const float4*>(src);
+    const float4 v = mg_ld_stream4(src);
     dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) dst[i] = src[i];
+    for (int i = 0; i < VEC; ++i) dst[i] = mg_ld_stream(src + i);
   }
 }
 
 template <int VEC>
 __device__ __forceinline__ void store_vec(float* __restrict__ dst, const float (&src)[VEC]) {
   if constexpr (VEC == 4) {
-    *reinterpret_cast<float4*>(dst) = make_float4(src[0], src[1], src[2], src[3]);
+    mg_st_stream4(dst, make_float4(src[0], src[1], src[2], src[3]));
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) dst[i] = src[i];
+    for (int i = 0; i < VEC; ++i) mg_st_stream(dst + i, src[i]);
   }
 }
 
