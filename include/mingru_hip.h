@@ -6,8 +6,14 @@
  *   - pointers are device pointers to contiguous row-major fp32 (bf16 where
  *     stated) tensors; sizes are int64 element counts;
  *   - `ws`/`ws_bytes` is a caller-provided device workspace of at least the
- *     size returned by the matching *_workspace_bytes query; its contents on
- *     entry are irrelevant (the call clears what it needs);
+ *     size returned by the matching *_workspace_bytes query.
+ *     Scan entry points (linear, log, affine, angle): the workspace must be
+ *     zero-filled once before its first use and may then be passed, unchanged,
+ *     to any sequence of scan calls ordered on one stream (of any op or size up
+ *     to its capacity); nothing is cleared between calls, because each launch
+ *     tags its look-back slots with a fresh epoch kept in the workspace header.
+ *     Calls that can run concurrently (different streams) need different
+ *     workspaces.  Delta entry points: contents on entry are irrelevant;
  *   - work is enqueued asynchronously on `stream`; nothing allocates, throws or
  *     synchronises;
  *   - the return value is a status: 0 ok, 1 invalid argument / outside the

@@ -112,29 +112,29 @@ __device__ __forceinline__ void st(float* __restrict__ dst, const float* src) {
 // Look-back slots: [lg][chunk][field][64] tagged words.
 template <int K, int W>
 __device__ __forceinline__ void af_lb_put(mg_slot_t* base, const AfGeom& g, int lg, int c,
-                                          int lane, const AffM<K, W>& x) {
+                                          int lane, const AffM<K, W>& x, unsigned epoch) {
   constexpr int NF = K * K + K * W;
   mg_slot_t* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
   const float* f = &x.P[0][0];
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) mg_slot_put(p + i * MG_WAVE, f[i]);
+  for (int i = 0; i < K * K; ++i) mg_slot_put(p + i * MG_WAVE, f[i], epoch);
   const float* l = &x.L[0][0];
 #pragma unroll
-  for (int i = 0; i < K * W; ++i) mg_slot_put(p + (K * K + i) * MG_WAVE, l[i]);
+  for (int i = 0; i < K * W; ++i) mg_slot_put(p + (K * K + i) * MG_WAVE, l[i], epoch);
 }
 
 template <int K, int W>
 __device__ __forceinline__ bool af_lb_try(const mg_slot_t* base, const AfGeom& g, int lg, int c,
-                                          int lane, AffM<K, W>& x) {
+                                          int lane, AffM<K, W>& x, unsigned epoch) {
   constexpr int NF = K * K + K * W;
   const mg_slot_t* p = base + (int64_t)(lg * g.n_chunks + c) * NF * MG_WAVE + lane;
   bool ok = true;
   float* f = &x.P[0][0];
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) ok &= mg_slot_get(p + i * MG_WAVE, f[i]);
+  for (int i = 0; i < K * K; ++i) ok &= mg_slot_get(p + i * MG_WAVE, f[i], epoch);
   float* l = &x.L[0][0];
 #pragma unroll
-  for (int i = 0; i < K * W; ++i) ok &= mg_slot_get(p + (K * K + i) * MG_WAVE, l[i]);
+  for (int i = 0; i < K * W; ++i) ok &= mg_slot_get(p + (K * K + i) * MG_WAVE, l[i], epoch);
   return ok;
 }
 
@@ -164,8 +164,8 @@ __device__ __forceinline__ void lds_get(const float* s, int lane, AffM<K, W>& x)
 // the map at the sequence start (forward) / end (reverse).
 template <int K, int W, int WAVES, bool REVERSE>
 __device__ void af_carry(const AffM<K, W>& loc, const AffM<K, W>& seed, const AfGeom& g, int lg,
-                         int c, unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data,
-                         AffM<K, W>& carry) {
+                         int c, unsigned* header, unsigned epoch, mg_slot_t* agg_data,
+                         mg_slot_t* incl_data, AffM<K, W>& carry) {
   constexpr int NF = K * K + K * W;
   __shared__ float s_buf[NF * MG_WAVE];
   const int lane = threadIdx.x & (MG_WAVE - 1);
@@ -192,14 +192,14 @@ __device__ void af_carry(const AffM<K, W>& loc, const AffM<K, W>& seed, const Af
       E = seed;
     } else {
       affm_identity(E);
-      af_lb_put(agg_data, g, lg, c, lane, G);
+      af_lb_put(agg_data, g, lg, c, lane, G, epoch);
       int j = c + dir;
       unsigned spins = 0;
       bool done = false;
       while (!done) {
-        bool have = af_lb_try(incl_data, g, lg, j, lane, X);
+        bool have = af_lb_try(incl_data, g, lg, j, lane, X, epoch);
         const bool incl = have;
-        if (!have && j != first) have = af_lb_try(agg_data, g, lg, j, lane, X);
+        if (!have && j != first) have = af_lb_try(agg_data, g, lg, j, lane, X, epoch);
         if (have) {
           affm_compose(X, E, acc);
           E = acc;
@@ -215,7 +215,7 @@ __device__ void af_carry(const AffM<K, W>& loc, const AffM<K, W>& seed, const Af
       }
     }
     affm_compose(E, G, acc);
-    af_lb_put(incl_data, g, lg, c, lane, acc);
+    af_lb_put(incl_data, g, lg, c, lane, acc, epoch);
     lds_put(s_buf, lane, E);
   }
   __syncthreads();
@@ -227,6 +227,8 @@ __device__ void af_carry(const AffM<K, W>& loc, const AffM<K, W>& seed, const Af
 
 struct AfThread {
   int lane, w, c, lg, bb;
+  unsigned epoch;
+  bool valid;  // false only for a ticket beyond the grid (workspace protocol broken)
   int64_t plane;
   bool ok;
 };
@@ -234,7 +236,10 @@ struct AfThread {
 template <bool REVERSE>
 __device__ __forceinline__ AfThread af_thread(const AfGeom& g, unsigned* header) {
   AfThread th;
-  unsigned ticket = mg_take_ticket(header);
+  const MgTicket tk = mg_take_ticket(header);
+  th.valid = tk.ticket < gridDim.x;
+  const unsigned ticket = th.valid ? tk.ticket : 0u;
+  th.epoch = tk.epoch;
   th.lane = threadIdx.x & (MG_WAVE - 1);
   th.w = threadIdx.x / MG_WAVE;
   int kk = (int)(ticket / (unsigned)g.n_lg);

@@ -14,13 +14,24 @@
 // Published values are self-validating 64-bit words {fp32 value, tag}
 // written and read with relaxed agent-scope atomics (single-copy atomic,
 // coherent across XCDs without any cache-wide maintenance).  A reader uses a
-// word only once its tag is non-zero, so no release/acquire fences -- which on
-// gfx950 write back / invalidate the whole L2 of an XCD -- are needed.
+// word only once its tag equals the current launch's epoch, so no
+// release/acquire fences -- which on gfx950 write back / invalidate the whole
+// L2 of an XCD -- are needed.
 //
-// Workspace header (first 256 bytes of every workspace):
-//   word 0: ticket counter, word 1: error counter (spin-limit overflows).
-// The host clears the header and every look-back slot with mg_clear_kernel
-// before each scan launch, so the caller may pass uninitialised memory.
+// Workspace protocol (no per-launch clearing)
+// -------------------------------------------
+// The workspace is zero-filled once by its owner and then reused, unchanged,
+// by launches that are ordered on one stream.  Header words (first 256 bytes):
+//   [MG_H_TICKET0], [MG_H_TICKET1]  ticket counters, used by alternate epochs
+//   [MG_H_ERROR]                    spin-limit overflows (diagnostic)
+//   [MG_H_EPOCH]                    epoch of the last completed launch
+// Every workgroup reads the epoch (previous + 1, never 0 on a zeroed
+// workspace), takes its ticket from the counter of the epoch's parity, and the
+// workgroup holding ticket 0 resets the other counter for the next launch.
+// The workgroup holding the last ticket publishes the new epoch.  Slots of earlier
+// launches carry older tags and never validate, so stale contents are
+// harmless.  The epoch lives on the device, so graph replays advance it too.
+// Launches that may overlap (different streams) need different workspaces.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,29 +49,54 @@
 
 typedef unsigned long long mg_slot_t;
 
-__device__ __forceinline__ unsigned mg_take_ticket(unsigned* header) {
-  __shared__ unsigned s_ticket;
-  if (threadIdx.x == 0) {
-    s_ticket = __hip_atomic_fetch_add(header, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  return s_ticket;
+enum : int { MG_H_TICKET0 = 0, MG_H_TICKET1 = 1, MG_H_ERROR = 2, MG_H_EPOCH = 3 };
+
+__device__ __forceinline__ void mg_count_error(unsigned* header) {
+  __hip_atomic_fetch_add(header + MG_H_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void mg_slot_put(mg_slot_t* p, float v) {
-  const mg_slot_t w = (1ull << 32) | (mg_slot_t)__float_as_uint(v);
+struct MgTicket {
+  unsigned ticket;  // dispatch-ordered index of this workgroup within the launch
+  unsigned epoch;   // tag of every slot this launch publishes
+};
+
+// Workspace protocol entry for a 1-D grid; see the header comment.  The ticket
+// counter's address depends on the loaded epoch, so every ticket is taken only
+// after its workgroup has read the epoch; the holder of the last ticket can
+// therefore publish the next epoch without racing any reader of this launch.
+__device__ __forceinline__ MgTicket mg_take_ticket(unsigned* header) {
+  __shared__ unsigned s_ticket, s_epoch;
+  if (threadIdx.x == 0) {
+    const unsigned e =
+        __hip_atomic_load(header + MG_H_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const unsigned t = __hip_atomic_fetch_add(header + MG_H_TICKET0 + (e & 1u), 1u,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0u)  // the previous launch, which used the other counter, has completed
+      __hip_atomic_store(header + MG_H_TICKET0 + ((e + 1u) & 1u), 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (t == gridDim.x - 1u)
+      __hip_atomic_store(header + MG_H_EPOCH, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // A ticket beyond the grid can only come from a workspace that broke the
+    // protocol (not zero-filled, or shared by overlapping launches): record it;
+    // the caller retires the workgroup instead of indexing past its slots.
+    if (t >= gridDim.x) mg_count_error(header);
+    s_ticket = t;
+    s_epoch = e;
+  }
+  __syncthreads();
+  return MgTicket{s_ticket, s_epoch};
+}
+
+__device__ __forceinline__ void mg_slot_put(mg_slot_t* p, float v, unsigned epoch) {
+  const mg_slot_t w = ((mg_slot_t)epoch << 32) | (mg_slot_t)__float_as_uint(v);
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Returns true and the value if the slot has been published.
-__device__ __forceinline__ bool mg_slot_get(const mg_slot_t* p, float& v) {
+// Returns true and the value if the slot has been published in this epoch.
+__device__ __forceinline__ bool mg_slot_get(const mg_slot_t* p, float& v, unsigned epoch) {
   const mg_slot_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   v = __uint_as_float((unsigned)(w & 0xffffffffull));
-  return (w >> 32) != 0ull;
-}
-
-__device__ __forceinline__ void mg_count_error(unsigned* header) {
-  __hip_atomic_fetch_add(header + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (unsigned)(w >> 32) == epoch;
 }
 
 // Streaming (non-temporal) global accesses for data read or written exactly
@@ -80,18 +116,4 @@ __device__ __forceinline__ void mg_st_stream4(float* p, float4 x) {
 __device__ __forceinline__ float mg_ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void mg_st_stream(float* p, float x) { __builtin_nontemporal_store(x, p); }
 
-// Zeroes `n16` 16-byte units (workspace header and look-back slots).
-__global__ void mg_clear_kernel(uint4* p, size_t n16);
-
 static inline size_t mg_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-static inline int mg_clear(void* ws, size_t bytes, hipStream_t stream) {
-  const size_t n16 = (bytes + 15) / 16;
-  const int threads = 256;
-  size_t blocks = (n16 + threads - 1) / threads;
-  if (blocks == 0) blocks = 1;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(mg_clear_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
-                     (uint4*)ws, n16);
-  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
-}

@@ -27,11 +27,18 @@ namespace {
 
 using namespace mg;
 
-constexpr int AF_WAVES = 4;
+// Chunk shape by block size and direction: waves per workgroup x steps per
+// wave.  Longer chunks mean fewer hops in the look-back chain, whose per-hop
+// latency (slot round trips that bypass the L2) bounds the 2x2 scans at long T;
+// the shapes were chosen by timing on MI355X at B=16, T=4096, n=256.
+template <int K, bool BWD>
+constexpr int af_waves() {
+  return K == 2 ? (BWD ? 8 : 16) : 4;
+}
 
-template <int K>
+template <int K, bool BWD>
 constexpr int af_tsub() {
-  return K == 1 ? 16 : (K == 2 ? 8 : 8);
+  return K == 1 ? 16 : 8;
 }
 
 template <int K>
@@ -50,6 +57,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
   constexpr bool HOLD = af_hold<K>();
   constexpr int HS = HOLD ? TSUB : 1;
   AfThread th = af_thread<false>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, n = g.n;
   auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
@@ -109,7 +117,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
   }
   AffM<K, V> seed;
   affm_identity(seed);
-  af_carry<K, V, WAVES, false>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data, carry);
+  af_carry<K, V, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
 
   // Final pass from the carry-in (Abar_{t0-1}, Bbar_{t0-1}).
 #pragma unroll
@@ -163,6 +171,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
   constexpr int HS = HOLD ? TSUB : 1;
   constexpr int W = K + V;  // adjoint state: [XA | XB]
   AfThread th = af_thread<true>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, n = g.n;
   auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
@@ -233,7 +242,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
   }
   AffM<K, W> seed;
   affm_identity(seed);
-  af_carry<K, W, WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data, carry);
+  af_carry<K, W, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
 
   // Y entering the sub-chunk from the right (Y_T = 0 seed applied).
   float Y[K][W];
@@ -386,13 +395,13 @@ struct AfPlan {
   size_t agg_off, incl_off, total;
 };
 
-AfPlan af_plan(int64_t B, int64_t T, int64_t n, int tsub, int nf) {
+AfPlan af_plan(int64_t B, int64_t T, int64_t n, int waves, int tsub, int nf) {
   AfPlan p;
   p.g.T = T;
   p.g.n = n;
   p.g.n_tiles = (int)((n + MG_WAVE - 1) / MG_WAVE);
   p.g.n_lg = (int)(B * p.g.n_tiles);
-  const int64_t cl = (int64_t)AF_WAVES * tsub;
+  const int64_t cl = (int64_t)waves * tsub;
   p.g.n_chunks = (int)((T + cl - 1) / cl);
   const size_t cnt = (size_t)p.g.n_lg * p.g.n_chunks;
   const size_t data = cnt * (size_t)nf * MG_WAVE * sizeof(mg_slot_t);
@@ -402,7 +411,11 @@ AfPlan af_plan(int64_t B, int64_t T, int64_t n, int tsub, int nf) {
   return p;
 }
 
-int tsub_for(int k) { return k == 1 ? af_tsub<1>() : k == 2 ? af_tsub<2>() : k == 4 ? af_tsub<4>() : af_tsub<8>(); }
+template <int K>
+size_t af_ws_bytes_k(int64_t B, int64_t T, int64_t n, int v) {
+  return std::max(af_plan(B, T, n, af_waves<K, false>(), af_tsub<K, false>(), K * K + K * v).total,
+                  af_plan(B, T, n, af_waves<K, true>(), af_tsub<K, true>(), K * K + K * (K + v)).total);
+}
 
 bool kv_ok(int k, int v) {
   return (k == 1 || k == 2 || k == 4 || k == 8) &&
@@ -412,7 +425,7 @@ bool kv_ok(int k, int v) {
 bool af_geometry_ok(int64_t B, int64_t T, int64_t n) {
   if (B <= 0 || T <= 0 || n <= 0) return false;
   const int64_t lgs = B * ((n + MG_WAVE - 1) / MG_WAVE);
-  const int64_t chunks = (T + AF_WAVES - 1) / AF_WAVES;
+  const int64_t chunks = (T + 3) / 4;  // every chunk shape spans at least 4 steps
   return lgs * chunks < (1ll << 24);
 }
 
@@ -421,14 +434,12 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 template <int K, int V>
 int af_launch_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B, int64_t T,
                   int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
-  constexpr int TS = af_tsub<K>();
-  AfPlan p = af_plan(B, T, n, TS, K * K + K * V);
+  constexpr int TS = af_tsub<K, false>(), WV = af_waves<K, false>();
+  AfPlan p = af_plan(B, T, n, WV, TS, K * K + K * V);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-  int rc = mg_clear(ws, p.total, stream);
-  if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
-  hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, AF_WAVES>),
-                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
+  hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, WV>),
+                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * WV), 0,
                      stream, A, Bm, Abar, Bbar, p.g, header,
                      (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
@@ -438,14 +449,12 @@ template <int K, int V>
 int af_launch_bwd(const float* A, const float* Bm, const float* Abar, const float* Bbar,
                   const float* GA, const float* GB, float* dA, float* dB, int64_t B, int64_t T,
                   int64_t n, void* ws, size_t ws_bytes, hipStream_t stream) {
-  constexpr int TS = af_tsub<K>();
-  AfPlan p = af_plan(B, T, n, TS, K * K + K * (K + V));
+  constexpr int TS = af_tsub<K, true>(), WV = af_waves<K, true>();
+  AfPlan p = af_plan(B, T, n, WV, TS, K * K + K * (K + V));
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-  int rc = mg_clear(ws, p.total, stream);
-  if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
-  hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, AF_WAVES>),
-                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * AF_WAVES), 0,
+  hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, WV>),
+                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * WV), 0,
                      stream, A, Bm, Abar, Bbar, GA, GB, dA, dB, p.g, header,
                      (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
@@ -482,9 +491,12 @@ extern "C" {
 
 size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v) {
   if (!kv_ok(k, v) || B <= 0 || T <= 0 || n <= 0) return 256;
-  const int ts = tsub_for(k);
-  return std::max(af_plan(B, T, n, ts, k * k + k * v).total,
-                  af_plan(B, T, n, ts, k * k + k * (k + v)).total);
+  switch (k) {
+    case 1: return af_ws_bytes_k<1>(B, T, n, v);
+    case 2: return af_ws_bytes_k<2>(B, T, n, v);
+    case 4: return af_ws_bytes_k<4>(B, T, n, v);
+    default: return af_ws_bytes_k<8>(B, T, n, v);
+  }
 }
 
 int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,

@@ -41,8 +41,12 @@ using namespace mg;
 
 enum : int { SCHED_BRICK = 0, SCHED_LEX = 1 };
 
-constexpr int AN_WAVES = 4;
-constexpr int AN_TSUB = 4;
+// Chunk = AN_WAVES * AN_TSUB tokens per workgroup.  64-token chunks keep the
+// look-back chain short (32 hops at T = 2048) while the per-thread aggregate
+// work (k + 1 rotated columns per token) stays in registers; chosen by timing
+// on MI355X at the 28-rotation SO(8) workload.
+constexpr int AN_WAVES = 8;
+constexpr int AN_TSUB = 8;
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -261,6 +265,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, 
                                                                       mg_slot_t* agg_data,
                                                                       mg_slot_t* incl_data) {
   AfThread th = af_thread<false>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (AN_WAVES * AN_TSUB) + th.w * AN_TSUB;
   const int64_t T = g.T, n = g.n;
 
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, 
 #pragma unroll
     for (int i = 0; i < K; ++i) seed.L[i][0] = hz[i];
   }
-  af_carry<K, 1, AN_WAVES, false>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data, carry);
+  af_carry<K, 1, AN_WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
 
   // Final pass: the state entering the sub-chunk is carry.L (the seed's P = 0
   // turns every prefix into a constant map).
@@ -419,6 +424,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_kernel(AnArgs a, 
                                                                       mg_slot_t* agg_data,
                                                                       mg_slot_t* incl_data) {
   AfThread th = af_thread<true>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (AN_WAVES * AN_TSUB) + th.w * AN_TSUB;
   const int64_t T = g.T, n = g.n;
 
@@ -450,7 +456,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_kernel(AnArgs a, 
     loc.L[i][0] = X[i][K];
   }
   affm_identity(seed);
-  af_carry<K, 1, AN_WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data, carry);
+  af_carry<K, 1, AN_WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
 
   float y[K][1];
 #pragma unroll
@@ -515,8 +521,6 @@ int an_launch(const AnArgs& a, int64_t B, int64_t T, int64_t n, void* ws, size_t
   const AfGeom g = an_geom(B, T, n);
   const size_t total = an_ws_bytes(B, T, n, K);
   if (ws_bytes < total) return MG_ERR_WORKSPACE;
-  int rc = mg_clear(ws, total, stream);
-  if (rc != MG_OK) return rc;
   const size_t data = (total - MG_HEADER_BYTES) / 2;
   unsigned* header = (unsigned*)ws;
   mg_slot_t* agg = (mg_slot_t*)((char*)ws + MG_HEADER_BYTES);

@@ -88,28 +88,28 @@ struct EwGeom {
 // Look-back slots: [lg][chunk][field][TILE] tagged words, TILE = 64*VEC.
 template <int NL, int VEC>
 __device__ __forceinline__ void lb_put(mg_slot_t* base, const EwGeom& g, int lg, int c, int lane,
-                                       const Aff<NL> (&x)[VEC]) {
+                                       const Aff<NL> (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
   mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    mg_slot_put(p + v, x[v].p);
+    mg_slot_put(p + v, x[v].p, epoch);
 #pragma unroll
-    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v, x[v].l[f]);
+    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v, x[v].l[f], epoch);
   }
 }
 
 template <int NL, int VEC>
 __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, int lg, int c,
-                                       int lane, Aff<NL> (&x)[VEC]) {
+                                       int lane, Aff<NL> (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
   const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
   bool ok = true;
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    ok &= mg_slot_get(p + v, x[v].p);
+    ok &= mg_slot_get(p + v, x[v].p, epoch);
 #pragma unroll
-    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v, x[v].l[f]);
+    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v, x[v].l[f], epoch);
   }
   return ok;
 }
@@ -121,8 +121,8 @@ __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, i
 template <int NL, int VEC, int WAVES, bool REVERSE>
 __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL> (&seed)[VEC],
                                          const EwGeom& g, int lg, int c, unsigned* header,
-                                         mg_slot_t* agg_data, mg_slot_t* incl_data,
-                                         Aff<NL> (&carry)[VEC]) {
+                                         unsigned epoch, mg_slot_t* agg_data,
+                                         mg_slot_t* incl_data, Aff<NL> (&carry)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
   constexpr int NF = NL + 1;
   __shared__ float s_agg[WAVES][NF][TILE];
@@ -176,7 +176,7 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
 #pragma unroll
       for (int v = 0; v < VEC; ++v) E[v] = seed[v];
     } else {
-      lb_put<NL, VEC>(agg_data, g, lg, c, lane, G);
+      lb_put<NL, VEC>(agg_data, g, lg, c, lane, G, epoch);
 #pragma unroll
       for (int v = 0; v < VEC; ++v) E[v] = aff_identity<NL>();
       // Per-lane walk over predecessors: an inclusive prefix ends the walk, an
@@ -187,11 +187,11 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
       bool done = false;
       while (!done) {
         Aff<NL> X[VEC];
-        if (lb_try<NL, VEC>(incl_data, g, lg, j, lane, X)) {
+        if (lb_try<NL, VEC>(incl_data, g, lg, j, lane, X, epoch)) {
 #pragma unroll
           for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
           done = true;
-        } else if (j != first && lb_try<NL, VEC>(agg_data, g, lg, j, lane, X)) {
+        } else if (j != first && lb_try<NL, VEC>(agg_data, g, lg, j, lane, X, epoch)) {
 #pragma unroll
           for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
           j += dir;
@@ -207,7 +207,7 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
     Aff<NL> I[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) I[v] = aff_compose(E[v], G[v]);
-    lb_put<NL, VEC>(incl_data, g, lg, c, lane, I);
+    lb_put<NL, VEC>(incl_data, g, lg, c, lane, I, epoch);
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       s_carry[0][lane * VEC + v] = E[v].p;
@@ -228,6 +228,8 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
 
 struct EwThread {
   int lane, w, c, lg, bb;
+  unsigned epoch;
+  bool valid;  // false only for a ticket beyond the grid (workspace protocol broken)
   int64_t col;
   bool col_ok;
 };
@@ -235,7 +237,10 @@ struct EwThread {
 template <int VEC, int TSUB, int WAVES, bool REVERSE>
 __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header) {
   EwThread th;
-  unsigned ticket = mg_take_ticket(header);
+  const MgTicket tk = mg_take_ticket(header);
+  th.valid = tk.ticket < gridDim.x;
+  const unsigned ticket = th.valid ? tk.ticket : 0u;
+  th.epoch = tk.epoch;
   th.lane = threadIdx.x & (MG_WAVE - 1);
   th.w = threadIdx.x / MG_WAVE;
   int k = (int)(ticket / (unsigned)g.n_lg);
@@ -258,6 +263,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
 
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
 #pragma unroll
     for (int v = 0; v < VEC; ++v) seed[v].l[0] = expf(h0[v]);
   }
-  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
+  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                  carry);
 
   float P[VEC], L[VEC];
@@ -353,6 +359,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
 
@@ -402,7 +409,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     }
     seed[v] = aff_identity<2>();
   }
-  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
+  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                 carry);
 
   float ya[VEC], yb[VEC];
@@ -451,6 +458,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     const float* __restrict__ gh, float* __restrict__ dlc, float* __restrict__ dlv, EwGeom g,
     unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
 
@@ -504,7 +512,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, agg_data, incl_data,
+  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                 carry);
 
   float y[VEC];
@@ -581,8 +589,6 @@ bool geometry_ok(int64_t B, int64_t T, int64_t D) {
 
 template <typename Kernel, typename... Args>
 int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... args) {
-  int rc = mg_clear(ws, p.total, stream);
-  if (rc != MG_OK) return rc;
   unsigned* header = (unsigned*)ws;
   mg_slot_t* agg = (mg_slot_t*)((char*)ws + p.agg_off);
   mg_slot_t* incl = (mg_slot_t*)((char*)ws + p.incl_off);
@@ -602,13 +608,6 @@ size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
 }
 
 }  // namespace
-
-__global__ void mg_clear_kernel(uint4* p, size_t n16) {
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
-       i += (size_t)gridDim.x * blockDim.x)
-    p[i] = z;
-}
 
 extern "C" {
 

@@ -100,7 +100,27 @@ def _stream(t: torch.Tensor):
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
+    """Scratch whose contents on entry do not matter (the delta kernels)."""
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# Look-back workspaces of the scan kernels, one per (device, stream).  The C ABI
+# asks for a workspace that was zero-filled once and is then reused only by
+# calls ordered on one stream: every launch tags its slots with a fresh epoch
+# kept in the workspace header, so nothing is cleared between calls.  A larger
+# request replaces the buffer with a new zero-filled one (the old one returns to
+# torch's caching allocator, ordered after the work already queued on the stream).
+_scan_ws: dict = {}
+
+
+def _scan_workspace(nbytes: int, device) -> torch.Tensor:
+    stream = torch.cuda.current_stream(device)
+    key = (stream.device_index, stream.cuda_stream)
+    ws = _scan_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+        _scan_ws[key] = ws
+    return ws
 
 
 class kernel_timer:
@@ -195,7 +215,7 @@ class _LinearScanFn(torch.autograd.Function):
         Bn, T, D = a32.shape
         A = torch.empty_like(a32)
         Bc = torch.empty_like(a32)
-        ws = _workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
         _call("mg_linear_scan_fwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), Bn, T, D,
               _ptr(ws), ws.numel(), _stream(a32))
         ctx.save_for_backward(a32, b32, A, Bc)
@@ -212,7 +232,7 @@ class _LinearScanFn(torch.autograd.Function):
         gA32, gB32 = _as_f32(gA, gB)
         da = torch.empty_like(a32)
         db = torch.empty_like(a32)
-        ws = _workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
         _call("mg_linear_scan_bwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), _ptr(gA32),
               _ptr(gB32), _ptr(da), _ptr(db), Bn, T, D, _ptr(ws), ws.numel(), _stream(a32))
         return da.to(ctx.out_dtype), db.to(ctx.out_dtype)
@@ -243,7 +263,7 @@ class _LogScanFn(torch.autograd.Function):
         lc, lv = _as_f32(log_coeffs, log_values)
         Bn, T, D = lc.shape
         h = torch.empty_like(lc)
-        ws = _workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
         _call("mg_log_scan_fwd", _ptr(lc), _ptr(lv), _ptr(h), Bn, T, D, _ptr(ws), ws.numel(),
               _stream(lc))
         ctx.save_for_backward(lc, lv, h)
@@ -258,7 +278,7 @@ class _LogScanFn(torch.autograd.Function):
         (gh32,) = _as_f32(gh)
         dlc = torch.empty_like(lc)
         dlv = torch.empty_like(lv)
-        ws = _workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
         _call("mg_log_scan_bwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(gh32), _ptr(dlc), _ptr(dlv),
               Bn, T, D, _ptr(ws), ws.numel(), _stream(lc))
         return dlc.to(ctx.out_dtype), dlv.to(ctx.out_dtype)
@@ -297,7 +317,7 @@ class _AffineScanFn(torch.autograd.Function):
         v = B32.shape[-1]
         Abar = torch.empty_like(A32)
         Bbar = torch.empty_like(B32)
-        ws = _workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_fwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), Bn, T, n, k, v,
               _ptr(ws), ws.numel(), _stream(A32))
         ctx.save_for_backward(A32, B32, Abar, Bbar)
@@ -315,7 +335,7 @@ class _AffineScanFn(torch.autograd.Function):
         gA32, gB32 = _as_f32(gAbar, gBbar)
         dA = torch.empty_like(A32)
         dB = torch.empty_like(B32)
-        ws = _workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_bwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), _ptr(gA32),
               _ptr(gB32), _ptr(dA), _ptr(dB), Bn, T, n, k, v, _ptr(ws), ws.numel(), _stream(A32))
         return dA.to(ctx.out_dtype), dB.to(ctx.out_dtype)
@@ -449,7 +469,7 @@ class _AngleScanFn(torch.autograd.Function):
         th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
         Bn, T, n, k = b32.shape
         h = torch.empty_like(b32)
-        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
+        ws = _scan_workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
         _call("mg_angle_scan_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032), _ptr(h),
               Bn, T, n, k, sched, rounds, flags, _ptr(ws), ws.numel(), _stream(b32))
         ctx.save_for_backward(th, sc, gm, h032, h)
@@ -471,7 +491,7 @@ class _AngleScanFn(torch.autograd.Function):
         dgm = torch.zeros_like(gm) if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
-        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
+        ws = _scan_workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
         _call("mg_angle_scan_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h), _ptr(gh32),
               _ptr(dth), _ptr(dsc), _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k, sched, rounds,
               flags, _ptr(ws), ws.numel(), _stream(h))
