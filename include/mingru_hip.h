@@ -7,13 +7,14 @@
  *     stated) tensors; sizes are int64 element counts;
  *   - `ws`/`ws_bytes` is a caller-provided device workspace of at least the
  *     size returned by the matching *_workspace_bytes query.
- *     Scan entry points (linear, log, affine, angle): the workspace must be
+ *     Look-back scan entry points (linear, log, affine): the workspace must be
  *     zero-filled once before its first use and may then be passed, unchanged,
  *     to any sequence of scan calls ordered on one stream (of any op or size up
  *     to its capacity); nothing is cleared between calls, because each launch
  *     tags its look-back slots with a fresh epoch kept in the workspace header.
  *     Calls that can run concurrently (different streams) need different
- *     workspaces.  Delta entry points: contents on entry are irrelevant;
+ *     workspaces.  Angle and delta entry points: contents on entry are
+ *     irrelevant;
  *   - work is enqueued asynchronously on `stream`; nothing allocates, throws or
  *     synchronises;
  *   - the return value is a status: 0 ok, 1 invalid argument / outside the
@@ -83,19 +84,22 @@ int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const
  * h0 (B,n,k); k in {2,4,8}.  sched 0: brick-wall rounds (NA = rounds*k/2),
  * sched 1: all pairs i<j in lexicographic order, one plane per round
  * (rounds = k(k-1)/2 = NA).  flags bit 0: scale coordinate 1 by `scale`,
- * bit 1: decay by `gamma`. */
+ * bit 1: decay by `gamma`.  The forward writes the per-chunk transition
+ * products to `chunk_prod` (mg_angle_scan_state_bytes); the backward reads
+ * them.  The workspace's contents on entry are irrelevant (no look-back). */
 size_t mg_angle_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
+size_t mg_angle_scan_state_bytes(int64_t B, int64_t T, int64_t n, int k);
 int mg_angle_scan_fwd(const float* theta, const float* scale, const float* gamma, const float* b,
-                      const float* h0, float* h, int64_t B, int64_t T, int64_t n, int k,
-                      int sched, int rounds, int flags, void* ws, size_t ws_bytes,
-                      mg_stream_t stream);
-/* h = forward output, gh = dL/dh -> dtheta, dscale, dgamma (written when the
- * flag is set), db, dh0. */
+                      const float* h0, float* h, float* chunk_prod, int64_t B, int64_t T,
+                      int64_t n, int k, int sched, int rounds, int flags, void* ws,
+                      size_t ws_bytes, mg_stream_t stream);
+/* h = forward output, chunk_prod = the forward's chunk products, gh = dL/dh
+ * -> dtheta, dscale, dgamma (written when the flag is set), db, dh0. */
 int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma, const float* h0,
-                      const float* h, const float* gh, float* dtheta, float* dscale,
-                      float* dgamma, float* db, float* dh0, int64_t B, int64_t T, int64_t n,
-                      int k, int sched, int rounds, int flags, void* ws, size_t ws_bytes,
-                      mg_stream_t stream);
+                      const float* h, const float* chunk_prod, const float* gh, float* dtheta,
+                      float* dscale, float* dgamma, float* db, float* dh0, int64_t B, int64_t T,
+                      int64_t n, int k, int sched, int rounds, int flags, void* ws,
+                      size_t ws_bytes, mg_stream_t stream);
 
 /* ---- DeltaMinGRU chunked-WY delta rule ----------------------------------------
  * Replaces the reference's three forward kernels (_delta_prepass_kernel,

@@ -32,11 +32,12 @@ _SIGNATURES = {
     "mg_affine_scan_fwd": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _SZ, _P]),
     "mg_affine_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _I32, _I32, _P, _SZ, _P]),
     "mg_angle_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
+    "mg_angle_scan_state_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
     "mg_angle_scan_fwd": (
-        _I32, [_P] * 6 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        _I32, [_P] * 7 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
     "mg_angle_scan_bwd": (
-        _I32, [_P] * 11 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        _I32, [_P] * 12 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
     "mg_delta_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
     "mg_delta_state_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),

@@ -53,10 +53,14 @@ __device__ __forceinline__ void affm_compose(const AffM<K, W>& inner, const AffM
   }
 }
 
-// Row loads/stores of N floats.  NT selects non-temporal accesses, used for
-// data a kernel touches exactly once (held inputs, every output).
-template <int N, bool NT = false>
+// Row loads/stores of N floats.  NT_REQ asks for non-temporal accesses, used for
+// data a kernel touches exactly once (held inputs, every output); it is honoured
+// only for rows of one vector (N <= 4), where a wave's instruction covers whole
+// contiguous lines -- longer rows are split into lane-strided pieces that the
+// L2 has to merge.
+template <int N, bool NT_REQ = false>
 __device__ __forceinline__ void ld(float* dst, const float* __restrict__ src) {
+  constexpr bool NT = NT_REQ && N <= 4;
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
@@ -67,8 +71,8 @@ __device__ __forceinline__ void ld(float* dst, const float* __restrict__ src) {
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
       if constexpr (NT) {
-        dst[i] = mg_ld_stream(src + i);
-        dst[i + 1] = mg_ld_stream(src + i + 1);
+        const float2 v = mg_ld_stream2(src + i);
+        dst[i] = v.x; dst[i + 1] = v.y;
       } else {
         float2 v = *reinterpret_cast<const float2*>(src + i);
         dst[i] = v.x; dst[i + 1] = v.y;
@@ -80,8 +84,9 @@ __device__ __forceinline__ void ld(float* dst, const float* __restrict__ src) {
   }
 }
 
-template <int N, bool NT = false>
+template <int N, bool NT_REQ = false>
 __device__ __forceinline__ void st(float* __restrict__ dst, const float* src) {
+  constexpr bool NT = NT_REQ && N <= 4;
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
@@ -93,8 +98,7 @@ __device__ __forceinline__ void st(float* __restrict__ dst, const float* src) {
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
       if constexpr (NT) {
-        mg_st_stream(dst + i, src[i]);
-        mg_st_stream(dst + i + 1, src[i + 1]);
+        mg_st_stream2(dst + i, make_float2(src[i], src[i + 1]));
       } else {
         *reinterpret_cast<float2*>(dst + i) = make_float2(src[i], src[i + 1]);
       }

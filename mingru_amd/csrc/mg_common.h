@@ -102,7 +102,10 @@ __device__ __forceinline__ bool mg_slot_get(const mg_slot_t* p, float& v, unsign
 // Streaming (non-temporal) global accesses for data read or written exactly
 // once: the hint keeps single-use lines from displacing the look-back slots
 // and the other streams in the caches, which raises sustained HBM bandwidth
-// (a 2-in/2-out stream measured 5.5 -> 6.2 TB/s on MI355X).
+// (a 2-in/2-out stream measured 5.5 -> 6.2 TB/s on MI355X).  Use the streaming
+// stores only where one store instruction of a wave covers whole contiguous
+// lines (consecutive lanes, consecutive vectors): partial-line streaming stores
+// are not merged in L2 and cost several times their size.
 typedef float mg_v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float4 mg_ld_stream4(const float* p) {
@@ -112,6 +115,16 @@ __device__ __forceinline__ float4 mg_ld_stream4(const float* p) {
 __device__ __forceinline__ void mg_st_stream4(float* p, float4 x) {
   const mg_v4f v = {x.x, x.y, x.z, x.w};
   __builtin_nontemporal_store(v, reinterpret_cast<mg_v4f*>(p));
+}
+typedef float mg_v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float2 mg_ld_stream2(const float* p) {
+  const mg_v2f v = __builtin_nontemporal_load(reinterpret_cast<const mg_v2f*>(p));
+  return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ void mg_st_stream2(float* p, float2 x) {
+  const mg_v2f v = {x.x, x.y};
+  __builtin_nontemporal_store(v, reinterpret_cast<mg_v2f*>(p));
 }
 __device__ __forceinline__ float mg_ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void mg_st_stream(float* p, float x) { __builtin_nontemporal_store(x, p); }

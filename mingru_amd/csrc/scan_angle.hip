@@ -17,19 +17,25 @@
 //   LEX:   one plane per round over all pairs i<j in lexicographic order,
 //          k(k-1)/2 angles per token (the 28-rotation SO(8) workload).
 //
-// Parallel scan over time: the chunk aggregate of the affine recurrence is
-// the map h -> P h + L with P the k x k product of the chunk's transitions;
-// each thread builds it for its sub-chunk by pushing the k columns of P and
-// the column L through the rotations (k+1 rotated columns per token), then
-// the shared look-back (mg_affm.h) chains the chunks.  The final pass
-// re-applies the rotations to the state vector only.
+// Parallel scan over time, reduce-then-scan over chunks of AN_CHUNK tokens
+// (no workgroup ever waits on another, so there is no serial chain of
+// cross-workgroup hops):
+//   pass 1  one lane per (block, chunk) builds the chunk's affine map
+//           h -> P_c h + L_c by pushing the k columns of P and the column L
+//           through the chunk's rotations (k+1 rotated columns per token);
+//   pass 2  one lane per block walks the chunk boundaries in order,
+//           h_{c+1} = P_c h_c + L_c, carrying only its k-vector;
+//   pass 3  one lane per (block, chunk) re-applies the rotations to the state
+//           vector from its chunk-entry state and writes every h_t.
+// The forward saves the chunk products P_c for the backward.
 //
 // Backward: exact stored-state recompute.  h_{t-1} is read from the forward
 // output (never reconstructed by dividing out gamma or the scale), the
 // per-rotation states are recovered from the recomputed v_R by applying each
 // rotation's transpose (orthogonal, so no error amplification), and the
-// adjoint y_t = M_t^T (g_t + y_{t+1}) runs through the same chunked
-// look-back in reverse time.
+// adjoint y_t = M_t^T (g_t + y_{t+1}) runs through the same three passes in
+// reverse time.  Its chunk maps are y -> P_c^T y + Lb_c: the linear part is
+// the saved forward product transposed, so pass 1 only sweeps one column.
 #include "mg_affm.h"
 
 #include <algorithm>
@@ -41,12 +47,14 @@ using namespace mg;
 
 enum : int { SCHED_BRICK = 0, SCHED_LEX = 1 };
 
-// Chunk = AN_WAVES * AN_TSUB tokens per workgroup.  64-token chunks keep the
-// look-back chain short (32 hops at T = 2048) while the per-thread aggregate
-// work (k + 1 rotated columns per token) stays in registers; chosen by timing
-// on MI355X at the 28-rotation SO(8) workload.
-constexpr int AN_WAVES = 8;
-constexpr int AN_TSUB = 8;
+// Reduce-then-scan over chunks of AN_CHUNK tokens: pass 1 builds every chunk's
+// affine map in parallel (one lane per (block, chunk)), pass 2 walks the chunk
+// boundaries of each block carrying only its k-vector, pass 3 re-applies the
+// rotations from each chunk's entry state.  No workgroup waits on another.
+constexpr int AN_WAVES = 4;          // waves per workgroup of the chunk-parallel passes
+constexpr int AN_CHUNK = 16;         // tokens per chunk
+constexpr int AN_SCAN_THREADS = 256;  // threads per workgroup of the boundary walk
+constexpr int AN_SCAN_AHEAD = 8;      // chunks prefetched ahead by the boundary walk
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -187,6 +195,56 @@ __device__ __forceinline__ void apply_M(float (&X)[K][NC], const float* __restri
   }
 }
 
+// Lexicographic schedule with the token's R angles already in registers.
+template <int K, bool HS, bool HD, int NC>
+__device__ __forceinline__ void apply_M_lex(float (&X)[K][NC], const float (&ang)[K * (K - 1) / 2],
+                                            float d, float gm) {
+  constexpr int R = K * (K - 1) / 2;
+  if (HS) {
+#pragma unroll
+    for (int q = 0; q < NC; ++q) X[1][q] *= d;
+  }
+  static_for(
+      [&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        float sn, cs;
+        mg_sincos(ang[r], sn, cs);
+        rot_rows<K, NC, lex_first(K, r), lex_second(K, r)>(X, cs, sn);
+      },
+      std::make_index_sequence<R>{});
+  if (HD) {
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int q = 0; q < NC; ++q) X[i][q] *= gm;
+  }
+}
+
+template <int K, bool HS, bool HD, int NC>
+__device__ __forceinline__ void apply_Mt_lex(float (&X)[K][NC],
+                                             const float (&ang)[K * (K - 1) / 2], float d,
+                                             float gm) {
+  constexpr int R = K * (K - 1) / 2;
+  if (HD) {
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int q = 0; q < NC; ++q) X[i][q] *= gm;
+  }
+  static_for(
+      [&](auto rc) {
+        constexpr int r = R - 1 - decltype(rc)::value;
+        float sn, cs;
+        mg_sincos(ang[r], sn, cs);
+        rot_rows_t<K, NC, lex_first(K, r), lex_second(K, r)>(X, cs, sn);
+      },
+      std::make_index_sequence<R>{});
+  if (HS) {
+#pragma unroll
+    for (int q = 0; q < NC; ++q) X[1][q] *= d;
+  }
+}
+
 // X <- M_t^T X.
 template <int K, int SCHED, bool HS, bool HD, int NC>
 __device__ __forceinline__ void apply_Mt(float (&X)[K][NC], const float* __restrict__ th,
@@ -255,31 +313,97 @@ struct AnArgs {
   float* dscale;
   float* dgamma;
   float* dh0;
+  float* prod;   // chunk products P_c, [chunk][block][K*K]: forward writes, backward reads
+  float* lsum;   // chunk offsets (forward L_c, backward adjoint offsets), [chunk][block][K]
+  float* bound;  // chunk-entry states (forward) / adjoints (backward), [chunk][block][K]
   int rounds;
   int na;  // angles per token
 };
 
-template <int K, int SCHED, bool HS, bool HD>
-__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, AfGeom g,
-                                                                      unsigned* header,
-                                                                      mg_slot_t* agg_data,
-                                                                      mg_slot_t* incl_data) {
-  AfThread th = af_thread<false>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (AN_WAVES * AN_TSUB) + th.w * AN_TSUB;
-  const int64_t T = g.T, n = g.n;
+// Per-token inputs of the lexicographic kernels, loaded one token ahead: at one
+// wave per SIMD nothing else hides a load issued only when it is needed.
+template <int K, bool HS, bool HD>
+struct LexTok {
+  static constexpr int R = K * (K - 1) / 2;
+  float ang[R];
+  float v[K];   // b_t (forward) or g_t (backward)
+  float hp[K];  // h_{t-1} (backward final pass only)
+  float d, gm;
 
-  // Local aggregate: push [P | L] through the sub-chunk's transitions.
+  template <bool HP>
+  __device__ __forceinline__ void load(const AnArgs& a, const float* vec, int64_t lane_tok,
+                                       int64_t t, int64_t n, int64_t blk) {
+    ld<R>(ang, a.theta + lane_tok * R);
+    ld<K>(v, vec + lane_tok * K);
+    d = HS ? a.scale[lane_tok] : 1.f;
+    gm = HD ? a.gamma[lane_tok] : 1.f;
+    if constexpr (HP) {
+      if (t > 0) ld<K>(hp, a.h + lane_tok * K - n * K);
+      else ld<K>(hp, a.h0 + blk * K);
+    }
+  }
+};
+
+struct AnGeom {
+  int64_t T, n, NB;  // tokens, blocks per batch row, blocks in total (B * n)
+  int n_tiles, n_lg, n_chunks;
+};
+
+// Chunk-parallel passes: one wave per (lane group, chunk), one lane per block.
+struct AnThread {
+  int64_t bb, plane, blk;
+  int c;
+  bool ok;
+};
+
+__device__ __forceinline__ AnThread an_thread(const AnGeom& g) {
+  AnThread th;
+  const int64_t gw = (int64_t)blockIdx.x * AN_WAVES + threadIdx.x / MG_WAVE;
+  const int lane = threadIdx.x & (MG_WAVE - 1);
+  const int lg = (int)(gw % g.n_lg);
+  th.c = (int)(gw / g.n_lg);
+  th.bb = lg / g.n_tiles;
+  th.plane = (int64_t)(lg % g.n_tiles) * MG_WAVE + lane;
+  th.ok = th.c < g.n_chunks && th.plane < g.n;
+  th.blk = th.bb * g.n + th.plane;
+  return th;
+}
+
+// Index of field f of chunk c for block blk in a [chunk][block][field] array:
+// a lane's fields are contiguous, and so are the k lanes of one block in the
+// boundary walk.
+__device__ __forceinline__ int64_t an_idx(const AnGeom& g, int c, int f, int nf, int64_t blk) {
+  return ((int64_t)c * g.NB + blk) * nf + f;
+}
+
+// ---- forward pass 1: chunk aggregates h -> P_c h + L_c ------------------------
+template <int K, int SCHED, bool HS, bool HD>
+__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, AnGeom g) {
+  const AnThread th = an_thread(g);
+  if (!th.ok) return;
+  const int64_t t0 = (int64_t)th.c * AN_CHUNK;
+  // Push [P | L] through the chunk's transitions.
   float X[K][K + 1];
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
     for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
+  const int64_t te = min(t0 + AN_CHUNK, g.T);
+  if constexpr (SCHED == SCHED_LEX) {
+    LexTok<K, HS, HD> cur, nxt;
+    cur.template load<false>(a, a.b, (th.bb * g.T + t0) * g.n + th.plane, t0, g.n, th.blk);
+    for (int64_t t = t0; t < te; ++t) {
+      if (t + 1 < te)
+        nxt.template load<false>(a, a.b, (th.bb * g.T + t + 1) * g.n + th.plane, t + 1, g.n,
+                                 th.blk);
+      apply_M_lex<K, HS, HD, K + 1>(X, cur.ang, cur.d, cur.gm);
 #pragma unroll
-  for (int s = 0; s < AN_TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.ok && t < T) {
-      const int64_t lane_tok = (th.bb * T + t) * n + th.plane;
+      for (int i = 0; i < K; ++i) X[i][K] += cur.v[i];
+      cur = nxt;
+    }
+  } else {
+    for (int64_t t = t0; t < te; ++t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
       const float d = HS ? a.scale[lane_tok] : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       apply_M<K, SCHED, HS, HD, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, gm);
@@ -289,35 +413,95 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, 
       for (int i = 0; i < K; ++i) X[i][K] += bt[i];
     }
   }
-  AffM<K, 1> loc, seed, carry;
+  float Pf[K * K], Lf[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-      loc.P[i][j] = X[i][j];
-      seed.P[i][j] = 0.f;
-    }
-    loc.L[i][0] = X[i][K];
-    seed.L[i][0] = 0.f;
+    for (int j = 0; j < K; ++j) Pf[i * K + j] = X[i][j];
+    Lf[i] = X[i][K];
   }
-  if (th.c == 0 && th.ok) {
-    float hz[K];
-    ld<K>(hz, a.h0 + (th.bb * n + th.plane) * K);
-#pragma unroll
-    for (int i = 0; i < K; ++i) seed.L[i][0] = hz[i];
-  }
-  af_carry<K, 1, AN_WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
+  st<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk), Pf);
+  st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
+}
 
-  // Final pass: the state entering the sub-chunk is carry.L (the seed's P = 0
-  // turns every prefix into a constant map).
+// ---- forward pass 2: states at chunk boundaries, h_{c+1} = P_c h_c + L_c -------
+// K lanes per block, lane q owning state row q; the state vector is exchanged
+// within the K-lane group by shuffles.  Each lane's row of (P_c, L_c) is
+// prefetched AN_SCAN_AHEAD chunks ahead, because one step is only K FMAs and
+// the walk would otherwise wait a full memory latency per chunk.
+template <int K>
+__global__ __launch_bounds__(AN_SCAN_THREADS) void angle_fwd_scan(AnArgs a, AnGeom g) {
+  const int64_t gt = (int64_t)blockIdx.x * AN_SCAN_THREADS + threadIdx.x;
+  const int64_t blk = gt / K;
+  const int q = (int)(gt % K);
+  if (blk >= g.NB) return;  // whole K-lane groups leave together
+  constexpr int D = AN_SCAN_AHEAD;
+  // Double-buffered batches of D chunks: the loads of batch b+1 are in flight
+  // while batch b is walked from registers.
+  float cur[D][K + 1], nxt[D][K + 1];
+  auto fetch = [&](int c0, float (&r)[D][K + 1]) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = min(c0 + d, g.n_chunks - 1);  // clamped reads past the end are unused
+      ld<K>(r[d], a.prod + an_idx(g, c, q * K, K * K, blk));
+      r[d][K] = a.lsum[an_idx(g, c, q, K, blk)];
+    }
+  };
+  fetch(0, cur);
+  float h = a.h0[blk * K + q];
+  for (int c0 = 0; c0 < g.n_chunks; c0 += D) {
+    fetch(c0 + D, nxt);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = c0 + d;
+      if (c < g.n_chunks) {
+        a.bound[an_idx(g, c, q, K, blk)] = h;
+        float acc = cur[d][K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) acc = fmaf(cur[d][j], __shfl(h, j, K), acc);
+        h = acc;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int j = 0; j <= K; ++j) cur[d][j] = nxt[d][j];
+  }
+}
+
+// ---- forward pass 3: every token's state from its chunk-entry state ------------
+template <int K, int SCHED, bool HS, bool HD>
+__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, AnGeom g) {
+  const AnThread th = an_thread(g);
+  if (!th.ok) return;
+  const int64_t t0 = (int64_t)th.c * AN_CHUNK;
   float v[K][1];
+  {
+    float b0[K];
+    ld<K>(b0, a.bound + an_idx(g, th.c, 0, K, th.blk));
 #pragma unroll
-  for (int i = 0; i < K; ++i) v[i][0] = carry.L[i][0];
+    for (int i = 0; i < K; ++i) v[i][0] = b0[i];
+  }
+  const int64_t te = min(t0 + AN_CHUNK, g.T);
+  if constexpr (SCHED == SCHED_LEX) {
+    LexTok<K, HS, HD> cur, nxt;
+    cur.template load<false>(a, a.b, (th.bb * g.T + t0) * g.n + th.plane, t0, g.n, th.blk);
+    for (int64_t t = t0; t < te; ++t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+      if (t + 1 < te) nxt.template load<false>(a, a.b, lane_tok + g.n, t + 1, g.n, th.blk);
+      apply_M_lex<K, HS, HD, 1>(v, cur.ang, cur.d, cur.gm);
+      float bt[K];
 #pragma unroll
-  for (int s = 0; s < AN_TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.ok && t < T) {
-      const int64_t lane_tok = (th.bb * T + t) * n + th.plane;
+      for (int i = 0; i < K; ++i) {
+        v[i][0] += cur.v[i];
+        bt[i] = v[i][0];
+      }
+      st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
+      cur = nxt;
+    }
+  } else {
+    for (int64_t t = t0; t < te; ++t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
       const float d = HS ? a.scale[lane_tok] : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       apply_M<K, SCHED, HS, HD, 1>(v, a.theta + lane_tok * a.na, a.rounds, d, gm);
@@ -328,8 +512,49 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_kernel(AnArgs a, 
         v[i][0] += bt[i];
         bt[i] = v[i][0];
       }
-      st<K, true>(a.out + lane_tok * K, bt);
+      st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
     }
+  }
+}
+
+// token_grad for the lexicographic schedule with the angles already loaded.
+template <int K, bool HS, bool HD>
+__device__ __forceinline__ void token_grad_lex(float (&x)[K][1], const float (&hp)[K],
+                                               const float (&ang)[K * (K - 1) / 2],
+                                               float* __restrict__ dth, float d, float gm,
+                                               float& dd, float& dg) {
+  constexpr int R = K * (K - 1) / 2;
+  float v[K][1];
+#pragma unroll
+  for (int i = 0; i < K; ++i) v[i][0] = hp[i];
+  if (HS) v[1][0] *= d;
+  float cs[R], sn[R], gr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) mg_sincos(ang[r], sn[r], cs[r]);
+  static_for(
+      [&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        rot_rows<K, 1, lex_first(K, r), lex_second(K, r)>(v, cs[r], sn[r]);
+      },
+      std::make_index_sequence<R>{});
+  if (HD) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) acc = fmaf(x[i][0], v[i][0], acc);
+    dg = acc;
+#pragma unroll
+    for (int i = 0; i < K; ++i) x[i][0] *= gm;
+  }
+  static_for(
+      [&](auto rc) {
+        constexpr int r = R - 1 - decltype(rc)::value;
+        gr[r] = rot_grad<K, lex_first(K, r), lex_second(K, r)>(v, x, cs[r], sn[r]);
+      },
+      std::make_index_sequence<R>{});
+  st<R>(dth, gr);  // partial-line rows: L2 merges them (no streaming hint)
+  if (HS) {
+    dd = x[1][0] * hp[1];
+    x[1][0] *= d;
   }
 }
 
@@ -369,7 +594,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
           gr[r] = rot_grad<K, lex_first(K, r), lex_second(K, r)>(v, x, cs[r], sn[r]);
         },
         std::make_index_sequence<R>{});
-    st<R, true>(dth, gr);
+    st<R>(dth, gr);  // partial-line rows: L2 merges them (no streaming hint)
   } else {
     constexpr int H = K / 2;
     for (int r = 0; r < rounds; ++r) {
@@ -409,7 +634,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
             },
             std::make_index_sequence<H>{});
       }
-      st<H, true>(dth + r * H, gr);
+      st<H>(dth + r * H, gr);  // partial-line rows: L2 merges them
     }
   }
   if (HS) {
@@ -418,66 +643,146 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
   }
 }
 
+// ---- backward pass 1: adjoint offsets of each chunk ---------------------------
+// The adjoint flowing out of chunk c to the left is y_out = P_c^T y_in + Lb_c,
+// with y_in the adjoint flowing in from the right, P_c the forward chunk
+// product (saved by the forward) and Lb_c this pass's zero-start reverse sweep
+// x <- M_t^T (x + g_t).
 template <int K, int SCHED, bool HS, bool HD>
-__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_kernel(AnArgs a, AfGeom g,
-                                                                      unsigned* header,
-                                                                      mg_slot_t* agg_data,
-                                                                      mg_slot_t* incl_data) {
-  AfThread th = af_thread<true>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (AN_WAVES * AN_TSUB) + th.w * AN_TSUB;
-  const int64_t T = g.T, n = g.n;
-
-  // Local reverse aggregate [Q | L]: X <- M_t^T (X + [0 | g_t]) from the end.
-  float X[K][K + 1];
+__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, AnGeom g) {
+  const AnThread th = an_thread(g);
+  if (!th.ok) return;
+  const int64_t t0 = (int64_t)th.c * AN_CHUNK;
+  float x[K][1];
 #pragma unroll
-  for (int i = 0; i < K; ++i)
+  for (int i = 0; i < K; ++i) x[i][0] = 0.f;
+  const int64_t te = min(t0 + AN_CHUNK, g.T);
+  if constexpr (SCHED == SCHED_LEX) {
+    LexTok<K, HS, HD> cur, nxt;
+    cur.template load<false>(a, a.gh, (th.bb * g.T + te - 1) * g.n + th.plane, te - 1, g.n,
+                             th.blk);
+    for (int64_t t = te - 1; t >= t0; --t) {
+      if (t > t0)
+        nxt.template load<false>(a, a.gh, (th.bb * g.T + t - 1) * g.n + th.plane, t - 1, g.n,
+                                 th.blk);
 #pragma unroll
-    for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
-#pragma unroll
-  for (int s = AN_TSUB - 1; s >= 0; --s) {
-    const int64_t t = t0 + s;
-    if (th.ok && t < T) {
-      const int64_t lane_tok = (th.bb * T + t) * n + th.plane;
+      for (int i = 0; i < K; ++i) x[i][0] += cur.v[i];
+      apply_Mt_lex<K, HS, HD, 1>(x, cur.ang, cur.d, cur.gm);
+      cur = nxt;
+    }
+  } else {
+    for (int64_t t = te - 1; t >= t0; --t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
       const float d = HS ? a.scale[lane_tok] : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       float gt[K];
       ld<K>(gt, a.gh + lane_tok * K);
 #pragma unroll
-      for (int i = 0; i < K; ++i) X[i][K] += gt[i];
-      apply_Mt<K, SCHED, HS, HD, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, gm);
+      for (int i = 0; i < K; ++i) x[i][0] += gt[i];
+      apply_Mt<K, SCHED, HS, HD, 1>(x, a.theta + lane_tok * a.na, a.rounds, d, gm);
     }
   }
-  AffM<K, 1> loc, seed, carry;
+  float xf[K];
 #pragma unroll
-  for (int i = 0; i < K; ++i) {
-#pragma unroll
-    for (int j = 0; j < K; ++j) loc.P[i][j] = X[i][j];
-    loc.L[i][0] = X[i][K];
-  }
-  affm_identity(seed);
-  af_carry<K, 1, AN_WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
+  for (int i = 0; i < K; ++i) xf[i] = x[i][0];
+  st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), xf);
+}
 
+// ---- backward pass 2: adjoints at chunk boundaries, right to left --------------
+// y_out = P_c^T y_in + Lb_c; K lanes per block, lane q owning adjoint row q
+// (column q of P_c), prefetched as in the forward walk.
+template <int K>
+__global__ __launch_bounds__(AN_SCAN_THREADS) void angle_bwd_scan(AnArgs a, AnGeom g) {
+  const int64_t gt = (int64_t)blockIdx.x * AN_SCAN_THREADS + threadIdx.x;
+  const int64_t blk = gt / K;
+  const int q = (int)(gt % K);
+  if (blk >= g.NB) return;
+  constexpr int D = AN_SCAN_AHEAD;
+  float cur[D][K + 1], nxt[D][K + 1];
+  auto fetch = [&](int c0, float (&r)[D][K + 1]) {  // chunks c0, c0-1, ..., c0-D+1
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = max(c0 - d, 0);  // clamped reads past the start are unused
+      const float* pc = a.prod + an_idx(g, c, 0, K * K, blk);
+#pragma unroll
+      for (int i = 0; i < K; ++i) r[d][i] = pc[i * K + q];
+      r[d][K] = a.lsum[an_idx(g, c, q, K, blk)];
+    }
+  };
+  const int last = g.n_chunks - 1;
+  fetch(last, cur);
+  float y = 0.f;
+  for (int c0 = last; c0 >= 0; c0 -= D) {
+    fetch(c0 - D, nxt);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = c0 - d;
+      if (c >= 0) {
+        a.bound[an_idx(g, c, q, K, blk)] = y;
+        float acc = cur[d][K];
+#pragma unroll
+        for (int i = 0; i < K; ++i) acc = fmaf(cur[d][i], __shfl(y, i, K), acc);
+        y = acc;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int i = 0; i <= K; ++i) cur[d][i] = nxt[d][i];
+  }
+  a.dh0[blk * K + q] = y;  // the adjoint leaving chunk 0 is dL/dh0
+}
+
+// ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
+template <int K, int SCHED, bool HS, bool HD>
+__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, AnGeom g) {
+  const AnThread th = an_thread(g);
+  if (!th.ok) return;
+  const int64_t t0 = (int64_t)th.c * AN_CHUNK;
   float y[K][1];
+  {
+    float b0[K];
+    ld<K>(b0, a.bound + an_idx(g, th.c, 0, K, th.blk));
 #pragma unroll
-  for (int i = 0; i < K; ++i) y[i][0] = carry.L[i][0];
+    for (int i = 0; i < K; ++i) y[i][0] = b0[i];
+  }
+  const int64_t te = min(t0 + AN_CHUNK, g.T);
+  if constexpr (SCHED == SCHED_LEX) {
+    LexTok<K, HS, HD> cur, nxt;
+    cur.template load<true>(a, a.gh, (th.bb * g.T + te - 1) * g.n + th.plane, te - 1, g.n,
+                            th.blk);
+    for (int64_t t = te - 1; t >= t0; --t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+      if (t > t0) nxt.template load<true>(a, a.gh, lane_tok - g.n, t - 1, g.n, th.blk);
+      float gt[K];
 #pragma unroll
-  for (int s = AN_TSUB - 1; s >= 0; --s) {
-    const int64_t t = t0 + s;
-    if (th.ok && t < T) {
-      const int64_t lane_tok = (th.bb * T + t) * n + th.plane;
+      for (int i = 0; i < K; ++i) {
+        y[i][0] += cur.v[i];
+        gt[i] = y[i][0];
+      }
+      st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
+      float dd = 0.f, dg = 0.f;
+      token_grad_lex<K, HS, HD>(y, cur.hp, cur.ang, a.dtheta + lane_tok * a.na, cur.d, cur.gm,
+                                dd, dg);
+      if (HS) a.dscale[lane_tok] = dd;
+      if (HD) a.dgamma[lane_tok] = dg;
+      cur = nxt;
+    }
+  } else {
+    for (int64_t t = te - 1; t >= t0; --t) {
+      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
       const float d = HS ? a.scale[lane_tok] : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       float gt[K], hp[K];
       ld<K>(gt, a.gh + lane_tok * K);
-      if (t > 0) ld<K>(hp, a.h + lane_tok * K - n * K);
-      else ld<K>(hp, a.h0 + (th.bb * n + th.plane) * K);
+      if (t > 0) ld<K>(hp, a.h + lane_tok * K - g.n * K);
+      else ld<K>(hp, a.h0 + th.blk * K);
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         y[i][0] += gt[i];
         gt[i] = y[i][0];
       }
-      st<K, true>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
+      st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
       float dd = 0.f, dg = 0.f;
       token_grad<K, SCHED, HS, HD>(y, hp, a.theta + lane_tok * a.na, a.dtheta + lane_tok * a.na,
                                    a.rounds, d, gm, dd, dg);
@@ -485,53 +790,57 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_kernel(AnArgs a, 
       if (HD) a.dgamma[lane_tok] = dg;
     }
   }
-  if (t0 == 0 && th.ok) {
-    float o[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) o[i] = y[i][0];
-    st<K>(a.dh0 + (th.bb * n + th.plane) * K, o);
-  }
 }
 
 // ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
 
-AfGeom an_geom(int64_t B, int64_t T, int64_t n) {
-  AfGeom g;
+AnGeom an_geom(int64_t B, int64_t T, int64_t n) {
+  AnGeom g;
   g.T = T;
   g.n = n;
+  g.NB = B * n;
   g.n_tiles = (int)((n + MG_WAVE - 1) / MG_WAVE);
   g.n_lg = (int)(B * g.n_tiles);
-  const int64_t cl = (int64_t)AN_WAVES * AN_TSUB;
-  g.n_chunks = (int)((T + cl - 1) / cl);
+  g.n_chunks = (int)((T + AN_CHUNK - 1) / AN_CHUNK);
   return g;
 }
 
+// Workspace: chunk offsets and chunk-entry states, K floats each per (chunk, block).
 size_t an_ws_bytes(int64_t B, int64_t T, int64_t n, int k) {
-  const AfGeom g = an_geom(B, T, n);
-  const size_t data = (size_t)g.n_lg * g.n_chunks * (size_t)(k * k + k) * MG_WAVE *
-                      sizeof(mg_slot_t);
-  return MG_HEADER_BYTES + 2 * mg_align_up(data, 256);
+  const AnGeom g = an_geom(B, T, n);
+  const size_t one = mg_align_up((size_t)g.n_chunks * k * g.NB * sizeof(float), 256);
+  return MG_HEADER_BYTES + 2 * one;
+}
+
+// Chunk products saved by the forward for the backward: K*K floats per (chunk, block).
+size_t an_state_bytes(int64_t B, int64_t T, int64_t n, int k) {
+  const AnGeom g = an_geom(B, T, n);
+  return (size_t)g.n_chunks * k * k * g.NB * sizeof(float);
 }
 
 template <int K, int SCHED, bool HS, bool HD, bool BWD>
-int an_launch(const AnArgs& a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_bytes,
+int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_bytes,
               hipStream_t stream) {
-  const AfGeom g = an_geom(B, T, n);
-  const size_t total = an_ws_bytes(B, T, n, K);
-  if (ws_bytes < total) return MG_ERR_WORKSPACE;
-  const size_t data = (total - MG_HEADER_BYTES) / 2;
-  unsigned* header = (unsigned*)ws;
-  mg_slot_t* agg = (mg_slot_t*)((char*)ws + MG_HEADER_BYTES);
-  mg_slot_t* incl = (mg_slot_t*)((char*)ws + MG_HEADER_BYTES + data);
-  const dim3 grid((unsigned)(g.n_lg * g.n_chunks)), block(MG_WAVE * AN_WAVES);
-  if (BWD)
-    hipLaunchKernelGGL((angle_bwd_kernel<K, SCHED, HS, HD>), grid, block, 0, stream, a, g, header,
-                       agg, incl);
-  else
-    hipLaunchKernelGGL((angle_fwd_kernel<K, SCHED, HS, HD>), grid, block, 0, stream, a, g, header,
-                       agg, incl);
+  const AnGeom g = an_geom(B, T, n);
+  if (ws_bytes < an_ws_bytes(B, T, n, K)) return MG_ERR_WORKSPACE;
+  const size_t one = mg_align_up((size_t)g.n_chunks * K * g.NB * sizeof(float), 256);
+  a.lsum = (float*)((char*)ws + MG_HEADER_BYTES);
+  a.bound = (float*)((char*)ws + MG_HEADER_BYTES + one);
+  const int64_t waves = (int64_t)g.n_lg * g.n_chunks;
+  const dim3 grid((unsigned)((waves + AN_WAVES - 1) / AN_WAVES)), block(MG_WAVE * AN_WAVES);
+  const dim3 sgrid((unsigned)((g.NB * K + AN_SCAN_THREADS - 1) / AN_SCAN_THREADS)),
+      sblock(AN_SCAN_THREADS);
+  if (BWD) {
+    hipLaunchKernelGGL((angle_bwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+  } else {
+    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_fwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+  }
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
@@ -565,8 +874,8 @@ bool an_args_ok(int64_t B, int64_t T, int64_t n, int k, int sched, int rounds) {
 }
 
 bool an_geometry_ok(int64_t B, int64_t T, int64_t n) {
-  const AfGeom g = an_geom(B, T, n);
-  return (int64_t)g.n_lg * g.n_chunks < (1ll << 24);
+  const AnGeom g = an_geom(B, T, n);
+  return (int64_t)g.n_lg * g.n_chunks < (1ll << 31) - AN_WAVES && g.NB * 8 < (1ll << 31);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -576,16 +885,21 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 extern "C" {
 
 size_t mg_angle_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k) {
-  if (B <= 0 || T <= 0 || n <= 0 || k <= 0) return 256;
+  if (B <= 0 || T <= 0 || n <= 0 || k <= 0 || k > 8) return 256;
   return an_ws_bytes(B, T, n, k);
 }
 
+size_t mg_angle_scan_state_bytes(int64_t B, int64_t T, int64_t n, int k) {
+  if (B <= 0 || T <= 0 || n <= 0 || k <= 0 || k > 8) return 0;
+  return an_state_bytes(B, T, n, k);
+}
+
 int mg_angle_scan_fwd(const float* theta, const float* scale, const float* gamma, const float* b,
-                      const float* h0, float* h, int64_t B, int64_t T, int64_t n, int k,
-                      int sched, int rounds, int flags, void* ws, size_t ws_bytes,
-                      hipStream_t stream) {
-  if (!theta || !b || !h0 || !h || !ws || !an_args_ok(B, T, n, k, sched, rounds) ||
-      !an_geometry_ok(B, T, n))
+                      const float* h0, float* h, float* chunk_prod, int64_t B, int64_t T,
+                      int64_t n, int k, int sched, int rounds, int flags, void* ws,
+                      size_t ws_bytes, hipStream_t stream) {
+  if (!theta || !b || !h0 || !h || !chunk_prod || !ws ||
+      !an_args_ok(B, T, n, k, sched, rounds) || !an_geometry_ok(B, T, n))
     return MG_ERR_ARG;
   if (((flags & 1) && !scale) || ((flags & 2) && !gamma)) return MG_ERR_ARG;
   if (!aligned16(theta) || !aligned16(b) || !aligned16(h0) || !aligned16(h)) return MG_ERR_ARG;
@@ -596,17 +910,18 @@ int mg_angle_scan_fwd(const float* theta, const float* scale, const float* gamma
   a.b = b;
   a.h0 = h0;
   a.out = h;
+  a.prod = chunk_prod;
   a.rounds = rounds;
   a.na = sched == SCHED_LEX ? k * (k - 1) / 2 : rounds * (k / 2);
   return an_dispatch<false>(a, B, T, n, k, sched, flags, ws, ws_bytes, stream);
 }
 
 int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma, const float* h0,
-                      const float* h, const float* gh, float* dtheta, float* dscale,
-                      float* dgamma, float* db, float* dh0, int64_t B, int64_t T, int64_t n,
-                      int k, int sched, int rounds, int flags, void* ws, size_t ws_bytes,
-                      hipStream_t stream) {
-  if (!theta || !h0 || !h || !gh || !dtheta || !db || !dh0 || !ws ||
+                      const float* h, const float* chunk_prod, const float* gh, float* dtheta,
+                      float* dscale, float* dgamma, float* db, float* dh0, int64_t B, int64_t T,
+                      int64_t n, int k, int sched, int rounds, int flags, void* ws,
+                      size_t ws_bytes, hipStream_t stream) {
+  if (!theta || !h0 || !h || !chunk_prod || !gh || !dtheta || !db || !dh0 || !ws ||
       !an_args_ok(B, T, n, k, sched, rounds) || !an_geometry_ok(B, T, n))
     return MG_ERR_ARG;
   if (((flags & 1) && (!scale || !dscale)) || ((flags & 2) && (!gamma || !dgamma)))
@@ -626,6 +941,7 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
   a.dscale = dscale;
   a.dgamma = dgamma;
   a.dh0 = dh0;
+  a.prod = const_cast<float*>(chunk_prod);
   a.rounds = rounds;
   a.na = sched == SCHED_LEX ? k * (k - 1) / 2 : rounds * (k / 2);
   return an_dispatch<true>(a, B, T, n, k, sched, flags, ws, ws_bytes, stream);

@@ -469,10 +469,14 @@ class _AngleScanFn(torch.autograd.Function):
         th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
         Bn, T, n, k = b32.shape
         h = torch.empty_like(b32)
-        ws = _scan_workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
+        lib = _lib()
+        # Chunk products P_c, saved for the backward (whose chunk maps are P_c^T).
+        prod = torch.empty(max(int(lib.mg_angle_scan_state_bytes(Bn, T, n, k)), 16) // 4,
+                           dtype=torch.float32, device=b32.device)
+        ws = _workspace(lib.mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
         _call("mg_angle_scan_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032), _ptr(h),
-              Bn, T, n, k, sched, rounds, flags, _ptr(ws), ws.numel(), _stream(b32))
-        ctx.save_for_backward(th, sc, gm, h032, h)
+              _ptr(prod), Bn, T, n, k, sched, rounds, flags, _ptr(ws), ws.numel(), _stream(b32))
+        ctx.save_for_backward(th, sc, gm, h032, h, prod)
         ctx.meta = (sched, rounds, flags, out_dtype, theta.dtype, scale.dtype, gamma.dtype,
                     h0.dtype)
         return h if out_dtype == torch.float32 else h.to(out_dtype)
@@ -480,7 +484,7 @@ class _AngleScanFn(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, gh):
-        th, sc, gm, h032, h = ctx.saved_tensors
+        th, sc, gm, h032, h, prod = ctx.saved_tensors
         sched, rounds, flags, out_dtype, tdt, sdt, gdt, hdt = ctx.meta
         Bn, T, n, k = h.shape
         (gh32,) = _as_f32(gh)
@@ -491,10 +495,10 @@ class _AngleScanFn(torch.autograd.Function):
         dgm = torch.zeros_like(gm) if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
-        ws = _scan_workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
-        _call("mg_angle_scan_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h), _ptr(gh32),
-              _ptr(dth), _ptr(dsc), _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k, sched, rounds,
-              flags, _ptr(ws), ws.numel(), _stream(h))
+        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
+        _call("mg_angle_scan_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h), _ptr(prod),
+              _ptr(gh32), _ptr(dth), _ptr(dsc), _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k,
+              sched, rounds, flags, _ptr(ws), ws.numel(), _stream(h))
         return (dth.to(tdt), None if dsc is None else dsc.to(sdt),
                 None if dgm is None else dgm.to(gdt), db.to(out_dtype), dh0.to(hdt),
                 None, None, None)

@@ -52,6 +52,8 @@ def test_workspace_queries(lib):
     assert lib.mg_linear_scan_workspace_bytes(16, 4096, 1024) >= 256
     assert lib.mg_affine_scan_workspace_bytes(16, 4096, 256, 2, 1) >= 256
     assert lib.mg_angle_scan_workspace_bytes(8, 2048, 64, 8) >= 256
+    # angle chunk products: 8x8 floats per (block, 16-token chunk)
+    assert lib.mg_angle_scan_state_bytes(8, 2048, 64, 8) == 128 * 64 * 8 * 64 * 4
     # delta: six padded 64 x 64 fp32 matrices per (batch, head, chunk)
     assert lib.mg_delta_workspace_bytes(8, 8, 8192, 1, 64, 64, 64) == 6 * 64 * 128 * 64 * 64 * 4
     assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 64 * 128 * 64 * 64 * 4
@@ -66,8 +68,12 @@ def test_invalid_arguments_are_rejected_on_the_host(lib):
     assert lib.mg_linear_scan_fwd(one, one, one, one, 0, 4, 4, one, 4096, NULL) == 1
     assert lib.mg_log_scan_fwd(one, one, NULL, 1, 4, 4, one, 4096, NULL) == 1
     assert lib.mg_affine_scan_fwd(one, one, one, one, 1, 4, 4, 3, 1, one, 4096, NULL) == 1
-    assert lib.mg_angle_scan_fwd(one, one, one, one, one, one, 1, 4, 4, 6, 0, 3, 0, one, 4096,
-                                 NULL) == 1
+    assert lib.mg_angle_scan_fwd(one, one, one, one, one, one, one, 1, 4, 4, 6, 0, 3, 0, one,
+                                 4096, NULL) == 1
+    assert lib.mg_angle_scan_fwd(one, one, one, one, one, one, NULL, 1, 4, 4, 8, 1, 28, 0, one,
+                                 4096, NULL) == 1  # no chunk-product buffer
+    assert lib.mg_angle_scan_bwd(*([one] * 5), NULL, *([one] * 6), 1, 4, 4, 8, 1, 28, 0, one,
+                                 4096, NULL) == 1
     # delta: d_k above 64, nh * chunk above 64, unknown dtype tag
     assert lib.mg_delta_fwd(one, one, one, one, one, one, one, one, 1, 1, 8, 1, 65, 64, 8, 1,
                             one, 1 << 20, NULL) == 1
