@@ -93,6 +93,31 @@ __device__ __forceinline__ floatx4 mma(floatx4 acc, const float* a, int ars, int
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
+// The four tiles of one 16-row block: acc[J] += A (16 x KD) * B_J (KD x 16) with
+// B_J[k][j] = b[J*jstride + k*brs + j*bcs].  The four accumulation chains are
+// interleaved (independent MFMAs back to back instead of one dependent chain)
+// and each A value is read once for all four tiles.
+template <int KD>
+__device__ __forceinline__ void mma_row4(floatx4 (&acc)[4], const float* a, int ars, int acs,
+                                         const float* b, int brs, int bcs, int jstride,
+                                         float sa = 1.f) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < KD / 4; ++s) {
+    const int k = (KD / 4) * g + s;
+    const float av = sa * a[r * ars + k * acs];
+#pragma unroll
+    for (int J = 0; J < 4; ++J)
+      acc[J] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[J * jstride + k * brs + r * bcs],
+                                                    acc[J], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void zero_row4(floatx4 (&acc)[4]) {
+#pragma unroll
+  for (int J = 0; J < 4; ++J) acc[J] = zero4();
+}
+
 // Accumulator layout: lane (g, r) holds rows 4g..4g+3 of column r.
 __device__ __forceinline__ void acc_store_lds(floatx4 acc, float* dst, int ld) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
@@ -248,14 +273,15 @@ __device__ void unit_lower_inverse(const float* sL, float* sT, float* sY) {
 // L = strict_lower(K K^T) * beta_col into sL; wave w builds block-row w.
 __device__ __forceinline__ void build_L(const float* sK, const float* sb, float* sL) {
   const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc[4];
+  zero_row4(acc);
+  mma_row4<64>(acc, sK + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
-    floatx4 acc = zero4();
-    if (J <= w) acc = mma<64>(acc, sK + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * w + 4 * g + i, col = 16 * J + r;
-      sL[row * LD + col] = col < row ? acc[i] * sb[col] : 0.f;
+      sL[row * LD + col] = col < row ? acc[J][i] * sb[col] : 0.f;
     }
   }
 }
@@ -291,23 +317,32 @@ __global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, cons
   tq.store(sL);
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  {
+    floatx4 wa[4], ua[4];
+    zero_row4(wa);
+    zero_row4(ua);
+    mma_row4<64>(wa, sT + 16 * w * LD, LD, 1, sK, LD, 1, 16);
+    mma_row4<64>(ua, sT + 16 * w * LD, LD, 1, sV, LD, 1, 16);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 wa = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
-    acc_store_ws(wa, Wo + mat + 16 * w * DN + 16 * J);
-    floatx4 ua = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sV + 16 * J, LD, 1);
-    acc_store_ws(ua, U0o + mat + 16 * w * DN + 16 * J);
+    for (int J = 0; J < 4; ++J) {
+      acc_store_ws(wa[J], Wo + mat + 16 * w * DN + 16 * J);
+      acc_store_ws(ua[J], U0o + mat + 16 * w * DN + 16 * J);
+    }
   }
   __syncthreads();
+  {
+    floatx4 sp[4];
+    zero_row4(sp);
+    mma_row4<64>(sp, sL + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 s = mma<64>(zero4(), sL + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+    for (int J = 0; J < 4; ++J) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-      s[i] = (m < (t + 1) * g.nh) ? s[i] * sb[m] : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
+        sp[J][i] = (m < (t + 1) * g.nh) ? sp[J][i] * sb[m] : 0.f;
+      }
+      acc_store_ws(sp[J], Po + mat + 16 * w * DN + 16 * J);
     }
-    acc_store_ws(s, Po + mat + 16 * w * DN + 16 * J);
   }
 }
 
@@ -460,35 +495,47 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
   build_L(sK, sb, sL);
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   // R = V - K Hc in place in sV (tile (w, J) read and written by wave w only).
+  {
+    floatx4 acc[4];
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 acc = acc_load_lds(sV + 16 * w * LD + 16 * J, LD);
-    acc = mma<64>(acc, sK + 16 * w * LD, LD, 1, sX + 16 * J, LD, 1, -1.f);
-    acc_store_lds(acc, sV + 16 * w * LD + 16 * J, LD);
+    for (int J = 0; J < 4; ++J) acc[J] = acc_load_lds(sV + 16 * w * LD + 16 * J, LD);
+    mma_row4<64>(acc, sK + 16 * w * LD, LD, 1, sX, LD, 1, 16, -1.f);
+#pragma unroll
+    for (int J = 0; J < 4; ++J) acc_store_lds(acc[J], sV + 16 * w * LD + 16 * J, LD);
   }
   __syncthreads();
   unit_lower_inverse(sL, sT, sY);
   // U = Tm^-1 R; P = (Q K^T) * beta_col * read into sL (free now).
+  {
+    floatx4 u[4], sp[4];
+    zero_row4(u);
+    zero_row4(sp);
+    mma_row4<64>(u, sT + 16 * w * LD, LD, 1, sV, LD, 1, 16);
+    mma_row4<64>(sp, sQ + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 u = mma<64>(zero4(), sT + 16 * w * LD, LD, 1, sV + 16 * J, LD, 1);
-    acc_store_ws(u, Uo + mat + 16 * w * DN + 16 * J);
-    floatx4 s = mma<64>(zero4(), sQ + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+    for (int J = 0; J < 4; ++J) {
+      acc_store_ws(u[J], Uo + mat + 16 * w * DN + 16 * J);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-      s[i] = (m < (t + 1) * g.nh) ? s[i] * sb[m] : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
+        sp[J][i] = (m < (t + 1) * g.nh) ? sp[J][i] * sb[m] : 0.f;
+      }
+      acc_store_lds(sp[J], sL + 16 * w * LD + 16 * J, LD);
     }
-    acc_store_lds(s, sL + 16 * w * LD + 16 * J, LD);
   }
   __syncthreads();
   // D1 = P^T dy into sX (Hc no longer needed); Q^T dy and E = Tm^-T diag(beta) K out.
+  {
+    floatx4 d1[4], qd[4];
+    zero_row4(d1);
+    zero_row4(qd);
+    mma_row4<64>(d1, sL + 16 * w, 1, LD, sD, LD, 1, 16);
+    mma_row4<64>(qd, sQ + 16 * w, 1, LD, sD, LD, 1, 16);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 d1 = mma<64>(zero4(), sL + 16 * w, 1, LD, sD + 16 * J, LD, 1);
-    acc_store_lds(d1, sX + 16 * w * LD + 16 * J, LD);
-    floatx4 qd = mma<64>(zero4(), sQ + 16 * w, 1, LD, sD + 16 * J, LD, 1);
-    acc_store_ws(qd, QdYo + mat + 16 * w * DN + 16 * J);
+    for (int J = 0; J < 4; ++J) {
+      acc_store_lds(d1[J], sX + 16 * w * LD + 16 * J, LD);
+      acc_store_ws(qd[J], QdYo + mat + 16 * w * DN + 16 * J);
+    }
   }
   // sK := diag(beta) K for E, once every wave is done with the unscaled K.
   __syncthreads();
@@ -497,12 +544,17 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
     sK[i * LD + j] *= sb[i];
   }
   __syncthreads();
+  {
+    floatx4 ea[4], g0[4];
+    zero_row4(ea);
+    zero_row4(g0);
+    mma_row4<64>(ea, sT + 16 * w, 1, LD, sK, LD, 1, 16);
+    mma_row4<64>(g0, sT + 16 * w, 1, LD, sX, LD, 1, 16);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 ea = mma<64>(zero4(), sT + 16 * w, 1, LD, sK + 16 * J, LD, 1);
-    acc_store_ws(ea, Eo + mat + 16 * w * DN + 16 * J);
-    floatx4 g0 = mma<64>(zero4(), sT + 16 * w, 1, LD, sX + 16 * J, LD, 1);
-    acc_store_ws(g0, G0o + mat + 16 * w * DN + 16 * J);
+    for (int J = 0; J < 4; ++J) {
+      acc_store_ws(ea[J], Eo + mat + 16 * w * DN + 16 * J);
+      acc_store_ws(g0[J], G0o + mat + 16 * w * DN + 16 * J);
+    }
   }
 }
 
@@ -623,10 +675,14 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
   }
   __syncthreads();
   // S = Q K^T, dP = dy U^T (rows = tokens of block w, cols = micro-rows of block J).
+  floatx4 s4[4], dp4[4];
+  zero_row4(s4);
+  zero_row4(dp4);
+  mma_row4<64>(s4, sQ + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
+  mma_row4<64>(dp4, sD + 16 * w * LD, LD, 1, sU, 1, LD, 16 * LD);
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
-    floatx4 s = mma<64>(zero4(), sQ + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
-    floatx4 dp = mma<64>(zero4(), sD + 16 * w * LD, LD, 1, sU + 16 * J * LD, 1, LD);
+    const floatx4 s = s4[J], dp = dp4[J];
     floatx4 ds, db;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -641,24 +697,33 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
   __syncthreads();
   // dQ = dy Hc^T + dS K; dK (kept in registers) = dS^T Q - G Hc^T.
   floatx4 dk[4];
+  {
+    floatx4 q[4];
+    zero_row4(q);
+    mma_row4<64>(q, sD + 16 * w * LD, LD, 1, sH, 1, LD, 16 * LD);
+    mma_row4<64>(q, sX + 16 * w * LD, LD, 1, sK, LD, 1, 16);
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
-    floatx4 q = mma<64>(zero4(), sD + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD);
-    q = mma<64>(q, sX + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
+    for (int J = 0; J < 4; ++J) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * gg + i, d = 16 * J + r;
-      if (t < ch.Ct && d < g.dk) stf(dQ, (trow0 + t) * g.dk + d, q[i]);
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * gg + i, d = 16 * J + r;
+        if (t < ch.Ct && d < g.dk) stf(dQ, (trow0 + t) * g.dk + d, q[J][i]);
+      }
     }
-    floatx4 a = mma<64>(zero4(), sX + 16 * w, 1, LD, sQ + 16 * J, LD, 1);
-    dk[J] = mma<64>(a, sG + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD, -1.f);
+    zero_row4(dk);
+    mma_row4<64>(dk, sX + 16 * w, 1, LD, sQ, LD, 1, 16);
+    mma_row4<64>(dk, sG + 16 * w * LD, LD, 1, sH, 1, LD, 16 * LD, -1.f);
   }
   __syncthreads();
   // dT = -G U^T, KK = K K^T; dKK = dT * beta_col * strict into sX.  dHn into sH.
+  floatx4 dt4[4], kk4[4];
+  zero_row4(dt4);
+  zero_row4(kk4);
+  mma_row4<64>(dt4, sG + 16 * w * LD, LD, 1, sU, 1, LD, 16 * LD, -1.f);
+  mma_row4<64>(kk4, sK + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
-    floatx4 dt = mma<64>(zero4(), sG + 16 * w * LD, LD, 1, sU + 16 * J * LD, 1, LD, -1.f);
-    floatx4 kk = mma<64>(zero4(), sK + 16 * w * LD, LD, 1, sK + 16 * J * LD, 1, LD);
+    const floatx4 dt = dt4[J], kk = kk4[J];
     floatx4 dkk, db;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -674,12 +739,17 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
   __syncthreads();
   // dK += dKK K + dKK^T K + (beta_row U) dHn^T; dbeta += rowsum(U * (K dHn)).
   float rowp[4] = {0.f, 0.f, 0.f, 0.f};
+  floatx4 bu4[4], x4[4];
+  mma_row4<64>(dk, sX + 16 * w * LD, LD, 1, sK, LD, 1, 16);
+  mma_row4<64>(dk, sX + 16 * w, 1, LD, sK, LD, 1, 16);
+  zero_row4(bu4);
+  zero_row4(x4);
+  mma_row4<64>(bu4, sU + 16 * w * LD, LD, 1, sH, 1, LD, 16 * LD);
+  mma_row4<64>(x4, sK + 16 * w * LD, LD, 1, sH, LD, 1, 16);
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
-    floatx4 a = mma<64>(dk[J], sX + 16 * w * LD, LD, 1, sK + 16 * J, LD, 1);
-    a = mma<64>(a, sX + 16 * w, 1, LD, sK + 16 * J, LD, 1);
-    floatx4 bu = mma<64>(zero4(), sU + 16 * w * LD, LD, 1, sH + 16 * J * LD, 1, LD);
-    floatx4 x = mma<64>(zero4(), sK + 16 * w * LD, LD, 1, sH + 16 * J, LD, 1);
+    floatx4 a = dk[J];
+    const floatx4 bu = bu4[J], x = x4[J];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * w + 4 * gg + i, d = 16 * J + r;
