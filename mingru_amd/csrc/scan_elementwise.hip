@@ -31,6 +31,7 @@ constexpr int EW_WAVES_FWD = 8;
 constexpr int EW_TSUB_FWD = 16;
 constexpr int EW_WAVES_BWD = 8;
 constexpr int EW_TSUB_BWD = 8;
+constexpr int EW_VEC_BWD = 4;  // columns per lane of the aligned backward (4 or 2)
 
 // Affine map y -> p*y + l (NL independent offsets sharing one slope).
 template <int NL>
@@ -64,6 +65,9 @@ __device__ __forceinline__ void load_vec(float (&dst)[VEC], const float* __restr
   if constexpr (VEC == 4) {
     const float4 v = mg_ld_stream4(src);
     dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+  } else if constexpr (VEC == 2) {
+    const float2 v = mg_ld_stream2(src);
+    dst[0] = v.x; dst[1] = v.y;
   } else {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) dst[i] = mg_ld_stream(src + i);
@@ -74,6 +78,8 @@ template <int VEC>
 __device__ __forceinline__ void store_vec(float* __restrict__ dst, const float (&src)[VEC]) {
   if constexpr (VEC == 4) {
     mg_st_stream4(dst, make_float4(src[0], src[1], src[2], src[3]));
+  } else if constexpr (VEC == 2) {
+    mg_st_stream2(dst, make_float2(src[0], src[1]));
   } else {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) mg_st_stream(dst + i, src[i]);
@@ -85,17 +91,18 @@ struct EwGeom {
   int n_tiles, n_lg, n_chunks;
 };
 
-// Look-back slots: [lg][chunk][field][TILE] tagged words, TILE = 64*VEC.
+// Look-back slots: [lg][chunk][field][VEC][64 lanes] tagged words, so each wave
+// store of one (field, vector element) covers 512 contiguous bytes (whole lines).
 template <int NL, int VEC>
 __device__ __forceinline__ void lb_put(mg_slot_t* base, const EwGeom& g, int lg, int c, int lane,
                                        const Aff<NL> (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
-  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
+  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane;
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    mg_slot_put(p + v, x[v].p, epoch);
+    mg_slot_put(p + v * MG_WAVE, x[v].p, epoch);
 #pragma unroll
-    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v, x[v].l[f], epoch);
+    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v * MG_WAVE, x[v].l[f], epoch);
   }
 }
 
@@ -103,13 +110,13 @@ template <int NL, int VEC>
 __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, int lg, int c,
                                        int lane, Aff<NL> (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
-  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane * VEC;
+  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane;
   bool ok = true;
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    ok &= mg_slot_get(p + v, x[v].p, epoch);
+    ok &= mg_slot_get(p + v * MG_WAVE, x[v].p, epoch);
 #pragma unroll
-    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v, x[v].l[f], epoch);
+    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v * MG_WAVE, x[v].l[f], epoch);
   }
   return ok;
 }
@@ -132,17 +139,17 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
 
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    s_agg[w][0][lane * VEC + v] = loc[v].p;
+    s_agg[w][0][v * MG_WAVE + lane] = loc[v].p;
 #pragma unroll
-    for (int f = 0; f < NL; ++f) s_agg[w][f + 1][lane * VEC + v] = loc[v].l[f];
+    for (int f = 0; f < NL; ++f) s_agg[w][f + 1][v * MG_WAVE + lane] = loc[v].l[f];
   }
   __syncthreads();
 
   auto wave_agg = [&](int j, int v) {
     Aff<NL> r;
-    r.p = s_agg[j][0][lane * VEC + v];
+    r.p = s_agg[j][0][v * MG_WAVE + lane];
 #pragma unroll
-    for (int f = 0; f < NL; ++f) r.l[f] = s_agg[j][f + 1][lane * VEC + v];
+    for (int f = 0; f < NL; ++f) r.l[f] = s_agg[j][f + 1][v * MG_WAVE + lane];
     return r;
   };
 
@@ -210,18 +217,18 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
     lb_put<NL, VEC>(incl_data, g, lg, c, lane, I, epoch);
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      s_carry[0][lane * VEC + v] = E[v].p;
+      s_carry[0][v * MG_WAVE + lane] = E[v].p;
 #pragma unroll
-      for (int f = 0; f < NL; ++f) s_carry[f + 1][lane * VEC + v] = E[v].l[f];
+      for (int f = 0; f < NL; ++f) s_carry[f + 1][v * MG_WAVE + lane] = E[v].l[f];
     }
   }
   __syncthreads();
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     Aff<NL> C;
-    C.p = s_carry[0][lane * VEC + v];
+    C.p = s_carry[0][v * MG_WAVE + lane];
 #pragma unroll
-    for (int f = 0; f < NL; ++f) C.l[f] = s_carry[f + 1][lane * VEC + v];
+    for (int f = 0; f < NL; ++f) C.l[f] = s_carry[f + 1][v * MG_WAVE + lane];
     carry[v] = aff_compose(C, ew[v]);
   }
 }
@@ -600,7 +607,7 @@ int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... a
 
 size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
   size_t m = 0;
-  for (int vec : {1, 4}) {
+  for (int vec : {1, 2, 4}) {
     m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_FWD, EW_WAVES_FWD, 1).total);
     m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_BWD, EW_WAVES_BWD, 2).total);
   }
@@ -639,10 +646,10 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
   const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
                   is_aligned16(Bc) && is_aligned16(gA) && is_aligned16(gB) &&
                   is_aligned16(da) && is_aligned16(db);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_BWD, EW_WAVES_BWD, 2);
+  EwPlan p = ew_plan(B, T, D, v4 ? EW_VEC_BWD : 1, EW_TSUB_BWD, EW_WAVES_BWD, 2);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   if (v4)
-    return ew_launch(linear_bwd_kernel<4, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
+    return ew_launch(linear_bwd_kernel<EW_VEC_BWD, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
                      gB, da, db);
   return ew_launch(linear_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
                    gB, da, db);
