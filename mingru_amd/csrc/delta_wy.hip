@@ -201,6 +201,22 @@ struct Tile {
   }
 };
 
+// Chain workgroup -> (head, d_v slice).  Workgroups are dispatched round-robin
+// over the 8 XCDs (blockIdx mod 8), each with its own L2; the slices of one
+// head are placed on one XCD so that their shared per-chunk operands (W, P, K,
+// Q forward; E, K backward) are fetched from HBM once and re-read from that L2.
+// The grid is padded to a multiple of 8 heads; padding workgroups return.
+constexpr int N_XCD = 8;
+__device__ __forceinline__ bool chain_slot(const DwGeom& g, int64_t BH, int64_t& bh, int& col0) {
+  const unsigned i = blockIdx.x, x = i % N_XCD, j = i / N_XCD;
+  bh = (int64_t)(j / g.ns) * N_XCD + x;
+  col0 = (int)(j % g.ns) * SLICE;
+  return bh < BH;
+}
+unsigned chain_grid(int64_t BH, const DwGeom& g) {
+  return (unsigned)((BH + N_XCD - 1) / N_XCD * N_XCD * g.ns);
+}
+
 // Chunk geometry of chunk c: first token, valid tokens, valid micro-rows.
 struct Chunk {
   int64_t t0;
@@ -377,12 +393,13 @@ __global__ __launch_bounds__(NT) void dw_fwd_chain(const TI* __restrict__ Q, con
                                                    const float* __restrict__ U0m,
                                                    const float* __restrict__ Pm, TI* __restrict__ y,
                                                    float* __restrict__ HT, float* __restrict__ Hb,
-                                                   DwGeom g) {
+                                                   DwGeom g, int64_t BH) {
   __shared__ float sK[2][DN * LD], sQ[2][DN * LD];
   __shared__ float sb[2][DN];
   __shared__ float sH[DN * LDS16], sU[DN * LDS16];
-  const int64_t bh = blockIdx.x / g.ns;
-  const int col0 = (blockIdx.x % g.ns) * SLICE;
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int col = col0 + r;
   // H slice rows 16w..16w+15 (d_k), columns col0..col0+15 (d_v), accumulator layout.
@@ -565,11 +582,12 @@ __global__ __launch_bounds__(NT) void dw_bwd_chain(const TI* __restrict__ K,
                                                    const float* __restrict__ G0m,
                                                    const float* __restrict__ QdYm,
                                                    float* __restrict__ Gm, float* __restrict__ dHn,
-                                                   float* __restrict__ dH0, DwGeom g) {
+                                                   float* __restrict__ dH0, DwGeom g, int64_t BH) {
   __shared__ float sK[2][DN * LD];
   __shared__ float sH[DN * LDS16], sG[DN * LDS16];
-  const int64_t bh = blockIdx.x / g.ns;
-  const int col0 = (blockIdx.x % g.ns) * SLICE;
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int col = col0 + r;
   floatx4 h;
@@ -797,7 +815,7 @@ bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk,
   g.dv = dv;
   g.C = chunk;
   const int64_t nc = (T + chunk - 1) / chunk;
-  if (nc > 65535 || BH > 65535 || BH * ((dv + SLICE - 1) / SLICE) > (1ll << 31) - 1) return false;
+  if (nc > 65535 || BH > 65535) return false;
   g.nc = (int)nc;
   g.ns = (dv + SLICE - 1) / SLICE;
   return true;
@@ -817,9 +835,9 @@ int dw_fwd(const void* Q, const void* K, const void* V, const void* beta, const 
   hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3((unsigned)(BH * g.ns)), dim3(NT), 0, stream,
+  hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, H0, Wm, U0m, Pm, (TI*)y, HT, Hb,
-                     g);
+                     g, BH);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
@@ -840,8 +858,8 @@ int dw_bwd(const void* Q, const void* K, const void* V, const void* beta, const 
                      (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, (const TI*)dy, Hb,
                      Um, Em, G0m, QdYm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3((unsigned)(BH * g.ns)), dim3(NT), 0, stream,
-                     (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g);
+  hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
+                     (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dw_bwd_grads<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, (const TI*)dy, Hb, dHn, Um, Gm,
