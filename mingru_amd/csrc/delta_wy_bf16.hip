@@ -1,0 +1,461 @@
+// DeltaMinGRU chunked-WY delta rule on bf16 MFMA (gfx950), for bf16 Q, K, V, beta.
+//
+// Same algorithm, chunk geometry and workspace layout as the fp32-operand
+// kernels of delta_wy.hip (reference src/mingru/triton_scans.py:473-605 and
+// :1859-2322; the formulas are listed at the top of delta_wy.hip); what
+// changes is how the products are evaluated.
+//
+// Every product is C[i][j] = sum_k A[i][k] B[j][k] over k < 64 with both
+// operands held in LDS as 64 x 64 bf16 "row x k" matrices (BMat): the row is
+// the operand's free index and k the contracted one, stored contiguously so an
+// MFMA fragment (8 consecutive k of one row) is a single 16-byte LDS read.
+// Products run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation:
+//   - bf16 inputs (Q, K, V, dy) are exact in bf16: one MFMA per fragment pair;
+//   - fp32 intermediates (states, Tm^-1, U, G, dS, ...) are stored as a pair
+//     hi = bf16(x), lo = bf16(x - hi), and a product takes hi*hi + hi*lo + lo*hi
+//     (or in*hi + in*lo against an exact input), which keeps about 16
+//     significant bits per operand -- fp32-level results for the reference's
+//     fp32 ("ieee") products -- at 2-3 bf16 MFMAs per fp32 one it replaces,
+//     each 16x more work per cycle than v_mfma_f32_16x16x4_f32.
+#include "mg_delta.h"
+
+namespace {
+
+using namespace mgd;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+// ---- bf16 operand matrices in LDS ------------------------------------------------
+// Row r holds 8 chunks of 8 consecutive k; chunk q sits at position
+// q ^ ((r ^ (r >> 3)) & 7) of the row.  Fragment reads (8 consecutive rows, one
+// chunk) and transposed element writes (rows 8 apart, one k) both touch 8
+// distinct 16-byte positions, i.e. all LDS banks once.
+struct BMat {
+  uint4 v[DN * 8];
+};
+
+__device__ __forceinline__ int bpos(int r, int q) { return r * 8 + (q ^ ((r ^ (r >> 3)) & 7)); }
+__device__ __forceinline__ u16* belem(BMat& m, int r, int k) {
+  return reinterpret_cast<u16*>(&m.v[bpos(r, k >> 3)]) + (k & 7);
+}
+__device__ __forceinline__ float bget(const BMat& m, int r, int k) {
+  const u16 h = reinterpret_cast<const u16*>(&m.v[bpos(r, k >> 3)])[k & 7];
+  return __uint_as_float((unsigned)h << 16);
+}
+
+__device__ __forceinline__ u16 bf_bits(float x) { return __builtin_bit_cast(u16, (__bf16)x); }
+__device__ __forceinline__ float bf_val(u16 h) { return __uint_as_float((unsigned)h << 16); }
+// x = hi + lo to about 16 significant bits (both round to nearest even).
+__device__ __forceinline__ void bf_split(float x, u16& hi, u16& lo) {
+  hi = bf_bits(x);
+  lo = bf_bits(x - bf_val(hi));
+}
+
+// Split pair (hi, lo) of an fp32 matrix.
+typedef BMat BPair[2];
+
+__device__ __forceinline__ void put_split(BPair& m, int r, int k, float x) {
+  u16 hi, lo;
+  bf_split(x, hi, lo);
+  *belem(m[0], r, k) = hi;
+  *belem(m[1], r, k) = lo;
+}
+// Four consecutive k (k % 4 == 0): one 8-byte write per half.
+__device__ __forceinline__ void put_split4(BPair& m, int r, int k, float x0, float x1, float x2,
+                                           float x3) {
+  u16 h[4], l[4];
+  bf_split(x0, h[0], l[0]);
+  bf_split(x1, h[1], l[1]);
+  bf_split(x2, h[2], l[2]);
+  bf_split(x3, h[3], l[3]);
+  *reinterpret_cast<uint2*>(belem(m[0], r, k)) =
+      make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+  *reinterpret_cast<uint2*>(belem(m[1], r, k)) =
+      make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
+}
+// Eight consecutive k (one chunk q): one 16-byte write per half.
+__device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (&x)[8]) {
+  unsigned h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    u16 h0, l0, h1, l1;
+    bf_split(x[2 * p], h0, l0);
+    bf_split(x[2 * p + 1], h1, l1);
+    h[p] = h0 | ((unsigned)h1 << 16);
+    l[p] = l0 | ((unsigned)l1 << 16);
+  }
+  m[0].v[bpos(r, q)] = make_uint4(h[0], h[1], h[2], h[3]);
+  m[1].v[bpos(r, q)] = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// Accumulator tile (lane (g, r) holds rows R0+4g..R0+4g+3 of column C0+r) into
+// a split BMat, either as (row = tile row, k = tile column) or transposed
+// (row = tile column, k = tile row; four consecutive k per lane).
+__device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) put_split(m, R0 + 4 * g + i, C0 + r, a[i]);
+}
+__device__ __forceinline__ void acc_put_t(BPair& m, floatx4 a, int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  put_split4(m, C0 + r, R0 + 4 * g, a[0], a[1], a[2], a[3]);
+}
+
+__device__ __forceinline__ bf16x8 bneg(bf16x8 x) {
+  uint4 u = __builtin_bit_cast(uint4, x);
+  u.x ^= 0x80008000u;
+  u.y ^= 0x80008000u;
+  u.z ^= 0x80008000u;
+  u.w ^= 0x80008000u;
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// Workgroups of the bf16 kernels: 8 waves; wave w computes the 16 x 32 output
+// block of row block rb = w % 4 and column tiles 2 ch, 2 ch + 1 (ch = w / 4).
+constexpr int NTB = 512;
+constexpr int WB = NTB / MG_WAVE;
+
+// Byte offsets of this lane's MFMA fragments inside a BMat.  Row 16 blk + r,
+// chunk q = 4 s + g sits at byte blk * 2048 + r * 128 + 16 (q ^ (r & 7) ^ (r >> 3)
+// ^ (2 blk & 7)); the wave's row block and its two column blocks are fixed, so
+// six lane constants address every fragment it reads, and each read is one
+// ds_read_b128 whose immediate offset is the matrix's LDS base.
+struct FragOff {
+  unsigned a[2];     // [s]: row block rb (A operand)
+  unsigned b[2][2];  // [s][jj]: row block 2 ch + jj (B operand)
+  int rb, ch;        // row block, column half
+
+  __device__ static __forceinline__ unsigned at(int blk, unsigned L, int r) {
+    return (unsigned)blk * 2048u + (unsigned)r * 128u + ((L ^ ((2u * blk) & 7u)) << 4);
+  }
+  __device__ __forceinline__ void init() {
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4, w = wave_id();
+    rb = w & 3;
+    ch = w >> 2;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const unsigned L = (unsigned)((4 * s + g) ^ (r & 7) ^ (r >> 3));
+      a[s] = at(rb, L, r);
+      b[s][0] = at(2 * ch, L, r);
+      b[s][1] = at(2 * ch + 1, L, r);
+    }
+  }
+};
+
+__device__ __forceinline__ bf16x8 frag_at(const BMat& m, unsigned off) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                        reinterpret_cast<const char*>(&m) + off));
+}
+
+// acc[jj] (+/-)= A[row block rb] . B[row block 2 ch + jj]^T over k < 64 (the wave's
+// 16 x 32 output block).  SA / SB: the operand is a split pair (the pointer is
+// its hi half, the lo half follows); NEG negates A.
+template <bool SA, bool SB, bool NEG = false>
+__device__ __forceinline__ void bmm(floatx4 (&acc)[2], const FragOff& F, const BMat* A,
+                                    const BMat* B) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    bf16x8 ah = frag_at(A[0], F.a[s]), al;
+    if constexpr (SA) al = frag_at(A[1], F.a[s]);
+    if constexpr (NEG) {
+      ah = bneg(ah);
+      if constexpr (SA) al = bneg(al);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const unsigned off = F.b[s][jj];
+      const bf16x8 bh = frag_at(B[0], off);
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[jj], 0, 0, 0);
+      if constexpr (SB)
+        acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[1], off), acc[jj], 0, 0, 0);
+      if constexpr (SA) acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[jj], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void zero2(floatx4 (&acc)[2]) { acc[0] = acc[1] = zero4(); }
+
+// Column sums of the wave's tile jj (over its 16 rows) into s[col]: each
+// (slot, column) is written by one lane, so reductions stay in a fixed order.
+__device__ __forceinline__ void colsum16(floatx4 v, float* s, int col) {
+  float p = v[0] + v[1] + v[2] + v[3];
+  p += __shfl_xor(p, 16);
+  p += __shfl_xor(p, 32);
+  if (lane_id() < 16) s[col] = p;
+}
+
+// ---- staging of global blocks ------------------------------------------------------
+// bf16 block (rows x cols, row stride ldg) of a row-major input: thread idx holds
+// row idx / 8, columns 8 (idx % 8) + 0..7, zero outside the block.
+struct BTile {
+  uint4 q;
+
+  __device__ __forceinline__ void load(const u16* src, int rows, int cols, int64_t ldg) {
+    const int idx = threadIdx.x, row = idx >> 3, c0 = (idx & 7) * 8;
+    if (cols == DN && ldg == DN && (((uintptr_t)src) & 15u) == 0) {
+      q = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + c0)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      u16 e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x)
+        e[x] = (row < rows && c0 + x < cols) ? src[(int64_t)row * ldg + c0 + x] : (u16)0;
+      q = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                     e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+    }
+  }
+  // (row, k = column)
+  __device__ __forceinline__ void put(BMat& m) const {
+    m.v[bpos(threadIdx.x >> 3, threadIdx.x & 7)] = q;
+  }
+  // transposed: (row = column, k = row)
+  __device__ __forceinline__ void put_t(BMat& m) const {
+    const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 8;
+    const u16* e = reinterpret_cast<const u16*>(&q);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) *belem(m, c0 + x, row) = e[x];
+  }
+};
+
+// fp32 block (rows x cols) of a padded 64 x 64 workspace matrix: thread idx holds
+// rows (idx + 512 v) / 16, columns 4 ((idx + 512 v) % 16) + 0..3, v = 0, 1; zero
+// outside the block.
+struct FTile {
+  float4 f[2];
+
+  __device__ __forceinline__ void load(const float* src, int rows, int cols) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      float4 x = row < rows ? *reinterpret_cast<const float4*>(src + row * DN + c0)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c0 + 0 >= cols) x.x = 0.f;
+      if (c0 + 1 >= cols) x.y = 0.f;
+      if (c0 + 2 >= cols) x.z = 0.f;
+      if (c0 + 3 >= cols) x.w = 0.f;
+      f[v] = x;
+    }
+  }
+  __device__ __forceinline__ void put_split(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB;
+      put_split4(m, idx >> 4, (idx & 15) * 4, f[v].x, f[v].y, f[v].z, f[v].w);
+    }
+  }
+  // bf16 copy of the block into a row-major output with row stride ldg.
+  __device__ __forceinline__ void store_bf16(u16* dst, int rows, int cols, int64_t ldg) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      if (row >= rows) continue;
+      const float e[4] = {f[v].x, f[v].y, f[v].z, f[v].w};
+      if (c0 + 4 <= cols && ldg == DN) {
+        *reinterpret_cast<uint2*>(dst + (int64_t)row * DN + c0) =
+            make_uint2(bf_bits(e[0]) | ((unsigned)bf_bits(e[1]) << 16),
+                       bf_bits(e[2]) | ((unsigned)bf_bits(e[3]) << 16));
+      } else {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          if (c0 + x < cols) dst[(int64_t)row * ldg + c0 + x] = bf_bits(e[x]);
+      }
+    }
+  }
+};
+
+// The wave's 16 x 32 output block (rows R0 + 4 g + i, columns C0 + 16 jj + r) into a
+// bf16 row-major output with row stride ld, keeping rows < nr and columns < nc.
+__device__ __forceinline__ void store_block_bf16(u16* dst, int64_t ld, const floatx4 (&v)[2],
+                                                 int R0, int C0, int nr, int nc) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  u16* p = dst + (int64_t)(R0 + 4 * g) * ld + C0 + r;
+  if (R0 + 16 <= nr && C0 + 32 <= nc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[0] = bf_bits(v[0][i]);
+      p[16] = bf_bits(v[1][i]);
+      p += ld;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool rok = R0 + 4 * g + i < nr;
+      if (rok && C0 + r < nc) p[0] = bf_bits(v[0][i]);
+      if (rok && C0 + 16 + r < nc) p[16] = bf_bits(v[1][i]);
+      p += ld;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, gradient kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   S = Q K^T, dP = dy U^T, dS = dP * beta_col * read         (rows t, cols m)
+//   dQ = dy Hc^T + dS K
+//   dT = -G U^T, dKK = dT * beta_col * strict, D2 = dKK + dKK^T
+//   dK = dS^T Q - G Hc^T + D2 K + beta_row (U dHn^T)
+//   dbeta_m = sum_t dP S read + sum_i dT KK strict + sum_d K[m][d] (U dHn^T)[m][d]
+//   dV = G
+__global__ __launch_bounds__(NTB) void dwb_bwd_grads(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
+    const u16* __restrict__ dy, const float* __restrict__ Hb, const float* __restrict__ dHn,
+    const float* __restrict__ Um, const float* __restrict__ Gm, u16* __restrict__ dQ,
+    u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dbeta, DwGeom g) {
+  __shared__ BMat sK, sKt, sQ, sQt, sDy;  // exact inputs
+  __shared__ BPair sU, sG, sHc;           // sG later holds D2, sHc later dHn
+  __shared__ BPair sS, sSt;               // dS as (t; m) and (m; t)
+  __shared__ float sT[DN * LD];           // dKK (fp32) for the symmetrisation
+  __shared__ float sb[DN];
+  // dbeta partials: [0..3] read-term column sums per row block, [4..7] strict-term
+  // column sums per row block, [8..9] row sums of K * (U dHn^T) per column half.
+  __shared__ float sdb[10][DN];
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  FTile tn;  // dHn, staged once Hc is no longer needed
+  {
+    BTile tk, tq, td;
+    FTile tu, tg, th;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
+    tu.load(Um + mat, ch.M, g.dv);
+    tg.load(Gm + mat, ch.M, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    tn.load(dHn + mat, g.dk, g.dv);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tq.put(sQ);
+    tq.put_t(sQt);
+    td.put(sDy);
+    tu.put_split(sU);
+    tg.put_split(sG);
+    th.put_split(sHc);
+    tg.store_bf16(dV + row0 * g.dv, ch.M, g.dv, g.dv);  // dV = G
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  }
+  __syncthreads();
+  // S and dP: rows t of block rb, columns m of the wave's two tiles.
+  {
+    floatx4 s2[2], dp2[2];
+    zero2(s2);
+    zero2(dp2);
+    bmm<false, false>(s2, F, &sQ, &sK);
+    bmm<false, true>(dp2, F, &sDy, sU);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+      floatx4 ds, db;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = R0 + 4 * gg + i, m = cj + r;
+        const bool rd = m < (t + 1) * g.nh;
+        ds[i] = rd ? dp2[jj][i] * sb[m] : 0.f;
+        db[i] = rd ? dp2[jj][i] * s2[jj][i] : 0.f;
+      }
+      acc_put(sS, ds, R0, cj);
+      acc_put_t(sSt, ds, R0, cj);
+      colsum16(db, sdb[F.rb], cj + r);
+    }
+  }
+  floatx4 dq[2], dk[2];
+  zero2(dq);
+  zero2(dk);
+  bmm<false, true>(dq, F, &sDy, sHc);     // dy Hc^T
+  bmm<true, true, true>(dk, F, sG, sHc);  // -G Hc^T
+  {
+    floatx4 dt2[2], kk2[2];
+    zero2(dt2);
+    zero2(kk2);
+    bmm<true, true, true>(dt2, F, sG, sU);  // dT = -G U^T
+    bmm<false, false>(kk2, F, &sK, &sK);    // K K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+      floatx4 dkk, db;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = R0 + 4 * gg + i, j = cj + r;
+        const bool st = j < m;
+        dkk[i] = st ? dt2[jj][i] * sb[j] : 0.f;
+        db[i] = st ? dt2[jj][i] * kk2[jj][i] : 0.f;
+      }
+      acc_store_lds(dkk, sT + R0 * LD + cj, LD);
+      colsum16(db, sdb[4 + F.rb], cj + r);
+    }
+  }
+  __syncthreads();
+  bmm<true, false>(dq, F, sS, &sKt);   // + dS K
+  bmm<true, false>(dk, F, sSt, &sQt);  // + dS^T Q
+  store_block_bf16(dQ + trow0 * g.dk, g.dk, dq, R0, C0, ch.Ct, g.dk);
+  // D2 = dKK + dKK^T into sG, dHn into sHc (neither is read again before the barrier).
+  {
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int col = 8 * q + e;
+      x[e] = sT[row * LD + col] + sT[col * LD + row];
+    }
+    put_split8(sG, row, q, x);
+  }
+  tn.put_split(sHc);
+  __syncthreads();
+  {
+    floatx4 bu2[2];
+    zero2(bu2);
+    bmm<true, false>(dk, F, sG, &sKt);  // + D2 K
+    bmm<true, true>(bu2, F, sU, sHc);   // U dHn^T
+    float rowp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = R0 + 4 * gg + i;
+      dk[0][i] += sb[m] * bu2[0][i];
+      dk[1][i] += sb[m] * bu2[1][i];
+      rowp[i] = bget(sK, m, C0 + r) * bu2[0][i] + bget(sK, m, C0 + 16 + r) * bu2[1][i];
+      rowp[i] += __shfl_xor(rowp[i], 1);
+      rowp[i] += __shfl_xor(rowp[i], 2);
+      rowp[i] += __shfl_xor(rowp[i], 4);
+      rowp[i] += __shfl_xor(rowp[i], 8);
+    }
+    store_block_bf16(dK + row0 * g.dk, g.dk, dk, R0, C0, ch.M, g.dk);
+    if (r == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sdb[8 + F.ch][R0 + 4 * gg + i] = rowp[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < ch.M) {
+    const int m = threadIdx.x;
+    float acc = sdb[8][m] + sdb[9][m];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc += sdb[q][m];
+    stf(dbeta, row0 + m, acc);
+  }
+}
+
+}  // namespace
+
+namespace mgd {
+
+int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
+                         const float* Hb, const float* dHn, const float* Um, const float* Gm,
+                         void* dQ, void* dK, void* dV, void* dbeta, int64_t BH, const DwGeom& g,
+                         hipStream_t stream) {
+  hipLaunchKernelGGL(dwb_bwd_grads, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
+                     (const u16*)K, (const u16*)beta, (const u16*)dy, Hb, dHn, Um, Gm, (u16*)dQ,
+                     (u16*)dK, (u16*)dV, (u16*)dbeta, g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+}  // namespace mgd

@@ -1,0 +1,322 @@
+// Shared pieces of the DeltaMinGRU chunked-WY kernels (gfx950): chunk geometry,
+// operand staging, fp32 MFMA tile helpers, the blocked unit-lower-triangular
+// inverse and the host-side envelope.  The fp32-operand kernels live in
+// delta_wy.hip, the bf16-operand kernels in delta_wy_bf16.hip.
+#pragma once
+
+#include "mg_common.h"
+
+#include <algorithm>
+
+namespace mgd {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int DN = 64;        // padded extent of every chunk matrix
+constexpr int LD = 65;        // LDS row stride (floats): conflict-free row and column reads
+constexpr int LDS16 = 17;     // LDS row stride of 16-column slices
+constexpr int NT = 256;       // threads per workgroup (4 waves)
+constexpr int SLICE = 16;     // d_v columns per chain workgroup
+constexpr int MAT = DN * DN;  // floats per padded chunk matrix in the workspace
+
+struct DwGeom {
+  int64_t T;   // tokens per head
+  int nh;      // micro-steps per token
+  int dk, dv;  // head dims
+  int C;       // tokens per chunk
+  int nc;      // chunks per head
+  int ns;      // d_v slices per head
+};
+
+// ---- element access: fp32 or bf16 (uint16_t storage, round-to-nearest-even) ----
+__device__ __forceinline__ float ldf(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float ldf(const uint16_t* p, int64_t i) {
+  return __uint_as_float((unsigned)p[i] << 16);
+}
+__device__ __forceinline__ uint16_t f2bf(float v) {
+  unsigned u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ void stf(float* p, int64_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void stf(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// acc += A (16 x KD) * B (KD x 16) with A[i][k] = a[i*ars + k*acs], B[k][j] = b[k*brs + j*bcs].
+// Lane group g = lane/16 supplies k in [g*KD/4, (g+1)*KD/4) over the KD/4 steps; any
+// bijection of k works as long as A and B agree, and this one keeps each lane's
+// k range contiguous.
+template <int KD>
+__device__ __forceinline__ floatx4 mma(floatx4 acc, const float* a, int ars, int acs,
+                                       const float* b, int brs, int bcs, float sa = 1.f) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < KD / 4; ++s) {
+    const int k = (KD / 4) * g + s;
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sa * a[r * ars + k * acs], b[k * brs + r * bcs],
+                                               acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// The four tiles of one 16-row block: acc[J] += A (16 x KD) * B_J (KD x 16) with
+// B_J[k][j] = b[J*jstride + k*brs + j*bcs].  The four accumulation chains are
+// interleaved (independent MFMAs back to back instead of one dependent chain)
+// and each A value is read once for all four tiles.
+template <int KD>
+__device__ __forceinline__ void mma_row4(floatx4 (&acc)[4], const float* a, int ars, int acs,
+                                         const float* b, int brs, int bcs, int jstride,
+                                         float sa = 1.f) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < KD / 4; ++s) {
+    const int k = (KD / 4) * g + s;
+    const float av = sa * a[r * ars + k * acs];
+#pragma unroll
+    for (int J = 0; J < 4; ++J)
+      acc[J] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[J * jstride + k * brs + r * bcs],
+                                                    acc[J], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void zero_row4(floatx4 (&acc)[4]) {
+#pragma unroll
+  for (int J = 0; J < 4; ++J) acc[J] = zero4();
+}
+
+// Accumulator layout: lane (g, r) holds rows 4g..4g+3 of column r.
+__device__ __forceinline__ void acc_store_lds(floatx4 acc, float* dst, int ld) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[(4 * g + i) * ld + r] = acc[i];
+}
+__device__ __forceinline__ floatx4 acc_load_lds(const float* src, int ld) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = src[(4 * g + i) * ld + r];
+  return acc;
+}
+// Padded 64 x 64 workspace matrices (row stride DN).
+__device__ __forceinline__ void acc_store_ws(floatx4 acc, float* dst) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[(4 * g + i) * DN + r] = acc[i];
+}
+__device__ __forceinline__ floatx4 acc_load_ws(const float* src) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = src[(4 * g + i) * DN + r];
+  return acc;
+}
+
+__device__ __forceinline__ float tof(float x) { return x; }
+__device__ __forceinline__ float tof(uint16_t x) { return __uint_as_float((unsigned)x << 16); }
+
+// Register staging of a rows x cols block (row stride ldg) of a row-major global
+// matrix, written later to a 64 x 64 LDS matrix (stride LD) with zeros outside
+// the block.  Each thread holds 16 elements; every load is issued before any LDS
+// store, and full-width, 16-byte aligned blocks move as 16-byte vectors.
+template <typename TI>
+struct Tile {
+  static constexpr int EPV = 16 / sizeof(TI);  // elements per 16-byte vector
+  static constexpr int NV = 16 / EPV;          // vectors per thread
+  static constexpr int VPR = DN / EPV;         // vectors per 64-element row
+  uint4 q[NV];
+  bool vec;
+
+  __device__ __forceinline__ void load(const TI* src, int rows, int cols, int64_t ldg) {
+    vec = cols == DN && ldg == DN && (((uintptr_t)src) & 15u) == 0;
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = threadIdx.x + v * NT;
+        const int row = idx / VPR, col = (idx % VPR) * EPV;
+        q[v] = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + col)
+                          : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+      TI* e = reinterpret_cast<TI*>(q);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        const int row = idx >> 6, col = idx & 63;
+        e[k] = (row < rows && col < cols) ? src[(int64_t)row * ldg + col] : TI(0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* s) const {
+    const TI* e = reinterpret_cast<const TI*>(q);
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = threadIdx.x + v * NT;
+        const int row = idx / VPR, col = (idx % VPR) * EPV;
+#pragma unroll
+        for (int x = 0; x < EPV; ++x) s[row * LD + col + x] = tof(e[v * EPV + x]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        s[(idx >> 6) * LD + (idx & 63)] = tof(e[k]);
+      }
+    }
+  }
+};
+
+// Chain workgroup -> (head, d_v slice).  Workgroups are dispatched round-robin
+// over the 8 XCDs (blockIdx mod 8), each with its own L2; the slices of one
+// head are placed on one XCD so that their shared per-chunk operands (W, P, K,
+// Q forward; E, K backward) are fetched from HBM once and re-read from that L2.
+// The grid is padded to a multiple of 8 heads; padding workgroups return.
+constexpr int N_XCD = 8;
+__device__ __forceinline__ bool chain_slot(const DwGeom& g, int64_t BH, int64_t& bh, int& col0) {
+  const unsigned i = blockIdx.x, x = i % N_XCD, j = i / N_XCD;
+  bh = (int64_t)(j / g.ns) * N_XCD + x;
+  col0 = (int)(j % g.ns) * SLICE;
+  return bh < BH;
+}
+inline unsigned chain_grid(int64_t BH, const DwGeom& g) {
+  return (unsigned)((BH + N_XCD - 1) / N_XCD * N_XCD * g.ns);
+}
+
+// Chunk geometry of chunk c: first token, valid tokens, valid micro-rows.
+struct Chunk {
+  int64_t t0;
+  int Ct, M;
+};
+__device__ __forceinline__ Chunk chunk_of(const DwGeom& g, int c) {
+  Chunk ch;
+  ch.t0 = (int64_t)c * g.C;
+  ch.Ct = (int)min((int64_t)g.C, g.T - ch.t0);
+  ch.M = ch.Ct * g.nh;
+  return ch;
+}
+
+// ---------------------------------------------------------------------------
+// Tm^-1 for Tm = I + L, L strictly lower (64 x 64 in LDS), blocked in 16 x 16:
+// diagonal blocks by forward substitution (one wave each), then
+// T_ab = -T_aa L_ab T_bb for the two 16-blocks below the diagonal of each
+// 32 x 32 half, then the lower-left 32 x 32 block -T_22' L' T_11'.
+// sT receives the full lower-triangular inverse with zeroed upper blocks.
+// ---------------------------------------------------------------------------
+__device__ inline void unit_lower_inverse(const float* sL, float* sT, float* sY) {
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
+  {
+    // Diagonal block w: column r of X = (I + L_ww)^-1; lane group g keeps rows
+    // 4q + g, q = 0..3.  X[i][r] = delta_ir - sum_k L[i][k] X[k][r].
+    const int o = 16 * w;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float p = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p += sL[(o + i) * LD + o + 4 * q + g] * x[q];
+      p += __shfl_xor(p, 16);
+      p += __shfl_xor(p, 32);
+      const float xi = (i == r ? 1.f : 0.f) - p;
+      if ((i & 3) == g) x[i >> 2] = xi;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + o + r] = x[q];
+    // Zero the blocks right of the diagonal in block-row w.
+    for (int jb = w + 1; jb < 4; ++jb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + 16 * jb + r] = 0.f;
+  }
+  __syncthreads();
+  if (w < 2) {
+    // Blocks (1,0) and (3,2).
+    const int a = 2 * w + 1, b = 2 * w;
+    floatx4 y = mma<16>(zero4(), sL + 16 * a * LD + 16 * b, LD, 1, sT + 16 * b * LD + 16 * b, LD, 1);
+    floatx4 t = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      t = __builtin_amdgcn_mfma_f32_16x16x4f32(-sT[(16 * a + r) * LD + 16 * a + 4 * g + s], y[s], t,
+                                               0, 0, 0);
+    acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
+  }
+  __syncthreads();
+  {
+    // Lower-left 32 x 32: Y = L[32:64, 0:32] T[0:32, 0:32], then -T[32:64, 32:64] Y.
+    const int a = 2 + (w >> 1), b = w & 1;
+    floatx4 y = mma<32>(zero4(), sL + 16 * a * LD, LD, 1, sT + 16 * b, LD, 1);
+    acc_store_lds(y, sY + b * 32 * LDS16 + (a - 2) * 16 * LDS16, LDS16);
+    __syncthreads();
+    floatx4 t = mma<32>(zero4(), sT + 16 * a * LD + 32, LD, 1, sY + b * 32 * LDS16, LDS16, 1, -1.f);
+    acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
+  }
+  __syncthreads();
+}
+
+// L = strict_lower(K K^T) * beta_col into sL; wave w builds block-row w.
+__device__ __forceinline__ void build_L(const float* sK, const float* sb, float* sL) {
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
+  floatx4 acc[4];
+  zero_row4(acc);
+  mma_row4<64>(acc, sK + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * w + 4 * g + i, col = 16 * J + r;
+      sL[row * LD + col] = col < row ? acc[J][i] * sb[col] : 0.f;
+    }
+  }
+}
+
+
+// Column sums of a tile (over the 4 rows of each lane and the 4 lane groups)
+// written to s[col]; every (slot, column) is written by exactly one lane, so the
+// final reduction order is fixed and the result bitwise reproducible.
+__device__ __forceinline__ void put_colsum(floatx4 v, float* s, int col) {
+  float p = v[0] + v[1] + v[2] + v[3];
+  p += __shfl_xor(p, 16);
+  p += __shfl_xor(p, 32);
+  if (lane_id() < 16) s[col] = p;
+}
+
+
+inline bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk, DwGeom& g,
+             int64_t& BH) {
+  if (B <= 0 || H <= 0 || T <= 0 || nh <= 0 || chunk <= 0) return false;
+  if (dk <= 0 || dk > DN || dv <= 0 || dv > DN || (int64_t)nh * chunk > DN) return false;
+  BH = B * H;
+  g.T = T;
+  g.nh = nh;
+  g.dk = dk;
+  g.dv = dv;
+  g.C = chunk;
+  const int64_t nc = (T + chunk - 1) / chunk;
+  if (nc > 65535 || BH > 65535) return false;
+  g.nc = (int)nc;
+  g.ns = (dv + SLICE - 1) / SLICE;
+  return true;
+}
+
+inline size_t dw_mat_bytes(int64_t BH, const DwGeom& g) { return (size_t)BH * g.nc * MAT * sizeof(float); }
+
+// bf16-input entry points (delta_wy_bf16.hip).  Q, K, V, beta, y, dy and the
+// input gradients are bf16 (uint16_t storage); states and workspaces are fp32.
+int dw_fwd_bf16(const void* Q, const void* K, const void* V, const void* beta, const float* H0,
+                void* y, float* HT, float* Hb, int64_t BH, const DwGeom& g, void* ws,
+                size_t ws_bytes, hipStream_t stream);
+int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, const float* Hb,
+                const void* dy, const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
+                float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
+                hipStream_t stream);
+
+int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
+                         const float* Hb, const float* dHn, const float* Um, const float* Gm,
+                         void* dQ, void* dK, void* dV, void* dbeta, int64_t BH, const DwGeom& g,
+                         hipStream_t stream);
+
+}  // namespace mgd
