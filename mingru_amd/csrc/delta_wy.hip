@@ -562,10 +562,15 @@ int dw_bwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* QdYm = (float*)((char*)ws + 3 * mb);
   float* Gm = (float*)((char*)ws + 4 * mb);
   float* dHn = (float*)((char*)ws + 5 * mb);
+  if constexpr (sizeof(TI) == 2) {
+    const int rc = dwb_launch_bwd_prep(Q, K, V, beta, dy, Hb, Um, Em, G0m, QdYm, BH, g, stream);
+    if (rc != MG_OK) return rc;
+  } else {
   hipLaunchKernelGGL(dw_bwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, (const TI*)dy, Hb,
                      Um, Em, G0m, QdYm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  }
   hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;

@@ -56,7 +56,7 @@ __device__ __forceinline__ void bf_split(float x, u16& hi, u16& lo) {
 // Split pair (hi, lo) of an fp32 matrix.
 typedef BMat BPair[2];
 
-__device__ __forceinline__ void put_split(BPair& m, int r, int k, float x) {
+__device__ __forceinline__ void put_split1(BPair& m, int r, int k, float x) {
   u16 hi, lo;
   bf_split(x, hi, lo);
   *belem(m[0], r, k) = hi;
@@ -96,7 +96,7 @@ __device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (
 __device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) put_split(m, R0 + 4 * g + i, C0 + r, a[i]);
+  for (int i = 0; i < 4; ++i) put_split1(m, R0 + 4 * g + i, C0 + r, a[i]);
 }
 __device__ __forceinline__ void acc_put_t(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
@@ -245,6 +245,17 @@ struct FTile {
       put_split4(m, idx >> 4, (idx & 15) * 4, f[v].x, f[v].y, f[v].z, f[v].w);
     }
   }
+  // transposed: (row = column, k = row)
+  __device__ __forceinline__ void put_split_t(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      put_split1(m, c0 + 0, row, f[v].x);
+      put_split1(m, c0 + 1, row, f[v].y);
+      put_split1(m, c0 + 2, row, f[v].z);
+      put_split1(m, c0 + 3, row, f[v].w);
+    }
+  }
   // bf16 copy of the block into a row-major output with row stride ldg.
   __device__ __forceinline__ void store_bf16(u16* dst, int rows, int cols, int64_t ldg) const {
 #pragma unroll
@@ -286,6 +297,139 @@ __device__ __forceinline__ void store_block_bf16(u16* dst, int64_t ld, const flo
       if (rok && C0 + 16 + r < nc) p[16] = bf_bits(v[1][i]);
       p += ld;
     }
+  }
+}
+
+// The wave's 16 x 32 output block into a padded 64 x 64 fp32 workspace matrix.
+__device__ __forceinline__ void store_block_f32(float* dst, const floatx4 (&v)[2], int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  float* p = dst + (R0 + 4 * g) * DN + C0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i * DN] = v[0][i];
+    p[i * DN + 16] = v[1][i];
+  }
+}
+
+// Split operands from a 64 x 64 fp32 LDS matrix (row stride LD), one chunk of 8
+// k per thread: (row, k) = src[row][k], and the transposed forms (row, k) =
+// src[k][row] and src[k][row] * scale[k].
+__device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, const float* src,
+                                            const float* scale) {
+  const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = src[row * LD + 8 * q + e];
+  put_split8(m, row, q, x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = src[(8 * q + e) * LD + row];
+  put_split8(mt, row, q, x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= scale[8 * q + e];
+  put_split8(mts, row, q, x);
+}
+
+// ---------------------------------------------------------------------------
+// backward, preparation kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
+//   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
+//   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
+// U, E, G0 and QdY go to the workspace for the reverse chain and the gradients.
+__global__ __launch_bounds__(NTB) void dwb_bwd_prep(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ beta, const u16* __restrict__ dy, const float* __restrict__ Hb,
+    float* __restrict__ Uo, float* __restrict__ Eo, float* __restrict__ G0o,
+    float* __restrict__ QdYo, DwGeom g) {
+  __shared__ BMat sK, sKt;
+  __shared__ BPair sRt, sPt, sD1t;
+  // Inputs Q, Q^T, dy^T, V and Hc^T until the inverse is formed, then the split
+  // operands T, T^T and (T diag(beta))^T.
+  __shared__ BMat sX[6];
+  __shared__ float sL[DN * LD], sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  BMat &sQ = sX[0], &sQt = sX[1], &sDyt = sX[2], &sV = sX[3];
+  BPair& sHct = *reinterpret_cast<BPair*>(&sX[4]);
+  BPair& sTn = *reinterpret_cast<BPair*>(&sX[0]);
+  BPair& sTt = *reinterpret_cast<BPair*>(&sX[2]);
+  BPair& sTbt = *reinterpret_cast<BPair*>(&sX[4]);
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  {
+    BTile tk, tv, tq, td;
+    FTile th;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tv.put(sV);
+    tq.put(sQ);
+    tq.put_t(sQt);
+    td.put_t(sDyt);
+    th.put_split_t(sHct);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  }
+  __syncthreads();
+  {
+    floatx4 kk[2], rr[2], pp[2], qd[2];
+    zero2(kk);
+    zero2(rr);
+    zero2(pp);
+    zero2(qd);
+    bmm<false, false>(kk, F, &sK, &sK);         // K K^T
+    bmm<false, true, true>(rr, F, &sK, sHct);   // -K Hc
+    bmm<false, false>(pp, F, &sQ, &sK);         // Q K^T
+    bmm<false, false>(qd, F, &sQt, &sDyt);      // Q^T dy
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
+        rr[jj][i] += bget(sV, row, col);
+        pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+      }
+      acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
+      acc_put_t(sRt, rr[jj], R0, cj);
+      acc_put_t(sPt, pp[jj], R0, cj);
+    }
+    store_block_f32(QdYo + mat, qd, R0, C0);
+  }
+  __syncthreads();
+  {
+    floatx4 d1[2];
+    zero2(d1);
+    bmm<true, false>(d1, F, sPt, &sDyt);  // P^T dy
+    acc_put_t(sD1t, d1[0], R0, C0);
+    acc_put_t(sD1t, d1[1], R0, C0 + 16);
+  }
+  unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes
+  stage_split(sTn, sTt, sTbt, sT, sb);
+  __syncthreads();
+  {
+    floatx4 u[2], e[2], g0[2];
+    zero2(u);
+    zero2(e);
+    zero2(g0);
+    bmm<true, true>(u, F, sTn, sRt);     // U = T R
+    bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K
+    bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1
+    store_block_f32(Uo + mat, u, R0, C0);
+    store_block_f32(Eo + mat, e, R0, C0);
+    store_block_f32(G0o + mat, g0, R0, C0);
   }
 }
 
@@ -447,6 +591,15 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
 }  // namespace
 
 namespace mgd {
+
+int dwb_launch_bwd_prep(const void* Q, const void* K, const void* V, const void* beta,
+                        const void* dy, const float* Hb, float* Um, float* Em, float* G0m,
+                        float* QdYm, int64_t BH, const DwGeom& g, hipStream_t stream) {
+  hipLaunchKernelGGL(dwb_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
+                     (const u16*)K, (const u16*)V, (const u16*)beta, (const u16*)dy, Hb, Um, Em,
+                     G0m, QdYm, g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
 
 int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
                          const float* Hb, const float* dHn, const float* Um, const float* Gm,

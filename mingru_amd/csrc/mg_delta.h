@@ -209,8 +209,10 @@ __device__ __forceinline__ Chunk chunk_of(const DwGeom& g, int c) {
 // sT receives the full lower-triangular inverse with zeroed upper blocks.
 // ---------------------------------------------------------------------------
 __device__ inline void unit_lower_inverse(const float* sL, float* sT, float* sY) {
+  // Waves 0..3 do the work; further waves of a larger workgroup only join the
+  // barriers.
   const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
-  {
+  if (w < 4) {
     // Diagonal block w: column r of X = (I + L_ww)^-1; lane group g keeps rows
     // 4q + g, q = 0..3.  X[i][r] = delta_ir - sum_k L[i][k] X[k][r].
     const int o = 16 * w;
@@ -245,12 +247,14 @@ __device__ inline void unit_lower_inverse(const float* sL, float* sT, float* sY)
     acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
   }
   __syncthreads();
-  {
-    // Lower-left 32 x 32: Y = L[32:64, 0:32] T[0:32, 0:32], then -T[32:64, 32:64] Y.
-    const int a = 2 + (w >> 1), b = w & 1;
+  // Lower-left 32 x 32: Y = L[32:64, 0:32] T[0:32, 0:32], then -T[32:64, 32:64] Y.
+  const int a = 2 + ((w & 3) >> 1), b = w & 1;
+  if (w < 4) {
     floatx4 y = mma<32>(zero4(), sL + 16 * a * LD, LD, 1, sT + 16 * b, LD, 1);
     acc_store_lds(y, sY + b * 32 * LDS16 + (a - 2) * 16 * LDS16, LDS16);
-    __syncthreads();
+  }
+  __syncthreads();
+  if (w < 4) {
     floatx4 t = mma<32>(zero4(), sT + 16 * a * LD + 32, LD, 1, sY + b * 32 * LDS16, LDS16, 1, -1.f);
     acc_store_lds(t, sT + 16 * a * LD + 16 * b, LD);
   }
@@ -314,6 +318,9 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
                 float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
                 hipStream_t stream);
 
+int dwb_launch_bwd_prep(const void* Q, const void* K, const void* V, const void* beta,
+                        const void* dy, const float* Hb, float* Um, float* Em, float* G0m,
+                        float* QdYm, int64_t BH, const DwGeom& g, hipStream_t stream);
 int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
                          const float* Hb, const float* dHn, const float* Um, const float* Gm,
                          void* dQ, void* dK, void* dV, void* dbeta, int64_t BH, const DwGeom& g,
