@@ -540,9 +540,14 @@ int dw_fwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* Wm = (float*)ws;
   float* U0m = (float*)((char*)ws + mb);
   float* Pm = (float*)((char*)ws + 2 * mb);
-  hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
-                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
-  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  if constexpr (sizeof(TI) == 2) {
+    const int rc = dwb_launch_fwd_prep(Q, K, V, beta, Wm, U0m, Pm, BH, g, stream);
+    if (rc != MG_OK) return rc;
+  } else {
+    hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
+                       (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
+    if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  }
   hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, H0, Wm, U0m, Pm, (TI*)y, HT, Hb,
                      g, BH);

@@ -330,6 +330,86 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 }
 
 // ---------------------------------------------------------------------------
+// forward, preparation kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
+//   W = T K, U0 = T V, P = (Q K^T) * beta_col * read  -> workspace
+__global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
+                                                    const u16* __restrict__ K,
+                                                    const u16* __restrict__ V,
+                                                    const u16* __restrict__ beta,
+                                                    float* __restrict__ Wo, float* __restrict__ U0o,
+                                                    float* __restrict__ Po, DwGeom g) {
+  __shared__ BMat sK, sKt, sVt, sQ;
+  // L (fp32) until the inverse is formed, then T as a split operand.
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];
+  __shared__ float sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  float* sL = reinterpret_cast<float*>(sLraw);
+  BPair& sTn = *reinterpret_cast<BPair*>(sLraw);
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  {
+    BTile tk, tv, tq;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+    tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tv.put_t(sVt);
+    tq.put(sQ);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  }
+  __syncthreads();
+  {
+    floatx4 kk[2], pp[2];
+    zero2(kk);
+    zero2(pp);
+    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
+    bmm<false, false>(pp, F, &sQ, &sK);  // Q K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
+        pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+      }
+      acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
+    }
+    store_block_f32(Po + mat, pp, R0, C0);
+  }
+  __syncthreads();
+  unit_lower_inverse(sL, sT, sY);  // ends with a barrier: sL is free
+  {
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = sT[row * LD + 8 * q + e];
+    put_split8(sTn, row, q, x);
+  }
+  __syncthreads();
+  {
+    floatx4 w2[2], u2[2];
+    zero2(w2);
+    zero2(u2);
+    bmm<true, false>(w2, F, sTn, &sKt);  // W = T K
+    bmm<true, false>(u2, F, sTn, &sVt);  // U0 = T V
+    store_block_f32(Wo + mat, w2, R0, C0);
+    store_block_f32(U0o + mat, u2, R0, C0);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // backward, preparation kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
@@ -591,6 +671,13 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
 }  // namespace
 
 namespace mgd {
+
+int dwb_launch_fwd_prep(const void* Q, const void* K, const void* V, const void* beta, float* Wm,
+                        float* U0m, float* Pm, int64_t BH, const DwGeom& g, hipStream_t stream) {
+  hipLaunchKernelGGL(dwb_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
+                     (const u16*)K, (const u16*)V, (const u16*)beta, Wm, U0m, Pm, g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
 
 int dwb_launch_bwd_prep(const void* Q, const void* K, const void* V, const void* beta,
                         const void* dy, const float* Hb, float* Um, float* Em, float* G0m,
