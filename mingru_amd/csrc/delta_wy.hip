@@ -540,14 +540,9 @@ int dw_fwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* Wm = (float*)ws;
   float* U0m = (float*)((char*)ws + mb);
   float* Pm = (float*)((char*)ws + 2 * mb);
-  if constexpr (sizeof(TI) == 2) {
-    const int rc = dwb_launch_fwd_prep(Q, K, V, beta, Wm, U0m, Pm, BH, g, stream);
-    if (rc != MG_OK) return rc;
-  } else {
-    hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
-                       (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
-    if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  }
+  hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
+                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, H0, Wm, U0m, Pm, (TI*)y, HT, Hb,
                      g, BH);
@@ -567,20 +562,13 @@ int dw_bwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* QdYm = (float*)((char*)ws + 3 * mb);
   float* Gm = (float*)((char*)ws + 4 * mb);
   float* dHn = (float*)((char*)ws + 5 * mb);
-  if constexpr (sizeof(TI) == 2) {
-    const int rc = dwb_launch_bwd_prep(Q, K, V, beta, dy, Hb, Um, Em, G0m, QdYm, BH, g, stream);
-    if (rc != MG_OK) return rc;
-  } else {
   hipLaunchKernelGGL(dw_bwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, (const TI*)dy, Hb,
                      Um, Em, G0m, QdYm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  }
   hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  if constexpr (sizeof(TI) == 2)
-    return dwb_launch_bwd_grads(Q, K, beta, dy, Hb, dHn, Um, Gm, dQ, dK, dV, dbeta, BH, g, stream);
   hipLaunchKernelGGL(dw_bwd_grads<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, (const TI*)dy, Hb, dHn, Um, Gm,
                      (TI*)dQ, (TI*)dK, (TI*)dV, (TI*)dbeta, g);
@@ -619,7 +607,7 @@ int mg_delta_fwd(const void* Q, const void* K, const void* V, const void* beta, 
   if (dtype == 0)
     return dw_fwd<float>(Q, K, V, beta, H0, y, HT, Hbound, BH, g, ws, ws_bytes, stream);
   if (dtype == 1)
-    return dw_fwd<uint16_t>(Q, K, V, beta, H0, y, HT, Hbound, BH, g, ws, ws_bytes, stream);
+    return dw_fwd_bf16(Q, K, V, beta, H0, y, HT, Hbound, BH, g, ws, ws_bytes, stream);
   return MG_ERR_ARG;
 }
 
@@ -639,8 +627,8 @@ int mg_delta_bwd(const void* Q, const void* K, const void* V, const void* beta,
     return dw_bwd<float>(Q, K, V, beta, Hbound, dy, dHT, dQ, dK, dV, dbeta, dH0, BH, g, ws,
                          ws_bytes, stream);
   if (dtype == 1)
-    return dw_bwd<uint16_t>(Q, K, V, beta, Hbound, dy, dHT, dQ, dK, dV, dbeta, dH0, BH, g, ws,
-                            ws_bytes, stream);
+    return dw_bwd_bf16(Q, K, V, beta, Hbound, dy, dHT, dQ, dK, dV, dbeta, dH0, BH, g, ws,
+                       ws_bytes, stream);
   return MG_ERR_ARG;
 }
 

@@ -311,6 +311,26 @@ __device__ __forceinline__ void store_block_f32(float* dst, const floatx4 (&v)[2
   }
 }
 
+// Split workspace matrix: a 64 x 64 row-major bf16 hi half followed by the lo
+// half (the 16 KB of one padded fp32 matrix slot).  Read back by the chains as
+// MFMA A fragments straight from memory.
+constexpr int SPLIT_LO = DN * DN;  // u16 offset of the lo half
+
+__device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2], int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  u16* p = dst + (R0 + 4 * g) * DN + C0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      u16 hi, lo;
+      bf_split(v[jj][i], hi, lo);
+      p[i * DN + 16 * jj] = hi;
+      p[SPLIT_LO + i * DN + 16 * jj] = lo;
+    }
+  }
+}
+
 // Split operands from a 64 x 64 fp32 LDS matrix (row stride LD), one chunk of 8
 // k per thread: (row, k) = src[row][k], and the transposed forms (row, k) =
 // src[k][row] and src[k][row] * scale[k].
@@ -334,6 +354,7 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 // ---------------------------------------------------------------------------
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
 //   W = T K, U0 = T V, P = (Q K^T) * beta_col * read  -> workspace
+// (W and P as split bf16 pairs, U0 in fp32).
 __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
                                                     const u16* __restrict__ K,
                                                     const u16* __restrict__ V,
@@ -386,7 +407,7 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
       }
       acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
     }
-    store_block_f32(Po + mat, pp, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Po + mat), pp, R0, C0);
   }
   __syncthreads();
   unit_lower_inverse(sL, sT, sY);  // ends with a barrier: sL is free
@@ -404,7 +425,7 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
     zero2(u2);
     bmm<true, false>(w2, F, sTn, &sKt);  // W = T K
     bmm<true, false>(u2, F, sTn, &sVt);  // U0 = T V
-    store_block_f32(Wo + mat, w2, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Wo + mat), w2, R0, C0);
     store_block_f32(U0o + mat, u2, R0, C0);
   }
 }
@@ -415,7 +436,8 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
 //   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
 //   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
-// U, E, G0 and QdY go to the workspace for the reverse chain and the gradients.
+// U, E (split bf16 pair), G0 and QdY go to the workspace for the reverse chain
+// and the gradients.
 __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ beta, const u16* __restrict__ dy, const float* __restrict__ Hb,
@@ -508,7 +530,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K
     bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1
     store_block_f32(Uo + mat, u, R0, C0);
-    store_block_f32(Eo + mat, e, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Eo + mat), e, R0, C0);
     store_block_f32(G0o + mat, g0, R0, C0);
   }
 }
@@ -668,30 +690,281 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
   }
 }
 
+// ---------------------------------------------------------------------------
+// serial chains: one workgroup of 4 waves per (head, 16-column d_v slice)
+// ---------------------------------------------------------------------------
+// Wave w keeps the state rows 16 w .. 16 w + 15 of the slice in an MFMA
+// accumulator.  Operands that come from memory (W, P, Q, K^T forward; E, K^T
+// backward) are A fragments loaded straight into registers one chunk ahead;
+// operands produced in the loop (H^T, U^T, (beta U)^T, G^T) pass through LDS as
+// 16-row split BMats.
+
+// LDS fragment offsets of rows 0..15 (lane row r, chunk 4 s + g).
+struct RowFrag {
+  unsigned o[2];
+  __device__ __forceinline__ void init() {
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) o[s] = FragOff::at(0, (unsigned)((4 * s + g) ^ (r & 7) ^ (r >> 3)), r);
+  }
+};
+
+__device__ __forceinline__ bf16x8 as_bf(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// acc += A B^T with A in registers ([s] fragments; lo half when SA) and B a split
+// 16-row BMat pair in LDS.
+template <bool SA>
+__device__ __forceinline__ floatx4 amm(floatx4 acc, const uint4 (&ah)[2], const uint4 (&al)[2],
+                                       const BMat* B, const RowFrag& rf) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 bh = frag_at(B[0], rf.o[s]), bl = frag_at(B[1], rf.o[s]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bl, acc, 0, 0, 0);
+    if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al[s]), bh, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// A fragments of a split workspace matrix: row `row`, chunks g and 4 + g.
+__device__ __forceinline__ void load_split_frag(uint4 (&hi)[2], uint4 (&lo)[2], const u16* m,
+                                                int row) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    hi[s] = *reinterpret_cast<const uint4*>(m + row * DN + 8 * (4 * s + g));
+    lo[s] = *reinterpret_cast<const uint4*>(m + SPLIT_LO + row * DN + 8 * (4 * s + g));
+  }
+}
+
+// A fragments of a row-major bf16 input block (rows x cols, row stride ld):
+// row `row`, chunks g and 4 + g, zero outside the block.
+__device__ __forceinline__ void load_in_frag(uint4 (&a)[2], const u16* src, int64_t ld, int row,
+                                             int rows, int cols) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int c0 = 8 * (4 * s + g);
+    const u16* p = src + (int64_t)row * ld + c0;
+    if (row < rows && c0 + 8 <= cols && ld == DN) {
+      a[s] = *reinterpret_cast<const uint4*>(p);
+    } else {
+      u16 e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) e[x] = (row < rows && c0 + x < cols) ? p[x] : (u16)0;
+      a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                        e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+    }
+  }
+}
+
+// A fragments of K^T (row d = column d of the chunk's K block, M x dk, row stride
+// dk): eight 2-byte loads per fragment, zero outside the block.
+__device__ __forceinline__ void load_kt_frag(uint4 (&a)[2], const u16* K, int dk, int d, int M) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int m0 = 8 * (4 * s + g);
+    u16 e[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) e[x] = (d < dk && m0 + x < M) ? K[(int64_t)(m0 + x) * dk + d] : (u16)0;    a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                      e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+  }
+}
+
+struct FwdOps {
+  uint4 wh[2], wl[2], ph[2], pl[2], q[2], kt[2];
+  floatx4 u0;
+  float bm[4];
+};
+
+//   U = U0 - W H, y = Q H + P U, H += K^T (beta U); H_c saved for the backward.
+__global__ __launch_bounds__(NT) void dwb_fwd_chain(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
+    const float* __restrict__ H0, const float* __restrict__ Wm, const float* __restrict__ U0m,
+    const float* __restrict__ Pm, u16* __restrict__ y, float* __restrict__ HT,
+    float* __restrict__ Hb, DwGeom g, int64_t BH) {
+  __shared__ BPair sHt, sUt, sBUt;
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  RowFrag rf;
+  rf.init();
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  auto fetch = [&](FwdOps& o, int c) {
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+    load_split_frag(o.wh, o.wl, reinterpret_cast<const u16*>(Wm + mat), 16 * w + r);
+    load_split_frag(o.ph, o.pl, reinterpret_cast<const u16*>(Pm + mat), 16 * w + r);
+    load_in_frag(o.q, Q + (bh * g.T + ch.t0) * g.dk, g.dk, 16 * w + r, ch.Ct, g.dk);
+    load_kt_frag(o.kt, K + row0 * g.dk, g.dk, 16 * w + r, ch.M);
+    o.u0 = acc_load_ws(U0m + mat + 16 * w * DN + col0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * w + 4 * gg + i;
+      o.bm[i] = m < ch.M ? ldf(beta, row0 + m) : 0.f;
+    }
+  };
+  // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
+  // ring, the loop unrolled by three so the buffers never move.
+  auto step = [&](const FwdOps& cur, FwdOps& fill, int c) {
+    if (c + 2 < g.nc) fetch(fill, c + 2);
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    acc_put_t(sHt, h, 16 * w, 0);
+    acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
+    __syncthreads();
+    const floatx4 wh = amm<true>(zero4(), cur.wh, cur.wl, sHt, rf);
+    floatx4 u, bu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u[i] = cur.u0[i] - wh[i];
+      bu[i] = cur.bm[i] * u[i];
+    }
+    acc_put_t(sUt, u, 16 * w, 0);
+    acc_put_t(sBUt, bu, 16 * w, 0);
+    floatx4 yy = amm<false>(zero4(), cur.q, cur.q, sHt, rf);
+    __syncthreads();
+    yy = amm<true>(yy, cur.ph, cur.pl, sUt, rf);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i;
+      if (t < ch.Ct && col < g.dv) y[(bh * g.T + ch.t0 + t) * g.dv + col] = bf_bits(yy[i]);
+    }
+    h = amm<false>(h, cur.kt, cur.kt, sBUt, rf);
+  };
+  FwdOps b0, b1, b2;
+  fetch(b0, 0);
+  if (g.nc > 1) fetch(b1, 1);
+  int c = 0;
+  for (; c + 3 <= g.nc; c += 3) {
+    step(b0, b2, c);
+    step(b1, b0, c + 1);
+    step(b2, b1, c + 2);
+  }
+  if (c < g.nc) step(b0, b2, c);
+  if (c + 1 < g.nc) step(b1, b0, c + 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) HT[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
+struct BwdOps {
+  uint4 eh[2], el[2], kt[2];
+  floatx4 g0, qd;
+};
+
+//   G = G0 + E dH (saved), dH <- dH + Q^T dy - K^T G, dH per chunk exit saved.
+__global__ __launch_bounds__(NT) void dwb_bwd_chain(
+    const u16* __restrict__ K, const float* __restrict__ dHT, const float* __restrict__ Em,
+    const float* __restrict__ G0m, const float* __restrict__ QdYm, float* __restrict__ Gm,
+    float* __restrict__ dHn, float* __restrict__ dH0, DwGeom g, int64_t BH) {
+  __shared__ BPair sHt, sGt;
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  RowFrag rf;
+  rf.init();
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  auto fetch = [&](BwdOps& o, int c) {
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    load_split_frag(o.eh, o.el, reinterpret_cast<const u16*>(Em + mat), 16 * w + r);
+    load_kt_frag(o.kt, K + (bh * g.T + ch.t0) * g.nh * g.dk, g.dk, 16 * w + r, ch.M);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) o.kt[s] = __builtin_bit_cast(uint4, bneg(as_bf(o.kt[s])));
+    o.g0 = acc_load_ws(G0m + mat + 16 * w * DN + col0);
+    o.qd = acc_load_ws(QdYm + mat + 16 * w * DN + col0);
+  };
+  // Chunk c - 2 is fetched while chunk c computes (ring of three buffers).
+  auto step = [&](const BwdOps& cur, BwdOps& fill, int c) {
+    if (c >= 2) fetch(fill, c - 2);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    acc_put_t(sHt, h, 16 * w, 0);
+    acc_store_ws(h, dHn + mat + 16 * w * DN + col0);
+    __syncthreads();
+    const floatx4 gacc = amm<true>(cur.g0, cur.eh, cur.el, sHt, rf);  // G = G0 + E dH
+    acc_store_ws(gacc, Gm + mat + 16 * w * DN + col0);
+    acc_put_t(sGt, gacc, 16 * w, 0);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] += cur.qd[i];
+    h = amm<false>(h, cur.kt, cur.kt, sGt, rf);  // - K^T G (negated fragments)
+  };
+  BwdOps b0, b1, b2;
+  fetch(b0, g.nc - 1);
+  if (g.nc > 1) fetch(b1, g.nc - 2);
+  int c = g.nc - 1;
+  for (; c - 2 >= 0; c -= 3) {
+    step(b0, b2, c);
+    step(b1, b0, c - 1);
+    step(b2, b1, c - 2);
+  }
+  if (c >= 0) step(b0, b2, c);
+  if (c - 1 >= 0) step(b1, b0, c - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) dH0[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
 }  // namespace
 
 namespace mgd {
 
-int dwb_launch_fwd_prep(const void* Q, const void* K, const void* V, const void* beta, float* Wm,
-                        float* U0m, float* Pm, int64_t BH, const DwGeom& g, hipStream_t stream) {
+int dw_fwd_bf16(const void* Q, const void* K, const void* V, const void* beta, const float* H0,
+                void* y, float* HT, float* Hb, int64_t BH, const DwGeom& g, void* ws,
+                size_t ws_bytes, hipStream_t stream) {
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 3 * mb) return MG_ERR_WORKSPACE;
+  float* Wm = (float*)ws;  // split pairs in the W and P slots
+  float* U0m = (float*)((char*)ws + mb);
+  float* Pm = (float*)((char*)ws + 2 * mb);
   hipLaunchKernelGGL(dwb_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
                      (const u16*)K, (const u16*)V, (const u16*)beta, Wm, U0m, Pm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dwb_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, (const u16*)Q,
+                     (const u16*)K, (const u16*)beta, H0, Wm, U0m, Pm, (u16*)y, HT, Hb, g, BH);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
-int dwb_launch_bwd_prep(const void* Q, const void* K, const void* V, const void* beta,
-                        const void* dy, const float* Hb, float* Um, float* Em, float* G0m,
-                        float* QdYm, int64_t BH, const DwGeom& g, hipStream_t stream) {
+int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, const float* Hb,
+                const void* dy, const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
+                float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
+                hipStream_t stream) {
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 6 * mb) return MG_ERR_WORKSPACE;
+  float* Um = (float*)ws;
+  float* Em = (float*)((char*)ws + mb);  // split pair
+  float* G0m = (float*)((char*)ws + 2 * mb);
+  float* QdYm = (float*)((char*)ws + 3 * mb);
+  float* Gm = (float*)((char*)ws + 4 * mb);
+  float* dHn = (float*)((char*)ws + 5 * mb);
   hipLaunchKernelGGL(dwb_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
                      (const u16*)K, (const u16*)V, (const u16*)beta, (const u16*)dy, Hb, Um, Em,
                      G0m, QdYm, g);
-  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
-}
-
-int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
-                         const float* Hb, const float* dHn, const float* Um, const float* Gm,
-                         void* dQ, void* dK, void* dV, void* dbeta, int64_t BH, const DwGeom& g,
-                         hipStream_t stream) {
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dwb_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, (const u16*)K,
+                     dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dwb_bwd_grads, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
                      (const u16*)K, (const u16*)beta, (const u16*)dy, Hb, dHn, Um, Gm, (u16*)dQ,
                      (u16*)dK, (u16*)dV, (u16*)dbeta, g);

@@ -318,14 +318,4 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
                 float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
                 hipStream_t stream);
 
-int dwb_launch_fwd_prep(const void* Q, const void* K, const void* V, const void* beta, float* Wm,
-                        float* U0m, float* Pm, int64_t BH, const DwGeom& g, hipStream_t stream);
-int dwb_launch_bwd_prep(const void* Q, const void* K, const void* V, const void* beta,
-                        const void* dy, const float* Hb, float* Um, float* Em, float* G0m,
-                        float* QdYm, int64_t BH, const DwGeom& g, hipStream_t stream);
-int dwb_launch_bwd_grads(const void* Q, const void* K, const void* beta, const void* dy,
-                         const float* Hb, const float* dHn, const float* Um, const float* Gm,
-                         void* dQ, void* dK, void* dV, void* dbeta, int64_t BH, const DwGeom& g,
-                         hipStream_t stream);
-
 }  // namespace mgd
