@@ -349,25 +349,39 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
   put_split8(mts, row, q, x);
 }
 
+// The serial chains carry each chunk as one affine map of the state, built
+// here in parallel over chunks (the products with K^T are done where K^T is
+// already in LDS):
+//   forward   H <- H + A H + B,     A = -K^T diag(beta) W,  B = K^T diag(beta) U0,
+//             y  = Qe H + Pu,       Qe = Q - P W,           Pu = P U0
+//   backward  dH <- dH + A' dH + b', A' = -K^T E,  b' = Q^T dy - K^T G0
+// (U = U0 - W H and G = G0 + E dH substituted into the chunk recurrences).
+// The identity part of each map stays exact: the chains add A H to H in fp32.
+
 // ---------------------------------------------------------------------------
 // forward, preparation kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
-//   W = T K, U0 = T V, P = (Q K^T) * beta_col * read  -> workspace
-// (W and P as split bf16 pairs, U0 in fp32).
+//   W = T K, U0 = T V, P = (Q K^T) * beta_col * read
+//   -> A, Qe (split bf16 pairs), B, Pu (fp32) in the workspace.
 __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
                                                     const u16* __restrict__ K,
                                                     const u16* __restrict__ V,
                                                     const u16* __restrict__ beta,
-                                                    float* __restrict__ Wo, float* __restrict__ U0o,
-                                                    float* __restrict__ Po, DwGeom g) {
+                                                    float* __restrict__ Ao, float* __restrict__ Bo,
+                                                    float* __restrict__ Qeo,
+                                                    float* __restrict__ Puo, DwGeom g) {
   __shared__ BMat sK, sKt, sVt, sQ;
-  // L (fp32) until the inverse is formed, then T as a split operand.
-  __shared__ uint4 sLraw[(DN * LD + 3) / 4];
-  __shared__ float sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ BPair sP;                          // P as (t; m)
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];    // L (fp32), then T split
+  __shared__ uint4 sTraw[(DN * LD + 3) / 4];    // T (fp32), then (beta W)^T split
+  __shared__ float sY[2 * 32 * LDS16];
+  __shared__ BPair sWt, sU0t, sBU0t;            // W^T, U0^T, (beta U0)^T as (col; m)
   __shared__ float sb[DN];
   float* sL = reinterpret_cast<float*>(sLraw);
+  float* sT = reinterpret_cast<float*>(sTraw);
   BPair& sTn = *reinterpret_cast<BPair*>(sLraw);
+  BPair& sBWt = *reinterpret_cast<BPair*>(sTraw);
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -406,8 +420,8 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
         pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
       }
       acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
+      acc_put(sP, pp[jj], R0, cj);
     }
-    store_block_split(reinterpret_cast<u16*>(Po + mat), pp, R0, C0);
   }
   __syncthreads();
   unit_lower_inverse(sL, sT, sY);  // ends with a barrier: sL is free
@@ -418,15 +432,48 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
     for (int e = 0; e < 8; ++e) x[e] = sT[row * LD + 8 * q + e];
     put_split8(sTn, row, q, x);
   }
-  __syncthreads();
+  __syncthreads();  // sT is free
   {
     floatx4 w2[2], u2[2];
     zero2(w2);
     zero2(u2);
-    bmm<true, false>(w2, F, sTn, &sKt);  // W = T K
-    bmm<true, false>(u2, F, sTn, &sVt);  // U0 = T V
-    store_block_split(reinterpret_cast<u16*>(Wo + mat), w2, R0, C0);
-    store_block_f32(U0o + mat, u2, R0, C0);
+    bmm<true, false>(w2, F, sTn, &sKt);  // W = T K      (rows m, cols d)
+    bmm<true, false>(u2, F, sTn, &sVt);  // U0 = T V     (rows m, cols j)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+      floatx4 bw, bu;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float b = sb[R0 + 4 * gg + i];
+        bw[i] = b * w2[jj][i];
+        bu[i] = b * u2[jj][i];
+      }
+      acc_put_t(sWt, w2[jj], R0, cj);
+      acc_put_t(sBWt, bw, R0, cj);
+      acc_put_t(sU0t, u2[jj], R0, cj);
+      acc_put_t(sBU0t, bu, R0, cj);
+    }
+  }
+  __syncthreads();
+  {
+    floatx4 a2[2], b2[2], qe[2], pu[2];
+    zero2(a2);
+    zero2(b2);
+    zero2(qe);
+    zero2(pu);
+    bmm<false, true, true>(a2, F, &sKt, sBWt);  // A = -K^T diag(beta) W
+    bmm<false, true>(b2, F, &sKt, sBU0t);       // B = K^T diag(beta) U0
+    bmm<true, true, true>(qe, F, sP, sWt);      // -P W
+    bmm<true, true>(pu, F, sP, sU0t);           // Pu = P U0
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qe[jj][i] += bget(sQ, R0 + 4 * gg + i, C0 + 16 * jj + r);
+    store_block_split(reinterpret_cast<u16*>(Ao + mat), a2, R0, C0);
+    store_block_f32(Bo + mat, b2, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Qeo + mat), qe, R0, C0);
+    store_block_f32(Puo + mat, pu, R0, C0);
   }
 }
 
@@ -436,25 +483,29 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
 //   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
 //   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
-// U, E (split bf16 pair), G0 and QdY go to the workspace for the reverse chain
-// and the gradients.
+//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32) for the
+//      reverse chain.
 __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ beta, const u16* __restrict__ dy, const float* __restrict__ Hb,
     float* __restrict__ Uo, float* __restrict__ Eo, float* __restrict__ G0o,
-    float* __restrict__ QdYo, DwGeom g) {
+    float* __restrict__ Apo, float* __restrict__ bpo, DwGeom g) {
   __shared__ BMat sK, sKt;
-  __shared__ BPair sRt, sPt, sD1t;
+  __shared__ BPair sRt, sPt, sD1t;  // sPt later holds E^T
   // Inputs Q, Q^T, dy^T, V and Hc^T until the inverse is formed, then the split
   // operands T, T^T and (T diag(beta))^T.
   __shared__ BMat sX[6];
-  __shared__ float sL[DN * LD], sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];  // L (fp32), then G0^T split
+  __shared__ float sT[DN * LD], sY[2 * 32 * LDS16];
   __shared__ float sb[DN];
+  float* sL = reinterpret_cast<float*>(sLraw);
   BMat &sQ = sX[0], &sQt = sX[1], &sDyt = sX[2], &sV = sX[3];
   BPair& sHct = *reinterpret_cast<BPair*>(&sX[4]);
   BPair& sTn = *reinterpret_cast<BPair*>(&sX[0]);
   BPair& sTt = *reinterpret_cast<BPair*>(&sX[2]);
   BPair& sTbt = *reinterpret_cast<BPair*>(&sX[4]);
+  BPair& sEt = sPt;
+  BPair& sG0t = *reinterpret_cast<BPair*>(sLraw);
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -484,12 +535,13 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     if (threadIdx.x < DN) sb[threadIdx.x] = bv;
   }
   __syncthreads();
+  floatx4 qd[2];  // Q^T dy, kept for b'
+  zero2(qd);
   {
-    floatx4 kk[2], rr[2], pp[2], qd[2];
+    floatx4 kk[2], rr[2], pp[2];
     zero2(kk);
     zero2(rr);
     zero2(pp);
-    zero2(qd);
     bmm<false, false>(kk, F, &sK, &sK);         // K K^T
     bmm<false, true, true>(rr, F, &sK, sHct);   // -K Hc
     bmm<false, false>(pp, F, &sQ, &sK);         // Q K^T
@@ -508,7 +560,6 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
       acc_put_t(sRt, rr[jj], R0, cj);
       acc_put_t(sPt, pp[jj], R0, cj);
     }
-    store_block_f32(QdYo + mat, qd, R0, C0);
   }
   __syncthreads();
   {
@@ -518,7 +569,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     acc_put_t(sD1t, d1[0], R0, C0);
     acc_put_t(sD1t, d1[1], R0, C0 + 16);
   }
-  unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes
+  unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes; sL and sPt are free
   stage_split(sTn, sTt, sTbt, sT, sb);
   __syncthreads();
   {
@@ -527,36 +578,52 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     zero2(e);
     zero2(g0);
     bmm<true, true>(u, F, sTn, sRt);     // U = T R
-    bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K
-    bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1
+    bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K   (rows m, cols d)
+    bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1           (rows m, cols j)
     store_block_f32(Uo + mat, u, R0, C0);
     store_block_split(reinterpret_cast<u16*>(Eo + mat), e, R0, C0);
     store_block_f32(G0o + mat, g0, R0, C0);
+    acc_put_t(sEt, e[0], R0, C0);
+    acc_put_t(sEt, e[1], R0, C0 + 16);
+    acc_put_t(sG0t, g0[0], R0, C0);
+    acc_put_t(sG0t, g0[1], R0, C0 + 16);
+  }
+  __syncthreads();
+  {
+    floatx4 a2[2];
+    zero2(a2);
+    bmm<false, true, true>(a2, F, &sKt, sEt);    // A' = -K^T E
+    bmm<false, true, true>(qd, F, &sKt, sG0t);   // b' = Q^T dy - K^T G0
+    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
+    store_block_f32(bpo + mat, qd, R0, C0);
   }
 }
 
 // ---------------------------------------------------------------------------
 // backward, gradient kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
+//   G = G0 + E dHn, dV = G
 //   S = Q K^T, dP = dy U^T, dS = dP * beta_col * read         (rows t, cols m)
 //   dQ = dy Hc^T + dS K
 //   dT = -G U^T, dKK = dT * beta_col * strict, D2 = dKK + dKK^T
 //   dK = dS^T Q - G Hc^T + D2 K + beta_row (U dHn^T)
 //   dbeta_m = sum_t dP S read + sum_i dT KK strict + sum_d K[m][d] (U dHn^T)[m][d]
-//   dV = G
 __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
     const u16* __restrict__ dy, const float* __restrict__ Hb, const float* __restrict__ dHn,
-    const float* __restrict__ Um, const float* __restrict__ Gm, u16* __restrict__ dQ,
-    u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dbeta, DwGeom g) {
+    const float* __restrict__ Um, const float* __restrict__ Em, const float* __restrict__ G0m,
+    u16* __restrict__ dQ, u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dbeta,
+    DwGeom g) {
   __shared__ BMat sK, sKt, sQ, sQt, sDy;  // exact inputs
   __shared__ BPair sU, sG, sHc;           // sG later holds D2, sHc later dHn
-  __shared__ BPair sS, sSt;               // dS as (t; m) and (m; t)
+  __shared__ BPair sS, sSt;               // E and dHn^T first, then dS as (t; m), (m; t)
   __shared__ float sT[DN * LD];           // dKK (fp32) for the symmetrisation
   __shared__ float sb[DN];
   // dbeta partials: [0..3] read-term column sums per row block, [4..7] strict-term
   // column sums per row block, [8..9] row sums of K * (U dHn^T) per column half.
   __shared__ float sdb[10][DN];
+  BPair& sE = sS;
+  BPair& sDHnt = sSt;
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -568,16 +635,23 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
   const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int R0 = 16 * F.rb, C0 = 32 * F.ch;
   FTile tn;  // dHn, staged once Hc is no longer needed
+  floatx4 gacc[2];
   {
     BTile tk, tq, td;
-    FTile tu, tg, th;
+    FTile tu, th;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
     td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
     tu.load(Um + mat, ch.M, g.dv);
-    tg.load(Gm + mat, ch.M, g.dv);
     th.load(Hb + mat, g.dk, g.dv);
     tn.load(dHn + mat, g.dk, g.dv);
+    const u16* es = reinterpret_cast<const u16*>(Em + mat);
+    const int erow = threadIdx.x >> 3, eq = threadIdx.x & 7;
+    const uint4 ehi = *reinterpret_cast<const uint4*>(es + erow * DN + 8 * eq);
+    const uint4 elo = *reinterpret_cast<const uint4*>(es + SPLIT_LO + erow * DN + 8 * eq);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      gacc[jj] = acc_load_ws(G0m + mat + R0 * DN + C0 + 16 * jj);
     const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
     tk.put(sK);
     tk.put_t(sKt);
@@ -585,11 +659,17 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
     tq.put_t(sQt);
     td.put(sDy);
     tu.put_split(sU);
-    tg.put_split(sG);
     th.put_split(sHc);
-    tg.store_bf16(dV + row0 * g.dv, ch.M, g.dv, g.dv);  // dV = G
+    tn.put_split_t(sDHnt);
+    sE[0].v[bpos(erow, eq)] = ehi;
+    sE[1].v[bpos(erow, eq)] = elo;
     if (threadIdx.x < DN) sb[threadIdx.x] = bv;
   }
+  __syncthreads();
+  bmm<true, true>(gacc, F, sE, sDHnt);  // G = G0 + E dHn   (rows m, cols j)
+  store_block_bf16(dV + row0 * g.dv, g.dv, gacc, R0, C0, ch.M, g.dv);
+  acc_put(sG, gacc[0], R0, C0);
+  acc_put(sG, gacc[1], R0, C0 + 16);
   __syncthreads();
   // S and dP: rows t of block rb, columns m of the wave's two tiles.
   {
@@ -694,10 +774,9 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
 // serial chains: one workgroup of 4 waves per (head, 16-column d_v slice)
 // ---------------------------------------------------------------------------
 // Wave w keeps the state rows 16 w .. 16 w + 15 of the slice in an MFMA
-// accumulator.  Operands that come from memory (W, P, Q, K^T forward; E, K^T
-// backward) are A fragments loaded straight into registers one chunk ahead;
-// operands produced in the loop (H^T, U^T, (beta U)^T, G^T) pass through LDS as
-// 16-row split BMats.
+// accumulator.  The chunk maps (A, Qe split; B, Pu fp32) are loaded straight
+// into registers two chunks ahead; the state's transpose H^T passes through
+// LDS (double-buffered, one barrier per chunk).
 
 // LDS fragment offsets of rows 0..15 (lane row r, chunk 4 s + g).
 struct RowFrag {
@@ -711,9 +790,7 @@ struct RowFrag {
 
 __device__ __forceinline__ bf16x8 as_bf(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// acc += A B^T with A in registers ([s] fragments; lo half when SA) and B a split
-// 16-row BMat pair in LDS.
-template <bool SA>
+// acc += A B^T, A split in registers ([s] fragments), B a split 16-row BMat pair.
 __device__ __forceinline__ floatx4 amm(floatx4 acc, const uint4 (&ah)[2], const uint4 (&al)[2],
                                        const BMat* B, const RowFrag& rf) {
 #pragma unroll
@@ -721,7 +798,7 @@ __device__ __forceinline__ floatx4 amm(floatx4 acc, const uint4 (&ah)[2], const 
     const bf16x8 bh = frag_at(B[0], rf.o[s]), bl = frag_at(B[1], rf.o[s]);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bl, acc, 0, 0, 0);
-    if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al[s]), bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al[s]), bh, acc, 0, 0, 0);
   }
   return acc;
 }
@@ -737,54 +814,20 @@ __device__ __forceinline__ void load_split_frag(uint4 (&hi)[2], uint4 (&lo)[2], 
   }
 }
 
-// A fragments of a row-major bf16 input block (rows x cols, row stride ld):
-// row `row`, chunks g and 4 + g, zero outside the block.
-__device__ __forceinline__ void load_in_frag(uint4 (&a)[2], const u16* src, int64_t ld, int row,
-                                             int rows, int cols) {
-  const int g = lane_id() >> 4;
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int c0 = 8 * (4 * s + g);
-    const u16* p = src + (int64_t)row * ld + c0;
-    if (row < rows && c0 + 8 <= cols && ld == DN) {
-      a[s] = *reinterpret_cast<const uint4*>(p);
-    } else {
-      u16 e[8];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) e[x] = (row < rows && c0 + x < cols) ? p[x] : (u16)0;
-      a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
-                        e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
-    }
-  }
-}
-
-// A fragments of K^T (row d = column d of the chunk's K block, M x dk, row stride
-// dk): eight 2-byte loads per fragment, zero outside the block.
-__device__ __forceinline__ void load_kt_frag(uint4 (&a)[2], const u16* K, int dk, int d, int M) {
-  const int g = lane_id() >> 4;
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int m0 = 8 * (4 * s + g);
-    u16 e[8];
-#pragma unroll
-    for (int x = 0; x < 8; ++x) e[x] = (d < dk && m0 + x < M) ? K[(int64_t)(m0 + x) * dk + d] : (u16)0;    a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
-                      e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
-  }
-}
-
 struct FwdOps {
-  uint4 wh[2], wl[2], ph[2], pl[2], q[2], kt[2];
-  floatx4 u0;
-  float bm[4];
+  uint4 ah[2], al[2], qh[2], ql[2];
+  floatx4 b, pu;
 };
 
-//   U = U0 - W H, y = Q H + P U, H += K^T (beta U); H_c saved for the backward.
-__global__ __launch_bounds__(NT) void dwb_fwd_chain(
-    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
-    const float* __restrict__ H0, const float* __restrict__ Wm, const float* __restrict__ U0m,
-    const float* __restrict__ Pm, u16* __restrict__ y, float* __restrict__ HT,
-    float* __restrict__ Hb, DwGeom g, int64_t BH) {
-  __shared__ BPair sHt, sUt, sBUt;
+//   H_c saved, y = Qe H_c + Pu, H_{c+1} = H_c + A H_c + B.
+__global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0,
+                                                    const float* __restrict__ Am,
+                                                    const float* __restrict__ Bm,
+                                                    const float* __restrict__ Qem,
+                                                    const float* __restrict__ Pum,
+                                                    u16* __restrict__ y, float* __restrict__ HT,
+                                                    float* __restrict__ Hb, DwGeom g, int64_t BH) {
+  __shared__ BPair sHt[2];
   int64_t bh;
   int col0;
   if (!chain_slot(g, BH, bh, col0)) return;
@@ -799,19 +842,11 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(
     h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
   }
   auto fetch = [&](FwdOps& o, int c) {
-    const Chunk ch = chunk_of(g, c);
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
-    load_split_frag(o.wh, o.wl, reinterpret_cast<const u16*>(Wm + mat), 16 * w + r);
-    load_split_frag(o.ph, o.pl, reinterpret_cast<const u16*>(Pm + mat), 16 * w + r);
-    load_in_frag(o.q, Q + (bh * g.T + ch.t0) * g.dk, g.dk, 16 * w + r, ch.Ct, g.dk);
-    load_kt_frag(o.kt, K + row0 * g.dk, g.dk, 16 * w + r, ch.M);
-    o.u0 = acc_load_ws(U0m + mat + 16 * w * DN + col0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 16 * w + 4 * gg + i;
-      o.bm[i] = m < ch.M ? ldf(beta, row0 + m) : 0.f;
-    }
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Am + mat), 16 * w + r);
+    load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), 16 * w + r);
+    o.b = acc_load_ws(Bm + mat + 16 * w * DN + col0);
+    o.pu = acc_load_ws(Pum + mat + 16 * w * DN + col0);
   };
   // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
   // ring, the loop unrolled by three so the buffers never move.
@@ -819,27 +854,20 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(
     if (c + 2 < g.nc) fetch(fill, c + 2);
     const Chunk ch = chunk_of(g, c);
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    acc_put_t(sHt, h, 16 * w, 0);
+    BPair& ht = sHt[c & 1];
+    acc_put_t(ht, h, 16 * w, 0);
     acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
     __syncthreads();
-    const floatx4 wh = amm<true>(zero4(), cur.wh, cur.wl, sHt, rf);
-    floatx4 u, bu;
+    floatx4 hn;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      u[i] = cur.u0[i] - wh[i];
-      bu[i] = cur.bm[i] * u[i];
-    }
-    acc_put_t(sUt, u, 16 * w, 0);
-    acc_put_t(sBUt, bu, 16 * w, 0);
-    floatx4 yy = amm<false>(zero4(), cur.q, cur.q, sHt, rf);
-    __syncthreads();
-    yy = amm<true>(yy, cur.ph, cur.pl, sUt, rf);
+    for (int i = 0; i < 4; ++i) hn[i] = h[i] + cur.b[i];
+    h = amm(hn, cur.ah, cur.al, ht, rf);
+    const floatx4 yy = amm(cur.pu, cur.qh, cur.ql, ht, rf);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * w + 4 * gg + i;
       if (t < ch.Ct && col < g.dv) y[(bh * g.T + ch.t0 + t) * g.dv + col] = bf_bits(yy[i]);
     }
-    h = amm<false>(h, cur.kt, cur.kt, sBUt, rf);
   };
   FwdOps b0, b1, b2;
   fetch(b0, 0);
@@ -860,16 +888,18 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(
 }
 
 struct BwdOps {
-  uint4 eh[2], el[2], kt[2];
-  floatx4 g0, qd;
+  uint4 ah[2], al[2];
+  floatx4 b;
 };
 
-//   G = G0 + E dH (saved), dH <- dH + Q^T dy - K^T G, dH per chunk exit saved.
-__global__ __launch_bounds__(NT) void dwb_bwd_chain(
-    const u16* __restrict__ K, const float* __restrict__ dHT, const float* __restrict__ Em,
-    const float* __restrict__ G0m, const float* __restrict__ QdYm, float* __restrict__ Gm,
-    float* __restrict__ dHn, float* __restrict__ dH0, DwGeom g, int64_t BH) {
-  __shared__ BPair sHt, sGt;
+//   dH (chunk exit) saved, dH <- dH + A' dH + b'.
+__global__ __launch_bounds__(NT) void dwb_bwd_chain(const float* __restrict__ dHT,
+                                                    const float* __restrict__ Apm,
+                                                    const float* __restrict__ bpm,
+                                                    float* __restrict__ dHn,
+                                                    float* __restrict__ dH0, DwGeom g,
+                                                    int64_t BH) {
+  __shared__ BPair sHt[2];
   int64_t bh;
   int col0;
   if (!chain_slot(g, BH, bh, col0)) return;
@@ -884,29 +914,22 @@ __global__ __launch_bounds__(NT) void dwb_bwd_chain(
     h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
   }
   auto fetch = [&](BwdOps& o, int c) {
-    const Chunk ch = chunk_of(g, c);
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    load_split_frag(o.eh, o.el, reinterpret_cast<const u16*>(Em + mat), 16 * w + r);
-    load_kt_frag(o.kt, K + (bh * g.T + ch.t0) * g.nh * g.dk, g.dk, 16 * w + r, ch.M);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) o.kt[s] = __builtin_bit_cast(uint4, bneg(as_bf(o.kt[s])));
-    o.g0 = acc_load_ws(G0m + mat + 16 * w * DN + col0);
-    o.qd = acc_load_ws(QdYm + mat + 16 * w * DN + col0);
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), 16 * w + r);
+    o.b = acc_load_ws(bpm + mat + 16 * w * DN + col0);
   };
   // Chunk c - 2 is fetched while chunk c computes (ring of three buffers).
   auto step = [&](const BwdOps& cur, BwdOps& fill, int c) {
     if (c >= 2) fetch(fill, c - 2);
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    acc_put_t(sHt, h, 16 * w, 0);
+    BPair& ht = sHt[c & 1];
+    acc_put_t(ht, h, 16 * w, 0);
     acc_store_ws(h, dHn + mat + 16 * w * DN + col0);
     __syncthreads();
-    const floatx4 gacc = amm<true>(cur.g0, cur.eh, cur.el, sHt, rf);  // G = G0 + E dH
-    acc_store_ws(gacc, Gm + mat + 16 * w * DN + col0);
-    acc_put_t(sGt, gacc, 16 * w, 0);
-    __syncthreads();
+    floatx4 hn;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] += cur.qd[i];
-    h = amm<false>(h, cur.kt, cur.kt, sGt, rf);  // - K^T G (negated fragments)
+    for (int i = 0; i < 4; ++i) hn[i] = h[i] + cur.b[i];
+    h = amm(hn, cur.ah, cur.al, ht, rf);
   };
   BwdOps b0, b1, b2;
   fetch(b0, g.nc - 1);
@@ -934,15 +957,16 @@ int dw_fwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
                 void* y, float* HT, float* Hb, int64_t BH, const DwGeom& g, void* ws,
                 size_t ws_bytes, hipStream_t stream) {
   const size_t mb = dw_mat_bytes(BH, g);
-  if (ws_bytes < 3 * mb) return MG_ERR_WORKSPACE;
-  float* Wm = (float*)ws;  // split pairs in the W and P slots
-  float* U0m = (float*)((char*)ws + mb);
-  float* Pm = (float*)((char*)ws + 2 * mb);
+  if (ws_bytes < 4 * mb) return MG_ERR_WORKSPACE;
+  float* Am = (float*)ws;  // split pair
+  float* Bm = (float*)((char*)ws + mb);
+  float* Qem = (float*)((char*)ws + 2 * mb);  // split pair
+  float* Pum = (float*)((char*)ws + 3 * mb);
   hipLaunchKernelGGL(dwb_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
-                     (const u16*)K, (const u16*)V, (const u16*)beta, Wm, U0m, Pm, g);
+                     (const u16*)K, (const u16*)V, (const u16*)beta, Am, Bm, Qem, Pum, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dwb_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, (const u16*)Q,
-                     (const u16*)K, (const u16*)beta, H0, Wm, U0m, Pm, (u16*)y, HT, Hb, g, BH);
+  hipLaunchKernelGGL(dwb_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, H0, Am, Bm, Qem,
+                     Pum, (u16*)y, HT, Hb, g, BH);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
@@ -955,19 +979,19 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
   float* Um = (float*)ws;
   float* Em = (float*)((char*)ws + mb);  // split pair
   float* G0m = (float*)((char*)ws + 2 * mb);
-  float* QdYm = (float*)((char*)ws + 3 * mb);
-  float* Gm = (float*)((char*)ws + 4 * mb);
+  float* Apm = (float*)((char*)ws + 3 * mb);  // split pair
+  float* bpm = (float*)((char*)ws + 4 * mb);
   float* dHn = (float*)((char*)ws + 5 * mb);
   hipLaunchKernelGGL(dwb_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
                      (const u16*)K, (const u16*)V, (const u16*)beta, (const u16*)dy, Hb, Um, Em,
-                     G0m, QdYm, g);
+                     G0m, Apm, bpm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dwb_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, (const u16*)K,
-                     dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);
+  hipLaunchKernelGGL(dwb_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, dHT, Apm, bpm,
+                     dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dwb_bwd_grads, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream, (const u16*)Q,
-                     (const u16*)K, (const u16*)beta, (const u16*)dy, Hb, dHn, Um, Gm, (u16*)dQ,
-                     (u16*)dK, (u16*)dV, (u16*)dbeta, g);
+                     (const u16*)K, (const u16*)beta, (const u16*)dy, Hb, dHn, Um, Em, G0m,
+                     (u16*)dQ, (u16*)dK, (u16*)dV, (u16*)dbeta, g);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
