@@ -361,9 +361,12 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 // ---------------------------------------------------------------------------
 // forward, preparation kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
-//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
-//   W = T K, U0 = T V, P = (Q K^T) * beta_col * read
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked),
+//   P = (Q K^T) * beta_col * read, M1 = (beta K)^T T, M2 = P T;
+//   A = -M1 K, B = M1 V, Qe = Q - M2 K, Pu = M2 V
 //   -> A, Qe (split bf16 pairs), B, Pu (fp32) in the workspace.
+// (W = T K and U0 = T V never materialise: A = -K^T diag(beta) W = -M1 K, etc.)
+// LDS stays under 80 KB, so two workgroups share a CU.
 __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
                                                     const u16* __restrict__ K,
                                                     const u16* __restrict__ V,
@@ -371,31 +374,43 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
                                                     float* __restrict__ Ao, float* __restrict__ Bo,
                                                     float* __restrict__ Qeo,
                                                     float* __restrict__ Puo, DwGeom g) {
-  __shared__ BMat sK, sKt, sVt, sQ;
-  __shared__ BPair sP;                          // P as (t; m)
-  __shared__ uint4 sLraw[(DN * LD + 3) / 4];    // L (fp32), then T split
-  __shared__ uint4 sTraw[(DN * LD + 3) / 4];    // T (fp32), then (beta W)^T split
+  __shared__ BMat sKt, sVt;                    // K^T, V^T as (col; m)
+  __shared__ BMat sX[2];                       // K, Q; then P split; then M2 split
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];   // L (fp32); then T^T split
+  __shared__ uint4 sTraw[(DN * LD + 3) / 4];   // T (fp32); then (beta K)^T split; then M1 split
   __shared__ float sY[2 * 32 * LDS16];
-  __shared__ BPair sWt, sU0t, sBU0t;            // W^T, U0^T, (beta U0)^T as (col; m)
   __shared__ float sb[DN];
   float* sL = reinterpret_cast<float*>(sLraw);
   float* sT = reinterpret_cast<float*>(sTraw);
-  BPair& sTn = *reinterpret_cast<BPair*>(sLraw);
-  BPair& sBWt = *reinterpret_cast<BPair*>(sTraw);
+  BMat &sK = sX[0], &sQ = sX[1];
+  BPair& sP = sX;
+  BPair& sM2 = sX;
+  BPair& sTt = *reinterpret_cast<BPair*>(sLraw);
+  BPair& sBKt = *reinterpret_cast<BPair*>(sTraw);
+  BPair& sM1 = *reinterpret_cast<BPair*>(sTraw);
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
   const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
   const size_t mat = ((size_t)bh * g.nc + c) * MAT;
   FragOff F;
   F.init();
   const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  float qv[2][4];  // Q at the wave's output positions of Qe
   {
     BTile tk, tv, tq;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
-    tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = R0 + 4 * gg + i, d = C0 + 16 * jj + r;
+        qv[jj][i] = (t < ch.Ct && d < g.dk) ? ldf(Q, (trow0 + t) * g.dk + d) : 0.f;
+      }
     const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
     tk.put(sK);
     tk.put_t(sKt);
@@ -404,8 +419,9 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
     if (threadIdx.x < DN) sb[threadIdx.x] = bv;
   }
   __syncthreads();
+  floatx4 pp[2];
   {
-    floatx4 kk[2], pp[2];
+    floatx4 kk[2];
     zero2(kk);
     zero2(pp);
     bmm<false, false>(kk, F, &sK, &sK);  // K K^T
@@ -420,56 +436,56 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
         pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
       }
       acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
-      acc_put(sP, pp[jj], R0, cj);
     }
   }
-  __syncthreads();
+  __syncthreads();  // K and Q are free
+  acc_put(sP, pp[0], R0, C0);  // P as (t; m): the B operand of M2^T
+  acc_put(sP, pp[1], R0, C0 + 16);
   unit_lower_inverse(sL, sT, sY);  // ends with a barrier: sL is free
   {
     const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
     float x[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = sT[row * LD + 8 * q + e];
-    put_split8(sTn, row, q, x);
+    for (int e = 0; e < 8; ++e) x[e] = sT[(8 * q + e) * LD + row];
+    put_split8(sTt, row, q, x);  // (m; m') = T[m'][m]
   }
   __syncthreads();  // sT is free
   {
-    floatx4 w2[2], u2[2];
-    zero2(w2);
-    zero2(u2);
-    bmm<true, false>(w2, F, sTn, &sKt);  // W = T K      (rows m, cols d)
-    bmm<true, false>(u2, F, sTn, &sVt);  // U0 = T V     (rows m, cols j)
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    const uint4 kq = sKt.v[bpos(row, q)];
+    const u16* e = reinterpret_cast<const u16*>(&kq);
+    float x[8];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int cj = C0 + 16 * jj;
-      floatx4 bw, bu;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float b = sb[R0 + 4 * gg + i];
-        bw[i] = b * w2[jj][i];
-        bu[i] = b * u2[jj][i];
-      }
-      acc_put_t(sWt, w2[jj], R0, cj);
-      acc_put_t(sBWt, bw, R0, cj);
-      acc_put_t(sU0t, u2[jj], R0, cj);
-      acc_put_t(sBU0t, bu, R0, cj);
-    }
+    for (int k = 0; k < 8; ++k) x[k] = sb[8 * q + k] * bf_val(e[k]);
+    put_split8(sBKt, row, q, x);  // (d; m) = beta_m K[m][d]
+  }
+  __syncthreads();
+  {
+    floatx4 m1[2], m2[2];
+    zero2(m1);
+    zero2(m2);
+    bmm<true, true>(m1, F, sTt, sBKt);  // M1^T = T^T diag(beta) K   (rows m, cols d)
+    bmm<true, true>(m2, F, sTt, sP);    // M2^T = (P T)^T           (rows m, cols t)
+    __syncthreads();  // sBKt and sP are free
+    acc_put_t(sM1, m1[0], R0, C0);  // M1 as (d; m)
+    acc_put_t(sM1, m1[1], R0, C0 + 16);
+    acc_put_t(sM2, m2[0], R0, C0);  // M2 as (t; m)
+    acc_put_t(sM2, m2[1], R0, C0 + 16);
   }
   __syncthreads();
   {
     floatx4 a2[2], b2[2], qe[2], pu[2];
     zero2(a2);
     zero2(b2);
-    zero2(qe);
     zero2(pu);
-    bmm<false, true, true>(a2, F, &sKt, sBWt);  // A = -K^T diag(beta) W
-    bmm<false, true>(b2, F, &sKt, sBU0t);       // B = K^T diag(beta) U0
-    bmm<true, true, true>(qe, F, sP, sWt);      // -P W
-    bmm<true, true>(pu, F, sP, sU0t);           // Pu = P U0
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qe[jj][i] += bget(sQ, R0 + 4 * gg + i, C0 + 16 * jj + r);
+      for (int i = 0; i < 4; ++i) qe[jj][i] = qv[jj][i];
+    bmm<true, false, true>(a2, F, sM1, &sKt);  // A = -M1 K
+    bmm<true, false>(b2, F, sM1, &sVt);        // B = M1 V
+    bmm<true, false, true>(qe, F, sM2, &sKt);  // Qe = Q - M2 K
+    bmm<true, false>(pu, F, sM2, &sVt);        // Pu = M2 V
     store_block_split(reinterpret_cast<u16*>(Ao + mat), a2, R0, C0);
     store_block_f32(Bo + mat, b2, R0, C0);
     store_block_split(reinterpret_cast<u16*>(Qeo + mat), qe, R0, C0);
