@@ -30,9 +30,10 @@
 //              dH += Q^T dy - K^T G; stores G and the chunk-exit state grads
 //   bwd_grads  grid (chunk, head): dQ, dK, dV, dbeta from Hc, dHn, U, G.
 // The serial passes are split over d_v because both recurrences act on the
-// columns of H independently.  Products run on v_mfma_f32_16x16x4_f32 with
-// fp32 operands: the state, Tm^-1, U and every accumulation stay fp32 while
-// Q, K, V, beta (and y, dy and the input gradients) may be bf16 in HBM.
+// columns of H independently.  These kernels serve fp32 inputs: products run
+// on v_mfma_f32_16x16x4_f32 with fp32 operands (gfx950 has no reduced-precision
+// fp32 MFMA).  bf16 inputs go to the bf16-MFMA kernels of delta_wy_bf16.hip;
+// the entry points below pick the path from the dtype tag.
 #include "mg_delta.h"
 
 namespace {
