@@ -615,31 +615,69 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   }
 }
 
+// A fragments of a row-major bf16 input block (rows x cols, row stride ld):
+// row `row`, chunks g and 4 + g, zero outside the block.
+__device__ __forceinline__ void load_in_frag(uint4 (&a)[2], const u16* src, int64_t ld, int row,
+                                             int rows, int cols) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int c0 = 8 * (4 * s + g);
+    const u16* p = src + (int64_t)row * ld + c0;
+    if (row < rows && c0 + 8 <= cols && ld == DN) {
+      a[s] = *reinterpret_cast<const uint4*>(p);
+    } else {
+      u16 e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) e[x] = (row < rows && c0 + x < cols) ? p[x] : (u16)0;
+      a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                        e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+    }
+  }
+}
+
+// acc[jj] += A . B[row block 2 ch + jj]^T with A an exact bf16 operand whose two
+// fragments (the wave's rows, chunks g and 4 + g) are held in registers.
+template <bool SB>
+__device__ __forceinline__ void rmm(floatx4 (&acc)[2], const FragOff& F, const uint4 (&a)[2],
+                                    const BMat* B) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 ah = __builtin_bit_cast(bf16x8, a[s]);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[0], F.b[s][jj]), acc[jj], 0, 0, 0);
+      if constexpr (SB)
+        acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[1], F.b[s][jj]), acc[jj], 0, 0, 0);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // backward, gradient kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
 //   G = G0 + E dHn, dV = G
 //   S = Q K^T, dP = dy U^T, dS = dP * beta_col * read         (rows t, cols m)
 //   dQ = dy Hc^T + dS K
-//   dT = -G U^T, dKK = dT * beta_col * strict, D2 = dKK + dKK^T
+//   dT = -G U^T, D2 = dT * beta_col * strict + (dT * beta_col * strict)^T
 //   dK = dS^T Q - G Hc^T + D2 K + beta_row (U dHn^T)
 //   dbeta_m = sum_t dP S read + sum_i dT KK strict + sum_d K[m][d] (U dHn^T)[m][d]
-__global__ __launch_bounds__(NTB) void dwb_bwd_grads(
+// Q and dy enter the products as A fragments straight from memory; the split
+// operands rotate through three 16 KB regions, so LDS stays under 80 KB (two
+// workgroups per CU).  D2 is symmetrised in registers from dT and dT^T = -U G^T.
+__global__ __launch_bounds__(NTB, 4) void dwb_bwd_grads(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
     const u16* __restrict__ dy, const float* __restrict__ Hb, const float* __restrict__ dHn,
     const float* __restrict__ Um, const float* __restrict__ Em, const float* __restrict__ G0m,
     u16* __restrict__ dQ, u16* __restrict__ dK, u16* __restrict__ dV, u16* __restrict__ dbeta,
     DwGeom g) {
-  __shared__ BMat sK, sKt, sQ, sQt, sDy;  // exact inputs
-  __shared__ BPair sU, sG, sHc;           // sG later holds D2, sHc later dHn
-  __shared__ BPair sS, sSt;               // E and dHn^T first, then dS as (t; m), (m; t)
-  __shared__ float sT[DN * LD];           // dKK (fp32) for the symmetrisation
+  __shared__ BMat sK, sKt, sQt;  // exact inputs
+  // Split regions: [E, dHn^T] -> [G, U, Hc] -> [dS, U, dS^T] -> [D2, U, dHn].
+  __shared__ BPair sR[3];
   __shared__ float sb[DN];
   // dbeta partials: [0..3] read-term column sums per row block, [4..7] strict-term
   // column sums per row block, [8..9] row sums of K * (U dHn^T) per column half.
   __shared__ float sdb[10][DN];
-  BPair& sE = sS;
-  BPair& sDHnt = sSt;
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -650,114 +688,114 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_grads(
   F.init();
   const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int R0 = 16 * F.rb, C0 = 32 * F.ch;
-  FTile tn;  // dHn, staged once Hc is no longer needed
   floatx4 gacc[2];
   {
-    BTile tk, tq, td;
-    FTile tu, th;
+    BTile tk, tq;
+    FTile tn;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
-    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
-    tu.load(Um + mat, ch.M, g.dv);
-    th.load(Hb + mat, g.dk, g.dv);
     tn.load(dHn + mat, g.dk, g.dv);
     const u16* es = reinterpret_cast<const u16*>(Em + mat);
     const int erow = threadIdx.x >> 3, eq = threadIdx.x & 7;
     const uint4 ehi = *reinterpret_cast<const uint4*>(es + erow * DN + 8 * eq);
     const uint4 elo = *reinterpret_cast<const uint4*>(es + SPLIT_LO + erow * DN + 8 * eq);
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-      gacc[jj] = acc_load_ws(G0m + mat + R0 * DN + C0 + 16 * jj);
+    for (int jj = 0; jj < 2; ++jj) gacc[jj] = acc_load_ws(G0m + mat + R0 * DN + C0 + 16 * jj);
     const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
     tk.put(sK);
     tk.put_t(sKt);
-    tq.put(sQ);
     tq.put_t(sQt);
-    td.put(sDy);
-    tu.put_split(sU);
-    th.put_split(sHc);
-    tn.put_split_t(sDHnt);
-    sE[0].v[bpos(erow, eq)] = ehi;
-    sE[1].v[bpos(erow, eq)] = elo;
+    sR[0][0].v[bpos(erow, eq)] = ehi;
+    sR[0][1].v[bpos(erow, eq)] = elo;
+    tn.put_split_t(sR[1]);
     if (threadIdx.x < DN) sb[threadIdx.x] = bv;
   }
   __syncthreads();
-  bmm<true, true>(gacc, F, sE, sDHnt);  // G = G0 + E dHn   (rows m, cols j)
-  store_block_bf16(dV + row0 * g.dv, g.dv, gacc, R0, C0, ch.M, g.dv);
-  acc_put(sG, gacc[0], R0, C0);
-  acc_put(sG, gacc[1], R0, C0 + 16);
+  {
+    // U and Hc are fetched while G forms, and staged once E and dHn^T are free.
+    FTile tu, th;
+    tu.load(Um + mat, ch.M, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    bmm<true, true>(gacc, F, sR[0], sR[1]);  // G = G0 + E dHn   (rows m, cols j)
+    store_block_bf16(dV + row0 * g.dv, g.dv, gacc, R0, C0, ch.M, g.dv);
+    __syncthreads();
+    acc_put(sR[0], gacc[0], R0, C0);  // G as (m; j)
+    acc_put(sR[0], gacc[1], R0, C0 + 16);
+    tu.put_split(sR[1]);              // U as (m; j)
+    th.put_split(sR[2]);              // Hc as (d; j)
+  }
+  uint4 qf[2], yf[2];  // Q and dy fragments of the wave's rows t
+  load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
+  load_in_frag(yf, dy + trow0 * g.dv, g.dv, R0 + r, ch.Ct, g.dv);
   __syncthreads();
-  // S and dP: rows t of block rb, columns m of the wave's two tiles.
+  BPair &sG = sR[0], &sU = sR[1], &sHc = sR[2];
+  floatx4 ds2[2], d2[2], dq[2], dk[2];
   {
     floatx4 s2[2], dp2[2];
     zero2(s2);
     zero2(dp2);
-    bmm<false, false>(s2, F, &sQ, &sK);
-    bmm<false, true>(dp2, F, &sDy, sU);
+    rmm<false>(s2, F, qf, &sK);  // S = Q K^T
+    rmm<true>(dp2, F, yf, sU);   // dP = dy U^T
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
-      floatx4 ds, db;
+      floatx4 db;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = R0 + 4 * gg + i, m = cj + r;
         const bool rd = m < (t + 1) * g.nh;
-        ds[i] = rd ? dp2[jj][i] * sb[m] : 0.f;
+        ds2[jj][i] = rd ? dp2[jj][i] * sb[m] : 0.f;
         db[i] = rd ? dp2[jj][i] * s2[jj][i] : 0.f;
       }
-      acc_put(sS, ds, R0, cj);
-      acc_put_t(sSt, ds, R0, cj);
       colsum16(db, sdb[F.rb], cj + r);
     }
   }
-  floatx4 dq[2], dk[2];
-  zero2(dq);
-  zero2(dk);
-  bmm<false, true>(dq, F, &sDy, sHc);     // dy Hc^T
-  bmm<true, true, true>(dk, F, sG, sHc);  // -G Hc^T
   {
-    floatx4 dt2[2], kk2[2];
+    floatx4 dt2[2], dtt2[2], kk2[2];
     zero2(dt2);
+    zero2(dtt2);
     zero2(kk2);
-    bmm<true, true, true>(dt2, F, sG, sU);  // dT = -G U^T
-    bmm<false, false>(kk2, F, &sK, &sK);    // K K^T
+    bmm<true, true, true>(dt2, F, sG, sU);   // dT = -G U^T
+    bmm<true, true, true>(dtt2, F, sU, sG);  // dT^T = -U G^T
+    bmm<false, false>(kk2, F, &sK, &sK);     // K K^T
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
-      floatx4 dkk, db;
+      floatx4 db;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = R0 + 4 * gg + i, j = cj + r;
-        const bool st = j < m;
-        dkk[i] = st ? dt2[jj][i] * sb[j] : 0.f;
-        db[i] = st ? dt2[jj][i] * kk2[jj][i] : 0.f;
+        d2[jj][i] = j < m ? dt2[jj][i] * sb[j] : (m < j ? dtt2[jj][i] * sb[m] : 0.f);
+        db[i] = j < m ? dt2[jj][i] * kk2[jj][i] : 0.f;
       }
-      acc_store_lds(dkk, sT + R0 * LD + cj, LD);
       colsum16(db, sdb[4 + F.rb], cj + r);
     }
   }
+  zero2(dq);
+  zero2(dk);
+  rmm<true>(dq, F, yf, sHc);              // dy Hc^T
+  bmm<true, true, true>(dk, F, sG, sHc);  // -G Hc^T
+  __syncthreads();  // G and Hc are free
+  acc_put(sR[0], ds2[0], R0, C0);  // dS as (t; m)
+  acc_put(sR[0], ds2[1], R0, C0 + 16);
+  acc_put_t(sR[2], ds2[0], R0, C0);  // dS^T as (m; t)
+  acc_put_t(sR[2], ds2[1], R0, C0 + 16);
   __syncthreads();
-  bmm<true, false>(dq, F, sS, &sKt);   // + dS K
-  bmm<true, false>(dk, F, sSt, &sQt);  // + dS^T Q
+  FTile tn;  // dHn again (an L2 hit), fetched while the dS products run
+  tn.load(dHn + mat, g.dk, g.dv);
+  bmm<true, false>(dq, F, sR[0], &sKt);  // + dS K
+  bmm<true, false>(dk, F, sR[2], &sQt);  // + dS^T Q
   store_block_bf16(dQ + trow0 * g.dk, g.dk, dq, R0, C0, ch.Ct, g.dk);
-  // D2 = dKK + dKK^T into sG, dHn into sHc (neither is read again before the barrier).
-  {
-    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int col = 8 * q + e;
-      x[e] = sT[row * LD + col] + sT[col * LD + row];
-    }
-    put_split8(sG, row, q, x);
-  }
-  tn.put_split(sHc);
+  __syncthreads();  // dS and dS^T are free
+  acc_put_t(sR[0], d2[0], R0, C0);  // D2 (symmetric)
+  acc_put_t(sR[0], d2[1], R0, C0 + 16);
+  tn.put_split(sR[2]);  // dHn as (d; j)
   __syncthreads();
   {
     floatx4 bu2[2];
     zero2(bu2);
-    bmm<true, false>(dk, F, sG, &sKt);  // + D2 K
-    bmm<true, true>(bu2, F, sU, sHc);   // U dHn^T
+    bmm<true, false>(dk, F, sR[0], &sKt);  // + D2 K
+    bmm<true, true>(bu2, F, sU, sR[2]);    // U dHn^T
     float rowp[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

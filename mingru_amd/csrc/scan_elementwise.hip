@@ -28,9 +28,10 @@ namespace {
 
 // Chunk = WAVES * TSUB time steps per workgroup.
 constexpr int EW_WAVES_FWD = 8;
-constexpr int EW_TSUB_FWD = 16;
+constexpr int EW_TSUB_FWD = 8;
 constexpr int EW_WAVES_BWD = 8;
 constexpr int EW_TSUB_BWD = 8;
+constexpr int EW_VEC_FWD = 4;  // columns per lane of the aligned forward (4 or 2)
 constexpr int EW_VEC_BWD = 4;  // columns per lane of the aligned backward (4 or 2)
 
 // Affine map y -> p*y + l (NL independent offsets sharing one slope).
@@ -631,10 +632,11 @@ int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int6
   if (!a || !b || !A || !Bc || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
   const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
                   is_aligned16(Bc);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
+  EwPlan p = ew_plan(B, T, D, v4 ? EW_VEC_FWD : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   if (v4)
-    return ew_launch(ew_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a, b, A, Bc);
+    return ew_launch(ew_fwd_kernel<EW_VEC_FWD, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a,
+                     b, A, Bc);
   return ew_launch(ew_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a, b, A, Bc);
 }
 
