@@ -134,8 +134,14 @@ class kernel_timer:
 
     active = None
 
-    def __init__(self):
+    def __init__(self, prealloc: int = 512):
         self.records = []
+        # Events are created here, outside any timed loop: creating one costs
+        # several microseconds of host time, recording one far less.
+        self._pool = [torch.cuda.Event(enable_timing=True) for _ in range(prealloc)]
+
+    def _event(self):
+        return self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
 
     def __enter__(self):
         kernel_timer.active = self
@@ -157,8 +163,8 @@ def _call(fn_name: str, *args) -> None:
 
     timer = kernel_timer.active
     if timer is not None:
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
+        start = timer._event()
+        stop = timer._event()
         start.record()
         rc = getattr(_lib(), fn_name)(*args)
         stop.record()
