@@ -857,6 +857,23 @@ __device__ __forceinline__ floatx4 amm(floatx4 acc, const uint4 (&ah)[2], const 
   return acc;
 }
 
+// Two independent products against the same B (the chain's state update and
+// readout): each B fragment is read once and the two MFMA chains interleave.
+__device__ __forceinline__ void amm2(floatx4& acc0, const uint4 (&ah0)[2], const uint4 (&al0)[2],
+                                     floatx4& acc1, const uint4 (&ah1)[2], const uint4 (&al1)[2],
+                                     const BMat* B, const RowFrag& rf) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 bh = frag_at(B[0], rf.o[s]), bl = frag_at(B[1], rf.o[s]);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah0[s]), bh, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah1[s]), bh, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah0[s]), bl, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah1[s]), bl, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al0[s]), bh, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al1[s]), bh, acc1, 0, 0, 0);
+  }
+}
+
 // A fragments of a split workspace matrix: row `row`, chunks g and 4 + g.
 __device__ __forceinline__ void load_split_frag(uint4 (&hi)[2], uint4 (&lo)[2], const u16* m,
                                                 int row) {
@@ -912,11 +929,10 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
     acc_put_t(ht, h, 16 * w, 0);
     acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
     __syncthreads();
-    floatx4 hn;
+    floatx4 yy = cur.pu;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hn[i] = h[i] + cur.b[i];
-    h = amm(hn, cur.ah, cur.al, ht, rf);
-    const floatx4 yy = amm(cur.pu, cur.qh, cur.ql, ht, rf);
+    for (int i = 0; i < 4; ++i) h[i] += cur.b[i];
+    amm2(h, cur.ah, cur.al, yy, cur.qh, cur.ql, ht, rf);  // H + A H + B, y = Qe H + Pu
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * w + 4 * gg + i;

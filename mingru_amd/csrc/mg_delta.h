@@ -203,34 +203,43 @@ __device__ __forceinline__ Chunk chunk_of(const DwGeom& g, int c) {
 
 // ---------------------------------------------------------------------------
 // Tm^-1 for Tm = I + L, L strictly lower (64 x 64 in LDS), blocked in 16 x 16:
-// diagonal blocks by forward substitution (one wave each), then
+// diagonal blocks by forward substitution (one wave, a lane group per block), then
 // T_ab = -T_aa L_ab T_bb for the two 16-blocks below the diagonal of each
 // 32 x 32 half, then the lower-left 32 x 32 block -T_22' L' T_11'.
 // sT receives the full lower-triangular inverse with zeroed upper blocks.
 // ---------------------------------------------------------------------------
 __device__ inline void unit_lower_inverse(const float* sL, float* sT, float* sY) {
   // Waves 0..3 do the work; further waves of a larger workgroup only join the
-  // barriers.
+  // barriers.  (An earlier form gave each wave one diagonal block and reduced the
+  // substitution sums across lane groups with shuffles: 16 dependent LDS round
+  // trips per block, about half the cost of the whole inverse.)
   const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
-  if (w < 4) {
-    // Diagonal block w: column r of X = (I + L_ww)^-1; lane group g keeps rows
-    // 4q + g, q = 0..3.  X[i][r] = delta_ir - sum_k L[i][k] X[k][r].
-    const int o = 16 * w;
-    float x[4] = {0.f, 0.f, 0.f, 0.f};
+  if (w == 0) {
+    // The four diagonal blocks at once: lane group g inverts block g, lane r
+    // solves its column r of X = (I + L_gg)^-1 by forward substitution,
+    // X[i][r] = delta_ir - sum_{k<i} L[i][k] X[k][r], with no cross-lane
+    // traffic (the L reads are broadcast within the lane group).  Two partial
+    // sums shorten the dependency chain of each step.
+    const int o = 16 * g;
+    const float* Lb = sL + o * LD + o;
+    float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float p = 0.f;
+      float a0 = (i == r) ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p += sL[(o + i) * LD + o + 4 * q + g] * x[q];
-      p += __shfl_xor(p, 16);
-      p += __shfl_xor(p, 32);
-      const float xi = (i == r ? 1.f : 0.f) - p;
-      if ((i & 3) == g) x[i >> 2] = xi;
+      for (int k = 0; k + 1 < i; k += 2) {
+        a0 = fmaf(-Lb[i * LD + k], x[k], a0);
+        a1 = fmaf(-Lb[i * LD + k + 1], x[k + 1], a1);
+      }
+      if (i & 1) a0 = fmaf(-Lb[i * LD + i - 1], x[i - 1], a0);
+      x[i] = a0 + a1;
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + o + r] = x[q];
-    // Zero the blocks right of the diagonal in block-row w.
-    for (int jb = w + 1; jb < 4; ++jb)
+    for (int i = 0; i < 16; ++i) sT[(o + i) * LD + o + r] = x[i];
+  } else if (w < 4) {
+    // Zero the blocks right of the diagonal in block-row w - 1 (rows 0..2 have some).
+    const int o = 16 * (w - 1);
+    for (int jb = w; jb < 4; ++jb)
 #pragma unroll
       for (int q = 0; q < 4; ++q) sT[(o + 4 * q + g) * LD + 16 * jb + r] = 0.f;
   }
