@@ -3,7 +3,8 @@
 Bars: fp32 inputs -- forward max abs err <= 1e-4, gradients <= 1e-3 against
 the float64 oracle (``oracle.scans.delta_chunked`` / ``delta_chunked_bwd``);
 bf16 inputs -- max abs err <= 2e-2 of the largest reference magnitude, with the
-oracle fed the same bf16-rounded values.  The full-size C5 workload is checked
+oracle fed the same bf16-rounded values, for the bf16 outputs (y, dQ, dK, dV,
+dbeta), and <= 1e-4 for the fp32 ones (H_T, dH0).  The full-size C5 workload is checked
 on two heads at full length (heads are independent).
 """
 
@@ -19,6 +20,7 @@ from oracle import scans as orc
 FWD_TOL = 1e-4
 GRAD_TOL = 1e-3
 BF16_REL = 2e-2
+SPLIT_REL = 1e-4  # fp32 outputs of the bf16-input path
 
 pytestmark = pytest.mark.gpu
 
@@ -87,7 +89,12 @@ def _rel(x, ref):
     return float(np.max(np.abs(_np(x) - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-@pytest.mark.parametrize("case", [(2, 2, 200, 1, 64, 64, 64), (1, 2, 70, 2, 32, 32, 32)])
+# The bf16 inputs run their own kernels (bf16 MFMA, split operands): every
+# fp32 case again (ragged d_k / d_v, nh > 1, partial chunks, T = 1), plus two.
+BF16_CASES = CASES + [(2, 2, 200, 1, 64, 64, 64), (1, 2, 70, 2, 32, 32, 32)]
+
+
+@pytest.mark.parametrize("case", BF16_CASES)
 def test_delta_bf16_matches_oracle(cuda, case):
     B, H, T, nh, dk, dv, C = case
     print(f"[gpu] delta bf16 case={case}", flush=True)
@@ -96,11 +103,14 @@ def test_delta_bf16_matches_oracle(cuda, case):
     assert y.dtype == torch.bfloat16 and grads[0].dtype == torch.bfloat16
     ry, rHT, _ = orc.delta_chunked(_np(Q), _np(K), _np(V), _np(beta), _np(H0), C)
     assert _rel(y, ry) <= BF16_REL
-    assert _rel(HT, rHT) <= BF16_REL
+    # H_T and dH0 stay fp32: with split (hi/lo) bf16 operands every product keeps
+    # about 16 significant bits, so they match the fp64 oracle to fp32 level.
+    assert _rel(HT, rHT) <= SPLIT_REL, f"H_T rel err {_rel(HT, rHT):.3e}"
     rg = orc.delta_chunked_bwd(_np(Q), _np(K), _np(V), _np(beta), _np(H0), C, _np(dy),
                                _np(dHT))
     for name, gk, rk in zip(("dQ", "dK", "dV", "dbeta", "dH0"), grads, rg):
-        assert _rel(gk, rk) <= BF16_REL, f"{name} rel err {_rel(gk, rk):.3e}"
+        bar = SPLIT_REL if name == "dH0" else BF16_REL
+        assert _rel(gk, rk) <= bar, f"{name} rel err {_rel(gk, rk):.3e}"
 
 
 def test_delta_c5_full_size(cuda):
