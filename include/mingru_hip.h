@@ -48,6 +48,23 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
                        const float* gA, const float* gB, float* da, float* db, int64_t B,
                        int64_t T, int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
 
+/* ---- fused SignedMinGRU gates + linear_scan, (B, T, D) -----------------------
+ * No reference kernel fuses these: replaces the mixer's coefficient code and
+ * its scan call (SignedMinGRU._coeffs / forward, src/mingru/min_gru.py:1788-1857):
+ * a = tanh(s) (times 1 - sigmoid(z) when `coupled`), b = sigmoid(z) * hpre,
+ * h = A * h0 + Bc with (A, Bc) = linear_scan(a, b).  One pass reads the three
+ * pre-activations and writes h; h0 / dh0 are (B, D).  Workspace as for
+ * linear_scan (its own size query). */
+size_t mg_signed_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
+int mg_signed_gate_scan_fwd(const float* s, const float* z, const float* hpre, const float* h0,
+                            float* h, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                            size_t ws_bytes, mg_stream_t stream);
+/* h = forward output, gh = dL/dh -> ds, dz, dhpre (B,T,D) and dh0 (B,D). */
+int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, const float* h0,
+                            const float* h, const float* gh, float* ds, float* dz, float* dhpre,
+                            float* dh0, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                            size_t ws_bytes, mg_stream_t stream);
+
 /* ---- parallel_scan_log: log-space inputs, (B, T, D) and (B, T+1, D) ---------
  * Replaces parallel_scan_log_fwd (src/mingru/triton_scans.py:1336-1357, kernel
  * :754-821) and its eager-recompute backward (:1489-1552) behind

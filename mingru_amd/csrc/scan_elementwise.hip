@@ -31,6 +31,10 @@ constexpr int EW_WAVES_FWD = 8;
 constexpr int EW_TSUB_FWD = 8;
 constexpr int EW_WAVES_BWD = 8;
 constexpr int EW_TSUB_BWD = 8;
+// Fused gate backward: four arrays per step stay live (sigmoid, tanh, hpre,
+// adjoint), so each wave holds 4 steps (32-step chunks) to stay clear of spills.
+constexpr int GATE_WAVES_BWD = 8;
+constexpr int GATE_TSUB_BWD = 4;
 constexpr int EW_VEC_FWD = 4;  // columns per lane of the aligned forward (4 or 2)
 constexpr int EW_VEC_BWD = 4;  // columns per lane of the aligned backward (4 or 2)
 
@@ -558,6 +562,188 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fused SignedMinGRU gates + scan (reference mixer src/mingru/min_gru.py:
+// 1807-1856: a = tanh(s) [* (1 - sigmoid(z)) when coupled], b = sigmoid(z) * hpre,
+// (A, Bc) = linear_scan(a, b), h = A * h0 + Bc).  The coefficients are formed in
+// registers from the three pre-activations and the scan is seeded with h0, so
+// one pass reads s, z, hpre and writes only h; the backward returns the
+// pre-activation gradients directly.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float mg_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+template <bool COUPLED>
+__device__ __forceinline__ void gate_coeffs(float s, float z, float hpre, float& a, float& b) {
+  const float sg = mg_sigmoid(z), th = tanhf(s);
+  a = COUPLED ? (1.f - sg) * th : th;
+  b = sg * hpre;
+}
+
+template <int VEC, int TSUB, int WAVES, bool COUPLED>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
+    const float* __restrict__ sp, const float* __restrict__ zp, const float* __restrict__ hp,
+    const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
+    mg_slot_t* agg_data, mg_slot_t* incl_data) {
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  if (!th.valid) return;
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  float av[TSUB][VEC], bv[TSUB][VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      float xs[VEC], xz[VEC], xh[VEC];
+      load_vec<VEC>(xs, sp + off);
+      load_vec<VEC>(xz, zp + off);
+      load_vec<VEC>(xh, hp + off);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) gate_coeffs<COUPLED>(xs[v], xz[v], xh[v], av[s][v], bv[s][v]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = 1.f;
+        bv[s][v] = 0.f;
+      }
+    }
+  }
+  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    loc[v] = aff_identity<1>();
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
+      loc[v].p *= av[s][v];
+    }
+    seed[v] = aff_identity<1>();
+  }
+  if (th.c == 0 && th.w == 0 && th.col_ok) {
+    float x[VEC];
+    load_vec<VEC>(x, h0 + th.bb * D + th.col);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) seed[v].l[0] = x[v];
+  }
+  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
+                                 carry);
+  float L[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) L[v] = carry[v].l[0];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) L[v] = fmaf(av[s][v], L[v], bv[s][v]);
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, L);
+  }
+}
+
+// Backward: x_t = dL/dh_t in total (reverse scan of g_t with the a's), then
+// da = x h_{t-1}, db = x, dh0 = a_1 x_1, through the gate derivatives.
+template <int VEC, int TSUB, int WAVES, bool COUPLED>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
+    const float* __restrict__ sp, const float* __restrict__ zp, const float* __restrict__ hp,
+    const float* __restrict__ h0, const float* __restrict__ h, const float* __restrict__ gh,
+    float* __restrict__ ds, float* __restrict__ dz, float* __restrict__ dhp,
+    float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
+    mg_slot_t* incl_data) {
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  if (!th.valid) return;
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  // Kept per step: sigmoid(z), tanh(s), hpre and the adjoint x.
+  float sgv[TSUB][VEC], thv[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      float xs[VEC], xz[VEC];
+      load_vec<VEC>(xs, sp + off);
+      load_vec<VEC>(xz, zp + off);
+      load_vec<VEC>(hv[s], hp + off);
+      load_vec<VEC>(x[s], gh + off);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        sgv[s][v] = mg_sigmoid(xz[v]);
+        thv[s][v] = tanhf(xs[v]);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        sgv[s][v] = 0.f;  // a = tanh(0) = 0 closes the adjoint chain past T
+        thv[s][v] = 0.f;
+        hv[s][v] = 0.f;
+        x[s][v] = 0.f;
+      }
+    }
+  }
+  auto coef_a = [&](int s, int v) {
+    return COUPLED ? (1.f - sgv[s][v]) * thv[s][v] : thv[s][v];
+  };
+  const bool first_sub = (t0 == 0);
+  float hprev[VEC];
+  if (th.col_ok && t0 <= T) {
+    if (first_sub) load_vec<VEC>(hprev, h0 + th.bb * D + th.col);
+    else load_vec<VEC>(hprev, h + (th.bb * T + t0 - 1) * D + th.col);
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) hprev[v] = 0.f;
+  }
+
+  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    loc[v] = aff_identity<1>();
+#pragma unroll
+    for (int s = TSUB - 1; s >= 0; --s) {
+      const float a = coef_a(s, v);
+      loc[v].l[0] = a * (x[s][v] + loc[v].l[0]);
+      loc[v].p *= a;
+    }
+    seed[v] = aff_identity<1>();
+  }
+  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
+                                carry);
+  float y[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
+#pragma unroll
+  for (int s = TSUB - 1; s >= 0; --s) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      x[s][v] += y[v];
+      y[v] = coef_a(s, v) * x[s][v];
+    }
+  }
+  if (first_sub && th.col_ok) store_vec<VEC>(dh0 + th.bb * D + th.col, y);
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float o_s[VEC], o_z[VEC], o_h[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const float sg = sgv[s][v], tv = thv[s][v], xv = x[s][v];
+      const float da = xv * hprev[v];     // dL/da_t
+      const float dsg = sg * (1.f - sg);  // sigmoid'
+      const float a = COUPLED ? (1.f - sg) * tv : tv;
+      o_s[v] = da * (COUPLED ? (1.f - sg) : 1.f) * (1.f - tv * tv);
+      o_z[v] = xv * hv[s][v] * dsg - (COUPLED ? da * tv * dsg : 0.f);
+      o_h[v] = xv * sg;
+      hprev[v] = fmaf(a, hprev[v], sg * hv[s][v]);
+    }
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      const int64_t off = (th.bb * T + t) * D + th.col;
+      store_vec<VEC>(ds + off, o_s);
+      store_vec<VEC>(dz + off, o_z);
+      store_vec<VEC>(dhp + off, o_h);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -655,6 +841,58 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
                      gB, da, db);
   return ew_launch(linear_bwd_kernel<1, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc, gA,
                    gB, da, db);
+}
+
+size_t mg_signed_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
+  size_t m = ew_ws_bytes(B, T, D);
+  for (int vec : {1, 4})
+    m = std::max(m, ew_plan(B, T, D, vec, GATE_TSUB_BWD, GATE_WAVES_BWD, 1).total);
+  return m;
+}
+
+int mg_signed_gate_scan_fwd(const float* s, const float* z, const float* hpre, const float* h0,
+                            float* h, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
+  if (!s || !z || !hpre || !h0 || !h || !ws || !geometry_ok(B, T, D) || (coupled & ~1))
+    return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(s) && is_aligned16(z) && is_aligned16(hpre) &&
+                  is_aligned16(h0) && is_aligned16(h);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+#define MG_GATE_FWD(V, C)                                                                        \
+  return ew_launch(gate_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, C>, p, ws, stream, s, z, hpre, \
+                   h0, h)
+  if (v4) {
+    if (coupled) MG_GATE_FWD(4, true);
+    MG_GATE_FWD(4, false);
+  }
+  if (coupled) MG_GATE_FWD(1, true);
+  MG_GATE_FWD(1, false);
+#undef MG_GATE_FWD
+}
+
+int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, const float* h0,
+                            const float* h, const float* gh, float* ds, float* dz, float* dhpre,
+                            float* dh0, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
+  if (!s || !z || !hpre || !h0 || !h || !gh || !ds || !dz || !dhpre || !dh0 || !ws ||
+      !geometry_ok(B, T, D) || (coupled & ~1))
+    return MG_ERR_ARG;
+  const bool v4 = D % 4 == 0 && is_aligned16(s) && is_aligned16(z) && is_aligned16(hpre) &&
+                  is_aligned16(h0) && is_aligned16(h) && is_aligned16(gh) && is_aligned16(ds) &&
+                  is_aligned16(dz) && is_aligned16(dhpre) && is_aligned16(dh0);
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, GATE_TSUB_BWD, GATE_WAVES_BWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+#define MG_GATE_BWD(V, C)                                                                     \
+  return ew_launch(gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, C>, p, ws, stream, s, z, \
+                   hpre, h0, h, gh, ds, dz, dhpre, dh0)
+  if (v4) {
+    if (coupled) MG_GATE_BWD(4, true);
+    MG_GATE_BWD(4, false);
+  }
+  if (coupled) MG_GATE_BWD(1, true);
+  MG_GATE_BWD(1, false);
+#undef MG_GATE_BWD
 }
 
 int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,

@@ -258,6 +258,69 @@ def _linear_scan_impl(a: torch.Tensor, b: torch.Tensor):
 
 
 # ---------------------------------------------------------------------------
+# fused SignedMinGRU gates + linear_scan
+# ---------------------------------------------------------------------------
+
+
+class _SignedGateScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, s, z, hpre, h0, coupled):
+        out_dtype = s.dtype
+        s32, z32, hp32, h032 = _as_f32(s, z, hpre, h0)
+        Bn, T, D = s32.shape
+        h = torch.empty_like(s32)
+        ws = _scan_workspace(_lib().mg_signed_gate_scan_workspace_bytes(Bn, T, D), s32.device)
+        _call("mg_signed_gate_scan_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
+              Bn, T, D, int(coupled), _ptr(ws), ws.numel(), _stream(s32))
+        ctx.save_for_backward(s32, z32, hp32, h032, h)
+        ctx.coupled = bool(coupled)
+        ctx.out_dtype = out_dtype
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        s32, z32, hp32, h032, h = ctx.saved_tensors
+        Bn, T, D = s32.shape
+        (gh32,) = _as_f32(gh)
+        ds, dz, dhp = (torch.empty_like(s32) for _ in range(3))
+        dh0 = torch.empty_like(h032)
+        ws = _scan_workspace(_lib().mg_signed_gate_scan_workspace_bytes(Bn, T, D), s32.device)
+        _call("mg_signed_gate_scan_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
+              _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, D, int(ctx.coupled),
+              _ptr(ws), ws.numel(), _stream(s32))
+        od = ctx.out_dtype
+        return ds.to(od), dz.to(od), dhp.to(od), dh0.to(od), None
+
+
+def signed_gate_scan_impl(s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor,
+                          h0: torch.Tensor, *, coupled: bool):
+    """Fused SignedMinGRU coefficients + ``linear_scan``: ``h`` (B, T, D).
+
+    No reference kernel fuses these; the arithmetic is the mixer's
+    (``src/mingru/min_gru.py:1788-1857``): ``a = tanh(s)`` (times
+    ``1 - sigmoid(z)`` when ``coupled``), ``b = sigmoid(z) * hpre`` and
+    ``h = A * h0 + Bc`` with ``(A, Bc) = linear_scan(a, b)``, for pre-activations
+    ``s, z, hpre`` (B, T, D) and ``h0`` (B, 1, D).  Differentiable in all four.
+    """
+    if (
+        s.ndim != 3
+        or z.shape != s.shape
+        or hpre.shape != s.shape
+        or tuple(h0.shape) != (s.shape[0], 1, s.shape[2])
+    ):
+        raise ScanFallback(
+            f"signed gate scan (s={tuple(s.shape)}, z={tuple(z.shape)}, hpre={tuple(hpre.shape)}, "
+            f"h0={tuple(h0.shape)}) outside the HIP envelope: need (B, T, D) pre-activations "
+            "and a (B, 1, D) h0"
+        )
+    _same_device(s, z, hpre, h0)
+    if s.numel() == 0:
+        return s.new_empty(s.shape)
+    return _funnel("signed gate scan", _SignedGateScanFn.apply, s, z, hpre, h0, bool(coupled))
+
+
+# ---------------------------------------------------------------------------
 # parallel_scan_log
 # ---------------------------------------------------------------------------
 

@@ -65,6 +65,7 @@ _warned_scan_fallback = False
 _warned_angle_fallback = False
 _warned_delta_fallback = False
 _warned_delta_decay_fallback = False
+_warned_gate_fallback = False
 
 # DeltaMinGRU ``auto`` region.  The HIP chunked-WY kernel beats the eager GPU
 # loop from a handful of chunks upward at every head size of its envelope, so
@@ -214,6 +215,43 @@ def _dispatch_angle_scan(
             stacklevel=3,
         )
         _warned_angle_fallback = True
+    return None
+
+
+def _dispatch_signed_gate_scan(
+    s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor, h0: torch.Tensor, *, coupled: bool
+):
+    """Run SignedMinGRU's coefficients and scan as one fused kernel, or return ``None``.
+
+    The reference has no fused path here; its mixer computes ``a, b`` eagerly
+    and calls ``linear_scan`` (``src/mingru/min_gru.py:1788-1857``), which is
+    what ``None`` falls back to.  Mode handling follows the other fast paths:
+    ``eager`` and CPU ``auto`` return ``None`` silently, ``auto`` warns once
+    on a decline, the forcing mode raises.  Returns ``h`` ``(B, T, D)``.
+    """
+    mode = _resolve_scan_mode(s.is_cuda)
+    if mode is None:
+        return None
+
+    def _call(backend):
+        status = backend.available()
+        if status is not True:
+            raise backend.ScanFallback(str(status))
+        if not hasattr(backend, "signed_gate_scan_impl"):
+            raise backend.ScanFallback("no fused SignedMinGRU gate kernel registered")
+        return backend.signed_gate_scan_impl(s, z, hpre, h0, coupled=coupled)
+
+    result, reason = _resolve_native_dispatch(mode, "the fused SignedMinGRU gate path", _call)
+    if reason is None:
+        return result
+    global _warned_gate_fallback
+    if not _warned_gate_fallback:
+        warnings.warn(
+            "MINGRU_SCAN=auto fell back to the eager SignedMinGRU coefficients "
+            f"(fused gate path) despite CUDA inputs: {reason}",
+            stacklevel=3,
+        )
+        _warned_gate_fallback = True
     return None
 
 
@@ -646,10 +684,13 @@ class SignedMinGRU(DecayMixin, nn.Module):
         self._init_decay(decay, decay_rate, log1p_delta, hidden_size)
 
     def _coeffs(self, x, dt=None):
-        z = torch.sigmoid(self.linear_z(x))
-        tanh_s = torch.tanh(self.linear_s(x))
+        return self._coeffs_from(self.linear_z(x), self.linear_h(x), self.linear_s(x), dt)
+
+    def _coeffs_from(self, z_pre, h_pre, s_pre, dt=None):
+        z = torch.sigmoid(z_pre)
+        tanh_s = torch.tanh(s_pre)
         a = (1 - z) * tanh_s if self.coupled else tanh_s
-        b = z * self.linear_h(x)
+        b = z * h_pre
         if dt is not None:
             a = self._decay_gamma(dt) * a
         return a, b
@@ -662,7 +703,13 @@ class SignedMinGRU(DecayMixin, nn.Module):
                 else x.new_zeros(x.size(0), 1, self.hidden_size)
             )
         dt = self._prepare_decay(delta_t, canonical_ndim=2)
-        a, b = self._coeffs(x, dt)
+        z_pre, h_pre, s_pre = self.linear_z(x), self.linear_h(x), self.linear_s(x)
+        if dt is None:
+            # GPU fast path: gates, scan and h = A h0 + Bc in one fused kernel.
+            h = _dispatch_signed_gate_scan(s_pre, z_pre, h_pre, h_0, coupled=self.coupled)
+            if h is not None:
+                return h
+        a, b = self._coeffs_from(z_pre, h_pre, s_pre, dt)
         A, Bc = linear_scan(a, b)
         return A * h_0 + Bc
 

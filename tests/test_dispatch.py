@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 
 import mingru_amd
-from mingru_amd import DeltaMinGRU, GivensMinGRU, hip_scans, linear_scan
+from mingru_amd import DeltaMinGRU, GivensMinGRU, SignedMinGRU, hip_scans, linear_scan
 from mingru_amd import min_gru as mg
 
 BACKEND = "mingru_amd.hip_scans"
@@ -35,7 +35,7 @@ class _FakeCudaTensor:
 def _isolate(monkeypatch):
     monkeypatch.delenv("MINGRU_SCAN", raising=False)
     for flag in ("_warned_scan_fallback", "_warned_angle_fallback", "_warned_delta_fallback",
-                 "_warned_delta_decay_fallback"):
+                 "_warned_delta_decay_fallback", "_warned_gate_fallback"):
         monkeypatch.setattr(mg, flag, False)
 
 
@@ -275,6 +275,83 @@ def test_angle_seam_reaches_backend(monkeypatch):
     with pytest.raises(RuntimeError, match="declined by the fake backend"):
         m(torch.randn(2, 7, 6))
     assert seen["theta"][:3] == (2, 7, 2)
+
+
+def _fake_backend(monkeypatch, **attrs):
+    class FakeFallback(Exception):
+        pass
+
+    fake = types.ModuleType(BACKEND)
+    fake.ScanFallback = FakeFallback
+    fake.available = lambda: True
+    fake.SCAN_IMPLS = {}
+    for k, v in attrs.items():
+        setattr(fake, k, v)
+    monkeypatch.setitem(sys.modules, BACKEND, fake)
+    monkeypatch.setattr(mingru_amd, "hip_scans", fake, raising=False)
+    return fake
+
+
+def test_signed_gate_seam_hands_preactivations_to_backend(monkeypatch):
+    """SignedMinGRU's fused path passes (s, z, hpre) pre-activations and a (B, 1, D) h0,
+    and returns the backend's h unchanged."""
+    seen = {}
+
+    def fake_gate(s, z, hpre, h0, *, coupled):
+        seen.update(s=tuple(s.shape), h0=tuple(h0.shape), coupled=coupled)
+        return torch.full(s.shape, 7.0)
+
+    _fake_backend(monkeypatch, signed_gate_scan_impl=fake_gate)
+    m = SignedMinGRU(5, 6, coupled=True)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    y = m(torch.randn(2, 9, 5))
+    assert seen == {"s": (2, 9, 6), "h0": (2, 1, 6), "coupled": True}
+    assert torch.equal(y, torch.full((2, 9, 6), 7.0))
+
+
+def test_signed_gate_seam_skips_fusion_under_decay(monkeypatch):
+    """With decay the coefficients carry gamma(dt): no fused call, the scan seam runs."""
+    calls = []
+
+    def fake_gate(*args, **kwargs):
+        calls.append("gate")
+        raise AssertionError("fused path must not run under decay")
+
+    def fake_linear(a, b):
+        calls.append("linear_scan")
+        return torch.cumprod(a, 1), _seq_bc(a, b)
+
+    _fake_backend(monkeypatch, signed_gate_scan_impl=fake_gate,
+                  SCAN_IMPLS={"linear_scan": fake_linear})
+    m = SignedMinGRU(4, 5, decay="fixed")
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m(torch.randn(2, 6, 4), delta_t=torch.rand(2, 6))
+    assert calls == ["linear_scan"]
+
+
+def _seq_bc(a, b):
+    h, out = torch.zeros_like(a[:, 0]), []
+    for t in range(a.shape[1]):
+        h = a[:, t] * h + b[:, t]
+        out.append(h)
+    return torch.stack(out, 1)
+
+
+def test_signed_gate_auto_fallback_warns_once_and_runs_eager(monkeypatch):
+    def fake_gate(*args, **kwargs):
+        raise sys.modules[BACKEND].ScanFallback("declined by the fake backend")
+
+    _fake_backend(monkeypatch, signed_gate_scan_impl=fake_gate)
+    f = _FakeCudaTensor()
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    with pytest.warns(UserWarning, match="fused gate path"):
+        assert mg._dispatch_signed_gate_scan(f, f, f, f, coupled=False) is None
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert mg._dispatch_signed_gate_scan(f, f, f, f, coupled=False) is None
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with pytest.raises(RuntimeError, match="declined by the fake backend"):
+        mg._dispatch_signed_gate_scan(f, f, f, f, coupled=False)
 
 
 def test_delta_module_forward_equals_step_recurrence():
