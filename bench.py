@@ -93,6 +93,12 @@ def build_ops(torch, wl):
     N = c["B"] * c["T"] * c["D"]
     ops["C2"] = Op("C2", "C2 SignedMinGRU linear_scan fwd+bwd", c["B"] * c["T"],
                    "mg_linear_scan_fwd", "mg_linear_scan_bwd", 4 * N * 4, 6 * N * 4)
+    # C2g: SignedMinGRU gates + linear_scan + h0 fused (same shape as C2).  Forward
+    # reads s, z, hpre and writes h; backward reads s, z, hpre, dL/dh and writes
+    # ds, dz, dhpre (h is read only at sub-chunk starts).
+    ops["C2g"] = Op("C2g", "C2g SignedMinGRU fused gates + linear_scan fwd+bwd (C2 shape)",
+                    c["B"] * c["T"], "mg_signed_gate_scan_fwd", "mg_signed_gate_scan_bwd",
+                    4 * N * 4, 7 * N * 4)
     # C1: parallel_scan_log
     c = wl.C1
     N = c["B"] * c["T"] * c["D"]
@@ -148,6 +154,19 @@ def make_step(key, torch, wl, dev):
             torch.autograd.grad((A, Bc), (ac, bc), (inp["grad_A"][:bs], inp["grad_Bc"][:bs]))
 
         return step, cpu, wl.C2["B"]
+    if key == "C2g":
+        from mingru_amd.min_gru import _dispatch_signed_gate_scan
+
+        inp = wl.c2g_inputs(**wl.C2)
+        xs = [inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre")]
+        h0 = inp["h0"].to(dev)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = _dispatch_signed_gate_scan(*xs, h0, coupled=False)
+            return torch.autograd.grad(h, xs, gh)
+
+        return step, None, wl.C2["B"]
     if key == "C1":
         inp = wl.c1_inputs(**wl.C1)
         lc = inp["log_coeffs"].to(dev).requires_grad_(True)
@@ -233,6 +252,31 @@ def make_step(key, torch, wl, dev):
 
         return step, cpu, wl.C5["B"]
     raise KeyError(key)
+
+
+def gate_unfused_gpu_ms(torch, wl, dev, steps):
+    """The unfused SignedMinGRU path at the C2 shape: eager gates on the GPU, the HIP
+    linear_scan, then h = A * h0 + Bc, fwd+bwd; ms per step over `steps` steps."""
+    import mingru_amd as mg
+
+    inp = wl.c2g_inputs(**wl.C2)
+    s, z, hp = (inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre"))
+    h0 = inp["h0"].to(dev)
+    gh = inp["grad_h"].to(dev)
+
+    def step():
+        sg = torch.sigmoid(z)
+        A, Bc = mg.linear_scan(torch.tanh(s), sg * hp)
+        torch.autograd.grad(A * h0 + Bc, (s, z, hp), gh)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def delta_eager_gpu_ms(torch, wl, dev, reps=3):
@@ -416,7 +460,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C1", "C3", "C3m", "C4", "C5"]
+    order = ["C2", "C2g", "C1", "C3", "C3m", "C4", "C5"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -433,6 +477,13 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
+        if key == "C2g":
+            uf = gate_unfused_gpu_ms(torch, wl, dev, args.steps)
+            res["unfused_ms_per_step"] = uf
+            res["speedup_vs_unfused"] = uf / res["ms_per_step"]
+            print(f"#   unfused (eager gates + HIP linear_scan + A*h0+Bc): {uf:.3f} ms/step "
+                  f"({res['speedup_vs_unfused']:.2f}x the fused time)", file=sys.stderr,
+                  flush=True)
         if key == "C5" and not args.no_eager:
             eg = delta_eager_gpu_ms(torch, wl, dev)
             res["eager_gpu_ms_per_step"] = eg
@@ -483,8 +534,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
-        "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C3": wl.C3,
-                                               "C3m": wl.C3, "C4": wl.C4,
+        "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C2g": wl.C2,
+                                               "C3": wl.C3, "C3m": wl.C3, "C4": wl.C4,
                                                "C5": wl.C5}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -569,11 +569,17 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
 // one pass reads s, z, hpre and writes only h; the backward returns the
 // pre-activation gradients directly.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float mg_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+// sigmoid(x) = 1 / (1 + e^-x) on the hardware exp2 and reciprocal (each about
+// 1 ulp; e^-x overflowing to inf gives 0, underflowing to 0 gives 1), and
+// tanh(s) = 2 sigmoid(2 s) - 1 (absolute error a few 1e-8 near 0).
+__device__ __forceinline__ float mg_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
+}
+__device__ __forceinline__ float mg_tanh(float x) { return fmaf(2.f, mg_sigmoid(2.f * x), -1.f); }
 
 template <bool COUPLED>
 __device__ __forceinline__ void gate_coeffs(float s, float z, float hpre, float& a, float& b) {
-  const float sg = mg_sigmoid(z), th = tanhf(s);
+  const float sg = mg_sigmoid(z), th = mg_tanh(s);
   a = COUPLED ? (1.f - sg) * th : th;
   b = sg * hpre;
 }
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
         sgv[s][v] = mg_sigmoid(xz[v]);
-        thv[s][v] = tanhf(xs[v]);
+        thv[s][v] = mg_tanh(xs[v]);
       }
     } else {
 #pragma unroll

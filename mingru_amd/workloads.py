@@ -56,6 +56,18 @@ def c2_inputs(B=16, T=4096, D=1024):
     return dict(a=a, b=b, grad_A=torch.zeros_like(gh), grad_Bc=gh)
 
 
+def c2g_inputs(B=16, T=4096, D=1024):
+    """SignedMinGRU pre-activations at the C2 shape for the fused gate scan:
+    ``s = 2 N(0,1)`` (so ``a = tanh(s)`` is distributed as C2's), ``z, hpre ~ N(0,1)``,
+    ``h0 = 0`` (B, 1, D), upstream ``dL/dh ~ N(0,1)``."""
+    g = _gen(1012)
+    s = 2.0 * torch.randn(B, T, D, generator=g)
+    z = torch.randn(B, T, D, generator=g)
+    hpre = torch.randn(B, T, D, generator=g)
+    gh = torch.randn(B, T, D, generator=_gen(2012))
+    return dict(s=s, z=z, hpre=hpre, h0=torch.zeros(B, 1, D), grad_h=gh)
+
+
 def c3_inputs(B=16, T=4096, n=256):
     """``A = sigmoid(N) R(theta)``, theta ~ U(-pi, pi); ``b ~ N``; ``h0 ~ N``."""
     g = _gen(1003)
