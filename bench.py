@@ -47,7 +47,8 @@ def _parse():
     ap.add_argument("--only", type=str, default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-eager", action="store_true",
-                    help="skip the eager-GPU delta comparison (used under rocprof counters)")
+                    help="skip the GPU comparison paths (eager delta loop, unfused gate path); "
+                         "used under rocprof")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time a plain 1 GiB device copy (rocprof counter calibration)")
     return ap.parse_args()
@@ -477,7 +478,7 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
-        if key == "C2g":
+        if key == "C2g" and not args.no_eager:
             uf = gate_unfused_gpu_ms(torch, wl, dev, args.steps)
             res["unfused_ms_per_step"] = uf
             res["speedup_vs_unfused"] = uf / res["ms_per_step"]
