@@ -106,6 +106,11 @@ def build_ops(torch, wl):
     N1 = c["B"] * (c["T"] + 1) * c["D"]
     ops["C1"] = Op("C1", "C1 MinGRU parallel_scan_log fwd+bwd", c["B"] * c["T"],
                    "mg_log_scan_fwd", "mg_log_scan_bwd", (2 * N + N1) * 4, (3 * N + 2 * N1) * 4)
+    # C1g: MinGRU log-space gates + parallel_scan_log fused (C1 shape).  Forward reads
+    # k, hpre and writes h; backward reads k, hpre, dL/dh and writes dk, dhpre.
+    ops["C1g"] = Op("C1g", "C1g MinGRU fused gates + parallel_scan_log fwd+bwd (C1 shape)",
+                    c["B"] * c["T"], "mg_mingru_gate_scan_fwd", "mg_mingru_gate_scan_bwd",
+                    3 * N * 4, 5 * N * 4)
     # C3: 2x2 matrix_affine_scan and matrix_scan (b = 0)
     c = wl.C3
     P = c["B"] * c["T"] * c["n"]
@@ -168,6 +173,19 @@ def make_step(key, torch, wl, dev):
             return torch.autograd.grad(h, xs, gh)
 
         return step, None, wl.C2["B"]
+    if key == "C1g":
+        from mingru_amd.min_gru import _dispatch_mingru_gate_scan
+
+        inp = wl.c1g_inputs(**wl.C1)
+        xs = [inp[k].to(dev).requires_grad_(True) for k in ("k", "hpre")]
+        lh0 = inp["log_h0"].to(dev)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = _dispatch_mingru_gate_scan(*xs, lh0)
+            return torch.autograd.grad(h, xs, gh)
+
+        return step, None, wl.C1["B"]
     if key == "C1":
         inp = wl.c1_inputs(**wl.C1)
         lc = inp["log_coeffs"].to(dev).requires_grad_(True)
@@ -255,20 +273,36 @@ def make_step(key, torch, wl, dev):
     raise KeyError(key)
 
 
-def gate_unfused_gpu_ms(torch, wl, dev, steps):
-    """The unfused SignedMinGRU path at the C2 shape: eager gates on the GPU, the HIP
-    linear_scan, then h = A * h0 + Bc, fwd+bwd; ms per step over `steps` steps."""
+def gate_unfused_gpu_ms(key, torch, wl, dev, steps):
+    """The unfused mixer path that a fused gate op replaces, fwd+bwd, ms per step over
+    `steps` steps.  C2g: SignedMinGRU's eager gates on the GPU, the HIP linear_scan,
+    then h = A * h0 + Bc.  C1g: MinGRU's eager log-space gates, the concatenation
+    with log h0 and the HIP parallel_scan_log."""
+    import torch.nn.functional as F
+
     import mingru_amd as mg
+    from mingru_amd.min_gru import log_g
 
-    inp = wl.c2g_inputs(**wl.C2)
-    s, z, hp = (inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre"))
-    h0 = inp["h0"].to(dev)
-    gh = inp["grad_h"].to(dev)
+    if key == "C2g":
+        inp = wl.c2g_inputs(**wl.C2)
+        s, z, hp = (inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre"))
+        h0 = inp["h0"].to(dev)
+        gh = inp["grad_h"].to(dev)
 
-    def step():
-        sg = torch.sigmoid(z)
-        A, Bc = mg.linear_scan(torch.tanh(s), sg * hp)
-        torch.autograd.grad(A * h0 + Bc, (s, z, hp), gh)
+        def step():
+            sg = torch.sigmoid(z)
+            A, Bc = mg.linear_scan(torch.tanh(s), sg * hp)
+            torch.autograd.grad(A * h0 + Bc, (s, z, hp), gh)
+    else:
+        inp = wl.c1g_inputs(**wl.C1)
+        k, hp = (inp[n].to(dev).requires_grad_(True) for n in ("k", "hpre"))
+        lh0 = inp["log_h0"].to(dev)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            lv = torch.cat([lh0, -F.softplus(-k) + log_g(hp)], dim=1)
+            h = mg.parallel_scan_log(-F.softplus(k), lv)
+            torch.autograd.grad(h, (k, hp), gh)
 
     for _ in range(2):
         step()
@@ -461,7 +495,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C2g", "C1", "C3", "C3m", "C4", "C5"]
+    order = ["C2", "C2g", "C1", "C1g", "C3", "C3m", "C4", "C5"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -478,11 +512,12 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
-        if key == "C2g" and not args.no_eager:
-            uf = gate_unfused_gpu_ms(torch, wl, dev, args.steps)
+        if key in ("C2g", "C1g") and not args.no_eager:
+            uf = gate_unfused_gpu_ms(key, torch, wl, dev, args.steps)
             res["unfused_ms_per_step"] = uf
             res["speedup_vs_unfused"] = uf / res["ms_per_step"]
-            print(f"#   unfused (eager gates + HIP linear_scan + A*h0+Bc): {uf:.3f} ms/step "
+            scan = "linear_scan + A*h0+Bc" if key == "C2g" else "parallel_scan_log"
+            print(f"#   unfused (eager gates + HIP {scan}): {uf:.3f} ms/step "
                   f"({res['speedup_vs_unfused']:.2f}x the fused time)", file=sys.stderr,
                   flush=True)
         if key == "C5" and not args.no_eager:
@@ -535,7 +570,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
-        "config": {"workload": op.workload, **{"C1": wl.C1, "C2": wl.C2, "C2g": wl.C2,
+        "config": {"workload": op.workload, **{"C1": wl.C1, "C1g": wl.C1, "C2": wl.C2, "C2g": wl.C2,
                                                "C3": wl.C3, "C3m": wl.C3, "C4": wl.C4,
                                                "C5": wl.C5}.get(head_key, {})},
         "roofline": roofline,

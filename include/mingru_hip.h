@@ -65,6 +65,25 @@ int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, c
                             float* dh0, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
                             size_t ws_bytes, mg_stream_t stream);
 
+/* ---- fused MinGRU gates + parallel_scan_log, (B, T, D) -------------------------
+ * No reference kernel fuses these: replaces MinGRU.forward's coefficient code and
+ * its scan call (src/mingru/min_gru.py:1366-1397): log(1 - z) = -softplus(k),
+ * log z = -softplus(-k), log h~ = log_g(hpre) and
+ * h = exp(parallel_scan_log(log(1 - z), [log h0, log z + log h~])).  The kernel
+ * runs the same recurrence in linear space (every term is positive):
+ * h_t = sigmoid(-k) h_{t-1} + sigmoid(k) g(hpre), h_0 = exp(log_h0).  One pass
+ * reads k and hpre and writes h; log_h0 / dlog_h0 are (B, D).  Workspace from its
+ * own size query. */
+size_t mg_mingru_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
+int mg_mingru_gate_scan_fwd(const float* k, const float* hpre, const float* log_h0, float* h,
+                            int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                            mg_stream_t stream);
+/* h = forward output, gh = dL/dh -> dk, dhpre (B,T,D) and dlog_h0 (B,D). */
+int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_h0,
+                            const float* h, const float* gh, float* dk, float* dhpre,
+                            float* dlog_h0, int64_t B, int64_t T, int64_t D, void* ws,
+                            size_t ws_bytes, mg_stream_t stream);
+
 /* ---- parallel_scan_log: log-space inputs, (B, T, D) and (B, T+1, D) ---------
  * Replaces parallel_scan_log_fwd (src/mingru/triton_scans.py:1336-1357, kernel
  * :754-821) and its eager-recompute backward (:1489-1552) behind

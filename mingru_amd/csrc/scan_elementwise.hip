@@ -22,6 +22,8 @@
 // forward output per thread sub-chunk boundary.
 #include "mg_common.h"
 
+#include <initializer_list>
+
 #include <algorithm>
 
 namespace {
@@ -562,13 +564,21 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fused SignedMinGRU gates + scan (reference mixer src/mingru/min_gru.py:
-// 1807-1856: a = tanh(s) [* (1 - sigmoid(z)) when coupled], b = sigmoid(z) * hpre,
-// (A, Bc) = linear_scan(a, b), h = A * h0 + Bc).  The coefficients are formed in
-// registers from the three pre-activations and the scan is seeded with h0, so
-// one pass reads s, z, hpre and writes only h; the backward returns the
+// Fused gates + scan.  The coefficients are formed in registers from the
+// mixer's pre-activations and the scan is seeded with h0, so one pass reads
+// the pre-activations and writes only h; the backward returns the
 // pre-activation gradients directly.
+//   GATE_SIGNED (/_COUPLED): SignedMinGRU (reference src/mingru/min_gru.py:
+//     1788-1857), inputs s, z, hpre and h0:
+//     a = tanh(s) [* (1 - sigmoid(z))], b = sigmoid(z) * hpre, h = A h0 + Bc.
+//   GATE_MINGRU: MinGRU (reference :1366-1397), inputs k, hpre and log h0:
+//     a = sigmoid(-k) = exp(-softplus(k)), b = sigmoid(k) g(hpre)
+//     = exp(log z + log_g(hpre)), h0 = exp(log h0); the log-space scan
+//     parallel_scan_log(log a, [log h0, log b]) run in linear space, where every
+//     term is positive.  g(x) = x + 1/2 for x >= 0, sigmoid(x) otherwise.
 // ---------------------------------------------------------------------------
+enum : int { GATE_SIGNED = 0, GATE_SIGNED_COUPLED = 1, GATE_MINGRU = 2 };
+
 // sigmoid(x) = 1 / (1 + e^-x) on the hardware exp2 and reciprocal (each about
 // 1 ulp; e^-x overflowing to inf gives 0, underflowing to 0 gives 1), and
 // tanh(s) = 2 sigmoid(2 s) - 1 (absolute error a few 1e-8 near 0).
@@ -576,17 +586,29 @@ __device__ __forceinline__ float mg_sigmoid(float x) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
 }
 __device__ __forceinline__ float mg_tanh(float x) { return fmaf(2.f, mg_sigmoid(2.f * x), -1.f); }
+__device__ __forceinline__ float mg_g(float x) { return x >= 0.f ? x + 0.5f : mg_sigmoid(x); }
 
-template <bool COUPLED>
-__device__ __forceinline__ void gate_coeffs(float s, float z, float hpre, float& a, float& b) {
-  const float sg = mg_sigmoid(z), th = mg_tanh(s);
-  a = COUPLED ? (1.f - sg) * th : th;
-  b = sg * hpre;
+template <int G>
+__device__ __forceinline__ void gate_coeffs(float p0, float p1, float p2, float& a, float& b) {
+  if constexpr (G == GATE_MINGRU) {
+    a = mg_sigmoid(-p0);
+    b = mg_sigmoid(p0) * mg_g(p1);
+  } else {
+    const float sg = mg_sigmoid(p1), th = mg_tanh(p0);
+    a = G == GATE_SIGNED_COUPLED ? (1.f - sg) * th : th;
+    b = sg * p2;
+  }
 }
 
-template <int VEC, int TSUB, int WAVES, bool COUPLED>
+// Pre-activation inputs: (s, z, hpre) for the signed gates, (k, hpre) for MinGRU.
+template <int G>
+constexpr int gate_inputs() {
+  return G == GATE_MINGRU ? 2 : 3;
+}
+
+template <int VEC, int TSUB, int WAVES, int G>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
-    const float* __restrict__ sp, const float* __restrict__ zp, const float* __restrict__ hp,
+    const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
     const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
@@ -600,12 +622,13 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
-      float xs[VEC], xz[VEC], xh[VEC];
-      load_vec<VEC>(xs, sp + off);
-      load_vec<VEC>(xz, zp + off);
-      load_vec<VEC>(xh, hp + off);
+      float x0[VEC], x1[VEC], x2[VEC];
+      load_vec<VEC>(x0, p0 + off);
+      load_vec<VEC>(x1, p1 + off);
+      if constexpr (gate_inputs<G>() == 3) load_vec<VEC>(x2, p2 + off);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) gate_coeffs<COUPLED>(xs[v], xz[v], xh[v], av[s][v], bv[s][v]);
+      for (int v = 0; v < VEC; ++v)
+        gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -629,7 +652,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     float x[VEC];
     load_vec<VEC>(x, h0 + th.bb * D + th.col);
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) seed[v].l[0] = x[v];
+    for (int v = 0; v < VEC; ++v) seed[v].l[0] = G == GATE_MINGRU ? expf(x[v]) : x[v];
   }
   ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                  carry);
@@ -646,54 +669,75 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
 }
 
 // Backward: x_t = dL/dh_t in total (reverse scan of g_t with the a's), then
-// da = x h_{t-1}, db = x, dh0 = a_1 x_1, through the gate derivatives.
-template <int VEC, int TSUB, int WAVES, bool COUPLED>
+// da = x h_{t-1}, db = x, dh0 = a_1 x_1, through the gate derivatives.  Per step
+// the kernel keeps the adjoint and three gate values:
+//   signed: sigmoid(z), tanh(s), hpre;   MinGRU: sigmoid(-k), sigmoid(k), hpre.
+template <int VEC, int TSUB, int WAVES, int G>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
-    const float* __restrict__ sp, const float* __restrict__ zp, const float* __restrict__ hp,
+    const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
     const float* __restrict__ h0, const float* __restrict__ h, const float* __restrict__ gh,
-    float* __restrict__ ds, float* __restrict__ dz, float* __restrict__ dhp,
+    float* __restrict__ d0, float* __restrict__ d1, float* __restrict__ d2,
     float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
+  constexpr bool MIN = G == GATE_MINGRU;
 
-  // Kept per step: sigmoid(z), tanh(s), hpre and the adjoint x.
-  float sgv[TSUB][VEC], thv[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
+  float ua[TSUB][VEC], ub[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
 #pragma unroll
   for (int s = 0; s < TSUB; ++s) {
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
-      float xs[VEC], xz[VEC];
-      load_vec<VEC>(xs, sp + off);
-      load_vec<VEC>(xz, zp + off);
-      load_vec<VEC>(hv[s], hp + off);
+      float x0[VEC];
+      load_vec<VEC>(x0, p0 + off);
       load_vec<VEC>(x[s], gh + off);
+      if constexpr (MIN) {
+        load_vec<VEC>(hv[s], p1 + off);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        sgv[s][v] = mg_sigmoid(xz[v]);
-        thv[s][v] = mg_tanh(xs[v]);
+        for (int v = 0; v < VEC; ++v) {
+          ua[s][v] = mg_sigmoid(-x0[v]);  // a
+          ub[s][v] = mg_sigmoid(x0[v]);   // z
+        }
+      } else {
+        float x1[VEC];
+        load_vec<VEC>(x1, p1 + off);
+        load_vec<VEC>(hv[s], p2 + off);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          ua[s][v] = mg_sigmoid(x1[v]);  // sigmoid(z)
+          ub[s][v] = mg_tanh(x0[v]);     // tanh(s)
+        }
       }
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        sgv[s][v] = 0.f;  // a = tanh(0) = 0 closes the adjoint chain past T
-        thv[s][v] = 0.f;
+        ua[s][v] = 0.f;  // a = 0 closes the adjoint chain past T
+        ub[s][v] = 0.f;
         hv[s][v] = 0.f;
         x[s][v] = 0.f;
       }
     }
   }
   auto coef_a = [&](int s, int v) {
-    return COUPLED ? (1.f - sgv[s][v]) * thv[s][v] : thv[s][v];
+    if constexpr (MIN) return ua[s][v];
+    else if constexpr (G == GATE_SIGNED_COUPLED) return (1.f - ua[s][v]) * ub[s][v];
+    else return ub[s][v];
   };
   const bool first_sub = (t0 == 0);
   float hprev[VEC];
   if (th.col_ok && t0 <= T) {
-    if (first_sub) load_vec<VEC>(hprev, h0 + th.bb * D + th.col);
-    else load_vec<VEC>(hprev, h + (th.bb * T + t0 - 1) * D + th.col);
+    if (first_sub) {
+      load_vec<VEC>(hprev, h0 + th.bb * D + th.col);
+      if constexpr (MIN) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) hprev[v] = expf(hprev[v]);
+      }
+    } else {
+      load_vec<VEC>(hprev, h + (th.bb * T + t0 - 1) * D + th.col);
+    }
   } else {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) hprev[v] = 0.f;
@@ -724,27 +768,46 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
       y[v] = coef_a(s, v) * x[s][v];
     }
   }
-  if (first_sub && th.col_ok) store_vec<VEC>(dh0 + th.bb * D + th.col, y);
+  if (first_sub && th.col_ok) {
+    // dL/dh0 = a_1 x_1; the MinGRU input is log h0: times h0.
+    if constexpr (MIN) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) y[v] *= hprev[v];
+    }
+    store_vec<VEC>(dh0 + th.bb * D + th.col, y);
+  }
 #pragma unroll
   for (int s = 0; s < TSUB; ++s) {
-    float o_s[VEC], o_z[VEC], o_h[VEC];
+    float o0[VEC], o1[VEC], o2[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      const float sg = sgv[s][v], tv = thv[s][v], xv = x[s][v];
-      const float da = xv * hprev[v];     // dL/da_t
-      const float dsg = sg * (1.f - sg);  // sigmoid'
-      const float a = COUPLED ? (1.f - sg) * tv : tv;
-      o_s[v] = da * (COUPLED ? (1.f - sg) : 1.f) * (1.f - tv * tv);
-      o_z[v] = xv * hv[s][v] * dsg - (COUPLED ? da * tv * dsg : 0.f);
-      o_h[v] = xv * sg;
-      hprev[v] = fmaf(a, hprev[v], sg * hv[s][v]);
+      const float xv = x[s][v], da = xv * hprev[v];  // dL/da_t
+      float a, b;
+      if constexpr (MIN) {
+        // a = sigmoid(-k): da/dk = -a z;  b = z g(hpre): db/dk = z a g, db/dhpre = z g'.
+        const float hp = hv[s][v], am = ua[s][v], zk = ub[s][v];
+        const float gv = hp >= 0.f ? hp + 0.5f : mg_sigmoid(hp);
+        const float gp = hp >= 0.f ? 1.f : gv * (1.f - gv);
+        a = am;
+        b = zk * gv;
+        o0[v] = (xv * gv - da) * am * zk;
+        o1[v] = xv * zk * gp;
+      } else {
+        const float sg = ua[s][v], tv = ub[s][v], dsg = sg * (1.f - sg);
+        a = G == GATE_SIGNED_COUPLED ? (1.f - sg) * tv : tv;
+        b = sg * hv[s][v];
+        o0[v] = da * (G == GATE_SIGNED_COUPLED ? (1.f - sg) : 1.f) * (1.f - tv * tv);
+        o1[v] = xv * hv[s][v] * dsg - (G == GATE_SIGNED_COUPLED ? da * tv * dsg : 0.f);
+        o2[v] = xv * sg;
+      }
+      hprev[v] = fmaf(a, hprev[v], b);
     }
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
-      store_vec<VEC>(ds + off, o_s);
-      store_vec<VEC>(dz + off, o_z);
-      store_vec<VEC>(dhp + off, o_h);
+      store_vec<VEC>(d0 + off, o0);
+      store_vec<VEC>(d1 + off, o1);
+      if constexpr (!MIN) store_vec<VEC>(d2 + off, o2);
     }
   }
 }
@@ -807,6 +870,48 @@ size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
   return m;
 }
 
+size_t gate_ws_bytes(int64_t B, int64_t T, int64_t D) {
+  size_t m = ew_ws_bytes(B, T, D);
+  for (int vec : {1, 4})
+    m = std::max(m, ew_plan(B, T, D, vec, GATE_TSUB_BWD, GATE_WAVES_BWD, 1).total);
+  return m;
+}
+
+bool all_aligned16(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p && !is_aligned16(p)) return false;
+  return true;
+}
+
+template <int G>
+int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const float* h0, float* h,
+                    int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    hipStream_t stream) {
+  const bool v4 = D % 4 == 0 && all_aligned16({p0, p1, p2, h0, h});
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  if (v4)
+    return ew_launch(gate_fwd_kernel<4, EW_TSUB_FWD, EW_WAVES_FWD, G>, p, ws, stream, p0, p1, p2,
+                     h0, h);
+  return ew_launch(gate_fwd_kernel<1, EW_TSUB_FWD, EW_WAVES_FWD, G>, p, ws, stream, p0, p1, p2, h0,
+                   h);
+}
+
+template <int G>
+int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const float* h0,
+                    const float* h, const float* gh, float* d0, float* d1, float* d2, float* dh0,
+                    int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    hipStream_t stream) {
+  const bool v4 = D % 4 == 0 && all_aligned16({p0, p1, p2, h0, h, gh, d0, d1, d2, dh0});
+  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, GATE_TSUB_BWD, GATE_WAVES_BWD, 1);
+  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+  if (v4)
+    return ew_launch(gate_bwd_kernel<4, GATE_TSUB_BWD, GATE_WAVES_BWD, G>, p, ws, stream, p0, p1,
+                     p2, h0, h, gh, d0, d1, d2, dh0);
+  return ew_launch(gate_bwd_kernel<1, GATE_TSUB_BWD, GATE_WAVES_BWD, G>, p, ws, stream, p0, p1, p2,
+                   h0, h, gh, d0, d1, d2, dh0);
+}
+
 }  // namespace
 
 extern "C" {
@@ -850,10 +955,7 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
 }
 
 size_t mg_signed_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
-  size_t m = ew_ws_bytes(B, T, D);
-  for (int vec : {1, 4})
-    m = std::max(m, ew_plan(B, T, D, vec, GATE_TSUB_BWD, GATE_WAVES_BWD, 1).total);
-  return m;
+  return gate_ws_bytes(B, T, D);
 }
 
 int mg_signed_gate_scan_fwd(const float* s, const float* z, const float* hpre, const float* h0,
@@ -861,20 +963,9 @@ int mg_signed_gate_scan_fwd(const float* s, const float* z, const float* hpre, c
                             size_t ws_bytes, hipStream_t stream) {
   if (!s || !z || !hpre || !h0 || !h || !ws || !geometry_ok(B, T, D) || (coupled & ~1))
     return MG_ERR_ARG;
-  const bool v4 = D % 4 == 0 && is_aligned16(s) && is_aligned16(z) && is_aligned16(hpre) &&
-                  is_aligned16(h0) && is_aligned16(h);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, EW_TSUB_FWD, EW_WAVES_FWD, 1);
-  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-#define MG_GATE_FWD(V, C)                                                                        \
-  return ew_launch(gate_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, C>, p, ws, stream, s, z, hpre, \
-                   h0, h)
-  if (v4) {
-    if (coupled) MG_GATE_FWD(4, true);
-    MG_GATE_FWD(4, false);
-  }
-  if (coupled) MG_GATE_FWD(1, true);
-  MG_GATE_FWD(1, false);
-#undef MG_GATE_FWD
+  return coupled ? gate_fwd_launch<GATE_SIGNED_COUPLED>(s, z, hpre, h0, h, B, T, D, ws, ws_bytes,
+                                                        stream)
+                 : gate_fwd_launch<GATE_SIGNED>(s, z, hpre, h0, h, B, T, D, ws, ws_bytes, stream);
 }
 
 int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, const float* h0,
@@ -884,21 +975,32 @@ int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, c
   if (!s || !z || !hpre || !h0 || !h || !gh || !ds || !dz || !dhpre || !dh0 || !ws ||
       !geometry_ok(B, T, D) || (coupled & ~1))
     return MG_ERR_ARG;
-  const bool v4 = D % 4 == 0 && is_aligned16(s) && is_aligned16(z) && is_aligned16(hpre) &&
-                  is_aligned16(h0) && is_aligned16(h) && is_aligned16(gh) && is_aligned16(ds) &&
-                  is_aligned16(dz) && is_aligned16(dhpre) && is_aligned16(dh0);
-  EwPlan p = ew_plan(B, T, D, v4 ? 4 : 1, GATE_TSUB_BWD, GATE_WAVES_BWD, 1);
-  if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-#define MG_GATE_BWD(V, C)                                                                     \
-  return ew_launch(gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, C>, p, ws, stream, s, z, \
-                   hpre, h0, h, gh, ds, dz, dhpre, dh0)
-  if (v4) {
-    if (coupled) MG_GATE_BWD(4, true);
-    MG_GATE_BWD(4, false);
-  }
-  if (coupled) MG_GATE_BWD(1, true);
-  MG_GATE_BWD(1, false);
-#undef MG_GATE_BWD
+  return coupled ? gate_bwd_launch<GATE_SIGNED_COUPLED>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0,
+                                                        B, T, D, ws, ws_bytes, stream)
+                 : gate_bwd_launch<GATE_SIGNED>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0, B, T,
+                                                D, ws, ws_bytes, stream);
+}
+
+size_t mg_mingru_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
+  return gate_ws_bytes(B, T, D);
+}
+
+int mg_mingru_gate_scan_fwd(const float* k, const float* hpre, const float* log_h0, float* h,
+                            int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                            hipStream_t stream) {
+  if (!k || !hpre || !log_h0 || !h || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
+  return gate_fwd_launch<GATE_MINGRU>(k, hpre, nullptr, log_h0, h, B, T, D, ws, ws_bytes, stream);
+}
+
+int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_h0,
+                            const float* h, const float* gh, float* dk, float* dhpre,
+                            float* dlog_h0, int64_t B, int64_t T, int64_t D, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
+  if (!k || !hpre || !log_h0 || !h || !gh || !dk || !dhpre || !dlog_h0 || !ws ||
+      !geometry_ok(B, T, D))
+    return MG_ERR_ARG;
+  return gate_bwd_launch<GATE_MINGRU>(k, hpre, nullptr, log_h0, h, gh, dk, dhpre, nullptr,
+                                      dlog_h0, B, T, D, ws, ws_bytes, stream);
 }
 
 int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,

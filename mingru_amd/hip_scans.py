@@ -28,7 +28,15 @@ import weakref
 import torch
 from torch.autograd.function import once_differentiable
 
-__all__ = ["available", "ScanFallback", "SCAN_IMPLS", "angle_scan_impl", "delta_scan_impl"]
+__all__ = [
+    "available",
+    "ScanFallback",
+    "SCAN_IMPLS",
+    "angle_scan_impl",
+    "delta_scan_impl",
+    "signed_gate_scan_impl",
+    "mingru_gate_scan_impl",
+]
 
 
 class ScanFallback(Exception):
@@ -318,6 +326,65 @@ def signed_gate_scan_impl(s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor,
     if s.numel() == 0:
         return s.new_empty(s.shape)
     return _funnel("signed gate scan", _SignedGateScanFn.apply, s, z, hpre, h0, bool(coupled))
+
+
+# ---------------------------------------------------------------------------
+# fused MinGRU gates + parallel_scan_log
+# ---------------------------------------------------------------------------
+
+
+class _MinGRUGateScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, k, hpre, log_h0):
+        out_dtype = k.dtype
+        k32, hp32, lh032 = _as_f32(k, hpre, log_h0)
+        Bn, T, D = k32.shape
+        h = torch.empty_like(k32)
+        ws = _scan_workspace(_lib().mg_mingru_gate_scan_workspace_bytes(Bn, T, D), k32.device)
+        _call("mg_mingru_gate_scan_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
+              Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
+        ctx.save_for_backward(k32, hp32, lh032, h)
+        ctx.out_dtype = out_dtype
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        k32, hp32, lh032, h = ctx.saved_tensors
+        Bn, T, D = k32.shape
+        (gh32,) = _as_f32(gh)
+        dk, dhp = torch.empty_like(k32), torch.empty_like(k32)
+        dlh0 = torch.empty_like(lh032)
+        ws = _scan_workspace(_lib().mg_mingru_gate_scan_workspace_bytes(Bn, T, D), k32.device)
+        _call("mg_mingru_gate_scan_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
+              _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), Bn, T, D,
+              _ptr(ws), ws.numel(), _stream(k32))
+        od = ctx.out_dtype
+        return dk.to(od), dhp.to(od), dlh0.to(od)
+
+
+def mingru_gate_scan_impl(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor):
+    """Fused MinGRU coefficients + ``parallel_scan_log``: ``h`` (B, T, D).
+
+    No reference kernel fuses these; the arithmetic is the mixer's
+    (``src/mingru/min_gru.py:1366-1397``): ``log(1 - z) = -softplus(k)``,
+    ``log z = -softplus(-k)``, ``log h~ = log_g(hpre)`` and
+    ``h = exp(parallel_scan_log(log(1 - z), [log_h0, log z + log h~]))``, run as
+    the equivalent linear recurrence ``h_t = sigmoid(-k) h_{t-1} +
+    sigmoid(k) g(hpre)`` from ``h_0 = exp(log_h0)`` (all terms positive).
+    ``k, hpre`` are (B, T, D) pre-activations, ``log_h0`` is (B, 1, D).
+    Differentiable in all three.
+    """
+    if k.ndim != 3 or hpre.shape != k.shape or tuple(log_h0.shape) != (k.shape[0], 1, k.shape[2]):
+        raise ScanFallback(
+            f"MinGRU gate scan (k={tuple(k.shape)}, hpre={tuple(hpre.shape)}, "
+            f"log_h0={tuple(log_h0.shape)}) outside the HIP envelope: need (B, T, D) "
+            "pre-activations and a (B, 1, D) log_h0"
+        )
+    _same_device(k, hpre, log_h0)
+    if k.numel() == 0:
+        return k.new_empty(k.shape)
+    return _funnel("MinGRU gate scan", _MinGRUGateScanFn.apply, k, hpre, log_h0)
 
 
 # ---------------------------------------------------------------------------

@@ -66,6 +66,7 @@ _warned_angle_fallback = False
 _warned_delta_fallback = False
 _warned_delta_decay_fallback = False
 _warned_gate_fallback = False
+_warned_mingru_gate_fallback = False
 
 # DeltaMinGRU ``auto`` region.  The HIP chunked-WY kernel beats the eager GPU
 # loop from a handful of chunks upward at every head size of its envelope, so
@@ -252,6 +253,41 @@ def _dispatch_signed_gate_scan(
             stacklevel=3,
         )
         _warned_gate_fallback = True
+    return None
+
+
+def _dispatch_mingru_gate_scan(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor):
+    """Run MinGRU's log-space coefficients and scan as one fused kernel, or return ``None``.
+
+    The reference has no fused path here; its mixer forms ``-softplus(k)``,
+    ``-softplus(-k) + log_g(hpre)`` eagerly and calls ``parallel_scan_log``
+    (``src/mingru/min_gru.py:1366-1397``), which is what ``None`` falls back
+    to.  Mode handling as for ``_dispatch_signed_gate_scan``.  Returns ``h``
+    ``(B, T, D)``.
+    """
+    mode = _resolve_scan_mode(k.is_cuda)
+    if mode is None:
+        return None
+
+    def _call(backend):
+        status = backend.available()
+        if status is not True:
+            raise backend.ScanFallback(str(status))
+        if not hasattr(backend, "mingru_gate_scan_impl"):
+            raise backend.ScanFallback("no fused MinGRU gate kernel registered")
+        return backend.mingru_gate_scan_impl(k, hpre, log_h0)
+
+    result, reason = _resolve_native_dispatch(mode, "the fused MinGRU gate path", _call)
+    if reason is None:
+        return result
+    global _warned_mingru_gate_fallback
+    if not _warned_mingru_gate_fallback:
+        warnings.warn(
+            "MINGRU_SCAN=auto fell back to the eager MinGRU coefficients "
+            f"(fused gate path) despite CUDA inputs: {reason}",
+            stacklevel=3,
+        )
+        _warned_mingru_gate_fallback = True
     return None
 
 
@@ -628,12 +664,18 @@ class MinGRU(DecayMixin, nn.Module):
             )
             log_h_0 = h_0.clamp_min(torch.finfo(h_0.dtype).tiny).log()
         k = self.linear_z(x)
+        dt = self._prepare_decay(delta_t, canonical_ndim=2)
+        h_pre = self.linear_h(x)
+        if dt is None:
+            # Coefficients and scan in one kernel where the native backend takes it.
+            h = _dispatch_mingru_gate_scan(k, h_pre, log_h_0)
+            if h is not None:
+                return h
         log_z = -F.softplus(-k)
         log_coeffs = -F.softplus(k)
-        dt = self._prepare_decay(delta_t, canonical_ndim=2)
         if dt is not None:
             log_coeffs = log_coeffs - self._decay_lambda() * dt.unsqueeze(-1)
-        log_tilde_h = log_g(self.linear_h(x))
+        log_tilde_h = log_g(h_pre)
         return parallel_scan_log(log_coeffs, torch.cat([log_h_0, log_z + log_tilde_h], dim=1))
 
     @torch.no_grad()

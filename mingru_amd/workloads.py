@@ -46,6 +46,19 @@ def c1_inputs(B=4, T=1024, D=256):
     return dict(log_coeffs=lc, log_values=lv, grad_h=gh)
 
 
+def c1g_inputs(B=4, T=1024, D=256):
+    """MinGRU pre-activations at the C1 shape for the fused gate scan:
+    ``k, hpre ~ N(0,1)``, ``log h0 = log g(N(0,1))`` (B, 1, D), upstream
+    ``dL/dh ~ N(0,1)``; the same distributions ``c1_inputs`` forms its log
+    coefficients from."""
+    g = _gen(1011)
+    k = torch.randn(B, T, D, generator=g)
+    hpre = torch.randn(B, T, D, generator=g)
+    log_h0 = _g(torch.randn(B, 1, D, generator=g)).log()
+    gh = torch.randn(B, T, D, generator=_gen(2011))
+    return dict(k=k, hpre=hpre, log_h0=log_h0, grad_h=gh)
+
+
 def c2_inputs(B=16, T=4096, D=1024):
     """Signed coefficients ``a = tanh(2 N(0,1))``, ``b ~ N(0,1)``, ``h0 = 0``."""
     g = _gen(1002)

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 
 import mingru_amd
-from mingru_amd import DeltaMinGRU, GivensMinGRU, SignedMinGRU, hip_scans, linear_scan
+from mingru_amd import DeltaMinGRU, GivensMinGRU, MinGRU, SignedMinGRU, hip_scans, linear_scan
 from mingru_amd import min_gru as mg
 
 BACKEND = "mingru_amd.hip_scans"
@@ -35,7 +35,8 @@ class _FakeCudaTensor:
 def _isolate(monkeypatch):
     monkeypatch.delenv("MINGRU_SCAN", raising=False)
     for flag in ("_warned_scan_fallback", "_warned_angle_fallback", "_warned_delta_fallback",
-                 "_warned_delta_decay_fallback", "_warned_gate_fallback"):
+                 "_warned_delta_decay_fallback", "_warned_gate_fallback",
+                 "_warned_mingru_gate_fallback"):
         monkeypatch.setattr(mg, flag, False)
 
 
@@ -352,6 +353,82 @@ def test_signed_gate_auto_fallback_warns_once_and_runs_eager(monkeypatch):
     monkeypatch.setenv("MINGRU_SCAN", "hip")
     with pytest.raises(RuntimeError, match="declined by the fake backend"):
         mg._dispatch_signed_gate_scan(f, f, f, f, coupled=False)
+
+
+def test_mingru_gate_seam_hands_preactivations_to_backend(monkeypatch):
+    """MinGRU's fused path passes the (k, hpre) pre-activations and log h0 = log 0.5
+    (B, 1, D), and returns the backend's h unchanged."""
+    seen = {}
+
+    def fake_gate(k, hpre, log_h0):
+        seen.update(k=tuple(k.shape), hpre=tuple(hpre.shape), log_h0=log_h0.clone())
+        return torch.full(k.shape, 3.0)
+
+    _fake_backend(monkeypatch, mingru_gate_scan_impl=fake_gate)
+    m = MinGRU(5, 6)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    x = torch.randn(2, 9, 5)
+    y = m(x)
+    assert seen["k"] == seen["hpre"] == (2, 9, 6)
+    assert torch.allclose(seen["log_h0"], torch.full((2, 1, 6), 0.5).log())
+    assert torch.equal(y, torch.full((2, 9, 6), 3.0))
+
+
+def test_mingru_gate_seam_skips_fusion_under_decay(monkeypatch):
+    """With decay log(1 - z) carries -lambda dt: no fused call, the parallel_scan_log
+    seam runs instead."""
+    calls = []
+
+    def fake_gate(*args, **kwargs):
+        calls.append("gate")
+        raise AssertionError("fused path must not run under decay")
+
+    def fake_log(lc, lv):
+        calls.append("parallel_scan_log")
+        return torch.zeros_like(lc)
+
+    _fake_backend(monkeypatch, mingru_gate_scan_impl=fake_gate,
+                  SCAN_IMPLS={"parallel_scan_log": fake_log})
+    m = MinGRU(4, 5, decay="fixed")
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m(torch.randn(2, 6, 4), delta_t=torch.rand(2, 6))
+    assert calls == ["parallel_scan_log"]
+
+
+def test_mingru_gate_auto_fallback_warns_once_and_runs_eager(monkeypatch):
+    def fake_gate(*args, **kwargs):
+        raise sys.modules[BACKEND].ScanFallback("declined by the fake backend")
+
+    _fake_backend(monkeypatch, mingru_gate_scan_impl=fake_gate)
+    f = _FakeCudaTensor()
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    with pytest.warns(UserWarning, match="MinGRU coefficients"):
+        assert mg._dispatch_mingru_gate_scan(f, f, f) is None
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert mg._dispatch_mingru_gate_scan(f, f, f) is None
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with pytest.raises(RuntimeError, match="declined by the fake backend"):
+        mg._dispatch_mingru_gate_scan(f, f, f)
+
+
+def test_mingru_linear_recurrence_equals_log_space_forward():
+    """The linear recurrence the fused kernel runs, h_t = sigmoid(-k) h_{t-1} +
+    sigmoid(k) g(hpre) from h_0 = exp(log h0), equals the log-space forward
+    (reference ``src/mingru/min_gru.py:1366-1397``) in float64, incl. a learned h0."""
+    torch.manual_seed(3)
+    m = MinGRU(4, 6, learnable_h0=True).double()
+    with torch.no_grad():
+        m.h0_pre.normal_()
+    x = torch.randn(2, 11, 4, dtype=torch.float64) * 3
+    ref = m(x)
+    k, hpre = m.linear_z(x), m.linear_h(x)
+    h = mg.g(m.h0_pre).expand(2, 1, 6)[:, 0]
+    out = []
+    for t in range(x.shape[1]):
+        h = torch.sigmoid(-k[:, t]) * h + torch.sigmoid(k[:, t]) * mg.g(hpre[:, t])
+        out.append(h)
+    assert torch.allclose(torch.stack(out, 1), ref, rtol=1e-12, atol=1e-12)
 
 
 def test_delta_module_forward_equals_step_recurrence():
