@@ -170,6 +170,29 @@ struct Tile {
       }
     }
   }
+
+  // Sum over this thread's elements of e * s[row * LD + col], at the positions
+  // store() writes them to.
+  __device__ __forceinline__ float dot(const float* s) const {
+    const TI* e = reinterpret_cast<const TI*>(q);
+    float acc = 0.f;
+    if (vec) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = threadIdx.x + v * NT;
+        const int row = idx / VPR, col = (idx % VPR) * EPV;
+#pragma unroll
+        for (int x = 0; x < EPV; ++x) acc = fmaf(tof(e[v * EPV + x]), s[row * LD + col + x], acc);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        acc = fmaf(tof(e[k]), s[(idx >> 6) * LD + (idx & 63)], acc);
+      }
+    }
+    return acc;
+  }
 };
 
 // Chain workgroup -> (head, d_v slice).  Workgroups are dispatched round-robin

@@ -34,6 +34,7 @@ __all__ = [
     "SCAN_IMPLS",
     "angle_scan_impl",
     "delta_scan_impl",
+    "delta_gated_scan_impl",
     "signed_gate_scan_impl",
     "mingru_gate_scan_impl",
 ]
@@ -822,6 +823,83 @@ def delta_scan_impl(Q, K, V, beta, H0, *, chunk_size: int):
         return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
     return _funnel("DeltaMinGRU chunked-WY", _DeltaScanFn.apply, Q, K, V, beta, H0,
                    int(chunk_size))
+
+
+# ---------------------------------------------------------------------------
+# DeltaMinGRU decay-gated chunked-WY
+# ---------------------------------------------------------------------------
+
+
+class _DeltaGatedScanFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, K, V, beta, log_gamma, H0, chunk_size):
+        q, k, v, bt, lg, h0 = (_contig(t, torch.float32) for t in (Q, K, V, beta, log_gamma, H0))
+        Bn, nhd, T, d_k = q.shape
+        nh = k.shape[3]
+        d_v = v.shape[4]
+        lib = _lib()
+        dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
+        y = torch.empty(Bn, nhd, T, d_v, dtype=torch.float32, device=q.device)
+        HT = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+        Hb = torch.empty(max(int(lib.mg_delta_state_bytes(*dims)), 16) // 4, dtype=torch.float32,
+                         device=q.device)
+        ws = _workspace(lib.mg_delta_gated_workspace_bytes(*dims), q.device)
+        _call("mg_delta_gated_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(h0),
+              _ptr(y), _ptr(HT), _ptr(Hb), *dims, _ptr(ws), ws.numel(), _stream(q))
+        ctx.save_for_backward(q, k, v, bt, lg, Hb)
+        ctx.meta = (chunk_size, Q.dtype, K.dtype, V.dtype, beta.dtype, log_gamma.dtype, H0.dtype)
+        return y.to(Q.dtype), HT.to(H0.dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gy, gHT):
+        q, k, v, bt, lg, Hb = ctx.saved_tensors
+        chunk_size, qdt, kdt, vdt, bdt, ldt, hdt = ctx.meta
+        Bn, nhd, T, d_k = q.shape
+        nh = k.shape[3]
+        d_v = v.shape[4]
+        dy = (torch.zeros(Bn, nhd, T, d_v, dtype=torch.float32, device=q.device) if gy is None
+              else _contig(gy, torch.float32))
+        dHT = (torch.zeros(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+               if gHT is None else _contig(gHT, torch.float32))
+        dQ, dK, dV, dbeta, dlg = (torch.empty_like(t) for t in (q, k, v, bt, lg))
+        dH0 = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
+        dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
+        ws = _workspace(_lib().mg_delta_gated_workspace_bytes(*dims), q.device)
+        _call("mg_delta_gated_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(Hb),
+              _ptr(dy), _ptr(dHT), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dbeta), _ptr(dlg),
+              _ptr(dH0), *dims, _ptr(ws), ws.numel(), _stream(q))
+        return (dQ.to(qdt), dK.to(kdt), dV.to(vdt), dbeta.to(bdt), dlg.to(ldt), dH0.to(hdt),
+                None)
+
+
+def delta_gated_scan_impl(Q, K, V, beta, log_gamma, H0, *, chunk_size: int):
+    """DeltaMinGRU decay-active chunked-WY forward; returns ``(y, H_T)``.
+
+    No reference kernel: the reference runs this eagerly
+    (``_forward_chunked_gated``, ``src/mingru/min_gru.py:3257-3448``).  Layouts
+    as ``delta_scan_impl`` plus ``log_gamma`` ``(B, n_heads, T)``, the per-token
+    log decay applied to the state before the token's micro-steps.  The kernels
+    compute in fp32 (half inputs are upcast); ``y`` comes back in Q's dtype and
+    ``H_T`` in H0's.  Differentiable in all six tensors.
+    """
+    _delta_validate_envelope(Q, K, V, beta, H0, chunk_size)
+    if tuple(log_gamma.shape) != tuple(Q.shape[:3]):
+        raise ScanFallback(
+            f"DeltaMinGRU gated kernel needs log_gamma of shape (B, n_heads, T)="
+            f"{tuple(Q.shape[:3])} (got {tuple(log_gamma.shape)})"
+        )
+    if log_gamma.dtype not in _DELTA_DTYPES or not log_gamma.is_cuda:
+        raise ScanFallback(
+            "DeltaMinGRU gated kernel needs a float32, bfloat16 or float16 GPU log_gamma "
+            f"(got {log_gamma.dtype} on {log_gamma.device})"
+        )
+    if log_gamma.device != Q.device:
+        raise ScanFallback("DeltaMinGRU gated kernel inputs live on different devices")
+    if Q.shape[2] == 0:
+        return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
+    return _funnel("DeltaMinGRU gated chunked-WY", _DeltaGatedScanFn.apply, Q, K, V, beta,
+                   log_gamma, H0, int(chunk_size))
 
 
 SCAN_IMPLS: dict = {

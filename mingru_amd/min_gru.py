@@ -357,29 +357,58 @@ def _dispatch_delta_scan(
     return None
 
 
-def _delta_decay_dispatch_guard(is_cuda: bool) -> None:
-    """``MINGRU_SCAN`` contract for DeltaMinGRU's decay-active forward (no kernel).
+def _dispatch_delta_gated_scan(
+    q: torch.Tensor,
+    ks: list[torch.Tensor],
+    vs: list[torch.Tensor],
+    betas: list[torch.Tensor],
+    log_gamma: torch.Tensor,
+    H: torch.Tensor,
+    *,
+    chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor] | None:
+    """Run DeltaMinGRU's decay-active forward on the gated chunked-WY kernel, or
+    return ``None`` for the eager ``_forward_chunked_gated``.
 
-    Reference ``src/mingru/min_gru.py:612-668``: the forcing mode raises,
-    CUDA ``auto`` warns once and runs eager, everything else runs eager
-    silently.
+    The reference has no kernel here; its guard (``src/mingru/min_gru.py:612-668``)
+    raises under the forcing mode and warns once under CUDA ``auto``.  This seam
+    keeps that contract for a backend that declines: the forcing mode raises, CUDA
+    ``auto`` warns once and runs eager, ``eager`` and CPU ``auto`` run eager
+    silently.  Layouts as ``_dispatch_delta_scan``, plus ``log_gamma``
+    ``(B, n_heads, T)`` (``log gamma_t = -lambda f(dt_t)`` per head and token).
     """
-    mode = _resolve_scan_mode(is_cuda)
+    mode = _resolve_scan_mode(q.is_cuda)
     if mode is None:
-        return
-    if mode != "auto":
-        raise RuntimeError(
-            f"MINGRU_SCAN={mode} requested for DeltaMinGRU's decay-active forward, but decay "
-            "has no HIP kernel; run it with MINGRU_SCAN=auto or eager"
-        )
+        return None
+
+    def _call(backend):
+        status = backend.available()
+        if status is not True:
+            raise backend.ScanFallback(str(status))
+        if not hasattr(backend, "delta_gated_scan_impl"):
+            raise backend.ScanFallback("decay has no HIP kernel registered")
+        K = torch.stack(ks, dim=2).permute(0, 3, 1, 2, 4)
+        V = torch.stack(vs, dim=2).permute(0, 3, 1, 2, 4)
+        beta = torch.stack(betas, dim=2).permute(0, 3, 1, 2)
+        Q = q.permute(0, 2, 1, 3)
+        y, H_T = backend.delta_gated_scan_impl(Q, K, V, beta, log_gamma, H,
+                                               chunk_size=chunk_size)
+        return y.permute(0, 2, 1, 3), H_T
+
+    result, reason = _resolve_native_dispatch(
+        mode, "DeltaMinGRU's decay-active forward (gated chunked-WY path)", _call
+    )
+    if reason is None:
+        return result
     global _warned_delta_decay_fallback
     if not _warned_delta_decay_fallback:
         warnings.warn(
             "MINGRU_SCAN=auto is running DeltaMinGRU's decay-active forward eagerly on CUDA "
-            "input: decay has no HIP kernel.",
+            f"input: {reason}",
             stacklevel=3,
         )
         _warned_delta_decay_fallback = True
+    return None
 
 
 def _cached_plane_meta_per_device(obj, attr: str, device: torch.device, build):
@@ -1222,8 +1251,8 @@ class DeltaMinGRU(DecayMixin, nn.Module):
             y = x.new_zeros(B, 0, self.n_heads * self.d_v)
             H = H.clone()
         elif dt is not None:
-            _delta_decay_dispatch_guard(x.is_cuda)
-            y, H = self._forward_chunked_gated(x, H, dt)
+            fused = self._delta_gated_fused_forward(x, H, dt)
+            y, H = fused if fused is not None else self._forward_chunked_gated(x, H, dt)
         else:
             fused = self._delta_fused_forward(x, H)
             y, H = fused if fused is not None else self._forward_chunked(x, H)
@@ -1231,6 +1260,20 @@ class DeltaMinGRU(DecayMixin, nn.Module):
         if return_state:
             return y, H.reshape(*expected)
         return y
+
+    def _delta_gated_fused_forward(self, x, H, dt):
+        if not _delta_scan_should_try(
+            x.is_cuda, T=x.shape[1], chunk_size=self.chunk_size, d_k=self.d_k
+        ):
+            return None
+        q, ks, vs, betas = self._coeffs(x)
+        B, T = dt.shape
+        # lambda is per head ("learnable") or one value ("fixed"): (B, n_heads, T) either way.
+        log_gamma = (-self._decay_lambda().reshape(1, -1, 1) * dt.unsqueeze(1)).expand(
+            B, self.n_heads, T
+        )
+        return _dispatch_delta_gated_scan(q, ks, vs, betas, log_gamma, H,
+                                          chunk_size=self.chunk_size)
 
     def _delta_fused_forward(self, x, H):
         if not _delta_scan_should_try(

@@ -28,6 +28,11 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``src/mingru/triton_scans.py:473-605``; pinned by the reference golden
   fixture (``tests/golden/``), sequential == chunked for every chunk size,
   and finite differences.
+* delta_gated_sequential / _bwd -- the decay-active delta rule of ``step``
+  (``src/mingru/min_gru.py:3611-3688``: decay the state, then the token's
+  micro-steps); pinned by log_gamma = 0 == delta_sequential, the beta = 0
+  closed form, the module's span-sum chunked forward (reference structure
+  ``:3257-3448``) in float64, and finite differences.
 """
 
 from __future__ import annotations
@@ -431,3 +436,73 @@ def delta_chunked_bwd(Q, K, V, beta, H0, chunk_size, dy, dHT):
         dbeta[:, :, s:e] = db_loc.reshape(Bn, nhd, C, nh)
         dH = dHc
     return dQ, dK, dV, dbeta, dH
+
+
+def delta_gated_sequential(Q, K, V, beta, log_gamma, H0, return_states=False):
+    """Decay-active delta rule, token by token (reference ``step``, ``:3611-3688``).
+
+    Per token ``t``: ``H <- exp(log_gamma[..., t]) H``, then the ``nh`` micro-steps
+    ``H <- H + beta k (v - H^T k)^T``, then ``y_t = H^T q_t``.  Layouts as
+    ``delta_sequential`` plus ``log_gamma`` ``(B,h,T)``.  Returns ``y``, ``H_T``
+    (and, with ``return_states``, the state before every token's decay,
+    ``(B,h,T,dk,dv)``).
+    """
+    Q, K, V, beta, lg = (np.asarray(x, np.float64) for x in (Q, K, V, beta, log_gamma))
+    H = np.asarray(H0, np.float64).copy()
+    T = Q.shape[2]
+    nh = K.shape[3]
+    y = np.empty(V.shape[:3] + (V.shape[-1],))
+    states = np.empty(H.shape[:2] + (T,) + H.shape[2:]) if return_states else None
+    for t in range(T):
+        if return_states:
+            states[:, :, t] = H
+        H = np.exp(lg[:, :, t])[..., None, None] * H
+        for j in range(nh):
+            k = K[:, :, t, j]
+            bt = beta[:, :, t, j][..., None, None]
+            u = V[:, :, t, j] - np.einsum("bhk,bhkv->bhv", k, H)
+            H = H + bt * np.einsum("bhk,bhv->bhkv", k, u)
+        y[:, :, t] = np.einsum("bhk,bhkv->bhv", Q[:, :, t], H)
+    return (y, H, states) if return_states else (y, H)
+
+
+def delta_gated_sequential_bwd(Q, K, V, beta, log_gamma, H0, dy, dHT):
+    """Adjoint of ``delta_gated_sequential``: ``(dQ, dK, dV, dbeta, dlog_gamma, dH0)``.
+
+    Reverse over tokens: ``dH += q_t dy_t^T`` (``dq_t = H_t dy_t``), then the
+    micro-steps in reverse, with ``H' = H + beta k u^T``, ``u = v - H^T k``:
+    ``dv = beta dH'^T k``, ``dbeta = k^T dH' u``,
+    ``dk = beta (dH' u - H dH'^T k)``, ``dH = dH' - beta k (k^T dH')``; then the
+    decay: ``dlog_gamma_t = gamma_t <dH, H_{t-1}>``, ``dH_{t-1} = gamma_t dH``.
+    """
+    Q, K, V, beta, lg, dy, dHT = (np.asarray(x, np.float64)
+                                  for x in (Q, K, V, beta, log_gamma, dy, dHT))
+    _, _, states = delta_gated_sequential(Q, K, V, beta, lg, H0, return_states=True)
+    T = Q.shape[2]
+    nh = K.shape[3]
+    dQ, dK, dV, dbeta, dlg = (np.zeros_like(x) for x in (Q, K, V, beta, lg))
+    dH = dHT.copy()
+    for t in range(T - 1, -1, -1):
+        g = np.exp(lg[:, :, t])[..., None, None]
+        # Recompute the token's micro-step inputs from the state before its decay.
+        Hs = [g * states[:, :, t]]
+        for j in range(nh):
+            k = K[:, :, t, j]
+            u = V[:, :, t, j] - np.einsum("bhk,bhkv->bhv", k, Hs[-1])
+            Hs.append(Hs[-1] + beta[:, :, t, j][..., None, None] * np.einsum("bhk,bhv->bhkv", k, u))
+        dQ[:, :, t] = np.einsum("bhkv,bhv->bhk", Hs[-1], dy[:, :, t])
+        dH = dH + np.einsum("bhk,bhv->bhkv", Q[:, :, t], dy[:, :, t])
+        for j in range(nh - 1, -1, -1):
+            H = Hs[j]
+            k = K[:, :, t, j]
+            bt = beta[:, :, t, j]
+            u = V[:, :, t, j] - np.einsum("bhk,bhkv->bhv", k, H)
+            dHk = np.einsum("bhkv,bhk->bhv", dH, k)  # dH'^T k
+            dV[:, :, t, j] = bt[..., None] * dHk
+            dbeta[:, :, t, j] = np.einsum("bhv,bhv->bh", dHk, u)
+            dK[:, :, t, j] = bt[..., None] * (np.einsum("bhkv,bhv->bhk", dH, u)
+                                              - np.einsum("bhkv,bhv->bhk", H, dHk))
+            dH = dH - bt[..., None, None] * np.einsum("bhk,bhv->bhkv", k, dHk)
+        dlg[:, :, t] = g[..., 0, 0] * np.einsum("bhkv,bhkv->bh", dH, states[:, :, t])
+        dH = g * dH
+    return dQ, dK, dV, dbeta, dlg, dH

@@ -133,17 +133,51 @@ def test_delta_auto_region_gate(monkeypatch):
     assert not mg._delta_scan_should_try(True, T=4096, chunk_size=64, d_k=64)
 
 
-def test_delta_decay_guard(monkeypatch):
+def test_delta_decay_seam_keeps_the_reference_guard_contract(monkeypatch):
+    """A backend without the gated kernel declines: the forcing mode raises, CUDA
+    ``auto`` warns once and runs eager, CPU ``auto`` stays silent (reference
+    ``_delta_decay_dispatch_guard``, ``src/mingru/min_gru.py:612-668``)."""
+    _fake_backend(monkeypatch)
+    f = _FakeCudaTensor()
     monkeypatch.setenv("MINGRU_SCAN", "hip")
     with pytest.raises(RuntimeError, match="decay"):
-        mg._delta_decay_dispatch_guard(True)
+        mg._dispatch_delta_gated_scan(f, [f], [f], [f], f, f, chunk_size=4)
     monkeypatch.setenv("MINGRU_SCAN", "auto")
     with pytest.warns(UserWarning, match="decay"):
-        mg._delta_decay_dispatch_guard(True)
+        assert mg._dispatch_delta_gated_scan(f, [f], [f], [f], f, f, chunk_size=4) is None
     with warnings.catch_warnings():
         warnings.simplefilter("error")
-        mg._delta_decay_dispatch_guard(True)
-        mg._delta_decay_dispatch_guard(False)
+        assert mg._dispatch_delta_gated_scan(f, [f], [f], [f], f, f, chunk_size=4) is None
+        c = torch.zeros(1)
+        assert mg._dispatch_delta_gated_scan(c, [c], [c], [c], c, c, chunk_size=4) is None
+
+
+def test_delta_decay_seam_hands_gated_layouts_to_backend(monkeypatch):
+    """DeltaMinGRU with decay passes the kernel layouts plus log_gamma = -lambda dt
+    (B, n_heads, T) to ``delta_gated_scan_impl`` and maps its y back through out_proj."""
+    seen = {}
+
+    def fake_gated(Q, K, V, beta, log_gamma, H0, *, chunk_size):
+        seen.update(Q=tuple(Q.shape), K=tuple(K.shape), V=tuple(V.shape),
+                    beta=tuple(beta.shape), lg=log_gamma.detach().clone(), H0=tuple(H0.shape),
+                    chunk=chunk_size)
+        return torch.zeros(Q.shape[:3] + (V.shape[-1],)), H0 + 1.0
+
+    _fake_backend(monkeypatch, delta_gated_scan_impl=fake_gated)
+    m = DeltaMinGRU(6, 12, n_heads=3, nh=2, chunk_size=5, decay="fixed", decay_rate=0.7)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    x = torch.randn(2, 9, 6)
+    dt = torch.rand(2, 9)
+    y, HT = m(x, delta_t=dt, return_state=True)
+    assert seen["Q"] == (2, 3, 9, 4) and seen["K"] == (2, 3, 9, 2, 4)
+    assert seen["V"] == (2, 3, 9, 2, 4) and seen["beta"] == (2, 3, 9, 2)
+    assert seen["H0"] == (2, 3, 4, 4) and seen["chunk"] == 5
+    lam = m._decay_lambda().reshape(1, -1, 1)  # one value under decay="fixed"
+    assert seen["lg"].shape == (2, 3, 9)
+    assert torch.allclose(seen["lg"], (-lam * dt.unsqueeze(1)).expand(2, 3, 9))
+    with torch.no_grad():
+        assert torch.allclose(y, m.out_proj(torch.zeros(2, 9, 12)))
+    assert torch.equal(HT, torch.ones(2, 1, 48))
 
 
 # ---------------------------------------------------------------- backend envelope

@@ -343,3 +343,68 @@ def test_delta_golden_fixture():
     # golden output gradient: loss = output.sum(), so dL/d(out_proj.bias) = B*T
     np.testing.assert_allclose(np.asarray(fx["param_grads"]["out_proj.bias"]), B * T, atol=1e-4)
     assert math.isfinite(float(np.sum(out)))
+
+
+# -------------------------------------------------------- gated delta rule
+
+
+def _gated_lg(B=2, H=2, T=11, seed=5, scale=0.6):
+    return -scale * np.random.default_rng(seed).random(size=(B, H, T))
+
+
+def test_delta_gated_zero_decay_is_the_ungated_rule():
+    """log gamma = 0: the gated recurrence is the golden-pinned ungated one."""
+    Q, K, V, beta, H0 = _delta_inputs(nh=2)
+    y0, H0T = orc.delta_sequential(Q, K, V, beta, H0)
+    y, HT = orc.delta_gated_sequential(Q, K, V, beta, np.zeros(Q.shape[:3]), H0)
+    np.testing.assert_allclose(y, y0, atol=1e-13)
+    np.testing.assert_allclose(HT, H0T, atol=1e-13)
+
+
+def test_delta_gated_beta_zero_is_pure_decay():
+    """beta = 0: H_t = exp(sum_{s<=t} l_s) H0 and y_t = H_t^T q_t in closed form."""
+    Q, K, V, beta, H0 = _delta_inputs(T=7)
+    beta[:] = 0.0
+    lg = _gated_lg(T=7)
+    y, HT = orc.delta_gated_sequential(Q, K, V, beta, lg, H0)
+    G = np.exp(np.cumsum(lg, axis=-1))
+    np.testing.assert_allclose(HT, G[..., -1, None, None] * H0, atol=1e-13)
+    ref = G[..., None] * np.einsum("bhtk,bhkv->bhtv", Q, H0)
+    np.testing.assert_allclose(y, ref, atol=1e-13)
+
+
+@pytest.mark.parametrize("nh,chunk", [(1, 4), (2, 3), (1, 16), (3, 5)])
+def test_delta_gated_matches_module_span_sum_forward(nh, chunk):
+    """The module's eager decay-active forward (span-sum chunked form of the
+    reference ``_forward_chunked_gated``) equals the token-by-token oracle in float64."""
+    from mingru_amd import DeltaMinGRU
+
+    torch.manual_seed(nh * 10 + chunk)
+    m = DeltaMinGRU(5, 8, n_heads=2, nh=nh, chunk_size=chunk, decay="learnable").double()
+    x = torch.randn(2, 13, 5, dtype=torch.float64)
+    dt = torch.rand(2, 13, dtype=torch.float64) * 2
+    dt[:, 4] = 40.0  # one gap that drives gamma to ~0 for every span containing it
+    with torch.no_grad():
+        y, HT = m(x, delta_t=dt, return_state=True)
+        q, ks, vs, betas = m._coeffs(x)
+        Q, K, V, beta = (t.numpy() for t in m._layouts(q, ks, vs, betas))
+        lg = (-m._decay_lambda().reshape(1, -1, 1) * dt.unsqueeze(1)).numpy()
+    yo, HTo = orc.delta_gated_sequential(Q, K, V, beta, lg, np.zeros((2, 2, 4, 4)))
+    with torch.no_grad():
+        ref = m.out_proj(torch.from_numpy(yo).permute(0, 2, 1, 3).reshape(2, 13, 8))
+    np.testing.assert_allclose(y.numpy(), ref.numpy(), atol=1e-11)
+    np.testing.assert_allclose(HT.numpy().reshape(HTo.shape), HTo, atol=1e-11)
+
+
+@pytest.mark.parametrize("nh", [1, 2])
+def test_delta_gated_bwd_finite_differences(nh):
+    Q, K, V, beta, H0 = _delta_inputs(T=8, nh=nh, seed=7)
+    lg = _gated_lg(T=8, seed=8)
+    r = np.random.default_rng(10)
+    dy = r.normal(size=(2, 2, 8, 3))
+    dHT = r.normal(size=(2, 2, 4, 3))
+    grads = orc.delta_gated_sequential_bwd(Q, K, V, beta, lg, H0, dy, dHT)
+    args = (Q, K, V, beta, lg, H0)
+    for idx, grad in enumerate(grads):
+        probes, fd = _fd(orc.delta_gated_sequential, args, idx, (dy, dHT))
+        np.testing.assert_allclose(grad.reshape(-1)[probes], fd, rtol=1e-6, atol=1e-7)
