@@ -34,6 +34,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 (the delta kernels' MFMA type at C5)
+MFMA_FP32_PEAK_TFLOPS = 157.3  # dense fp32 (the gated delta kernels' MFMA type)
 HEADLINE = "C2"  # the workload BASELINE.json's metric is quoted on
 
 METRIC = "fwd+bwd tokens/s + achieved HBM TB/s (% of peak) per scan op, 1 MI355X"
@@ -74,8 +75,9 @@ class Op:
     """One benchmark workload: input builder, one fwd+bwd step, byte (or FLOP) accounting."""
 
     def __init__(self, key, workload, tokens, fwd_entry, bwd_entry, fwd_bytes, bwd_bytes,
-                 fwd_flops=None, bwd_flops=None):
+                 fwd_flops=None, bwd_flops=None, mfma=("bf16", MFMA_BF16_PEAK_TFLOPS)):
         self.key = key
+        self.mfma = mfma  # (operand type, dense peak TFLOP/s) the FLOP figures are priced at
         self.workload = workload
         self.tokens = tokens
         self.fwd_entry = fwd_entry
@@ -136,6 +138,14 @@ def build_ops(torch, wl):
     ops["C5"] = Op("C5", "C5 DeltaMinGRU chunked-WY fwd+bwd (bf16 in, fp32 state)",
                    c["B"] * c["T"], "mg_delta_fwd", "mg_delta_bwd",
                    4 * bt + bt // c["d"], 7 * bt + 2 * bt // c["d"], f_fwd, 2 * f_fwd)
+    # C5d: C5 with per-token decay on the gated kernels (fp32 in and out).  Bytes: Q, K, V
+    # read and y written forward, plus beta and log_gamma; backward reads Q, K, V, dy, beta,
+    # log_gamma and writes dQ, dK, dV, dbeta, dlog_gamma.  Same FLOP floor as C5.
+    bt32 = 2 * bt
+    ops["C5d"] = Op("C5d", "C5d DeltaMinGRU decay-gated chunked-WY fwd+bwd (C5 shape, fp32)",
+                    c["B"] * c["T"], "mg_delta_gated_fwd", "mg_delta_gated_bwd",
+                    4 * bt32 + 2 * bt32 // c["d"], 7 * bt32 + 4 * bt32 // c["d"], f_fwd,
+                    2 * f_fwd, mfma=("fp32", MFMA_FP32_PEAK_TFLOPS))
     return ops
 
 
@@ -270,6 +280,21 @@ def make_step(key, torch, wl, dev):
                                               inp["grad_HT"][:bs]))
 
         return step, cpu, wl.C5["B"]
+    if key == "C5d":
+        from mingru_amd import hip_scans
+
+        inp = wl.c5d_inputs(**wl.C5)
+        names = ("Q", "K", "V", "beta", "log_gamma", "H0")
+        xs = [inp[k].to(dev).requires_grad_(True) for k in names]
+        gy = inp["grad_y"].to(dev)
+        gH = inp["grad_HT"].to(dev)
+        C = inp["chunk_size"]
+
+        def step():
+            y, HT = hip_scans.delta_gated_scan_impl(*xs, chunk_size=C)
+            return torch.autograd.grad((y, HT), xs, (gy, gH))
+
+        return step, None, wl.C5["B"]
     raise KeyError(key)
 
 
@@ -326,6 +351,33 @@ def delta_eager_gpu_ms(torch, wl, dev, reps=3):
 
     def step():
         y, HT = delta_chunked_eager(*xs, inp["chunk_size"])
+        torch.autograd.grad((y, HT), xs, (gy, gH))
+
+    step()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def delta_gated_eager_gpu_ms(torch, wl, dev, reps=3):
+    """The eager decay-gated chunked-WY loop (the module's ``_forward_chunked_gated``,
+    torch ops on the GPU, fp32) fwd+bwd at C5d; returns the median ms per step."""
+    from mingru_amd.min_gru import delta_chunked_gated_eager
+
+    inp = wl.c5d_inputs(**wl.C5)
+    names = ("Q", "K", "V", "beta", "log_gamma", "H0")
+    xs = [inp[k].to(dev).requires_grad_(True) for k in names]
+    gy = inp["grad_y"].to(dev).permute(0, 2, 1, 3)
+    gH = inp["grad_HT"].to(dev)
+
+    def step():
+        y, HT = delta_chunked_gated_eager(*xs, inp["chunk_size"])
         torch.autograd.grad((y, HT), xs, (gy, gH))
 
     step()
@@ -398,7 +450,7 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans, headline=False):
         fl = op.fwd_flops + op.bwd_flops
         res["algorithmic_flops"] = fl
         res["achieved_TFLOPs"] = fl / (ms * 1e-3) / 1e12
-        res["frac_of_bf16_mfma_peak"] = res["achieved_TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+        res[f"frac_of_{op.mfma[0]}_mfma_peak"] = res["achieved_TFLOPs"] / op.mfma[1]
     return res, cpu_step, B
 
 
@@ -495,7 +547,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C2g", "C1", "C1g", "C3", "C3m", "C4", "C5"]
+    order = ["C2", "C2g", "C1", "C1g", "C3", "C3m", "C4", "C5", "C5d"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -520,8 +572,8 @@ def main():
             print(f"#   unfused (eager gates + HIP {scan}): {uf:.3f} ms/step "
                   f"({res['speedup_vs_unfused']:.2f}x the fused time)", file=sys.stderr,
                   flush=True)
-        if key == "C5" and not args.no_eager:
-            eg = delta_eager_gpu_ms(torch, wl, dev)
+        if key in ("C5", "C5d") and not args.no_eager:
+            eg = (delta_eager_gpu_ms if key == "C5" else delta_gated_eager_gpu_ms)(torch, wl, dev)
             res["eager_gpu_ms_per_step"] = eg
             res["speedup_vs_eager_gpu"] = eg / res["ms_per_step"]
             print(f"#   eager GPU chunked-WY: {eg:.2f} ms/step "
@@ -572,7 +624,7 @@ def main():
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
         "config": {"workload": op.workload, **{"C1": wl.C1, "C1g": wl.C1, "C2": wl.C2, "C2g": wl.C2,
                                                "C3": wl.C3, "C3m": wl.C3, "C4": wl.C4,
-                                               "C5": wl.C5}.get(head_key, {})},
+                                               "C5": wl.C5, "C5d": wl.C5}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "achieved_TBs": head["achieved_TBs"],

@@ -1183,8 +1183,6 @@ class DeltaMinGRU(DecayMixin, nn.Module):
 
     def _forward_chunked_gated(self, x, H, dt):
         """Decay-gated chunked-WY forward with span-sum factors (reference ``:3257-3448``)."""
-        B, T, _ = x.shape
-        nh = self.nh
         q, ks, vs, betas = self._coeffs(x)
         Q_all, K_all, V_all, beta_all = self._layouts(q, ks, vs, betas)
         lam = self._decay_lambda()
@@ -1202,38 +1200,8 @@ class DeltaMinGRU(DecayMixin, nn.Module):
                 stacklevel=2,
             )
             self._warned_fp32_decay_saturation = True
-        n_heads, d_k, d_v = self.n_heads, self.d_k, self.d_v
-        ys = []
-        for s in range(0, T, self.chunk_size):
-            e = min(s + self.chunk_size, T)
-            C = e - s
-            M = nh * C
-            K = K_all[:, :, s:e].reshape(B, n_heads, M, d_k)
-            V = V_all[:, :, s:e].reshape(B, n_heads, M, d_v)
-            beta = beta_all[:, :, s:e].reshape(B, n_heads, M)
-            Q = Q_all[:, :, s:e]
-            span, logP = self._span_log_decay(log_gamma[:, :, s:e])
-            span_cm = span.repeat_interleave(nh, dim=-1)
-            span_mm = span_cm.repeat_interleave(nh, dim=-2)
-            P_tok = torch.exp(logP)
-            P_micro = P_tok.repeat_interleave(nh, dim=-1)
-            strict = torch.tril(K.new_ones(M, M), diagonal=-1)
-            eye = torch.eye(M, dtype=K.dtype, device=K.device)
-            dec_lower = torch.exp(span_mm.masked_fill(strict == 0, float("-inf")))
-            T_mat = eye + (K @ K.transpose(-1, -2)) * beta.unsqueeze(-2) * dec_lower
-            U = torch.linalg.solve_triangular(
-                T_mat, V - P_micro.unsqueeze(-1) * (K @ H), upper=False, unitriangular=True
-            )
-            read = torch.tril(Q.new_ones(C, C)).repeat_interleave(nh, dim=1)
-            dec_read = torch.exp(span_cm.masked_fill(read == 0, float("-inf")))
-            y = P_tok.unsqueeze(-1) * (Q @ H) + (
-                (Q @ K.transpose(-1, -2)) * beta.unsqueeze(-2) * dec_read
-            ) @ U
-            carry = torch.exp(span_cm[:, :, -1, :])
-            P_C = P_tok[:, :, -1].unsqueeze(-1).unsqueeze(-1)
-            H = P_C * H + K.transpose(-1, -2) @ ((carry * beta).unsqueeze(-1) * U)
-            ys.append(y)
-        return torch.cat(ys, dim=2).permute(0, 2, 1, 3), H
+        return delta_chunked_gated_eager(Q_all, K_all, V_all, beta_all, log_gamma, H,
+                                         self.chunk_size)
 
     def forward(self, x, h_0=None, delta_t=None, return_state=False):
         delta_t = _match_delta_t_dtype(delta_t, self)
@@ -1339,6 +1307,51 @@ def delta_chunked_eager(Q, K, V, beta, H, chunk_size):
         read = torch.tril(Qc.new_ones(C, C)).repeat_interleave(nh, dim=1)
         y = Qc @ H + ((Qc @ Kc.transpose(-1, -2)) * bc.unsqueeze(-2) * read) @ U
         H = H + Kc.transpose(-1, -2) @ (bc.unsqueeze(-1) * U)
+        ys.append(y)
+    return torch.cat(ys, dim=2).permute(0, 2, 1, 3), H
+
+
+def delta_chunked_gated_eager(Q_all, K_all, V_all, beta_all, log_gamma, H, chunk_size):
+    """Decay-gated chunked-WY delta rule on the kernel layouts (eager, any device/dtype).
+
+    Layouts as ``delta_chunked_eager`` plus ``log_gamma`` ``(B, h, T)`` (or
+    broadcastable to it).  Returns ``y`` ``(B, T, h, d_v)`` and ``H_T``.  This is the
+    loop of ``DeltaMinGRU._forward_chunked_gated`` (reference
+    ``src/mingru/min_gru.py:3257-3448``): every decay factor is ``exp`` of a span sum
+    taken from its own terms, shared with the benchmark's eager-GPU leg.
+    """
+    B, n_heads, T, d_k = Q_all.shape
+    nh = K_all.shape[3]
+    d_v = V_all.shape[4]
+    ys = []
+    for s in range(0, T, chunk_size):
+        e = min(s + chunk_size, T)
+        C = e - s
+        M = nh * C
+        K = K_all[:, :, s:e].reshape(B, n_heads, M, d_k)
+        V = V_all[:, :, s:e].reshape(B, n_heads, M, d_v)
+        beta = beta_all[:, :, s:e].reshape(B, n_heads, M)
+        Q = Q_all[:, :, s:e]
+        span, logP = DeltaMinGRU._span_log_decay(log_gamma[:, :, s:e])
+        span_cm = span.repeat_interleave(nh, dim=-1)
+        span_mm = span_cm.repeat_interleave(nh, dim=-2)
+        P_tok = torch.exp(logP)
+        P_micro = P_tok.repeat_interleave(nh, dim=-1)
+        strict = torch.tril(K.new_ones(M, M), diagonal=-1)
+        eye = torch.eye(M, dtype=K.dtype, device=K.device)
+        dec_lower = torch.exp(span_mm.masked_fill(strict == 0, float("-inf")))
+        T_mat = eye + (K @ K.transpose(-1, -2)) * beta.unsqueeze(-2) * dec_lower
+        U = torch.linalg.solve_triangular(
+            T_mat, V - P_micro.unsqueeze(-1) * (K @ H), upper=False, unitriangular=True
+        )
+        read = torch.tril(Q.new_ones(C, C)).repeat_interleave(nh, dim=1)
+        dec_read = torch.exp(span_cm.masked_fill(read == 0, float("-inf")))
+        y = P_tok.unsqueeze(-1) * (Q @ H) + (
+            (Q @ K.transpose(-1, -2)) * beta.unsqueeze(-2) * dec_read
+        ) @ U
+        carry = torch.exp(span_cm[:, :, -1, :])
+        P_C = P_tok[:, :, -1].unsqueeze(-1).unsqueeze(-1)
+        H = P_C * H + K.transpose(-1, -2) @ ((carry * beta).unsqueeze(-1) * U)
         ys.append(y)
     return torch.cat(ys, dim=2).permute(0, 2, 1, 3), H
 

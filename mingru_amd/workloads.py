@@ -137,3 +137,12 @@ def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
     dHT = torch.randn(B, H, d, d, generator=g2)
     return dict(Q=q.to(dtype), K=k.to(dtype), V=v.to(dtype), beta=beta.to(dtype),
                 H0=torch.zeros(B, H, d, d), chunk_size=chunk, grad_y=dy, grad_HT=dHT)
+
+
+def c5d_inputs(B=8, H=8, T=8192, d=64, chunk=64):
+    """C5 heads with per-token decay for the gated delta kernels (fp32, the dtype they
+    compute in): ``log gamma = -0.5 U(0, 1)`` per (head, token), the span a fixed
+    decay rate of 0.5 gives over unit-scale gaps."""
+    inp = c5_inputs(B, H, T, d, chunk, dtype=torch.float32)
+    inp["log_gamma"] = -0.5 * torch.rand(B, H, T, generator=_gen(1015))
+    return inp
