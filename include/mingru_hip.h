@@ -184,6 +184,23 @@ int mg_delta_gated_bwd(const float* Q, const float* K, const float* V, const flo
                        float* dlog_gamma, float* dH0, int64_t B, int64_t H, int64_t T, int nh,
                        int dk, int dv, int chunk, void* ws, size_t ws_bytes, mg_stream_t stream);
 
+/* ---- streaming decode: one recurrent step (inference) -----------------------------
+ * No reference kernels: these replace the eager bodies of the mixers' step()
+ * (src/mingru/min_gru.py:1399-1448 MinGRU, SignedMinGRU.step, 3611-3688
+ * DeltaMinGRU.step).  No workspace.
+ * mg_gate_step: h = gamma * a * h_prev + b over n elements, kind 0 SignedMinGRU
+ * (p0, p1, p2 = s, z, hpre), 1 SignedMinGRU coupled, 2 MinGRU (p0, p1 = k, hpre;
+ * p2 unused, may be NULL); gamma may be NULL (no decay). */
+int mg_gate_step(int kind, const float* p0, const float* p1, const float* p2, const float* gamma,
+                 const float* h_prev, float* h, int64_t n, mg_stream_t stream);
+/* mg_delta_step: per head of BH, H (dk,dv) -> H_out = H after exp(log_gamma)
+ * decay (log_gamma (BH) may be NULL) and nh micro-steps H += beta k (v - H^T k)^T;
+ * y (dv) = H_out^T q.  q (BH,dk), k (BH,nh,dk), v (BH,nh,dv), beta (BH,nh), all
+ * fp32; 1 <= dk, dv <= 64.  H_out may equal H (in-place update). */
+int mg_delta_step(const float* H, const float* q, const float* k, const float* v,
+                  const float* beta, const float* log_gamma, float* H_out, float* y, int64_t BH,
+                  int nh, int dk, int dv, mg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

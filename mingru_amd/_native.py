@@ -32,6 +32,8 @@ _SIGNATURES = {
     "mg_mingru_gate_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "mg_mingru_gate_scan_fwd": (_I32, [_P] * 4 + [_I64, _I64, _I64, _P, _SZ, _P]),
     "mg_mingru_gate_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_gate_step": (_I32, [_I32] + [_P] * 6 + [_I64, _P]),
+    "mg_delta_step": (_I32, [_P] * 8 + [_I64, _I32, _I32, _I32, _P]),
     "mg_log_scan_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mg_log_scan_bwd": (_I32, [_P] * 6 + [_I64, _I64, _I64, _P, _SZ, _P]),
     "mg_affine_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32]),

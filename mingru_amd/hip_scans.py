@@ -37,6 +37,8 @@ __all__ = [
     "delta_gated_scan_impl",
     "signed_gate_scan_impl",
     "mingru_gate_scan_impl",
+    "gate_step_impl",
+    "delta_step_impl",
 ]
 
 
@@ -900,6 +902,89 @@ def delta_gated_scan_impl(Q, K, V, beta, log_gamma, H0, *, chunk_size: int):
         return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
     return _funnel("DeltaMinGRU gated chunked-WY", _DeltaGatedScanFn.apply, Q, K, V, beta,
                    log_gamma, H0, int(chunk_size))
+
+
+# ---------------------------------------------------------------------------
+# streaming decode (one recurrent step; inference only)
+# ---------------------------------------------------------------------------
+
+GATE_STEP_KINDS = {"signed": 0, "signed_coupled": 1, "mingru": 2}
+
+
+def _inference_only(what, *ts):
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
+        raise ScanFallback(f"{what} is inference-only (autograd is recording)")
+
+
+def gate_step_impl(kind: str, p0, p1, p2, gamma, h_prev):
+    """One step ``h = gamma * a * h_prev + b`` of a diagonal mixer; returns ``h``.
+
+    No reference kernel; the arithmetic is the mixers' ``step()``
+    (``src/mingru/min_gru.py:1399-1448`` for MinGRU, SignedMinGRU's
+    ``_coeffs`` + ``step``).  ``kind`` is ``"signed"`` / ``"signed_coupled"``
+    (``p0, p1, p2 = s, z, hpre``) or ``"mingru"`` (``p0, p1 = k, hpre``; ``p2``
+    unused).  ``gamma`` (decay) may be ``None`` or broadcastable to ``h_prev``.
+    """
+    if kind not in GATE_STEP_KINDS:
+        raise ScanFallback(f"unknown gate step kind {kind!r}")
+    ins = [p0, p1] + ([] if kind == "mingru" else [p2])
+    for t in ins:
+        if t.shape != h_prev.shape:
+            raise ScanFallback(
+                f"gate step pre-activation shape {tuple(t.shape)} differs from h_prev "
+                f"{tuple(h_prev.shape)}"
+            )
+    _same_device(h_prev, *ins)
+    _inference_only("the gate step kernel", h_prev, gamma, *ins)
+    out_dtype = h_prev.dtype
+    f32 = _as_f32(*ins, h_prev)
+    hp32 = f32[-1]
+    g32 = None
+    if gamma is not None:
+        _same_device(h_prev, gamma)
+        (g32,) = _as_f32(gamma.expand(h_prev.shape))
+    h = torch.empty_like(hp32)
+    q0, q1 = f32[0], f32[1]
+    q2 = f32[2] if kind != "mingru" else None
+    _call("mg_gate_step", GATE_STEP_KINDS[kind], _ptr(q0), _ptr(q1), _ptr(q2), _ptr(g32),
+          _ptr(hp32), _ptr(h), h.numel(), _stream(h))
+    return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+
+def delta_step_impl(H, q, K, V, beta, log_gamma):
+    """One DeltaMinGRU step on the kernel layouts; returns ``(y, H_new)``.
+
+    No reference kernel; the arithmetic is ``DeltaMinGRU.step``
+    (``src/mingru/min_gru.py:3611-3688``): ``H <- exp(log_gamma) H`` (when given),
+    then for each micro-step ``H <- H + beta k (v - H^T k)^T``, then ``y = H^T q``.
+    ``H`` ``(B, n_heads, d_k, d_v)``, ``q`` ``(B, n_heads, d_k)``, ``K``
+    ``(B, n_heads, nh, d_k)``, ``V`` ``(B, n_heads, nh, d_v)``, ``beta``
+    ``(B, n_heads, nh)``, ``log_gamma`` ``(B, n_heads)`` or ``None``;
+    ``y`` is ``(B, n_heads, d_v)``.  ``H`` is not modified.
+    """
+    if H.ndim != 4 or q.ndim != 3 or K.ndim != 4 or V.ndim != 4 or beta.ndim != 3:
+        raise ScanFallback("DeltaMinGRU step kernel needs H (B,h,dk,dv), q (B,h,dk), "
+                           "K (B,h,nh,dk), V (B,h,nh,dv), beta (B,h,nh)")
+    Bn, nhd, dk, dv = H.shape
+    nh = K.shape[2]
+    if (tuple(q.shape) != (Bn, nhd, dk) or tuple(K.shape) != (Bn, nhd, nh, dk)
+            or tuple(V.shape) != (Bn, nhd, nh, dv) or tuple(beta.shape) != (Bn, nhd, nh)
+            or (log_gamma is not None and tuple(log_gamma.shape) != (Bn, nhd))):
+        raise ScanFallback("DeltaMinGRU step kernel shapes disagree")
+    if not (1 <= dk <= _DELTA_MAX_DIM and 1 <= dv <= _DELTA_MAX_DIM):
+        raise ScanFallback(f"DeltaMinGRU step kernel needs d_k, d_v <= {_DELTA_MAX_DIM}")
+    ts = [H, q, K, V, beta] + ([] if log_gamma is None else [log_gamma])
+    _same_device(*ts)
+    _inference_only("the DeltaMinGRU step kernel", *ts)
+    if Bn * nhd == 0:
+        return q.new_zeros(Bn, nhd, dv), H.clone()
+    h32, q32, k32, v32, b32 = _as_f32(H, q, K, V, beta)
+    lg32 = None if log_gamma is None else _as_f32(log_gamma)[0]
+    y = torch.empty(Bn, nhd, dv, dtype=torch.float32, device=H.device)
+    Hn = torch.empty_like(h32)
+    _call("mg_delta_step", _ptr(h32), _ptr(q32), _ptr(k32), _ptr(v32), _ptr(b32), _ptr(lg32),
+          _ptr(Hn), _ptr(y), Bn * nhd, nh, dk, dv, _stream(h32))
+    return y.to(q.dtype), Hn.to(H.dtype)
 
 
 SCAN_IMPLS: dict = {

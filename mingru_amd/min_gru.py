@@ -67,6 +67,7 @@ _warned_delta_fallback = False
 _warned_delta_decay_fallback = False
 _warned_gate_fallback = False
 _warned_mingru_gate_fallback = False
+_warned_step_fallback = False
 
 # DeltaMinGRU ``auto`` region.  The HIP chunked-WY kernel beats the eager GPU
 # loop from a handful of chunks upward at every head size of its envelope, so
@@ -289,6 +290,64 @@ def _dispatch_mingru_gate_scan(k: torch.Tensor, hpre: torch.Tensor, log_h0: torc
         )
         _warned_mingru_gate_fallback = True
     return None
+
+
+def _dispatch_step(what: str, is_cuda: bool, call):
+    """Shared mode handling of the streaming decode kernels: run ``call(backend)`` or
+    return ``None`` for the eager step body.
+
+    The reference's ``step()`` bodies are eager only (``src/mingru/min_gru.py:
+    1399-1448, 3611-3688``).  ``eager`` and CPU ``auto`` stay eager silently;
+    CUDA ``auto`` warns once on a decline; the forcing mode raises.
+    """
+    mode = _resolve_scan_mode(is_cuda)
+    if mode is None:
+        return None
+
+    def _call(backend):
+        status = backend.available()
+        if status is not True:
+            raise backend.ScanFallback(str(status))
+        return call(backend)
+
+    result, reason = _resolve_native_dispatch(mode, what, _call)
+    if reason is None:
+        return result
+    global _warned_step_fallback
+    if not _warned_step_fallback:
+        warnings.warn(
+            f"MINGRU_SCAN=auto ran the eager step() despite CUDA inputs ({what}): {reason}",
+            stacklevel=4,
+        )
+        _warned_step_fallback = True
+    return None
+
+
+def _dispatch_gate_step(kind: str, p0, p1, p2, gamma, h_prev):
+    """One fused decode step ``h = gamma a h_prev + b`` (MinGRU / SignedMinGRU), or
+    ``None`` for the eager body."""
+
+    def call(backend):
+        if not hasattr(backend, "gate_step_impl"):
+            raise backend.ScanFallback("no gate step kernel registered")
+        return backend.gate_step_impl(kind, p0, p1, p2, gamma, h_prev)
+
+    return _dispatch_step("the fused gate step", h_prev.is_cuda, call)
+
+
+def _dispatch_delta_step(H, q, ks, vs, betas, log_gamma):
+    """One fused DeltaMinGRU decode step on ``(B, n_heads, ...)`` layouts, returning
+    ``(y (B, n_heads, d_v), H_new)``, or ``None`` for the eager body."""
+
+    def call(backend):
+        if not hasattr(backend, "delta_step_impl"):
+            raise backend.ScanFallback("no DeltaMinGRU step kernel registered")
+        K = torch.stack(ks, dim=2)
+        V = torch.stack(vs, dim=2)
+        beta = torch.stack(betas, dim=2)
+        return backend.delta_step_impl(H, q, K, V, beta, log_gamma)
+
+    return _dispatch_step("the fused DeltaMinGRU step", H.is_cuda, call)
 
 
 def _delta_scan_should_try(is_cuda: bool, *, T: int, chunk_size: int, d_k: int) -> bool:
@@ -714,12 +773,18 @@ class MinGRU(DecayMixin, nn.Module):
                 h_prev = g(self.h0_pre)[:, 0].expand(x_t.size(0), self.hidden_size)
             else:
                 h_prev = x_t.new_full((x_t.size(0), self.hidden_size), 0.5)
-        z = torch.sigmoid(self.linear_z(x_t))
-        h_tilde = g(self.linear_h(x_t))
-        a = 1 - z
+        k = self.linear_z(x_t)
+        h_pre = self.linear_h(x_t)
         dt = self._prepare_decay(delta_t, canonical_ndim=1)
-        if dt is not None:
-            a = self._decay_gamma(dt) * a
+        gamma = self._decay_gamma(dt) if dt is not None else None
+        h = _dispatch_gate_step("mingru", k, h_pre, None, gamma, h_prev)
+        if h is not None:
+            return h
+        z = torch.sigmoid(k)
+        h_tilde = g(h_pre)
+        a = 1 - z
+        if gamma is not None:
+            a = gamma * a
         return a * h_prev + z * h_tilde
 
     def extra_repr(self) -> str:
@@ -793,7 +858,13 @@ class SignedMinGRU(DecayMixin, nn.Module):
                 else x_t.new_zeros(x_t.size(0), self.hidden_size)
             )
         dt = self._prepare_decay(delta_t, canonical_ndim=1)
-        a, b = self._coeffs(x_t, dt)
+        z_pre, h_pre, s_pre = self.linear_z(x_t), self.linear_h(x_t), self.linear_s(x_t)
+        gamma = self._decay_gamma(dt) if dt is not None else None
+        kind = "signed_coupled" if self.coupled else "signed"
+        h = _dispatch_gate_step(kind, s_pre, z_pre, h_pre, gamma, h_prev)
+        if h is not None:
+            return h
+        a, b = self._coeffs_from(z_pre, h_pre, s_pre, dt)
         return a * h_prev + b
 
     def extra_repr(self) -> str:
@@ -1263,9 +1334,17 @@ class DeltaMinGRU(DecayMixin, nn.Module):
             if tuple(h_prev.shape) != expected:
                 raise ValueError(f"h_prev must have shape {expected} (got {tuple(h_prev.shape)})")
             H = h_prev.reshape(B, self.n_heads, self.d_k, self.d_v)
+        q, ks, vs, betas = self._coeffs(x_t)
+        log_gamma = None
+        if dt is not None:
+            log_gamma = (-self._decay_lambda() * dt.unsqueeze(-1)).expand(B, self.n_heads)
+        fused = _dispatch_delta_step(H, q, ks, vs, betas, log_gamma)
+        if fused is not None:
+            y, H = fused
+            y = self.out_proj(y.reshape(B, self.n_heads * self.d_v))
+            return y, H.reshape(*expected)
         if dt is not None:
             H = self._decay_gamma(dt).unsqueeze(-1).unsqueeze(-1) * H
-        q, ks, vs, betas = self._coeffs(x_t)
         for j in range(self.nh):
             H = self._micro_step(H, ks[j], vs[j], betas[j])
         y = self.out_proj(self._contract_state(q, H).reshape(B, self.n_heads * self.d_v))

@@ -36,7 +36,7 @@ def _isolate(monkeypatch):
     monkeypatch.delenv("MINGRU_SCAN", raising=False)
     for flag in ("_warned_scan_fallback", "_warned_angle_fallback", "_warned_delta_fallback",
                  "_warned_delta_decay_fallback", "_warned_gate_fallback",
-                 "_warned_mingru_gate_fallback"):
+                 "_warned_mingru_gate_fallback", "_warned_step_fallback"):
         monkeypatch.setattr(mg, flag, False)
 
 
@@ -478,3 +478,77 @@ def test_delta_module_forward_equals_step_recurrence():
         ys.append(yt)
     torch.testing.assert_close(y, torch.stack(ys, 1), rtol=0, atol=1e-12)
     assert F.mse_loss(y, y).item() == 0.0
+
+
+# ------------------------------------------------------------ streaming decode seams
+
+
+def test_mingru_step_hands_preactivations_to_gate_step(monkeypatch):
+    seen = {}
+
+    def fake_step(kind, p0, p1, p2, gamma, h_prev):
+        seen.update(kind=kind, p0=tuple(p0.shape), p2=p2, gamma=gamma, hp=h_prev.clone())
+        return torch.full(h_prev.shape, 2.0)
+
+    _fake_backend(monkeypatch, gate_step_impl=fake_step)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m = MinGRU(5, 6)
+    h = m.step(torch.randn(3, 5))
+    assert seen["kind"] == "mingru" and seen["p0"] == (3, 6)
+    assert seen["p2"] is None and seen["gamma"] is None
+    assert torch.equal(seen["hp"], torch.full((3, 6), 0.5))  # g(0) default state
+    assert torch.equal(h, torch.full((3, 6), 2.0))
+
+
+def test_signed_step_passes_decay_gamma_and_kind(monkeypatch):
+    seen = {}
+
+    def fake_step(kind, p0, p1, p2, gamma, h_prev):
+        seen.update(kind=kind, gamma=gamma)
+        return h_prev + 1
+
+    _fake_backend(monkeypatch, gate_step_impl=fake_step)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m = SignedMinGRU(4, 5, coupled=True, decay="fixed", decay_rate=0.3)
+    dt = torch.rand(2)
+    m.step(torch.randn(2, 4), torch.zeros(2, 5), delta_t=dt)
+    assert seen["kind"] == "signed_coupled"
+    assert torch.allclose(seen["gamma"].expand(2, 5), torch.exp(-0.3 * dt)[:, None].expand(2, 5))
+
+
+def test_delta_step_hands_stacked_layouts(monkeypatch):
+    seen = {}
+
+    def fake_step(H, q, K, V, beta, log_gamma):
+        seen.update(H=tuple(H.shape), q=tuple(q.shape), K=tuple(K.shape), V=tuple(V.shape),
+                    beta=tuple(beta.shape), lg=None if log_gamma is None else log_gamma.clone())
+        return torch.zeros(q.shape[0], q.shape[1], V.shape[-1]), H + 1
+
+    _fake_backend(monkeypatch, delta_step_impl=fake_step)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m = DeltaMinGRU(6, 12, n_heads=3, nh=2, decay="fixed", decay_rate=0.5)
+    dt = torch.rand(2)
+    y, H = m.step(torch.randn(2, 6), delta_t=dt)
+    assert seen["H"] == (2, 3, 4, 4) and seen["q"] == (2, 3, 4)
+    assert seen["K"] == (2, 3, 2, 4) and seen["V"] == (2, 3, 2, 4) and seen["beta"] == (2, 3, 2)
+    assert torch.allclose(seen["lg"], (-0.5 * dt)[:, None].expand(2, 3))
+    assert torch.equal(H, torch.ones(2, 48))
+    with torch.no_grad():
+        assert torch.allclose(y, m.out_proj(torch.zeros(2, 12)))
+
+
+def test_step_auto_fallback_warns_once(monkeypatch):
+    def fake_step(*args):
+        raise sys.modules[BACKEND].ScanFallback("declined by the fake backend")
+
+    _fake_backend(monkeypatch, gate_step_impl=fake_step)
+    f = _FakeCudaTensor()
+    monkeypatch.setenv("MINGRU_SCAN", "auto")
+    with pytest.warns(UserWarning, match="step"):
+        assert mg._dispatch_gate_step("mingru", f, f, None, None, f) is None
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert mg._dispatch_gate_step("mingru", f, f, None, None, f) is None
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with pytest.raises(RuntimeError, match="declined by the fake backend"):
+        mg._dispatch_gate_step("mingru", f, f, None, None, f)
