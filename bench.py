@@ -392,6 +392,81 @@ def delta_gated_eager_gpu_ms(torch, wl, dev, reps=3):
     return ts[len(ts) // 2]
 
 
+def decode_bench(torch, wl, dev, steps):
+    """Streaming decode: one recurrent step per call, fused kernel vs the eager step body on
+    the GPU (the same arithmetic as the mixers' step()), median over `steps` calls.
+
+    D5: DeltaMinGRU state update at C5's heads (B=8, H=8, d_k=d_v=64, nh=1, with decay);
+        bytes = the state read and written plus q, k, v, beta.
+    D2: SignedMinGRU step at C2's width (B=16, D=1024); bytes = s, z, hpre, h_prev in, h out.
+    """
+    from mingru_amd import hip_scans
+
+    g = torch.Generator().manual_seed(1099)
+    out = {}
+    c = wl.C5
+    B, Hh, d = c["B"], c["H"], c["d"]
+    H = torch.randn(B, Hh, d, d, generator=g).to(dev)
+    q = torch.randn(B, Hh, d, generator=g).to(dev)
+    K = torch.nn.functional.normalize(torch.randn(B, Hh, 1, d, generator=g), dim=-1).to(dev)
+    V = torch.randn(B, Hh, 1, d, generator=g).to(dev)
+    beta = torch.rand(B, Hh, 1, generator=g).to(dev)
+    lg = -torch.rand(B, Hh, generator=g).to(dev)
+
+    def fused5():
+        return hip_scans.delta_step_impl(H, q, K, V, beta, lg)
+
+    def eager5():
+        Hx = torch.exp(lg)[..., None, None] * H
+        k, v, bt = K[:, :, 0], V[:, :, 0], beta[:, :, 0]
+        kH = torch.einsum("bhk,bhkv->bhv", k, Hx)
+        Hx = Hx + bt[..., None, None] * torch.einsum("bhk,bhv->bhkv", k, v - kH)
+        return torch.einsum("bhk,bhkv->bhv", q, Hx), Hx
+
+    b5 = 2 * H.numel() * 4 + (q.numel() + K.numel() + V.numel() + beta.numel() + lg.numel()) * 4
+    c2 = wl.C2
+    n = c2["B"] * c2["D"]
+    s_, z_, hp_, h_ = (torch.randn(c2["B"], c2["D"], generator=g).to(dev) for _ in range(4))
+
+    def fused2():
+        return hip_scans.gate_step_impl("signed", s_, z_, hp_, None, h_)
+
+    def eager2():
+        return torch.tanh(s_) * h_ + torch.sigmoid(z_) * hp_
+
+    for key, fused, eager, nbytes, tok in (("D5", fused5, eager5, b5, B),
+                                            ("D2", fused2, eager2, 5 * n * 4, c2["B"])):
+        res = {}
+        for name, fn in (("fused", fused), ("eager", eager)):
+            with torch.no_grad():
+                for _ in range(5):
+                    fn()
+                torch.cuda.synchronize()
+                # latency: one step, then wait for it (a decode loop that reads each result)
+                ts = []
+                for _ in range(steps):
+                    t0 = time.perf_counter()
+                    fn()
+                    torch.cuda.synchronize()
+                    ts.append((time.perf_counter() - t0) * 1e6)
+                # throughput: 10 * steps calls queued back to back, one wait at the end
+                t0 = time.perf_counter()
+                for _ in range(10 * steps):
+                    fn()
+                torch.cuda.synchronize()
+                tput = (time.perf_counter() - t0) * 1e6 / (10 * steps)
+            ts.sort()
+            res[f"{name}_us_per_step"] = ts[len(ts) // 2]
+            res[f"{name}_us_per_step_queued"] = tput
+        res["speedup_vs_eager"] = res["eager_us_per_step"] / res["fused_us_per_step"]
+        res["speedup_vs_eager_queued"] = (res["eager_us_per_step_queued"]
+                                          / res["fused_us_per_step_queued"])
+        res["bytes_per_step"] = nbytes
+        res["tokens_per_step"] = tok
+        out[key] = res
+    return out
+
+
 def _timed(step, steps, torch):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -589,12 +664,24 @@ def main():
             if key == "C2":
                 cpu = cb
         torch.cuda.empty_cache()
+    decode = None
+    if not args.only or "decode" in args.only.split(","):
+        decode = dec = decode_bench(torch, wl, dev, max(args.steps, 20))
+        for k, r in dec.items():
+            print(f"# {k} decode step: fused {r['fused_us_per_step']:.1f} us, eager "
+                  f"{r['eager_us_per_step']:.1f} us ({r['speedup_vs_eager']:.1f}x); queued: fused "
+                  f"{r['fused_us_per_step_queued']:.1f} us, eager "
+                  f"{r['eager_us_per_step_queued']:.1f} us ({r['speedup_vs_eager_queued']:.1f}x)",
+                  file=sys.stderr, flush=True)
     copy = None
     if args.copy_probe:
         copy = copy_probe(torch, dev)
         print(f"# copy probe: {copy['achieved_GBs']:.0f} GB/s ({copy['avg_us']:.1f} us per "
               "1 GiB copy)", file=sys.stderr, flush=True)
 
+    if not results:  # --only decode
+        print(json.dumps({"decode": decode}))
+        return
     head = results.get(HEADLINE) or next(iter(results.values()))
     head_key = HEADLINE if HEADLINE in results else next(iter(results))
     op = ops[head_key]
@@ -633,6 +720,8 @@ def main():
     }
     if copy is not None:
         line["copy_probe"] = copy
+    if decode is not None:
+        line["decode"] = decode
     print(json.dumps(line))
 
 

@@ -22,7 +22,6 @@ is not supported (``once_differentiable``).
 
 from __future__ import annotations
 
-import ctypes
 import weakref
 
 import torch
@@ -102,12 +101,19 @@ def available() -> bool | str:
 # ---------------------------------------------------------------------------
 
 
-def _ptr(t: torch.Tensor | None):
-    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+def _ptr(t: torch.Tensor | None) -> int:
+    # Plain ints: the ctypes signatures declare void*, which converts them directly.
+    return t.data_ptr() if t is not None else 0
 
 
-def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(t: torch.Tensor) -> int:
+    """torch's current stream on ``t``'s device, as the raw ``hipStream_t`` value."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
