@@ -131,8 +131,9 @@ _scan_ws: dict = {}
 
 
 def _scan_workspace(nbytes: int, device) -> torch.Tensor:
-    stream = torch.cuda.current_stream(device)
-    key = (stream.device_index, stream.cuda_stream)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    raw = _raw_stream(idx) if _raw_stream is not None else torch.cuda.current_stream(idx).cuda_stream
+    key = (idx, raw)
     ws = _scan_ws.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
