@@ -9,7 +9,7 @@
 //     span(t, t') = sum_{s=t'+1..t} l_s,   E[t][t'] = exp(span(t, t')) (t' <= t, else 0),
 //     Lc_t = sum_{s<=t} l_s,  p_m = exp(Lc_tau(m)),  ptok_t = exp(Lc_t),
 //     a_m = E[C-1][tau(m)],   PC = exp(Lc_{C-1}),     tau(m) = m / nh,
-// each accumulated from its own terms (never a difference of running sums).
+// each a sum of its own terms (never a difference of running sums).
 // With Hc the state entering the chunk:
 //     L  = strict_lower(K K^T) * beta_col * E[tau(i)][tau(j)],  Tm = I + L
 //     U  = Tm^-1 (V - diag(p) K Hc) = U0 - W Hc,   U0 = Tm^-1 V,  W = Tm^-1 diag(p) K
@@ -25,7 +25,8 @@
 // and the decay gradient through every factor's log: with F[t][t'] the summed
 // d/d span(t, t') and f[t] the summed d/d Lc_t,
 //     dl_s = sum_{t >= s} ( f[t] + sum_{t' < s} F[t][t'] ),
-// taken as row prefix sums then column suffix sums of F (fixed order).
+// taken as wave-level prefix scans along the rows of F and per-wave column sums
+// added in a fixed order.
 //
 // Kernels mirror delta_wy.hip (fp32 operands on v_mfma_f32_16x16x4_f32); the
 // per-chunk decay vectors (a beta, ptok, p, PC) travel in a small vector region.
@@ -40,19 +41,26 @@ constexpr int VECN = 256;  // floats per chunk in the vector region
 // [128, 192) p_m, [192] PC.
 constexpr int V_AB = 0, V_PT = 64, V_P = 128, V_PC = 192;
 
-// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above; sLc[t] = Lc_t.  Thread t sums
-// its row from s = t down to 0, the order of the reference's reverse cumulative
-// sum over the masked row, so each span holds only its own terms.
+// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above; sLc[t] = Lc_t.  Wave w fills
+// rows 16w..16w+15: lane s holds l_s masked to s <= t, and an inclusive suffix
+// scan across the wave gives sum_{s' >= s}; span(t, t') is the scan value of lane
+// t' + 1.  Every span is a sum of its own terms only (never a difference of
+// running sums), so a saturated gap affects only the spans that contain it.
 __device__ __forceinline__ void decay_tables(const float* sl, float* sE, float* sLc) {
-  const int t = threadIdx.x;
-  if (t < DN) {
-    for (int tp = DN - 1; tp > t; --tp) sE[t * LD + tp] = 0.f;
-    float acc = 0.f;
-    for (int tp = t; tp >= 0; --tp) {
-      sE[t * LD + tp] = expf(acc);
-      acc += sl[tp];
+  const int w = wave_id(), lane = lane_id();
+  const float lv = sl[lane];
+  for (int rr = 0; rr < DN / (NT / 64); ++rr) {
+    const int t = (DN / (NT / 64)) * w + rr;
+    float x = lane <= t ? lv : 0.f;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_down(x, d);
+      if (lane + d < 64) x += y;
     }
-    sLc[t] = acc;
+    float ex = __shfl_down(x, 1);
+    if (lane == 63) ex = 0.f;
+    sE[t * LD + lane] = lane <= t ? expf(ex) : 0.f;
+    if (lane == 0) sLc[t] = x;
   }
 }
 
@@ -509,6 +517,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
   // column sums per wave, [8] a_m * row sums of U * (K dHn).
   __shared__ float sdb[9][DN];
   __shared__ float sred[NT / 64];
+  __shared__ float sdl[NT / 64][DN];
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -736,22 +745,31 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     sfv[3][t] = f;
   }
   __syncthreads();
-  // Row prefix sums: sQ[t][s] = f[t] + sum_{t' < s} F[t][t'].
-  if (threadIdx.x < ch.Ct) {
-    const int t = threadIdx.x;
-    float run = sfv[3][t];
-    for (int s = 0; s < ch.Ct; ++s) {
-      const float x = sQ[t * LD + s];
-      sQ[t * LD + s] = run;
-      run += x;
+  // dl_s = sum_{t >= s} (f[t] + sum_{t' < s} F[t][t']).  Wave w scans rows
+  // 16w..16w+15 of F: an exclusive prefix scan along each row (lane s), then each
+  // lane adds the rows t >= s; the four wave partials are summed in a fixed order.
+  {
+    float acc = 0.f;
+    for (int rr = 0; rr < DN / (NT / 64); ++rr) {
+      const int t = (DN / (NT / 64)) * w + rr;
+      float x = sQ[t * LD + lane];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+      }
+      float ex = __shfl_up(x, 1);
+      if (lane == 0) ex = 0.f;
+      if (t >= lane && t < ch.Ct) acc += sfv[3][t] + ex;
     }
+    sdl[w][lane] = acc;
   }
   __syncthreads();
-  // Column suffix sums: dl_s = sum_{t >= s} sQ[t][s].
   if (threadIdx.x < ch.Ct) {
     const int s = threadIdx.x;
     float acc = 0.f;
-    for (int t = ch.Ct - 1; t >= s; --t) acc += sQ[t * LD + s];
+#pragma unroll
+    for (int q = 0; q < NT / 64; ++q) acc += sdl[q][s];
     dlg[trow0 + s] = acc;
   }
 }
