@@ -138,14 +138,14 @@ def build_ops(torch, wl):
     ops["C5"] = Op("C5", "C5 DeltaMinGRU chunked-WY fwd+bwd (bf16 in, fp32 state)",
                    c["B"] * c["T"], "mg_delta_fwd", "mg_delta_bwd",
                    4 * bt + bt // c["d"], 7 * bt + 2 * bt // c["d"], f_fwd, 2 * f_fwd)
-    # C5d: C5 with per-token decay on the gated kernels (fp32 in and out).  Bytes: Q, K, V
-    # read and y written forward, plus beta and log_gamma; backward reads Q, K, V, dy, beta,
-    # log_gamma and writes dQ, dK, dV, dbeta, dlog_gamma.  Same FLOP floor as C5.
-    bt32 = 2 * bt
-    ops["C5d"] = Op("C5d", "C5d DeltaMinGRU decay-gated chunked-WY fwd+bwd (C5 shape, fp32)",
+    # C5d: C5 with per-token decay on the gated kernels (bf16 in, fp32 state and decay).
+    # Bytes: as C5 plus log_gamma (fp32, (B,H,T)) read forward and backward and dlog_gamma
+    # written.  Same FLOP floor as C5.
+    lgb = c["B"] * c["H"] * c["T"] * 4
+    ops["C5d"] = Op("C5d", "C5d DeltaMinGRU decay-gated chunked-WY fwd+bwd (C5 shape, bf16 in)",
                     c["B"] * c["T"], "mg_delta_gated_fwd", "mg_delta_gated_bwd",
-                    4 * bt32 + 2 * bt32 // c["d"], 7 * bt32 + 4 * bt32 // c["d"], f_fwd,
-                    2 * f_fwd, mfma=("fp32", MFMA_FP32_PEAK_TFLOPS))
+                    4 * bt + bt // c["d"] + lgb, 7 * bt + 2 * bt // c["d"] + 2 * lgb, f_fwd,
+                    2 * f_fwd)
     return ops
 
 
@@ -286,7 +286,7 @@ def make_step(key, torch, wl, dev):
         inp = wl.c5d_inputs(**wl.C5)
         names = ("Q", "K", "V", "beta", "log_gamma", "H0")
         xs = [inp[k].to(dev).requires_grad_(True) for k in names]
-        gy = inp["grad_y"].to(dev)
+        gy = inp["grad_y"].to(dev).to(inp["Q"].dtype)
         gH = inp["grad_HT"].to(dev)
         C = inp["chunk_size"]
 
@@ -367,12 +367,13 @@ def delta_eager_gpu_ms(torch, wl, dev, reps=3):
 
 def delta_gated_eager_gpu_ms(torch, wl, dev, reps=3):
     """The eager decay-gated chunked-WY loop (the module's ``_forward_chunked_gated``,
-    torch ops on the GPU, fp32) fwd+bwd at C5d; returns the median ms per step."""
+    torch ops on the GPU, fp32 since the triangular solve has no bf16 kernel) fwd+bwd
+    at C5d; returns the median ms per step."""
     from mingru_amd.min_gru import delta_chunked_gated_eager
 
     inp = wl.c5d_inputs(**wl.C5)
     names = ("Q", "K", "V", "beta", "log_gamma", "H0")
-    xs = [inp[k].to(dev).requires_grad_(True) for k in names]
+    xs = [inp[k].to(dev).float().requires_grad_(True) for k in names]
     gy = inp["grad_y"].to(dev).permute(0, 2, 1, 3)
     gH = inp["grad_HT"].to(dev)
 

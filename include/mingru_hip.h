@@ -163,26 +163,27 @@ int mg_delta_bwd(const void* Q, const void* K, const void* V, const void* beta,
                  int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
                  mg_stream_t stream);
 
-/* ---- DeltaMinGRU decay-gated chunked-WY delta rule (fp32) -------------------------
+/* ---- DeltaMinGRU decay-gated chunked-WY delta rule ------------------------------------
  * No reference kernel: replaces the eager decay-active forward
  * (DeltaMinGRU._forward_chunked_gated, src/mingru/min_gru.py:3257-3448, guarded by
  * _delta_decay_dispatch_guard :612-668) and its autograd backward.  Per token t the
  * state decays by gamma_t = exp(log_gamma[b,h,t]) before the token's nh micro-steps.
- * Layouts as mg_delta_fwd with every tensor fp32, plus log_gamma / dlog_gamma
- * (B,H,T).  `Hbound` takes mg_delta_state_bytes; `ws` mg_delta_gated_workspace_bytes
- * (forward and backward). */
+ * Layouts and dtype tag as mg_delta_fwd (dtype 1 = bf16 requires nh = 1), plus
+ * log_gamma / dlog_gamma (B,H,T) fp32.  `Hbound` takes mg_delta_state_bytes; `ws`
+ * mg_delta_gated_workspace_bytes (forward and backward). */
 size_t mg_delta_gated_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
                                       int chunk);
-int mg_delta_gated_fwd(const float* Q, const float* K, const float* V, const float* beta,
-                       const float* log_gamma, const float* H0, float* y, float* HT,
+int mg_delta_gated_fwd(const void* Q, const void* K, const void* V, const void* beta,
+                       const float* log_gamma, const float* H0, void* y, float* HT,
                        float* Hbound, int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
-                       int chunk, void* ws, size_t ws_bytes, mg_stream_t stream);
-/* dy, dHT -> dQ, dK, dV, dbeta, dlog_gamma and dH0. */
-int mg_delta_gated_bwd(const float* Q, const float* K, const float* V, const float* beta,
-                       const float* log_gamma, const float* Hbound, const float* dy,
-                       const float* dHT, float* dQ, float* dK, float* dV, float* dbeta,
+                       int chunk, int dtype, void* ws, size_t ws_bytes, mg_stream_t stream);
+/* dy (dtype), dHT -> dQ, dK, dV, dbeta (dtype), dlog_gamma and dH0 (fp32). */
+int mg_delta_gated_bwd(const void* Q, const void* K, const void* V, const void* beta,
+                       const float* log_gamma, const float* Hbound, const void* dy,
+                       const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
                        float* dlog_gamma, float* dH0, int64_t B, int64_t H, int64_t T, int nh,
-                       int dk, int dv, int chunk, void* ws, size_t ws_bytes, mg_stream_t stream);
+                       int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
+                       mg_stream_t stream);
 
 /* ---- streaming decode: one recurrent step (inference) -----------------------------
  * No reference kernels: these replace the eager bodies of the mixers' step()

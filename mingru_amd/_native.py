@@ -59,10 +59,10 @@ _SIGNATURES = {
     ),
     "mg_delta_gated_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
     "mg_delta_gated_fwd": (
-        _I32, [_P] * 9 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        _I32, [_P] * 9 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
     "mg_delta_gated_bwd": (
-        _I32, [_P] * 14 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
+        _I32, [_P] * 14 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
 }
 

@@ -28,41 +28,16 @@
 // taken as wave-level prefix scans along the rows of F and per-wave column sums
 // added in a fixed order.
 //
-// Kernels mirror delta_wy.hip (fp32 operands on v_mfma_f32_16x16x4_f32); the
-// per-chunk decay vectors (a beta, ptok, p, PC) travel in a small vector region.
-#include "mg_delta.h"
+// These kernels mirror delta_wy.hip (fp32 operands on v_mfma_f32_16x16x4_f32) and
+// serve fp32 inputs and nh > 1; bf16 inputs with nh = 1 run the gated
+// instantiations of the bf16-MFMA kernels (delta_wy_bf16.hip), chosen by the
+// dtype tag of the entry points.  The per-chunk decay vectors (a beta, ptok, p,
+// PC) travel in a small vector region after the workspace matrices.
+#include "mg_delta_bf16.h"
 
 namespace {
 
 using namespace mgd;
-
-constexpr int VECN = 256;  // floats per chunk in the vector region
-// Vector region layout per chunk: [0, 64) a_m beta_m, [64, 128) ptok_t,
-// [128, 192) p_m, [192] PC.
-constexpr int V_AB = 0, V_PT = 64, V_P = 128, V_PC = 192;
-
-// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above; sLc[t] = Lc_t.  Wave w fills
-// rows 16w..16w+15: lane s holds l_s masked to s <= t, and an inclusive suffix
-// scan across the wave gives sum_{s' >= s}; span(t, t') is the scan value of lane
-// t' + 1.  Every span is a sum of its own terms only (never a difference of
-// running sums), so a saturated gap affects only the spans that contain it.
-__device__ __forceinline__ void decay_tables(const float* sl, float* sE, float* sLc) {
-  const int w = wave_id(), lane = lane_id();
-  const float lv = sl[lane];
-  for (int rr = 0; rr < DN / (NT / 64); ++rr) {
-    const int t = (DN / (NT / 64)) * w + rr;
-    float x = lane <= t ? lv : 0.f;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_down(x, d);
-      if (lane + d < 64) x += y;
-    }
-    float ex = __shfl_down(x, 1);
-    if (lane == 63) ex = 0.f;
-    sE[t * LD + lane] = lane <= t ? expf(ex) : 0.f;
-    if (lane == 0) sLc[t] = x;
-  }
-}
 
 // L = strict_lower(K K^T) * beta_col * E[tau(i)][tau(j)] into sL; wave w builds block-row w.
 __device__ __forceinline__ void build_L_gated(const float* sK, const float* sb, const float* sE,
@@ -80,33 +55,6 @@ __device__ __forceinline__ void build_L_gated(const float* sK, const float* sb, 
           col < row ? acc[J][i] * sb[col] * sE[(row / nh) * LD + col / nh] : 0.f;
     }
   }
-}
-
-// Per-chunk decay vectors from the tables: sp[m] = p_m, sab[m] = a_m beta_m.
-__device__ __forceinline__ void decay_vectors(const float* sE, const float* sLc, const float* sb,
-                                              const Chunk& ch, int nh, float* sp, float* sab) {
-  const int m = threadIdx.x;
-  if (m < DN) {
-    const bool ok = m < ch.M;
-    sp[m] = ok ? expf(sLc[m / nh]) : 0.f;
-    sab[m] = ok ? sE[(ch.Ct - 1) * LD + m / nh] * sb[m] : 0.f;
-  }
-}
-
-__device__ __forceinline__ void write_vectors(float* vv, const float* sLc, const float* sp,
-                                              const float* sab, const Chunk& ch) {
-  const int m = threadIdx.x;
-  if (m < DN) {
-    vv[V_AB + m] = sab[m];
-    vv[V_PT + m] = m < ch.Ct ? expf(sLc[m]) : 0.f;
-    vv[V_P + m] = sp[m];
-    if (m == 0) vv[V_PC] = expf(sLc[ch.Ct - 1]);
-  }
-}
-
-__device__ __forceinline__ float ld_l(const float* lg, int64_t bh, const DwGeom& g,
-                                      const Chunk& ch) {
-  return threadIdx.x < ch.Ct ? lg[bh * g.T + ch.t0 + threadIdx.x] : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -140,7 +88,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
     sl[threadIdx.x] = lv;
   }
   __syncthreads();
-  decay_tables(sl, sE, sLc);
+  decay_tables<NT>(sl, sE, sLc);
   __syncthreads();
   decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
   build_L_gated(sK, sb, sE, g.nh, sL);
@@ -339,7 +287,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
     }
   }
   __syncthreads();
-  decay_tables(sl, sE, sLc);
+  decay_tables<NT>(sl, sE, sLc);
   __syncthreads();
   decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
   if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
@@ -549,7 +497,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     }
   }
   __syncthreads();
-  decay_tables(sl, sE, sLc);
+  decay_tables<NT>(sl, sE, sLc);
   // PC term: <dHn, Hc>, with dHn in this thread's tile registers and Hc in sH.
   {
     float part = tn.dot(sH);
@@ -785,6 +733,60 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// bf16 inputs (nh = 1): the gated instantiations of the bf16-MFMA kernels
+// ---------------------------------------------------------------------------
+namespace mgd {
+
+int dw_fwd_bf16_gated(const void* Q, const void* K, const void* V, const void* beta,
+                      const float* lg, const float* H0, void* y, float* HT, float* Hb, int64_t BH,
+                      const DwGeom& g, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 4 * mb + (size_t)BH * g.nc * VECN * sizeof(float)) return MG_ERR_WORKSPACE;
+  float* Am = (float*)ws;  // split pair
+  float* Bm = (float*)((char*)ws + mb);
+  float* Qem = (float*)((char*)ws + 2 * mb);  // split pair
+  float* Pum = (float*)((char*)ws + 3 * mb);
+  float* vm = (float*)((char*)ws + 4 * mb);
+  hipLaunchKernelGGL(dwb_fwd_prep<true>, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream,
+                     (const u16*)Q, (const u16*)K, (const u16*)V, (const u16*)beta, lg, Am, Bm,
+                     Qem, Pum, vm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dwb_fwd_chain<true>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, H0, Am, Bm,
+                     Qem, Pum, vm, (u16*)y, HT, Hb, g, BH);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+int dw_bwd_bf16_gated(const void* Q, const void* K, const void* V, const void* beta,
+                      const float* lg, const float* Hb, const void* dy, const float* dHT, void* dQ,
+                      void* dK, void* dV, void* dbeta, float* dlg, float* dH0, int64_t BH,
+                      const DwGeom& g, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (g.nh != 1) return MG_ERR_ARG;  // the gated gradients are token-level
+  const size_t mb = dw_mat_bytes(BH, g);
+  if (ws_bytes < 6 * mb + (size_t)BH * g.nc * VECN * sizeof(float)) return MG_ERR_WORKSPACE;
+  float* Um = (float*)ws;
+  float* Em = (float*)((char*)ws + mb);  // split pair
+  float* G0m = (float*)((char*)ws + 2 * mb);
+  float* Apm = (float*)((char*)ws + 3 * mb);  // split pair
+  float* bpm = (float*)((char*)ws + 4 * mb);
+  float* dHn = (float*)((char*)ws + 5 * mb);
+  float* vm = (float*)((char*)ws + 6 * mb);
+  const dim3 pgrid(g.nc, (unsigned)BH);
+  const u16 *q = (const u16*)Q, *k = (const u16*)K, *v = (const u16*)V, *b = (const u16*)beta,
+            *d = (const u16*)dy;
+  hipLaunchKernelGGL(dwb_bwd_prep<true>, pgrid, dim3(NTB), 0, stream, q, k, v, b, lg, d, Hb, Um,
+                     Em, G0m, Apm, bpm, vm, g);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dwb_bwd_chain<true>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, dHT, Apm,
+                     bpm, vm, dHn, dH0, g, BH);
+  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  hipLaunchKernelGGL(dwb_bwd_grads<true>, pgrid, dim3(NTB), 0, stream, q, k, b, lg, d, Hb, dHn, Um,
+                     Em, G0m, (u16*)dQ, (u16*)dK, (u16*)dV, (u16*)dbeta, dlg, g);
+  return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
+}
+
+}  // namespace mgd
+
 extern "C" {
 
 size_t mg_delta_gated_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
@@ -795,35 +797,43 @@ size_t mg_delta_gated_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, i
   return 6 * dw_mat_bytes(BH, g) + dg_vec_bytes(BH, g);
 }
 
-int mg_delta_gated_fwd(const float* Q, const float* K, const float* V, const float* beta,
-                       const float* log_gamma, const float* H0, float* y, float* HT,
+int mg_delta_gated_fwd(const void* Q, const void* K, const void* V, const void* beta,
+                       const float* log_gamma, const float* H0, void* y, float* HT,
                        float* Hbound, int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
-                       int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
+                       int chunk, int dtype, void* ws, size_t ws_bytes, hipStream_t stream) {
   DwGeom g;
   int64_t BH;
   if (!Q || !K || !V || !beta || !log_gamma || !H0 || !y || !HT || !Hbound || !ws)
     return MG_ERR_ARG;
   if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
   if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
+  if (dtype == 1) {
+    if (nh != 1) return MG_ERR_ARG;
+    return dw_fwd_bf16_gated(Q, K, V, beta, log_gamma, H0, y, HT, Hbound, BH, g, ws, ws_bytes,
+                             stream);
+  }
+  if (dtype != 0) return MG_ERR_ARG;
   const size_t mb = dw_mat_bytes(BH, g);
   if (ws_bytes < 3 * mb + dg_vec_bytes(BH, g)) return MG_ERR_WORKSPACE;
   float* Wm = (float*)ws;
   float* U0m = (float*)((char*)ws + mb);
   float* Pm = (float*)((char*)ws + 2 * mb);
   float* vm = (float*)((char*)ws + 3 * mb);
-  hipLaunchKernelGGL(dg_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, Q, K, V, beta,
+  const float *q = (const float*)Q, *k = (const float*)K, *v = (const float*)V,
+              *b = (const float*)beta;
+  hipLaunchKernelGGL(dg_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, q, k, v, b,
                      log_gamma, Wm, U0m, Pm, vm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dg_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, Q, K, H0, Wm,
-                     U0m, Pm, vm, y, HT, Hbound, g, BH);
+  hipLaunchKernelGGL(dg_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, q, k, H0, Wm,
+                     U0m, Pm, vm, (float*)y, HT, Hbound, g, BH);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
-int mg_delta_gated_bwd(const float* Q, const float* K, const float* V, const float* beta,
-                       const float* log_gamma, const float* Hbound, const float* dy,
-                       const float* dHT, float* dQ, float* dK, float* dV, float* dbeta,
+int mg_delta_gated_bwd(const void* Q, const void* K, const void* V, const void* beta,
+                       const float* log_gamma, const float* Hbound, const void* dy,
+                       const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
                        float* dlog_gamma, float* dH0, int64_t B, int64_t H, int64_t T, int nh,
-                       int dk, int dv, int chunk, void* ws, size_t ws_bytes,
+                       int dk, int dv, int chunk, int dtype, void* ws, size_t ws_bytes,
                        hipStream_t stream) {
   DwGeom g;
   int64_t BH;
@@ -832,6 +842,12 @@ int mg_delta_gated_bwd(const float* Q, const float* K, const float* V, const flo
     return MG_ERR_ARG;
   if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
   if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
+  if (dtype == 1) {
+    if (nh != 1) return MG_ERR_ARG;
+    return dw_bwd_bf16_gated(Q, K, V, beta, log_gamma, Hbound, dy, dHT, dQ, dK, dV, dbeta,
+                             dlog_gamma, dH0, BH, g, ws, ws_bytes, stream);
+  }
+  if (dtype != 0) return MG_ERR_ARG;
   const size_t mb = dw_mat_bytes(BH, g);
   if (ws_bytes < 6 * mb + dg_vec_bytes(BH, g)) return MG_ERR_WORKSPACE;
   float* Um = (float*)ws;
@@ -841,14 +857,17 @@ int mg_delta_gated_bwd(const float* Q, const float* K, const float* V, const flo
   float* Gm = (float*)((char*)ws + 4 * mb);
   float* dHn = (float*)((char*)ws + 5 * mb);
   float* vm = (float*)((char*)ws + 6 * mb);
-  hipLaunchKernelGGL(dg_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, Q, K, V, beta,
-                     log_gamma, dy, Hbound, Um, Em, G0m, QdYm, vm, g);
+  const float *q = (const float*)Q, *k = (const float*)K, *v = (const float*)V,
+              *b = (const float*)beta, *d = (const float*)dy;
+  hipLaunchKernelGGL(dg_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, q, k, v, b,
+                     log_gamma, d, Hbound, Um, Em, G0m, QdYm, vm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dg_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, K, dHT, Em, G0m,
+  hipLaunchKernelGGL(dg_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, k, dHT, Em, G0m,
                      QdYm, vm, Gm, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
-  hipLaunchKernelGGL(dg_bwd_grads, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, Q, K, beta,
-                     log_gamma, dy, Hbound, dHn, Um, Gm, dQ, dK, dV, dbeta, dlog_gamma, g);
+  hipLaunchKernelGGL(dg_bwd_grads, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, q, k, b,
+                     log_gamma, d, Hbound, dHn, Um, Gm, (float*)dQ, (float*)dK, (float*)dV,
+                     (float*)dbeta, dlog_gamma, g);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 

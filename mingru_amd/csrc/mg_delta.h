@@ -321,6 +321,70 @@ __device__ __forceinline__ void put_colsum(floatx4 v, float* s, int col) {
 }
 
 
+// ---------------------------------------------------------------------------
+// Decay tables of the gated chunked-WY kernels (per-token log decay l_t <= 0,
+// tau(m) = m / nh the token of micro-row m; every table is rebuilt per chunk).
+// ---------------------------------------------------------------------------
+constexpr int VECN = 256;  // floats per chunk in the vector region
+// Vector region layout per chunk: [0, 64) a_m beta_m, [64, 128) ptok_t,
+// [128, 192) p_m, [192] PC.
+constexpr int V_AB = 0, V_PT = 64, V_P = 128, V_PC = 192;
+
+// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above; sLc[t] = Lc_t.  Each wave of
+// the NTH-thread workgroup fills 64 / (NTH / 64) consecutive rows t: lane s holds
+// l_s masked to s <= t, and an inclusive suffix
+// scan across the wave gives sum_{s' >= s}; span(t, t') is the scan value of lane
+// t' + 1.  Every span is a sum of its own terms only (never a difference of
+// running sums), so a saturated gap affects only the spans that contain it.
+template <int NTH>
+__device__ __forceinline__ void decay_tables(const float* sl, float* sE, float* sLc) {
+  constexpr int ROWS = DN / (NTH / 64);  // rows per wave
+  const int w = wave_id(), lane = lane_id();
+  const float lv = sl[lane];
+  for (int rr = 0; rr < ROWS; ++rr) {
+    const int t = ROWS * w + rr;
+    float x = lane <= t ? lv : 0.f;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_down(x, d);
+      if (lane + d < 64) x += y;
+    }
+    float ex = __shfl_down(x, 1);
+    if (lane == 63) ex = 0.f;
+    sE[t * LD + lane] = lane <= t ? expf(ex) : 0.f;
+    if (lane == 0) sLc[t] = x;
+  }
+}
+
+// Per-chunk decay vectors from the tables: sp[m] = p_m, sab[m] = a_m beta_m
+// (threads 0..63).
+__device__ __forceinline__ void decay_vectors(const float* sE, const float* sLc, const float* sb,
+                                              const Chunk& ch, int nh, float* sp, float* sab) {
+  const int m = threadIdx.x;
+  if (m < DN) {
+    const bool ok = m < ch.M;
+    sp[m] = ok ? expf(sLc[m / nh]) : 0.f;
+    sab[m] = ok ? sE[(ch.Ct - 1) * LD + m / nh] * sb[m] : 0.f;
+  }
+}
+
+__device__ __forceinline__ void write_vectors(float* vv, const float* sLc, const float* sp,
+                                              const float* sab, const Chunk& ch) {
+  const int m = threadIdx.x;
+  if (m < DN) {
+    vv[V_AB + m] = sab[m];
+    vv[V_PT + m] = m < ch.Ct ? expf(sLc[m]) : 0.f;
+    vv[V_P + m] = sp[m];
+    if (m == 0) vv[V_PC] = expf(sLc[ch.Ct - 1]);
+  }
+}
+
+__device__ __forceinline__ float ld_l(const float* lg, int64_t bh, const DwGeom& g,
+                                      const Chunk& ch) {
+  return threadIdx.x < ch.Ct ? lg[bh * g.T + ch.t0 + threadIdx.x] : 0.f;
+}
+
+
 inline bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk, DwGeom& g,
              int64_t& BH) {
   if (B <= 0 || H <= 0 || T <= 0 || nh <= 0 || chunk <= 0) return false;
@@ -349,5 +413,16 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
                 const void* dy, const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
                 float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
                 hipStream_t stream);
+
+// Decay-gated forms (delta_gated.hip), bf16 inputs and nh = 1: lg / dlg are the
+// per-token log decay and its gradient, fp32 (B*H, T); the workspace adds a
+// vector region of VECN floats per chunk after the matrices.
+int dw_fwd_bf16_gated(const void* Q, const void* K, const void* V, const void* beta,
+                      const float* lg, const float* H0, void* y, float* HT, float* Hb, int64_t BH,
+                      const DwGeom& g, void* ws, size_t ws_bytes, hipStream_t stream);
+int dw_bwd_bf16_gated(const void* Q, const void* K, const void* V, const void* beta,
+                      const float* lg, const float* Hb, const void* dy, const float* dHT, void* dQ,
+                      void* dK, void* dV, void* dbeta, float* dlg, float* dH0, int64_t BH,
+                      const DwGeom& g, void* ws, size_t ws_bytes, hipStream_t stream);
 
 }  // namespace mgd

@@ -1,0 +1,1305 @@
+// bf16-MFMA operand machinery and the chunked-WY kernels on it (gfx950), shared by
+// the ungated entry points (delta_wy_bf16.hip) and the decay-gated ones
+// (delta_gated.hip).  Each kernel is a template on GATED; a translation unit
+// instantiates only the form it launches (one unit holding both forms allocated
+// the ungated gradient kernel's registers worse: 12 spills instead of 5).
+//
+// DeltaMinGRU chunked-WY delta rule on bf16 MFMA (gfx950), for bf16 Q, K, V, beta.
+//
+// Same algorithm, chunk geometry and workspace layout as the fp32-operand
+// kernels of delta_wy.hip (reference src/mingru/triton_scans.py:473-605 and
+// :1859-2322; the formulas are listed at the top of delta_wy.hip); what
+// changes is how the products are evaluated.
+//
+// Every product is C[i][j] = sum_k A[i][k] B[j][k] over k < 64 with both
+// operands held in LDS as 64 x 64 bf16 "row x k" matrices (BMat): the row is
+// the operand's free index and k the contracted one, stored contiguously so an
+// MFMA fragment (8 consecutive k of one row) is a single 16-byte LDS read.
+// Products run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation:
+//   - bf16 inputs (Q, K, V, dy) are exact in bf16: one MFMA per fragment pair;
+//   - fp32 intermediates (states, Tm^-1, U, G, dS, ...) are stored as a pair
+//     hi = bf16(x), lo = bf16(x - hi), and a product takes hi*hi + hi*lo + lo*hi
+//     (or in*hi + in*lo against an exact input), which keeps about 16
+//     significant bits per operand -- fp32-level results for the reference's
+//     fp32 ("ieee") products -- at 2-3 bf16 MFMAs per fp32 one it replaces,
+//     each 16x more work per cycle than v_mfma_f32_16x16x4_f32.
+#pragma once
+
+#include "mg_delta.h"
+
+namespace {
+
+using namespace mgd;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+// ---- bf16 operand matrices in LDS ------------------------------------------------
+// Row r holds 8 chunks of 8 consecutive k; chunk q sits at position
+// q ^ ((r ^ (r >> 3)) & 7) of the row.  Fragment reads (8 consecutive rows, one
+// chunk) and transposed element writes (rows 8 apart, one k) both touch 8
+// distinct 16-byte positions, i.e. all LDS banks once.
+struct BMat {
+  uint4 v[DN * 8];
+};
+
+__device__ __forceinline__ int bpos(int r, int q) { return r * 8 + (q ^ ((r ^ (r >> 3)) & 7)); }
+__device__ __forceinline__ u16* belem(BMat& m, int r, int k) {
+  return reinterpret_cast<u16*>(&m.v[bpos(r, k >> 3)]) + (k & 7);
+}
+__device__ __forceinline__ float bget(const BMat& m, int r, int k) {
+  const u16 h = reinterpret_cast<const u16*>(&m.v[bpos(r, k >> 3)])[k & 7];
+  return __uint_as_float((unsigned)h << 16);
+}
+
+__device__ __forceinline__ u16 bf_bits(float x) { return __builtin_bit_cast(u16, (__bf16)x); }
+__device__ __forceinline__ float bf_val(u16 h) { return __uint_as_float((unsigned)h << 16); }
+// x = hi + lo to about 16 significant bits (both round to nearest even).
+__device__ __forceinline__ void bf_split(float x, u16& hi, u16& lo) {
+  hi = bf_bits(x);
+  lo = bf_bits(x - bf_val(hi));
+}
+
+// Split pair (hi, lo) of an fp32 matrix.
+typedef BMat BPair[2];
+
+__device__ __forceinline__ void put_split1(BPair& m, int r, int k, float x) {
+  u16 hi, lo;
+  bf_split(x, hi, lo);
+  *belem(m[0], r, k) = hi;
+  *belem(m[1], r, k) = lo;
+}
+// Four consecutive k (k % 4 == 0): one 8-byte write per half.
+__device__ __forceinline__ void put_split4(BPair& m, int r, int k, float x0, float x1, float x2,
+                                           float x3) {
+  u16 h[4], l[4];
+  bf_split(x0, h[0], l[0]);
+  bf_split(x1, h[1], l[1]);
+  bf_split(x2, h[2], l[2]);
+  bf_split(x3, h[3], l[3]);
+  *reinterpret_cast<uint2*>(belem(m[0], r, k)) =
+      make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+  *reinterpret_cast<uint2*>(belem(m[1], r, k)) =
+      make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
+}
+// Eight consecutive k (one chunk q): one 16-byte write per half.
+__device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (&x)[8]) {
+  unsigned h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    u16 h0, l0, h1, l1;
+    bf_split(x[2 * p], h0, l0);
+    bf_split(x[2 * p + 1], h1, l1);
+    h[p] = h0 | ((unsigned)h1 << 16);
+    l[p] = l0 | ((unsigned)l1 << 16);
+  }
+  m[0].v[bpos(r, q)] = make_uint4(h[0], h[1], h[2], h[3]);
+  m[1].v[bpos(r, q)] = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// Accumulator tile (lane (g, r) holds rows R0+4g..R0+4g+3 of column C0+r) into
+// a split BMat, either as (row = tile row, k = tile column) or transposed
+// (row = tile column, k = tile row; four consecutive k per lane).
+__device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) put_split1(m, R0 + 4 * g + i, C0 + r, a[i]);
+}
+__device__ __forceinline__ void acc_put_t(BPair& m, floatx4 a, int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  put_split4(m, C0 + r, R0 + 4 * g, a[0], a[1], a[2], a[3]);
+}
+
+__device__ __forceinline__ bf16x8 bneg(bf16x8 x) {
+  uint4 u = __builtin_bit_cast(uint4, x);
+  u.x ^= 0x80008000u;
+  u.y ^= 0x80008000u;
+  u.z ^= 0x80008000u;
+  u.w ^= 0x80008000u;
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// Workgroups of the bf16 kernels: 8 waves; wave w computes the 16 x 32 output
+// block of row block rb = w % 4 and column tiles 2 ch, 2 ch + 1 (ch = w / 4).
+constexpr int NTB = 512;
+constexpr int WB = NTB / MG_WAVE;
+
+// Byte offsets of this lane's MFMA fragments inside a BMat.  Row 16 blk + r,
+// chunk q = 4 s + g sits at byte blk * 2048 + r * 128 + 16 (q ^ (r & 7) ^ (r >> 3)
+// ^ (2 blk & 7)); the wave's row block and its two column blocks are fixed, so
+// six lane constants address every fragment it reads, and each read is one
+// ds_read_b128 whose immediate offset is the matrix's LDS base.
+struct FragOff {
+  unsigned a[2];     // [s]: row block rb (A operand)
+  unsigned b[2][2];  // [s][jj]: row block 2 ch + jj (B operand)
+  int rb, ch;        // row block, column half
+
+  __device__ static __forceinline__ unsigned at(int blk, unsigned L, int r) {
+    return (unsigned)blk * 2048u + (unsigned)r * 128u + ((L ^ ((2u * blk) & 7u)) << 4);
+  }
+  __device__ __forceinline__ void init() {
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4, w = wave_id();
+    rb = w & 3;
+    ch = w >> 2;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const unsigned L = (unsigned)((4 * s + g) ^ (r & 7) ^ (r >> 3));
+      a[s] = at(rb, L, r);
+      b[s][0] = at(2 * ch, L, r);
+      b[s][1] = at(2 * ch + 1, L, r);
+    }
+  }
+};
+
+__device__ __forceinline__ bf16x8 frag_at(const BMat& m, unsigned off) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                        reinterpret_cast<const char*>(&m) + off));
+}
+
+// acc[jj] (+/-)= A[row block rb] . B[row block 2 ch + jj]^T over k < 64 (the wave's
+// 16 x 32 output block).  SA / SB: the operand is a split pair (the pointer is
+// its hi half, the lo half follows); NEG negates A.
+template <bool SA, bool SB, bool NEG = false>
+__device__ __forceinline__ void bmm(floatx4 (&acc)[2], const FragOff& F, const BMat* A,
+                                    const BMat* B) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    bf16x8 ah = frag_at(A[0], F.a[s]), al;
+    if constexpr (SA) al = frag_at(A[1], F.a[s]);
+    if constexpr (NEG) {
+      ah = bneg(ah);
+      if constexpr (SA) al = bneg(al);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const unsigned off = F.b[s][jj];
+      const bf16x8 bh = frag_at(B[0], off);
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[jj], 0, 0, 0);
+      if constexpr (SB)
+        acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[1], off), acc[jj], 0, 0, 0);
+      if constexpr (SA) acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[jj], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void zero2(floatx4 (&acc)[2]) { acc[0] = acc[1] = zero4(); }
+
+// Column sums of the wave's tile jj (over its 16 rows) into s[col]: each
+// (slot, column) is written by one lane, so reductions stay in a fixed order.
+__device__ __forceinline__ void colsum16(floatx4 v, float* s, int col) {
+  float p = v[0] + v[1] + v[2] + v[3];
+  p += __shfl_xor(p, 16);
+  p += __shfl_xor(p, 32);
+  if (lane_id() < 16) s[col] = p;
+}
+
+// ---- staging of global blocks ------------------------------------------------------
+// bf16 block (rows x cols, row stride ldg) of a row-major input: thread idx holds
+// row idx / 8, columns 8 (idx % 8) + 0..7, zero outside the block.
+struct BTile {
+  uint4 q;
+
+  __device__ __forceinline__ void load(const u16* src, int rows, int cols, int64_t ldg) {
+    const int idx = threadIdx.x, row = idx >> 3, c0 = (idx & 7) * 8;
+    if (cols == DN && ldg == DN && (((uintptr_t)src) & 15u) == 0) {
+      q = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + c0)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      u16 e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x)
+        e[x] = (row < rows && c0 + x < cols) ? src[(int64_t)row * ldg + c0 + x] : (u16)0;
+      q = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                     e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+    }
+  }
+  // (row, k = column)
+  __device__ __forceinline__ void put(BMat& m) const {
+    m.v[bpos(threadIdx.x >> 3, threadIdx.x & 7)] = q;
+  }
+  // transposed: (row = column, k = row)
+  __device__ __forceinline__ void put_t(BMat& m) const {
+    const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 8;
+    const u16* e = reinterpret_cast<const u16*>(&q);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) *belem(m, c0 + x, row) = e[x];
+  }
+};
+
+// fp32 block (rows x cols) of a padded 64 x 64 workspace matrix: thread idx holds
+// rows (idx + 512 v) / 16, columns 4 ((idx + 512 v) % 16) + 0..3, v = 0, 1; zero
+// outside the block.
+struct FTile {
+  float4 f[2];
+
+  __device__ __forceinline__ void load(const float* src, int rows, int cols) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      float4 x = row < rows ? *reinterpret_cast<const float4*>(src + row * DN + c0)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c0 + 0 >= cols) x.x = 0.f;
+      if (c0 + 1 >= cols) x.y = 0.f;
+      if (c0 + 2 >= cols) x.z = 0.f;
+      if (c0 + 3 >= cols) x.w = 0.f;
+      f[v] = x;
+    }
+  }
+  __device__ __forceinline__ void put_split(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB;
+      put_split4(m, idx >> 4, (idx & 15) * 4, f[v].x, f[v].y, f[v].z, f[v].w);
+    }
+  }
+  // transposed: (row = column, k = row)
+  __device__ __forceinline__ void put_split_t(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      put_split1(m, c0 + 0, row, f[v].x);
+      put_split1(m, c0 + 1, row, f[v].y);
+      put_split1(m, c0 + 2, row, f[v].z);
+      put_split1(m, c0 + 3, row, f[v].w);
+    }
+  }
+  // bf16 copy of the block into a row-major output with row stride ldg.
+  __device__ __forceinline__ void store_bf16(u16* dst, int rows, int cols, int64_t ldg) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+      if (row >= rows) continue;
+      const float e[4] = {f[v].x, f[v].y, f[v].z, f[v].w};
+      if (c0 + 4 <= cols && ldg == DN) {
+        *reinterpret_cast<uint2*>(dst + (int64_t)row * DN + c0) =
+            make_uint2(bf_bits(e[0]) | ((unsigned)bf_bits(e[1]) << 16),
+                       bf_bits(e[2]) | ((unsigned)bf_bits(e[3]) << 16));
+      } else {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          if (c0 + x < cols) dst[(int64_t)row * ldg + c0 + x] = bf_bits(e[x]);
+      }
+    }
+  }
+};
+
+// The wave's 16 x 32 output block (rows R0 + 4 g + i, columns C0 + 16 jj + r) into a
+// bf16 row-major output with row stride ld, keeping rows < nr and columns < nc.
+__device__ __forceinline__ void store_block_bf16(u16* dst, int64_t ld, const floatx4 (&v)[2],
+                                                 int R0, int C0, int nr, int nc) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  u16* p = dst + (int64_t)(R0 + 4 * g) * ld + C0 + r;
+  if (R0 + 16 <= nr && C0 + 32 <= nc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[0] = bf_bits(v[0][i]);
+      p[16] = bf_bits(v[1][i]);
+      p += ld;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool rok = R0 + 4 * g + i < nr;
+      if (rok && C0 + r < nc) p[0] = bf_bits(v[0][i]);
+      if (rok && C0 + 16 + r < nc) p[16] = bf_bits(v[1][i]);
+      p += ld;
+    }
+  }
+}
+
+// The wave's 16 x 32 output block into a padded 64 x 64 fp32 workspace matrix.
+__device__ __forceinline__ void store_block_f32(float* dst, const floatx4 (&v)[2], int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  float* p = dst + (R0 + 4 * g) * DN + C0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i * DN] = v[0][i];
+    p[i * DN + 16] = v[1][i];
+  }
+}
+
+// Split workspace matrix: a 64 x 64 row-major bf16 hi half followed by the lo
+// half (the 16 KB of one padded fp32 matrix slot).  Read back by the chains as
+// MFMA A fragments straight from memory.
+constexpr int SPLIT_LO = DN * DN;  // u16 offset of the lo half
+
+__device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2], int R0, int C0) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+  u16* p = dst + (R0 + 4 * g) * DN + C0 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      u16 hi, lo;
+      bf_split(v[jj][i], hi, lo);
+      p[i * DN + 16 * jj] = hi;
+      p[SPLIT_LO + i * DN + 16 * jj] = lo;
+    }
+  }
+}
+
+// Split operands from a 64 x 64 fp32 LDS matrix (row stride LD), one chunk of 8
+// k per thread: (row, k) = src[row][k], and the transposed forms (row, k) =
+// src[k][row] and src[k][row] * scale[k].
+__device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, const float* src,
+                                            const float* scale) {
+  const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = src[row * LD + 8 * q + e];
+  put_split8(m, row, q, x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = src[(8 * q + e) * LD + row];
+  put_split8(mt, row, q, x);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= scale[8 * q + e];
+  put_split8(mts, row, q, x);
+}
+
+// The serial chains carry each chunk as one affine map of the state, built
+// here in parallel over chunks (the products with K^T are done where K^T is
+// already in LDS):
+//   forward   H <- H + A H + B,     A = -K^T diag(beta) W,  B = K^T diag(beta) U0,
+//             y  = Qe H + Pu,       Qe = Q - P W,           Pu = P U0
+//   backward  dH <- dH + A' dH + b', A' = -K^T E,  b' = Q^T dy - K^T G0
+// (U = U0 - W H and G = G0 + E dH substituted into the chunk recurrences).
+// The identity part of each map stays exact: the chains add A H to H in fp32.
+
+// ---------------------------------------------------------------------------
+// forward, preparation kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked),
+//   P = (Q K^T) * beta_col * read, M1 = (beta K)^T T, M2 = P T;
+//   A = -M1 K, B = M1 V, Qe = Q - M2 K, Pu = M2 V
+//   -> A, Qe (split bf16 pairs), B, Pu (fp32) in the workspace.
+// (W = T K and U0 = T V never materialise: A = -K^T diag(beta) W = -M1 K, etc.)
+// LDS stays under 80 KB, so two workgroups share a CU.
+// GATED (per-token decay, decay tables in mg_delta.h): L and P are weighted by
+// the span factors E, M1 = (a beta K)^T T, A = -M1 (p K), Qe = ptok Q - M2 (p K),
+// and the chunk's vector region (a beta, ptok, p, PC) is written for the chains.
+// The span table lives in T's buffer until the inverse, and the split (p K)^T in
+// the buffer of T^T once M1 and M2 are formed, so the LDS plan is unchanged.
+template <bool GATED>
+__global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
+                                                    const u16* __restrict__ K,
+                                                    const u16* __restrict__ V,
+                                                    const u16* __restrict__ beta,
+                                                    const float* __restrict__ lg,
+                                                    float* __restrict__ Ao, float* __restrict__ Bo,
+                                                    float* __restrict__ Qeo,
+                                                    float* __restrict__ Puo,
+                                                    float* __restrict__ vo, DwGeom g) {
+  __shared__ BMat sKt, sVt;                    // K^T, V^T as (col; m)
+  __shared__ BMat sX[2];                       // K, Q; then P split; then M2 split
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];   // L (fp32); then T^T split
+  __shared__ uint4 sTraw[(DN * LD + 3) / 4];   // T (fp32); then (beta K)^T split; then M1 split
+  __shared__ float sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
+  float* sL = reinterpret_cast<float*>(sLraw);
+  float* sT = reinterpret_cast<float*>(sTraw);
+  float* sE = sT;  // span table until the inverse
+  float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
+        *spt = sdec + 4 * DN;
+  BMat &sK = sX[0], &sQ = sX[1];
+  BPair& sP = sX;
+  BPair& sM2 = sX;
+  BPair& sTt = *reinterpret_cast<BPair*>(sLraw);
+  BPair& sPKt = *reinterpret_cast<BPair*>(sLraw);  // (d; m) = p_m K[m][d], gated
+  BPair& sBKt = *reinterpret_cast<BPair*>(sTraw);
+  BPair& sM1 = *reinterpret_cast<BPair*>(sTraw);
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  float qv[2][4];  // Q at the wave's output positions of Qe
+  {
+    BTile tk, tv, tq;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = R0 + 4 * gg + i, d = C0 + 16 * jj + r;
+        qv[jj][i] = (t < ch.Ct && d < g.dk) ? ldf(Q, (trow0 + t) * g.dk + d) : 0.f;
+      }
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tv.put_t(sVt);
+    tq.put(sQ);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    if constexpr (GATED) {
+      const float lv = ld_l(lg, bh, g, ch);
+      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+    }
+  }
+  __syncthreads();
+  if constexpr (GATED) {
+    decay_tables<NTB>(sl, sE, sLc);
+    __syncthreads();
+    decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
+    if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
+  }
+  floatx4 pp[2];
+  {
+    floatx4 kk[2];
+    zero2(kk);
+    zero2(pp);
+    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
+    bmm<false, false>(pp, F, &sQ, &sK);  // Q K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        if constexpr (GATED) {
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + col / g.nh] : 0.f;
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + col / g.nh]
+                                             : 0.f;
+        } else {
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+        }
+      }
+      acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
+    }
+  }
+  __syncthreads();  // K and Q are free (and, gated, the span table)
+  if constexpr (GATED) write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
+  acc_put(sP, pp[0], R0, C0);  // P as (t; m): the B operand of M2^T
+  acc_put(sP, pp[1], R0, C0 + 16);
+  unit_lower_inverse(sL, sT, sY);  // ends with a barrier: sL is free
+  {
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = sT[(8 * q + e) * LD + row];
+    put_split8(sTt, row, q, x);  // (m; m') = T[m'][m]
+  }
+  __syncthreads();  // sT is free
+  {
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    const uint4 kq = sKt.v[bpos(row, q)];
+    const u16* e = reinterpret_cast<const u16*>(&kq);
+    float x[8];
+    const float* sc = GATED ? sab : sb;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = sc[8 * q + k] * bf_val(e[k]);
+    put_split8(sBKt, row, q, x);  // (d; m) = beta_m K[m][d]  (gated: a_m beta_m K[m][d])
+  }
+  __syncthreads();
+  {
+    floatx4 m1[2], m2[2];
+    zero2(m1);
+    zero2(m2);
+    bmm<true, true>(m1, F, sTt, sBKt);  // M1^T = T^T diag(beta) K   (rows m, cols d)
+    bmm<true, true>(m2, F, sTt, sP);    // M2^T = (P T)^T           (rows m, cols t)
+    __syncthreads();  // sBKt and sP are free
+    acc_put_t(sM1, m1[0], R0, C0);  // M1 as (d; m)
+    acc_put_t(sM1, m1[1], R0, C0 + 16);
+    acc_put_t(sM2, m2[0], R0, C0);  // M2 as (t; m)
+    acc_put_t(sM2, m2[1], R0, C0 + 16);
+    if constexpr (GATED) {  // T^T is free: (p K)^T as a split pair
+      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+      const uint4 kq = sKt.v[bpos(row, q)];
+      const u16* e = reinterpret_cast<const u16*>(&kq);
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = sp[8 * q + k] * bf_val(e[k]);
+      put_split8(sPKt, row, q, x);
+    }
+  }
+  __syncthreads();
+  {
+    floatx4 a2[2], b2[2], qe[2], pu[2];
+    zero2(a2);
+    zero2(b2);
+    zero2(pu);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        qe[jj][i] = GATED ? qv[jj][i] * spt[R0 + 4 * gg + i] : qv[jj][i];
+    if constexpr (GATED) {
+      bmm<true, true, true>(a2, F, sM1, sPKt);  // A = -M1 (p K)
+      bmm<true, true, true>(qe, F, sM2, sPKt);  // Qe = ptok Q - M2 (p K)
+    } else {
+      bmm<true, false, true>(a2, F, sM1, &sKt);  // A = -M1 K
+      bmm<true, false, true>(qe, F, sM2, &sKt);  // Qe = Q - M2 K
+    }
+    bmm<true, false>(b2, F, sM1, &sVt);  // B = M1 V
+    bmm<true, false>(pu, F, sM2, &sVt);  // Pu = M2 V
+    store_block_split(reinterpret_cast<u16*>(Ao + mat), a2, R0, C0);
+    store_block_f32(Bo + mat, b2, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Qeo + mat), qe, R0, C0);
+    store_block_f32(Puo + mat, pu, R0, C0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, preparation kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
+//   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
+//   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
+//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32) for the
+//      reverse chain.
+// GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
+// E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E; the
+// span table lives in T's buffer until the inverse, diag(ptok) dy in P^T's once D1
+// is formed, and the split (p K)^T in the T operand buffers for the last products.
+template <bool GATED>
+__global__ __launch_bounds__(NTB) void dwb_bwd_prep(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ beta, const float* __restrict__ lg, const u16* __restrict__ dy,
+    const float* __restrict__ Hb, float* __restrict__ Uo, float* __restrict__ Eo,
+    float* __restrict__ G0o, float* __restrict__ Apo, float* __restrict__ bpo,
+    float* __restrict__ vo, DwGeom g) {
+  __shared__ BMat sK, sKt;
+  __shared__ BPair sRt, sPt, sD1t;  // sPt later holds E^T
+  // Inputs Q, Q^T, dy^T, V and Hc^T until the inverse is formed, then the split
+  // operands T, T^T and (T diag(beta))^T.
+  __shared__ BMat sX[6];
+  __shared__ uint4 sLraw[(DN * LD + 3) / 4];  // L (fp32), then G0^T split
+  __shared__ float sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ float sb[DN];
+  __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
+  float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
+        *spt = sdec + 4 * DN;
+  float* sE = sT;  // span table until the inverse
+  float* sL = reinterpret_cast<float*>(sLraw);
+  BMat &sQ = sX[0], &sQt = sX[1], &sDyt = sX[2], &sV = sX[3];
+  BPair& sHct = *reinterpret_cast<BPair*>(&sX[4]);
+  BPair& sTn = *reinterpret_cast<BPair*>(&sX[0]);
+  BPair& sTt = *reinterpret_cast<BPair*>(&sX[2]);
+  BPair& sTbt = *reinterpret_cast<BPair*>(&sX[4]);
+  BPair& sEt = sPt;
+  BPair& sG0t = *reinterpret_cast<BPair*>(sLraw);
+  BPair& sDys = sPt;                                // (j; t) = ptok_t dy[t][j], gated
+  BPair& sPKt = *reinterpret_cast<BPair*>(&sX[0]);  // (d; m) = p_m K[m][d], gated
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  {
+    BTile tk, tv, tq, td;
+    FTile th;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tv.put(sV);
+    tq.put(sQ);
+    tq.put_t(sQt);
+    td.put_t(sDyt);
+    th.put_split_t(sHct);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    if constexpr (GATED) {
+      const float lv = ld_l(lg, bh, g, ch);
+      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+    }
+  }
+  __syncthreads();
+  if constexpr (GATED) {
+    decay_tables<NTB>(sl, sE, sLc);
+    __syncthreads();
+    decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
+    if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
+    __syncthreads();
+    write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
+  }
+  floatx4 qd[2];  // Q^T dy (gated: Q^T diag(ptok) dy), kept for b'
+  zero2(qd);
+  {
+    floatx4 kk[2], rr[2], pp[2];
+    zero2(kk);
+    zero2(rr);
+    zero2(pp);
+    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
+    if constexpr (GATED)
+      bmm<false, true>(rr, F, &sK, sHct);  // K Hc
+    else
+      bmm<false, true, true>(rr, F, &sK, sHct);  // -K Hc
+    bmm<false, false>(pp, F, &sQ, &sK);  // Q K^T
+    if constexpr (!GATED) bmm<false, false>(qd, F, &sQt, &sDyt);  // Q^T dy
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        if constexpr (GATED) {
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + col / g.nh] : 0.f;
+          rr[jj][i] = fmaf(-sp[row], rr[jj][i], bget(sV, row, col));
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + col / g.nh]
+                                             : 0.f;
+        } else {
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
+          rr[jj][i] += bget(sV, row, col);
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+        }
+      }
+      acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
+      acc_put_t(sRt, rr[jj], R0, cj);
+      acc_put_t(sPt, pp[jj], R0, cj);
+    }
+  }
+  __syncthreads();
+  {
+    floatx4 d1[2];
+    zero2(d1);
+    bmm<true, false>(d1, F, sPt, &sDyt);  // P^T dy
+    acc_put_t(sD1t, d1[0], R0, C0);
+    acc_put_t(sD1t, d1[1], R0, C0 + 16);
+  }
+  if constexpr (GATED) {
+    __syncthreads();  // P^T is free: diag(ptok) dy as a split pair, then Q^T of it
+    {
+      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+      const uint4 dq = sDyt.v[bpos(row, q)];
+      const u16* e = reinterpret_cast<const u16*>(&dq);
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = spt[8 * q + k] * bf_val(e[k]);
+      put_split8(sDys, row, q, x);
+    }
+    __syncthreads();
+    bmm<false, true>(qd, F, &sQt, sDys);  // Q^T diag(ptok) dy
+  }
+  unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes; sL and sPt are free
+  stage_split(sTn, sTt, sTbt, sT, GATED ? sab : sb);
+  __syncthreads();
+  {
+    floatx4 u[2], e[2], g0[2];
+    zero2(u);
+    zero2(e);
+    zero2(g0);
+    bmm<true, true>(u, F, sTn, sRt);     // U = T R
+    bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K   (rows m, cols d)
+    bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1           (rows m, cols j)
+    store_block_f32(Uo + mat, u, R0, C0);
+    store_block_split(reinterpret_cast<u16*>(Eo + mat), e, R0, C0);
+    store_block_f32(G0o + mat, g0, R0, C0);
+    acc_put_t(sEt, e[0], R0, C0);
+    acc_put_t(sEt, e[1], R0, C0 + 16);
+    acc_put_t(sG0t, g0[0], R0, C0);
+    acc_put_t(sG0t, g0[1], R0, C0 + 16);
+  }
+  __syncthreads();
+  if constexpr (GATED) {  // the T operands are free: (p K)^T as a split pair
+    {
+      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+      const uint4 kq = sKt.v[bpos(row, q)];
+      const u16* e = reinterpret_cast<const u16*>(&kq);
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = sp[8 * q + k] * bf_val(e[k]);
+      put_split8(sPKt, row, q, x);
+    }
+    __syncthreads();
+    floatx4 a2[2];
+    zero2(a2);
+    bmm<true, true, true>(a2, F, sPKt, sEt);   // A' = -(p K)^T E
+    bmm<true, true, true>(qd, F, sPKt, sG0t);  // b' = Q^T diag(ptok) dy - (p K)^T G0
+    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
+    store_block_f32(bpo + mat, qd, R0, C0);
+  } else {
+    floatx4 a2[2];
+    zero2(a2);
+    bmm<false, true, true>(a2, F, &sKt, sEt);    // A' = -K^T E
+    bmm<false, true, true>(qd, F, &sKt, sG0t);   // b' = Q^T dy - K^T G0
+    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
+    store_block_f32(bpo + mat, qd, R0, C0);
+  }
+}
+
+// A fragments of a row-major bf16 input block (rows x cols, row stride ld):
+// row `row`, chunks g and 4 + g, zero outside the block.
+__device__ __forceinline__ void load_in_frag(uint4 (&a)[2], const u16* src, int64_t ld, int row,
+                                             int rows, int cols) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int c0 = 8 * (4 * s + g);
+    const u16* p = src + (int64_t)row * ld + c0;
+    if (row < rows && c0 + 8 <= cols && ld == DN) {
+      a[s] = *reinterpret_cast<const uint4*>(p);
+    } else {
+      u16 e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) e[x] = (row < rows && c0 + x < cols) ? p[x] : (u16)0;
+      a[s] = make_uint4(e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16),
+                        e[4] | ((unsigned)e[5] << 16), e[6] | ((unsigned)e[7] << 16));
+    }
+  }
+}
+
+// acc[jj] += A . B[row block 2 ch + jj]^T with A an exact bf16 operand whose two
+// fragments (the wave's rows, chunks g and 4 + g) are held in registers.
+template <bool SB>
+__device__ __forceinline__ void rmm(floatx4 (&acc)[2], const FragOff& F, const uint4 (&a)[2],
+                                    const BMat* B) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 ah = __builtin_bit_cast(bf16x8, a[s]);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[0], F.b[s][jj]), acc[jj], 0, 0, 0);
+      if constexpr (SB)
+        acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[1], F.b[s][jj]), acc[jj], 0, 0, 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, gradient kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   G = G0 + E dHn, dV = G
+//   S = Q K^T, dP = dy U^T, dS = dP * beta_col * read         (rows t, cols m)
+//   dQ = dy Hc^T + dS K
+//   dT = -G U^T, D2 = dT * beta_col * strict + (dT * beta_col * strict)^T
+//   dK = dS^T Q - G Hc^T + D2 K + beta_row (U dHn^T)
+//   dbeta_m = sum_t dP S read + sum_i dT KK strict + sum_d K[m][d] (U dHn^T)[m][d]
+// Q and dy enter the products as A fragments straight from memory; the split
+// operands rotate through three 16 KB regions, so LDS stays under 80 KB (two
+// workgroups per CU).  D2 is symmetrised in registers from dT and dT^T = -U G^T.
+// GATED (nh = 1, decay tables in mg_delta.h): the products are weighted as in
+// the forward -- dS = (dy U^T) beta_col E_read, D2 = (-G U^T) beta E_mm (both
+// triangles), dQ = diag(ptok) dy Hc^T + dS K, dK = -diag(p) G Hc^T + dS^T Q + D2 K
+// + diag(a beta) U dHn^T, dbeta's U (K dHn) term times a -- and the span
+// gradients F[t][t'] = dP P + dT L (token level, registers), the row Ct-1 term
+// a beta rowsum(U (K dHn)) and f[t] (ptok: ptok_t sum_d Q (dy Hc^T), p: p_m
+// sum_d K (-G Hc^T), PC: PC <dHn, Hc>) give dl_s = sum_{t >= s} (f[t] +
+// sum_{t' < s} F[t][t']) by wave-level prefix scans.  The span table needs its
+// own 16 KB, so a gated workgroup has the CU to itself.
+template <bool GATED>
+__global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
+    const float* __restrict__ lg, const u16* __restrict__ dy, const float* __restrict__ Hb,
+    const float* __restrict__ dHn, const float* __restrict__ Um, const float* __restrict__ Em,
+    const float* __restrict__ G0m, u16* __restrict__ dQ, u16* __restrict__ dK,
+    u16* __restrict__ dV, u16* __restrict__ dbeta, float* __restrict__ dlg, DwGeom g) {
+  __shared__ BMat sK, sKt, sQt;  // exact inputs
+  // Split regions: [E, dHn^T] -> [G, U, Hc] -> [dS, U, dS^T] -> [D2, U, dHn].
+  __shared__ BPair sR[3];
+  __shared__ float sb[DN];
+  // dbeta partials: [0..3] read-term column sums per row block, [4..7] strict-term
+  // column sums per row block, [8..9] row sums of K * (U dHn^T) per column half.
+  __shared__ float sdb[10][DN];
+  // gated: span table; l, Lc, p, a beta, a, ptok; f partials (ptok and p terms per
+  // column half); <dHn, Hc> per wave; dl partials per wave.
+  __shared__ float sEg[GATED ? DN * LD : 1];
+  __shared__ float sdec[GATED ? 6 * DN : 1];
+  __shared__ float sfp[GATED ? 4 * DN : 1];
+  __shared__ float sred[GATED ? WB : 1];
+  __shared__ float sdl[GATED ? WB * DN : 1];
+  float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
+        *sa = sdec + 4 * DN, *spt = sdec + 5 * DN;
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  floatx4 gacc[2];
+  {
+    BTile tk, tq;
+    FTile tn;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    tn.load(dHn + mat, g.dk, g.dv);
+    const u16* es = reinterpret_cast<const u16*>(Em + mat);
+    const int erow = threadIdx.x >> 3, eq = threadIdx.x & 7;
+    const uint4 ehi = *reinterpret_cast<const uint4*>(es + erow * DN + 8 * eq);
+    const uint4 elo = *reinterpret_cast<const uint4*>(es + SPLIT_LO + erow * DN + 8 * eq);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) gacc[jj] = acc_load_ws(G0m + mat + R0 * DN + C0 + 16 * jj);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tk.put_t(sKt);
+    tq.put_t(sQt);
+    sR[0][0].v[bpos(erow, eq)] = ehi;
+    sR[0][1].v[bpos(erow, eq)] = elo;
+    tn.put_split_t(sR[1]);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    if constexpr (GATED) {
+      const float lv = ld_l(lg, bh, g, ch);
+      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+    }
+  }
+  __syncthreads();
+  if constexpr (GATED) {
+    decay_tables<NTB>(sl, sEg, sLc);
+    __syncthreads();
+    decay_vectors(sEg, sLc, sb, ch, g.nh, sp, sab);
+    if (threadIdx.x < DN) {
+      const int m = threadIdx.x;
+      spt[m] = m < ch.Ct ? expf(sLc[m]) : 0.f;
+      sa[m] = m < ch.M ? sEg[(ch.Ct - 1) * LD + m] : 0.f;
+    }
+  }
+  {
+    // U and Hc are fetched while G forms, and staged once E and dHn^T are free.
+    FTile tu, th;
+    tu.load(Um + mat, ch.M, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    bmm<true, true>(gacc, F, sR[0], sR[1]);  // G = G0 + E dHn   (rows m, cols j)
+    store_block_bf16(dV + row0 * g.dv, g.dv, gacc, R0, C0, ch.M, g.dv);
+    if constexpr (GATED) {  // <dHn, Hc> from two fp32 tiles of the same layout
+      FTile tn2;
+      tn2.load(dHn + mat, g.dk, g.dv);
+      float part = 0.f;
+#pragma unroll
+      for (int v = 0; v < 2; ++v)
+        part += tn2.f[v].x * th.f[v].x + tn2.f[v].y * th.f[v].y + tn2.f[v].z * th.f[v].z +
+                tn2.f[v].w * th.f[v].w;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+      if (lane == 0) sred[wave_id()] = part;
+    }
+    __syncthreads();
+    acc_put(sR[0], gacc[0], R0, C0);  // G as (m; j)
+    acc_put(sR[0], gacc[1], R0, C0 + 16);
+    tu.put_split(sR[1]);              // U as (m; j)
+    th.put_split(sR[2]);              // Hc as (d; j)
+  }
+  uint4 qf[2], yf[2];  // Q and dy fragments of the wave's rows t
+  load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
+  load_in_frag(yf, dy + trow0 * g.dv, g.dv, R0 + r, ch.Ct, g.dv);
+  __syncthreads();
+  BPair &sG = sR[0], &sU = sR[1], &sHc = sR[2];
+  floatx4 ds2[2], d2[2], dq[2], dk[2];
+  floatx4 f2[2];  // gated: span gradients F at the wave's (t, t') positions
+  {
+    floatx4 s2[2], dp2[2];
+    zero2(s2);
+    zero2(dp2);
+    rmm<false>(s2, F, qf, &sK);  // S = Q K^T
+    rmm<true>(dp2, F, yf, sU);   // dP = dy U^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+      floatx4 db;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = R0 + 4 * gg + i, m = cj + r;
+        const bool rd = m < (t + 1) * g.nh;
+        if constexpr (GATED) {
+          const float er = rd ? sEg[t * LD + m] : 0.f;
+          ds2[jj][i] = dp2[jj][i] * sb[m] * er;
+          db[i] = dp2[jj][i] * s2[jj][i] * er;
+          f2[jj][i] = db[i] * sb[m];
+        } else {
+          ds2[jj][i] = rd ? dp2[jj][i] * sb[m] : 0.f;
+          db[i] = rd ? dp2[jj][i] * s2[jj][i] : 0.f;
+        }
+      }
+      colsum16(db, sdb[F.rb], cj + r);
+    }
+  }
+  {
+    floatx4 dt2[2], dtt2[2], kk2[2];
+    zero2(dt2);
+    zero2(dtt2);
+    zero2(kk2);
+    bmm<true, true, true>(dt2, F, sG, sU);   // dT = -G U^T
+    bmm<true, true, true>(dtt2, F, sU, sG);  // dT^T = -U G^T
+    bmm<false, false>(kk2, F, &sK, &sK);     // K K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+      floatx4 db;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = R0 + 4 * gg + i, j = cj + r;
+        if constexpr (GATED) {
+          const float elo = j < m ? sEg[m * LD + j] : 0.f, ehi = m < j ? sEg[j * LD + m] : 0.f;
+          d2[jj][i] = j < m ? dt2[jj][i] * sb[j] * elo : dtt2[jj][i] * sb[m] * ehi;
+          db[i] = dt2[jj][i] * kk2[jj][i] * elo;
+          f2[jj][i] += db[i] * sb[j];
+        } else {
+          d2[jj][i] = j < m ? dt2[jj][i] * sb[j] : (m < j ? dtt2[jj][i] * sb[m] : 0.f);
+          db[i] = j < m ? dt2[jj][i] * kk2[jj][i] : 0.f;
+        }
+      }
+      colsum16(db, sdb[4 + F.rb], cj + r);
+    }
+  }
+  zero2(dq);
+  zero2(dk);
+  rmm<true>(dq, F, yf, sHc);              // dy Hc^T
+  bmm<true, true, true>(dk, F, sG, sHc);  // -G Hc^T
+  if constexpr (GATED) {
+    // f terms: ptok_t sum_d Q[t][d] (dy Hc^T)[t][d] and p_m sum_d K[m][d] (-G Hc^T)[m][d],
+    // then the row scalings diag(ptok) and diag(p) of those two products.
+    float fq[4], fpv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = R0 + 4 * gg + i;
+      float a = 0.f, b = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int d = C0 + 16 * jj + r;
+        a = fmaf(bget(sQt, d, row), dq[jj][i], a);
+        b = fmaf(bget(sK, row, d), dk[jj][i], b);
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        a += __shfl_xor(a, o);
+        b += __shfl_xor(b, o);
+      }
+      fq[i] = a;
+      fpv[i] = b;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        dq[jj][i] *= spt[row];
+        dk[jj][i] *= sp[row];
+      }
+    }
+    if (r == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i;
+        sfp[F.ch * DN + row] = spt[row] * fq[i];
+        sfp[(2 + F.ch) * DN + row] = sp[row] * fpv[i];
+      }
+    }
+  }
+  __syncthreads();  // G and Hc are free
+  acc_put(sR[0], ds2[0], R0, C0);  // dS as (t; m)
+  acc_put(sR[0], ds2[1], R0, C0 + 16);
+  acc_put_t(sR[2], ds2[0], R0, C0);  // dS^T as (m; t)
+  acc_put_t(sR[2], ds2[1], R0, C0 + 16);
+  __syncthreads();
+  FTile tn;  // dHn again (an L2 hit), fetched while the dS products run
+  tn.load(dHn + mat, g.dk, g.dv);
+  bmm<true, false>(dq, F, sR[0], &sKt);  // + dS K
+  bmm<true, false>(dk, F, sR[2], &sQt);  // + dS^T Q
+  store_block_bf16(dQ + trow0 * g.dk, g.dk, dq, R0, C0, ch.Ct, g.dk);
+  __syncthreads();  // dS and dS^T are free
+  acc_put_t(sR[0], d2[0], R0, C0);  // D2 (symmetric)
+  acc_put_t(sR[0], d2[1], R0, C0 + 16);
+  tn.put_split(sR[2]);  // dHn as (d; j)
+  __syncthreads();
+  {
+    floatx4 bu2[2];
+    zero2(bu2);
+    bmm<true, false>(dk, F, sR[0], &sKt);  // + D2 K
+    bmm<true, true>(bu2, F, sU, sR[2]);    // U dHn^T
+    float rowp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = R0 + 4 * gg + i;
+      const float sc = GATED ? sab[m] : sb[m];
+      dk[0][i] += sc * bu2[0][i];
+      dk[1][i] += sc * bu2[1][i];
+      rowp[i] = bget(sK, m, C0 + r) * bu2[0][i] + bget(sK, m, C0 + 16 + r) * bu2[1][i];
+      rowp[i] += __shfl_xor(rowp[i], 1);
+      rowp[i] += __shfl_xor(rowp[i], 2);
+      rowp[i] += __shfl_xor(rowp[i], 4);
+      rowp[i] += __shfl_xor(rowp[i], 8);
+    }
+    store_block_bf16(dK + row0 * g.dk, g.dk, dk, R0, C0, ch.M, g.dk);
+    if (r == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sdb[8 + F.ch][R0 + 4 * gg + i] = rowp[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < ch.M) {
+    const int m = threadIdx.x;
+    float acc = sdb[8][m] + sdb[9][m];
+    if constexpr (GATED) acc *= sa[m];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc += sdb[q][m];
+    stf(dbeta, row0 + m, acc);
+  }
+  if constexpr (GATED) {
+    // Token-level F (t' < t) into U's buffer, plus the carry term on row Ct - 1;
+    // f[t] in sdec's l slot.
+    float* sF = reinterpret_cast<float*>(&sR[1]);  // 64 x 64, stride DN
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = R0 + 4 * gg + i, tp = C0 + 16 * jj + r;
+        sF[t * DN + tp] = (tp < t && t < ch.Ct) ? f2[jj][i] : 0.f;
+      }
+    __syncthreads();
+    if (threadIdx.x < DN) {
+      const int t = threadIdx.x;
+      if (t < ch.Ct - 1)
+        sF[(ch.Ct - 1) * DN + t] += sab[t] * (sdb[8][t] + sdb[9][t]);
+      float f = 0.f;
+      if (t < ch.Ct) {
+        f = sfp[t] + sfp[DN + t] + sfp[2 * DN + t] + sfp[3 * DN + t];
+        if (t == ch.Ct - 1) {
+          float pcs = 0.f;
+#pragma unroll
+          for (int q = 0; q < WB; ++q) pcs += sred[q];
+          f = fmaf(expf(sLc[t]), pcs, f);
+        }
+      }
+      sl[t] = f;
+    }
+    __syncthreads();
+    // dl_s = sum_{t >= s} (f[t] + sum_{t' < s} F[t][t']): wave-level prefix scans of
+    // the rows of F, per-wave column partials summed in a fixed order.
+    {
+      constexpr int ROWS = DN / WB;
+      const int w = wave_id();
+      float acc = 0.f;
+      for (int rr = 0; rr < ROWS; ++rr) {
+        const int t = ROWS * w + rr;
+        float x = sF[t * DN + lane];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float y = __shfl_up(x, d);
+          if (lane >= d) x += y;
+        }
+        float ex = __shfl_up(x, 1);
+        if (lane == 0) ex = 0.f;
+        if (t >= lane && t < ch.Ct) acc += sl[t] + ex;
+      }
+      sdl[w * DN + lane] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < ch.Ct) {
+      const int s = threadIdx.x;
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < WB; ++q) acc += sdl[q * DN + s];
+      dlg[trow0 + s] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// serial chains: one workgroup of 4 waves per (head, 16-column d_v slice)
+// ---------------------------------------------------------------------------
+// Wave w keeps the state rows 16 w .. 16 w + 15 of the slice in an MFMA
+// accumulator.  The chunk maps (A, Qe split; B, Pu fp32) are loaded straight
+// into registers two chunks ahead; the state's transpose H^T passes through
+// LDS (double-buffered, one barrier per chunk).
+
+// LDS fragment offsets of rows 0..15 (lane row r, chunk 4 s + g).
+struct RowFrag {
+  unsigned o[2];
+  __device__ __forceinline__ void init() {
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) o[s] = FragOff::at(0, (unsigned)((4 * s + g) ^ (r & 7) ^ (r >> 3)), r);
+  }
+};
+
+__device__ __forceinline__ bf16x8 as_bf(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// acc += A B^T, A split in registers ([s] fragments), B a split 16-row BMat pair.
+__device__ __forceinline__ floatx4 amm(floatx4 acc, const uint4 (&ah)[2], const uint4 (&al)[2],
+                                       const BMat* B, const RowFrag& rf) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 bh = frag_at(B[0], rf.o[s]), bl = frag_at(B[1], rf.o[s]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[s]), bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al[s]), bh, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Two independent products against the same B (the chain's state update and
+// readout): each B fragment is read once and the two MFMA chains interleave.
+__device__ __forceinline__ void amm2(floatx4& acc0, const uint4 (&ah0)[2], const uint4 (&al0)[2],
+                                     floatx4& acc1, const uint4 (&ah1)[2], const uint4 (&al1)[2],
+                                     const BMat* B, const RowFrag& rf) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bf16x8 bh = frag_at(B[0], rf.o[s]), bl = frag_at(B[1], rf.o[s]);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah0[s]), bh, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah1[s]), bh, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah0[s]), bl, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah1[s]), bl, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al0[s]), bh, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al1[s]), bh, acc1, 0, 0, 0);
+  }
+}
+
+// A fragments of a split workspace matrix: row `row`, chunks g and 4 + g.
+__device__ __forceinline__ void load_split_frag(uint4 (&hi)[2], uint4 (&lo)[2], const u16* m,
+                                                int row) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    hi[s] = *reinterpret_cast<const uint4*>(m + row * DN + 8 * (4 * s + g));
+    lo[s] = *reinterpret_cast<const uint4*>(m + SPLIT_LO + row * DN + 8 * (4 * s + g));
+  }
+}
+
+struct FwdOps {
+  uint4 ah[2], al[2], qh[2], ql[2];
+  floatx4 b, pu;
+  float pc;  // gated: the chunk's total decay PC
+};
+
+//   H_c saved, y = Qe H_c + Pu, H_{c+1} = H_c + A H_c + B (gated: PC H_c + A H_c + B).
+template <bool GATED>
+__global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0,
+                                                    const float* __restrict__ Am,
+                                                    const float* __restrict__ Bm,
+                                                    const float* __restrict__ Qem,
+                                                    const float* __restrict__ Pum,
+                                                    const float* __restrict__ vm,
+                                                    u16* __restrict__ y, float* __restrict__ HT,
+                                                    float* __restrict__ Hb, DwGeom g, int64_t BH) {
+  __shared__ BPair sHt[2];
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  RowFrag rf;
+  rf.init();
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  auto fetch = [&](FwdOps& o, int c) {
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Am + mat), 16 * w + r);
+    load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), 16 * w + r);
+    o.b = acc_load_ws(Bm + mat + 16 * w * DN + col0);
+    o.pu = acc_load_ws(Pum + mat + 16 * w * DN + col0);
+    if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
+  };
+  // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
+  // ring, the loop unrolled by three so the buffers never move.
+  auto step = [&](const FwdOps& cur, FwdOps& fill, int c) {
+    if (c + 2 < g.nc) fetch(fill, c + 2);
+    const Chunk ch = chunk_of(g, c);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    BPair& ht = sHt[c & 1];
+    acc_put_t(ht, h, 16 * w, 0);
+    acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
+    __syncthreads();
+    floatx4 yy = cur.pu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = GATED ? fmaf(cur.pc, h[i], cur.b[i]) : h[i] + cur.b[i];
+    amm2(h, cur.ah, cur.al, yy, cur.qh, cur.ql, ht, rf);  // H + A H + B, y = Qe H + Pu
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * gg + i;
+      if (t < ch.Ct && col < g.dv) y[(bh * g.T + ch.t0 + t) * g.dv + col] = bf_bits(yy[i]);
+    }
+  };
+  FwdOps b0, b1, b2;
+  fetch(b0, 0);
+  if (g.nc > 1) fetch(b1, 1);
+  int c = 0;
+  for (; c + 3 <= g.nc; c += 3) {
+    step(b0, b2, c);
+    step(b1, b0, c + 1);
+    step(b2, b1, c + 2);
+  }
+  if (c < g.nc) step(b0, b2, c);
+  if (c + 1 < g.nc) step(b1, b0, c + 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) HT[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
+struct BwdOps {
+  uint4 ah[2], al[2];
+  floatx4 b;
+  float pc;  // gated: the chunk's total decay PC
+};
+
+//   dH (chunk exit) saved, dH <- dH + A' dH + b' (gated: PC dH + A' dH + b').
+template <bool GATED>
+__global__ __launch_bounds__(NT) void dwb_bwd_chain(const float* __restrict__ dHT,
+                                                    const float* __restrict__ Apm,
+                                                    const float* __restrict__ bpm,
+                                                    const float* __restrict__ vm,
+                                                    float* __restrict__ dHn,
+                                                    float* __restrict__ dH0, DwGeom g,
+                                                    int64_t BH) {
+  __shared__ BPair sHt[2];
+  int64_t bh;
+  int col0;
+  if (!chain_slot(g, BH, bh, col0)) return;
+  const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int col = col0 + r;
+  RowFrag rf;
+  rf.init();
+  floatx4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
+  }
+  auto fetch = [&](BwdOps& o, int c) {
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), 16 * w + r);
+    o.b = acc_load_ws(bpm + mat + 16 * w * DN + col0);
+    if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
+  };
+  // Chunk c - 2 is fetched while chunk c computes (ring of three buffers).
+  auto step = [&](const BwdOps& cur, BwdOps& fill, int c) {
+    if (c >= 2) fetch(fill, c - 2);
+    const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+    BPair& ht = sHt[c & 1];
+    acc_put_t(ht, h, 16 * w, 0);
+    acc_store_ws(h, dHn + mat + 16 * w * DN + col0);
+    __syncthreads();
+    floatx4 hn;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hn[i] = GATED ? fmaf(cur.pc, h[i], cur.b[i]) : h[i] + cur.b[i];
+    h = amm(hn, cur.ah, cur.al, ht, rf);
+  };
+  BwdOps b0, b1, b2;
+  fetch(b0, g.nc - 1);
+  if (g.nc > 1) fetch(b1, g.nc - 2);
+  int c = g.nc - 1;
+  for (; c - 2 >= 0; c -= 3) {
+    step(b0, b2, c);
+    step(b1, b0, c - 1);
+    step(b2, b1, c - 2);
+  }
+  if (c >= 0) step(b0, b2, c);
+  if (c - 1 >= 0) step(b1, b0, c - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 16 * w + 4 * gg + i;
+    if (d < g.dk && col < g.dv) dH0[(bh * g.dk + d) * g.dv + col] = h[i];
+  }
+}
+
+}  // namespace

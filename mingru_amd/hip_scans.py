@@ -842,42 +842,48 @@ def delta_scan_impl(Q, K, V, beta, H0, *, chunk_size: int):
 class _DeltaGatedScanFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, beta, log_gamma, H0, chunk_size):
-        q, k, v, bt, lg, h0 = (_contig(t, torch.float32) for t in (Q, K, V, beta, log_gamma, H0))
+        # bf16 inputs with nh = 1 read natively (bf16 MFMA); everything else in fp32.
+        nh = K.shape[3]
+        cdt = _delta_compute_dtype(Q, K, V, beta) if nh == 1 else torch.float32
+        q, k, v, bt = (_contig(t, cdt) for t in (Q, K, V, beta))
+        lg, h0 = _contig(log_gamma, torch.float32), _contig(H0, torch.float32)
         Bn, nhd, T, d_k = q.shape
-        nh = k.shape[3]
         d_v = v.shape[4]
         lib = _lib()
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
-        y = torch.empty(Bn, nhd, T, d_v, dtype=torch.float32, device=q.device)
+        y = torch.empty(Bn, nhd, T, d_v, dtype=cdt, device=q.device)
         HT = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
         Hb = torch.empty(max(int(lib.mg_delta_state_bytes(*dims)), 16) // 4, dtype=torch.float32,
                          device=q.device)
         ws = _workspace(lib.mg_delta_gated_workspace_bytes(*dims), q.device)
+        tag = 1 if cdt == torch.bfloat16 else 0
         _call("mg_delta_gated_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(h0),
-              _ptr(y), _ptr(HT), _ptr(Hb), *dims, _ptr(ws), ws.numel(), _stream(q))
+              _ptr(y), _ptr(HT), _ptr(Hb), *dims, tag, _ptr(ws), ws.numel(), _stream(q))
         ctx.save_for_backward(q, k, v, bt, lg, Hb)
-        ctx.meta = (chunk_size, Q.dtype, K.dtype, V.dtype, beta.dtype, log_gamma.dtype, H0.dtype)
+        ctx.meta = (chunk_size, cdt, Q.dtype, K.dtype, V.dtype, beta.dtype, log_gamma.dtype,
+                    H0.dtype)
         return y.to(Q.dtype), HT.to(H0.dtype)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gy, gHT):
         q, k, v, bt, lg, Hb = ctx.saved_tensors
-        chunk_size, qdt, kdt, vdt, bdt, ldt, hdt = ctx.meta
+        chunk_size, cdt, qdt, kdt, vdt, bdt, ldt, hdt = ctx.meta
         Bn, nhd, T, d_k = q.shape
         nh = k.shape[3]
         d_v = v.shape[4]
-        dy = (torch.zeros(Bn, nhd, T, d_v, dtype=torch.float32, device=q.device) if gy is None
-              else _contig(gy, torch.float32))
+        dy = (torch.zeros(Bn, nhd, T, d_v, dtype=cdt, device=q.device) if gy is None
+              else _contig(gy, cdt))
         dHT = (torch.zeros(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
                if gHT is None else _contig(gHT, torch.float32))
         dQ, dK, dV, dbeta, dlg = (torch.empty_like(t) for t in (q, k, v, bt, lg))
         dH0 = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
         ws = _workspace(_lib().mg_delta_gated_workspace_bytes(*dims), q.device)
+        tag = 1 if cdt == torch.bfloat16 else 0
         _call("mg_delta_gated_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(Hb),
               _ptr(dy), _ptr(dHT), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dbeta), _ptr(dlg),
-              _ptr(dH0), *dims, _ptr(ws), ws.numel(), _stream(q))
+              _ptr(dH0), *dims, tag, _ptr(ws), ws.numel(), _stream(q))
         return (dQ.to(qdt), dK.to(kdt), dV.to(vdt), dbeta.to(bdt), dlg.to(ldt), dH0.to(hdt),
                 None)
 
@@ -888,9 +894,10 @@ def delta_gated_scan_impl(Q, K, V, beta, log_gamma, H0, *, chunk_size: int):
     No reference kernel: the reference runs this eagerly
     (``_forward_chunked_gated``, ``src/mingru/min_gru.py:3257-3448``).  Layouts
     as ``delta_scan_impl`` plus ``log_gamma`` ``(B, n_heads, T)``, the per-token
-    log decay applied to the state before the token's micro-steps.  The kernels
-    compute in fp32 (half inputs are upcast); ``y`` comes back in Q's dtype and
-    ``H_T`` in H0's.  Differentiable in all six tensors.
+    log decay applied to the state before the token's micro-steps.  bf16 Q, K, V,
+    beta with ``nh = 1`` run the bf16-MFMA kernels (fp32 state); other inputs and
+    ``nh > 1`` run in fp32 (half inputs are upcast).  ``y`` comes back in Q's dtype
+    and ``H_T`` in H0's.  Differentiable in all six tensors.
     """
     _delta_validate_envelope(Q, K, V, beta, H0, chunk_size)
     if tuple(log_gamma.shape) != tuple(Q.shape[:3]):

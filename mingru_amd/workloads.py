@@ -139,10 +139,10 @@ def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
                 H0=torch.zeros(B, H, d, d), chunk_size=chunk, grad_y=dy, grad_HT=dHT)
 
 
-def c5d_inputs(B=8, H=8, T=8192, d=64, chunk=64):
-    """C5 heads with per-token decay for the gated delta kernels (fp32, the dtype they
-    compute in): ``log gamma = -0.5 U(0, 1)`` per (head, token), the span a fixed
-    decay rate of 0.5 gives over unit-scale gaps."""
-    inp = c5_inputs(B, H, T, d, chunk, dtype=torch.float32)
+def c5d_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
+    """C5 heads (bf16, as C5) with per-token decay for the gated delta kernels:
+    ``log gamma = -0.5 U(0, 1)`` per (head, token) in fp32, the span a fixed decay
+    rate of 0.5 gives over unit-scale gaps."""
+    inp = c5_inputs(B, H, T, d, chunk, dtype=dtype)
     inp["log_gamma"] = -0.5 * torch.rand(B, H, T, generator=_gen(1015))
     return inp

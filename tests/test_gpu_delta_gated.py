@@ -159,3 +159,68 @@ def _graph_nodes(fn, seen=None):
         seen.add(f)
         yield f
         stack.extend(n for n, _ in f.next_functions)
+
+
+# bf16 Q, K, V, beta with nh = 1 run the gated bf16-MFMA kernels.  Bars as for the
+# ungated bf16 path: bf16 outputs (y, dQ, dK, dV, dbeta) within 2e-2 of the largest
+# reference magnitude (the oracle sees the same bf16-rounded inputs); the fp32
+# outputs (H_T, dH0, dlog_gamma) within 1e-4 of it.
+BF16_REL = 2e-2
+SPLIT_REL = 1e-4
+
+BF16_CASES = [
+    # B, H, T, dk, dv, chunk, log-gamma kind
+    (1, 1, 1, 4, 4, 4, "mod"),
+    (2, 2, 100, 16, 16, 16, "mod"),
+    (1, 3, 128, 64, 64, 64, "mod"),
+    (2, 1, 130, 32, 48, 32, "spikes"),
+    (1, 2, 300, 64, 64, 64, "weak"),
+    (2, 2, 200, 64, 64, 64, "spikes"),
+    (1, 2, 70, 24, 40, 20, "zero"),
+]
+
+
+def _rel(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(_np(got) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+@pytest.mark.parametrize("case", BF16_CASES)
+def test_delta_gated_bf16_matches_oracle(cuda, case):
+    B, H, T, dk, dv, C, kind = case
+    print(f"[gpu] delta gated bf16 case={case}", flush=True)
+    Q, K, V, beta, lg, H0, dy, dHT = _inputs(B, H, T, 1, dk, dv, seed=41 + T, lg_kind=kind)
+    Q, K, V, beta, dy = (t.to(torch.bfloat16) for t in (Q, K, V, beta, dy))
+    y, HT, grads = _run((Q, K, V, beta, lg, H0), dy, dHT, C, cuda)
+    assert y.dtype == torch.bfloat16 and grads[0].dtype == torch.bfloat16
+    assert grads[4].dtype == torch.float32
+    ref = [_np(t) for t in (Q, K, V, beta, lg, H0)]
+    ry, rHT = orc.delta_gated_sequential(*ref)
+    assert _rel(y, ry) <= BF16_REL
+    assert _rel(HT, rHT) <= SPLIT_REL, f"H_T rel err {_rel(HT, rHT):.3e}"
+    rg = orc.delta_gated_sequential_bwd(*ref, _np(dy), _np(dHT))
+    for name, gk, gr in zip(("dQ", "dK", "dV", "dbeta", "dlog_gamma", "dH0"), grads, rg):
+        assert torch.isfinite(gk.float()).all(), name
+        bar = SPLIT_REL if name in ("dlog_gamma", "dH0") else BF16_REL
+        assert _rel(gk, gr) <= bar, f"{name} rel err {_rel(gk, gr):.3e}"
+
+
+def test_delta_gated_bf16_c5_heads(cuda):
+    """The C5d workload in bf16 (B=8, H=8, T=8192, d=64, chunk 64): two heads at full
+    length against the oracle."""
+    from mingru_amd import workloads as wl
+
+    print("[gpu] delta gated bf16 C5 heads", flush=True)
+    inp = wl.c5d_inputs(**wl.C5)
+    Q, K, V, beta = (inp[k].to(torch.bfloat16) for k in ("Q", "K", "V", "beta"))
+    lg, H0 = inp["log_gamma"], inp["H0"]
+    dy, dHT = inp["grad_y"].to(torch.bfloat16), inp["grad_HT"]
+    y, HT, grads = _run((Q, K, V, beta, lg, H0), dy, dHT, inp["chunk_size"], cuda)
+    sel = (slice(5, 6), slice(1, 3))
+    sub = [_np(t[sel]) for t in (Q, K, V, beta, lg, H0)]
+    ry, rHT = orc.delta_gated_sequential(*sub)
+    assert _rel(y[sel], ry) <= BF16_REL
+    assert _rel(HT[sel], rHT) <= BF16_REL
+    rg = orc.delta_gated_sequential_bwd(*sub, _np(dy[sel]), _np(dHT[sel]))
+    for name, gk, gr in zip(("dQ", "dK", "dV", "dbeta", "dlog_gamma", "dH0"), grads, rg):
+        assert _rel(gk[sel], gr) <= BF16_REL, f"{name} rel err {_rel(gk[sel], gr):.3e}"
