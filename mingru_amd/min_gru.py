@@ -996,6 +996,10 @@ class RotationMinGRU(DecayMixin, nn.Module):
             h_prev = self.h0.expand(B, 1, self.hidden_size)[:, 0]
         hp = h_prev.reshape(B, self.n_blocks, 2)
         dt = self._prepare_decay(delta_t, canonical_ndim=1)
+        # Decode on the angle-fused kernel: one token with h_prev as the carried state.
+        fused = self._angle_fused_forward(x_t.unsqueeze(1), hp, None if dt is None else dt[:, None])
+        if fused is not None:
+            return fused[:, 0]
         M, b = self._coeffs(x_t, dt)
         return (torch.einsum("bnij,bnj->bni", M, hp) + b).reshape(B, self.hidden_size)
 
@@ -1141,6 +1145,10 @@ class GivensMinGRU(DecayMixin, nn.Module):
             h_prev = self.h0.expand(B, 1, self.hidden_size)[:, 0]
         hp = h_prev.reshape(B, self.n_blocks, self.k)
         dt = self._prepare_decay(delta_t, canonical_ndim=1)
+        # Decode on the angle-fused kernel: one token with h_prev as the carried state.
+        fused = self._angle_fused_forward(x_t.unsqueeze(1), hp, None if dt is None else dt[:, None])
+        if fused is not None:
+            return fused[:, 0]
         M, b = self._coeffs(x_t, dt)
         return (torch.einsum("bnij,bnj->bni", M, hp) + b).reshape(B, self.hidden_size)
 

@@ -552,3 +552,22 @@ def test_step_auto_fallback_warns_once(monkeypatch):
     monkeypatch.setenv("MINGRU_SCAN", "hip")
     with pytest.raises(RuntimeError, match="declined by the fake backend"):
         mg._dispatch_gate_step("mingru", f, f, None, None, f)
+
+
+def test_givens_step_runs_the_angle_scan_for_one_token(monkeypatch):
+    """GivensMinGRU.step on the GPU path hands a T = 1 angle problem with h_prev as the
+    carried state to the angle-fused kernel and returns its single output row."""
+    seen = {}
+
+    def fake_angle(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale, has_decay):
+        seen.update(theta=tuple(theta.shape), h0=h0.clone(), has_decay=has_decay)
+        return torch.full(b.shape, 4.0)
+
+    _fake_backend(monkeypatch, angle_scan_impl=fake_angle)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    m = GivensMinGRU(6, 16, block_size=8, decay="fixed")
+    hp = torch.randn(3, 16)
+    h = m.step(torch.randn(3, 6), hp, delta_t=torch.rand(3))
+    assert seen["theta"][:3] == (3, 1, 2) and seen["has_decay"] == 1
+    assert torch.equal(seen["h0"], hp.reshape(3, 2, 8))
+    assert torch.equal(h, torch.full((3, 16), 4.0))

@@ -2,7 +2,8 @@
 
 * The DeltaMinGRU step op is checked against the float64 gated oracle run for one
   token (``oracle.scans.delta_gated_sequential`` with T = 1, pinned on the CPU).
-* The mixers' ``step()`` on the GPU (fused kernels) is checked against the same
+* The mixers' ``step()`` on the GPU (fused kernels; Rotation and Givens run the
+  angle-fused scan for one token) is checked against the same
   module's float64 eager ``step()`` on the CPU, which follows the reference's step
   bodies (``src/mingru/min_gru.py:1399-1448, 3611-3688``).
 * Running the fused step token by token reproduces the fused chunked forward, the
@@ -17,7 +18,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from mingru_amd import DeltaMinGRU, MinGRU, SignedMinGRU, hip_scans
+from mingru_amd import DeltaMinGRU, GivensMinGRU, MinGRU, RotationMinGRU, SignedMinGRU, hip_scans
 from oracle import scans as orc
 
 TOL = 1e-4
@@ -62,6 +63,10 @@ def _module_cases():
         ("signed-coupled-decay", lambda: SignedMinGRU(12, 40, coupled=True, decay="fixed"), True),
         ("delta", lambda: DeltaMinGRU(12, 32, n_heads=2, nh=2), False),
         ("delta-decay", lambda: DeltaMinGRU(12, 64, n_heads=1, decay="learnable"), True),
+        ("rotation", lambda: RotationMinGRU(12, 40), False),
+        ("rotation-decay", lambda: RotationMinGRU(12, 40, decay="fixed"), True),
+        ("givens", lambda: GivensMinGRU(12, 32, block_size=8), False),
+        ("givens-decay", lambda: GivensMinGRU(12, 32, block_size=4, decay="learnable"), True),
     ]
 
 
@@ -96,7 +101,9 @@ def test_module_step_fused_matches_fp64_eager(cuda, name, make, decay, monkeypat
 
 
 @pytest.mark.parametrize("make", [lambda: MinGRU(8, 24), lambda: SignedMinGRU(8, 24, coupled=True),
-                                  lambda: DeltaMinGRU(8, 32, n_heads=2, nh=2, chunk_size=8)])
+                                  lambda: DeltaMinGRU(8, 32, n_heads=2, nh=2, chunk_size=8),
+                                  lambda: RotationMinGRU(8, 24),
+                                  lambda: GivensMinGRU(8, 24, block_size=8)])
 def test_fused_step_loop_reproduces_fused_forward(cuda, make):
     """forward == step: the fused step run over T tokens gives the fused forward's outputs."""
     torch.manual_seed(9)
