@@ -88,9 +88,9 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
     sl[threadIdx.x] = lv;
   }
   __syncthreads();
-  decay_tables<NT>(sl, sE, sLc);
+  decay_tables<NT>(sl, sE);
+  decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab);
   __syncthreads();
-  decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
   build_L_gated(sK, sb, sE, g.nh, sL);
   __syncthreads();
   unit_lower_inverse(sL, sT, sY);
@@ -287,10 +287,9 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
     }
   }
   __syncthreads();
-  decay_tables<NT>(sl, sE, sLc);
+  decay_tables<NT>(sl, sE);
+  decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
   __syncthreads();
-  decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
-  if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
   build_L_gated(sK, sb, sE, g.nh, sL);
   __syncthreads();
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
@@ -497,7 +496,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     }
   }
   __syncthreads();
-  decay_tables<NT>(sl, sE, sLc);
+  decay_tables<NT>(sl, sE);
+  decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
   // PC term: <dHn, Hc>, with dHn in this thread's tile registers and Hc in sH.
   {
     float part = tn.dot(sH);
@@ -505,9 +505,6 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
     if (lane == 0) sred[w] = part;
   }
-  __syncthreads();
-  decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
-  if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
   __syncthreads();
   // Phase 1.  S = Q K^T, dP = dy U^T (rows tokens, cols micro-rows); Q Hc, K Hc for
   // the ptok and p log-gradients.

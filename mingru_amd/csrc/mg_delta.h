@@ -330,14 +330,14 @@ constexpr int VECN = 256;  // floats per chunk in the vector region
 // [128, 192) p_m, [192] PC.
 constexpr int V_AB = 0, V_PT = 64, V_P = 128, V_PC = 192;
 
-// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above; sLc[t] = Lc_t.  Each wave of
-// the NTH-thread workgroup fills 64 / (NTH / 64) consecutive rows t: lane s holds
-// l_s masked to s <= t, and an inclusive suffix
-// scan across the wave gives sum_{s' >= s}; span(t, t') is the scan value of lane
-// t' + 1.  Every span is a sum of its own terms only (never a difference of
-// running sums), so a saturated gap affects only the spans that contain it.
+// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above.  Each wave of the NTH-thread
+// workgroup fills 64 / (NTH / 64) consecutive rows t: lane s holds l_s masked to
+// s <= t, and an inclusive suffix scan across the wave gives sum_{s' >= s};
+// span(t, t') is the scan value of lane t' + 1.  Every span is a sum of its own
+// terms only (never a difference of running sums), so a saturated gap affects only
+// the spans that contain it.
 template <int NTH>
-__device__ __forceinline__ void decay_tables(const float* sl, float* sE, float* sLc) {
+__device__ __forceinline__ void decay_tables(const float* sl, float* sE) {
   constexpr int ROWS = DN / (NTH / 64);  // rows per wave
   const int w = wave_id(), lane = lane_id();
   const float lv = sl[lane];
@@ -352,20 +352,39 @@ __device__ __forceinline__ void decay_tables(const float* sl, float* sE, float* 
     float ex = __shfl_down(x, 1);
     if (lane == 63) ex = 0.f;
     sE[t * LD + lane] = lane <= t ? expf(ex) : 0.f;
-    if (lane == 0) sLc[t] = x;
   }
 }
 
-// Per-chunk decay vectors from the tables: sp[m] = p_m, sab[m] = a_m beta_m
-// (threads 0..63).
-__device__ __forceinline__ void decay_vectors(const float* sE, const float* sLc, const float* sb,
-                                              const Chunk& ch, int nh, float* sp, float* sab) {
-  const int m = threadIdx.x;
-  if (m < DN) {
-    const bool ok = m < ch.M;
-    sp[m] = ok ? expf(sLc[m / nh]) : 0.f;
-    sab[m] = ok ? sE[(ch.Ct - 1) * LD + m / nh] * sb[m] : 0.f;
+// The chunk's decay vectors, straight from l by wave 0 (no other wave's results are
+// read, so no barrier separates them from decay_tables):
+//   sLc[t] = Lc_t (inclusive prefix scan), sp[m] = exp(Lc_tau(m)) for m < M,
+//   sab[m] = a_m beta_m with a_m = exp(sum_{s=tau(m)+1..Ct-1} l_s) (masked suffix
+//   scan, the last row of the span table), and when given spt[t] = exp(Lc_t) for
+//   t < Ct and sa[m] = a_m.
+__device__ __forceinline__ void decay_vectors(const float* sl, const float* sb, const Chunk& ch,
+                                              int nh, float* sLc, float* sp, float* sab,
+                                              float* spt = nullptr, float* sa = nullptr) {
+  if (wave_id() != 0) return;
+  const int lane = lane_id();
+  const float lv = sl[lane];
+  float pre = lv, suf = lane < ch.Ct ? lv : 0.f;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float y = __shfl_up(pre, d), z = __shfl_down(suf, d);
+    if (lane >= d) pre += y;
+    if (lane + d < 64) suf += z;
   }
+  float carry = __shfl_down(suf, 1);  // sum over (lane, Ct - 1]
+  if (lane == 63) carry = 0.f;
+  sLc[lane] = pre;
+  if (spt) spt[lane] = lane < ch.Ct ? expf(pre) : 0.f;
+  const int tau = lane / nh;
+  const float lc_m = __shfl(pre, tau), carry_m = __shfl(carry, tau);
+  const bool ok = lane < ch.M;
+  const float a = ok ? expf(carry_m) : 0.f;
+  sp[lane] = ok ? expf(lc_m) : 0.f;
+  sab[lane] = a * sb[lane];
+  if (sa) sa[lane] = a;
 }
 
 __device__ __forceinline__ void write_vectors(float* vv, const float* sLc, const float* sp,

@@ -445,10 +445,9 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
   }
   __syncthreads();
   if constexpr (GATED) {
-    decay_tables<NTB>(sl, sE, sLc);
+    decay_tables<NTB>(sl, sE);
+    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
     __syncthreads();
-    decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
-    if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
   }
   floatx4 pp[2];
   {
@@ -463,10 +462,9 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED) {
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + col / g.nh] : 0.f;
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + col / g.nh]
-                                             : 0.f;
+        if constexpr (GATED) {  // nh = 1: micro-rows are tokens
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
+          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
         } else {
           kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
           pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
@@ -557,8 +555,9 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 //      reverse chain.
 // GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
 // E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E; the
-// span table lives in T's buffer until the inverse, diag(ptok) dy in P^T's once D1
-// is formed, and the split (p K)^T in the T operand buffers for the last products.
+// span table lives in T's buffer until the inverse, diag(ptok) dy in D1's until D1
+// is formed, and the split (p K)^T in T's buffer once the T operands are split.
+// The gated forms assume nh = 1 (the entry points check it).
 template <bool GATED>
 __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
@@ -572,7 +571,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   // operands T, T^T and (T diag(beta))^T.
   __shared__ BMat sX[6];
   __shared__ uint4 sLraw[(DN * LD + 3) / 4];  // L (fp32), then G0^T split
-  __shared__ float sT[DN * LD], sY[2 * 32 * LDS16];
+  __shared__ __align__(16) float sT[DN * LD];  // 16-byte aligned: holds a BPair (gated)
+  __shared__ float sY[2 * 32 * LDS16];
   __shared__ float sb[DN];
   __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
   float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
@@ -586,8 +586,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   BPair& sTbt = *reinterpret_cast<BPair*>(&sX[4]);
   BPair& sEt = sPt;
   BPair& sG0t = *reinterpret_cast<BPair*>(sLraw);
-  BPair& sDys = sPt;                                // (j; t) = ptok_t dy[t][j], gated
-  BPair& sPKt = *reinterpret_cast<BPair*>(&sX[0]);  // (d; m) = p_m K[m][d], gated
+  BPair& sDys = sD1t;                            // (j; t) = ptok_t dy[t][j], gated, until D1
+  BPair& sPKt = *reinterpret_cast<BPair*>(sT);  // (d; m) = p_m K[m][d], gated, after the split
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const Chunk ch = chunk_of(g, c);
@@ -622,10 +622,29 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   }
   __syncthreads();
   if constexpr (GATED) {
-    decay_tables<NTB>(sl, sE, sLc);
-    __syncthreads();
-    decay_vectors(sE, sLc, sb, ch, g.nh, sp, sab);
-    if (threadIdx.x < DN) spt[threadIdx.x] = threadIdx.x < ch.Ct ? expf(sLc[threadIdx.x]) : 0.f;
+    decay_tables<NTB>(sl, sE);
+    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
+    {
+      // diag(ptok) dy as a split pair (j; t) into D1's buffer, free until D1: each thread
+      // takes ptok_t = exp(Lc_t) of its 8 tokens from its own wave's prefix scan of l.
+      const int lane = lane_id();
+      float pre = sl[lane];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(pre, d);
+        if (lane >= d) pre += y;
+      }
+      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+      const uint4 dq = sDyt.v[bpos(row, q)];
+      const u16* e = reinterpret_cast<const u16*>(&dq);
+      float x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float lc = __shfl(pre, 8 * q + k);
+        x[k] = (8 * q + k < ch.Ct ? expf(lc) : 0.f) * bf_val(e[k]);
+      }
+      put_split8(sDys, row, q, x);
+    }
     __syncthreads();
     write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
   }
@@ -642,18 +661,20 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     else
       bmm<false, true, true>(rr, F, &sK, sHct);  // -K Hc
     bmm<false, false>(pp, F, &sQ, &sK);  // Q K^T
-    if constexpr (!GATED) bmm<false, false>(qd, F, &sQt, &sDyt);  // Q^T dy
+    if constexpr (GATED)
+      bmm<false, true>(qd, F, &sQt, sDys);  // Q^T diag(ptok) dy
+    else
+      bmm<false, false>(qd, F, &sQt, &sDyt);  // Q^T dy
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED) {
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + col / g.nh] : 0.f;
+        if constexpr (GATED) {  // nh = 1: micro-rows are tokens
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
           rr[jj][i] = fmaf(-sp[row], rr[jj][i], bget(sV, row, col));
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + col / g.nh]
-                                             : 0.f;
+          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
         } else {
           kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
           rr[jj][i] += bget(sV, row, col);
@@ -673,23 +694,18 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     acc_put_t(sD1t, d1[0], R0, C0);
     acc_put_t(sD1t, d1[1], R0, C0 + 16);
   }
-  if constexpr (GATED) {
-    __syncthreads();  // P^T is free: diag(ptok) dy as a split pair, then Q^T of it
-    {
-      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
-      const uint4 dq = sDyt.v[bpos(row, q)];
-      const u16* e = reinterpret_cast<const u16*>(&dq);
-      float x[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = spt[8 * q + k] * bf_val(e[k]);
-      put_split8(sDys, row, q, x);
-    }
-    __syncthreads();
-    bmm<false, true>(qd, F, &sQt, sDys);  // Q^T diag(ptok) dy
-  }
   unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes; sL and sPt are free
   stage_split(sTn, sTt, sTbt, sT, GATED ? sab : sb);
   __syncthreads();
+  if constexpr (GATED) {  // T's fp32 buffer is free: (p K)^T as a split pair for the last products
+    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+    const uint4 kq = sKt.v[bpos(row, q)];
+    const u16* e = reinterpret_cast<const u16*>(&kq);
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = sp[8 * q + k] * bf_val(e[k]);
+    put_split8(sPKt, row, q, x);
+  }
   {
     floatx4 u[2], e[2], g0[2];
     zero2(u);
@@ -707,17 +723,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     acc_put_t(sG0t, g0[1], R0, C0 + 16);
   }
   __syncthreads();
-  if constexpr (GATED) {  // the T operands are free: (p K)^T as a split pair
-    {
-      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
-      const uint4 kq = sKt.v[bpos(row, q)];
-      const u16* e = reinterpret_cast<const u16*>(&kq);
-      float x[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = sp[8 * q + k] * bf_val(e[k]);
-      put_split8(sPKt, row, q, x);
-    }
-    __syncthreads();
+  if constexpr (GATED) {
     floatx4 a2[2];
     zero2(a2);
     bmm<true, true, true>(a2, F, sPKt, sEt);   // A' = -(p K)^T E
@@ -854,14 +860,8 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
   }
   __syncthreads();
   if constexpr (GATED) {
-    decay_tables<NTB>(sl, sEg, sLc);
-    __syncthreads();
-    decay_vectors(sEg, sLc, sb, ch, g.nh, sp, sab);
-    if (threadIdx.x < DN) {
-      const int m = threadIdx.x;
-      spt[m] = m < ch.Ct ? expf(sLc[m]) : 0.f;
-      sa[m] = m < ch.M ? sEg[(ch.Ct - 1) * LD + m] : 0.f;
-    }
+    decay_tables<NTB>(sl, sEg);
+    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt, sa);
   }
   {
     // U and Hc are fetched while G forms, and staged once E and dHn^T are free.
