@@ -1199,28 +1199,32 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
     if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
   };
   // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
-  // ring, the loop unrolled by three so the buffers never move.
+  // ring, the loop unrolled by three so the buffers never move.  The fetch is
+  // unconditional (the index clamped to the last chunk): a conditional one leaves
+  // the compiler a merge of old and new buffer contents, resolved by register
+  // copies that wait for the loads at once.
   auto step = [&](const FwdOps& cur, FwdOps& fill, int c) {
-    if (c + 2 < g.nc) fetch(fill, c + 2);
+    fetch(fill, min(c + 2, g.nc - 1));
     const Chunk ch = chunk_of(g, c);
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     BPair& ht = sHt[c & 1];
     acc_put_t(ht, h, 16 * w, 0);
     acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
     __syncthreads();
-    floatx4 yy = cur.pu;
+    floatx4 yy = {0.f, 0.f, 0.f, 0.f};  // Pu is added after the products
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = GATED ? fmaf(cur.pc, h[i], cur.b[i]) : h[i] + cur.b[i];
     amm2(h, cur.ah, cur.al, yy, cur.qh, cur.ql, ht, rf);  // H + A H + B, y = Qe H + Pu
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * w + 4 * gg + i;
-      if (t < ch.Ct && col < g.dv) y[(bh * g.T + ch.t0 + t) * g.dv + col] = bf_bits(yy[i]);
+      if (t < ch.Ct && col < g.dv)
+        y[(bh * g.T + ch.t0 + t) * g.dv + col] = bf_bits(yy[i] + cur.pu[i]);
     }
   };
   FwdOps b0, b1, b2;
   fetch(b0, 0);
-  if (g.nc > 1) fetch(b1, 1);
+  fetch(b1, min(1, g.nc - 1));
   int c = 0;
   for (; c + 3 <= g.nc; c += 3) {
     step(b0, b2, c);
