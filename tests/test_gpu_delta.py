@@ -132,6 +132,49 @@ def test_delta_c5_full_size(cuda):
         assert _rel(gk[sel], rk) <= BF16_REL, f"{name} rel err {_rel(gk[sel], rk):.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_delta_chaining_at_misaligned_boundary(cuda, dtype):
+    """Running [0, T1) and then [T1, T) with the first call's H_T as the second's H_0
+    gives the single run's y and H_T, at a split that is not a chunk boundary (the
+    reference's chaining property, tests/test_mixers.py:834-854).  The runs differ only
+    by chunk association, so the bars are the parity bars: fp32 y and H_T within twice
+    the 1e-4 fp64 bar; bf16 y within the bf16 bar; the fp32 state within 2e-4 relative."""
+    B, H, T, C, T1 = 2, 2, 150, 32, 77
+    print(f"[gpu] delta chaining dtype={dtype}", flush=True)
+    Q, K, V, beta, H0, _, _ = _inputs(B, H, T, 1, 64, 64, seed=41, dtype=dtype)
+    seq = [t.to(cuda) for t in (Q, K, V, beta)]
+    h0 = H0.to(cuda)
+    with torch.no_grad():
+        y, HT = hip_scans.delta_scan_impl(*seq, h0, chunk_size=C)
+        ya, Ha = hip_scans.delta_scan_impl(*(t[:, :, :T1] for t in seq), h0, chunk_size=C)
+        yb, Hb = hip_scans.delta_scan_impl(*(t[:, :, T1:] for t in seq), Ha, chunk_size=C)
+    torch.cuda.synchronize()
+    ys = torch.cat([ya, yb], dim=2)
+    if dtype == torch.float32:
+        assert (ys - y).abs().max().item() <= 2 * FWD_TOL
+        assert (Hb - HT).abs().max().item() <= 2 * FWD_TOL
+    else:
+        assert _rel(ys, _np(y)) <= BF16_REL
+        assert _rel(Hb, _np(HT)) <= 2 * SPLIT_REL
+
+
+@pytest.mark.parametrize("nh,chunks", [(1, (1, 3, 40, 64)), (2, (1, 5, 32))])
+def test_delta_chunk_size_invariance(cuda, nh, chunks):
+    """One input set at several chunk sizes (1, ragged, T and > T) gives the same outputs
+    and gradients as chunk 16, within the fp32 bars (the reference's chunk-size
+    invariance, tests/test_mixers.py:748-775)."""
+    B, H, T, dk, dv = 2, 2, 40, 16, 24
+    Q, K, V, beta, H0, dy, dHT = _inputs(B, H, T, nh, dk, dv, seed=77 + nh)
+    print(f"[gpu] delta chunk invariance nh={nh} chunks={chunks}", flush=True)
+    y0, H0T, g0 = _run(Q, K, V, beta, H0, dy, dHT, 16, cuda)
+    for C in chunks:
+        y, HT, grads = _run(Q, K, V, beta, H0, dy, dHT, C, cuda)
+        assert (y - y0).abs().max().item() <= FWD_TOL, f"chunk {C}: y"
+        assert (HT - H0T).abs().max().item() <= FWD_TOL, f"chunk {C}: H_T"
+        for name, gk, rk in zip(("dQ", "dK", "dV", "dbeta", "dH0"), grads, g0):
+            assert (gk - rk).abs().max().item() <= GRAD_TOL, f"chunk {C}: {name}"
+
+
 def test_delta_deterministic(cuda):
     Q, K, V, beta, H0, dy, dHT = _inputs(2, 2, 257, 1, 64, 64, seed=3)
     a = _run(Q, K, V, beta, H0, dy, dHT, 64, cuda)

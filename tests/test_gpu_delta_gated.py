@@ -224,3 +224,31 @@ def test_delta_gated_bf16_c5_heads(cuda):
     rg = orc.delta_gated_sequential_bwd(*sub, _np(dy[sel]), _np(dHT[sel]))
     for name, gk, gr in zip(("dQ", "dK", "dV", "dbeta", "dlog_gamma", "dH0"), grads, rg):
         assert _rel(gk[sel], gr) <= BF16_REL, f"{name} rel err {_rel(gk[sel], gr):.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_delta_gated_chaining_at_misaligned_boundary(cuda, dtype):
+    """Gated chaining: [0, T1) then [T1, T) with the first call's H_T as the second's H_0
+    gives the single run's y and H_T at a split inside a chunk, including decay spikes
+    (the reference's chaining property, tests/test_mixers.py:834-854, with the decay of
+    _forward_chunked_gated).  Bars as the parity bars: fp32 within twice 1e-4, bf16 y
+    within the bf16 bar, the fp32 state within 2e-4 relative."""
+    B, H, T, C, T1 = 2, 2, 150, 32, 77
+    print(f"[gpu] delta gated chaining dtype={dtype}", flush=True)
+    Q, K, V, beta, lg, H0, _, _ = _inputs(B, H, T, 1, 64, 64, seed=43, lg_kind="spikes")
+    seq = [t.to(dtype).to(cuda) for t in (Q, K, V, beta)]
+    lg, h0 = lg.to(cuda), H0.to(cuda)
+    with torch.no_grad():
+        y, HT = hip_scans.delta_gated_scan_impl(*seq, lg, h0, chunk_size=C)
+        ya, Ha = hip_scans.delta_gated_scan_impl(*(t[:, :, :T1] for t in seq), lg[:, :, :T1], h0,
+                                                 chunk_size=C)
+        yb, Hb = hip_scans.delta_gated_scan_impl(*(t[:, :, T1:] for t in seq), lg[:, :, T1:], Ha,
+                                                 chunk_size=C)
+    torch.cuda.synchronize()
+    ys = torch.cat([ya, yb], dim=2)
+    if dtype == torch.float32:
+        assert (ys - y).abs().max().item() <= 2 * FWD_TOL
+        assert (Hb - HT).abs().max().item() <= 2 * FWD_TOL
+    else:
+        assert _rel(ys, _np(y)) <= BF16_REL
+        assert _rel(Hb, _np(HT)) <= 2 * SPLIT_REL
