@@ -110,3 +110,18 @@ def test_identity_transitions_give_cumsum(cuda):
     Abar, Bbar = matrix_affine_scan(A.to(cuda), Bm.to(cuda))
     assert torch.equal(Abar.cpu(), A)
     assert _maxerr(Bbar, np.cumsum(Bm.double().numpy(), axis=1)) <= 1e-3
+
+
+def test_identity_transitions_long_sequence_exact(cuda):
+    """T = 2**20 with identity transitions and integer B in [-2, 2]: Abar = I and
+    Bbar = cumsum(B) exactly (integer partial sums below 2**21 are exact in fp32 under any
+    association), across about 8,000 look-back chunks along T."""
+    B, T, n = 1, 1 << 20, 16
+    print(f"[gpu] matrix_affine_scan long sequence T={T}", flush=True)
+    gen = torch.Generator(device=cuda).manual_seed(14)
+    Bm = torch.randint(-2, 3, (B, T, n, 2, 1), device=cuda, generator=gen).float()
+    A = torch.eye(2, device=cuda).expand(B, T, n, 2, 2).contiguous()
+    Abar, Bbar = matrix_affine_scan(A, Bm)
+    torch.cuda.synchronize()
+    assert torch.equal(Abar, A)
+    assert torch.equal(Bbar.double(), Bm.double().cumsum(1))

@@ -101,6 +101,30 @@ def test_linear_scan_identity_is_cumsum(cuda):
     assert _maxerr(Bc, ref) <= 1e-3  # cumsum of 3000 N(0,1): fp32 rounding of |x| ~ 50
 
 
+def test_linear_scan_long_sequence_exact(cuda):
+    """T = 2**20 (about 8,000 look-back chunks along T; C2 has 32) with a = 1 and integer
+    b, gB in [-2, 2]: every partial sum is an integer below 2**21, exact in fp32 under any
+    association, so the scan must equal the fp64 closed forms bit for bit: A = 1,
+    Bc = cumsum(b), db = reverse cumsum(gB) and da_t = db_t * Bc_{t-1} (one rounding)."""
+    B, T, D = 1, 1 << 20, 64
+    print(f"[gpu] linear_scan long sequence T={T}", flush=True)
+    gen = torch.Generator(device=cuda).manual_seed(12)
+    b = torch.randint(-2, 3, (B, T, D), device=cuda, generator=gen).float()
+    gB = torch.randint(-2, 3, (B, T, D), device=cuda, generator=gen).float()
+    a = torch.ones(B, T, D, device=cuda, requires_grad=True)
+    bg = b.clone().requires_grad_(True)
+    A, Bc = linear_scan(a, bg)
+    torch.autograd.backward([A, Bc], [torch.zeros_like(A), gB])
+    torch.cuda.synchronize()
+    assert torch.equal(A, torch.ones_like(A))
+    ref = b.double().cumsum(1)
+    assert torch.equal(Bc.double(), ref)
+    y = gB.double().flip(1).cumsum(1).flip(1)
+    assert torch.equal(bg.grad.double(), y)
+    prev = torch.cat([torch.zeros_like(ref[:, :1]), ref[:, :-1]], dim=1)
+    assert torch.equal(a.grad, (y * prev).float())
+
+
 def _run_log(lc, lv, gh, cuda):
     lcg = lc.to(cuda).requires_grad_(True)
     lvg = lv.to(cuda).requires_grad_(True)
@@ -160,3 +184,20 @@ def test_non_contiguous_inputs(cuda):
     h = parallel_scan_log(lc, lv)
     rh = orc.parallel_scan_log(lc.double().cpu().numpy(), lv.double().cpu().numpy())
     assert _maxerr(h, rh) <= FWD_TOL
+
+
+def test_parallel_scan_log_long_sequence(cuda):
+    """T = 2**20 with log a = 0: h_t = h_0 + sum_{s<=t} b_s with b_s = exp(lv_s) > 0, a sum of
+    positive terms (no cancellation), checked against the fp64 cumulative sum to 1e-5
+    relative at every step."""
+    B, T, D = 1, 1 << 20, 64
+    print(f"[gpu] parallel_scan_log long sequence T={T}", flush=True)
+    gen = torch.Generator(device=cuda).manual_seed(13)
+    lc = torch.zeros(B, T, D, device=cuda)
+    lv = -2.0 + 0.5 * torch.randn(B, T + 1, D, device=cuda, generator=gen)
+    h = parallel_scan_log(lc, lv)
+    torch.cuda.synchronize()
+    ref = lv.double().exp().cumsum(1)[:, 1:]
+    rel = ((h.double() - ref).abs() / ref).max().item()
+    print(f"[gpu] parallel_scan_log long sequence max rel err {rel:.3e}", flush=True)
+    assert rel <= 1e-5
