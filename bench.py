@@ -477,6 +477,30 @@ def _timed(step, steps, torch):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def graphed_ms(step, torch, steps):
+    """ms per step of ``step`` (forward + autograd.grad) captured once in a HIP graph and
+    replayed: the launch-bound workloads' kernels with no host dispatch between them.  The
+    warm-up runs on the capture stream, so the scan workspace of that stream exists before
+    capture and nothing is allocated or filled inside it.  The first replay's gradients are
+    checked against an eager step before timing."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = step()
+    g.replay()
+    ref = step()
+    torch.cuda.synchronize()
+    for x, r in zip(out, ref):
+        if not torch.allclose(x, r, rtol=1e-5, atol=1e-6):
+            raise RuntimeError("graph replay disagrees with the eager step")
+    return _timed(g.replay, steps, torch)
+
+
 def run_op(op, torch, wl, dev, steps, warmup, hip_scans, headline=False):
     """Times `steps` steps after `warmup` untimed ones.  Per-kernel durations come
     from HIP events recorded around every C-ABI call.  For the headline workload
@@ -522,6 +546,10 @@ def run_op(op, torch, wl, dev, steps, warmup, hip_scans, headline=False):
         "kernels": kern,
         "ms_per_step_instrumented": ms_instr,
     }
+    if op.key in ("C1", "C1g"):  # host-bound: also the GPU-side rate, replayed from a graph
+        gms = graphed_ms(step, torch, steps)
+        res["graph_ms_per_step"] = gms
+        res["graph_tokens_per_s"] = op.tokens / (gms * 1e-3)
     if op.fwd_flops is not None:
         fl = op.fwd_flops + op.bwd_flops
         res["algorithmic_flops"] = fl
@@ -640,6 +668,9 @@ def main():
         for kname, kres in res["kernels"].items():
             print(f"#   {kname}: {kres['avg_us']:.1f} us, {kres['achieved_GBs']:.0f} GB/s",
                   file=sys.stderr, flush=True)
+        if "graph_ms_per_step" in res:
+            print(f"#   replayed from a HIP graph: {res['graph_ms_per_step']:.3f} ms/step, "
+                  f"{res['graph_tokens_per_s']:.4g} tok/s", file=sys.stderr, flush=True)
         if key in ("C2g", "C1g") and not args.no_eager:
             uf = gate_unfused_gpu_ms(key, torch, wl, dev, args.steps)
             res["unfused_ms_per_step"] = uf

@@ -11,7 +11,7 @@ synchronisations between the replays, and checks every replay against eager.
 import pytest
 import torch
 
-from mingru_amd import hip_scans, linear_scan
+from mingru_amd import hip_scans, linear_scan, parallel_scan_log
 from mingru_amd.min_gru import _dispatch_mingru_gate_scan
 
 pytestmark = pytest.mark.gpu
@@ -105,3 +105,42 @@ def test_delta_step_graph_replays(cuda):
         y_e, H_e = fn(nH_, nq)
         torch.cuda.synchronize()
         assert torch.equal(y_s, y_e) and torch.equal(H_s, H_e), f"replay {rep}"
+
+
+def test_log_scan_fwd_bwd_graph_replays(cuda):
+    """Forward and backward (autograd.grad) of parallel_scan_log captured together, the
+    way a launch-bound caller runs them; every replay on new data against eager."""
+    print("[gpu] graph: parallel_scan_log fwd+bwd", flush=True)
+    gen = torch.Generator(device=cuda).manual_seed(3)
+    B, T, D = 2, 700, 96
+    lc = torch.empty(B, T, D, device=cuda).requires_grad_(True)
+    lv = torch.empty(B, T + 1, D, device=cuda).requires_grad_(True)
+    gh = torch.empty(B, T, D, device=cuda)
+
+    def fill():
+        with torch.no_grad():
+            lc.copy_(torch.nn.functional.logsigmoid(torch.randn(B, T, D, device=cuda, generator=gen)))
+            lv.copy_(torch.randn(B, T + 1, D, device=cuda, generator=gen) - 1.0)
+            gh.copy_(torch.randn(B, T, D, device=cuda, generator=gen))
+
+    def fn():
+        h = parallel_scan_log(lc, lv)
+        return (h,) + torch.autograd.grad(h, (lc, lv), gh)
+
+    fill()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = fn()
+    for rep in range(4):
+        fill()
+        g.replay()
+        ref = fn()
+        torch.cuda.synchronize()
+        for name, x, r in zip(("h", "dlc", "dlv"), out, ref):
+            assert torch.allclose(x, r, rtol=1e-5, atol=1e-6), f"replay {rep}: {name}"
