@@ -264,24 +264,6 @@ struct FTile {
       put_split1(m, c0 + 3, row, f[v].w);
     }
   }
-  // bf16 copy of the block into a row-major output with row stride ldg.
-  __device__ __forceinline__ void store_bf16(u16* dst, int rows, int cols, int64_t ldg) const {
-#pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
-      if (row >= rows) continue;
-      const float e[4] = {f[v].x, f[v].y, f[v].z, f[v].w};
-      if (c0 + 4 <= cols && ldg == DN) {
-        *reinterpret_cast<uint2*>(dst + (int64_t)row * DN + c0) =
-            make_uint2(bf_bits(e[0]) | ((unsigned)bf_bits(e[1]) << 16),
-                       bf_bits(e[2]) | ((unsigned)bf_bits(e[3]) << 16));
-      } else {
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-          if (c0 + x < cols) dst[(int64_t)row * ldg + c0 + x] = bf_bits(e[x]);
-      }
-    }
-  }
 };
 
 // The wave's 16 x 32 output block (rows R0 + 4 g + i, columns C0 + 16 jj + r) into a
