@@ -769,11 +769,10 @@ int dw_bwd_bf16_gated(const void* Q, const void* K, const void* V, const void* b
   float* dHn = (float*)((char*)ws + 5 * mb);
   float* vm = (float*)((char*)ws + 6 * mb);
   const dim3 pgrid(g.nc, (unsigned)BH);
-  const u16 *q = (const u16*)Q, *k = (const u16*)K, *v = (const u16*)V, *b = (const u16*)beta,
-            *d = (const u16*)dy;
-  hipLaunchKernelGGL(dwb_bwd_prep<true>, pgrid, dim3(NTB), 0, stream, q, k, v, b, lg, d, Hb, Um,
-                     Em, G0m, Apm, bpm, vm, g);
-  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  const u16 *q = (const u16*)Q, *k = (const u16*)K, *b = (const u16*)beta, *d = (const u16*)dy;
+  const int rc = dwb_bwd_prep_launch(true, Q, K, V, beta, lg, dy, Hb, Um, Em, G0m, Apm, bpm, vm, BH,
+                                     g, stream);
+  if (rc != MG_OK) return rc;
   hipLaunchKernelGGL(dwb_bwd_chain<true>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, dHT, Apm,
                      bpm, vm, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;

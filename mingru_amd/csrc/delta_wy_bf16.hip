@@ -52,11 +52,10 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
   float* bpm = (float*)((char*)ws + 4 * mb);
   float* dHn = (float*)((char*)ws + 5 * mb);
   const dim3 pgrid(g.nc, (unsigned)BH);
-  const u16 *q = (const u16*)Q, *k = (const u16*)K, *v = (const u16*)V, *b = (const u16*)beta,
-            *d = (const u16*)dy;
-  hipLaunchKernelGGL(dwb_bwd_prep<false>, pgrid, dim3(NTB), 0, stream, q, k, v, b, nullptr, d, Hb,
-                     Um, Em, G0m, Apm, bpm, nullptr, g);
-  if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+  const u16 *q = (const u16*)Q, *k = (const u16*)K, *b = (const u16*)beta, *d = (const u16*)dy;
+  const int rc = dwb_bwd_prep_launch(false, Q, K, V, beta, nullptr, dy, Hb, Um, Em, G0m, Apm, bpm,
+                                     nullptr, BH, g, stream);
+  if (rc != MG_OK) return rc;
   hipLaunchKernelGGL(dwb_bwd_chain<false>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, dHT, Apm,
                      bpm, nullptr, dHn, dH0, g, BH);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;

@@ -330,13 +330,13 @@ constexpr int VECN = 256;  // floats per chunk in the vector region
 // [128, 192) p_m, [192] PC.
 constexpr int V_AB = 0, V_PT = 64, V_P = 128, V_PC = 192;
 
-// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above.  Each wave of the NTH-thread
+// sE[t][t'] = exp(span(t, t')) for t' <= t, 0 above (row stride LDE).  Each wave of the NTH-thread
 // workgroup fills 64 / (NTH / 64) consecutive rows t: lane s holds l_s masked to
 // s <= t, and an inclusive suffix scan across the wave gives sum_{s' >= s};
 // span(t, t') is the scan value of lane t' + 1.  Every span is a sum of its own
 // terms only (never a difference of running sums), so a saturated gap affects only
 // the spans that contain it.
-template <int NTH>
+template <int NTH, int LDE = LD>
 __device__ __forceinline__ void decay_tables(const float* sl, float* sE) {
   constexpr int ROWS = DN / (NTH / 64);  // rows per wave
   const int w = wave_id(), lane = lane_id();
@@ -351,7 +351,7 @@ __device__ __forceinline__ void decay_tables(const float* sl, float* sE) {
     }
     float ex = __shfl_down(x, 1);
     if (lane == 63) ex = 0.f;
-    sE[t * LD + lane] = lane <= t ? expf(ex) : 0.f;
+    sE[t * LDE + lane] = lane <= t ? expf(ex) : 0.f;
   }
 }
 
@@ -432,6 +432,13 @@ int dw_bwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
                 const void* dy, const float* dHT, void* dQ, void* dK, void* dV, void* dbeta,
                 float* dH0, int64_t BH, const DwGeom& g, void* ws, size_t ws_bytes,
                 hipStream_t stream);
+
+// The bf16 backward preparation kernel, either form (gated: lg and the vector
+// region vm), launched from a translation unit of its own (delta_bwd_prep_bf16.hip).
+int dwb_bwd_prep_launch(bool gated, const void* Q, const void* K, const void* V, const void* beta,
+                        const float* lg, const void* dy, const float* Hb, float* Um, float* Em,
+                        float* G0m, float* Apm, float* bpm, float* vm, int64_t BH,
+                        const DwGeom& g, hipStream_t stream);
 
 // Decay-gated forms (delta_gated.hip), bf16 inputs and nh = 1: lg / dlg are the
 // per-token log decay and its gradient, fp32 (B*H, T); the workspace adds a

@@ -527,201 +527,6 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
   }
 }
 
-// ---------------------------------------------------------------------------
-// backward, preparation kernel: one workgroup per (chunk, head)
-// ---------------------------------------------------------------------------
-//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
-//   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
-//   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
-//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32) for the
-//      reverse chain.
-// GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
-// E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E; the
-// span table lives in T's buffer until the inverse, diag(ptok) dy in D1's until D1
-// is formed, and the split (p K)^T in T's buffer once the T operands are split.
-// The gated forms assume nh = 1 (the entry points check it).
-template <bool GATED>
-__global__ __launch_bounds__(NTB) void dwb_bwd_prep(
-    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
-    const u16* __restrict__ beta, const float* __restrict__ lg, const u16* __restrict__ dy,
-    const float* __restrict__ Hb, float* __restrict__ Uo, float* __restrict__ Eo,
-    float* __restrict__ G0o, float* __restrict__ Apo, float* __restrict__ bpo,
-    float* __restrict__ vo, DwGeom g) {
-  __shared__ BMat sK, sKt;
-  __shared__ BPair sRt, sPt, sD1t;  // sPt later holds E^T
-  // Inputs Q, Q^T, dy^T, V and Hc^T until the inverse is formed, then the split
-  // operands T, T^T and (T diag(beta))^T.
-  __shared__ BMat sX[6];
-  __shared__ uint4 sLraw[(DN * LD + 3) / 4];  // L (fp32), then G0^T split
-  __shared__ __align__(16) float sT[DN * LD];  // 16-byte aligned: holds a BPair (gated)
-  __shared__ float sY[2 * 32 * LDS16];
-  __shared__ float sb[DN];
-  __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
-  float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
-        *spt = sdec + 4 * DN;
-  float* sE = sT;  // span table until the inverse
-  float* sL = reinterpret_cast<float*>(sLraw);
-  BMat &sQ = sX[0], &sQt = sX[1], &sDyt = sX[2], &sV = sX[3];
-  BPair& sHct = *reinterpret_cast<BPair*>(&sX[4]);
-  BPair& sTn = *reinterpret_cast<BPair*>(&sX[0]);
-  BPair& sTt = *reinterpret_cast<BPair*>(&sX[2]);
-  BPair& sTbt = *reinterpret_cast<BPair*>(&sX[4]);
-  BPair& sEt = sPt;
-  BPair& sG0t = *reinterpret_cast<BPair*>(sLraw);
-  BPair& sDys = sD1t;                            // (j; t) = ptok_t dy[t][j], gated, until D1
-  BPair& sPKt = *reinterpret_cast<BPair*>(sT);  // (d; m) = p_m K[m][d], gated, after the split
-  const int c = blockIdx.x;
-  const int64_t bh = blockIdx.y;
-  const Chunk ch = chunk_of(g, c);
-  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
-  const int64_t trow0 = bh * g.T + ch.t0;
-  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-  FragOff F;
-  F.init();
-  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
-  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
-  {
-    BTile tk, tv, tq, td;
-    FTile th;
-    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
-    tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
-    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
-    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
-    th.load(Hb + mat, g.dk, g.dv);
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
-    tk.put(sK);
-    tk.put_t(sKt);
-    tv.put(sV);
-    tq.put(sQ);
-    tq.put_t(sQt);
-    td.put_t(sDyt);
-    th.put_split_t(sHct);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
-    if constexpr (GATED) {
-      const float lv = ld_l(lg, bh, g, ch);
-      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
-    }
-  }
-  __syncthreads();
-  if constexpr (GATED) {
-    decay_tables<NTB>(sl, sE);
-    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
-    {
-      // diag(ptok) dy as a split pair (j; t) into D1's buffer, free until D1: each thread
-      // takes ptok_t = exp(Lc_t) of its 8 tokens from its own wave's prefix scan of l.
-      const int lane = lane_id();
-      float pre = sl[lane];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(pre, d);
-        if (lane >= d) pre += y;
-      }
-      const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
-      const uint4 dq = sDyt.v[bpos(row, q)];
-      const u16* e = reinterpret_cast<const u16*>(&dq);
-      float x[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float lc = __shfl(pre, 8 * q + k);
-        x[k] = (8 * q + k < ch.Ct ? expf(lc) : 0.f) * bf_val(e[k]);
-      }
-      put_split8(sDys, row, q, x);
-    }
-    __syncthreads();
-    write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
-  }
-  floatx4 qd[2];  // Q^T dy (gated: Q^T diag(ptok) dy), kept for b'
-  zero2(qd);
-  {
-    floatx4 kk[2], rr[2], pp[2];
-    zero2(kk);
-    zero2(rr);
-    zero2(pp);
-    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
-    if constexpr (GATED)
-      bmm<false, true>(rr, F, &sK, sHct);  // K Hc
-    else
-      bmm<false, true, true>(rr, F, &sK, sHct);  // -K Hc
-    bmm<false, false>(pp, F, &sQ, &sK);  // Q K^T
-    if constexpr (GATED)
-      bmm<false, true>(qd, F, &sQt, sDys);  // Q^T diag(ptok) dy
-    else
-      bmm<false, false>(qd, F, &sQt, &sDyt);  // Q^T dy
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int cj = C0 + 16 * jj;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED) {  // nh = 1: micro-rows are tokens
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
-          rr[jj][i] = fmaf(-sp[row], rr[jj][i], bget(sV, row, col));
-          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
-        } else {
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
-          rr[jj][i] += bget(sV, row, col);
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
-        }
-      }
-      acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
-      acc_put_t(sRt, rr[jj], R0, cj);
-      acc_put_t(sPt, pp[jj], R0, cj);
-    }
-  }
-  __syncthreads();
-  {
-    floatx4 d1[2];
-    zero2(d1);
-    bmm<true, false>(d1, F, sPt, &sDyt);  // P^T dy
-    acc_put_t(sD1t, d1[0], R0, C0);
-    acc_put_t(sD1t, d1[1], R0, C0 + 16);
-  }
-  unit_lower_inverse(sL, sT, sY);  // its barriers also order the D1 writes; sL and sPt are free
-  stage_split(sTn, sTt, sTbt, sT, GATED ? sab : sb);
-  __syncthreads();
-  if constexpr (GATED) {  // T's fp32 buffer is free: (p K)^T as a split pair for the last products
-    const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
-    const uint4 kq = sKt.v[bpos(row, q)];
-    const u16* e = reinterpret_cast<const u16*>(&kq);
-    float x[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = sp[8 * q + k] * bf_val(e[k]);
-    put_split8(sPKt, row, q, x);
-  }
-  {
-    floatx4 u[2], e[2], g0[2];
-    zero2(u);
-    zero2(e);
-    zero2(g0);
-    bmm<true, true>(u, F, sTn, sRt);     // U = T R
-    bmm<true, false>(e, F, sTbt, &sKt);  // E = T^T diag(beta) K   (rows m, cols d)
-    bmm<true, true>(g0, F, sTt, sD1t);   // G0 = T^T D1           (rows m, cols j)
-    store_block_f32(Uo + mat, u, R0, C0);
-    store_block_split(reinterpret_cast<u16*>(Eo + mat), e, R0, C0);
-    store_block_f32(G0o + mat, g0, R0, C0);
-    acc_put_t(sEt, e[0], R0, C0);
-    acc_put_t(sEt, e[1], R0, C0 + 16);
-    acc_put_t(sG0t, g0[0], R0, C0);
-    acc_put_t(sG0t, g0[1], R0, C0 + 16);
-  }
-  __syncthreads();
-  if constexpr (GATED) {
-    floatx4 a2[2];
-    zero2(a2);
-    bmm<true, true, true>(a2, F, sPKt, sEt);   // A' = -(p K)^T E
-    bmm<true, true, true>(qd, F, sPKt, sG0t);  // b' = Q^T diag(ptok) dy - (p K)^T G0
-    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
-    store_block_f32(bpo + mat, qd, R0, C0);
-  } else {
-    floatx4 a2[2];
-    zero2(a2);
-    bmm<false, true, true>(a2, F, &sKt, sEt);    // A' = -K^T E
-    bmm<false, true, true>(qd, F, &sKt, sG0t);   // b' = Q^T dy - K^T G0
-    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
-    store_block_f32(bpo + mat, qd, R0, C0);
-  }
-}
-
 // A fragments of a row-major bf16 input block (rows x cols, row stride ld):
 // row `row`, chunks g and 4 + g, zero outside the block.
 __device__ __forceinline__ void load_in_frag(uint4 (&a)[2], const u16* src, int64_t ld, int row,
@@ -757,6 +562,327 @@ __device__ __forceinline__ void rmm(floatx4 (&acc)[2], const FragOff& F, const u
       if constexpr (SB)
         acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, frag_at(B[1], F.b[s][jj]), acc[jj], 0, 0, 0);
     }
+  }
+}
+
+// ---- register operands built from LDS ---------------------------------------------
+// An fp32 A fragment as a split pair: x[e] = hi + lo (about 16 significant bits).
+__device__ __forceinline__ void split_frag(const float (&x)[8], uint4& hi, uint4& lo) {
+  unsigned h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    u16 h0, l0, h1, l1;
+    bf_split(x[2 * p], h0, l0);
+    bf_split(x[2 * p + 1], h1, l1);
+    h[p] = h0 | ((unsigned)h1 << 16);
+    l[p] = l0 | ((unsigned)l1 << 16);
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// Split A fragments of rows R0 + r of an fp32 LDS matrix (row stride LD): with
+// TRANS, row m of its transpose (x = T[k][m]), optionally times scale[k].
+template <bool TRANS>
+__device__ __forceinline__ void t_frags(uint4 (&hi)[2], uint4 (&lo)[2], const float* T, int R0,
+                                        const float* scale) {
+  const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int k0 = 8 * (4 * s + g);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = TRANS ? T[(k0 + e) * LD + R0 + r] : T[(R0 + r) * LD + k0 + e];
+      if (scale) x[e] *= scale[k0 + e];
+    }
+    split_frag(x, hi[s], lo[s]);
+  }
+}
+
+// Fragments of the transpose of an exact bf16 BMat, gathered by column: row n of
+// M^T, i.e. (k, n) elements M[k][n] for the lane's 8 consecutive k.
+__device__ __forceinline__ uint4 col_frag(const BMat& M, int n, int s) {
+  const int k0 = 8 * (4 * s + (lane_id() >> 4));
+  const u16* base = reinterpret_cast<const u16*>(&M);
+  unsigned p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int k = k0 + 2 * e;
+    const u16 a = base[bpos(k, n >> 3) * 8 + (n & 7)], b = base[bpos(k + 1, n >> 3) * 8 + (n & 7)];
+    p[e] = a | ((unsigned)b << 16);
+  }
+  return make_uint4(p[0], p[1], p[2], p[3]);
+}
+
+// acc[jj] (+/-)= A . B[row block 2 ch + jj]^T with A a split pair in registers and
+// B a split pair in LDS (hi hi + hi lo + lo hi) or, with !SB, an exact BMat.
+template <bool SB, bool NEG = false>
+__device__ __forceinline__ void smm(floatx4 (&acc)[2], const FragOff& F, const uint4 (&ah)[2],
+                                    const uint4 (&al)[2], const BMat* B) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    bf16x8 h = __builtin_bit_cast(bf16x8, ah[s]), l = __builtin_bit_cast(bf16x8, al[s]);
+    if constexpr (NEG) {
+      h = bneg(h);
+      l = bneg(l);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const bf16x8 bh = frag_at(B[0], F.b[s][jj]);
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h, bh, acc[jj], 0, 0, 0);
+      if constexpr (SB)
+        acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h, frag_at(B[1], F.b[s][jj]), acc[jj], 0, 0, 0);
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l, bh, acc[jj], 0, 0, 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, preparation kernel: one workgroup per (chunk, head)
+// ---------------------------------------------------------------------------
+//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
+//   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
+//   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
+//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32) for the
+//      reverse chain.
+// GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
+// E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E.
+// The gated forms assume nh = 1 (the entry points check it).
+//
+// The products run in dependency order so that few 64 x 64 operands are live at
+// once, and LDS stays under 80 KB (two workgroups per CU):
+//   A  L (fp32), then T = (I + L)^-1 in place; the inverse's workspace and the
+//      gated span table sit in split regions that are still free;
+//   B  Hc^T (split) -> R = V - K Hc, V read per element from memory -> R^T (split);
+//   C  U = T R;
+//   D  P = Q K^T with Q as register fragments -> P^T (split); Q^T dy; D1 = P^T dy;
+//   E  G0 = T^T D1 -> G0^T; E = (T diag(beta))^T K;  F  A' and b' from E^T, G0^T.
+// Every operand derived from T (rows of T, of T^T, of (T diag(beta))^T) is split
+// into registers straight from the fp32 T, the K^T operands are gathered by column
+// from K, and the gated diag(ptok) and diag(p) scalings are applied to those
+// register operands, so none of them takes LDS.
+template <bool GATED>
+__global__ __launch_bounds__(NTB) void dwb_bwd_prep(
+    const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
+    const u16* __restrict__ beta, const float* __restrict__ lg, const u16* __restrict__ dy,
+    const float* __restrict__ Hb, float* __restrict__ Uo, float* __restrict__ Eo,
+    float* __restrict__ G0o, float* __restrict__ Apo, float* __restrict__ bpo,
+    float* __restrict__ vo, DwGeom g) {
+  __shared__ BMat sK;        // K as (m; d), exact
+  __shared__ BMat sQD[2];    // Q^T as (d; t), dy^T as (j; t), exact
+  __shared__ BPair sR1;      // [gated span table] -> Hc^T -> P^T -> G0^T
+  __shared__ BPair sR2;      // inverse workspace -> R^T -> D1^T -> E^T
+  __shared__ float sT[DN * LD];  // L, then T (in place)
+  __shared__ float sb[DN];
+  __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
+  float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
+        *spt = sdec + 4 * DN;
+  BMat &sQt = sQD[0], &sDyt = sQD[1];
+  const int c = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const Chunk ch = chunk_of(g, c);
+  const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
+  const int64_t trow0 = bh * g.T + ch.t0;
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  FragOff F;
+  F.init();
+  const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
+  const int R0 = 16 * F.rb, C0 = 32 * F.ch;
+  FTile th;  // Hc, staged in stage B
+  {
+    BTile tk, tq, td;
+    tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
+    tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
+    td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
+    th.load(Hb + mat, g.dk, g.dv);
+    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    tk.put(sK);
+    tq.put_t(sQt);
+    td.put_t(sDyt);
+    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    if constexpr (GATED) {
+      const float lv = ld_l(lg, bh, g, ch);
+      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+    }
+  }
+  __syncthreads();
+  // ---- A: L, then T = (I + L)^-1 in place ----
+  float ew[2][4];  // gated: E[row][col] at the wave's fragment positions (nh = 1)
+  if constexpr (GATED) {
+    float* sE = reinterpret_cast<float*>(&sR1);  // span table, row stride DN
+    decay_tables<NTB, DN>(sl, sE);
+    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
+    write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);  // wave 0's own values
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = C0 + 16 * jj + r;
+        ew[jj][i] = col <= row ? sE[row * DN + col] : 0.f;
+      }
+  }
+  {
+    floatx4 kk[2];
+    zero2(kk);
+    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        kk[jj][i] = col < row ? kk[jj][i] * sb[col] * (GATED ? ew[jj][i] : 1.f) : 0.f;
+      }
+      acc_store_lds(kk[jj], sT + R0 * LD + cj, LD);
+    }
+  }
+  __syncthreads();  // L complete (and, gated, the span table read)
+  unit_lower_inverse(sT, sT, reinterpret_cast<float*>(&sR2));  // ends with a barrier
+  // ---- B: R = V - K Hc (gated: V - diag(p) K Hc) -> R^T ----
+  th.put_split_t(sR1);  // Hc^T as (j; d)
+  __syncthreads();
+  {
+    floatx4 rr[2];
+    zero2(rr);
+    bmm<false, true>(rr, F, &sK, sR1);  // K Hc
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = R0 + 4 * gg + i, j = cj + r;
+        const float v = (m < ch.M && j < g.dv) ? ldf(V, (row0 + m) * g.dv + j) : 0.f;
+        rr[jj][i] = fmaf(GATED ? -sp[m] : -1.f, rr[jj][i], v);
+      }
+      acc_put_t(sR2, rr[jj], R0, cj);
+    }
+  }
+  __syncthreads();
+  // ---- C: U = T R ----
+  {
+    uint4 ah[2], al[2];
+    t_frags<false>(ah, al, sT, R0, nullptr);
+    floatx4 u[2];
+    zero2(u);
+    smm<true>(u, F, ah, al, sR2);
+    store_block_f32(Uo + mat, u, R0, C0);
+  }
+  // ---- D: P = (Q K^T) * beta_col * read -> P^T; qd = Q^T dy; D1 = P^T dy ----
+  floatx4 qd[2];  // Q^T dy (gated: Q^T diag(ptok) dy), kept for b'
+  zero2(qd);
+  {
+    uint4 qf[2];
+    load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
+    floatx4 pp[2];
+    zero2(pp);
+    rmm<false>(pp, F, qf, &sK);  // Q K^T
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int cj = C0 + 16 * jj;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = R0 + 4 * gg + i, col = cj + r;
+        if constexpr (GATED)  // nh = 1: micro-rows are tokens
+          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * ew[jj][i] : 0.f;
+        else
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+      }
+      acc_put_t(sR1, pp[jj], R0, cj);  // P^T as (m; t)
+    }
+  }
+  if constexpr (GATED) {  // (Q diag(ptok))^T as split register fragments
+    uint4 ah[2], al[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int k0 = 8 * (4 * s + gg);
+      const uint4 qv = sQt.v[bpos(R0 + r, 4 * s + gg)];
+      const u16* e = reinterpret_cast<const u16*>(&qv);
+      float x[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = bf_val(e[q]) * spt[k0 + q];
+      split_frag(x, ah[s], al[s]);
+    }
+    smm<false>(qd, F, ah, al, &sDyt);
+  } else {
+    bmm<false, false>(qd, F, &sQt, &sDyt);  // Q^T dy
+  }
+  __syncthreads();  // P^T complete; every wave is past C (R^T free)
+  {
+    floatx4 d1[2];
+    zero2(d1);
+    bmm<true, false>(d1, F, sR1, &sDyt);  // P^T dy
+    acc_put_t(sR2, d1[0], R0, C0);        // D1^T as (j; m)
+    acc_put_t(sR2, d1[1], R0, C0 + 16);
+  }
+  __syncthreads();
+  // ---- E: G0 = T^T D1 -> G0^T; E = (T diag(s))^T K, s = beta (gated: a beta) ----
+  floatx4 ev[2];
+  {
+    uint4 ah[2], al[2];
+    t_frags<true>(ah, al, sT, R0, nullptr);
+    floatx4 g0[2];
+    zero2(g0);
+    smm<true>(g0, F, ah, al, sR2);
+    store_block_f32(G0o + mat, g0, R0, C0);
+    acc_put_t(sR1, g0[0], R0, C0);  // G0^T as (j; m); P^T is free
+    acc_put_t(sR1, g0[1], R0, C0 + 16);
+    t_frags<true>(ah, al, sT, R0, GATED ? sab : sb);
+    zero2(ev);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const bf16x8 h = __builtin_bit_cast(bf16x8, ah[s]), l = __builtin_bit_cast(bf16x8, al[s]);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const bf16x8 kb = __builtin_bit_cast(bf16x8, col_frag(sK, C0 + 16 * jj + r, s));
+        ev[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h, kb, ev[jj], 0, 0, 0);
+        ev[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l, kb, ev[jj], 0, 0, 0);
+      }
+    }
+    store_block_split(reinterpret_cast<u16*>(Eo + mat), ev, R0, C0);
+  }
+  __syncthreads();  // D1^T read by every wave
+  acc_put_t(sR2, ev[0], R0, C0);  // E^T as (d; m)
+  acc_put_t(sR2, ev[1], R0, C0 + 16);
+  __syncthreads();
+  // ---- F: A' = -K^T E, b' = qd - K^T G0 (gated: (p K)^T) ----
+  {
+    floatx4 a2[2];
+    zero2(a2);
+    if constexpr (GATED) {
+      uint4 ah[2], al[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int k0 = 8 * (4 * s + gg);
+        const uint4 kv = col_frag(sK, R0 + r, s);
+        const u16* e = reinterpret_cast<const u16*>(&kv);
+        float x[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = bf_val(e[q]) * sp[k0 + q];
+        split_frag(x, ah[s], al[s]);
+      }
+      smm<true, true>(a2, F, ah, al, sR2);  // -(p K)^T E
+      smm<true, true>(qd, F, ah, al, sR1);  // b' = Q^T diag(ptok) dy - (p K)^T G0
+    } else {
+      uint4 kf[2];
+      kf[0] = col_frag(sK, R0 + r, 0);
+      kf[1] = col_frag(sK, R0 + r, 1);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 a = bneg(__builtin_bit_cast(bf16x8, kf[s]));
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const unsigned off = F.b[s][jj];
+          a2[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, frag_at(sR2[0], off), a2[jj], 0, 0, 0);
+          a2[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, frag_at(sR2[1], off), a2[jj], 0, 0, 0);
+          qd[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, frag_at(sR1[0], off), qd[jj], 0, 0, 0);
+          qd[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, frag_at(sR1[1], off), qd[jj], 0, 0, 0);
+        }
+      }
+    }
+    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
+    store_block_f32(bpo + mat, qd, R0, C0);
   }
 }
 
