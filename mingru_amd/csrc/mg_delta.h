@@ -231,7 +231,7 @@ __device__ __forceinline__ Chunk chunk_of(const DwGeom& g, int c) {
 // 32 x 32 half, then the lower-left 32 x 32 block -T_22' L' T_11'.
 // sT receives the full lower-triangular inverse with zeroed upper blocks.
 // ---------------------------------------------------------------------------
-__device__ inline void unit_lower_inverse(const float* sL, float* sT, float* sY) {
+__device__ __forceinline__ void unit_lower_inverse(const float* sL, float* sT, float* sY) {
   // Waves 0..3 do the work; further waves of a larger workgroup only join the
   // barriers.  (An earlier form gave each wave one diagonal block and reduced the
   // substitution sums across lane groups with shuffles: 16 dependent LDS round
