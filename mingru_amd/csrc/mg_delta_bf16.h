@@ -301,6 +301,22 @@ __device__ __forceinline__ void store_block_f32(float* dst, const floatx4 (&v)[2
   }
 }
 
+// Fragment-major fp32 workspace matrix: the 16 x 16 tile (row block rb, column
+// block cb) holds, for lane L = 16 g + r, rows 16 rb + 4 g + i (i = 0..3) of column
+// 16 cb + r as 4 consecutive floats, so one wave moves a tile in accumulator layout
+// with a single 16-byte access per lane (1 KiB contiguous).  The chains' fp32 chunk
+// operands (B, Pu, b') use it: loaded with one instruction per tile instead of
+// four, a step keeps fewer vector-memory operations in flight per wave.
+__device__ __forceinline__ void store_block_frag(float* dst, const floatx4 (&v)[2], int R0, int C0) {
+  const int t0 = (R0 >> 4) * 4 + (C0 >> 4);
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+    *reinterpret_cast<floatx4*>(dst + (t0 + jj) * 256 + lane_id() * 4) = v[jj];
+}
+__device__ __forceinline__ floatx4 load_tile_frag(const float* src, int rb, int cb) {
+  return *reinterpret_cast<const floatx4*>(src + (rb * 4 + cb) * 256 + lane_id() * 4);
+}
+
 // Split workspace matrix: a 64 x 64 row-major bf16 hi half followed by the lo
 // half (the 16 KB of one padded fp32 matrix slot).  Read back by the chains as
 // MFMA A fragments straight from memory.
@@ -354,7 +370,7 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked),
 //   P = (Q K^T) * beta_col * read, M1 = (beta K)^T T, M2 = P T;
 //   A = -M1 K, B = M1 V, Qe = Q - M2 K, Pu = M2 V
-//   -> A, Qe (split bf16 pairs), B, Pu (fp32) in the workspace.
+//   -> A, Qe (split bf16 pairs), B, Pu (fp32, fragment-major) in the workspace.
 // (W = T K and U0 = T V never materialise: A = -K^T diag(beta) W = -M1 K, etc.)
 // LDS stays under 80 KB, so two workgroups share a CU.
 // GATED (per-token decay, decay tables in mg_delta.h): L and P are weighted by
@@ -521,9 +537,9 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
     bmm<true, false>(b2, F, sM1, &sVt);  // B = M1 V
     bmm<true, false>(pu, F, sM2, &sVt);  // Pu = M2 V
     store_block_split(reinterpret_cast<u16*>(Ao + mat), a2, R0, C0);
-    store_block_f32(Bo + mat, b2, R0, C0);
+    store_block_frag(Bo + mat, b2, R0, C0);
     store_block_split(reinterpret_cast<u16*>(Qeo + mat), qe, R0, C0);
-    store_block_f32(Puo + mat, pu, R0, C0);
+    store_block_frag(Puo + mat, pu, R0, C0);
   }
 }
 
@@ -644,7 +660,7 @@ __device__ __forceinline__ void smm(floatx4 (&acc)[2], const FragOff& F, const u
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
 //   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
 //   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
-//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32) for the
+//   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32, fragment-major) for the
 //      reverse chain.
 // GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
 // E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E.
@@ -882,7 +898,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
       }
     }
     store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
-    store_block_f32(bpo + mat, qd, R0, C0);
+    store_block_frag(bpo + mat, qd, R0, C0);
   }
 }
 
@@ -1302,8 +1318,8 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Am + mat), 16 * w + r);
     load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), 16 * w + r);
-    o.b = acc_load_ws(Bm + mat + 16 * w * DN + col0);
-    o.pu = acc_load_ws(Pum + mat + 16 * w * DN + col0);
+    o.b = load_tile_frag(Bm + mat, w, col0 >> 4);
+    o.pu = load_tile_frag(Pum + mat, w, col0 >> 4);
     if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
   };
   // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
@@ -1380,7 +1396,7 @@ __global__ __launch_bounds__(NT) void dwb_bwd_chain(const float* __restrict__ dH
   auto fetch = [&](BwdOps& o, int c) {
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), 16 * w + r);
-    o.b = acc_load_ws(bpm + mat + 16 * w * DN + col0);
+    o.b = load_tile_frag(bpm + mat, w, col0 >> 4);
     if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
   };
   // Chunk c - 2 is fetched while chunk c computes (ring of three buffers).
