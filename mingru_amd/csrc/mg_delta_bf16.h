@@ -266,6 +266,67 @@ struct FTile {
   }
 };
 
+// fp32 block (rows x cols) of a fragment-major workspace matrix (store_tile_frag's
+// layout): thread idx holds entry e = idx + 512 v (v = 0, 1), i.e. tile t = e / 64 and
+// lane L = e % 64 of it -- rows 16 (t / 4) + 4 (L / 16) + 0..3 of column 16 (t % 4) +
+// L % 16 -- with one contiguous 16-byte load; zero outside the block.
+struct FTileF {
+  float4 f[2];
+
+  __device__ static __forceinline__ void coords(int v, int& d0, int& j) {
+    const int e = threadIdx.x + v * NTB, t = e >> 6, L = e & 63;
+    d0 = 16 * (t >> 2) + 4 * (L >> 4);
+    j = 16 * (t & 3) + (L & 15);
+  }
+  __device__ __forceinline__ void load(const float* src, int rows, int cols) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      int d0, j;
+      coords(v, d0, j);
+      float4 x = *reinterpret_cast<const float4*>(src + (threadIdx.x + v * NTB) * 4);
+      if (j >= cols || d0 + 0 >= rows) x.x = 0.f;
+      if (j >= cols || d0 + 1 >= rows) x.y = 0.f;
+      if (j >= cols || d0 + 2 >= rows) x.z = 0.f;
+      if (j >= cols || d0 + 3 >= rows) x.w = 0.f;
+      f[v] = x;
+    }
+  }
+  // The same entries of a row-major matrix (row stride DN): four rows of one column.
+  __device__ __forceinline__ void load_rowmajor(const float* src, int rows, int cols) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      int d0, j;
+      coords(v, d0, j);
+      const bool c = j < cols;
+      f[v] = make_float4(c && d0 + 0 < rows ? src[(d0 + 0) * DN + j] : 0.f,
+                         c && d0 + 1 < rows ? src[(d0 + 1) * DN + j] : 0.f,
+                         c && d0 + 2 < rows ? src[(d0 + 2) * DN + j] : 0.f,
+                         c && d0 + 3 < rows ? src[(d0 + 3) * DN + j] : 0.f);
+    }
+  }
+  // (row, k = column)
+  __device__ __forceinline__ void put_split(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      int d0, j;
+      coords(v, d0, j);
+      put_split1(m, d0 + 0, j, f[v].x);
+      put_split1(m, d0 + 1, j, f[v].y);
+      put_split1(m, d0 + 2, j, f[v].z);
+      put_split1(m, d0 + 3, j, f[v].w);
+    }
+  }
+  // transposed: (row = column, k = row), four consecutive k per entry
+  __device__ __forceinline__ void put_split_t(BPair& m) const {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      int d0, j;
+      coords(v, d0, j);
+      put_split4(m, j, d0, f[v].x, f[v].y, f[v].z, f[v].w);
+    }
+  }
+};
+
 // The wave's 16 x 32 output block (rows R0 + 4 g + i, columns C0 + 16 jj + r) into a
 // bf16 row-major output with row stride ld, keeping rows < nr and columns < nc.
 __device__ __forceinline__ void store_block_bf16(u16* dst, int64_t ld, const floatx4 (&v)[2],
@@ -306,12 +367,16 @@ __device__ __forceinline__ void store_block_f32(float* dst, const floatx4 (&v)[2
 // 16 cb + r as 4 consecutive floats, so one wave moves a tile in accumulator layout
 // with a single 16-byte access per lane (1 KiB contiguous).  The chains' fp32 chunk
 // operands (B, Pu, b') use it: loaded with one instruction per tile instead of
-// four, a step keeps fewer vector-memory operations in flight per wave.
+// four, a step keeps fewer vector-memory operations in flight per wave.  So does the
+// forward chain's state output Hb (one store per lane per step).
 __device__ __forceinline__ void store_block_frag(float* dst, const floatx4 (&v)[2], int R0, int C0) {
   const int t0 = (R0 >> 4) * 4 + (C0 >> 4);
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj)
     *reinterpret_cast<floatx4*>(dst + (t0 + jj) * 256 + lane_id() * 4) = v[jj];
+}
+__device__ __forceinline__ void store_tile_frag(float* dst, int rb, int cb, const floatx4& v) {
+  *reinterpret_cast<floatx4*>(dst + (rb * 4 + cb) * 256 + lane_id() * 4) = v;
 }
 __device__ __forceinline__ floatx4 load_tile_frag(const float* src, int rb, int cb) {
   return *reinterpret_cast<const floatx4*>(src + (rb * 4 + cb) * 256 + lane_id() * 4);
@@ -705,7 +770,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   F.init();
   const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int R0 = 16 * F.rb, C0 = 32 * F.ch;
-  FTile th;  // Hc, staged in stage B
+  FTileF th;  // Hc, staged in stage B
   {
     BTile tk, tq, td;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
@@ -989,14 +1054,15 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
   }
   {
     // U and Hc are fetched while G forms, and staged once E and dHn^T are free.
-    FTile tu, th;
+    FTile tu;
+    FTileF th;
     tu.load(Um + mat, ch.M, g.dv);
     th.load(Hb + mat, g.dk, g.dv);
     bmm<true, true>(gacc, F, sR[0], sR[1]);  // G = G0 + E dHn   (rows m, cols j)
     store_block_bf16(dV + row0 * g.dv, g.dv, gacc, R0, C0, ch.M, g.dv);
     if constexpr (GATED) {  // <dHn, Hc> from two fp32 tiles of the same layout
-      FTile tn2;
-      tn2.load(dHn + mat, g.dk, g.dv);
+      FTileF tn2;  // dHn at th's positions (row-major source)
+      tn2.load_rowmajor(dHn + mat, g.dk, g.dv);
       float part = 0.f;
 #pragma unroll
       for (int v = 0; v < 2; ++v)
@@ -1333,7 +1399,7 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     BPair& ht = sHt[c & 1];
     acc_put_t(ht, h, 16 * w, 0);
-    acc_store_ws(h, Hb + mat + 16 * w * DN + col0);
+    store_tile_frag(Hb + mat, w, col0 >> 4, h);
     __syncthreads();
     floatx4 yy = {0.f, 0.f, 0.f, 0.f};  // Pu is added after the products
 #pragma unroll
