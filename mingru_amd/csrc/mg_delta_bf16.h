@@ -987,7 +987,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 // a beta rowsum(U (K dHn)) and f[t] (ptok: ptok_t sum_d Q (dy Hc^T), p: p_m
 // sum_d K (-G Hc^T), PC: PC <dHn, Hc>) give dl_s = sum_{t >= s} (f[t] +
 // sum_{t' < s} F[t][t']) by wave-level prefix scans.  The span table needs its
-// own 16 KB, so a gated workgroup has the CU to itself.
+// own 16 KB and the span gradients stay in registers to the end (about 180 VGPRs),
+// so a gated workgroup has the CU to itself.
 template <bool GATED>
 __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ beta,
