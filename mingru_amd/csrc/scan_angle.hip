@@ -23,8 +23,8 @@
 //   pass 1  one lane per (block, chunk) builds the chunk's affine map
 //           h -> P_c h + L_c by pushing the k columns of P and the column L
 //           through the chunk's rotations (k+1 rotated columns per token);
-//   pass 2  one lane per block walks the chunk boundaries in order,
-//           h_{c+1} = P_c h_c + L_c, carrying only its k-vector;
+//   pass 2  two lanes per block walk the chunk boundaries in order,
+//           h_{c+1} = P_c h_c + L_c, carrying only its k-vector (half each);
 //   pass 3  one lane per (block, chunk) re-applies the rotations to the state
 //           vector from its chunk-entry state and writes every h_t.
 // The forward saves the chunk products P_c for the backward.
@@ -53,8 +53,8 @@ enum : int { SCHED_BRICK = 0, SCHED_LEX = 1 };
 // rotations from each chunk's entry state.  No workgroup waits on another.
 constexpr int AN_WAVES = 4;          // waves per workgroup of the chunk-parallel passes
 constexpr int AN_CHUNK = 16;         // tokens per chunk
-constexpr int AN_SCAN_THREADS = 256;  // threads per workgroup of the boundary walk
-constexpr int AN_SCAN_AHEAD = 8;      // chunks prefetched ahead by the boundary walk
+constexpr int AN_WALK_THREADS = 64;  // boundary walk: one wave per workgroup (each on its own CU)
+constexpr int AN_WALK_AHEAD = 3;     // chunks prefetched ahead by the boundary walk
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -425,48 +425,78 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
 }
 
 // ---- forward pass 2: states at chunk boundaries, h_{c+1} = P_c h_c + L_c -------
-// K lanes per block, lane q owning state row q; the state vector is exchanged
-// within the K-lane group by shuffles.  Each lane's row of (P_c, L_c) is
-// prefetched AN_SCAN_AHEAD chunks ahead, because one step is only K FMAs and
-// the walk would otherwise wait a full memory latency per chunk.
+// Two lanes per block, lane p owning state rows K/2 p .. K/2 p + K/2 - 1.  Each
+// lane loads columns K/2 p .. of every row of P_c (one 16-byte piece per row, so
+// the two lanes of a block read each row's 32 bytes together), forms the partial
+// sums of all K rows over its own half of h, and the pair exchanges the partials
+// of each other's rows by DPP quad_perm moves (no LDS crossbar).  The loads are
+// prefetched AN_WALK_AHEAD chunks ahead in a ring of registers.
+
+// The partner lane's value (lane ^ 1), by DPP quad_perm [1, 0, 3, 2].
+__device__ __forceinline__ float pair_swap(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+
+// Own-row results from partial sums over the lane's half: part[i] covers all K rows;
+// out[i] = base[i] + own partial + the partner's partial for row H p + i.
 template <int K>
-__global__ __launch_bounds__(AN_SCAN_THREADS) void angle_fwd_scan(AnArgs a, AnGeom g) {
-  const int64_t gt = (int64_t)blockIdx.x * AN_SCAN_THREADS + threadIdx.x;
-  const int64_t blk = gt / K;
-  const int q = (int)(gt % K);
-  if (blk >= g.NB) return;  // whole K-lane groups leave together
-  constexpr int D = AN_SCAN_AHEAD;
-  // Double-buffered batches of D chunks: the loads of batch b+1 are in flight
-  // while batch b is walked from registers.
-  float cur[D][K + 1], nxt[D][K + 1];
-  auto fetch = [&](int c0, float (&r)[D][K + 1]) {
+__device__ __forceinline__ void pair_reduce(const float (&part)[K], int p, const float* base,
+                                            float* out) {
+  constexpr int H = K / 2;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = min(c0 + d, g.n_chunks - 1);  // clamped reads past the end are unused
-      ld<K>(r[d], a.prod + an_idx(g, c, q * K, K * K, blk));
-      r[d][K] = a.lsum[an_idx(g, c, q, K, blk)];
-    }
-  };
-  fetch(0, cur);
-  float h = a.h0[blk * K + q];
-  for (int c0 = 0; c0 < g.n_chunks; c0 += D) {
-    fetch(c0 + D, nxt);
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = c0 + d;
-      if (c < g.n_chunks) {
-        a.bound[an_idx(g, c, q, K, blk)] = h;
-        float acc = cur[d][K];
-#pragma unroll
-        for (int j = 0; j < K; ++j) acc = fmaf(cur[d][j], __shfl(h, j, K), acc);
-        h = acc;
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int j = 0; j <= K; ++j) cur[d][j] = nxt[d][j];
+  for (int i = 0; i < H; ++i) {
+    const float mine = p ? part[H + i] : part[i], theirs = p ? part[i] : part[H + i];
+    out[i] = base[i] + mine + pair_swap(theirs);
   }
+}
+
+template <int K>
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_fwd_scan(AnArgs a, AnGeom g) {
+  constexpr int H = K / 2;
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int64_t blk = gt >> 1;
+  const int p = (int)(gt & 1);
+  if (blk >= g.NB) return;  // the two lanes of a block leave together
+  struct Op {
+    float P[K * H];  // [i][jj]: row i of P_c, column H p + jj
+    float L[H];
+  };
+  auto fetch = [&](Op& o, int c) {
+    c = min(c, g.n_chunks - 1);  // clamped reads past the end are unused
+    const float* pc = a.prod + an_idx(g, c, H * p, K * K, blk);
+#pragma unroll
+    for (int i = 0; i < K; ++i) ld<H>(o.P + i * H, pc + i * K);
+    ld<H>(o.L, a.lsum + an_idx(g, c, H * p, K, blk));
+  };
+  float h[H];
+  ld<H>(h, a.h0 + blk * K + H * p);
+  auto step = [&](const Op& o, Op& fill, int c) {
+    fetch(fill, c + AN_WALK_AHEAD);
+    st<H>(a.bound + an_idx(g, c, H * p, K, blk), h);
+    float part[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < H; ++jj) acc = fmaf(o.P[i * H + jj], h[jj], acc);
+      part[i] = acc;
+    }
+    pair_reduce<K>(part, p, o.L, h);
+  };
+  Op b0, b1, b2, b3;  // ring: chunk c sits in slot c % 4, the loop unrolled by four
+  fetch(b0, 0);
+  fetch(b1, 1);
+  fetch(b2, 2);
+  int c = 0;
+  for (; c + 4 <= g.n_chunks; c += 4) {
+    step(b0, b3, c);
+    step(b1, b0, c + 1);
+    step(b2, b1, c + 2);
+    step(b3, b2, c + 3);
+  }
+  if (c < g.n_chunks) step(b0, b3, c);
+  if (c + 1 < g.n_chunks) step(b1, b0, c + 1);
+  if (c + 2 < g.n_chunks) step(b2, b1, c + 2);
 }
 
 // ---- forward pass 3: every token's state from its chunk-entry state ------------
@@ -688,49 +718,74 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, 
   st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), xf);
 }
 
+// The whole state from the lane's half: lo = rows 0 .. K/2 - 1, hi = the rest.
+template <int H>
+__device__ __forceinline__ void pair_state(const float (&own)[H], int p, float (&lo)[H],
+                                           float (&hi)[H]) {
+#pragma unroll
+  for (int j = 0; j < H; ++j) {
+    const float o = pair_swap(own[j]);
+    lo[j] = p ? o : own[j];
+    hi[j] = p ? own[j] : o;
+  }
+}
+
 // ---- backward pass 2: adjoints at chunk boundaries, right to left --------------
-// y_out = P_c^T y_in + Lb_c; K lanes per block, lane q owning adjoint row q
-// (column q of P_c), prefetched as in the forward walk.
+// y_out = P_c^T y_in + Lb_c; two lanes per block as in the forward walk, lane p
+// loading columns K/2 p .. K/2 p + K/2 - 1 of P_c (one 16-byte piece per row).
 template <int K>
-__global__ __launch_bounds__(AN_SCAN_THREADS) void angle_bwd_scan(AnArgs a, AnGeom g) {
-  const int64_t gt = (int64_t)blockIdx.x * AN_SCAN_THREADS + threadIdx.x;
-  const int64_t blk = gt / K;
-  const int q = (int)(gt % K);
-  if (blk >= g.NB) return;
-  constexpr int D = AN_SCAN_AHEAD;
-  float cur[D][K + 1], nxt[D][K + 1];
-  auto fetch = [&](int c0, float (&r)[D][K + 1]) {  // chunks c0, c0-1, ..., c0-D+1
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_bwd_scan(AnArgs a, AnGeom g) {
+  constexpr int H = K / 2;
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int64_t blk = gt >> 1;
+  const int p = (int)(gt & 1);
+  if (blk >= g.NB) return;  // the two lanes of a block leave together
+  struct Op {
+    float P[K * H];  // [j][i]: columns H p .. H p + H - 1 of P_c, row j
+    float L[H];
+  };
+  auto fetch = [&](Op& o, int c) {
+    c = max(c, 0);  // clamped reads past the start are unused
+    const float* pc = a.prod + an_idx(g, c, H * p, K * K, blk);
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = max(c0 - d, 0);  // clamped reads past the start are unused
-      const float* pc = a.prod + an_idx(g, c, 0, K * K, blk);
+    for (int j = 0; j < K; ++j) ld<H>(o.P + j * H, pc + j * K);
+    ld<H>(o.L, a.lsum + an_idx(g, c, H * p, K, blk));
+  };
+  float y[H];
 #pragma unroll
-      for (int i = 0; i < K; ++i) r[d][i] = pc[i * K + q];
-      r[d][K] = a.lsum[an_idx(g, c, q, K, blk)];
+  for (int i = 0; i < H; ++i) y[i] = 0.f;
+  // y <- P_c^T y + Lb_c, rows H p + i of the result from column H p + i of P_c.
+  auto step = [&](const Op& o, Op& fill, int c) {
+    fetch(fill, c - AN_WALK_AHEAD);
+    st<H>(a.bound + an_idx(g, c, H * p, K, blk), y);
+    float lo[H], hi[H];
+    pair_state<H>(y, p, lo, hi);
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      float acc = o.L[i];
+#pragma unroll
+      for (int j = 0; j < H; ++j) acc = fmaf(o.P[j * H + i], lo[j], acc);
+#pragma unroll
+      for (int j = 0; j < H; ++j) acc = fmaf(o.P[(H + j) * H + i], hi[j], acc);
+      y[i] = acc;
     }
   };
   const int last = g.n_chunks - 1;
-  fetch(last, cur);
-  float y = 0.f;
-  for (int c0 = last; c0 >= 0; c0 -= D) {
-    fetch(c0 - D, nxt);
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = c0 - d;
-      if (c >= 0) {
-        a.bound[an_idx(g, c, q, K, blk)] = y;
-        float acc = cur[d][K];
-#pragma unroll
-        for (int i = 0; i < K; ++i) acc = fmaf(cur[d][i], __shfl(y, i, K), acc);
-        y = acc;
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int i = 0; i <= K; ++i) cur[d][i] = nxt[d][i];
+  Op b0, b1, b2, b3;  // ring, as in the forward walk, in reverse chunk order
+  fetch(b0, last);
+  fetch(b1, last - 1);
+  fetch(b2, last - 2);
+  int c = last;
+  for (; c - 3 >= 0; c -= 4) {
+    step(b0, b3, c);
+    step(b1, b0, c - 1);
+    step(b2, b1, c - 2);
+    step(b3, b2, c - 3);
   }
-  a.dh0[blk * K + q] = y;  // the adjoint leaving chunk 0 is dL/dh0
+  if (c >= 0) step(b0, b3, c);
+  if (c - 1 >= 0) step(b1, b0, c - 1);
+  if (c - 2 >= 0) step(b2, b1, c - 2);
+  st<H>(a.dh0 + blk * K + H * p, y);  // the adjoint leaving chunk 0 is dL/dh0
 }
 
 // ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
@@ -830,8 +885,8 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
   a.bound = (float*)((char*)ws + MG_HEADER_BYTES + one);
   const int64_t waves = (int64_t)g.n_lg * g.n_chunks;
   const dim3 grid((unsigned)((waves + AN_WAVES - 1) / AN_WAVES)), block(MG_WAVE * AN_WAVES);
-  const dim3 sgrid((unsigned)((g.NB * K + AN_SCAN_THREADS - 1) / AN_SCAN_THREADS)),
-      sblock(AN_SCAN_THREADS);
+  const dim3 sgrid((unsigned)((g.NB * 2 + AN_WALK_THREADS - 1) / AN_WALK_THREADS)),
+      sblock(AN_WALK_THREADS);
   if (BWD) {
     hipLaunchKernelGGL((angle_bwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
     hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, a, g);
