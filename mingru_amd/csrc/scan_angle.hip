@@ -54,7 +54,8 @@ enum : int { SCHED_BRICK = 0, SCHED_LEX = 1 };
 constexpr int AN_WAVES = 4;          // waves per workgroup of the chunk-parallel passes
 constexpr int AN_CHUNK = 16;         // tokens per chunk
 constexpr int AN_WALK_THREADS = 64;  // boundary walk: one wave per workgroup (each on its own CU)
-constexpr int AN_WALK_AHEAD = 3;     // chunks prefetched ahead by the boundary walk
+constexpr int AN_WALK_AHEAD = 4;     // chunks prefetched ahead by the boundary walk
+constexpr int AN_WALK_RING = AN_WALK_AHEAD + 1;
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -483,20 +484,18 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_fwd_scan(AnArgs a, AnGe
     }
     pair_reduce<K>(part, p, o.L, h);
   };
-  Op b0, b1, b2, b3;  // ring: chunk c sits in slot c % 4, the loop unrolled by four
-  fetch(b0, 0);
-  fetch(b1, 1);
-  fetch(b2, 2);
+  constexpr int R = AN_WALK_RING;  // ring: chunk c sits in slot c % R, the loop unrolled by R
+  Op buf[R];
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d) fetch(buf[d], d);
   int c = 0;
-  for (; c + 4 <= g.n_chunks; c += 4) {
-    step(b0, b3, c);
-    step(b1, b0, c + 1);
-    step(b2, b1, c + 2);
-    step(b3, b2, c + 3);
+  for (; c + R <= g.n_chunks; c += R) {
+#pragma unroll
+    for (int d = 0; d < R; ++d) step(buf[d], buf[(d + R - 1) % R], c + d);
   }
-  if (c < g.n_chunks) step(b0, b3, c);
-  if (c + 1 < g.n_chunks) step(b1, b0, c + 1);
-  if (c + 2 < g.n_chunks) step(b2, b1, c + 2);
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d)
+    if (c + d < g.n_chunks) step(buf[d], buf[(d + R - 1) % R], c + d);
 }
 
 // ---- forward pass 3: every token's state from its chunk-entry state ------------
@@ -771,20 +770,18 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_bwd_scan(AnArgs a, AnGe
     }
   };
   const int last = g.n_chunks - 1;
-  Op b0, b1, b2, b3;  // ring, as in the forward walk, in reverse chunk order
-  fetch(b0, last);
-  fetch(b1, last - 1);
-  fetch(b2, last - 2);
+  constexpr int R = AN_WALK_RING;  // ring, as in the forward walk, in reverse chunk order
+  Op buf[R];
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d) fetch(buf[d], last - d);
   int c = last;
-  for (; c - 3 >= 0; c -= 4) {
-    step(b0, b3, c);
-    step(b1, b0, c - 1);
-    step(b2, b1, c - 2);
-    step(b3, b2, c - 3);
+  for (; c - (R - 1) >= 0; c -= R) {
+#pragma unroll
+    for (int d = 0; d < R; ++d) step(buf[d], buf[(d + R - 1) % R], c - d);
   }
-  if (c >= 0) step(b0, b3, c);
-  if (c - 1 >= 0) step(b1, b0, c - 1);
-  if (c - 2 >= 0) step(b2, b1, c - 2);
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d)
+    if (c - d >= 0) step(buf[d], buf[(d + R - 1) % R], c - d);
   st<H>(a.dh0 + blk * K + H * p, y);  // the adjoint leaving chunk 0 is dL/dh0
 }
 
