@@ -636,9 +636,12 @@ class _AngleScanFn(torch.autograd.Function):
         (gh32,) = _as_f32(gh)
         dth = torch.empty_like(th)
         need = ctx.needs_input_grad
-        # Grads of a disabled scale / decay channel are zero (never read by the kernel).
-        dsc = torch.zeros_like(sc) if (flags & 1 or need[1]) else None
-        dgm = torch.zeros_like(gm) if (flags & 2 or need[2]) else None
+        # An enabled scale / decay channel has every element of its grad written by the
+        # kernel; a disabled one's grad is zero (the kernel never touches it).
+        dsc = (torch.empty_like(sc) if flags & 1 else torch.zeros_like(sc)) \
+            if (flags & 1 or need[1]) else None
+        dgm = (torch.empty_like(gm) if flags & 2 else torch.zeros_like(gm)) \
+            if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
         ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
