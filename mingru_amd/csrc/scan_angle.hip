@@ -345,6 +345,29 @@ struct LexTok {
   }
 };
 
+// Runs body(tok, t) over `count` tokens t = first, first + dir, ..., each token's
+// inputs loaded one token ahead into two alternating buffers.  The next token's
+// loads are issued unconditionally (the index clamped to the range) before the
+// current token's body and in the same basic block, so they overlap it.  A
+// conditional prefetch into a buffer copied at the loop's end let the compiler
+// sink the loads down to the copy, next to their first use.
+template <typename Tok, typename Load, typename Body>
+__device__ __forceinline__ void token_pairs(int64_t first, int count, int dir, Load&& load,
+                                            Body&& body) {
+  Tok A, B;
+  load(A, first);
+  const int64_t last = first + (int64_t)(count - 1) * dir;
+  int i = 0;
+  for (; i + 2 <= count; i += 2) {
+    const int64_t t = first + (int64_t)i * dir;
+    load(B, t + dir);
+    body(A, t);
+    load(A, i + 2 < count ? t + 2 * dir : last);
+    body(B, t + dir);
+  }
+  if (i < count) body(A, first + (int64_t)i * dir);
+}
+
 struct AnGeom {
   int64_t T, n, NB;  // tokens, blocks per batch row, blocks in total (B * n)
   int n_tiles, n_lg, n_chunks;
@@ -391,17 +414,17 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
     for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
   const int64_t te = min(t0 + AN_CHUNK, g.T);
   if constexpr (SCHED == SCHED_LEX) {
-    LexTok<K, HS, HD> cur, nxt;
-    cur.template load<false>(a, a.b, (th.bb * g.T + t0) * g.n + th.plane, t0, g.n, th.blk);
-    for (int64_t t = t0; t < te; ++t) {
-      if (t + 1 < te)
-        nxt.template load<false>(a, a.b, (th.bb * g.T + t + 1) * g.n + th.plane, t + 1, g.n,
-                                 th.blk);
-      apply_M_lex<K, HS, HD, K + 1>(X, cur.ang, cur.d, cur.gm);
+    using Tok = LexTok<K, HS, HD>;
+    token_pairs<Tok>(
+        t0, (int)(te - t0), 1,
+        [&](Tok& k, int64_t t) {
+          k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+        },
+        [&](const Tok& cur, int64_t) {
+          apply_M_lex<K, HS, HD, K + 1>(X, cur.ang, cur.d, cur.gm);
 #pragma unroll
-      for (int i = 0; i < K; ++i) X[i][K] += cur.v[i];
-      cur = nxt;
-    }
+          for (int i = 0; i < K; ++i) X[i][K] += cur.v[i];
+        });
   } else {
     for (int64_t t = t0; t < te; ++t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
@@ -513,21 +536,23 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, A
   }
   const int64_t te = min(t0 + AN_CHUNK, g.T);
   if constexpr (SCHED == SCHED_LEX) {
-    LexTok<K, HS, HD> cur, nxt;
-    cur.template load<false>(a, a.b, (th.bb * g.T + t0) * g.n + th.plane, t0, g.n, th.blk);
-    for (int64_t t = t0; t < te; ++t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      if (t + 1 < te) nxt.template load<false>(a, a.b, lane_tok + g.n, t + 1, g.n, th.blk);
-      apply_M_lex<K, HS, HD, 1>(v, cur.ang, cur.d, cur.gm);
-      float bt[K];
+    using Tok = LexTok<K, HS, HD>;
+    token_pairs<Tok>(
+        t0, (int)(te - t0), 1,
+        [&](Tok& k, int64_t t) {
+          k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+        },
+        [&](const Tok& cur, int64_t t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          apply_M_lex<K, HS, HD, 1>(v, cur.ang, cur.d, cur.gm);
+          float bt[K];
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        v[i][0] += cur.v[i];
-        bt[i] = v[i][0];
-      }
-      st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
-      cur = nxt;
-    }
+          for (int i = 0; i < K; ++i) {
+            v[i][0] += cur.v[i];
+            bt[i] = v[i][0];
+          }
+          st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
+        });
   } else {
     for (int64_t t = t0; t < te; ++t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
@@ -687,18 +712,17 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, 
   for (int i = 0; i < K; ++i) x[i][0] = 0.f;
   const int64_t te = min(t0 + AN_CHUNK, g.T);
   if constexpr (SCHED == SCHED_LEX) {
-    LexTok<K, HS, HD> cur, nxt;
-    cur.template load<false>(a, a.gh, (th.bb * g.T + te - 1) * g.n + th.plane, te - 1, g.n,
-                             th.blk);
-    for (int64_t t = te - 1; t >= t0; --t) {
-      if (t > t0)
-        nxt.template load<false>(a, a.gh, (th.bb * g.T + t - 1) * g.n + th.plane, t - 1, g.n,
-                                 th.blk);
+    using Tok = LexTok<K, HS, HD>;
+    token_pairs<Tok>(
+        te - 1, (int)(te - t0), -1,
+        [&](Tok& k, int64_t t) {
+          k.template load<false>(a, a.gh, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+        },
+        [&](const Tok& cur, int64_t) {
 #pragma unroll
-      for (int i = 0; i < K; ++i) x[i][0] += cur.v[i];
-      apply_Mt_lex<K, HS, HD, 1>(x, cur.ang, cur.d, cur.gm);
-      cur = nxt;
-    }
+          for (int i = 0; i < K; ++i) x[i][0] += cur.v[i];
+          apply_Mt_lex<K, HS, HD, 1>(x, cur.ang, cur.d, cur.gm);
+        });
   } else {
     for (int64_t t = te - 1; t >= t0; --t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
@@ -800,26 +824,27 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, A
   }
   const int64_t te = min(t0 + AN_CHUNK, g.T);
   if constexpr (SCHED == SCHED_LEX) {
-    LexTok<K, HS, HD> cur, nxt;
-    cur.template load<true>(a, a.gh, (th.bb * g.T + te - 1) * g.n + th.plane, te - 1, g.n,
-                            th.blk);
-    for (int64_t t = te - 1; t >= t0; --t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      if (t > t0) nxt.template load<true>(a, a.gh, lane_tok - g.n, t - 1, g.n, th.blk);
-      float gt[K];
+    using Tok = LexTok<K, HS, HD>;
+    token_pairs<Tok>(
+        te - 1, (int)(te - t0), -1,
+        [&](Tok& k, int64_t t) {
+          k.template load<true>(a, a.gh, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+        },
+        [&](const Tok& cur, int64_t t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          float gt[K];
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        y[i][0] += cur.v[i];
-        gt[i] = y[i][0];
-      }
-      st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
-      float dd = 0.f, dg = 0.f;
-      token_grad_lex<K, HS, HD>(y, cur.hp, cur.ang, a.dtheta + lane_tok * a.na, cur.d, cur.gm,
-                                dd, dg);
-      if (HS) a.dscale[lane_tok] = dd;
-      if (HD) a.dgamma[lane_tok] = dg;
-      cur = nxt;
-    }
+          for (int i = 0; i < K; ++i) {
+            y[i][0] += cur.v[i];
+            gt[i] = y[i][0];
+          }
+          st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
+          float dd = 0.f, dg = 0.f;
+          token_grad_lex<K, HS, HD>(y, cur.hp, cur.ang, a.dtheta + lane_tok * a.na, cur.d,
+                                    cur.gm, dd, dg);
+          if (HS) a.dscale[lane_tok] = dd;
+          if (HD) a.dgamma[lane_tok] = dg;
+        });
   } else {
     for (int64_t t = te - 1; t >= t0; --t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
