@@ -147,8 +147,9 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
  * y (B,H,T,dv), all of element type `dtype` (0 = fp32, 1 = bf16);
  * H0 / HT / dHT / dH0 (B,H,dk,dv) fp32.  Envelope: 1 <= dk, dv <= 64,
  * chunk >= 1, nh * chunk <= 64.
- * `Hbound` (mg_delta_state_bytes) receives the chunk-entry states and is
- * read back by mg_delta_bwd; `ws` needs mg_delta_workspace_bytes. */
+ * `Hbound` (mg_delta_state_bytes) receives the chunk-entry states in a layout
+ * private to the library (it differs between dtypes) and is read back only by
+ * mg_delta_bwd with the same shape and dtype; `ws` needs mg_delta_workspace_bytes. */
 size_t mg_delta_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
                                 int chunk);
 size_t mg_delta_state_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk);

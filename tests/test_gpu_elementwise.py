@@ -48,6 +48,9 @@ LINEAR_SHAPES = [
     (2, 1000, 128),
     (1, 4097, 1024),
     (4, 333, 12),
+    # the launch picks 4 columns per lane here, 2 at D=128 below, 1 for the small shapes
+    (8, 2048, 512),
+    (32, 1024, 128),
 ]
 
 
@@ -135,7 +138,8 @@ def _run_log(lc, lv, gh, cuda):
     return h, lcg.grad, lvg.grad
 
 
-LOG_SHAPES = [(1, 1, 1), (2, 7, 5), (3, 64, 64), (2, 200, 130), (4, 1024, 256), (1, 2049, 512)]
+LOG_SHAPES = [(1, 1, 1), (2, 7, 5), (3, 64, 64), (2, 200, 130), (4, 1024, 256), (1, 2049, 512),
+              (8, 2048, 512), (32, 1024, 128)]
 
 
 @pytest.mark.parametrize("shape", LOG_SHAPES)

@@ -40,6 +40,8 @@ CASES = [
     (1, 300, 7, True),
     (4, 1024, 256, False),
     (2, 65, 260, True),
+    (8, 2048, 512, False),  # 4 columns per lane
+    (32, 1024, 128, True),  # 2 columns per lane
 ]
 
 

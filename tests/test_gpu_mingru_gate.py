@@ -40,6 +40,8 @@ CASES = [
     (4, 1024, 256, 1.0),
     (2, 65, 260, 2.0),
     (2, 129, 64, 30.0),  # saturated gates: z and g at 0/1, sigmoid(-k) underflowing
+    (8, 2048, 512, 1.0),  # 4 columns per lane
+    (32, 1024, 128, 2.0),  # 2 columns per lane
 ]
 
 
