@@ -413,6 +413,10 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
 #pragma unroll
     for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
   const int64_t te = min(t0 + AN_CHUNK, g.T);
+  // The decay is a scalar per token, so it commutes with the rotations: P's K
+  // columns take the chunk's product of decays once at the end, and only the
+  // offset column, which receives b_t every token, is decayed token by token.
+  float gprod = 1.f;
   if constexpr (SCHED == SCHED_LEX) {
     using Tok = LexTok<K, HS, HD>;
     token_pairs<Tok>(
@@ -421,21 +425,29 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
           k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
         },
         [&](const Tok& cur, int64_t) {
-          apply_M_lex<K, HS, HD, K + 1>(X, cur.ang, cur.d, cur.gm);
+          apply_M_lex<K, HS, false, K + 1>(X, cur.ang, cur.d, 1.f);
+          if (HD) gprod *= cur.gm;
 #pragma unroll
-          for (int i = 0; i < K; ++i) X[i][K] += cur.v[i];
+          for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
         });
   } else {
     for (int64_t t = t0; t < te; ++t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
       const float d = HS ? a.scale[lane_tok] : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
-      apply_M<K, SCHED, HS, HD, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, gm);
+      apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
+      if (HD) gprod *= gm;
       float bt[K];
       ld<K>(bt, a.b + lane_tok * K);
 #pragma unroll
-      for (int i = 0; i < K; ++i) X[i][K] += bt[i];
+      for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
     }
+  }
+  if (HD) {
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int q = 0; q < K; ++q) X[i][q] *= gprod;
   }
   float Pf[K * K], Lf[K];
 #pragma unroll
