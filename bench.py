@@ -637,8 +637,8 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 "
-                          "(the scan path shards with no communication over batch and lanes; "
-                          "see DESIGN.md)"}))
+                          "(the scan path would shard over batch rows and lanes with no "
+                          "communication between GPUs)"}))
         sys.exit(2)
     import torch
 
