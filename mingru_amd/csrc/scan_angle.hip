@@ -400,6 +400,35 @@ __device__ __forceinline__ int64_t an_idx(const AnGeom& g, int c, int f, int nf,
   return ((int64_t)c * g.NB + blk) * nf + f;
 }
 
+// Orders the LDS accesses of one wave's lanes around it (no s_barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stores one R-float row per lane when the 64 lanes' rows are consecutive in
+// memory (lane l's row at dst0 + l R; the whole wave active).  The rows pass
+// through LDS, so each store instruction writes 1 KiB of consecutive bytes (whole
+// lines) instead of a 16-byte piece of each of 64 rows.  Called at the end of a
+// token's work: its waits then find the next token's prefetched loads done.
+template <int R>
+__device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const float (&row)[R],
+                                                float* lds, int lane) {
+  static_assert(R % 4 == 0, "rows of whole 16-byte pieces");
+  wave_sync();  // the previous call's reads are done before this call's writes
+#pragma unroll
+  for (int k = 0; k < R; k += 4)
+    *reinterpret_cast<float4*>(lds + lane * R + k) =
+        make_float4(row[k], row[k + 1], row[k + 2], row[k + 3]);
+  wave_sync();
+#pragma unroll
+  for (int k = 0; k < R / 4; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(lds + (k * MG_WAVE + lane) * 4);
+    *reinterpret_cast<float4*>(dst0 + (k * MG_WAVE + lane) * 4) = v;
+  }
+}
+
 // ---- forward pass 1: chunk aggregates h -> P_c h + L_c ------------------------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, AnGeom g) {
@@ -456,7 +485,14 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
     for (int j = 0; j < K; ++j) Pf[i * K + j] = X[i][j];
     Lf[i] = X[i][K];
   }
-  st<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk), Pf);
+  // A whole wave's P rows are consecutive: they leave through LDS as whole lines.
+  __shared__ __attribute__((aligned(16))) float s_prod[AN_WAVES][MG_WAVE * K * K];
+  const int lane = threadIdx.x & (MG_WAVE - 1);
+  if (__builtin_amdgcn_read_exec() == ~0ull)
+    wave_rows_store<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk - lane), Pf,
+                           s_prod[threadIdx.x / MG_WAVE], lane);
+  else
+    st<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk), Pf);
   st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
 }
 
@@ -531,35 +567,6 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_fwd_scan(AnArgs a, AnGe
 #pragma unroll
   for (int d = 0; d < R - 1; ++d)
     if (c + d < g.n_chunks) step(buf[d], buf[(d + R - 1) % R], c + d);
-}
-
-// Orders the LDS accesses of one wave's lanes around it (no s_barrier).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Stores one R-float row per lane when the 64 lanes' rows are consecutive in
-// memory (lane l's row at dst0 + l R; the whole wave active).  The rows pass
-// through LDS, so each store instruction writes 1 KiB of consecutive bytes (whole
-// lines) instead of a 16-byte piece of each of 64 rows.  Called at the end of a
-// token's work: its waits then find the next token's prefetched loads done.
-template <int R>
-__device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const float (&row)[R],
-                                                float* lds, int lane) {
-  static_assert(R % 4 == 0, "rows of whole 16-byte pieces");
-  wave_sync();  // the previous call's reads are done before this call's writes
-#pragma unroll
-  for (int k = 0; k < R; k += 4)
-    *reinterpret_cast<float4*>(lds + lane * R + k) =
-        make_float4(row[k], row[k + 1], row[k + 2], row[k + 3]);
-  wave_sync();
-#pragma unroll
-  for (int k = 0; k < R / 4; ++k) {
-    const float4 v = *reinterpret_cast<const float4*>(lds + (k * MG_WAVE + lane) * 4);
-    *reinterpret_cast<float4*>(dst0 + (k * MG_WAVE + lane) * 4) = v;
-  }
 }
 
 // ---- forward pass 3: every token's state from its chunk-entry state ------------
