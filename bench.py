@@ -256,7 +256,17 @@ def make_step(key, torch, wl, dev):
             h = hip_scans.angle_scan_impl(th, sc, gm, bb, h0, *meta, has_scale=0, has_decay=1)
             return torch.autograd.grad(h, (th, gm, bb, h0), gh)
 
-        return step, None, wl.C4["B"]
+        def cpu(bs):
+            # The eager path: every 8x8 transition materialised from its 28 angles,
+            # then the eager matrix_affine_scan (reference GivensMinGRU fallback).
+            from mingru_amd.min_gru import angle_scan_eager
+
+            xc = [inp[k][:bs].clone().requires_grad_(True) for k in ("theta", "gamma", "b", "h0")]
+            h = angle_scan_eager(xc[0], inp["scale"][:bs], xc[1], xc[2], xc[3], inp["perm"],
+                                 inp["sgn"], inp["p2p"], has_scale=0, has_decay=1)
+            torch.autograd.grad(h, xc, inp["grad_h"][:bs])
+
+        return step, cpu, wl.C4["B"]
     if key == "C5":
         from mingru_amd import hip_scans
 

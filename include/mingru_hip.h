@@ -18,7 +18,8 @@
  *   - work is enqueued asynchronously on `stream`; nothing allocates, throws or
  *     synchronises;
  *   - the return value is a status: 0 ok, 1 invalid argument / outside the
- *     envelope, 2 kernel launch failed, 3 workspace too small.
+ *     envelope, 2 kernel launch failed, 3 workspace too small, 5 a HIP
+ *     runtime call failed.
  *
  * Each declaration cites the reference interface it replaces
  * (chris-santiago/minGRU, paths relative to the repository root).
@@ -87,15 +88,34 @@ int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_
 /* ---- parallel_scan_log: log-space inputs, (B, T, D) and (B, T+1, D) ---------
  * Replaces parallel_scan_log_fwd (src/mingru/triton_scans.py:1336-1357, kernel
  * :754-821) and its eager-recompute backward (:1489-1552) behind
- * SCAN_IMPLS["parallel_scan_log"] (:2467-2490). */
+ * SCAN_IMPLS["parallel_scan_log"] (:2467-2490).  Inputs anywhere in fp32's
+ * range: the kernels hold every product and sum as an fp32 significand with a
+ * separate exponent, so e^lc, e^lv and the backward's adjoint never overflow or
+ * underflow before the result is formed (the reference evaluates in log space,
+ * src/mingru/min_gru.py:804-807).  `hstate` (mg_log_scan_state_bytes, fp32)
+ * receives extended-range forward states at every 8-step boundary for the
+ * backward; it may be NULL in both calls, and the backward then restarts from
+ * the fp32 outputs h (exact unless h under- or overflowed). */
 size_t mg_log_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
-/* lc = log a (B,T,D), lv = [log h0, log b] (B,T+1,D) -> h (B,T,D). */
-int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,
+size_t mg_log_scan_state_bytes(int64_t B, int64_t T, int64_t D);
+/* lc = log a (B,T,D), lv = [log h0, log b] (B,T+1,D) -> h (B,T,D) [, hstate]. */
+int mg_log_scan_fwd(const float* lc, const float* lv, float* h, float* hstate, int64_t B,
+                    int64_t T, int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
+/* h = forward output, hstate = the forward's record (or NULL), gh = dL/dh
+ * -> dlc (B,T,D), dlv (B,T+1,D). */
+int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* hstate,
+                    const float* gh, float* dlc, float* dlv, int64_t B, int64_t T, int64_t D,
                     void* ws, size_t ws_bytes, mg_stream_t stream);
-/* h = forward output, gh = dL/dh -> dlc (B,T,D), dlv (B,T+1,D). */
-int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* gh, float* dlc,
-                    float* dlv, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
-                    mg_stream_t stream);
+
+/* ---- look-back workspace diagnostics ----------------------------------------
+ * No reference counterpart (the reference's kernels have no look-back).  Copies
+ * the count of failed look-back waits recorded in a linear / log / affine / fused
+ * gate scan workspace to *count, after the work queued on `stream`.  Every wait
+ * is bounded: a wait that gives up (or a workspace that broke the protocol)
+ * increments the count and the kernel finishes with a partial carry, so a
+ * nonzero count means results since the workspace was zeroed are not to be
+ * trusted.  The one entry point that synchronises (`stream`). */
+int mg_scan_workspace_errors(const void* ws, unsigned* count, mg_stream_t stream);
 
 /* ---- matrix_scan / matrix_affine_scan: k x k blocks, (B, T, n, k, k) -------
  * Replaces affine_scan_fwd / affine_scan_bwd (src/mingru/triton_scans.py:

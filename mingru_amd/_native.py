@@ -14,7 +14,13 @@ import os
 from .build import LIB_PATH
 
 MG_OK = 0
-MG_STATUS = {0: "ok", 1: "invalid argument", 2: "kernel launch failed", 3: "workspace too small"}
+MG_STATUS = {
+    0: "ok",
+    1: "invalid argument",
+    2: "kernel launch failed",
+    3: "workspace too small",
+    5: "HIP runtime call failed",
+}
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -34,8 +40,10 @@ _SIGNATURES = {
     "mg_mingru_gate_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _P, _SZ, _P]),
     "mg_gate_step": (_I32, [_I32] + [_P] * 6 + [_I64, _P]),
     "mg_delta_step": (_I32, [_P] * 8 + [_I64, _I32, _I32, _I32, _P]),
-    "mg_log_scan_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
-    "mg_log_scan_bwd": (_I32, [_P] * 6 + [_I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_log_scan_state_bytes": (_SZ, [_I64, _I64, _I64]),
+    "mg_log_scan_fwd": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_log_scan_bwd": (_I32, [_P] * 7 + [_I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_scan_workspace_errors": (_I32, [_P, ctypes.POINTER(ctypes.c_uint), _P]),
     "mg_affine_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32]),
     "mg_affine_scan_fwd": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _P, _SZ, _P]),
     "mg_affine_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _I32, _I32, _P, _SZ, _P]),

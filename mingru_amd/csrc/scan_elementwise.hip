@@ -47,30 +47,131 @@ constexpr int GATE_TSUB_FWD_NARROW = 8;
 // Workgroups a launch needs before it runs 4 columns per lane: one per CU.
 constexpr int64_t EW_FILL_WGS = 256;
 
-// Affine map y -> p*y + l (NL independent offsets sharing one slope).
+// Affine map y -> p*y + l (NL independent offsets sharing one slope).  The
+// look-back machinery below moves any map type that names its NF fp32 fields
+// (get / set), an identity and compose(inner, outer).
 template <int NL>
 struct Aff {
+  static constexpr int NF = NL + 1;
   float p;
   float l[NL];
+  __device__ __forceinline__ float get(int f) const { return f == 0 ? p : l[f > 0 ? f - 1 : 0]; }
+  __device__ __forceinline__ void set(int f, float v) {
+    if (f == 0)
+      p = v;
+    else
+      l[f > 0 ? f - 1 : 0] = v;
+  }
+  __device__ __forceinline__ static Aff identity() {
+    Aff r;
+    r.p = 1.f;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) r.l[i] = 0.f;
+    return r;
+  }
 };
 
 template <int NL>
 __device__ __forceinline__ Aff<NL> aff_identity() {
-  Aff<NL> r;
-  r.p = 1.f;
-#pragma unroll
-  for (int i = 0; i < NL; ++i) r.l[i] = 0.f;
-  return r;
+  return Aff<NL>::identity();
 }
 
 // outer o inner: apply `inner` first, then `outer`.
 template <int NL>
-__device__ __forceinline__ Aff<NL> aff_compose(const Aff<NL>& inner, const Aff<NL>& outer) {
+__device__ __forceinline__ Aff<NL> compose(const Aff<NL>& inner, const Aff<NL>& outer) {
   Aff<NL> r;
   r.p = outer.p * inner.p;
 #pragma unroll
   for (int i = 0; i < NL; ++i) r.l[i] = fmaf(outer.p, inner.l[i], outer.l[i]);
   return r;
+}
+
+// ---------------------------------------------------------------------------
+// Extended-range values for parallel_scan_log
+// ---------------------------------------------------------------------------
+// The log scan's inputs are logs: a term exp(lv) or a product of exp(lc) can
+// leave fp32's range (e^-87 .. e^88) while the output h stays inside it (an
+// initial state e^-150 grown by e^+1 per step), and the backward's adjoint can
+// overflow while the gradients it forms stay finite.  Such values are held as
+// Xf {s, e} = s * 2^e: an fp32 significand s and an integer-valued fp32
+// exponent e, with zero as {0, -inf}.  Products multiply significands and add
+// exponents, sums align on the larger exponent, so no intermediate overflows or
+// underflows and each operation keeps fp32's relative rounding.  The reference
+// reaches the same range by evaluating in log space
+// (src/mingru/min_gru.py:804-807; its kernel's online max-shift,
+// src/mingru/triton_scans.py:797-821).
+struct Xf {
+  float s, e;
+};
+
+__device__ __forceinline__ Xf xf_zero() { return Xf{0.f, -INFINITY}; }
+
+// s * 2^d for an alignment or output shift d; |d| beyond 512 is as good as
+// infinite for an fp32 significand (and a NaN shift only pairs with s = 0).
+__device__ __forceinline__ float xf_ldexp(float s, float d) {
+  return __builtin_amdgcn_ldexpf(s, (int)fminf(fmaxf(d, -512.f), 512.f));
+}
+
+// e^x split as s * 2^k with |log s| <= ln2 / 2: k = rint(x log2 e) and the
+// remainder x - k ln2 taken with ln2 in two parts (Cody & Waite), so the
+// remainder is exact to fp32 rounding for any |x| below 1e6.  Inputs are clamped
+// to +-1e6 (e^-1e6 is zero and e^1e6 infinite for every fp32 combination);
+// NaN passes through.
+__device__ __forceinline__ Xf xf_exp(float x) {
+  constexpr float LOG2E = 1.44269504088896341f;
+  constexpr float LN2_HI = 0.693145751953125f;
+  constexpr float LN2_LO = 1.42860682030941723e-6f;
+  x = x < -1.0e6f ? -1.0e6f : x;
+  x = x > 1.0e6f ? 1.0e6f : x;
+  const float k = rintf(x * LOG2E);
+  float r = fmaf(-k, LN2_HI, x);
+  r = fmaf(-k, LN2_LO, r);
+  return Xf{__builtin_amdgcn_exp2f(r * LOG2E), k};
+}
+
+// Significand into [0.5, 1); an exact zero gets exponent -inf.
+__device__ __forceinline__ Xf xf_norm(Xf v) {
+  const float m = __builtin_amdgcn_frexp_mantf(v.s);
+  const int ex = __builtin_amdgcn_frexp_expf(v.s);
+  return Xf{m, m == 0.f ? -INFINITY : v.e + (float)ex};
+}
+
+__device__ __forceinline__ Xf xf_from(float x) { return xf_norm(Xf{x, 0.f}); }
+
+__device__ __forceinline__ float xf_to_float(Xf v) { return xf_ldexp(v.s, v.e); }
+
+__device__ __forceinline__ Xf xf_mul(Xf a, Xf b) { return Xf{a.s * b.s, a.e + b.e}; }
+
+__device__ __forceinline__ Xf xf_add(Xf a, Xf b) {
+  const float em = fmaxf(a.e, b.e);
+  return Xf{xf_ldexp(a.s, a.e - em) + xf_ldexp(b.s, b.e - em), em};
+}
+
+// a * y + b
+__device__ __forceinline__ Xf xf_fma(Xf a, Xf y, Xf b) { return xf_add(xf_mul(a, y), b); }
+
+// Affine map y -> p*y + l over Xf values (one offset); four look-back fields.
+struct XAff {
+  static constexpr int NF = 4;
+  Xf p, l;
+  __device__ __forceinline__ float get(int f) const {
+    return f == 0 ? p.s : f == 1 ? p.e : f == 2 ? l.s : l.e;
+  }
+  __device__ __forceinline__ void set(int f, float v) {
+    if (f == 0)
+      p.s = v;
+    else if (f == 1)
+      p.e = v;
+    else if (f == 2)
+      l.s = v;
+    else
+      l.e = v;
+  }
+  __device__ __forceinline__ static XAff identity() { return XAff{Xf{1.f, 0.f}, xf_zero()}; }
+};
+
+__device__ __forceinline__ XAff compose(const XAff& inner, const XAff& outer) {
+  return XAff{xf_norm(xf_mul(outer.p, inner.p)), xf_norm(xf_fma(outer.p, inner.l, outer.l))};
 }
 
 // Data streams are read and written once: non-temporal accesses.
@@ -107,31 +208,31 @@ struct EwGeom {
 
 // Look-back slots: [lg][chunk][field][VEC][64 lanes] tagged words, so each wave
 // store of one (field, vector element) covers 512 contiguous bytes (whole lines).
-template <int NL, int VEC>
+template <typename Map, int VEC>
 __device__ __forceinline__ void lb_put(mg_slot_t* base, const EwGeom& g, int lg, int c, int lane,
-                                       const Aff<NL> (&x)[VEC], unsigned epoch) {
+                                       const Map (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
-  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane;
+  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    mg_slot_put(p + v * MG_WAVE, x[v].p, epoch);
+  for (int v = 0; v < VEC; ++v)
 #pragma unroll
-    for (int f = 0; f < NL; ++f) mg_slot_put(p + (f + 1) * TILE + v * MG_WAVE, x[v].l[f], epoch);
-  }
+    for (int f = 0; f < Map::NF; ++f) mg_slot_put(p + f * TILE + v * MG_WAVE, x[v].get(f), epoch);
 }
 
-template <int NL, int VEC>
+template <typename Map, int VEC>
 __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, int lg, int c,
-                                       int lane, Aff<NL> (&x)[VEC], unsigned epoch) {
+                                       int lane, Map (&x)[VEC], unsigned epoch) {
   constexpr int TILE = MG_WAVE * VEC;
-  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * (NL + 1)) * TILE + lane;
+  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
   bool ok = true;
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    ok &= mg_slot_get(p + v * MG_WAVE, x[v].p, epoch);
+  for (int v = 0; v < VEC; ++v)
 #pragma unroll
-    for (int f = 0; f < NL; ++f) ok &= mg_slot_get(p + (f + 1) * TILE + v * MG_WAVE, x[v].l[f], epoch);
-  }
+    for (int f = 0; f < Map::NF; ++f) {
+      float val;
+      ok &= mg_slot_get(p + f * TILE + v * MG_WAVE, val, epoch);
+      x[v].set(f, val);
+    }
   return ok;
 }
 
@@ -139,67 +240,64 @@ __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, i
 // this thread's columns, the composition of everything before (forward) or
 // after (REVERSE) this thread's sub-chunk.  `seed` is the map applied at the
 // sequence start (forward) or end (reverse).
-template <int NL, int VEC, int WAVES, bool REVERSE>
-__device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL> (&seed)[VEC],
+template <typename Map, int VEC, int WAVES, bool REVERSE>
+__device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed)[VEC],
                                          const EwGeom& g, int lg, int c, unsigned* header,
                                          unsigned epoch, mg_slot_t* agg_data,
-                                         mg_slot_t* incl_data, Aff<NL> (&carry)[VEC]) {
+                                         mg_slot_t* incl_data, Map (&carry)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
-  constexpr int NF = NL + 1;
+  constexpr int NF = Map::NF;
   __shared__ float s_agg[WAVES][NF][TILE];
   __shared__ float s_carry[NF][TILE];
   const int lane = threadIdx.x & (MG_WAVE - 1);
   const int w = threadIdx.x / MG_WAVE;
 
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    s_agg[w][0][v * MG_WAVE + lane] = loc[v].p;
+  for (int v = 0; v < VEC; ++v)
 #pragma unroll
-    for (int f = 0; f < NL; ++f) s_agg[w][f + 1][v * MG_WAVE + lane] = loc[v].l[f];
-  }
+    for (int f = 0; f < NF; ++f) s_agg[w][f][v * MG_WAVE + lane] = loc[v].get(f);
   __syncthreads();
 
   auto wave_agg = [&](int j, int v) {
-    Aff<NL> r;
-    r.p = s_agg[j][0][v * MG_WAVE + lane];
+    Map r;
 #pragma unroll
-    for (int f = 0; f < NL; ++f) r.l[f] = s_agg[j][f + 1][v * MG_WAVE + lane];
+    for (int f = 0; f < NF; ++f) r.set(f, s_agg[j][f][v * MG_WAVE + lane]);
     return r;
   };
 
   // Exclusive prefix of this wave inside the workgroup.
-  Aff<NL> ew[VEC];
+  Map ew[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    ew[v] = aff_identity<NL>();
+    ew[v] = Map::identity();
     if (!REVERSE) {
-      for (int j = 0; j < w; ++j) ew[v] = aff_compose(ew[v], wave_agg(j, v));
+      for (int j = 0; j < w; ++j) ew[v] = compose(ew[v], wave_agg(j, v));
     } else {
-      for (int j = WAVES - 1; j > w; --j) ew[v] = aff_compose(ew[v], wave_agg(j, v));
+      for (int j = WAVES - 1; j > w; --j) ew[v] = compose(ew[v], wave_agg(j, v));
     }
   }
 
   if (w == 0) {
-    Aff<NL> G[VEC];
+    Map G[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      G[v] = aff_identity<NL>();
+      G[v] = Map::identity();
       if (!REVERSE) {
-        for (int j = 0; j < WAVES; ++j) G[v] = aff_compose(G[v], wave_agg(j, v));
+        for (int j = 0; j < WAVES; ++j) G[v] = compose(G[v], wave_agg(j, v));
       } else {
-        for (int j = WAVES - 1; j >= 0; --j) G[v] = aff_compose(G[v], wave_agg(j, v));
+        for (int j = WAVES - 1; j >= 0; --j) G[v] = compose(G[v], wave_agg(j, v));
       }
     }
     const int first = REVERSE ? g.n_chunks - 1 : 0;
     const int dir = REVERSE ? 1 : -1;  // step towards predecessors
-    Aff<NL> E[VEC];
+    Map E[VEC];
     if (c == first) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) E[v] = seed[v];
     } else {
-      lb_put<NL, VEC>(agg_data, g, lg, c, lane, G, epoch);
+      lb_put<Map, VEC>(agg_data, g, lg, c, lane, G, epoch);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) E[v] = aff_identity<NL>();
+      for (int v = 0; v < VEC; ++v) E[v] = Map::identity();
       // Per-lane walk over predecessors: an inclusive prefix ends the walk, an
       // aggregate is composed in and the walk continues; the first chunk only
       // ever publishes its inclusive prefix.
@@ -207,14 +305,14 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
       unsigned spins = 0;
       bool done = false;
       while (!done) {
-        Aff<NL> X[VEC];
-        if (lb_try<NL, VEC>(incl_data, g, lg, j, lane, X, epoch)) {
+        Map X[VEC];
+        if (lb_try<Map, VEC>(incl_data, g, lg, j, lane, X, epoch)) {
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
+          for (int v = 0; v < VEC; ++v) E[v] = compose(X[v], E[v]);
           done = true;
-        } else if (j != first && lb_try<NL, VEC>(agg_data, g, lg, j, lane, X, epoch)) {
+        } else if (j != first && lb_try<Map, VEC>(agg_data, g, lg, j, lane, X, epoch)) {
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) E[v] = aff_compose(X[v], E[v]);
+          for (int v = 0; v < VEC; ++v) E[v] = compose(X[v], E[v]);
           j += dir;
         } else {
           __builtin_amdgcn_s_sleep(1);
@@ -225,25 +323,22 @@ __device__ __forceinline__ void ew_carry(const Aff<NL> (&loc)[VEC], const Aff<NL
         }
       }
     }
-    Aff<NL> I[VEC];
+    Map I[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) I[v] = aff_compose(E[v], G[v]);
-    lb_put<NL, VEC>(incl_data, g, lg, c, lane, I, epoch);
+    for (int v = 0; v < VEC; ++v) I[v] = compose(E[v], G[v]);
+    lb_put<Map, VEC>(incl_data, g, lg, c, lane, I, epoch);
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      s_carry[0][v * MG_WAVE + lane] = E[v].p;
+    for (int v = 0; v < VEC; ++v)
 #pragma unroll
-      for (int f = 0; f < NL; ++f) s_carry[f + 1][v * MG_WAVE + lane] = E[v].l[f];
-    }
+      for (int f = 0; f < NF; ++f) s_carry[f][v * MG_WAVE + lane] = E[v].get(f);
   }
   __syncthreads();
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    Aff<NL> C;
-    C.p = s_carry[0][v * MG_WAVE + lane];
+    Map C;
 #pragma unroll
-    for (int f = 0; f < NL; ++f) C.l[f] = s_carry[f + 1][v * MG_WAVE + lane];
-    carry[v] = aff_compose(C, ew[v]);
+    for (int f = 0; f < NF; ++f) C.set(f, s_carry[f][v * MG_WAVE + lane]);
+    carry[v] = compose(C, ew[v]);
   }
 }
 
@@ -275,10 +370,9 @@ __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header)
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  LOG=false: x0=a, x1=b -> out0=A, out1=Bc.
-//           LOG=true : x0=lc (B,T,D), x1=lv (B,T+1,D) -> out0=h.
+// Forward of linear_scan: a, b -> A (running product), Bc (zero-start solution).
 // ---------------------------------------------------------------------------
-template <int VEC, int TSUB, int WAVES, bool LOG>
+template <int VEC, int TSUB, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     const float* __restrict__ x0, const float* __restrict__ x1, float* __restrict__ out0,
     float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
@@ -294,27 +388,14 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       load_vec<VEC>(av[s], x0 + (th.bb * T + t) * D + th.col);
-      if (LOG) {
-        load_vec<VEC>(bv[s], x1 + (th.bb * (T + 1) + t + 1) * D + th.col);
-      } else {
-        load_vec<VEC>(bv[s], x1 + (th.bb * T + t) * D + th.col);
-      }
+      load_vec<VEC>(bv[s], x1 + (th.bb * T + t) * D + th.col);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        av[s][v] = LOG ? 0.f : 1.f;  // exp(0) = 1 below
-        bv[s][v] = LOG ? -INFINITY : 0.f;
+        av[s][v] = 1.f;
+        bv[s][v] = 0.f;
       }
     }
-  }
-  if (LOG) {
-#pragma unroll
-    for (int s = 0; s < TSUB; ++s)
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        av[s][v] = expf(av[s][v]);
-        bv[s][v] = expf(bv[s][v]);
-      }
   }
 
   Aff<1> loc[VEC], seed[VEC], carry[VEC];
@@ -328,19 +409,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  if (LOG && th.c == 0 && th.w == 0) {
-    float h0[VEC];
-    if (th.col_ok) {
-      load_vec<VEC>(h0, x1 + (th.bb * (T + 1)) * D + th.col);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) h0[v] = -INFINITY;
-    }
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) seed[v].l[0] = expf(h0[v]);
-  }
-  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
-                                 carry);
+  ew_carry<Aff<1>, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                      incl_data, carry);
 
   float P[VEC], L[VEC];
 #pragma unroll
@@ -358,12 +428,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
-      if (LOG) {
-        store_vec<VEC>(out0 + off, L);
-      } else {
-        store_vec<VEC>(out0 + off, P);
-        store_vec<VEC>(out1 + off, L);
-      }
+      store_vec<VEC>(out0 + off, P);
+      store_vec<VEC>(out1 + off, L);
     }
   }
 }
@@ -430,7 +496,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     }
     seed[v] = aff_identity<2>();
   }
-  ew_carry<2, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
+  ew_carry<Aff<2>, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                 carry);
 
   float ya[VEC], yb[VEC];
@@ -468,89 +534,195 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward of parallel_scan_log.  Inputs lc, lv, saved h, grad gh; outputs
-// dlc (B,T,D) and dlv (B,T+1,D).
-//   x_t = gh_t + a_{t+1} x_{t+1};  dlc_t = x_t a_t h_{t-1};  dlv_{t+1} = x_t b_t;
-//   dlv_0 = a_0 x_0 h_{-1}.
+// parallel_scan_log (reference src/mingru/min_gru.py:755-807) on
+// extended-range values (Xf above).
+//   forward:  h_t = a_t h_{t-1} + b_t with a_t = e^{lc_t}, b_t = e^{lv_{t+1}}
+//             and h_{-1} = e^{lv_0}.  Every term is positive, so there is no
+//             cancellation and each step keeps fp32's relative rounding.  The
+//             forward also records h_{t0-1} (as Xf) at every sub-chunk start
+//             t0 into `hstate` (B, ceil(T/LOG_TSUB), 2, D) when it is given, so
+//             the backward restarts the recurrence from values that an fp32 h
+//             could not hold.
+//   backward: adjoint x_t = gh_t + a_{t+1} x_{t+1};  dlc_t = x_t a_t h_{t-1};
+//             dlv_{t+1} = x_t b_t;  dlv_0 = a_0 x_0 h_{-1}.
+// Both directions use LOG_TSUB-step sub-chunks, the granularity of `hstate`.
 // ---------------------------------------------------------------------------
-template <int VEC, int TSUB, int WAVES>
+constexpr int LOG_TSUB = 8;
+constexpr int LOG_WAVES = 8;
+
+template <int VEC>
+__device__ __forceinline__ void load_xf_exp(Xf (&dst)[VEC], const float* __restrict__ src) {
+  float x[VEC];
+  load_vec<VEC>(x, src);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) dst[v] = xf_exp(x[v]);
+}
+
+template <int VEC, int WAVES>
+__global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
+    const float* __restrict__ lc, const float* __restrict__ lv, float* __restrict__ h,
+    float* __restrict__ hstate, EwGeom g, unsigned* header, mg_slot_t* agg_data,
+    mg_slot_t* incl_data) {
+  constexpr int TSUB = LOG_TSUB;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  if (!th.valid) return;
+  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+  const int64_t T = g.T, D = g.D;
+
+  Xf av[TSUB][VEC], bv[TSUB][VEC];
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) {
+      load_xf_exp<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
+      load_xf_exp<VEC>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = Xf{1.f, 0.f};
+        bv[s][v] = xf_zero();
+      }
+    }
+  }
+
+  XAff loc[VEC], seed[VEC], carry[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    Xf P{1.f, 0.f}, L = xf_zero();
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      L = xf_fma(av[s][v], L, bv[s][v]);
+      P = xf_mul(P, av[s][v]);
+    }
+    loc[v] = XAff{xf_norm(P), xf_norm(L)};
+    seed[v] = XAff::identity();
+  }
+  if (th.c == 0 && th.w == 0 && th.col_ok) {
+    Xf h0[VEC];
+    load_xf_exp<VEC>(h0, lv + (th.bb * (T + 1)) * D + th.col);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) seed[v].l = h0[v];
+  }
+  ew_carry<XAff, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                    incl_data, carry);
+
+  Xf L[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) L[v] = carry[v].l;
+  if (hstate != nullptr && th.col_ok && t0 < T) {
+    const int64_t nsub = (T + TSUB - 1) / TSUB;
+    float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
+    float ss[VEC], se[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      ss[v] = L[v].s;
+      se[v] = L[v].e;
+    }
+    store_vec<VEC>(st, ss);
+    store_vec<VEC>(st + D, se);
+  }
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s) {
+    float out[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      L[v] = xf_fma(av[s][v], L[v], bv[s][v]);
+      out[v] = xf_to_float(L[v]);
+    }
+    const int64_t t = t0 + s;
+    if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, out);
+  }
+}
+
+template <int VEC, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     const float* __restrict__ lc, const float* __restrict__ lv, const float* __restrict__ h,
-    const float* __restrict__ gh, float* __restrict__ dlc, float* __restrict__ dlv, EwGeom g,
-    unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data) {
+    const float* __restrict__ hstate, const float* __restrict__ gh, float* __restrict__ dlc,
+    float* __restrict__ dlv, EwGeom g, unsigned* header, mg_slot_t* agg_data,
+    mg_slot_t* incl_data) {
+  constexpr int TSUB = LOG_TSUB;
   EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
 
-  float av[TSUB][VEC], bv[TSUB][VEC], x[TSUB][VEC];
-  float hp[VEC];
+  // a as Xf; lv and gh raw until needed.
+  Xf av[TSUB][VEC];
+  float lvr[TSUB][VEC], gr[TSUB][VEC];
 #pragma unroll
   for (int s = 0; s < TSUB; ++s) {
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
-      load_vec<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
-      load_vec<VEC>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
-      load_vec<VEC>(x[s], gh + (th.bb * T + t) * D + th.col);
+      load_xf_exp<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
+      load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+      load_vec<VEC>(gr[s], gh + (th.bb * T + t) * D + th.col);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        av[s][v] = 0.f;
-        bv[s][v] = -INFINITY;
-        x[s][v] = 0.f;
+        av[s][v] = Xf{1.f, 0.f};
+        lvr[s][v] = -INFINITY;
+        gr[s][v] = 0.f;
       }
     }
   }
-  const bool first_sub = (t0 == 0);
-  if (th.col_ok && t0 <= T) {
-    if (first_sub) {
-      load_vec<VEC>(hp, lv + (th.bb * (T + 1)) * D + th.col);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) hp[v] = expf(hp[v]);
-    } else {
-      load_vec<VEC>(hp, h + (th.bb * T + t0 - 1) * D + th.col);
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) hp[v] = 0.f;
-  }
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s)
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      av[s][v] = expf(av[s][v]);
-      bv[s][v] = expf(bv[s][v]);
-    }
+  // An fp32 value as Xf without normalising: only an exact zero needs exponent -inf.
+  auto raw = [](float x) { return Xf{x, x == 0.f ? -INFINITY : 0.f}; };
 
-  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+  XAff loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    loc[v] = aff_identity<1>();
+    Xf P{1.f, 0.f}, L = xf_zero();
 #pragma unroll
     for (int s = TSUB - 1; s >= 0; --s) {
-      loc[v].l[0] = av[s][v] * (x[s][v] + loc[v].l[0]);
-      loc[v].p *= av[s][v];
+      L = xf_mul(av[s][v], xf_add(raw(gr[s][v]), L));
+      P = xf_mul(P, av[s][v]);
     }
-    seed[v] = aff_identity<1>();
+    loc[v] = XAff{xf_norm(P), xf_norm(L)};
+    seed[v] = XAff::identity();
   }
-  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
-                                carry);
+  ew_carry<XAff, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                   incl_data, carry);
 
-  float y[VEC];
+  // Total adjoint x_s of every step; y ends as a_{t0} x_{t0}.
+  Xf x[TSUB][VEC], y[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
+  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l;
 #pragma unroll
   for (int s = TSUB - 1; s >= 0; --s) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      x[s][v] += y[v];
-      y[v] = av[s][v] * x[s][v];
+      x[s][v] = xf_add(raw(gr[s][v]), y[v]);
+      y[v] = xf_mul(av[s][v], x[s][v]);
+    }
+  }
+
+  // h_{t0-1}: e^{lv_0} at the sequence start, else the forward's record.
+  Xf hp[VEC];
+  const bool first_sub = (t0 == 0);
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) hp[v] = xf_zero();
+  if (th.col_ok && t0 < T) {
+    if (first_sub) {
+      load_xf_exp<VEC>(hp, lv + (th.bb * (T + 1)) * D + th.col);
+    } else if (hstate != nullptr) {
+      const int64_t nsub = (T + TSUB - 1) / TSUB;
+      const float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
+      float ss[VEC], se[VEC];
+      load_vec<VEC>(ss, st);
+      load_vec<VEC>(se, st + D);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) hp[v] = Xf{ss[v], se[v]};
+    } else {
+      float hv[VEC];
+      load_vec<VEC>(hv, h + (th.bb * T + t0 - 1) * D + th.col);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) hp[v] = xf_from(hv[v]);
     }
   }
   if (first_sub && th.col_ok) {
     float d0[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) d0[v] = y[v] * hp[v];
+    for (int v = 0; v < VEC; ++v) d0[v] = xf_to_float(xf_mul(y[v], hp[v]));
     store_vec<VEC>(dlv + (th.bb * (T + 1)) * D + th.col, d0);
   }
 #pragma unroll
@@ -558,9 +730,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     float d_c[VEC], d_v[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      d_c[v] = x[s][v] * av[s][v] * hp[v];
-      d_v[v] = x[s][v] * bv[s][v];
-      hp[v] = fmaf(av[s][v], hp[v], bv[s][v]);
+      const Xf b = lvr[s][v] == -INFINITY ? xf_zero() : xf_exp(lvr[s][v]);
+      d_c[v] = xf_to_float(xf_mul(xf_mul(x[s][v], av[s][v]), hp[v]));
+      d_v[v] = xf_to_float(xf_mul(x[s][v], b));
+      hp[v] = xf_fma(av[s][v], hp[v], b);
     }
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
@@ -638,7 +811,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
 #pragma unroll
     for (int v = 0; v < VEC; ++v) seed[v].l[0] = G == GATE_MINGRU ? expf(x[v]) : x[v];
   }
-  ew_carry<1, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
+  ew_carry<Aff<1>, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                  carry);
   float L[VEC];
 #pragma unroll
@@ -739,7 +912,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  ew_carry<1, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
+  ew_carry<Aff<1>, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
                                 carry);
   float y[VEC];
 #pragma unroll
@@ -878,6 +1051,22 @@ size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
   return m;
 }
 
+// Columns per lane of the log scans: 2 or 1.  Their extended-range values take
+// twice the registers of the linear scan's, and 4 columns per lane spill.
+int log_vec(int64_t B, int64_t T, int64_t D, std::initializer_list<const void*> ps) {
+  uintptr_t bits = 0;
+  for (const void* p : ps) bits |= (uintptr_t)p;
+  const bool v2 = D % 2 == 0 && bits % 8 == 0;
+  return std::min(2, ew_vec(B, T, D, v2, LOG_WAVES * LOG_TSUB));
+}
+
+// parallel_scan_log: Xf maps carry four look-back fields (ew_plan's nl = 3).
+size_t log_ws_bytes(int64_t B, int64_t T, int64_t D) {
+  size_t m = 0;
+  for (int vec : {1, 2, 4}) m = std::max(m, ew_plan(B, T, D, vec, LOG_TSUB, LOG_WAVES, 3).total);
+  return m;
+}
+
 size_t gate_ws_bytes(int64_t B, int64_t T, int64_t D) {
   size_t m = ew_ws_bytes(B, T, D);
   for (int vec : {1, 2, 4})
@@ -924,6 +1113,20 @@ int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const flo
   });
 }
 
+int linear_fwd_launch(const float* a, const float* b, float* A, float* Bc, int64_t B, int64_t T,
+                      int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
+                  is_aligned16(Bc);
+  const int vec = ew_vec(B, T, D, v4, EW_WAVES_FWD * EW_TSUB_FWD);
+  return by_vec(vec, [&](auto v) {
+    constexpr int V = decltype(v)::value;
+    EwPlan p = ew_plan(B, T, D, V, EW_TSUB_FWD, EW_WAVES_FWD, 1);
+    if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
+    return ew_launch(ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD>, p, ws, stream, a, b, A,
+                     Bc);
+  });
+}
+
 }  // namespace
 
 extern "C" {
@@ -933,22 +1136,29 @@ size_t mg_linear_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
 }
 
 size_t mg_log_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
-  return ew_ws_bytes(B, T, D);
+  return log_ws_bytes(B, T, D);
+}
+
+size_t mg_log_scan_state_bytes(int64_t B, int64_t T, int64_t D) {
+  if (B <= 0 || T <= 0 || D <= 0) return 0;
+  return (size_t)B * (size_t)((T + LOG_TSUB - 1) / LOG_TSUB) * 2 * (size_t)D * sizeof(float);
 }
 
 int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int64_t B, int64_t T,
                        int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!a || !b || !A || !Bc || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
-  const bool v4 = D % 4 == 0 && is_aligned16(a) && is_aligned16(b) && is_aligned16(A) &&
-                  is_aligned16(Bc);
-  const int vec = ew_vec(B, T, D, v4, EW_WAVES_FWD * EW_TSUB_FWD);
-  return by_vec(vec, [&](auto v) {
-    constexpr int V = decltype(v)::value;
-    EwPlan p = ew_plan(B, T, D, V, EW_TSUB_FWD, EW_WAVES_FWD, 1);
-    if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, false>, p, ws, stream, a, b, A,
-                     Bc);
-  });
+  return linear_fwd_launch(a, b, A, Bc, B, T, D, ws, ws_bytes, stream);
+}
+
+int mg_scan_workspace_errors(const void* ws, unsigned* count, hipStream_t stream) {
+  if (!ws || !count) return MG_ERR_ARG;
+  unsigned v = 0;
+  if (hipMemcpyAsync(&v, (const unsigned*)ws + MG_H_ERROR, sizeof(unsigned),
+                     hipMemcpyDeviceToHost, stream) != hipSuccess)
+    return MG_ERR_RUNTIME;
+  if (hipStreamSynchronize(stream) != hipSuccess) return MG_ERR_RUNTIME;
+  *count = v;
+  return MG_OK;
 }
 
 int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
@@ -1018,35 +1228,32 @@ int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_
                                       dlog_h0, B, T, D, ws, ws_bytes, stream);
 }
 
-int mg_log_scan_fwd(const float* lc, const float* lv, float* h, int64_t B, int64_t T, int64_t D,
-                    void* ws, size_t ws_bytes, hipStream_t stream) {
+int mg_log_scan_fwd(const float* lc, const float* lv, float* h, float* hstate, int64_t B,
+                    int64_t T, int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!lc || !lv || !h || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
-  const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h);
-  const int vec = ew_vec(B, T, D, v4, EW_WAVES_FWD * EW_TSUB_FWD);
-  return by_vec(vec, [&](auto v) {
+  const int vec = log_vec(B, T, D, {lc, lv, h, hstate});
+  auto run = [&](auto v) {
     constexpr int V = decltype(v)::value;
-    EwPlan p = ew_plan(B, T, D, V, EW_TSUB_FWD, EW_WAVES_FWD, 1);
+    EwPlan p = ew_plan(B, T, D, V, LOG_TSUB, LOG_WAVES, 3);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    float* none = nullptr;
-    return ew_launch(ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, true>, p, ws, stream, lc, lv, h,
-                     none);
-  });
+    return ew_launch(log_fwd_kernel<V, LOG_WAVES>, p, ws, stream, lc, lv, h, hstate);
+  };
+  return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});
 }
 
-int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* gh, float* dlc,
-                    float* dlv, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
-                    hipStream_t stream) {
+int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const float* hstate,
+                    const float* gh, float* dlc, float* dlv, int64_t B, int64_t T, int64_t D,
+                    void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!lc || !lv || !h || !gh || !dlc || !dlv || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
-  const bool v4 = D % 4 == 0 && is_aligned16(lc) && is_aligned16(lv) && is_aligned16(h) &&
-                  is_aligned16(gh) && is_aligned16(dlc) && is_aligned16(dlv);
-  const int vec = ew_vec(B, T, D, v4, EW_WAVES_BWD * EW_TSUB_BWD);
-  return by_vec(vec, [&](auto v) {
+  const int vec = log_vec(B, T, D, {lc, lv, h, hstate, gh, dlc, dlv});
+  auto run = [&](auto v) {
     constexpr int V = decltype(v)::value;
-    EwPlan p = ew_plan(B, T, D, V, EW_TSUB_BWD, EW_WAVES_BWD, 1);
+    EwPlan p = ew_plan(B, T, D, V, LOG_TSUB, LOG_WAVES, 3);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(log_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, lc, lv, h, gh,
-                     dlc, dlv);
-  });
+    return ew_launch(log_bwd_kernel<V, LOG_WAVES>, p, ws, stream, lc, lv, h, hstate, gh, dlc,
+                     dlv);
+  };
+  return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});
 }
 
 }  // extern "C"

@@ -22,6 +22,8 @@ is not supported (``once_differentiable``).
 
 from __future__ import annotations
 
+import ctypes
+import os
 import weakref
 
 import torch
@@ -38,6 +40,8 @@ __all__ = [
     "mingru_gate_scan_impl",
     "gate_step_impl",
     "delta_step_impl",
+    "workspace_errors",
+    "LookbackError",
 ]
 
 
@@ -141,6 +145,47 @@ def _scan_workspace(nbytes: int, device) -> torch.Tensor:
     return ws
 
 
+class LookbackError(RuntimeError):
+    """A look-back scan reported a failed wait (raised only under ``MINGRU_HIP_CHECK=1``)."""
+
+
+def _ws_error_count(ws: torch.Tensor) -> int:
+    """Failed look-back waits recorded in a scan workspace; synchronises its stream."""
+    from . import _native
+
+    cnt = ctypes.c_uint(0)
+    rc = _lib().mg_scan_workspace_errors(_ptr(ws), ctypes.byref(cnt), _stream(ws))
+    _native.check(rc, "mg_scan_workspace_errors")
+    return int(cnt.value)
+
+
+def workspace_errors() -> int:
+    """Failed look-back waits recorded so far in this process's cached scan workspaces.
+
+    Every look-back wait is bounded: one that gives up counts an error in its
+    workspace header and the kernel finishes with a partial carry, so a nonzero
+    count means some result was wrong.  Synchronises each workspace's stream.
+    """
+    return sum(_ws_error_count(ws) for ws in list(_scan_ws.values()))
+
+
+def _check_workspace(ws: torch.Tensor, t: torch.Tensor) -> None:
+    """Under ``MINGRU_HIP_CHECK=1``: wait for the call just queued and raise
+    ``LookbackError`` if its workspace recorded a failed look-back wait.  The
+    workspace is then dropped, so later calls start from a fresh one."""
+    if os.environ.get("MINGRU_HIP_CHECK", "0") in ("", "0"):
+        return
+    n = _ws_error_count(ws)
+    if n:
+        for key, cached in list(_scan_ws.items()):
+            if cached is ws:
+                del _scan_ws[key]
+        raise LookbackError(
+            f"HIP look-back scan on {t.device} recorded {n} failed wait(s): the results of the "
+            "calls since its workspace was created are not to be trusted"
+        )
+
+
 class kernel_timer:
     """Context manager recording HIP events around every C-ABI launch.
 
@@ -220,7 +265,7 @@ def _funnel(what: str, fn, *args):
     """Run ``fn`` and turn any launch-side failure into ``ScanFallback``."""
     try:
         return fn(*args)
-    except ScanFallback:
+    except (ScanFallback, LookbackError):
         raise
     except Exception as exc:  # noqa: BLE001 - every launch failure becomes a decline
         raise ScanFallback(f"{what} HIP kernel failed: {exc}") from exc
@@ -242,6 +287,7 @@ class _LinearScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
         _call("mg_linear_scan_fwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), Bn, T, D,
               _ptr(ws), ws.numel(), _stream(a32))
+        _check_workspace(ws, a32)
         ctx.save_for_backward(a32, b32, A, Bc)
         ctx.out_dtype = out_dtype
         if out_dtype != torch.float32:
@@ -259,6 +305,7 @@ class _LinearScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
         _call("mg_linear_scan_bwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), _ptr(gA32),
               _ptr(gB32), _ptr(da), _ptr(db), Bn, T, D, _ptr(ws), ws.numel(), _stream(a32))
+        _check_workspace(ws, a32)
         return da.to(ctx.out_dtype), db.to(ctx.out_dtype)
 
 
@@ -290,6 +337,7 @@ class _SignedGateScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_signed_gate_scan_workspace_bytes(Bn, T, D), s32.device)
         _call("mg_signed_gate_scan_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
               Bn, T, D, int(coupled), _ptr(ws), ws.numel(), _stream(s32))
+        _check_workspace(ws, s32)
         ctx.save_for_backward(s32, z32, hp32, h032, h)
         ctx.coupled = bool(coupled)
         ctx.out_dtype = out_dtype
@@ -307,6 +355,7 @@ class _SignedGateScanFn(torch.autograd.Function):
         _call("mg_signed_gate_scan_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
               _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, D, int(ctx.coupled),
               _ptr(ws), ws.numel(), _stream(s32))
+        _check_workspace(ws, s32)
         od = ctx.out_dtype
         return ds.to(od), dz.to(od), dhp.to(od), dh0.to(od), None
 
@@ -353,6 +402,7 @@ class _MinGRUGateScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_mingru_gate_scan_workspace_bytes(Bn, T, D), k32.device)
         _call("mg_mingru_gate_scan_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
               Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
+        _check_workspace(ws, k32)
         ctx.save_for_backward(k32, hp32, lh032, h)
         ctx.out_dtype = out_dtype
         return h if out_dtype == torch.float32 else h.to(out_dtype)
@@ -369,6 +419,7 @@ class _MinGRUGateScanFn(torch.autograd.Function):
         _call("mg_mingru_gate_scan_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
               _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), Bn, T, D,
               _ptr(ws), ws.numel(), _stream(k32))
+        _check_workspace(ws, k32)
         od = ctx.out_dtype
         return dk.to(od), dhp.to(od), dlh0.to(od)
 
@@ -409,24 +460,32 @@ class _LogScanFn(torch.autograd.Function):
         lc, lv = _as_f32(log_coeffs, log_values)
         Bn, T, D = lc.shape
         h = torch.empty_like(lc)
+        # Extended-range states at every 8-step boundary, kept for the backward so it
+        # can restart from values an fp32 h under- or overflows.
+        hstate = None
+        if any(ctx.needs_input_grad):
+            nfloat = _lib().mg_log_scan_state_bytes(Bn, T, D) // 4
+            hstate = torch.empty(nfloat, dtype=torch.float32, device=lc.device)
         ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
-        _call("mg_log_scan_fwd", _ptr(lc), _ptr(lv), _ptr(h), Bn, T, D, _ptr(ws), ws.numel(),
-              _stream(lc))
-        ctx.save_for_backward(lc, lv, h)
+        _call("mg_log_scan_fwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(hstate), Bn, T, D, _ptr(ws),
+              ws.numel(), _stream(lc))
+        _check_workspace(ws, lc)
+        ctx.save_for_backward(lc, lv, h, hstate)
         ctx.out_dtype = out_dtype
         return h if out_dtype == torch.float32 else h.to(out_dtype)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gh):
-        lc, lv, h = ctx.saved_tensors
+        lc, lv, h, hstate = ctx.saved_tensors
         Bn, T, D = lc.shape
         (gh32,) = _as_f32(gh)
         dlc = torch.empty_like(lc)
         dlv = torch.empty_like(lv)
         ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
-        _call("mg_log_scan_bwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(gh32), _ptr(dlc), _ptr(dlv),
-              Bn, T, D, _ptr(ws), ws.numel(), _stream(lc))
+        _call("mg_log_scan_bwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(hstate), _ptr(gh32),
+              _ptr(dlc), _ptr(dlv), Bn, T, D, _ptr(ws), ws.numel(), _stream(lc))
+        _check_workspace(ws, lc)
         return dlc.to(ctx.out_dtype), dlv.to(ctx.out_dtype)
 
 
@@ -466,6 +525,7 @@ class _AffineScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_fwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), Bn, T, n, k, v,
               _ptr(ws), ws.numel(), _stream(A32))
+        _check_workspace(ws, A32)
         ctx.save_for_backward(A32, B32, Abar, Bbar)
         ctx.out_dtype = out_dtype
         if out_dtype != torch.float32:
@@ -484,6 +544,7 @@ class _AffineScanFn(torch.autograd.Function):
         ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_bwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), _ptr(gA32),
               _ptr(gB32), _ptr(dA), _ptr(dB), Bn, T, n, k, v, _ptr(ws), ws.numel(), _stream(A32))
+        _check_workspace(ws, A32)
         return dA.to(ctx.out_dtype), dB.to(ctx.out_dtype)
 
 

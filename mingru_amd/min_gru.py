@@ -1366,6 +1366,40 @@ class DeltaMinGRU(DecayMixin, nn.Module):
         )
 
 
+def angle_scan_eager(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale, has_decay):
+    """Angle-fused scan contract evaluated eagerly by materialising every transition.
+
+    ``theta`` ``(B, T, n, R, half)``, ``scale``/``gamma`` ``(B, T, n)``, ``b``
+    ``(B, T, n, k)``, ``h0`` ``(B, n, k)`` and the plane tables ``perm``/``sgn``/``p2p``
+    ``(R, k)`` of ``_angle_plane_meta``.  Builds ``M_t = gamma_t R(theta_t) S_t``
+    ``(B, T, n, k, k)`` by the modules' row-update rule (round r maps
+    ``row_p <- c row_p + sgn_p s row_perm(p)`` on every position whose partner is not
+    itself; reference ``src/mingru/min_gru.py:2583-2602``), runs ``matrix_affine_scan``
+    and returns ``h = Abar h0 + Bbar`` ``(B, T, n, k)``: the path the reference's
+    Givens/Rotation modules take when the angle kernel declines, for any schedule.
+    """
+    Bn, T, n, R, _ = theta.shape
+    k = perm.shape[1]
+    M = torch.eye(k, dtype=theta.dtype, device=theta.device).expand(Bn, T, n, k, k)
+    if has_scale:
+        col = torch.ones(k, dtype=theta.dtype, device=theta.device)
+        col[1] = 0.0
+        M = M * (col + (1.0 - col) * scale[..., None]).unsqueeze(-2)
+    perm_l = perm.to(device=theta.device, dtype=torch.long)
+    p2p_l = p2p.to(device=theta.device, dtype=torch.long)
+    sgn_f = sgn.to(device=theta.device, dtype=theta.dtype)
+    pos = torch.arange(k, device=theta.device)
+    for r in range(R):
+        ang = theta[:, :, :, r, :].index_select(-1, p2p_l[r]).unsqueeze(-1)
+        rows = M.index_select(-2, perm_l[r])
+        rotated = torch.cos(ang) * M + sgn_f[r][:, None] * torch.sin(ang) * rows
+        M = torch.where((perm_l[r] != pos)[:, None], rotated, M)
+    if has_decay:
+        M = M * gamma[..., None, None]
+    Abar, Bbar = matrix_affine_scan(M, b.unsqueeze(-1))
+    return torch.einsum("btnij,bnj->btni", Abar, h0) + Bbar.squeeze(-1)
+
+
 def delta_chunked_eager(Q, K, V, beta, H, chunk_size):
     """Chunked-WY delta rule on the kernel layouts (eager, any device/dtype).
 

@@ -50,6 +50,11 @@ def test_ctypes_table_matches_header(lib):
 
 def test_workspace_queries(lib):
     assert lib.mg_linear_scan_workspace_bytes(16, 4096, 1024) >= 256
+    assert lib.mg_log_scan_workspace_bytes(4, 1024, 256) >= 256
+    # log scan forward record: (s, e) per column at every 8-step boundary
+    assert lib.mg_log_scan_state_bytes(4, 1024, 256) == 4 * 128 * 2 * 256 * 4
+    assert lib.mg_log_scan_state_bytes(2, 13, 5) == 2 * 2 * 2 * 5 * 4
+    assert lib.mg_log_scan_state_bytes(0, 13, 5) == 0
     assert lib.mg_affine_scan_workspace_bytes(16, 4096, 256, 2, 1) >= 256
     assert lib.mg_angle_scan_workspace_bytes(8, 2048, 64, 8) >= 256
     # angle chunk products: 8x8 floats per (block, 16-token chunk)
@@ -66,7 +71,10 @@ def test_invalid_arguments_are_rejected_on_the_host(lib):
     one = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     assert lib.mg_linear_scan_fwd(NULL, one, one, one, 1, 4, 4, one, 4096, NULL) == 1
     assert lib.mg_linear_scan_fwd(one, one, one, one, 0, 4, 4, one, 4096, NULL) == 1
-    assert lib.mg_log_scan_fwd(one, one, NULL, 1, 4, 4, one, 4096, NULL) == 1
+    assert lib.mg_log_scan_fwd(one, one, NULL, NULL, 1, 4, 4, one, 4096, NULL) == 1
+    assert lib.mg_log_scan_bwd(one, one, one, NULL, NULL, one, one, 1, 4, 4, one, 4096,
+                               NULL) == 1  # no upstream gradient
+    assert lib.mg_scan_workspace_errors(NULL, None, NULL) == 1
     assert lib.mg_affine_scan_fwd(one, one, one, one, 1, 4, 4, 3, 1, one, 4096, NULL) == 1
     assert lib.mg_angle_scan_fwd(one, one, one, one, one, one, one, 1, 4, 4, 6, 0, 3, 0, one,
                                  4096, NULL) == 1

@@ -205,3 +205,108 @@ def test_parallel_scan_log_long_sequence(cuda):
     rel = ((h.double() - ref).abs() / ref).max().item()
     print(f"[gpu] parallel_scan_log long sequence max rel err {rel:.3e}", flush=True)
     assert rel <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# parallel_scan_log over the whole fp32 log domain
+# ---------------------------------------------------------------------------
+
+FLT_MAX = float(np.finfo(np.float32).max)
+FLT_MIN = float(np.finfo(np.float32).tiny)
+
+
+def _heinsen_fp64(lc, lv):
+    """The reference's log-space formula (src/mingru/min_gru.py:804-807) in float64:
+    a* = pad(cumsum(lc)), h = exp(a* + logcumsumexp(lv - a*))[1:]."""
+    lc = np.asarray(lc, np.float64)
+    lv = np.asarray(lv, np.float64)
+    a_star = np.concatenate([np.zeros_like(lc[:, :1]), np.cumsum(lc, axis=1)], axis=1)
+    log_h = a_star + np.logaddexp.accumulate(lv - a_star, axis=1)
+    return np.exp(log_h)[:, 1:]
+
+
+def _assert_extended_close(x, ref, rtol, what):
+    """Elementwise check of an fp32 result against a float64 reference that may lie
+    outside fp32's range: +-inf where the reference overflows fp32, |err| <= 2 FLT_MIN
+    where it underflows, and relative error <= rtol (plus rtol times the column's
+    largest finite magnitude, for sums with cancellation) elsewhere."""
+    x = x.detach().double().cpu().numpy()
+    ref = np.asarray(ref, np.float64)
+    big = np.abs(ref) > FLT_MAX * (1 + 1e-6)
+    assert np.all(np.isinf(x[big]) & (np.sign(x[big]) == np.sign(ref[big]))), f"{what}: overflow"
+    tiny = np.abs(ref) < FLT_MIN
+    assert np.all(np.abs(x[tiny] - ref[tiny]) <= 2 * FLT_MIN), f"{what}: underflow"
+    mid = ~big & ~tiny & (np.abs(ref) < FLT_MAX * (1 - 1e-6))
+    scale = np.where(np.isfinite(ref) & ~big, np.abs(ref), 0.0).max(axis=1, keepdims=True)
+    bound = rtol * (np.abs(ref) + 1e-3 * scale)
+    err = np.abs(x - ref)
+    worst = float(np.max(np.where(mid, err / np.maximum(bound, 1e-300), 0.0)))
+    assert np.all(err[mid] <= bound[mid]), f"{what}: worst err/bound {worst:.3g}"
+
+
+EXTREME_CASES = {
+    # e^-150 initial state grown by e per step: h_199 = e^50 (5.18e21) although
+    # h_-1 and every b_t underflow fp32.
+    "grow_from_underflow": (1.0, -150.0, -200.0),
+    # e^120 initial state (overflows fp32) decaying by e^-1 per step towards the
+    # small inputs: h_199 = 0.0107.
+    "decay_from_overflow": (-1.0, 120.0, -5.0),
+}
+
+
+@pytest.mark.parametrize("case", sorted(EXTREME_CASES))
+def test_parallel_scan_log_extended_range(cuda, case):
+    """Inputs whose exponentials leave fp32's range while the outputs (or part of them)
+    stay inside it: fwd and grads against the float64 oracle, and the forward also
+    against the reference's float64 log-space formula."""
+    c, v0, v = EXTREME_CASES[case]
+    B, T, D = 2, 200, 70
+    print(f"[gpu] parallel_scan_log extended range case={case}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    lc = torch.full((B, T, D), c) + 0.01 * torch.randn(B, T, D, generator=g)
+    lv = torch.full((B, T + 1, D), v) + 0.5 * torch.randn(B, T + 1, D, generator=g)
+    lv[:, 0] = v0 + 0.5 * torch.randn(B, D, generator=g)
+    gh = torch.randn(B, T, D, generator=g)
+    h, dlc, dlv = _run_log(lc, lv, gh, cuda)
+    rh = orc.parallel_scan_log(lc.numpy(), lv.numpy())
+    np.testing.assert_allclose(rh, _heinsen_fp64(lc.numpy(), lv.numpy()), rtol=1e-9)
+    if case == "grow_from_underflow":
+        assert 1e20 < rh[0, -1, 0] < 1e23
+    else:
+        assert 0.005 < rh[0, -1, 0] < 0.03 and np.isinf(np.float32(rh[0, 0, 0]))
+    rdlc, rdlv = orc.parallel_scan_log_bwd(lc.numpy(), lv.numpy(), gh.numpy())
+    _assert_extended_close(h, rh, 2e-5, "h")
+    _assert_extended_close(dlc, rdlc, 1e-4, "dlc")
+    _assert_extended_close(dlv, rdlv, 1e-4, "dlv")
+
+
+def test_parallel_scan_log_backward_without_state_record(cuda):
+    """The C ABI's backward with no forward record (hstate = NULL) restarts from the fp32
+    outputs: same gradients as with the record for inputs inside fp32's range."""
+    import ctypes
+
+    from mingru_amd import _native
+
+    print("[gpu] parallel_scan_log backward with hstate = NULL", flush=True)
+    lib = _native.load()
+    inp = wl.c1_inputs(3, 517, 96)
+    lc, lv, gh = (inp[k].to(cuda).contiguous() for k in ("log_coeffs", "log_values", "grad_h"))
+    B, T, D = lc.shape
+    p = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws = torch.zeros(lib.mg_log_scan_workspace_bytes(B, T, D), dtype=torch.uint8, device=cuda)
+    hs = torch.empty(lib.mg_log_scan_state_bytes(B, T, D) // 4, device=cuda)
+    h = torch.empty_like(lc)
+    assert lib.mg_log_scan_fwd(p(lc), p(lv), p(h), p(hs), B, T, D, p(ws), ws.numel(), stream) == 0
+    grads = []
+    for state in (hs, None):
+        dlc, dlv = torch.empty_like(lc), torch.empty_like(lv)
+        assert lib.mg_log_scan_bwd(p(lc), p(lv), p(h), p(state), p(gh), p(dlc), p(dlv), B, T, D,
+                                   p(ws), ws.numel(), stream) == 0
+        grads.append((dlc, dlv))
+    torch.cuda.synchronize()
+    rdlc, rdlv = orc.parallel_scan_log_bwd(*(inp[k].numpy() for k in ("log_coeffs", "log_values",
+                                                                     "grad_h")))
+    for dlc, dlv in grads:
+        assert _maxerr(dlc, rdlc) <= GRAD_TOL and _maxerr(dlv, rdlv) <= GRAD_TOL
+    assert int(ws[8:12].view(torch.int32).item()) == 0

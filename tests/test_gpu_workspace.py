@@ -104,3 +104,55 @@ def test_side_stream_gets_its_own_workspace(cuda, monkeypatch):
     keys = [k for k in hip_scans._scan_ws if k[0] == cuda.index]
     assert (cuda.index, side.cuda_stream) in keys
     assert (cuda.index, torch.cuda.current_stream().cuda_stream) in keys
+
+
+def test_broken_workspace_is_reported_not_silent(cuda, monkeypatch):
+    """A workspace whose ticket counter already lies past the grid (as after a protocol
+    violation) makes every workgroup record an error and retire at once -- no wait, no
+    fault -- and the error is visible through mg_scan_workspace_errors and, under
+    MINGRU_HIP_CHECK=1, as a LookbackError.  The workspace is private to this test."""
+    print("[gpu] broken workspace reporting", flush=True)
+    lib = _native.load()
+    B, T, D = 2, 300, 64
+    a = torch.rand(B, T, D, device=cuda)
+    b = torch.randn(B, T, D, device=cuda)
+    nbytes = lib.mg_linear_scan_workspace_bytes(B, T, D)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+    # A zeroed workspace's first launch runs epoch 1, whose tickets come from counter 1.
+    ws[:16].view(torch.int32)[H_TICKET1] = 1 << 30
+    A, Bc = torch.empty_like(a), torch.empty_like(a)
+    rc = lib.mg_linear_scan_fwd(_p(a), _p(b), _p(A), _p(Bc), B, T, D, _p(ws), nbytes, _stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    hdr = ws[:16].view(torch.int32).cpu().numpy()
+    assert hdr[H_ERROR] > 0
+    assert hdr[H_EPOCH] == 0  # no workgroup held the last ticket
+    cnt = ctypes.c_uint(0)
+    assert lib.mg_scan_workspace_errors(_p(ws), ctypes.byref(cnt), _stream()) == 0
+    assert cnt.value == hdr[H_ERROR]
+    monkeypatch.setenv("MINGRU_HIP_CHECK", "1")
+    with pytest.raises(hip_scans.LookbackError):
+        hip_scans._check_workspace(ws, a)
+    monkeypatch.setenv("MINGRU_HIP_CHECK", "0")
+    hip_scans._check_workspace(ws, a)  # check mode off: nothing is read
+
+
+def test_check_mode_passes_on_healthy_workspaces(cuda, monkeypatch):
+    """MINGRU_HIP_CHECK=1 through the public ops: every call synchronises, reads its
+    workspace's error count (zero) and returns the same results."""
+    print("[gpu] check mode on healthy workspaces", flush=True)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    monkeypatch.setenv("MINGRU_HIP_CHECK", "1")
+    g = torch.Generator().manual_seed(29)
+    a = torch.tanh(torch.randn(2, 700, 96, generator=g)).to(cuda).requires_grad_()
+    b = torch.randn(2, 700, 96, generator=g).to(cuda).requires_grad_()
+    A, Bc = linear_scan(a, b)
+    (A.sum() + Bc.sum()).backward()
+    lc = -torch.nn.functional.softplus(torch.randn(2, 700, 96, generator=g)).to(cuda)
+    lv = torch.randn(2, 701, 96, generator=g).to(cuda)
+    h = parallel_scan_log(lc.requires_grad_(), lv.requires_grad_())
+    h.sum().backward()
+    torch.cuda.synchronize()
+    assert hip_scans.workspace_errors() == 0
+    rA, rB = orc.linear_scan(a.detach().double().cpu().numpy(), b.detach().double().cpu().numpy())
+    assert np.max(np.abs(Bc.detach().double().cpu().numpy() - rB)) <= 1e-4
