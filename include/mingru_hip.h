@@ -18,8 +18,8 @@
  *   - work is enqueued asynchronously on `stream`; nothing allocates, throws or
  *     synchronises;
  *   - the return value is a status: 0 ok, 1 invalid argument / outside the
- *     envelope, 2 kernel launch failed, 3 workspace too small, 5 a HIP
- *     runtime call failed.
+ *     envelope, 2 kernel launch failed, 3 workspace too small, 4 problem too
+ *     large for a fixed static scratch, 5 a HIP runtime call failed.
  *
  * Each declaration cites the reference interface it replaces
  * (chris-santiago/minGRU, paths relative to the repository root).
@@ -48,6 +48,20 @@ int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int6
 int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
                        const float* gA, const float* gB, float* da, float* db, int64_t B,
                        int64_t T, int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
+
+/* Allocation-free variant of mg_linear_scan_fwd.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * look-back workspace is a static device array of MG_NOALLOC_SCRATCH_BYTES per
+ * GPU, held from the library's first call on that GPU until the process ends
+ * and zero-filled once by that call (on `stream`).  Problems whose forward
+ * workspace exceeds it (about B*T*D > 2^27 elements) return
+ * MG_ERR_TOO_LARGE (4) without touching the device.  Every call on one GPU
+ * shares the array: calls must be ordered on one stream; calls that can
+ * overlap on one GPU race.  Allocates nothing, never synchronises. */
+#define MG_NOALLOC_SCRATCH_BYTES (32u << 20)
+int mg_linear_scan_fwd_noalloc(const float* a, const float* b, float* A, float* Bc, int64_t B,
+                               int64_t T, int64_t D, mg_stream_t stream);
 
 /* ---- fused SignedMinGRU gates + linear_scan, (B, T, D) -----------------------
  * No reference kernel fuses these: replaces the mixer's coefficient code and

@@ -46,6 +46,7 @@
 #define MG_ERR_ARG 1
 #define MG_ERR_LAUNCH 2
 #define MG_ERR_WORKSPACE 3
+#define MG_ERR_TOO_LARGE 4  // problem needs more than a fixed static scratch holds
 #define MG_ERR_RUNTIME 5    // a HIP runtime call (not a launch) failed
 
 typedef unsigned long long mg_slot_t;

@@ -26,6 +26,7 @@
 #include "mg_gates.h"
 
 #include <initializer_list>
+#include <mutex>
 #include <type_traits>
 
 #include <algorithm>
@@ -1097,6 +1098,59 @@ int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const flo
   });
 }
 
+// ---------------------------------------------------------------------------
+// Static look-back scratch for callers that cannot allocate
+// ---------------------------------------------------------------------------
+// One array per device, holding the workspace of mg_linear_scan_fwd_noalloc.
+// In host code `scratch` names a host-side stand-in, never the device memory:
+// every host use goes through the address hipGetSymbolAddress returns for the
+// current device, which is looked up once per device and cached.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;  // == MG_NOALLOC_SCRATCH_BYTES
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+struct NoallocDevice {
+  std::once_flag once;
+  void* ptr = nullptr;
+  int status = MG_ERR_RUNTIME;
+};
+NoallocDevice g_noalloc[NOALLOC_MAX_DEVICES];
+
+__global__ void zero_fill_kernel(uint4* __restrict__ p, size_t n16) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's scratch address, set up on the first call per device:
+// the symbol lookup, then one zero fill on `stream` (the look-back workspace
+// protocol starts from zeroed memory; later calls ordered on a stream after it
+// reuse the contents unchanged).
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return MG_ERR_RUNTIME;
+  NoallocDevice& d = g_noalloc[dev];
+  std::call_once(d.once, [&] {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      d.status = MG_ERR_RUNTIME;
+      return;
+    }
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)p,
+                       NOALLOC_SCRATCH_BYTES / 16);
+    if (hipGetLastError() != hipSuccess) {
+      d.status = MG_ERR_LAUNCH;
+      return;
+    }
+    d.ptr = p;
+    d.status = MG_OK;
+  });
+  *out = d.ptr;
+  return d.status;
+}
+
 template <int G>
 int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const float* h0,
                     const float* h, const float* gh, float* d0, float* d1, float* d2, float* dh0,
@@ -1127,6 +1181,14 @@ int linear_fwd_launch(const float* a, const float* b, float* A, float* Bc, int64
   });
 }
 
+// Workspace of the linear_scan forward alone, whatever lane width it picks.
+size_t linear_fwd_ws_bytes(int64_t B, int64_t T, int64_t D) {
+  size_t m = 0;
+  for (int vec : {1, 2, 4})
+    m = std::max(m, ew_plan(B, T, D, vec, EW_TSUB_FWD, EW_WAVES_FWD, 1).total);
+  return m;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1148,6 +1210,16 @@ int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int6
                        int64_t D, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!a || !b || !A || !Bc || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
   return linear_fwd_launch(a, b, A, Bc, B, T, D, ws, ws_bytes, stream);
+}
+
+int mg_linear_scan_fwd_noalloc(const float* a, const float* b, float* A, float* Bc, int64_t B,
+                               int64_t T, int64_t D, hipStream_t stream) {
+  if (!a || !b || !A || !Bc || !geometry_ok(B, T, D)) return MG_ERR_ARG;
+  if (linear_fwd_ws_bytes(B, T, D) > NOALLOC_SCRATCH_BYTES) return MG_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(stream, &ws);
+  if (rc != MG_OK) return rc;
+  return linear_fwd_launch(a, b, A, Bc, B, T, D, ws, NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int mg_scan_workspace_errors(const void* ws, unsigned* count, hipStream_t stream) {

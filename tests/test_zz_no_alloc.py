@@ -1,0 +1,70 @@
+"""The allocation-free linear_scan forward (``mg_linear_scan_fwd_noalloc``) against the
+existing entry point (``mg_linear_scan_fwd`` with a caller workspace), through the C ABI.
+
+The entry point keeps its look-back workspace in a static device array of the library
+(``MG_NOALLOC_SCRATCH_BYTES`` per GPU), so it must give the same results as the
+workspace entry point on consecutive calls of different sizes, and reject a problem
+whose workspace would not fit before touching the device."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from mingru_amd import _native
+from oracle import scans as orc
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-4  # fp32 forward bar against the float64 oracle
+MG_ERR_TOO_LARGE = 4
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _inputs(B, T, D, seed, cuda):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.tanh(2 * torch.randn(B, T, D, generator=g))
+    b = torch.randn(B, T, D, generator=g)
+    return a.to(cuda), b.to(cuda)
+
+
+def test_noalloc_matches_workspace_entry_point(cuda):
+    lib = _native.load()
+    # Two calls in a row, the second smaller (and with a narrower lane width).
+    for (B, T, D), seed in (((4, 3000, 512), 1), ((2, 777, 96), 2)):
+        print(f"[gpu] mg_linear_scan_fwd_noalloc B={B} T={T} D={D}", flush=True)
+        a, b = _inputs(B, T, D, seed, cuda)
+        A0, B0 = torch.empty_like(a), torch.empty_like(a)
+        A1, B1 = torch.full_like(a, float("nan")), torch.full_like(a, float("nan"))
+        nbytes = lib.mg_linear_scan_workspace_bytes(B, T, D)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+        assert lib.mg_linear_scan_fwd(_p(a), _p(b), _p(A0), _p(B0), B, T, D, _p(ws), nbytes,
+                                      _stream()) == 0
+        assert lib.mg_linear_scan_fwd_noalloc(_p(a), _p(b), _p(A1), _p(B1), B, T, D,
+                                              _stream()) == 0
+        torch.cuda.synchronize()
+        assert torch.isfinite(A1).all() and torch.isfinite(B1).all()
+        assert float((A1 - A0).abs().max()) <= FWD_TOL
+        assert float((B1 - B0).abs().max()) <= FWD_TOL
+        rA, rB = orc.linear_scan(a[:1].double().cpu().numpy(), b[:1].double().cpu().numpy())
+        assert np.max(np.abs(A1[:1].double().cpu().numpy() - rA)) <= FWD_TOL
+        assert np.max(np.abs(B1[:1].double().cpu().numpy() - rB)) <= FWD_TOL
+
+
+def test_noalloc_rejects_problems_beyond_the_scratch(cuda):
+    """B*T*D = 2^28 needs more look-back slots than the static array holds: status 4,
+    nothing launched (the pointers are never dereferenced)."""
+    print("[gpu] mg_linear_scan_fwd_noalloc size limit", flush=True)
+    lib = _native.load()
+    x = torch.zeros(16, device=cuda)
+    rc = lib.mg_linear_scan_fwd_noalloc(_p(x), _p(x), _p(x), _p(x), 64, 4096, 1024, _stream())
+    assert rc == MG_ERR_TOO_LARGE
+    assert lib.mg_linear_scan_fwd_noalloc(None, _p(x), _p(x), _p(x), 1, 4, 4, _stream()) == 1
