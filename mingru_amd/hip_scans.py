@@ -60,12 +60,18 @@ _AFFINE_V = frozenset({1, 2, 4, 8, 16})
 _ANGLE_K = frozenset({2, 4, 8})
 _ANGLE_MAX_ROT = 64
 
-# DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``).  The
-# kernels zero-pad every chunk matrix to 64 x 64, so any d_k, d_v up to 64 runs
-# (d_k need not equal d_v) and a chunk holds at most 64 micro-steps.
+# DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``): chunks
+# of at most 64 tokens and nh * chunk_size <= 128 micro-steps.  The kernels
+# zero-pad every chunk matrix to 64 x 64, so any d_k, d_v up to 64 runs (d_k need
+# not equal d_v) and one kernel tile holds at most 64 micro-steps.  A requested
+# chunk with more micro-steps than that runs as tiles of floor(64 / nh) tokens
+# (``_delta_tile_chunk``): the chunked-WY result does not depend on the chunk
+# size in exact arithmetic (reference ``tests/test_mixers.py:767-775``), so the
+# tiling changes only the rounding, which the parity bars against float64 cover.
 _DELTA_MAX_DIM = 64
 _DELTA_MAX_CHUNK = 64
-_DELTA_MAX_MICROSTEPS = 64
+_DELTA_MAX_MICROSTEPS = 128
+_DELTA_TILE_MICROSTEPS = 64
 _DELTA_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 _SUPPORTED_ARCH = "gfx950"
@@ -787,7 +793,17 @@ def _delta_envelope_reason(*, is_cuda: bool, q_dtype, k_dtype, v_dtype, beta_dty
     if nh * chunk_size > _DELTA_MAX_MICROSTEPS:
         return (f"DeltaMinGRU HIP kernel requires nh * chunk_size <= {_DELTA_MAX_MICROSTEPS} "
                 f"(got nh={nh}, chunk_size={chunk_size}, product={nh * chunk_size})")
+    if nh > _DELTA_TILE_MICROSTEPS:
+        return (f"DeltaMinGRU HIP kernel holds a token's micro-steps in one "
+                f"{_DELTA_TILE_MICROSTEPS}-step tile, so nh must be <= {_DELTA_TILE_MICROSTEPS} "
+                f"(got nh={nh})")
     return None
+
+
+def _delta_tile_chunk(nh: int, chunk_size: int) -> int:
+    """Tokens per kernel chunk: the requested chunk, capped so that one chunk holds at
+    most 64 micro-steps (same result in exact arithmetic; see ``_DELTA_MAX_MICROSTEPS``)."""
+    return max(1, min(int(chunk_size), _DELTA_TILE_MICROSTEPS // max(1, int(nh))))
 
 
 def _delta_validate_envelope(Q, K, V, beta, H0, chunk_size: int) -> None:
@@ -895,7 +911,7 @@ def delta_scan_impl(Q, K, V, beta, H0, *, chunk_size: int):
     if Q.shape[2] == 0:
         return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
     return _funnel("DeltaMinGRU chunked-WY", _DeltaScanFn.apply, Q, K, V, beta, H0,
-                   int(chunk_size))
+                   _delta_tile_chunk(K.shape[3], chunk_size))
 
 
 # ---------------------------------------------------------------------------
@@ -979,7 +995,7 @@ def delta_gated_scan_impl(Q, K, V, beta, log_gamma, H0, *, chunk_size: int):
     if Q.shape[2] == 0:
         return Q.new_zeros(Q.shape[:3] + (V.shape[-1],)), H0.clone()
     return _funnel("DeltaMinGRU gated chunked-WY", _DeltaGatedScanFn.apply, Q, K, V, beta,
-                   log_gamma, H0, int(chunk_size))
+                   log_gamma, H0, _delta_tile_chunk(K.shape[3], chunk_size))
 
 
 # ---------------------------------------------------------------------------

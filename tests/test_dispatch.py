@@ -203,7 +203,8 @@ _VIOLATIONS = {
     "dk": dict(d_k=65),
     "dv": dict(d_v=0),
     "chunk": dict(chunk_size=65),
-    "micro": dict(nh=2, chunk_size=33),
+    "micro": dict(nh=3, chunk_size=43),
+    "nh_tile": dict(nh=65, chunk_size=1),
 }
 
 
@@ -211,6 +212,18 @@ def test_delta_envelope_in_range_is_none():
     assert hip_scans._delta_envelope_reason(**_OK) is None
     assert hip_scans._delta_envelope_reason(**{**_OK, "d_k": 5, "d_v": 48, "nh": 4,
                                                "chunk_size": 16}) is None
+    # the reference's micro-step bound (nh * chunk_size <= 128), e.g. nh=2 at the
+    # module's default chunk_size=64
+    assert hip_scans._delta_envelope_reason(**{**_OK, "nh": 2, "chunk_size": 64}) is None
+    assert hip_scans._delta_envelope_reason(**{**_OK, "nh": 64, "chunk_size": 2}) is None
+
+
+@pytest.mark.parametrize("nh,chunk,tile", [(1, 64, 64), (1, 7, 7), (2, 64, 32), (2, 20, 20),
+                                           (3, 42, 21), (5, 25, 12), (64, 2, 1)])
+def test_delta_tile_chunk(nh, chunk, tile):
+    """Chunks of more than 64 micro-steps run as tiles of floor(64 / nh) tokens."""
+    assert hip_scans._delta_tile_chunk(nh, chunk) == tile
+    assert nh * hip_scans._delta_tile_chunk(nh, chunk) <= 64
 
 
 def test_delta_envelope_reasons_are_distinct():

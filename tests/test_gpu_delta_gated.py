@@ -75,6 +75,9 @@ CASES = [
     (1, 1, 300, 1, 64, 64, 64, "weak"),
     (1, 2, 95, 4, 64, 64, 16, "mod"),
     (1, 2, 200, 1, 64, 64, 64, "spikes"),
+    # nh * chunk above one 64-micro-step kernel tile (the reference allows 128)
+    (1, 2, 150, 2, 32, 32, 64, "mod"),
+    (1, 1, 90, 3, 16, 16, 40, "spikes"),
 ]
 
 
