@@ -256,4 +256,14 @@ __device__ __forceinline__ AfThread af_thread(const AfGeom& g, unsigned* header)
   return th;
 }
 
+// 8x8 and 16x16 blocks run on the matrix cores (scan_affine_mfma.hip).
+size_t affine_mfma_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
+bool affine_mfma_geometry_ok(int64_t B, int64_t T, int64_t n, int k);
+int affine_mfma_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,
+                    int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
+                    hipStream_t stream);
+int affine_mfma_bwd(const float* A, const float* Abar, const float* Bbar, const float* GA,
+                    const float* GB, float* dA, float* dB, int64_t B, int64_t T, int64_t n, int k,
+                    int v, void* ws, size_t ws_bytes, hipStream_t stream);
+
 }  // namespace mg

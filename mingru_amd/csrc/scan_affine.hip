@@ -423,9 +423,12 @@ size_t af_ws_bytes_k(int64_t B, int64_t T, int64_t n, int v) {
 }
 
 bool kv_ok(int k, int v) {
-  return (k == 1 || k == 2 || k == 4 || k == 8) &&
+  return (k == 1 || k == 2 || k == 4 || k == 8 || k == 16) &&
          (v == 1 || v == 2 || v == 4 || v == 8 || v == 16);
 }
+
+// 8x8 and 16x16 blocks: one wave per 16x16 block on the matrix cores.
+bool uses_mfma(int k) { return k >= 8; }
 
 bool af_geometry_ok(int64_t B, int64_t T, int64_t n) {
   if (B <= 0 || T <= 0 || n <= 0) return false;
@@ -496,6 +499,7 @@ extern "C" {
 
 size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v) {
   if (!kv_ok(k, v) || B <= 0 || T <= 0 || n <= 0) return 256;
+  if (uses_mfma(k)) return affine_mfma_workspace_bytes(B, T, n, k);
   switch (k) {
     case 1: return af_ws_bytes_k<1>(B, T, n, v);
     case 2: return af_ws_bytes_k<2>(B, T, n, v);
@@ -510,6 +514,10 @@ int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar
   if (!A || !Bm || !Abar || !Bbar || !ws || !kv_ok(k, v) || !af_geometry_ok(B, T, n))
     return MG_ERR_ARG;
   if (!al16(A) || !al16(Bm) || !al16(Abar) || !al16(Bbar)) return MG_ERR_ARG;
+  if (uses_mfma(k)) {
+    if (!affine_mfma_geometry_ok(B, T, n, k)) return MG_ERR_ARG;
+    return affine_mfma_fwd(A, Bm, Abar, Bbar, B, T, n, k, v, ws, ws_bytes, stream);
+  }
   MG_AF_DISPATCH(af_launch_fwd, A, Bm, Abar, Bbar, B, T, n, ws, ws_bytes, stream)
 }
 
@@ -523,6 +531,11 @@ int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const
   if (!al16(A) || !al16(Bm) || !al16(Abar) || !al16(Bbar) || !al16(gAbar) || !al16(gBbar) ||
       !al16(dA) || !al16(dBm))
     return MG_ERR_ARG;
+  if (uses_mfma(k)) {
+    if (!affine_mfma_geometry_ok(B, T, n, k)) return MG_ERR_ARG;
+    return affine_mfma_bwd(A, Abar, Bbar, gAbar, gBbar, dA, dBm, B, T, n, k, v, ws, ws_bytes,
+                           stream);
+  }
   MG_AF_DISPATCH(af_launch_bwd, A, Bm, Abar, Bbar, gAbar, gBbar, dA, dBm, B, T, n, ws, ws_bytes,
                  stream)
 }

@@ -50,10 +50,10 @@ class ScanFallback(Exception):
 
 
 # Block sizes the matrix kernels are compiled for (k x k transitions, k x v
-# injections).  Same set as the reference's envelope
-# (``src/mingru/triton_scans.py:183``) minus k = 16, whose 256-float block
-# product does not fit one thread's registers.
-_AFFINE_K = frozenset({1, 2, 4, 8})
+# injections): the reference's envelope (``src/mingru/triton_scans.py:183``).
+# k <= 4 run one plane per thread; k = 8 and 16 run one 16x16 block (two 8x8
+# planes or one 16x16 plane) per wave on the matrix cores.
+_AFFINE_K = frozenset({1, 2, 4, 8, 16})
 _AFFINE_V = frozenset({1, 2, 4, 8, 16})
 
 # Angle-fused kernel: block sizes and rotation-count limit.

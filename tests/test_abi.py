@@ -63,7 +63,13 @@ def test_workspace_queries(lib):
     assert lib.mg_delta_workspace_bytes(8, 8, 8192, 1, 64, 64, 64) == 6 * 64 * 128 * 64 * 64 * 4
     assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 64 * 128 * 64 * 64 * 4
     # outside the envelope: the minimum / zero answer, never a crash
-    assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 16, 1) == 256
+    assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 32, 1) == 256
+    assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 16, 3) == 256
+    # 16x16 blocks: one wave per block, (P, LA, LB) backward slots of 12 tagged words
+    # per lane for each 32-step chunk, an aggregate and an inclusive copy
+    assert lib.mg_affine_scan_workspace_bytes(2, 64, 3, 16, 4) == 256 + 2 * (6 * 2 * 12 * 64 * 8)
+    # 8x8 blocks: two planes per wave
+    assert lib.mg_affine_scan_workspace_bytes(2, 64, 3, 8, 4) == 256 + 2 * (4 * 2 * 12 * 64 * 8)
     assert lib.mg_delta_state_bytes(1, 1, 8, 1, 65, 64, 8) == 0
 
 

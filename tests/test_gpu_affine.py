@@ -46,6 +46,18 @@ CASES = [
     (2, 45, 66, 8, 1),
     (1, 19, 9, 8, 16),
     (1, 1000, 64, 1, 4),
+    # 2x2 blocks with re-read offsets, several chunks (look-back)
+    (2, 300, 70, 2, 4),
+    (2, 300, 70, 2, 8),
+    # 8x8 and 16x16 blocks on the matrix cores: odd plane counts (a half-empty
+    # 16x16 block for k = 8), single steps, ragged and multi-chunk lengths
+    (2, 300, 5, 8, 4),
+    (1, 1000, 4, 8, 2),
+    (2, 1, 1, 16, 4),
+    (2, 100, 3, 16, 1),
+    (1, 257, 2, 16, 16),
+    (3, 70, 7, 16, 8),
+    (1, 130, 1, 16, 2),
 ]
 
 
@@ -125,3 +137,31 @@ def test_identity_transitions_long_sequence_exact(cuda):
     torch.cuda.synchronize()
     assert torch.equal(Abar, A)
     assert torch.equal(Bbar.double(), Bm.double().cumsum(1))
+
+
+@pytest.mark.parametrize("case", [(1, 257, 2, 16, 16), (2, 300, 5, 8, 4)])
+def test_matrix_affine_scan_mfma_repeatable(cuda, case):
+    """Matrix-core blocks: five runs of one multi-chunk case give bitwise identical
+    outputs and gradients (the look-back consumes a predecessor's map only once the
+    whole wave sees it published, so no lane mixes in a stale part of it)."""
+    B, T, n, k, v = case
+    print(f"[gpu] matrix_affine_scan repeatable case={case}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    A = _contractive(B, T, n, k, g).to(cuda)
+    Bm = torch.randn(B, T, n, k, v, generator=g).to(cuda)
+    gA = torch.randn(B, T, n, k, k, generator=g).to(cuda)
+    gB = torch.randn(B, T, n, k, v, generator=g).to(cuda)
+    runs = []
+    for _ in range(5):
+        Ag = A.clone().requires_grad_(True)
+        Bg = Bm.clone().requires_grad_(True)
+        Abar, Bbar = matrix_affine_scan(Ag, Bg)
+        torch.autograd.backward([Abar, Bbar], [gA, gB])
+        runs.append([Abar.detach(), Bbar.detach(), Ag.grad, Bg.grad])
+    torch.cuda.synchronize()
+    for r in runs[1:]:
+        for x, y in zip(r, runs[0]):
+            assert torch.equal(x, y)
+    rdA, _ = orc.affine_scan_bwd(A.cpu().numpy(), Bm.cpu().numpy(), gA.cpu().numpy(),
+                                 gB.cpu().numpy())
+    assert _maxerr(runs[0][2], rdA) <= GRAD_TOL
