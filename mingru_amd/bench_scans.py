@@ -6,7 +6,9 @@ these too.  ``python -m mingru_amd.bench_scans [--check] [--bench] [--memory]
 [--out DIR] [--quick]`` writes, under ``DIR`` (default ``experiments/bench``):
 
 * ``--check``  -> ``scan_parity.json`` / ``.md``: ``{"meta": {...}, "rows": [...]}``,
-  one row per gated case with the reference's keys (``src/mingru/triton_scans.py:
+  one row per gated case over the reference's grid (every scan op at T in {1, 13,
+  64, 128, 1024} x B in {2, 128}; ``matrix_affine_scan`` over the whole k x v
+  envelope), with the reference's keys (``src/mingru/triton_scans.py:
   2634-2679``): ``op, shape, dtype, direction ("fwd" | "grad"), gate_atol,
   gate_rtol, max_abs_err, max_rel_err, pass, ref_fp64_dev``.  Each case runs the
   HIP path on fp32 inputs and the package's eager path in float64 on the same
@@ -40,6 +42,12 @@ import torch.nn.functional as F
 
 FWD_ATOL = 1e-4
 GRAD_ATOL = 1e-3
+
+# The reference's parity grid (``src/mingru/triton_scans.py:2753-2754``) and its
+# block envelope (``:183``).
+PARITY_TS = (1, 13, 64, 128, 1024)
+PARITY_BS = (2, 128)
+AFFINE_ENVELOPE = (1, 2, 4, 8, 16)
 
 LAB_SHAPE = {"label": "lab", "B": 128, "T": 64, "d": 64, "k": 8, "warmup": 10, "reps": 30}
 LONGT_SHAPE = {"label": "long-T", "B": 16, "T": 1024, "d": 64, "k": 8, "warmup": 5, "reps": 10}
@@ -91,6 +99,17 @@ def op_inputs(op: str, B: int, T: int, d: int, k: int, seed: int = 0):
         return (A, torch.randn(B, T, n, k, 1, generator=gen)), {"B": B, "T": T, "n": n, "k": k,
                                                                 "v": 1}
     raise ValueError(f"unknown op {op!r}")
+
+
+def affine_inputs(B: int, T: int, n: int, k: int, v: int, seed: int = 0):
+    """``matrix_affine_scan`` inputs for a generic (k, v): k x k transitions scaled to
+    spectral norm below 1 (so long products stay finite) and N(0, 1) offsets."""
+    gen = _gen(seed)
+    A = torch.randn(B, T, n, k, k, generator=gen, dtype=torch.float64)
+    A = A / torch.linalg.matrix_norm(A, ord=2)[..., None, None]
+    A = (A * torch.rand(B, T, n, 1, 1, generator=gen, dtype=torch.float64)).float()
+    Bm = torch.randn(B, T, n, k, v, generator=gen)
+    return (A, Bm), {"B": B, "T": T, "n": n, "k": k, "v": v}
 
 
 def _op_fn(op: str):
@@ -287,17 +306,29 @@ def run_check(out: Path, quick: bool = False) -> int:
 
     dev = torch.device("cuda")
     rows: list[dict] = []
-    shapes = [(2, 1, 16, 4), (2, 64, 32, 4), (3, 257, 48, 8)]
-    if quick:
-        shapes = shapes[:2]
+    Ts, Bs = ((1, 13, 64), (2,)) if quick else (PARITY_TS, PARITY_BS)
+    envelope = (1, 2, 8, 16) if quick else AFFINE_ENVELOPE
     seed = 0
-    for op in OPS:
+
+    def case(op, ins, shp):
+        nonlocal seed
+        seed += 1
+        tag = " ".join(f"{key}={v}" for key, v in shp.items())
+        print(f"  {op} {tag}", flush=True)
         fn = _op_fn(op)
-        for B, T, d, k in shapes:
-            seed += 1
-            ins, shp = op_inputs(op, B, T, d, k, seed)
-            tag = " ".join(f"{key}={v}" for key, v in shp.items())
-            _gate_rows(op, tag, fn, fn, ins, dev, rows, seed)
+        _gate_rows(op, tag, fn, fn, ins, dev, rows, seed)
+
+    # The reference's sweep: every scan op over T x B; matrix_affine_scan over the
+    # whole (k, v) envelope with one plane, then k = 8, v = 4 with three planes.
+    for B in Bs:
+        for T in Ts:
+            case("parallel_scan_log", *op_inputs("parallel_scan_log", B, T, 64, 1, seed))
+            case("linear_scan", *op_inputs("linear_scan", B, T, 64, 1, seed))
+            case("matrix_scan", *op_inputs("matrix_scan", B, T, 8, 2, seed))
+            for k in envelope:
+                for v in envelope:
+                    case("matrix_affine_scan", *affine_inputs(B, T, 1, k, v, seed))
+            case("matrix_affine_scan", *affine_inputs(B, T, 3, 8, 4, seed))
     # Mixer-level paths: the fused gate scans, the angle-fused Givens scan and the
     # chunked-WY delta rule (plain and decay-gated), each against its eager module.
     mixers = [
@@ -420,11 +451,17 @@ def run_memory(out: Path) -> int:
         torch.cuda.synchronize()
 
     def peak(mode):
+        # Bytes allocated during one forward+backward above what was already live
+        # when the window opened (the module, its input and anything an earlier
+        # mode of this process left behind), plus the module and input themselves,
+        # which a fresh process measuring only this step would hold too.
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
         once(mode)
-        return torch.cuda.max_memory_allocated()
+        return torch.cuda.max_memory_allocated() - base + own
 
+    own = sum(p.numel() * p.element_size() for p in m.parameters()) + x.numel() * x.element_size()
     once("eager")
     once("hip")
     eager_b, hip_b = peak("eager"), peak("hip")
@@ -433,7 +470,10 @@ def run_memory(out: Path) -> int:
              "peak_bytes": b, "peak_mb": b / 2**20}
             for impl, b in (("eager_phase1_generic", eager_b), ("angle_fused_hip", hip_b))]
     md = ("# GivensMinGRU backward peak memory (angle-fused HIP vs generic eager)\n\n"
-          f"Shape: {shape}\n\n| impl | peak MB |\n| --- | --- |\n"
+          f"Shape: {shape}\n\n"
+          "Peak bytes allocated by one forward+backward above the allocations live when "
+          "the measurement window opens, plus the module's parameters and its input.\n\n"
+          "| impl | peak MB |\n| --- | --- |\n"
           + "".join(f"| {r['impl']} | {r['peak_mb']:.2f} |\n" for r in rows))
     _write(out, "scan_memory", {"rows": rows}, md)
     return 0

@@ -63,3 +63,14 @@ def test_gpu_artefacts(tmp_path):
     mem = json.loads((tmp_path / "scan_memory.json").read_text())
     assert all(set(r) == REF_MEMORY_KEYS for r in mem["rows"])
     assert rc == 0
+
+
+def test_affine_inputs_cover_the_envelope():
+    """The parity sweep's generic (k, v) inputs: shapes, and transitions of spectral
+    norm below 1 so products over the longest grid length stay finite."""
+    assert bs.AFFINE_ENVELOPE == (1, 2, 4, 8, 16)
+    assert bs.PARITY_TS == (1, 13, 64, 128, 1024) and bs.PARITY_BS == (2, 128)
+    (A, Bm), shape = bs.affine_inputs(2, 5, 3, 16, 4, seed=1)
+    assert A.shape == (2, 5, 3, 16, 16) and Bm.shape == (2, 5, 3, 16, 4)
+    assert shape == {"B": 2, "T": 5, "n": 3, "k": 16, "v": 4}
+    assert float(torch.linalg.matrix_norm(A.double(), ord=2).max()) < 1.0
