@@ -171,6 +171,25 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
                       int64_t n, int k, int sched, int rounds, int flags, void* ws,
                       size_t ws_bytes, mg_stream_t stream);
 
+/* ---- angle-fused scan driven by run-time plane tables -------------------------
+ * Replaces the same reference kernels as mg_angle_scan_fwd/bwd
+ * (src/mingru/triton_scans.py:1039-1291, angle_scan_impl :1743-1812), taking
+ * their plane metadata as the reference kernel does: perm/p2p (R,k) int32 and
+ * sgn (R,k) fp32 on the device, theta (B,T,n,R,half).  k in {2,4,8,16},
+ * half <= 64, any R; the tables must describe disjoint plane rotations (perm an
+ * involution, partners sharing an angle, signs -1/+1; a position whose partner
+ * is itself is untouched).  flags as mg_angle_scan_fwd.  No workspace. */
+int mg_angle_scan_tables_fwd(const float* theta, const float* scale, const float* gamma,
+                             const float* b, const float* h0, const int* perm, const float* sgn,
+                             const int* p2p, float* h, int64_t B, int64_t T, int64_t n, int k,
+                             int R, int half, int flags, mg_stream_t stream);
+/* h = forward output, gh = dL/dh -> dtheta, dscale, dgamma (when flagged), db, dh0. */
+int mg_angle_scan_tables_bwd(const float* theta, const float* scale, const float* gamma,
+                             const float* h0, const float* h, const float* gh, const int* perm,
+                             const float* sgn, const int* p2p, float* dtheta, float* dscale,
+                             float* dgamma, float* db, float* dh0, int64_t B, int64_t T,
+                             int64_t n, int k, int R, int half, int flags, mg_stream_t stream);
+
 /* ---- DeltaMinGRU chunked-WY delta rule ----------------------------------------
  * Replaces the reference's three forward kernels (_delta_prepass_kernel,
  * _delta_state_kernel, _delta_readout_kernel, src/mingru/triton_scans.py:

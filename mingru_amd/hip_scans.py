@@ -56,9 +56,14 @@ class ScanFallback(Exception):
 _AFFINE_K = frozenset({1, 2, 4, 8, 16})
 _AFFINE_V = frozenset({1, 2, 4, 8, 16})
 
-# Angle-fused kernel: block sizes and rotation-count limit.
+# Angle-fused kernels.  The compiled-schedule kernels (brick-wall and
+# lexicographic rounds, chunk-parallel) take k in {2, 4, 8} and up to 64 rounds;
+# the table-driven kernel takes any valid plane tables for k up to 16 (the
+# reference's envelope, ``src/mingru/triton_scans.py:1791``).
 _ANGLE_K = frozenset({2, 4, 8})
 _ANGLE_MAX_ROT = 64
+_ANGLE_TABLE_K = frozenset({2, 4, 8, 16})
+_ANGLE_TABLE_MAX_HALF = 64
 
 # DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``): chunks
 # of at most 64 tokens and nh * chunk_size <= 128 micro-steps.  The kernels
@@ -675,6 +680,96 @@ def _classify_schedule(perm, sgn, p2p, k: int, R: int, half: int):
     return result
 
 
+_SCHED_TABLES = 2
+# id(perm) -> (weakref to perm, validity key, device tables) for the table-driven kernel.
+_table_cache: dict = {}
+
+
+def _table_reason(perm, sgn, p2p, k: int, half: int) -> str | None:
+    """Why the tables do not describe disjoint plane rotations, or ``None``.
+
+    Per round: ``perm`` is an involution on 0..k-1; a position paired with another
+    shares its partner's angle index (in 0..half-1) and has the opposite sign, -1
+    or +1; a position paired with itself is left untouched.
+    """
+    idx = torch.arange(k)
+    if perm.min() < 0 or perm.max() >= k:
+        return "perm entries must lie in [0, k)"
+    if not torch.equal(torch.gather(perm, 1, perm), idx.expand_as(perm)):
+        return "every round's perm must be an involution (partners pair up)"
+    act = perm != idx
+    part_q = torch.gather(p2p, 1, perm)
+    part_s = torch.gather(sgn, 1, perm)
+    if bool((act & ((p2p < 0) | (p2p >= half))).any()):
+        return "p2p entries of paired positions must lie in [0, half)"
+    if bool((act & (part_q != p2p)).any()):
+        return "paired positions must share one angle (equal p2p)"
+    if bool((act & ((sgn.abs() != 1) | (part_s != -sgn))).any()):
+        return "paired positions must carry opposite unit signs (sgn -1/+1)"
+    return None
+
+
+def _device_tables(perm, sgn, p2p, k: int, half: int, device):
+    """Validated int32/fp32 copies of the plane tables on ``device`` (cached per tensor)."""
+    key = (perm._version, sgn.data_ptr(), sgn._version, p2p.data_ptr(), p2p._version, k, half,
+           str(device))
+    hit = _table_cache.get(id(perm))
+    if hit is not None and hit[0]() is perm and hit[1] == key:
+        return hit[2]
+    pc = perm.detach().to("cpu", torch.int64)
+    sc = sgn.detach().to("cpu", torch.float64)
+    qc = p2p.detach().to("cpu", torch.int64)
+    reason = _table_reason(pc, sc, qc, k, half)
+    if reason is not None:
+        raise ScanFallback(f"angle-fused HIP kernel: plane tables rejected: {reason}")
+    tables = (pc.to(device, torch.int32).contiguous(), sc.to(device, torch.float32).contiguous(),
+              qc.to(device, torch.int32).contiguous())
+    if len(_table_cache) > 256:
+        for dead in [i for i, v in _table_cache.items() if v[0]() is None]:
+            del _table_cache[dead]
+    _table_cache[id(perm)] = (weakref.ref(perm), key, tables)
+    return tables
+
+
+class _AngleTablesFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, theta, scale, gamma, b, h0, perm, sgn, p2p, flags):
+        out_dtype = b.dtype
+        th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
+        Bn, T, n, k = b32.shape
+        R, half = th.shape[3], th.shape[4]
+        h = torch.empty_like(b32)
+        _call("mg_angle_scan_tables_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032),
+              _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(h), Bn, T, n, k, R, half, flags,
+              _stream(b32))
+        ctx.save_for_backward(th, sc, gm, h032, h, perm, sgn, p2p)
+        ctx.meta = (flags, out_dtype, theta.dtype, scale.dtype, gamma.dtype, h0.dtype)
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        th, sc, gm, h032, h, perm, sgn, p2p = ctx.saved_tensors
+        flags, out_dtype, tdt, sdt, gdt, hdt = ctx.meta
+        Bn, T, n, k = h.shape
+        R, half = th.shape[3], th.shape[4]
+        (gh32,) = _as_f32(gh)
+        need = ctx.needs_input_grad
+        dth = torch.empty_like(th)
+        dsc = (torch.empty_like(sc) if flags & 1 else torch.zeros_like(sc)) \
+            if (flags & 1 or need[1]) else None
+        dgm = (torch.empty_like(gm) if flags & 2 else torch.zeros_like(gm)) \
+            if (flags & 2 or need[2]) else None
+        db = torch.empty_like(h)
+        dh0 = torch.empty_like(h032)
+        _call("mg_angle_scan_tables_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h),
+              _ptr(gh32), _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(dth), _ptr(dsc), _ptr(dgm),
+              _ptr(db), _ptr(dh0), Bn, T, n, k, R, half, flags, _stream(h))
+        return (dth.to(tdt), None if dsc is None else dsc.to(sdt),
+                None if dgm is None else dgm.to(gdt), db.to(out_dtype), dh0.to(hdt),
+                None, None, None, None)
+
+
 class _AngleScanFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, theta, scale, gamma, b, h0, sched, rounds, flags):
@@ -736,7 +831,8 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
     Bn, T, n, R, half = theta.shape
     k = b.shape[-1]
     if (
-        k not in _ANGLE_K
+        k not in _ANGLE_TABLE_K
+        or half > _ANGLE_TABLE_MAX_HALF
         or tuple(b.shape[:3]) != (Bn, T, n)
         or tuple(scale.shape) != (Bn, T, n)
         or tuple(gamma.shape) != (Bn, T, n)
@@ -744,19 +840,31 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
         or tuple(perm.shape) != (R, k)
         or tuple(sgn.shape) != (R, k)
         or tuple(p2p.shape) != (R, k)
-        or R > _ANGLE_MAX_ROT
     ):
         raise ScanFallback(
             f"angle-fused kernel (theta={tuple(theta.shape)}, scale={tuple(scale.shape)}, "
             f"gamma={tuple(gamma.shape)}, b={tuple(b.shape)}, h0={tuple(h0.shape)}, "
-            f"perm={tuple(perm.shape)}) outside the envelope: need k in {sorted(_ANGLE_K)}, "
-            f"R <= {_ANGLE_MAX_ROT} and shapes agreeing on (B, T, n, R, k)"
+            f"perm={tuple(perm.shape)}) outside the envelope: need k in "
+            f"{sorted(_ANGLE_TABLE_K)}, at most {_ANGLE_TABLE_MAX_HALF} angles per round and "
+            "shapes agreeing on (B, T, n, R, k)"
         )
     _same_device(theta, scale, gamma, b, h0)
-    sched, rounds = _classify_schedule(perm, sgn, p2p, k, R, half)
+    flags = (1 if has_scale else 0) | (2 if has_decay else 0)
+    sched = None
+    if k in _ANGLE_K and R <= _ANGLE_MAX_ROT:
+        try:
+            sched, rounds = _classify_schedule(perm, sgn, p2p, k, R, half)
+        except ScanFallback:
+            sched = None
+    if sched is None:
+        # Any other schedule, more rounds, or k = 16: the table-driven kernel.
+        tables = _device_tables(perm, sgn, p2p, k, half, b.device)
+        if T == 0:
+            return b.new_empty(b.shape)
+        return _funnel("angle-fused (plane tables)", _AngleTablesFn.apply, theta, scale, gamma,
+                       b, h0, *tables, flags)
     if T == 0:
         return b.new_empty(b.shape)
-    flags = (1 if has_scale else 0) | (2 if has_decay else 0)
     return _funnel("angle-fused", _AngleScanFn.apply, theta, scale, gamma, b, h0, sched, rounds,
                    flags)
 

@@ -584,3 +584,61 @@ def test_givens_step_runs_the_angle_scan_for_one_token(monkeypatch):
     assert seen["theta"][:3] == (3, 1, 2) and seen["has_decay"] == 1
     assert torch.equal(seen["h0"], hp.reshape(3, 2, 8))
     assert torch.equal(h, torch.full((3, 16), 4.0))
+
+
+# ---------------------------------------------------------------- angle plane tables
+
+
+def _random_tables(k, R, half, seed, inactive=False):
+    """Random disjoint plane rotations per round: a random pairing of the positions,
+    random signs and random angle indices (shared by partners)."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.arange(k).repeat(R, 1)
+    sgn = torch.zeros(R, k)
+    p2p = torch.zeros(R, k, dtype=torch.int64)
+    for r in range(R):
+        order = torch.randperm(k, generator=g)
+        npairs = k // 2 - (1 if inactive else 0)
+        for m in range(npairs):
+            i, j = int(order[2 * m]), int(order[2 * m + 1])
+            s = 1.0 if torch.rand(1, generator=g).item() < 0.5 else -1.0
+            a = int(torch.randint(half, (1,), generator=g))
+            perm[r, i], perm[r, j] = j, i
+            sgn[r, i], sgn[r, j] = s, -s
+            p2p[r, i] = p2p[r, j] = a
+    return perm.to(torch.int32), sgn, p2p.to(torch.int32)
+
+
+def test_plane_tables_accepted():
+    for k, R in ((2, 1), (8, 3), (16, 3)):
+        perm, sgn, p2p = hip_scans._brick_tables(k, R)
+        assert hip_scans._table_reason(perm, sgn, p2p, k, k // 2) is None
+    from mingru_amd import workloads as wl
+
+    perm, sgn, p2p = wl.lexicographic_schedule(16)
+    assert hip_scans._table_reason(perm.long(), sgn.double(), p2p.long(), 16, 1) is None
+    perm, sgn, p2p = _random_tables(8, 5, 3, seed=1, inactive=True)
+    assert hip_scans._table_reason(perm.long(), sgn.double(), p2p.long(), 8, 3) is None
+
+
+def test_plane_tables_rejected_with_distinct_reasons():
+    base = [t.clone() for t in hip_scans._brick_tables(8, 2)]
+    bad = {}
+    p, s, q = (t.clone() for t in base)
+    p[0, 0] = 9
+    bad["range"] = (p, s, q)
+    p, s, q = (t.clone() for t in base)
+    p[0, 0], p[0, 1] = 2, 0  # 0 -> 2 but 2 -> 3
+    bad["involution"] = (p, s, q)
+    p, s, q = (t.clone() for t in base)
+    q[0, 0] = 3
+    bad["angle"] = (p, s, q)
+    p, s, q = (t.clone() for t in base)
+    s[0, 0] = 1.0  # same sign as its partner
+    bad["sign"] = (p, s, q)
+    p, s, q = (t.clone() for t in base)
+    q[0, 0] = q[0, 1] = 7
+    bad["p2p range"] = (p, s, q)
+    reasons = {name: hip_scans._table_reason(*t, 8, 4) for name, t in bad.items()}
+    assert all(r is not None for r in reasons.values()), reasons
+    assert len(set(reasons.values())) == len(reasons)

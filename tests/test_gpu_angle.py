@@ -52,7 +52,7 @@ def _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, hs, hd):
     ts = [t.to(cuda).requires_grad_(True) for t in (theta, scale, gamma, b, h0)]
     h = hip_scans.angle_scan_impl(*ts, perm.to(cuda), sgn.to(cuda), p2p.to(cuda),
                                   has_scale=hs, has_decay=hd)
-    assert "AngleScanFn" in type(h.grad_fn).__name__
+    assert type(h.grad_fn).__name__.startswith(("_AngleScanFn", "_AngleTablesFn"))
     h.backward(gh.to(cuda))
     torch.cuda.synchronize()
     npy = [t.numpy() for t in (theta, scale, gamma, b, h0)]
@@ -108,6 +108,56 @@ def test_lexicographic_schedule_matches_oracle(cuda, case):
     _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, 0, hd)
 
 
+TABLE_CASES = [
+    # B, T, n, k, R, half, schedule, has_scale, has_decay
+    (2, 50, 3, 16, 3, 8, "brick", 0, 1),
+    (1, 70, 2, 16, 5, 8, "brick", 0, 0),
+    (2, 20, 2, 16, 120, 1, "lex", 0, 1),
+    (2, 40, 5, 8, 5, 3, "random", 1, 1),
+    (1, 33, 4, 4, 7, 2, "random_inactive", 0, 1),
+    (2, 25, 3, 2, 2, 1, "random", 1, 0),
+    (1, 1, 2, 16, 3, 8, "brick", 1, 1),
+    (2, 30, 4, 8, 70, 4, "random", 0, 1),  # more rounds than the compiled kernels take
+]
+
+
+def _tables(k, R, half, kind, seed):
+    from test_dispatch import _random_tables
+
+    if kind == "brick":
+        return _brick_meta(k, R)
+    if kind == "lex":
+        return wl.lexicographic_schedule(k)
+    return _random_tables(k, R, half, seed, inactive=kind == "random_inactive")
+
+
+@pytest.mark.parametrize("case", TABLE_CASES)
+def test_plane_table_kernel_matches_oracle(cuda, case, monkeypatch):
+    """The table-driven kernel (k = 16, any valid plane tables, any round count) against
+    the float64 oracle, fwd and all gradients."""
+    B, T, n, k, R, half, kind, hs, hd = case
+    print(f"[gpu] angle tables case={case}", flush=True)
+    perm, sgn, p2p = _tables(k, R, half, kind, seed=T + k + R)
+    theta, scale, gamma, b, h0, gh = _inputs(B, T, n, k, R, half, seed=3 * T + n + k, std=0.6)
+    used = []
+    real = hip_scans._AngleTablesFn.apply
+
+    def spy(*a):
+        used.append(True)
+        return real(*a)
+
+    monkeypatch.setattr(hip_scans._AngleTablesFn, "apply", spy)
+    _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, hs, hd)
+    assert used, "the table-driven kernel did not run"
+
+
+def test_givens_block16_module_matches_fp64(cuda, monkeypatch):
+    """GivensMinGRU(block_size=16) under MINGRU_SCAN=hip (table-driven angle kernel)."""
+    torch.manual_seed(5)
+    _module_vs_fp64(cuda, mg.GivensMinGRU(12, 48, block_size=16), torch.randn(2, 60, 12),
+                    monkeypatch)
+
+
 def test_c4_full_size(cuda):
     print("[gpu] angle C4 full size", flush=True)
     inp = wl.c4_inputs(**wl.C4)
@@ -156,40 +206,49 @@ def test_c4_norm_preserved_full_size(cuda):
     assert drift <= 1e-4
 
 
-def _module_parity(cuda, layer, T=64, B=3):
-    torch.manual_seed(0)
-    layer = layer.to(cuda)
-    x = torch.randn(B, T, layer.input_size, device=cuda)
-    os.environ["MINGRU_SCAN"] = "eager"
-    y_ref = layer(x)
-    y_ref.square().sum().backward()
-    g_ref = {n: p.grad.clone() for n, p in layer.named_parameters()}
-    layer.zero_grad()
-    os.environ["MINGRU_SCAN"] = "hip"
-    y = layer(x)
+def _module_vs_fp64(cuda, layer, x, monkeypatch, dt=None):
+    """A mixer under MINGRU_SCAN=hip on the GPU (fp32) against a float64 copy of it on
+    the CPU eager path: output within 1e-4 and the input and parameter gradients within
+    1e-3, each relative to max(1, max |ref|) (the undecayed rotation state grows to
+    |h| ~ 10 over a sequence)."""
+    import copy
+
+    ref = copy.deepcopy(layer).double()
+    xr = x.double().requires_grad_(True)
+    dtr = None if dt is None else dt.double()
+    monkeypatch.setenv("MINGRU_SCAN", "eager")
+    yr = ref(xr, delta_t=dtr)
+    yr.square().sum().backward()
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    lg = layer.to(cuda)
+    xg = x.to(cuda).requires_grad_(True)
+    y = lg(xg, delta_t=None if dt is None else dt.to(cuda))
     y.square().sum().backward()
-    assert (y - y_ref).abs().max().item() <= FWD_TOL * 10
-    for n, p in layer.named_parameters():
-        scale = max(1.0, g_ref[n].abs().max().item())
-        assert (p.grad - g_ref[n]).abs().max().item() <= 1e-3 * scale, n
+    torch.cuda.synchronize()
+
+    def rel(a, r):
+        return (a.double().cpu() - r).abs().max().item() / max(1.0, r.abs().max().item())
+
+    assert rel(y, yr) <= FWD_TOL, f"output {rel(y, yr):.2e}"
+    assert rel(xg.grad, xr.grad) <= GRAD_TOL
+    gp = dict(ref.named_parameters())
+    for name, p in lg.named_parameters():
+        assert rel(p.grad, gp[name].grad) <= GRAD_TOL, name
 
 
-def test_givens_module_matches_eager(cuda):
-    _module_parity(cuda, mg.GivensMinGRU(16, 64))
+def test_givens_module_matches_eager(cuda, monkeypatch):
+    torch.manual_seed(0)
+    _module_vs_fp64(cuda, mg.GivensMinGRU(16, 64), torch.randn(3, 64, 16), monkeypatch)
 
 
-def test_givens_module_decay_matches_eager(cuda):
-    layer = mg.GivensMinGRU(16, 32, decay="learnable")
-    layer = layer.to(cuda)
+def test_givens_module_decay_matches_eager(cuda, monkeypatch):
     torch.manual_seed(1)
-    x = torch.randn(2, 40, 16, device=cuda)
-    dt = torch.rand(2, 40, device=cuda)
-    os.environ["MINGRU_SCAN"] = "eager"
-    y_ref = layer(x, delta_t=dt)
-    os.environ["MINGRU_SCAN"] = "hip"
-    y = layer(x, delta_t=dt)
-    assert (y - y_ref).abs().max().item() <= 1e-4
+    layer = mg.GivensMinGRU(16, 32, decay="learnable")
+    _module_vs_fp64(cuda, layer, torch.randn(2, 40, 16), monkeypatch, dt=torch.rand(2, 40))
 
 
-def test_rotation_module_matches_eager(cuda):
-    _module_parity(cuda, mg.RotationMinGRU(16, 32, snap=None))
+@pytest.mark.parametrize("snap", [None, (2, 3, 4, 6)], ids=["nosnap", "default_snap"])
+def test_rotation_module_matches_eager(cuda, monkeypatch, snap):
+    torch.manual_seed(2)
+    _module_vs_fp64(cuda, mg.RotationMinGRU(16, 32, snap=snap), torch.randn(3, 64, 16),
+                    monkeypatch)
