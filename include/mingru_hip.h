@@ -176,19 +176,28 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
  * (src/mingru/triton_scans.py:1039-1291, angle_scan_impl :1743-1812), taking
  * their plane metadata as the reference kernel does: perm/p2p (R,k) int32 and
  * sgn (R,k) fp32 on the device, theta (B,T,n,R,half).  k in {2,4,8,16},
- * half <= 64, any R; the tables must describe disjoint plane rotations (perm an
- * involution, partners sharing an angle, signs -1/+1; a position whose partner
- * is itself is untouched).  flags as mg_angle_scan_fwd.  No workspace. */
+ * half <= 64, R <= 128; the tables must describe disjoint plane rotations (perm
+ * an involution, partners sharing an angle that no other plane of the round
+ * uses, signs -1/+1; a position whose partner is itself is untouched).  flags as
+ * mg_angle_scan_fwd.  The forward writes the per-chunk transition products to
+ * `chunk_prod` (mg_angle_scan_tables_state_bytes), which the backward reads;
+ * the workspace (mg_angle_scan_tables_workspace_bytes) needs no initialisation.
+ * The backward writes dtheta only for angles some plane uses. */
+size_t mg_angle_scan_tables_state_bytes(int64_t B, int64_t T, int64_t n, int k);
+size_t mg_angle_scan_tables_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
 int mg_angle_scan_tables_fwd(const float* theta, const float* scale, const float* gamma,
                              const float* b, const float* h0, const int* perm, const float* sgn,
-                             const int* p2p, float* h, int64_t B, int64_t T, int64_t n, int k,
-                             int R, int half, int flags, mg_stream_t stream);
-/* h = forward output, gh = dL/dh -> dtheta, dscale, dgamma (when flagged), db, dh0. */
+                             const int* p2p, float* h, float* chunk_prod, int64_t B, int64_t T,
+                             int64_t n, int k, int R, int half, int flags, void* ws,
+                             size_t ws_bytes, mg_stream_t stream);
+/* h = forward output, chunk_prod = the forward's chunk products, gh = dL/dh
+ * -> dtheta, dscale, dgamma (when flagged), db, dh0. */
 int mg_angle_scan_tables_bwd(const float* theta, const float* scale, const float* gamma,
-                             const float* h0, const float* h, const float* gh, const int* perm,
-                             const float* sgn, const int* p2p, float* dtheta, float* dscale,
-                             float* dgamma, float* db, float* dh0, int64_t B, int64_t T,
-                             int64_t n, int k, int R, int half, int flags, mg_stream_t stream);
+                             const float* h0, const float* h, const float* chunk_prod,
+                             const float* gh, const int* perm, const float* sgn, const int* p2p,
+                             float* dtheta, float* dscale, float* dgamma, float* db, float* dh0,
+                             int64_t B, int64_t T, int64_t n, int k, int R, int half, int flags,
+                             void* ws, size_t ws_bytes, mg_stream_t stream);
 
 /* ---- DeltaMinGRU chunked-WY delta rule ----------------------------------------
  * Replaces the reference's three forward kernels (_delta_prepass_kernel,

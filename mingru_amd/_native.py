@@ -57,8 +57,14 @@ _SIGNATURES = {
     "mg_angle_scan_bwd": (
         _I32, [_P] * 12 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
-    "mg_angle_scan_tables_fwd": (_I32, [_P] * 9 + [_I64, _I64, _I64] + [_I32] * 4 + [_P]),
-    "mg_angle_scan_tables_bwd": (_I32, [_P] * 14 + [_I64, _I64, _I64] + [_I32] * 4 + [_P]),
+    "mg_angle_scan_tables_state_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
+    "mg_angle_scan_tables_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
+    "mg_angle_scan_tables_fwd": (
+        _I32, [_P] * 10 + [_I64, _I64, _I64] + [_I32] * 4 + [_P, _SZ, _P],
+    ),
+    "mg_angle_scan_tables_bwd": (
+        _I32, [_P] * 15 + [_I64, _I64, _I64] + [_I32] * 4 + [_P, _SZ, _P],
+    ),
     "mg_delta_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
     "mg_delta_state_bytes": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I32]),
     "mg_delta_fwd": (

@@ -64,6 +64,7 @@ _ANGLE_K = frozenset({2, 4, 8})
 _ANGLE_MAX_ROT = 64
 _ANGLE_TABLE_K = frozenset({2, 4, 8, 16})
 _ANGLE_TABLE_MAX_HALF = 64
+_ANGLE_TABLE_MAX_ROUNDS = 128
 
 # DeltaMinGRU envelope (reference ``src/mingru/triton_scans.py:294-300``): chunks
 # of at most 64 tokens and nh * chunk_size <= 128 micro-steps.  The kernels
@@ -706,7 +707,22 @@ def _table_reason(perm, sgn, p2p, k: int, half: int) -> str | None:
         return "paired positions must share one angle (equal p2p)"
     if bool((act & ((sgn.abs() != 1) | (part_s != -sgn))).any()):
         return "paired positions must carry opposite unit signs (sgn -1/+1)"
+    for r in range(perm.shape[0]):
+        firsts = act[r] & (sgn[r] < 0)  # one member of each plane
+        used = p2p[r][firsts]
+        if used.numel() != torch.unique(used).numel():
+            return "an angle may drive at most one plane per round"
     return None
+
+
+def _tables_cover_all_angles(perm, p2p, half: int) -> bool:
+    """Whether every angle index of every round drives a plane (then the backward
+    writes every dtheta element; otherwise the unused ones must start at zero)."""
+    act = perm != torch.arange(perm.shape[1])
+    for r in range(perm.shape[0]):
+        if torch.unique(p2p[r][act[r]]).numel() != half:
+            return False
+    return True
 
 
 def _device_tables(perm, sgn, p2p, k: int, half: int, device):
@@ -723,7 +739,7 @@ def _device_tables(perm, sgn, p2p, k: int, half: int, device):
     if reason is not None:
         raise ScanFallback(f"angle-fused HIP kernel: plane tables rejected: {reason}")
     tables = (pc.to(device, torch.int32).contiguous(), sc.to(device, torch.float32).contiguous(),
-              qc.to(device, torch.int32).contiguous())
+              qc.to(device, torch.int32).contiguous(), _tables_cover_all_angles(pc, qc, half))
     if len(_table_cache) > 256:
         for dead in [i for i, v in _table_cache.items() if v[0]() is None]:
             del _table_cache[dead]
@@ -733,41 +749,49 @@ def _device_tables(perm, sgn, p2p, k: int, half: int, device):
 
 class _AngleTablesFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, theta, scale, gamma, b, h0, perm, sgn, p2p, flags):
+    def forward(ctx, theta, scale, gamma, b, h0, perm, sgn, p2p, cover, flags):
         out_dtype = b.dtype
         th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
         Bn, T, n, k = b32.shape
         R, half = th.shape[3], th.shape[4]
         h = torch.empty_like(b32)
+        lib = _lib()
+        # Chunk products P_c, saved for the backward (whose chunk maps are P_c^T).
+        prod = torch.empty(max(int(lib.mg_angle_scan_tables_state_bytes(Bn, T, n, k)), 16) // 4,
+                           dtype=torch.float32, device=b32.device)
+        ws = _workspace(lib.mg_angle_scan_tables_workspace_bytes(Bn, T, n, k), b32.device)
         _call("mg_angle_scan_tables_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032),
-              _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(h), Bn, T, n, k, R, half, flags,
-              _stream(b32))
-        ctx.save_for_backward(th, sc, gm, h032, h, perm, sgn, p2p)
-        ctx.meta = (flags, out_dtype, theta.dtype, scale.dtype, gamma.dtype, h0.dtype)
+              _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(h), _ptr(prod), Bn, T, n, k, R, half, flags,
+              _ptr(ws), ws.numel(), _stream(b32))
+        ctx.save_for_backward(th, sc, gm, h032, h, prod, perm, sgn, p2p)
+        ctx.meta = (flags, cover, out_dtype, theta.dtype, scale.dtype, gamma.dtype, h0.dtype)
         return h if out_dtype == torch.float32 else h.to(out_dtype)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gh):
-        th, sc, gm, h032, h, perm, sgn, p2p = ctx.saved_tensors
-        flags, out_dtype, tdt, sdt, gdt, hdt = ctx.meta
+        th, sc, gm, h032, h, prod, perm, sgn, p2p = ctx.saved_tensors
+        flags, cover, out_dtype, tdt, sdt, gdt, hdt = ctx.meta
         Bn, T, n, k = h.shape
         R, half = th.shape[3], th.shape[4]
         (gh32,) = _as_f32(gh)
         need = ctx.needs_input_grad
-        dth = torch.empty_like(th)
+        # dtheta of an angle no plane uses is zero; the kernel writes only used ones.
+        dth = torch.empty_like(th) if cover else torch.zeros_like(th)
         dsc = (torch.empty_like(sc) if flags & 1 else torch.zeros_like(sc)) \
             if (flags & 1 or need[1]) else None
         dgm = (torch.empty_like(gm) if flags & 2 else torch.zeros_like(gm)) \
             if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
+        ws = _workspace(_lib().mg_angle_scan_tables_workspace_bytes(Bn, T, n, k), h.device)
         _call("mg_angle_scan_tables_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h),
-              _ptr(gh32), _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(dth), _ptr(dsc), _ptr(dgm),
-              _ptr(db), _ptr(dh0), Bn, T, n, k, R, half, flags, _stream(h))
+              _ptr(prod), _ptr(gh32), _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(dth), _ptr(dsc),
+              _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k, R, half, flags, _ptr(ws), ws.numel(),
+              _stream(h))
         return (dth.to(tdt), None if dsc is None else dsc.to(sdt),
                 None if dgm is None else dgm.to(gdt), db.to(out_dtype), dh0.to(hdt),
-                None, None, None, None)
+                None, None, None, None, None)
 
 
 class _AngleScanFn(torch.autograd.Function):
@@ -833,6 +857,7 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
     if (
         k not in _ANGLE_TABLE_K
         or half > _ANGLE_TABLE_MAX_HALF
+        or R > _ANGLE_TABLE_MAX_ROUNDS
         or tuple(b.shape[:3]) != (Bn, T, n)
         or tuple(scale.shape) != (Bn, T, n)
         or tuple(gamma.shape) != (Bn, T, n)
@@ -845,8 +870,8 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
             f"angle-fused kernel (theta={tuple(theta.shape)}, scale={tuple(scale.shape)}, "
             f"gamma={tuple(gamma.shape)}, b={tuple(b.shape)}, h0={tuple(h0.shape)}, "
             f"perm={tuple(perm.shape)}) outside the envelope: need k in "
-            f"{sorted(_ANGLE_TABLE_K)}, at most {_ANGLE_TABLE_MAX_HALF} angles per round and "
-            "shapes agreeing on (B, T, n, R, k)"
+            f"{sorted(_ANGLE_TABLE_K)}, at most {_ANGLE_TABLE_MAX_HALF} angles per round, at "
+            f"most {_ANGLE_TABLE_MAX_ROUNDS} rounds and shapes agreeing on (B, T, n, R, k)"
         )
     _same_device(theta, scale, gamma, b, h0)
     flags = (1 if has_scale else 0) | (2 if has_decay else 0)

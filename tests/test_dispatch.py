@@ -599,10 +599,12 @@ def _random_tables(k, R, half, seed, inactive=False):
     for r in range(R):
         order = torch.randperm(k, generator=g)
         npairs = k // 2 - (1 if inactive else 0)
+        angles = torch.randperm(half, generator=g)  # one distinct angle per plane
+        assert npairs <= half
         for m in range(npairs):
             i, j = int(order[2 * m]), int(order[2 * m + 1])
             s = 1.0 if torch.rand(1, generator=g).item() < 0.5 else -1.0
-            a = int(torch.randint(half, (1,), generator=g))
+            a = int(angles[m])
             perm[r, i], perm[r, j] = j, i
             sgn[r, i], sgn[r, j] = s, -s
             p2p[r, i] = p2p[r, j] = a
@@ -639,6 +641,17 @@ def test_plane_tables_rejected_with_distinct_reasons():
     p, s, q = (t.clone() for t in base)
     q[0, 0] = q[0, 1] = 7
     bad["p2p range"] = (p, s, q)
+    p, s, q = (t.clone() for t in base)
+    q[0, 2] = q[0, 3] = 0  # planes (0,1) and (2,3) both driven by angle 0
+    bad["shared angle"] = (p, s, q)
     reasons = {name: hip_scans._table_reason(*t, 8, 4) for name, t in bad.items()}
     assert all(r is not None for r in reasons.values()), reasons
     assert len(set(reasons.values())) == len(reasons)
+
+
+def test_plane_table_angle_cover():
+    perm, sgn, p2p = hip_scans._brick_tables(8, 3)
+    assert hip_scans._tables_cover_all_angles(perm, p2p, 4)
+    assert not hip_scans._tables_cover_all_angles(perm, p2p, 5)  # angle 4 unused
+    perm, sgn, p2p = _random_tables(4, 3, 2, seed=2, inactive=True)
+    assert not hip_scans._tables_cover_all_angles(perm.long(), p2p.long(), 2)

@@ -113,11 +113,13 @@ TABLE_CASES = [
     (2, 50, 3, 16, 3, 8, "brick", 0, 1),
     (1, 70, 2, 16, 5, 8, "brick", 0, 0),
     (2, 20, 2, 16, 120, 1, "lex", 0, 1),
-    (2, 40, 5, 8, 5, 3, "random", 1, 1),
+    (2, 40, 5, 8, 5, 6, "random", 1, 1),  # two of six angles unused per round
     (1, 33, 4, 4, 7, 2, "random_inactive", 0, 1),
     (2, 25, 3, 2, 2, 1, "random", 1, 0),
     (1, 1, 2, 16, 3, 8, "brick", 1, 1),
     (2, 30, 4, 8, 70, 4, "random", 0, 1),  # more rounds than the compiled kernels take
+    (1, 300, 3, 16, 3, 8, "brick", 0, 1),  # many chunks: the boundary walks
+    (2, 129, 2, 8, 4, 4, "random", 1, 0),
 ]
 
 
