@@ -83,10 +83,16 @@ _DELTA_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 _SUPPORTED_ARCH = "gfx950"
 
 
-def _lib():
-    from . import _native
+from . import _native
 
-    return _native.load()
+_loaded = None
+
+
+def _lib():
+    global _loaded
+    if _loaded is None:
+        _loaded = _native.load()
+    return _loaded
 
 
 _avail_cache: dict = {}
@@ -94,6 +100,8 @@ _avail_cache: dict = {}
 
 def available() -> bool | str:
     """``True`` if the HIP kernels can run in this process, else the reason."""
+    if _loaded is not None and _avail_cache.get(torch.cuda.current_device()) == _SUPPORTED_ARCH:
+        return True  # this device was checked before and the library is loaded
     if not torch.cuda.is_available():
         return "CUDA/HIP device not available"
     if torch.version.hip is None:
@@ -163,8 +171,6 @@ class LookbackError(RuntimeError):
 
 def _ws_error_count(ws: torch.Tensor) -> int:
     """Failed look-back waits recorded in a scan workspace; synchronises its stream."""
-    from . import _native
-
     cnt = ctypes.c_uint(0)
     rc = _lib().mg_scan_workspace_errors(_ptr(ws), ctypes.byref(cnt), _stream(ws))
     _native.check(rc, "mg_scan_workspace_errors")
@@ -234,8 +240,6 @@ class kernel_timer:
 
 
 def _call(fn_name: str, *args) -> None:
-    from . import _native
-
     timer = kernel_timer.active
     if timer is not None:
         start = timer._event()
