@@ -25,6 +25,9 @@
 //           through the chunk's rotations (k+1 rotated columns per token);
 //   pass 2  two lanes per block walk the chunk boundaries in order,
 //           h_{c+1} = P_c h_c + L_c, carrying only its k-vector (half each);
+//           for long sequences over groups of AN_GROUP chunks instead (group
+//           maps composed in parallel, the walk over the groups, then each
+//           group's chunk states filled in in parallel);
 //   pass 3  one lane per (block, chunk) re-applies the rotations to the state
 //           vector from its chunk-entry state and writes every h_t.
 // The forward saves the chunk products P_c for the backward.
@@ -56,6 +59,12 @@ constexpr int AN_CHUNK = 16;         // tokens per chunk
 constexpr int AN_WALK_THREADS = 64;  // boundary walk: one wave per workgroup (each on its own CU)
 constexpr int AN_WALK_AHEAD = 4;     // chunks prefetched ahead by the boundary walk
 constexpr int AN_WALK_RING = AN_WALK_AHEAD + 1;
+// Two-level boundary walk: the chunk maps of AN_GROUP consecutive chunks are
+// composed into one group map (in parallel over groups), the walk runs over the
+// groups, and each group's chunk-entry states are filled in from its entry state
+// (in parallel again).  Used once a sequence has more than AN_GROUP_MIN chunks.
+constexpr int AN_GROUP = 8;
+constexpr int AN_GROUP_MIN = 2 * AN_GROUP;
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -856,6 +865,133 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_bwd_scan(AnArgs a, AnGe
   st<H>(a.dh0 + blk * K + H * p, y);  // the adjoint leaving chunk 0 is dL/dh0
 }
 
+// ---- two-level walk: group maps and the chunk states inside each group ---------
+// Forward group map over chunks c0 .. c1 (applied in order): h -> Pg h + Lg.
+// Backward group map over the same chunks applied from c1 down to c0:
+// y -> Qg y + lg with Qg = P_c0^T ... P_c1^T.  K lanes per (block, group): lane j
+// carries column j of the group's linear part (and, redundantly, its offset), so
+// a chunk costs each lane two k x k matrix-vector products; the next chunk's map
+// is loaded while the current one is applied.  `gp`, `gl` are [group][block][K*K]
+// and [group][block][K].
+template <int K, bool BWD>
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_compose(AnArgs a, AnGeom g,
+                                                                       float* gp, float* gl,
+                                                                       int n_groups) {
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int j = (int)(gt % K);
+  const int64_t gb = gt / K;
+  const int64_t blk = gb % g.NB;
+  const int grp = (int)(gb / g.NB);
+  if (grp >= n_groups) return;
+  const int c0 = grp * AN_GROUP, c1 = min(c0 + AN_GROUP, g.n_chunks) - 1;
+  float m[K], l[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    m[i] = (i == j) ? 1.f : 0.f;
+    l[i] = 0.f;
+  }
+  struct Op {
+    float P[K * K], L[K];
+  };
+  auto fetch = [&](Op& o, int s) {
+    s = min(s, c1 - c0);  // clamped reads past the group's end are unused
+    const int c = BWD ? c1 - s : c0 + s;
+    ld<K * K>(o.P, a.prod + an_idx(g, c, 0, K * K, blk));
+    ld<K>(o.L, a.lsum + an_idx(g, c, 0, K, blk));
+  };
+  auto apply = [&](const Op& o) {
+    // forward: column <- P column, l <- P l + L;  backward: with P^T
+    float nm[K], nl[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float am = 0.f, al = o.L[i];
+#pragma unroll
+      for (int q = 0; q < K; ++q) {
+        const float pe = BWD ? o.P[q * K + i] : o.P[i * K + q];
+        am = fmaf(pe, m[q], am);
+        al = fmaf(pe, l[q], al);
+      }
+      nm[i] = am;
+      nl[i] = al;
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      m[i] = nm[i];
+      l[i] = nl[i];
+    }
+  };
+  Op A, B;
+  fetch(A, 0);
+  const int cnt = c1 - c0 + 1;
+  int s = 0;
+  for (; s + 2 <= cnt; s += 2) {
+    fetch(B, s + 1);
+    apply(A);
+    fetch(A, s + 2);
+    apply(B);
+  }
+  if (s < cnt) apply(A);
+  // The group walk reads these as it reads chunk maps: forward P rows, backward P
+  // columns, so the backward map is stored transposed (Qg^T = P_c1 ... P_c0).
+  float* out = gp + an_idx(g, grp, 0, K * K, blk);
+  if (BWD) {
+    st<K>(out + j * K, m);  // row j of Qg^T is column j of Qg
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) out[i * K + j] = m[i];
+  }
+  if (j == 0) st<K>(gl + an_idx(g, grp, 0, K, blk), l);
+}
+
+// Chunk-entry states (forward) / adjoints (backward) of every chunk of a group
+// from the group's entry value `gb` [group][block][K].  K lanes per (block,
+// group), lane i owning coordinate i: all of the group's rows i of P_c (columns,
+// backward) and offsets are loaded up front, and a chunk step is one partner read
+// per coordinate and K multiply-adds.
+template <int K, bool BWD>
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_fill(AnArgs a, AnGeom g,
+                                                                    const float* gb,
+                                                                    int n_groups) {
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int i = (int)(gt % K);
+  const int64_t gbk = gt / K;
+  const int64_t blk = gbk % g.NB;
+  const int grp = (int)(gbk / g.NB);
+  const bool ok = grp < n_groups;  // every lane stays for the partner reads
+  const int lane = threadIdx.x & (MG_WAVE - 1), base = lane - i;
+  const int c0 = ok ? grp * AN_GROUP : 0;
+  const int c1 = ok ? min(c0 + AN_GROUP, g.n_chunks) - 1 : 0;
+  const int cnt = c1 - c0 + 1;
+  float P[AN_GROUP][K], L[AN_GROUP];
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    const int c = BWD ? c1 - min(s, cnt - 1) : c0 + min(s, cnt - 1);
+    const float* pc = a.prod + an_idx(g, c, 0, K * K, blk);
+    if (ok) {
+      if (BWD) {
+#pragma unroll
+        for (int q = 0; q < K; ++q) P[s][q] = pc[q * K + i];
+      } else {
+        ld<K>(P[s], pc + i * K);
+      }
+      L[s] = a.lsum[an_idx(g, c, i, K, blk)];
+    } else {
+#pragma unroll
+      for (int q = 0; q < K; ++q) P[s][q] = 0.f;
+      L[s] = 0.f;
+    }
+  }
+  float h = ok ? gb[an_idx(g, grp, i, K, blk)] : 0.f;
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    if (ok && s < cnt) a.bound[an_idx(g, BWD ? c1 - s : c0 + s, i, K, blk)] = h;
+    float acc = L[s];
+#pragma unroll
+    for (int q = 0; q < K; ++q) acc = fmaf(P[s][q], __shfl(h, base + q), acc);
+    h = acc;
+  }
+}
+
 // ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, AnGeom g) {
@@ -945,10 +1081,17 @@ AnGeom an_geom(int64_t B, int64_t T, int64_t n) {
 }
 
 // Workspace: chunk offsets and chunk-entry states, K floats each per (chunk, block).
+int an_groups(const AnGeom& g) { return (g.n_chunks + AN_GROUP - 1) / AN_GROUP; }
+
+// Header, chunk offsets and chunk-entry values ([chunk][block][k] each), then the
+// two-level walk's group maps ([group][block][k*k] and [group][block][k]) and
+// group-entry values.
 size_t an_ws_bytes(int64_t B, int64_t T, int64_t n, int k) {
   const AnGeom g = an_geom(B, T, n);
   const size_t one = mg_align_up((size_t)g.n_chunks * k * g.NB * sizeof(float), 256);
-  return MG_HEADER_BYTES + 2 * one;
+  const size_t gv = mg_align_up((size_t)an_groups(g) * k * g.NB * sizeof(float), 256);
+  const size_t gm = mg_align_up((size_t)an_groups(g) * k * k * g.NB * sizeof(float), 256);
+  return MG_HEADER_BYTES + 2 * one + gm + 2 * gv;
 }
 
 // Chunk products saved by the forward for the backward: K*K floats per (chunk, block).
@@ -969,13 +1112,41 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
   const dim3 grid((unsigned)((waves + AN_WAVES - 1) / AN_WAVES)), block(MG_WAVE * AN_WAVES);
   const dim3 sgrid((unsigned)((g.NB * 2 + AN_WALK_THREADS - 1) / AN_WALK_THREADS)),
       sblock(AN_WALK_THREADS);
+  // Boundary walk: direct over the chunks, or over groups of AN_GROUP chunks.
+  auto walk = [&]() {
+    if (g.n_chunks <= AN_GROUP_MIN) {
+      if (BWD) hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+      else hipLaunchKernelGGL((angle_fwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+      return;
+    }
+    const int ng = an_groups(g);
+    const size_t gv = mg_align_up((size_t)ng * K * g.NB * sizeof(float), 256);
+    const size_t gm = mg_align_up((size_t)ng * K * K * g.NB * sizeof(float), 256);
+    char* base = (char*)ws + MG_HEADER_BYTES + 2 * one;
+    float* gp = (float*)base;
+    float* gl = (float*)(base + gm);
+    float* gb = (float*)(base + gm + gv);
+    const dim3 cgrid((unsigned)((g.NB * ng * K + AN_WALK_THREADS - 1) / AN_WALK_THREADS));
+    hipLaunchKernelGGL((angle_group_compose<K, BWD>), cgrid, sblock, 0, stream, a, g, gp, gl, ng);
+    // The walk kernels over the group maps: chunks -> groups.
+    AnArgs ag = a;
+    AnGeom gg = g;
+    ag.prod = gp;
+    ag.lsum = gl;
+    ag.bound = gb;
+    gg.n_chunks = ng;
+    if (BWD) hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, ag, gg);
+    else hipLaunchKernelGGL((angle_fwd_scan<K>), sgrid, sblock, 0, stream, ag, gg);
+    hipLaunchKernelGGL((angle_group_fill<K, BWD>), cgrid, sblock, 0, stream, a, g,
+                       (const float*)gb, ng);
+  };
   if (BWD) {
     hipLaunchKernelGGL((angle_bwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
-    hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+    walk();
     hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   } else {
     hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
-    hipLaunchKernelGGL((angle_fwd_scan<K>), sgrid, sblock, 0, stream, a, g);
+    walk();
     hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   }
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;

@@ -83,6 +83,10 @@ BRICK_CASES = [
     (2, 90, 65, 2, 1, 1, 0),
     (2, 71, 12, 2, 1, 1, 1),
     (1, 40, 7, 2, 3, 0, 1),
+    # more than 16 chunks of 16 tokens: the two-level boundary walk, last group partial
+    (2, 300, 5, 8, 3, 0, 1),
+    (1, 530, 3, 2, 1, 1, 1),
+    (1, 260, 4, 4, 2, 0, 0),
 ]
 
 
@@ -95,7 +99,8 @@ def test_brick_schedule_matches_oracle(cuda, case):
     _check(cuda, theta, scale, gamma, b, h0, gh, perm, sgn, p2p, hs, hd)
 
 
-LEX_CASES = [(2, 33, 10, 8, 1), (1, 120, 64, 8, 1), (2, 45, 20, 4, 1), (2, 30, 66, 8, 0)]
+LEX_CASES = [(2, 33, 10, 8, 1), (1, 120, 64, 8, 1), (2, 45, 20, 4, 1), (2, 30, 66, 8, 0),
+             (1, 400, 6, 8, 1)]
 
 
 @pytest.mark.parametrize("case", LEX_CASES)
