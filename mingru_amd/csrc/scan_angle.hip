@@ -40,6 +40,7 @@
 // reverse time.  Its chunk maps are y -> P_c^T y + Lb_c: the linear part is
 // the saved forward product transposed, so pass 1 only sweeps one column.
 #include "mg_affm.h"
+#include "mg_sincos.h"
 
 #include <algorithm>
 #include <utility>
@@ -92,34 +93,6 @@ constexpr int angles_per_round() {
 template <typename F, std::size_t... Is>
 __device__ __forceinline__ void static_for(F&& f, std::index_sequence<Is...>) {
   (f(std::integral_constant<int, (int)Is>{}), ...);
-}
-
-// sin and cos of x (radians), about 1 ulp for |x| up to a few thousand.
-// Cody-Waite reduction by the nearest multiple q of pi/2 (pi/2 split into a
-// float head and tail), Taylor polynomials on [-pi/4, pi/4] (sin to r^9,
-// cos to r^10: the first omitted terms are below 2e-9), then the quadrant
-// q mod 4 selects and negates.  The hardware sine (about 6 ulp) drifts a
-// state vector measurably over thousands of rotations; this costs about
-// twice as many VALU instructions and keeps the drift at fp32 rounding.
-__device__ __forceinline__ void mg_sincos(float x, float& s, float& c) {
-  const float q = rintf(x * 0.636619772367581343f);  // x / (pi/2)
-  float r = fmaf(-q, 1.57079637050628662f, x);
-  r = fmaf(-q, -4.37113900018624283e-8f, r);
-  const float r2 = r * r;
-  float ps = fmaf(r2, 2.75573192239858907e-6f, -1.98412698412698413e-4f);
-  ps = fmaf(ps, r2, 8.33333333333333333e-3f);
-  ps = fmaf(ps, r2, -1.66666666666666667e-1f);
-  const float sr = fmaf(ps * r2, r, r);
-  float pc = fmaf(r2, -2.75573192239858907e-7f, 2.48015873015873016e-5f);
-  pc = fmaf(pc, r2, -1.38888888888888889e-3f);
-  pc = fmaf(pc, r2, 4.16666666666666667e-2f);
-  pc = fmaf(pc, r2, -0.5f);
-  const float cr = fmaf(pc, r2, 1.0f);
-  const int quad = (int)q & 3;
-  const float ss = (quad & 1) ? cr : sr;
-  const float cc = (quad & 1) ? sr : cr;
-  s = (quad & 2) ? -ss : ss;
-  c = ((quad + 1) & 2) ? -cc : cc;
 }
 
 // Rows I, J of an NC-column block: row_I <- c row_I - s row_J, row_J <- s row_I + c row_J.
@@ -441,6 +414,7 @@ __device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const 
 // ---- forward pass 1: chunk aggregates h -> P_c h + L_c ------------------------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, AnGeom g) {
+  mg_sincos_setup();
   const AnThread th = an_thread(g);
   if (!th.ok) return;
   const int64_t t0 = (int64_t)th.c * AN_CHUNK;
@@ -581,6 +555,7 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_fwd_scan(AnArgs a, AnGe
 // ---- forward pass 3: every token's state from its chunk-entry state ------------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, AnGeom g) {
+  mg_sincos_setup();
   const AnThread th = an_thread(g);
   if (!th.ok) return;
   const int64_t t0 = (int64_t)th.c * AN_CHUNK;
@@ -760,6 +735,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
 // x <- M_t^T (x + g_t).
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, AnGeom g) {
+  mg_sincos_setup();
   const AnThread th = an_thread(g);
   if (!th.ok) return;
   const int64_t t0 = (int64_t)th.c * AN_CHUNK;
@@ -995,6 +971,7 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_fill(AnArgs a, An
 // ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, AnGeom g) {
+  mg_sincos_setup();
   const AnThread th = an_thread(g);
   if (!th.ok) return;
   const int64_t t0 = (int64_t)th.c * AN_CHUNK;

@@ -36,39 +36,19 @@
 //               input by the transposed rotation, and write dtheta, dscale,
 //               dgamma and db.
 #include "mg_common.h"
+#include "mg_sincos.h"
 
 #include <algorithm>
 
 namespace {
 
+using mg::mg_sincos;
+using mg::mg_sincos_setup;
+
 constexpr int AT_THREADS = 256;
 constexpr int AT_CHUNK = 16;        // tokens per chunk
 constexpr int AT_MAX_HALF = 64;     // angles per round
 constexpr int AT_MAX_ROUNDS = 128;  // rounds held in LDS
-
-// Cody-Waite sin/cos (same method as the compiled-schedule kernels): reduction
-// by the nearest multiple of pi/2 with pi/2 in two parts, Taylor polynomials on
-// [-pi/4, pi/4], quadrant select.
-__device__ __forceinline__ void at_sincos(float x, float& s, float& c) {
-  const float q = rintf(x * 0.636619772367581343f);
-  float r = fmaf(-q, 1.57079637050628662f, x);
-  r = fmaf(-q, -4.37113900018624283e-8f, r);
-  const float r2 = r * r;
-  float ps = fmaf(r2, 2.75573192239858907e-6f, -1.98412698412698413e-4f);
-  ps = fmaf(ps, r2, 8.33333333333333333e-3f);
-  ps = fmaf(ps, r2, -1.66666666666666667e-1f);
-  const float sr = fmaf(ps * r2, r, r);
-  float pc = fmaf(r2, -2.75573192239858907e-7f, 2.48015873015873016e-5f);
-  pc = fmaf(pc, r2, -1.38888888888888889e-3f);
-  pc = fmaf(pc, r2, 4.16666666666666667e-2f);
-  pc = fmaf(pc, r2, -0.5f);
-  const float cr = fmaf(pc, r2, 1.0f);
-  const int quad = (int)q & 3;
-  const float ss = (quad & 1) ? cr : sr;
-  const float cc = (quad & 1) ? sr : cr;
-  s = (quad & 2) ? -ss : ss;
-  c = ((quad + 1) & 2) ? -cc : cc;
-}
 
 // Value of `v` held by lane `src` of this wave.
 __device__ __forceinline__ float at_shfl(float v, int src) {
@@ -107,7 +87,7 @@ __device__ __forceinline__ void at_load_tables(const AtArgs& a, int* s_tab) {
     const int an = min(max(a.p2p[i], 0), a.half - 1);
     s_tab[i] = pp | (an << 8) | ((a.sgn[i] < 0.f ? 1 : 0) << 16) | ((pp != p ? 1 : 0) << 17);
   }
-  __syncthreads();
+  mg_sincos_setup();  // ends in the barrier that also publishes s_tab
 }
 
 struct AtRound {
@@ -178,7 +158,7 @@ __device__ __forceinline__ float at_rounds_fwd(const AtArgs& a, const int* s_tab
   for (int r = 0; r < a.R; ++r) {
     const AtRound q = at_round(s_tab, a.k, r, L.p, L.base);
     float s = 0.f, c = 1.f;
-    if (L.ok) at_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
+    if (L.ok) mg_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
     const float vp = at_shfl(v, q.partner);
     if (q.act) v = fmaf(c, v, q.sg * s * vp);
   }
@@ -210,7 +190,7 @@ __global__ __launch_bounds__(AT_THREADS) void angle_tables_fwd_reduce(AtArgs a) 
     for (int r = 0; r < a.R; ++r) {
       const AtRound q = at_round(s_tab, K, r, L.p, L.base);
       float s = 0.f, c = 1.f;
-      if (L.ok) at_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
+      if (L.ok) mg_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
       const float cs = q.sg * s;
 #pragma unroll
       for (int j = 0; j <= K; ++j) {
@@ -308,7 +288,7 @@ __global__ __launch_bounds__(AT_THREADS) void angle_tables_bwd_reduce(AtArgs a) 
     for (int r = a.R - 1; r >= 0; --r) {
       const AtRound q = at_round(s_tab, K, r, L.p, L.base);
       float s = 0.f, c = 1.f;
-      if (L.ok) at_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
+      if (L.ok) mg_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
       const float yp = at_shfl(y, q.partner);
       if (q.act) y = fmaf(c, y, -q.sg * s * yp);
     }
@@ -384,7 +364,7 @@ __global__ __launch_bounds__(AT_THREADS) void angle_tables_bwd_final(AtArgs a) {
     for (int r = a.R - 1; r >= 0; --r) {
       const AtRound q = at_round(s_tab, K, r, L.p, L.base);
       float s = 0.f, c = 1.f;
-      if (L.ok) at_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
+      if (L.ok) mg_sincos(a.theta[(tk * a.R + r) * a.half + q.ang], s, c);
       // u holds u_r (after the rotation); recover u_{r-1} by the transposed rotation.
       const float up = at_shfl(u, q.partner);
       const float u_prev = q.act ? fmaf(c, u, -q.sg * s * up) : u;
