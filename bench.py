@@ -55,20 +55,34 @@ def _parse():
     return ap.parse_args()
 
 
-def _traffic(name: str):
-    """HBM bytes per C-ABI call (fetch + write) from the committed rocprof counter
-    summaries: lines ``traffic <workload>:<entry> <fetch bytes> <write bytes>`` in
-    ``profiles/*.md``; ``None`` when no summary covers ``name``."""
+def _profile_line(kind: str, name: str):
+    """Integers of the line ``<kind> <name> <int> ...`` in the committed rocprof
+    summaries ``profiles/*.md``; ``None`` when no summary has one."""
     import glob
     import re
 
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
         with open(path) as f:
             for line in f:
-                m = re.match(r"^traffic (\S+) (\d+) (\d+)\s*$", line)
+                m = re.match(rf"^{kind} (\S+)((?: \d+)+)\s*$", line)
                 if m and m.group(1) == name:
-                    return int(m.group(2)) + int(m.group(3))
+                    return [int(x) for x in m.group(2).split()]
     return None
+
+
+def _traffic(name: str):
+    """HBM bytes per C-ABI call (fetch + write) from the summaries' lines
+    ``traffic <workload>:<entry> <fetch bytes> <write bytes>``."""
+    v = _profile_line("traffic", name)
+    return None if v is None else v[0] + v[1]
+
+
+def _valu_floor_us(name: str):
+    """VALU issue floor of one C-ABI call, from the summaries' lines
+    ``valu <workload>:<entry> <wave64 VALU instructions per call>``: 4 cycles per
+    instruction over MI355X's 1024 SIMDs at 2.4 GHz."""
+    v = _profile_line("valu", name)
+    return None if v is None else v[0] * 4 / 1024 / 2400
 
 
 class Op:
@@ -683,6 +697,12 @@ def main():
         res, cpu_step, B = run_op(ops[key], torch, wl, dev, args.steps, args.warmup, hip_scans,
                                   headline=(key == HEADLINE))
         results[key] = res
+        floors = {e: _valu_floor_us(f"{key}:{e}") for e in res["kernels"]}
+        if floors and all(v is not None for v in floors.values()):
+            for e, fl in floors.items():
+                res["kernels"][e]["valu_floor_us"] = fl
+            res["valu_floor_ms"] = sum(floors.values()) / 1e3
+            res["frac_of_valu_floor"] = res["valu_floor_ms"] / res["ms_per_step"]
         print(f"# {key}: {res['tokens_per_s']:.4g} tok/s, {res['ms_per_step']:.3f} ms/step, "
               f"{res['achieved_TBs']:.3f} TB/s ({100 * res['frac_of_hbm_peak']:.1f}% of peak)",
               file=sys.stderr, flush=True)

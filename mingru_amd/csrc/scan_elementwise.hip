@@ -17,7 +17,11 @@
 //     owns TSUB consecutive steps and keeps all its inputs in registers;
 //   * per thread: local affine aggregate -> LDS combine across waves ->
 //     look-back over earlier chunks (wave 0) -> final recompute from the carry
-//     and streaming stores.
+//     and streaming stores;
+//   * small problems (few chunks per sequence, inputs that stay cached) run the
+//     log and gate scans as two launches over the same grid instead: chunk
+//     aggregates, then every chunk folds its predecessors' aggregates itself
+//     (EW_REDUCE / EW_FINAL), so no workgroup waits on another.
 // The backward is the same machinery run in reverse time order over the
 // adjoint recurrence y_t = a_t (g_t + y_{t+1}); forward values needed for the
 // gradient (A_{t-1}, Bc_{t-1} or h_{t-1}) are recomputed from one saved
@@ -47,6 +51,21 @@ constexpr int GATE_TSUB_BWD = 4;
 constexpr int GATE_TSUB_FWD_NARROW = 8;
 // Workgroups a launch needs before it runs 4 columns per lane: one per CU.
 constexpr int64_t EW_FILL_WGS = 256;
+
+// Launch forms of the chunked scans.  EW_LOOKBACK is one launch whose
+// workgroups combine chunk carries by decoupled look-back.  A small problem
+// instead runs two launches over the same grid: EW_REDUCE stores every chunk's
+// aggregate map (the first chunk's with the sequence seed folded in), and
+// EW_FINAL folds the stored aggregates of all a chunk's predecessors -- at most
+// EW_FINAL_MAX_CHUNKS - 1, loaded a few per wave at once, so nothing waits on
+// another workgroup -- then recomputes the chunk from its carry.  The second
+// launch re-reads the inputs; the same grid puts each chunk on the XCD whose L2
+// the first launch filled with them, and EW_TWO_LAUNCH_BYTES keeps them there.
+// At B=4, T=1024, D=256 a sequence is 16 chunks, and the look-back walks them
+// one round trip after another.
+enum : int { EW_LOOKBACK = 0, EW_REDUCE = 1, EW_FINAL = 2 };
+constexpr int EW_FINAL_MAX_CHUNKS = 32;
+constexpr int64_t EW_TWO_LAUNCH_BYTES = (int64_t)32 << 20;  // input bytes of both launches
 
 // Affine map y -> p*y + l (NL independent offsets sharing one slope).  The
 // look-back machinery below moves any map type that names its NF fp32 fields
@@ -175,18 +194,19 @@ __device__ __forceinline__ XAff compose(const XAff& inner, const XAff& outer) {
   return XAff{xf_norm(xf_mul(outer.p, inner.p)), xf_norm(xf_fma(outer.p, inner.l, outer.l))};
 }
 
-// Data streams are read and written once: non-temporal accesses.
-template <int VEC>
+// Data streams are read and written once: non-temporal accesses.  NT = false
+// for a read that a later launch repeats (EW_REDUCE), so the lines stay cached.
+template <int VEC, bool NT = true>
 __device__ __forceinline__ void load_vec(float (&dst)[VEC], const float* __restrict__ src) {
   if constexpr (VEC == 4) {
-    const float4 v = mg_ld_stream4(src);
+    const float4 v = NT ? mg_ld_stream4(src) : *reinterpret_cast<const float4*>(src);
     dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
   } else if constexpr (VEC == 2) {
-    const float2 v = mg_ld_stream2(src);
+    const float2 v = NT ? mg_ld_stream2(src) : *reinterpret_cast<const float2*>(src);
     dst[0] = v.x; dst[1] = v.y;
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) dst[i] = mg_ld_stream(src + i);
+    for (int i = 0; i < VEC; ++i) dst[i] = NT ? mg_ld_stream(src + i) : src[i];
   }
 }
 
@@ -237,26 +257,80 @@ __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, i
   return ok;
 }
 
-// Intra-workgroup combine + decoupled look-back.  On return `carry` holds, for
-// this thread's columns, the composition of everything before (forward) or
-// after (REVERSE) this thread's sub-chunk.  `seed` is the map applied at the
-// sequence start (forward) or end (reverse).
-template <typename Map, int VEC, int WAVES, bool REVERSE>
+// Stored chunk aggregates of the two-launch form: plain floats laid out like
+// the look-back slots, [lg][chunk][field][VEC][64 lanes].
+template <typename Map, int VEC>
+__device__ __forceinline__ void agg_store(float* base, const EwGeom& g, int lg, int c, int lane,
+                                          const Map (&x)[VEC]) {
+  constexpr int TILE = MG_WAVE * VEC;
+  float* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
+#pragma unroll
+  for (int v = 0; v < VEC; ++v)
+#pragma unroll
+    for (int f = 0; f < Map::NF; ++f) p[f * TILE + v * MG_WAVE] = x[v].get(f);
+}
+
+template <typename Map, int VEC>
+__device__ __forceinline__ void agg_load(const float* base, const EwGeom& g, int lg, int c,
+                                         int lane, Map (&x)[VEC]) {
+  constexpr int TILE = MG_WAVE * VEC;
+  const float* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
+#pragma unroll
+  for (int v = 0; v < VEC; ++v)
+#pragma unroll
+    for (int f = 0; f < Map::NF; ++f) x[v].set(f, p[f * TILE + v * MG_WAVE]);
+}
+
+// Intra-workgroup combine + the carry from earlier chunks: decoupled look-back
+// (PH = EW_LOOKBACK) or the stored aggregates of the two-launch form (PH =
+// EW_FINAL; PH = EW_REDUCE only stores this chunk's aggregate and leaves
+// `carry` unset).  On return `carry` holds, for this thread's columns, the
+// composition of everything before (forward) or after (REVERSE) this thread's
+// sub-chunk.  `seed` is the map applied at the sequence start (forward) or end
+// (reverse).
+template <typename Map, int VEC, int WAVES, bool REVERSE, int PH = EW_LOOKBACK>
 __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed)[VEC],
                                          const EwGeom& g, int lg, int c, unsigned* header,
                                          unsigned epoch, mg_slot_t* agg_data,
                                          mg_slot_t* incl_data, Map (&carry)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
   constexpr int NF = Map::NF;
+  constexpr int PER = EW_FINAL_MAX_CHUNKS / WAVES;  // predecessors per wave (EW_FINAL)
+  static_assert(EW_FINAL_MAX_CHUNKS % WAVES == 0, "predecessors split evenly over the waves");
   __shared__ float s_agg[WAVES][NF][TILE];
-  __shared__ float s_carry[NF][TILE];
+  __shared__ float s_carry[PH == EW_FINAL ? WAVES : 1][NF][TILE];
   const int lane = threadIdx.x & (MG_WAVE - 1);
   const int w = threadIdx.x / MG_WAVE;
+  const int first = REVERSE ? g.n_chunks - 1 : 0;
 
 #pragma unroll
   for (int v = 0; v < VEC; ++v)
 #pragma unroll
     for (int f = 0; f < NF; ++f) s_agg[w][f][v * MG_WAVE + lane] = loc[v].get(f);
+  if constexpr (PH == EW_FINAL) {
+    // Wave w folds predecessors w*PER .. w*PER+PER-1 in application order
+    // (forward: chunks 0, 1, ...; reverse: chunks n-1, n-2, ...), all its loads
+    // issued before the first compose.
+    const float* stored = reinterpret_cast<const float*>(agg_data);
+    const int npred = REVERSE ? g.n_chunks - 1 - c : c;
+    Map X[PER][VEC];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int k = w * PER + i;
+      if (k < npred) agg_load<Map, VEC>(stored, g, lg, REVERSE ? g.n_chunks - 1 - k : k, lane, X[i]);
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      // Only wave 0 holds the seed; it matters only to the first chunk, which has
+      // no predecessors.
+      Map part = (w == 0 && c == first) ? seed[v] : Map::identity();
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (w * PER + i < npred) part = compose(part, X[i][v]);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) s_carry[w][f][v * MG_WAVE + lane] = part.get(f);
+    }
+  }
   __syncthreads();
 
   auto wave_agg = [&](int j, int v) {
@@ -265,6 +339,23 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
     for (int f = 0; f < NF; ++f) r.set(f, s_agg[j][f][v * MG_WAVE + lane]);
     return r;
   };
+
+  if constexpr (PH == EW_REDUCE) {
+    if (w == 0) {
+      Map G[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        G[v] = c == first ? seed[v] : Map::identity();
+        if (!REVERSE) {
+          for (int j = 0; j < WAVES; ++j) G[v] = compose(G[v], wave_agg(j, v));
+        } else {
+          for (int j = WAVES - 1; j >= 0; --j) G[v] = compose(G[v], wave_agg(j, v));
+        }
+      }
+      agg_store<Map, VEC>(reinterpret_cast<float*>(agg_data), g, lg, c, lane, G);
+    }
+    return;
+  }
 
   // Exclusive prefix of this wave inside the workgroup.
   Map ew[VEC];
@@ -276,6 +367,22 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
     } else {
       for (int j = WAVES - 1; j > w; --j) ew[v] = compose(ew[v], wave_agg(j, v));
     }
+  }
+
+  if constexpr (PH == EW_FINAL) {
+    // The partials in order; the first chunk's stored aggregate carries the seed.
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      Map E = Map::identity();
+      for (int j = 0; j < WAVES; ++j) {
+        Map P;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) P.set(f, s_carry[j][f][v * MG_WAVE + lane]);
+        E = compose(E, P);
+      }
+      carry[v] = compose(E, ew[v]);
+    }
+    return;
   }
 
   if (w == 0) {
@@ -331,14 +438,14 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
 #pragma unroll
     for (int v = 0; v < VEC; ++v)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) s_carry[f][v * MG_WAVE + lane] = E[v].get(f);
+      for (int f = 0; f < NF; ++f) s_carry[0][f][v * MG_WAVE + lane] = E[v].get(f);
   }
   __syncthreads();
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     Map C;
 #pragma unroll
-    for (int f = 0; f < NF; ++f) C.set(f, s_carry[f][v * MG_WAVE + lane]);
+    for (int f = 0; f < NF; ++f) C.set(f, s_carry[0][f][v * MG_WAVE + lane]);
     carry[v] = compose(C, ew[v]);
   }
 }
@@ -351,13 +458,21 @@ struct EwThread {
   bool col_ok;
 };
 
-template <int VEC, int TSUB, int WAVES, bool REVERSE>
+template <int VEC, int TSUB, int WAVES, bool REVERSE, int PH = EW_LOOKBACK>
 __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header) {
   EwThread th;
-  const MgTicket tk = mg_take_ticket(header);
-  th.valid = tk.ticket < gridDim.x;
-  const unsigned ticket = th.valid ? tk.ticket : 0u;
-  th.epoch = tk.epoch;
+  unsigned ticket;
+  if constexpr (PH == EW_LOOKBACK) {
+    const MgTicket tk = mg_take_ticket(header);
+    th.valid = tk.ticket < gridDim.x;
+    ticket = th.valid ? tk.ticket : 0u;
+    th.epoch = tk.epoch;
+  } else {
+    // No workgroup waits on another: the workgroup index is the chunk order.
+    th.valid = true;
+    ticket = blockIdx.x;
+    th.epoch = 0u;
+  }
   th.lane = threadIdx.x & (MG_WAVE - 1);
   th.w = threadIdx.x / MG_WAVE;
   int k = (int)(ticket / (unsigned)g.n_lg);
@@ -551,21 +666,22 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
 constexpr int LOG_TSUB = 8;
 constexpr int LOG_WAVES = 8;
 
-template <int VEC>
+template <int VEC, bool NT = true>
 __device__ __forceinline__ void load_xf_exp(Xf (&dst)[VEC], const float* __restrict__ src) {
   float x[VEC];
-  load_vec<VEC>(x, src);
+  load_vec<VEC, NT>(x, src);
 #pragma unroll
   for (int v = 0; v < VEC; ++v) dst[v] = xf_exp(x[v]);
 }
 
-template <int VEC, int WAVES>
+template <int VEC, int WAVES, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
     const float* __restrict__ lc, const float* __restrict__ lv, float* __restrict__ h,
     float* __restrict__ hstate, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  constexpr bool NT = PH != EW_REDUCE;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -575,8 +691,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
   for (int s = 0; s < TSUB; ++s) {
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
-      load_xf_exp<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
-      load_xf_exp<VEC>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+      load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
+      load_xf_exp<VEC, NT>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -604,8 +720,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
 #pragma unroll
     for (int v = 0; v < VEC; ++v) seed[v].l = h0[v];
   }
-  ew_carry<XAff, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                    incl_data, carry);
+  ew_carry<XAff, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                        incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
 
   Xf L[VEC];
 #pragma unroll
@@ -635,14 +752,15 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
   }
 }
 
-template <int VEC, int WAVES>
+template <int VEC, int WAVES, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     const float* __restrict__ lc, const float* __restrict__ lv, const float* __restrict__ h,
     const float* __restrict__ hstate, const float* __restrict__ gh, float* __restrict__ dlc,
     float* __restrict__ dlv, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  constexpr bool NT = PH != EW_REDUCE;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -654,9 +772,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
   for (int s = 0; s < TSUB; ++s) {
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
-      load_xf_exp<VEC>(av[s], lc + (th.bb * T + t) * D + th.col);
-      load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
-      load_vec<VEC>(gr[s], gh + (th.bb * T + t) * D + th.col);
+      load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
+      if constexpr (PH != EW_REDUCE) load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+      load_vec<VEC, NT>(gr[s], gh + (th.bb * T + t) * D + th.col);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -681,8 +799,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     loc[v] = XAff{xf_norm(P), xf_norm(L)};
     seed[v] = XAff::identity();
   }
-  ew_carry<XAff, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                   incl_data, carry);
+  ew_carry<XAff, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                       incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
 
   // Total adjoint x_s of every step; y ends as a_{t0} x_{t0}.
   Xf x[TSUB][VEC], y[VEC];
@@ -764,12 +883,13 @@ constexpr int gate_inputs() {
   return G == GATE_MINGRU ? 2 : 3;
 }
 
-template <int VEC, int TSUB, int WAVES, int G>
+template <int VEC, int TSUB, int WAVES, int G, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
     const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  constexpr bool NT = PH != EW_REDUCE;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -781,9 +901,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
       float x0[VEC], x1[VEC], x2[VEC];
-      load_vec<VEC>(x0, p0 + off);
-      load_vec<VEC>(x1, p1 + off);
-      if constexpr (gate_inputs<G>() == 3) load_vec<VEC>(x2, p2 + off);
+      load_vec<VEC, NT>(x0, p0 + off);
+      load_vec<VEC, NT>(x1, p1 + off);
+      if constexpr (gate_inputs<G>() == 3) load_vec<VEC, NT>(x2, p2 + off);
 #pragma unroll
       for (int v = 0; v < VEC; ++v)
         gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
@@ -812,8 +932,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
 #pragma unroll
     for (int v = 0; v < VEC; ++v) seed[v].l[0] = G == GATE_MINGRU ? expf(x[v]) : x[v];
   }
-  ew_carry<Aff<1>, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
-                                 carry);
+  ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                          incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
   float L[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) L[v] = carry[v].l[0];
@@ -830,18 +951,19 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
 // da = x h_{t-1}, db = x, dh0 = a_1 x_1, through the gate derivatives.  Per step
 // the kernel keeps the adjoint and three gate values:
 //   signed: sigmoid(z), tanh(s), hpre;   MinGRU: sigmoid(-k), sigmoid(k), hpre.
-template <int VEC, int TSUB, int WAVES, int G>
+template <int VEC, int TSUB, int WAVES, int G, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
     const float* __restrict__ h0, const float* __restrict__ h, const float* __restrict__ gh,
     float* __restrict__ d0, float* __restrict__ d1, float* __restrict__ d2,
     float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
   constexpr bool MIN = G == GATE_MINGRU;
+  constexpr bool NT = PH != EW_REDUCE;
 
   float ua[TSUB][VEC], ub[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
 #pragma unroll
@@ -850,10 +972,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
       float x0[VEC];
-      load_vec<VEC>(x0, p0 + off);
-      load_vec<VEC>(x[s], gh + off);
+      load_vec<VEC, NT>(x0, p0 + off);
+      load_vec<VEC, NT>(x[s], gh + off);
       if constexpr (MIN) {
-        load_vec<VEC>(hv[s], p1 + off);
+        if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p1 + off);
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           ua[s][v] = mg_sigmoid(-x0[v]);  // a
@@ -861,8 +983,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
         }
       } else {
         float x1[VEC];
-        load_vec<VEC>(x1, p1 + off);
-        load_vec<VEC>(hv[s], p2 + off);
+        load_vec<VEC, NT>(x1, p1 + off);
+        if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p2 + off);
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           ua[s][v] = mg_sigmoid(x1[v]);  // sigmoid(z)
@@ -913,8 +1035,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  ew_carry<Aff<1>, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
-                                carry);
+  ew_carry<Aff<1>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                         incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
   float y[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
@@ -1043,6 +1166,23 @@ int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... a
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 
+// The two-launch form (EW_REDUCE then EW_FINAL) for a problem of `arrays` input
+// arrays of B*T*D floats: few enough chunks per sequence for EW_FINAL's fold,
+// and inputs small enough to stay cached between the launches.
+bool ew_two_launch(const EwPlan& p, int64_t B, int64_t T, int64_t D, int arrays) {
+  return p.g.n_chunks <= EW_FINAL_MAX_CHUNKS &&
+         B * T * D * (int64_t)sizeof(float) * arrays <= EW_TWO_LAUNCH_BYTES;
+}
+
+// One look-back launch, or the reduce and final launches over the same grid.
+template <typename K0, typename K1, typename K2, typename... Args>
+int ew_run(bool two, K0 lookback, K1 reduce, K2 fin, const EwPlan& p, void* ws,
+           hipStream_t stream, Args... args) {
+  if (!two) return ew_launch(lookback, p, ws, stream, args...);
+  const int rc = ew_launch(reduce, p, ws, stream, args...);
+  return rc != MG_OK ? rc : ew_launch(fin, p, ws, stream, args...);
+}
+
 size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
   size_t m = 0;
   for (int vec : {1, 2, 4}) {
@@ -1094,7 +1234,11 @@ int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const flo
     constexpr int TS = V == 4 ? EW_TSUB_FWD : GATE_TSUB_FWD_NARROW;
     EwPlan p = ew_plan(B, T, D, V, TS, EW_WAVES_FWD, 1);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(gate_fwd_kernel<V, TS, EW_WAVES_FWD, G>, p, ws, stream, p0, p1, p2, h0, h);
+    return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>()),
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_REDUCE>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_FINAL>, p, ws, stream, p0, p1, p2, h0,
+                  h);
   });
 }
 
@@ -1162,8 +1306,11 @@ int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const flo
     constexpr int V = decltype(v)::value;
     EwPlan p = ew_plan(B, T, D, V, GATE_TSUB_BWD, GATE_WAVES_BWD, 1);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G>, p, ws, stream, p0, p1,
-                     p2, h0, h, gh, d0, d1, d2, dh0);
+    return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>() + 1),
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_REDUCE>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_FINAL>, p, ws, stream,
+                  p0, p1, p2, h0, h, gh, d0, d1, d2, dh0);
   });
 }
 
@@ -1308,7 +1455,9 @@ int mg_log_scan_fwd(const float* lc, const float* lv, float* h, float* hstate, i
     constexpr int V = decltype(v)::value;
     EwPlan p = ew_plan(B, T, D, V, LOG_TSUB, LOG_WAVES, 3);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(log_fwd_kernel<V, LOG_WAVES>, p, ws, stream, lc, lv, h, hstate);
+    return ew_run(ew_two_launch(p, B, T, D, 2), log_fwd_kernel<V, LOG_WAVES>,
+                  log_fwd_kernel<V, LOG_WAVES, EW_REDUCE>, log_fwd_kernel<V, LOG_WAVES, EW_FINAL>,
+                  p, ws, stream, lc, lv, h, hstate);
   };
   return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});
 }
@@ -1322,8 +1471,9 @@ int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const floa
     constexpr int V = decltype(v)::value;
     EwPlan p = ew_plan(B, T, D, V, LOG_TSUB, LOG_WAVES, 3);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(log_bwd_kernel<V, LOG_WAVES>, p, ws, stream, lc, lv, h, hstate, gh, dlc,
-                     dlv);
+    return ew_run(ew_two_launch(p, B, T, D, 3), log_bwd_kernel<V, LOG_WAVES>,
+                  log_bwd_kernel<V, LOG_WAVES, EW_REDUCE>, log_bwd_kernel<V, LOG_WAVES, EW_FINAL>,
+                  p, ws, stream, lc, lv, h, hstate, gh, dlc, dlv);
   };
   return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});
 }

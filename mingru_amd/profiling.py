@@ -16,6 +16,8 @@ Usage (on the directories the rocprofv3 runs wrote)::
   device-to-device copy in the same run, so the figures are HBM bytes.
 * ``--counters``: further ``--pmc`` directories; their counters are tabulated per
   kernel (average per dispatch).
+* ``--valu``: a ``--pmc`` directory with ``SQ_INSTS_VALU``; adds each call's VALU issue
+  floor (``valu`` lines, read by ``bench.py``).
 * ``--bench``: the JSON line ``bench.py`` printed, for the HIP-event timings.
 
 Kernels are attributed to C-ABI entry points by name (``ENTRIES``), independent of
@@ -45,13 +47,25 @@ ENTRIES = {
     "C1": [("mg_log_scan_fwd", r"\blog_fwd_kernel<"), ("mg_log_scan_bwd", r"\blog_bwd_kernel<")],
     "C3": [("mg_affine_scan_fwd", r"\baffine_fwd_kernel<2, 1,"),
            ("mg_affine_scan_bwd", r"\baffine_bwd_kernel<2, 1,")],
-    "C4": [("mg_angle_scan_fwd", r"\bangle_fwd_\w+<"), ("mg_angle_scan_bwd", r"\bangle_bwd_\w+<")],
+    "C4": [("mg_angle_scan_fwd", r"\bangle_fwd_\w+<|\bangle_group_\w+<\d+, false>"),
+           ("mg_angle_scan_bwd", r"\bangle_bwd_\w+<|\bangle_group_\w+<\d+, true>")],
     "C5": [("mg_delta_fwd", r"\bdwb_fwd_\w+<false>"), ("mg_delta_bwd", r"\bdwb_bwd_\w+<false>")],
     "C5d": [("mg_delta_gated_fwd", r"\bdwb_fwd_\w+<true>"),
             ("mg_delta_gated_bwd", r"\bdwb_bwd_\w+<true>")],
 }
 
 COPY_PROBE_BYTES = 1 << 30  # bench.py --copy-probe: one 1 GiB device-to-device copy
+
+# VALU issue floor: a wave64 fp32 VALU instruction occupies a 16-lane SIMD for 4
+# cycles; MI355X has 256 CUs x 4 SIMDs at a 2.4 GHz peak engine clock.
+VALU_CYCLES_PER_INST = 4
+SIMDS = 1024
+CLOCK_MHZ = 2400
+
+
+def valu_floor_us(wave_insts: float) -> float:
+    """Time the SIMDs need just to issue `wave_insts` wave64 VALU instructions."""
+    return wave_insts * VALU_CYCLES_PER_INST / SIMDS / CLOCK_MHZ
 
 
 def short_name(name: str) -> str:
@@ -93,6 +107,15 @@ def copy_scale(per_kernel: dict) -> float:
     if not vals:
         raise SystemExit("no copy-probe dispatch in the counter run (run bench.py --copy-probe)")
     return COPY_PROBE_BYTES / (statistics.median(vals) * 1024)
+
+
+def entry_sum(per_kernel: dict, pattern: str, what: str) -> float:
+    """Counter per call of one entry point: per-kernel dispatch averages, summed."""
+    rx = re.compile(pattern)
+    hits = {k: v for k, v in per_kernel.items() if rx.search(k)}
+    if not hits:
+        raise SystemExit(f"{what}: no dispatch matches {pattern!r}")
+    return sum(sum(v) / len(v) for v in hits.values())
 
 
 def entry_bytes(per_kernel: dict, pattern: str, scale: float, what: str) -> float:
@@ -193,6 +216,28 @@ def summarize(args) -> str:
         traffic.append(f"traffic {args.workload}:{entry} {int(f)} {int(w)}")
     L += ["", "Machine-readable lines read by `bench.py` "
           "(`traffic <workload>:<entry> <fetch bytes> <write bytes>`):", "", "```", *traffic, "```"]
+    if args.valu:
+        insts = read_counters(args.valu).get("SQ_INSTS_VALU")
+        if not insts:
+            raise SystemExit(f"{args.valu}: no SQ_INSTS_VALU counter")
+        L += ["", "## VALU issue floor per C-ABI call (`SQ_INSTS_VALU`)", "",
+              f"Wave64 VALU instructions per call (per-kernel dispatch averages, summed) times "
+              f"{VALU_CYCLES_PER_INST} cycles each, spread over {SIMDS} SIMDs at {CLOCK_MHZ} MHz: "
+              "the time the SIMDs need only to issue them.", "",
+              "| entry point | VALU wave instructions | floor µs | measured µs | share of floor |",
+              "|---|---:|---:|---:|---:|"]
+        lines = []
+        for entry, pat in entries:
+            n = entry_sum(insts, pat, f"{args.workload}:{entry} SQ_INSTS_VALU")
+            fl = valu_floor_us(n)
+            meas = ops.get("kernels", {}).get(entry, {}).get("avg_us")
+            L.append(f"| `{entry}` | {n:.4g} | {fl:.1f} | "
+                     f"{'—' if meas is None else f'{meas:.1f}'} | "
+                     f"{'—' if not meas else f'{100 * fl / meas:.0f}%'} |")
+            lines.append(f"valu {args.workload}:{entry} {int(n)}")
+        L += ["", "Machine-readable lines read by `bench.py` "
+              "(`valu <workload>:<entry> <VALU wave instructions per call>`):", "", "```",
+              *lines, "```"]
     if args.counters:
         L += ["", "## Issue and memory counters per kernel (average per dispatch)", "",
               *counter_table(args.counters, [p for _, p in entries])]
@@ -211,6 +256,8 @@ def main(argv=None):
     ap.add_argument("--write", required=True)
     ap.add_argument("--bench", required=True)
     ap.add_argument("--counters", nargs="*", default=[])
+    ap.add_argument("--valu", default=None,
+                    help="a --pmc run with SQ_INSTS_VALU: adds the VALU issue floor per call")
     ap.add_argument("--command", action="append", default=[])
     ap.add_argument("--out", required=True)
     args = ap.parse_args(argv)

@@ -92,6 +92,44 @@ def test_profile_summary_attributes_traffic(tmp_path):
     assert "traffic C2:mg_linear_scan_fwd 409600 10240" in text
     assert "traffic C2:mg_linear_scan_bwd 102400 20480" in text
     assert "ew_fwd_kernel<4, 16, 8>" in text and "rocprofv3 x" in text
+    _write_counters(tmp_path / "v", "SQ_INSTS_VALU", [(fwd, 1000.0), (fwd, 3000.0), (bwd, 614400.0)])
+    profiling.main(base + ["--valu", str(tmp_path / "v")])
+    text = out.read_text()
+    # per-call averages: fwd 2000, bwd 614400 wave instructions; the bwd floor is
+    # 614400 * 4 cycles / 1024 SIMDs / 2400 MHz = 1.0 us
+    assert "valu C2:mg_linear_scan_fwd 2000" in text
+    assert "valu C2:mg_linear_scan_bwd 614400" in text
+    assert profiling.valu_floor_us(614400) == pytest.approx(1.0)
     _write_counters(tmp_path / "w", "WRITE_SIZE", [(copy, 1048576.0), (fwd, 10.0)])
     with pytest.raises(SystemExit, match="linear_bwd"):
         profiling.main(base)
+
+
+def test_profile_entry_patterns_split_angle_walk_kernels():
+    """The angle scan's walk kernels are attributed by their direction argument."""
+    import re
+
+    fwd, bwd = (p for _, p in profiling.ENTRIES["C4"])
+    for name in ("angle_fwd_reduce<8, 1, false, true>", "angle_fwd_scan<8>",
+                 "angle_group_compose<8, false>", "angle_group_fill<8, false>"):
+        assert re.search(fwd, name) and not re.search(bwd, name), name
+    for name in ("angle_bwd_final<8, 1, false, true>", "angle_bwd_scan<8>",
+                 "angle_group_compose<8, true>", "angle_group_fill<8, true>"):
+        assert re.search(bwd, name) and not re.search(fwd, name), name
+
+
+def test_bench_reads_profile_lines(tmp_path, monkeypatch):
+    """bench.py takes traffic and the VALU floor from the committed summaries' lines."""
+    import importlib
+    import sys
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    bench = importlib.import_module("bench")
+    (tmp_path / "profiles").mkdir()
+    (tmp_path / "profiles" / "x.md").write_text(
+        "text\n```\ntraffic C4:mg_angle_scan_fwd 300 200\nvalu C4:mg_angle_scan_fwd 614400\n```\n")
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    assert bench._traffic("C4:mg_angle_scan_fwd") == 500
+    assert bench._valu_floor_us("C4:mg_angle_scan_fwd") == pytest.approx(1.0)
+    assert bench._traffic("C4:mg_angle_scan_bwd") is None
+    assert bench._valu_floor_us("C2:mg_linear_scan_fwd") is None

@@ -138,8 +138,13 @@ def _run_log(lc, lv, gh, cuda):
     return h, lcg.grad, lvg.grad
 
 
-LOG_SHAPES = [(1, 1, 1), (2, 7, 5), (3, 64, 64), (2, 200, 130), (4, 1024, 256), (1, 2049, 512),
-              (8, 2048, 512), (32, 1024, 128)]
+# Launch forms (64-step chunks): up to 32 chunks per sequence and 32 MB of inputs run
+# as two launches (chunk aggregates, then every chunk folds its predecessors'), the
+# rest as one look-back launch.  (2, 2048, 64) is the longest two-launch sequence and
+# (2, 2049, 64) / (1, 2049, 512) the shortest look-back ones; (8, 2048, 512) and
+# (32, 1024, 128) take the look-back form by size.
+LOG_SHAPES = [(1, 1, 1), (2, 7, 5), (3, 64, 64), (2, 200, 130), (4, 1024, 256), (2, 2048, 64),
+              (2, 2049, 64), (1, 2049, 512), (8, 2048, 512), (32, 1024, 128)]
 
 
 @pytest.mark.parametrize("shape", LOG_SHAPES)

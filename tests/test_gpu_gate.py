@@ -42,6 +42,10 @@ CASES = [
     (2, 65, 260, True),
     (8, 2048, 512, False),  # 4 columns per lane
     (32, 1024, 128, True),  # 2 columns per lane
+    # The backward's 32-step chunks: 32 per sequence still run as two launches,
+    # 33 as one look-back launch.
+    (2, 1024, 64, False),
+    (2, 1025, 64, True),
 ]
 
 

@@ -42,6 +42,10 @@ CASES = [
     (2, 129, 64, 30.0),  # saturated gates: z and g at 0/1, sigmoid(-k) underflowing
     (8, 2048, 512, 1.0),  # 4 columns per lane
     (32, 1024, 128, 2.0),  # 2 columns per lane
+    # The backward's 32-step chunks: 32 per sequence still run as two launches,
+    # 33 as one look-back launch.
+    (2, 1024, 64, 1.0),
+    (2, 1025, 64, 1.0),
 ]
 
 
