@@ -40,10 +40,11 @@ import statistics
 ENTRIES = {
     "C2": [("mg_linear_scan_fwd", r"\bew_fwd_kernel<"),
            ("mg_linear_scan_bwd", r"\blinear_bwd_kernel<")],
-    "C2g": [("mg_signed_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, [01]>"),
-            ("mg_signed_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, [01]>")],
-    "C1g": [("mg_mingru_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, 2>"),
-            ("mg_mingru_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, 2>")],
+    # gate kernels: <columns per lane, steps per wave, waves, gate kind[, launch form]>
+    "C2g": [("mg_signed_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, [01](, \d)?>"),
+            ("mg_signed_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, [01](, \d)?>")],
+    "C1g": [("mg_mingru_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, 2(, \d)?>"),
+            ("mg_mingru_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, 2(, \d)?>")],
     "C1": [("mg_log_scan_fwd", r"\blog_fwd_kernel<"), ("mg_log_scan_bwd", r"\blog_bwd_kernel<")],
     "C3": [("mg_affine_scan_fwd", r"\baffine_fwd_kernel<2, 1,"),
            ("mg_affine_scan_bwd", r"\baffine_bwd_kernel<2, 1,")],

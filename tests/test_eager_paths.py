@@ -106,8 +106,18 @@ def test_profile_summary_attributes_traffic(tmp_path):
 
 
 def test_profile_entry_patterns_split_angle_walk_kernels():
-    """The angle scan's walk kernels are attributed by their direction argument."""
+    """The angle scan's walk kernels are attributed by their direction argument, and the
+    gate kernels by their gate kind whatever their launch form."""
     import re
+
+    sfwd, sbwd = (p for _, p in profiling.ENTRIES["C2g"])
+    mfwd, mbwd = (p for _, p in profiling.ENTRIES["C1g"])
+    for name, pat, others in (("gate_fwd_kernel<4, 16, 8, 0>", sfwd, (sbwd, mfwd, mbwd)),
+                              ("gate_fwd_kernel<4, 16, 8, 1, 2>", sfwd, (sbwd, mfwd, mbwd)),
+                              ("gate_bwd_kernel<1, 4, 8, 0, 1>", sbwd, (sfwd, mfwd, mbwd)),
+                              ("gate_fwd_kernel<1, 8, 8, 2, 1>", mfwd, (sfwd, sbwd, mbwd)),
+                              ("gate_bwd_kernel<4, 4, 8, 2>", mbwd, (sfwd, sbwd, mfwd))):
+        assert re.search(pat, name) and not any(re.search(o, name) for o in others), name
 
     fwd, bwd = (p for _, p in profiling.ENTRIES["C4"])
     for name in ("angle_fwd_reduce<8, 1, false, true>", "angle_fwd_scan<8>",
