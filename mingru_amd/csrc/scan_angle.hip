@@ -66,6 +66,8 @@ constexpr int AN_WALK_RING = AN_WALK_AHEAD + 1;
 // (in parallel again).  Used once a sequence has more than AN_GROUP_MIN chunks.
 constexpr int AN_GROUP = 8;
 constexpr int AN_GROUP_MIN = 2 * AN_GROUP;
+// Up to this many groups the group walk and the fill run as one launch.
+constexpr int AN_WALKFILL_GROUPS = 16;
 
 constexpr int lex_first(int K, int r) {
   int i = 0;
@@ -968,6 +970,92 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_fill(AnArgs a, An
   }
 }
 
+// Group walk and fill in one launch, for at most AN_WALKFILL_GROUPS groups: each
+// team of K lanes (one per (block, group), lane i holding row i) forms its group's
+// entry value itself by applying every preceding group map -- forward from h0 over
+// groups 0 .. grp-1, backward from zero over groups n_groups-1 .. grp+1 -- with all
+// those maps loaded at once, then fills the group's chunk-entry values as
+// angle_group_fill does.  Group 0's backward team also writes dL/dh0.  The
+// redundant walks cost at most AN_WALKFILL_GROUPS - 1 matrix-vector steps per team
+// and save the separate group walk's launch.
+template <int K, bool BWD>
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_walk_fill(AnArgs a, AnGeom g,
+                                                                         const float* gp,
+                                                                         const float* gl,
+                                                                         int n_groups) {
+  constexpr int NP = AN_WALKFILL_GROUPS - 1;  // predecessor groups, at most
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int i = (int)(gt % K);
+  const int64_t gbk = gt / K;
+  const int64_t blk = gbk % g.NB;
+  const int grp = (int)(gbk / g.NB);
+  const bool ok = grp < n_groups;  // every lane stays for the partner reads
+  const int lane = threadIdx.x & (MG_WAVE - 1), base = lane - i;
+  const int npred = ok ? (BWD ? n_groups - 1 - grp : grp) : 0;
+  // Row i of each predecessor's map (backward: column i of the stored transposed
+  // map) and its offset, in the order they apply.
+  float GP[NP][K], GL[NP];
+#pragma unroll
+  for (int s = 0; s < NP; ++s) {
+    const int gq = BWD ? n_groups - 1 - s : s;
+    if (s < npred) {
+      const float* pg = gp + an_idx(g, gq, 0, K * K, blk);
+      if (BWD) {
+#pragma unroll
+        for (int q = 0; q < K; ++q) GP[s][q] = pg[q * K + i];
+      } else {
+        ld<K>(GP[s], pg + i * K);
+      }
+      GL[s] = gl[an_idx(g, gq, i, K, blk)];
+    } else {
+#pragma unroll
+      for (int q = 0; q < K; ++q) GP[s][q] = 0.f;
+      GL[s] = 0.f;
+    }
+  }
+  const int c0 = ok ? grp * AN_GROUP : 0;
+  const int c1 = ok ? min(c0 + AN_GROUP, g.n_chunks) - 1 : 0;
+  const int cnt = c1 - c0 + 1;
+  float P[AN_GROUP][K], L[AN_GROUP];
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    const int c = BWD ? c1 - min(s, cnt - 1) : c0 + min(s, cnt - 1);
+    const float* pc = a.prod + an_idx(g, c, 0, K * K, blk);
+    if (ok) {
+      if (BWD) {
+#pragma unroll
+        for (int q = 0; q < K; ++q) P[s][q] = pc[q * K + i];
+      } else {
+        ld<K>(P[s], pc + i * K);
+      }
+      L[s] = a.lsum[an_idx(g, c, i, K, blk)];
+    } else {
+#pragma unroll
+      for (int q = 0; q < K; ++q) P[s][q] = 0.f;
+      L[s] = 0.f;
+    }
+  }
+  float h = (ok && !BWD) ? a.h0[blk * K + i] : 0.f;
+#pragma unroll
+  for (int s = 0; s < NP; ++s) {
+    if (s < npred) {  // uniform across the team
+      float acc = GL[s];
+#pragma unroll
+      for (int q = 0; q < K; ++q) acc = fmaf(GP[s][q], __shfl(h, base + q), acc);
+      h = acc;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    if (ok && s < cnt) a.bound[an_idx(g, BWD ? c1 - s : c0 + s, i, K, blk)] = h;
+    float acc = L[s];
+#pragma unroll
+    for (int q = 0; q < K; ++q) acc = fmaf(P[s][q], __shfl(h, base + q), acc);
+    h = acc;
+  }
+  if (BWD && ok && grp == 0) a.dh0[blk * K + i] = h;  // the adjoint leaving chunk 0
+}
+
 // ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, AnGeom g) {
@@ -1105,6 +1193,11 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
     float* gb = (float*)(base + gm + gv);
     const dim3 cgrid((unsigned)((g.NB * ng * K + AN_WALK_THREADS - 1) / AN_WALK_THREADS));
     hipLaunchKernelGGL((angle_group_compose<K, BWD>), cgrid, sblock, 0, stream, a, g, gp, gl, ng);
+    if (ng <= AN_WALKFILL_GROUPS) {
+      hipLaunchKernelGGL((angle_group_walk_fill<K, BWD>), cgrid, sblock, 0, stream, a, g,
+                         (const float*)gp, (const float*)gl, ng);
+      return;
+    }
     // The walk kernels over the group maps: chunks -> groups.
     AnArgs ag = a;
     AnGeom gg = g;
