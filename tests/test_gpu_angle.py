@@ -87,6 +87,9 @@ BRICK_CASES = [
     (2, 300, 5, 8, 3, 0, 1),
     (1, 530, 3, 2, 1, 1, 1),
     (1, 260, 4, 4, 2, 0, 0),
+    # more than 16 groups of 8 chunks (T > 2048): the group walk and the fill as two
+    # launches instead of one
+    (1, 2200, 3, 4, 2, 0, 1),
 ]
 
 
@@ -100,7 +103,7 @@ def test_brick_schedule_matches_oracle(cuda, case):
 
 
 LEX_CASES = [(2, 33, 10, 8, 1), (1, 120, 64, 8, 1), (2, 45, 20, 4, 1), (2, 30, 66, 8, 0),
-             (1, 400, 6, 8, 1)]
+             (1, 400, 6, 8, 1), (1, 2100, 2, 8, 1)]
 
 
 @pytest.mark.parametrize("case", LEX_CASES)
