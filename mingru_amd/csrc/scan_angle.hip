@@ -119,26 +119,63 @@ __device__ __forceinline__ void rot_rows_t(float (&X)[K][NC], float c, float s) 
   }
 }
 
-// One round of the brick-wall schedule (planes given by the round parity).
+// One plane of a brick-wall round: (I, J) rotated, or its transpose applied.
+template <int K, int NC, bool TRANSPOSE, int I, int J>
+__device__ __forceinline__ void brick_plane(float (&X)[K][NC], float c, float s) {
+  if constexpr (TRANSPOSE) rot_rows_t<K, NC, I, J>(X, c, s);
+  else rot_rows<K, NC, I, J>(X, c, s);
+}
+
+// The K/2 planes of a round of parity PAR: (2m + PAR, 2m + PAR + 1 mod K).  A fold
+// over the plane index pack, with no lambda holding X, keeps X in registers when
+// the caller loops over rounds at run time.
+template <int K, int NC, bool TRANSPOSE, int PAR, int... M>
+__device__ __forceinline__ void brick_planes(float (&X)[K][NC], const float (&cs)[K / 2],
+                                             const float (&sn)[K / 2],
+                                             std::integer_sequence<int, M...>) {
+  (brick_plane<K, NC, TRANSPOSE, 2 * M + PAR, (2 * M + PAR + 1) % K>(X, cs[M], sn[M]), ...);
+}
+
+// Round r of the brick-wall schedule with its parity PAR fixed at compile time:
+// the round's K/2 angles read from th + r K/2 and its planes rotated (TRANSPOSE:
+// the transposed rotations).
+template <int K, int NC, bool TRANSPOSE, int PAR>
+__device__ __forceinline__ void brick_round_at(float (&X)[K][NC], const float* __restrict__ th,
+                                               int r) {
+  constexpr int H = K / 2;
+  float ang[H], cs[H], sn[H];
+  ld<H>(ang, th + r * H);
+#pragma unroll
+  for (int m = 0; m < H; ++m) mg_sincos(ang[m], sn[m], cs[m]);
+  brick_planes<K, NC, TRANSPOSE, PAR>(X, cs, sn, std::make_integer_sequence<int, H>{});
+}
+
+// All `rounds` rounds of a token: 0 .. rounds-1 in order, or (TRANSPOSE) their
+// transposes from rounds-1 down to 0.  Two rounds per iteration, even then odd
+// (transposed: odd then even), so that no branch inside the loop depends on a
+// round's parity: with one, the fwd reduce pass's state block [P | L] was kept in
+// scratch memory instead of registers.
 template <int K, int NC, bool TRANSPOSE>
-__device__ __forceinline__ void brick_round(float (&X)[K][NC], int r, const float (&cs)[K / 2],
-                                            const float (&sn)[K / 2]) {
-  if ((r & 1) == 0) {
-    static_for(
-        [&](auto m) {
-          constexpr int I = 2 * decltype(m)::value, J = I + 1;
-          if (TRANSPOSE) rot_rows_t<K, NC, I, J>(X, cs[decltype(m)::value], sn[decltype(m)::value]);
-          else rot_rows<K, NC, I, J>(X, cs[decltype(m)::value], sn[decltype(m)::value]);
-        },
-        std::make_index_sequence<K / 2>{});
+__device__ __forceinline__ void brick_rounds(float (&X)[K][NC], const float* __restrict__ th,
+                                             int rounds) {
+  if constexpr (!TRANSPOSE) {
+    int r = 0;
+    for (; r + 2 <= rounds; r += 2) {
+      brick_round_at<K, NC, false, 0>(X, th, r);
+      brick_round_at<K, NC, false, 1>(X, th, r + 1);
+    }
+    if (r < rounds) brick_round_at<K, NC, false, 0>(X, th, r);
   } else {
-    static_for(
-        [&](auto m) {
-          constexpr int I = 2 * decltype(m)::value + 1, J = (I + 1) % K;
-          if (TRANSPOSE) rot_rows_t<K, NC, I, J>(X, cs[decltype(m)::value], sn[decltype(m)::value]);
-          else rot_rows<K, NC, I, J>(X, cs[decltype(m)::value], sn[decltype(m)::value]);
-        },
-        std::make_index_sequence<K / 2>{});
+    int r = rounds - 1;
+    if (r >= 1 && (r & 1)) {  // the last round is odd: it goes first
+      brick_round_at<K, NC, true, 1>(X, th, r);
+      --r;
+    }
+    for (; r >= 2; r -= 2) {  // r even
+      brick_round_at<K, NC, true, 0>(X, th, r);
+      brick_round_at<K, NC, true, 1>(X, th, r - 1);
+    }
+    if (r == 0) brick_round_at<K, NC, true, 0>(X, th, 0);
   }
 }
 
@@ -163,14 +200,7 @@ __device__ __forceinline__ void apply_M(float (&X)[K][NC], const float* __restri
         },
         std::make_index_sequence<R>{});
   } else {
-    constexpr int H = K / 2;
-    for (int r = 0; r < rounds; ++r) {
-      float ang[H], cs[H], sn[H];
-      ld<H>(ang, th + r * H);
-#pragma unroll
-      for (int m = 0; m < H; ++m) mg_sincos(ang[m], sn[m], cs[m]);
-      brick_round<K, NC, false>(X, r, cs, sn);
-    }
+    brick_rounds<K, NC, false>(X, th, rounds);
   }
   if (HD) {
 #pragma unroll
@@ -253,14 +283,7 @@ __device__ __forceinline__ void apply_Mt(float (&X)[K][NC], const float* __restr
         },
         std::make_index_sequence<R>{});
   } else {
-    constexpr int H = K / 2;
-    for (int r = rounds - 1; r >= 0; --r) {
-      float ang[H], cs[H], sn[H];
-      ld<H>(ang, th + r * H);
-#pragma unroll
-      for (int m = 0; m < H; ++m) mg_sincos(ang[m], sn[m], cs[m]);
-      brick_round<K, NC, true>(X, r, cs, sn);
-    }
+    brick_rounds<K, NC, true>(X, th, rounds);
   }
   if (HS) {
 #pragma unroll
@@ -684,13 +707,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
     st<R>(dth, gr);  // partial-line rows: L2 merges them (no streaming hint)
   } else {
     constexpr int H = K / 2;
-    for (int r = 0; r < rounds; ++r) {
-      float ang[H], cs[H], sn[H];
-      ld<H>(ang, th + r * H);
-#pragma unroll
-      for (int m = 0; m < H; ++m) mg_sincos(ang[m], sn[m], cs[m]);
-      brick_round<K, 1, false>(v, r, cs, sn);
-    }
+    brick_rounds<K, 1, false>(v, th, rounds);
     if (HD) {
       float acc = 0.f;
 #pragma unroll
