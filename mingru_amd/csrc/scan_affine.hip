@@ -1,5 +1,6 @@
 // Block-matrix affine scans: matrix_scan (k=2, v=1) and matrix_affine_scan
-// (k in {1,2,4,8}, v in {1,2,4,8,16}), fwd + bwd.
+// (k in {1,2,4,8,16}, v in {1,2,4,8,16}), fwd + bwd.  The kernels below take
+// k <= 4; 8x8 and 16x16 blocks run on the matrix cores (scan_affine_mfma.hip).
 //
 // Recurrence per plane (reference src/mingru/min_gru.py:1513-1655):
 //   Abar_t = A_t Abar_{t-1},  Bbar_t = A_t Bbar_{t-1} + B_t,  Abar_0 = I, Bbar_0 = 0.
@@ -15,9 +16,9 @@
 // (P, L): S -> P S + L of each chunk.  Inside a workgroup the waves combine
 // their sub-chunk maps through one LDS buffer in time order.
 //
-// For k <= 2 every input of the thread's sub-chunk stays in registers between
-// the aggregate pass and the final pass (one HBM read).  For k >= 4 the
-// register file cannot hold them: inputs are re-read for the final pass and
+// For k <= 2 with at most two offset columns every input of the thread's
+// sub-chunk stays in registers between the aggregate pass and the final pass
+// (one HBM read).  Otherwise the register file cannot hold them: inputs are re-read for the final pass and
 // the backward reads the saved forward outputs Abar_{t-1}, Bbar_{t-1}.
 #include "mg_affm.h"
 
@@ -485,12 +486,7 @@ int af_launch_bwd(const float* A, const float* Bm, const float* Abar, const floa
     case 404: return FN<4, 4>(__VA_ARGS__);                        \
     case 408: return FN<4, 8>(__VA_ARGS__);                        \
     case 416: return FN<4, 16>(__VA_ARGS__);                       \
-    case 801: return FN<8, 1>(__VA_ARGS__);                        \
-    case 802: return FN<8, 2>(__VA_ARGS__);                        \
-    case 804: return FN<8, 4>(__VA_ARGS__);                        \
-    case 808: return FN<8, 8>(__VA_ARGS__);                        \
-    case 816: return FN<8, 16>(__VA_ARGS__);                       \
-    default: return MG_ERR_ARG;                                    \
+    default: return MG_ERR_ARG; /* k >= 8 runs on the matrix cores */ \
   }
 
 }  // namespace
@@ -503,8 +499,7 @@ size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, in
   switch (k) {
     case 1: return af_ws_bytes_k<1>(B, T, n, v);
     case 2: return af_ws_bytes_k<2>(B, T, n, v);
-    case 4: return af_ws_bytes_k<4>(B, T, n, v);
-    default: return af_ws_bytes_k<8>(B, T, n, v);
+    default: return af_ws_bytes_k<4>(B, T, n, v);
   }
 }
 
