@@ -239,6 +239,22 @@ class kernel_timer:
         return out
 
 
+_sizes: dict = {}
+
+
+def _size(fn_name: str, *args) -> int:
+    """A size query of the C ABI (workspace or state bytes), cached per arguments: the
+    answer depends only on them, and each ctypes call costs microseconds of host time
+    on every step of a launch-bound workload."""
+    key = (fn_name,) + args
+    v = _sizes.get(key)
+    if v is None:
+        if len(_sizes) >= 4096:
+            _sizes.clear()
+        v = _sizes[key] = int(getattr(_lib(), fn_name)(*args))
+    return v
+
+
 def _call(fn_name: str, *args) -> None:
     timer = kernel_timer.active
     if timer is not None:
@@ -300,7 +316,7 @@ class _LinearScanFn(torch.autograd.Function):
         Bn, T, D = a32.shape
         A = torch.empty_like(a32)
         Bc = torch.empty_like(a32)
-        ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        ws = _scan_workspace(_size("mg_linear_scan_workspace_bytes", Bn, T, D), a32.device)
         _call("mg_linear_scan_fwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), Bn, T, D,
               _ptr(ws), ws.numel(), _stream(a32))
         _check_workspace(ws, a32)
@@ -318,7 +334,7 @@ class _LinearScanFn(torch.autograd.Function):
         gA32, gB32 = _as_f32(gA, gB)
         da = torch.empty_like(a32)
         db = torch.empty_like(a32)
-        ws = _scan_workspace(_lib().mg_linear_scan_workspace_bytes(Bn, T, D), a32.device)
+        ws = _scan_workspace(_size("mg_linear_scan_workspace_bytes", Bn, T, D), a32.device)
         _call("mg_linear_scan_bwd", _ptr(a32), _ptr(b32), _ptr(A), _ptr(Bc), _ptr(gA32),
               _ptr(gB32), _ptr(da), _ptr(db), Bn, T, D, _ptr(ws), ws.numel(), _stream(a32))
         _check_workspace(ws, a32)
@@ -350,7 +366,7 @@ class _SignedGateScanFn(torch.autograd.Function):
         s32, z32, hp32, h032 = _as_f32(s, z, hpre, h0)
         Bn, T, D = s32.shape
         h = torch.empty_like(s32)
-        ws = _scan_workspace(_lib().mg_signed_gate_scan_workspace_bytes(Bn, T, D), s32.device)
+        ws = _scan_workspace(_size("mg_signed_gate_scan_workspace_bytes", Bn, T, D), s32.device)
         _call("mg_signed_gate_scan_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
               Bn, T, D, int(coupled), _ptr(ws), ws.numel(), _stream(s32))
         _check_workspace(ws, s32)
@@ -367,7 +383,7 @@ class _SignedGateScanFn(torch.autograd.Function):
         (gh32,) = _as_f32(gh)
         ds, dz, dhp = (torch.empty_like(s32) for _ in range(3))
         dh0 = torch.empty_like(h032)
-        ws = _scan_workspace(_lib().mg_signed_gate_scan_workspace_bytes(Bn, T, D), s32.device)
+        ws = _scan_workspace(_size("mg_signed_gate_scan_workspace_bytes", Bn, T, D), s32.device)
         _call("mg_signed_gate_scan_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
               _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, D, int(ctx.coupled),
               _ptr(ws), ws.numel(), _stream(s32))
@@ -415,7 +431,7 @@ class _MinGRUGateScanFn(torch.autograd.Function):
         k32, hp32, lh032 = _as_f32(k, hpre, log_h0)
         Bn, T, D = k32.shape
         h = torch.empty_like(k32)
-        ws = _scan_workspace(_lib().mg_mingru_gate_scan_workspace_bytes(Bn, T, D), k32.device)
+        ws = _scan_workspace(_size("mg_mingru_gate_scan_workspace_bytes", Bn, T, D), k32.device)
         _call("mg_mingru_gate_scan_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
               Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
         _check_workspace(ws, k32)
@@ -431,7 +447,7 @@ class _MinGRUGateScanFn(torch.autograd.Function):
         (gh32,) = _as_f32(gh)
         dk, dhp = torch.empty_like(k32), torch.empty_like(k32)
         dlh0 = torch.empty_like(lh032)
-        ws = _scan_workspace(_lib().mg_mingru_gate_scan_workspace_bytes(Bn, T, D), k32.device)
+        ws = _scan_workspace(_size("mg_mingru_gate_scan_workspace_bytes", Bn, T, D), k32.device)
         _call("mg_mingru_gate_scan_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
               _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), Bn, T, D,
               _ptr(ws), ws.numel(), _stream(k32))
@@ -480,9 +496,9 @@ class _LogScanFn(torch.autograd.Function):
         # can restart from values an fp32 h under- or overflows.
         hstate = None
         if any(ctx.needs_input_grad):
-            nfloat = _lib().mg_log_scan_state_bytes(Bn, T, D) // 4
+            nfloat = _size("mg_log_scan_state_bytes", Bn, T, D) // 4
             hstate = torch.empty(nfloat, dtype=torch.float32, device=lc.device)
-        ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        ws = _scan_workspace(_size("mg_log_scan_workspace_bytes", Bn, T, D), lc.device)
         _call("mg_log_scan_fwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(hstate), Bn, T, D, _ptr(ws),
               ws.numel(), _stream(lc))
         _check_workspace(ws, lc)
@@ -498,7 +514,7 @@ class _LogScanFn(torch.autograd.Function):
         (gh32,) = _as_f32(gh)
         dlc = torch.empty_like(lc)
         dlv = torch.empty_like(lv)
-        ws = _scan_workspace(_lib().mg_log_scan_workspace_bytes(Bn, T, D), lc.device)
+        ws = _scan_workspace(_size("mg_log_scan_workspace_bytes", Bn, T, D), lc.device)
         _call("mg_log_scan_bwd", _ptr(lc), _ptr(lv), _ptr(h), _ptr(hstate), _ptr(gh32),
               _ptr(dlc), _ptr(dlv), Bn, T, D, _ptr(ws), ws.numel(), _stream(lc))
         _check_workspace(ws, lc)
@@ -538,7 +554,7 @@ class _AffineScanFn(torch.autograd.Function):
         v = B32.shape[-1]
         Abar = torch.empty_like(A32)
         Bbar = torch.empty_like(B32)
-        ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        ws = _scan_workspace(_size("mg_affine_scan_workspace_bytes", Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_fwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), Bn, T, n, k, v,
               _ptr(ws), ws.numel(), _stream(A32))
         _check_workspace(ws, A32)
@@ -557,7 +573,7 @@ class _AffineScanFn(torch.autograd.Function):
         gA32, gB32 = _as_f32(gAbar, gBbar)
         dA = torch.empty_like(A32)
         dB = torch.empty_like(B32)
-        ws = _scan_workspace(_lib().mg_affine_scan_workspace_bytes(Bn, T, n, k, v), A32.device)
+        ws = _scan_workspace(_size("mg_affine_scan_workspace_bytes", Bn, T, n, k, v), A32.device)
         _call("mg_affine_scan_bwd", _ptr(A32), _ptr(B32), _ptr(Abar), _ptr(Bbar), _ptr(gA32),
               _ptr(gB32), _ptr(dA), _ptr(dB), Bn, T, n, k, v, _ptr(ws), ws.numel(), _stream(A32))
         _check_workspace(ws, A32)
@@ -759,11 +775,10 @@ class _AngleTablesFn(torch.autograd.Function):
         Bn, T, n, k = b32.shape
         R, half = th.shape[3], th.shape[4]
         h = torch.empty_like(b32)
-        lib = _lib()
         # Chunk products P_c, saved for the backward (whose chunk maps are P_c^T).
-        prod = torch.empty(max(int(lib.mg_angle_scan_tables_state_bytes(Bn, T, n, k)), 16) // 4,
+        prod = torch.empty(max(_size("mg_angle_scan_tables_state_bytes", Bn, T, n, k), 16) // 4,
                            dtype=torch.float32, device=b32.device)
-        ws = _workspace(lib.mg_angle_scan_tables_workspace_bytes(Bn, T, n, k), b32.device)
+        ws = _workspace(_size("mg_angle_scan_tables_workspace_bytes", Bn, T, n, k), b32.device)
         _call("mg_angle_scan_tables_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032),
               _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(h), _ptr(prod), Bn, T, n, k, R, half, flags,
               _ptr(ws), ws.numel(), _stream(b32))
@@ -788,7 +803,7 @@ class _AngleTablesFn(torch.autograd.Function):
             if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
-        ws = _workspace(_lib().mg_angle_scan_tables_workspace_bytes(Bn, T, n, k), h.device)
+        ws = _workspace(_size("mg_angle_scan_tables_workspace_bytes", Bn, T, n, k), h.device)
         _call("mg_angle_scan_tables_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h),
               _ptr(prod), _ptr(gh32), _ptr(perm), _ptr(sgn), _ptr(p2p), _ptr(dth), _ptr(dsc),
               _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k, R, half, flags, _ptr(ws), ws.numel(),
@@ -805,11 +820,10 @@ class _AngleScanFn(torch.autograd.Function):
         th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
         Bn, T, n, k = b32.shape
         h = torch.empty_like(b32)
-        lib = _lib()
         # Chunk products P_c, saved for the backward (whose chunk maps are P_c^T).
-        prod = torch.empty(max(int(lib.mg_angle_scan_state_bytes(Bn, T, n, k)), 16) // 4,
+        prod = torch.empty(max(_size("mg_angle_scan_state_bytes", Bn, T, n, k), 16) // 4,
                            dtype=torch.float32, device=b32.device)
-        ws = _workspace(lib.mg_angle_scan_workspace_bytes(Bn, T, n, k), b32.device)
+        ws = _workspace(_size("mg_angle_scan_workspace_bytes", Bn, T, n, k), b32.device)
         _call("mg_angle_scan_fwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(b32), _ptr(h032), _ptr(h),
               _ptr(prod), Bn, T, n, k, sched, rounds, flags, _ptr(ws), ws.numel(), _stream(b32))
         ctx.save_for_backward(th, sc, gm, h032, h, prod)
@@ -834,7 +848,7 @@ class _AngleScanFn(torch.autograd.Function):
             if (flags & 2 or need[2]) else None
         db = torch.empty_like(h)
         dh0 = torch.empty_like(h032)
-        ws = _workspace(_lib().mg_angle_scan_workspace_bytes(Bn, T, n, k), h.device)
+        ws = _workspace(_size("mg_angle_scan_workspace_bytes", Bn, T, n, k), h.device)
         _call("mg_angle_scan_bwd", _ptr(th), _ptr(sc), _ptr(gm), _ptr(h032), _ptr(h), _ptr(prod),
               _ptr(gh32), _ptr(dth), _ptr(dsc), _ptr(dgm), _ptr(db), _ptr(dh0), Bn, T, n, k,
               sched, rounds, flags, _ptr(ws), ws.numel(), _stream(h))
@@ -998,13 +1012,12 @@ class _DeltaScanFn(torch.autograd.Function):
         Bn, nhd, T, d_k = q.shape
         nh = k.shape[3]
         d_v = v.shape[4]
-        lib = _lib()
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
         y = torch.empty(Bn, nhd, T, d_v, dtype=cdt, device=q.device)
         HT = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
-        Hb = torch.empty(max(int(lib.mg_delta_state_bytes(*dims)), 16) // 4, dtype=torch.float32,
+        Hb = torch.empty(max(_size("mg_delta_state_bytes", *dims), 16) // 4, dtype=torch.float32,
                          device=q.device)
-        ws = _workspace(lib.mg_delta_workspace_bytes(*dims), q.device)
+        ws = _workspace(_size("mg_delta_workspace_bytes", *dims), q.device)
         _call("mg_delta_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(h0), _ptr(y), _ptr(HT),
               _ptr(Hb), *dims[:6], chunk_size, 1 if cdt == torch.bfloat16 else 0, _ptr(ws),
               ws.numel(), _stream(q))
@@ -1027,7 +1040,7 @@ class _DeltaScanFn(torch.autograd.Function):
         dQ, dK, dV, dbeta = (torch.empty_like(t) for t in (q, k, v, bt))
         dH0 = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
-        ws = _workspace(_lib().mg_delta_workspace_bytes(*dims), q.device)
+        ws = _workspace(_size("mg_delta_workspace_bytes", *dims), q.device)
         _call("mg_delta_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(Hb), _ptr(dy), _ptr(dHT),
               _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dbeta), _ptr(dH0), *dims[:6], chunk_size,
               1 if cdt == torch.bfloat16 else 0, _ptr(ws), ws.numel(), _stream(q))
@@ -1066,13 +1079,12 @@ class _DeltaGatedScanFn(torch.autograd.Function):
         lg, h0 = _contig(log_gamma, torch.float32), _contig(H0, torch.float32)
         Bn, nhd, T, d_k = q.shape
         d_v = v.shape[4]
-        lib = _lib()
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
         y = torch.empty(Bn, nhd, T, d_v, dtype=cdt, device=q.device)
         HT = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
-        Hb = torch.empty(max(int(lib.mg_delta_state_bytes(*dims)), 16) // 4, dtype=torch.float32,
+        Hb = torch.empty(max(_size("mg_delta_state_bytes", *dims), 16) // 4, dtype=torch.float32,
                          device=q.device)
-        ws = _workspace(lib.mg_delta_gated_workspace_bytes(*dims), q.device)
+        ws = _workspace(_size("mg_delta_gated_workspace_bytes", *dims), q.device)
         tag = 1 if cdt == torch.bfloat16 else 0
         _call("mg_delta_gated_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(h0),
               _ptr(y), _ptr(HT), _ptr(Hb), *dims, tag, _ptr(ws), ws.numel(), _stream(q))
@@ -1096,7 +1108,7 @@ class _DeltaGatedScanFn(torch.autograd.Function):
         dQ, dK, dV, dbeta, dlg = (torch.empty_like(t) for t in (q, k, v, bt, lg))
         dH0 = torch.empty(Bn, nhd, d_k, d_v, dtype=torch.float32, device=q.device)
         dims = (Bn, nhd, T, nh, d_k, d_v, chunk_size)
-        ws = _workspace(_lib().mg_delta_gated_workspace_bytes(*dims), q.device)
+        ws = _workspace(_size("mg_delta_gated_workspace_bytes", *dims), q.device)
         tag = 1 if cdt == torch.bfloat16 else 0
         _call("mg_delta_gated_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(bt), _ptr(lg), _ptr(Hb),
               _ptr(dy), _ptr(dHT), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(dbeta), _ptr(dlg),
