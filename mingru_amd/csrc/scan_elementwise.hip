@@ -55,7 +55,8 @@ constexpr int64_t EW_FILL_WGS = 256;
 // Launch forms of the chunked scans.  EW_LOOKBACK is one launch whose
 // workgroups combine chunk carries by decoupled look-back.  A small problem
 // instead runs two launches over the same grid: EW_REDUCE stores every chunk's
-// aggregate map (the first chunk's with the sequence seed folded in), and
+// aggregate map (the first chunk's with the sequence seed folded in, in the
+// look-back slots with a tag no launch uses), and
 // EW_FINAL folds the stored aggregates of all a chunk's predecessors -- at most
 // EW_FINAL_MAX_CHUNKS - 1, loaded a few per wave at once, so nothing waits on
 // another workgroup -- then recomputes the chunk from its carry.  The second
@@ -257,28 +258,33 @@ __device__ __forceinline__ bool lb_try(const mg_slot_t* base, const EwGeom& g, i
   return ok;
 }
 
-// Stored chunk aggregates of the two-launch form: plain floats laid out like
-// the look-back slots, [lg][chunk][field][VEC][64 lanes].
+// Stored chunk aggregates of the two-launch form, in the look-back slot layout
+// [lg][chunk][field][VEC][64 lanes] and format, with tag 0: the slot regions are
+// shared with look-back launches on the same workspace, whose epochs are never
+// 0, so these words can never pass for a later launch's published values (a raw
+// float there could: a denormal's bit pattern is a small integer, like an epoch).
 template <typename Map, int VEC>
-__device__ __forceinline__ void agg_store(float* base, const EwGeom& g, int lg, int c, int lane,
-                                          const Map (&x)[VEC]) {
+__device__ __forceinline__ void agg_store(mg_slot_t* base, const EwGeom& g, int lg, int c,
+                                          int lane, const Map (&x)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
-  float* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
+  mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
 #pragma unroll
   for (int v = 0; v < VEC; ++v)
 #pragma unroll
-    for (int f = 0; f < Map::NF; ++f) p[f * TILE + v * MG_WAVE] = x[v].get(f);
+    for (int f = 0; f < Map::NF; ++f)
+      p[f * TILE + v * MG_WAVE] = (mg_slot_t)__float_as_uint(x[v].get(f));
 }
 
 template <typename Map, int VEC>
-__device__ __forceinline__ void agg_load(const float* base, const EwGeom& g, int lg, int c,
+__device__ __forceinline__ void agg_load(const mg_slot_t* base, const EwGeom& g, int lg, int c,
                                          int lane, Map (&x)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
-  const float* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
+  const mg_slot_t* p = base + ((int64_t)(lg * g.n_chunks + c) * Map::NF) * TILE + lane;
 #pragma unroll
   for (int v = 0; v < VEC; ++v)
 #pragma unroll
-    for (int f = 0; f < Map::NF; ++f) x[v].set(f, p[f * TILE + v * MG_WAVE]);
+    for (int f = 0; f < Map::NF; ++f)
+      x[v].set(f, __uint_as_float((unsigned)p[f * TILE + v * MG_WAVE]));
 }
 
 // Intra-workgroup combine + the carry from earlier chunks: decoupled look-back
@@ -311,13 +317,12 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
     // Wave w folds predecessors w*PER .. w*PER+PER-1 in application order
     // (forward: chunks 0, 1, ...; reverse: chunks n-1, n-2, ...), all its loads
     // issued before the first compose.
-    const float* stored = reinterpret_cast<const float*>(agg_data);
     const int npred = REVERSE ? g.n_chunks - 1 - c : c;
     Map X[PER][VEC];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int k = w * PER + i;
-      if (k < npred) agg_load<Map, VEC>(stored, g, lg, REVERSE ? g.n_chunks - 1 - k : k, lane, X[i]);
+      if (k < npred) agg_load<Map, VEC>(agg_data, g, lg, REVERSE ? g.n_chunks - 1 - k : k, lane, X[i]);
     }
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
@@ -352,7 +357,7 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
           for (int j = WAVES - 1; j >= 0; --j) G[v] = compose(G[v], wave_agg(j, v));
         }
       }
-      agg_store<Map, VEC>(reinterpret_cast<float*>(agg_data), g, lg, c, lane, G);
+      agg_store<Map, VEC>(agg_data, g, lg, c, lane, G);
     }
     return;
   }
