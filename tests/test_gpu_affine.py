@@ -141,9 +141,11 @@ def test_identity_transitions_long_sequence_exact(cuda):
 
 @pytest.mark.parametrize("case", [(1, 257, 2, 16, 16), (2, 300, 5, 8, 4)])
 def test_matrix_affine_scan_mfma_repeatable(cuda, case):
-    """Matrix-core blocks: five runs of one multi-chunk case give bitwise identical
+    """Matrix-core blocks: five runs of one multi-chunk case agree to rounding in
     outputs and gradients (the look-back consumes a predecessor's map only once the
-    whole wave sees it published, so no lane mixes in a stale part of it)."""
+    whole wave sees it published, so no lane mixes in a stale part of it; a stale
+    mix showed up as errors of order 1).  Not bitwise: which predecessors have
+    published their inclusive maps when a chunk looks back decides the association."""
     B, T, n, k, v = case
     print(f"[gpu] matrix_affine_scan repeatable case={case}", flush=True)
     g = torch.Generator().manual_seed(3)
@@ -161,7 +163,8 @@ def test_matrix_affine_scan_mfma_repeatable(cuda, case):
     torch.cuda.synchronize()
     for r in runs[1:]:
         for x, y in zip(r, runs[0]):
-            assert torch.equal(x, y)
+            scale = max(1.0, y.abs().max().item())
+            assert (x - y).abs().max().item() <= 1e-5 * scale
     rdA, _ = orc.affine_scan_bwd(A.cpu().numpy(), Bm.cpu().numpy(), gA.cpu().numpy(),
                                  gB.cpu().numpy())
     assert _maxerr(runs[0][2], rdA) <= GRAD_TOL
