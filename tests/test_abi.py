@@ -97,3 +97,33 @@ def test_invalid_arguments_are_rejected_on_the_host(lib):
                             one, 1 << 20, NULL) == 1
     assert lib.mg_delta_bwd(*([one] * 11), NULL, 1, 1, 8, 1, 64, 64, 8, 1, one, 1 << 20,
                             NULL) == 1
+
+
+def test_size_queries_are_cached_per_arguments(lib, monkeypatch):
+    """The wrappers' size queries answer from a per-arguments cache: same value as the
+    C ABI, one call per distinct argument tuple, and the cache is bounded."""
+    from mingru_amd import hip_scans
+
+    monkeypatch.setattr(hip_scans, "_sizes", {})
+    calls = []
+    real = lib.mg_log_scan_workspace_bytes
+
+    class Counting:
+        def __getattr__(self, name):
+            fn = getattr(lib, name)
+
+            def wrapped(*args):
+                calls.append((name, args))
+                return fn(*args)
+            return wrapped
+
+    monkeypatch.setattr(hip_scans, "_lib", lambda: Counting())
+    for _ in range(3):
+        assert hip_scans._size("mg_log_scan_workspace_bytes", 4, 1024, 256) == \
+            real(4, 1024, 256)
+    assert len(calls) == 1
+    assert hip_scans._size("mg_log_scan_workspace_bytes", 4, 1025, 256) == real(4, 1025, 256)
+    assert len(calls) == 2
+    for t in range(1, 4100):
+        hip_scans._size("mg_log_scan_workspace_bytes", 1, t, 8)
+    assert len(hip_scans._sizes) <= 4096
