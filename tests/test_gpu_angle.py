@@ -83,6 +83,8 @@ BRICK_CASES = [
     (2, 90, 65, 2, 1, 1, 0),
     (2, 71, 12, 2, 1, 1, 1),
     (1, 40, 7, 2, 3, 0, 1),
+    # exactly 16 chunks of 16 tokens: the last sequence length walked chunk by chunk
+    (1, 256, 6, 8, 3, 0, 1),
     # more than 16 chunks of 16 tokens: the two-level boundary walk, last group partial
     (2, 300, 5, 8, 3, 0, 1),
     (1, 530, 3, 2, 1, 1, 1),
