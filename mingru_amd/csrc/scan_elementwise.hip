@@ -18,8 +18,8 @@
 //   * per thread: local affine aggregate -> LDS combine across waves ->
 //     look-back over earlier chunks (wave 0) -> final recompute from the carry
 //     and streaming stores;
-//   * small problems (few chunks per sequence, inputs that stay cached) run the
-//     log and gate scans as two launches over the same grid instead: chunk
+//   * small problems (few chunks per sequence, inputs that stay cached) run as
+//     two launches over the same grid instead: chunk
 //     aggregates, then every chunk folds its predecessors' aggregates itself
 //     (EW_REDUCE / EW_FINAL), so no workgroup waits on another.
 // The backward is the same machinery run in reverse time order over the
@@ -493,12 +493,13 @@ __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header)
 // ---------------------------------------------------------------------------
 // Forward of linear_scan: a, b -> A (running product), Bc (zero-start solution).
 // ---------------------------------------------------------------------------
-template <int VEC, int TSUB, int WAVES>
+template <int VEC, int TSUB, int WAVES, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     const float* __restrict__ x0, const float* __restrict__ x1, float* __restrict__ out0,
     float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false>(g, header);
+  constexpr bool NT = PH != EW_REDUCE;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -508,8 +509,8 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
   for (int s = 0; s < TSUB; ++s) {
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
-      load_vec<VEC>(av[s], x0 + (th.bb * T + t) * D + th.col);
-      load_vec<VEC>(bv[s], x1 + (th.bb * T + t) * D + th.col);
+      load_vec<VEC, NT>(av[s], x0 + (th.bb * T + t) * D + th.col);
+      load_vec<VEC, NT>(bv[s], x1 + (th.bb * T + t) * D + th.col);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -530,8 +531,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     }
     seed[v] = aff_identity<1>();
   }
-  ew_carry<Aff<1>, VEC, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                      incl_data, carry);
+  ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                          incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
 
   float P[VEC], L[VEC];
 #pragma unroll
@@ -560,13 +562,14 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
 // outputs da, db.  Adjoint: x_t = g_t + a_{t+1} x_{t+1} for both streams;
 // da_t = xA_t A_{t-1} + xB_t Bc_{t-1}, db_t = xB_t.
 // ---------------------------------------------------------------------------
-template <int VEC, int TSUB, int WAVES>
+template <int VEC, int TSUB, int WAVES, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ A,
     const float* __restrict__ Bc, const float* __restrict__ gA, const float* __restrict__ gB,
     float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true>(g, header);
+  constexpr bool NT = PH != EW_REDUCE;
+  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
   if (!th.valid) return;
   const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
   const int64_t T = g.T, D = g.D;
@@ -578,10 +581,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     const int64_t t = t0 + s;
     if (th.col_ok && t < T) {
       const int64_t off = (th.bb * T + t) * D + th.col;
-      load_vec<VEC>(av[s], a + off);
-      load_vec<VEC>(bv[s], b + off);
-      load_vec<VEC>(xa[s], gA + off);
-      load_vec<VEC>(xb[s], gB + off);
+      load_vec<VEC, NT>(av[s], a + off);
+      if constexpr (PH != EW_REDUCE) load_vec<VEC>(bv[s], b + off);
+      load_vec<VEC, NT>(xa[s], gA + off);
+      load_vec<VEC, NT>(xb[s], gB + off);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -617,8 +620,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     }
     seed[v] = aff_identity<2>();
   }
-  ew_carry<Aff<2>, VEC, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data,
-                                carry);
+  ew_carry<Aff<2>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                         incl_data, carry);
+  if constexpr (PH == EW_REDUCE) return;
 
   float ya[VEC], yb[VEC];
 #pragma unroll
@@ -1328,8 +1332,10 @@ int linear_fwd_launch(const float* a, const float* b, float* A, float* Bc, int64
     constexpr int V = decltype(v)::value;
     EwPlan p = ew_plan(B, T, D, V, EW_TSUB_FWD, EW_WAVES_FWD, 1);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD>, p, ws, stream, a, b, A,
-                     Bc);
+    return ew_run(ew_two_launch(p, B, T, D, 2), ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD>,
+                  ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_REDUCE>,
+                  ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_FINAL>, p, ws, stream, a, b, A,
+                  Bc);
   });
 }
 
@@ -1398,8 +1404,10 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
     constexpr int V = decltype(v)::value;
     EwPlan p = ew_plan(B, T, D, V, EW_TSUB_BWD, EW_WAVES_BWD, 2);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
-    return ew_launch(linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD>, p, ws, stream, a, b, A, Bc,
-                     gA, gB, da, db);
+    return ew_run(ew_two_launch(p, B, T, D, 4), linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD>,
+                  linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_REDUCE>,
+                  linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_FINAL>, p, ws, stream, a, b,
+                  A, Bc, gA, gB, da, db);
   });
 }
 

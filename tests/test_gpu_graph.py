@@ -35,10 +35,13 @@ def _capture(fn, warm_args):
     return g, out
 
 
-def test_linear_scan_graph_replays(cuda):
-    print("[gpu] graph: linear_scan", flush=True)
+# (2, 777, 136) runs as two launches (chunk aggregates, then the fold); (2, 4225, 64) has
+# 34 forward chunks per sequence and runs the look-back launch, whose epoch advances on
+# the device at every replay.
+@pytest.mark.parametrize("shape", [(2, 777, 136), (2, 4225, 64)], ids=["two_launch", "lookback"])
+def test_linear_scan_graph_replays(cuda, shape):
+    print(f"[gpu] graph: linear_scan shape={shape}", flush=True)
     gen = torch.Generator(device=cuda).manual_seed(0)
-    shape = (2, 777, 136)
     sa = torch.empty(shape, device=cuda)
     sb = torch.empty(shape, device=cuda)
     sa.copy_(torch.tanh(torch.randn(shape, device=cuda, generator=gen)))
