@@ -771,6 +771,19 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   const int lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const int R0 = 16 * F.rb, C0 = 32 * F.ch;
   FTileF th;  // Hc, staged in stage B
+  // V at the wave's positions of R (stage B) and Q as A fragments (stage D): loaded
+  // with the tiles, so the first barrier waits for all of them at once instead of
+  // each stage paying its own memory round trip.
+  float vpre[2][4];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = R0 + 4 * gg + i, j = C0 + 16 * jj + r;
+      vpre[jj][i] = (m < ch.M && j < g.dv) ? ldf(V, (row0 + m) * g.dv + j) : 0.f;
+    }
+  uint4 qf[2];
+  load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
   {
     BTile tk, tq, td;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
@@ -833,9 +846,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
       const int cj = C0 + 16 * jj;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int m = R0 + 4 * gg + i, j = cj + r;
-        const float v = (m < ch.M && j < g.dv) ? ldf(V, (row0 + m) * g.dv + j) : 0.f;
-        rr[jj][i] = fmaf(GATED ? -sp[m] : -1.f, rr[jj][i], v);
+        const int m = R0 + 4 * gg + i;
+        rr[jj][i] = fmaf(GATED ? -sp[m] : -1.f, rr[jj][i], vpre[jj][i]);
       }
       acc_put_t(sR2, rr[jj], R0, cj);
     }
@@ -854,8 +866,6 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   floatx4 qd[2];  // Q^T dy (gated: Q^T diag(ptok) dy), kept for b'
   zero2(qd);
   {
-    uint4 qf[2];
-    load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
     floatx4 pp[2];
     zero2(pp);
     rmm<false>(pp, F, qf, &sK);  // Q K^T
