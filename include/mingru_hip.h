@@ -155,7 +155,8 @@ int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const
  * sched 1: all pairs i<j in lexicographic order, one plane per round
  * (rounds = k(k-1)/2 = NA).  flags bit 0: scale coordinate 1 by `scale`,
  * bit 1: decay by `gamma`.  The forward writes the per-chunk transition
- * products to `chunk_prod` (mg_angle_scan_state_bytes); the backward reads
+ * products (and, past 16 chunks of 16 tokens, the products over groups of 8
+ * chunks) to `chunk_prod` (mg_angle_scan_state_bytes); the backward reads
  * them.  The workspace's contents on entry are irrelevant (no look-back). */
 size_t mg_angle_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
 size_t mg_angle_scan_state_bytes(int64_t B, int64_t T, int64_t n, int k);

@@ -324,6 +324,10 @@ struct AnArgs {
   float* prod;   // chunk products P_c, [chunk][block][K*K]: forward writes, backward reads
   float* lsum;   // chunk offsets (forward L_c, backward adjoint offsets), [chunk][block][K]
   float* bound;  // chunk-entry states (forward) / adjoints (backward), [chunk][block][K]
+  // Two-level walk only: group maps [group][block][K*K] (the forward's, saved after
+  // the chunk products) and group offsets [group][block][K] of the pass's direction.
+  float* gprod;
+  float* gsum;
   int rounds;
   int na;  // angles per token
 };
@@ -378,6 +382,7 @@ __device__ __forceinline__ void token_pairs(int64_t first, int count, int dir, L
 struct AnGeom {
   int64_t T, n, NB;  // tokens, blocks per batch row, blocks in total (B * n)
   int n_tiles, n_lg, n_chunks;
+  int n_run, n_groups;  // runs of AN_RUN consecutive blocks, groups of AN_GROUP chunks
 };
 
 // Chunk-parallel passes: one wave per (lane group, chunk), one lane per block.
@@ -398,6 +403,47 @@ __device__ __forceinline__ AnThread an_thread(const AnGeom& g) {
   th.ok = th.c < g.n_chunks && th.plane < g.n;
   th.blk = th.bb * g.n + th.plane;
   return th;
+}
+
+// Forward reduce pass: one workgroup per (run of AN_RUN consecutive blocks, group of
+// AN_GROUP consecutive chunks); thread 32 j + b holds chunk j of the group for block
+// b of the run, so wave w holds chunks 2w and 2w + 1 (a token row of 32 consecutive
+// blocks per chunk, 3.5 KB of angles at k = 8) and the workgroup holds every chunk
+// map of its blocks' group, which it composes into the group maps of the two-level
+// walk through LDS.
+constexpr int AN_RUN = 32;
+static_assert(AN_RUN * AN_GROUP == MG_WAVE * AN_WAVES, "a workgroup is one group of chunks");
+
+struct AnRThread {
+  int64_t bb, plane, blk;
+  int c, grp, j, b, cnt;  // cnt: chunks in the group (uniform)
+  bool live;              // the block exists: the thread joins the compose
+  bool ok;                // ... and so does the chunk: the thread reduces it
+  bool full;              // every lane of the wave is ok (wave-uniform)
+};
+
+__device__ __forceinline__ AnRThread an_rthread(const AnGeom& g) {
+  AnRThread th;
+  const int run = (int)(blockIdx.x % (unsigned)g.n_run);
+  th.grp = (int)(blockIdx.x / (unsigned)g.n_run);
+  th.j = threadIdx.x / AN_RUN;
+  th.b = threadIdx.x % AN_RUN;
+  th.blk = (int64_t)run * AN_RUN + th.b;
+  th.c = th.grp * AN_GROUP + th.j;
+  th.cnt = min(AN_GROUP, g.n_chunks - th.grp * AN_GROUP);
+  th.live = th.blk < g.NB;
+  th.ok = th.live && th.c < g.n_chunks;
+  th.full = (int64_t)(run + 1) * AN_RUN <= g.NB && (th.c | 1) < g.n_chunks;
+  th.bb = th.blk / g.n;
+  th.plane = th.blk % g.n;
+  return th;
+}
+
+// LDS row of one reduce thread: its chunk map [P | L] (K*K + K floats), padded so
+// that the rows of 16 consecutive blocks of one chunk fall in distinct banks.
+template <int K>
+constexpr int an_row_stride() {
+  return (K * K + K + 3) / 4 * 4 + 4;
 }
 
 // Index of field f of chunk c for block blk in a [chunk][block][field] array:
@@ -437,47 +483,52 @@ __device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const 
 }
 
 // ---- forward pass 1: chunk aggregates h -> P_c h + L_c ------------------------
+// With the two-level walk the workgroup then composes its group maps h -> Pg h + Lg
+// over chunks c0 .. c1: thread (j < K, b) carries column j of block b's Pg (and,
+// redundantly, its Lg) through the group's chunk maps read back from LDS.
 template <int K, int SCHED, bool HS, bool HD>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, AnGeom g) {
   mg_sincos_setup();
-  const AnThread th = an_thread(g);
-  if (!th.ok) return;
-  const int64_t t0 = (int64_t)th.c * AN_CHUNK;
+  const AnRThread th = an_rthread(g);
   // Push [P | L] through the chunk's transitions.
   float X[K][K + 1];
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
     for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
-  const int64_t te = min(t0 + AN_CHUNK, g.T);
   // The decay is a scalar per token, so it commutes with the rotations: P's K
   // columns take the chunk's product of decays once at the end, and only the
   // offset column, which receives b_t every token, is decayed token by token.
   float gprod = 1.f;
-  if constexpr (SCHED == SCHED_LEX) {
-    using Tok = LexTok<K, HS, HD>;
-    token_pairs<Tok>(
-        t0, (int)(te - t0), 1,
-        [&](Tok& k, int64_t t) {
-          k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
-        },
-        [&](const Tok& cur, int64_t) {
-          apply_M_lex<K, HS, false, K + 1>(X, cur.ang, cur.d, 1.f);
-          if (HD) gprod *= cur.gm;
+  if (th.ok) {
+    const int64_t t0 = (int64_t)th.c * AN_CHUNK;
+    const int64_t te = min(t0 + AN_CHUNK, g.T);
+    if constexpr (SCHED == SCHED_LEX) {
+      using Tok = LexTok<K, HS, HD>;
+      token_pairs<Tok>(
+          t0, (int)(te - t0), 1,
+          [&](Tok& k, int64_t t) {
+            k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+          },
+          [&](const Tok& cur, int64_t) {
+            apply_M_lex<K, HS, false, K + 1>(X, cur.ang, cur.d, 1.f);
+            if (HD) gprod *= cur.gm;
 #pragma unroll
-          for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
-        });
-  } else {
-    for (int64_t t = t0; t < te; ++t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? a.scale[lane_tok] : 1.f;
-      const float gm = HD ? a.gamma[lane_tok] : 1.f;
-      apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
-      if (HD) gprod *= gm;
-      float bt[K];
-      ld<K>(bt, a.b + lane_tok * K);
+            for (int i = 0; i < K; ++i)
+              X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
+          });
+    } else {
+      for (int64_t t = t0; t < te; ++t) {
+        const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+        const float d = HS ? a.scale[lane_tok] : 1.f;
+        const float gm = HD ? a.gamma[lane_tok] : 1.f;
+        apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
+        if (HD) gprod *= gm;
+        float bt[K];
+        ld<K>(bt, a.b + lane_tok * K);
 #pragma unroll
-      for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+        for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+      }
     }
   }
   if (HD) {
@@ -493,15 +544,80 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
     for (int j = 0; j < K; ++j) Pf[i * K + j] = X[i][j];
     Lf[i] = X[i][K];
   }
-  // A whole wave's P rows are consecutive: they leave through LDS as whole lines.
-  __shared__ __attribute__((aligned(16))) float s_prod[AN_WAVES][MG_WAVE * K * K];
-  const int lane = threadIdx.x & (MG_WAVE - 1);
-  if (__builtin_amdgcn_read_exec() == ~0ull)
-    wave_rows_store<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk - lane), Pf,
-                           s_prod[threadIdx.x / MG_WAVE], lane);
-  else
+  // The threads' [P | L] rows pass through LDS (row = thread): the chunk products
+  // leave as whole lines (a wave's rows are two chunks of 32 consecutive blocks,
+  // consecutive in memory) and the group compose reads them back.
+  constexpr int RS = an_row_stride<K>();
+  __shared__ __attribute__((aligned(16))) float s_rows[MG_WAVE * AN_WAVES * RS];
+  const int lane = threadIdx.x & (MG_WAVE - 1), w = threadIdx.x / MG_WAVE;
+  if (th.ok) {
+#pragma unroll
+    for (int k = 0; k < K * K; k += 4)
+      *reinterpret_cast<float4*>(s_rows + threadIdx.x * RS + k) =
+          make_float4(Pf[k], Pf[k + 1], Pf[k + 2], Pf[k + 3]);
+#pragma unroll
+    for (int i = 0; i < K; ++i) s_rows[threadIdx.x * RS + K * K + i] = Lf[i];
+  }
+  wave_sync();
+  if (th.full) {
+    // Piece q: floats 4 (64 q + lane) .. of the wave's 64 rows; the rows of one
+    // piece are consecutive blocks of one chunk.
+    const int64_t blk0 = th.blk - th.b;
+#pragma unroll
+    for (int q = 0; q < K * K / 4; ++q) {
+      const int o = (q * MG_WAVE + lane) * 4, r = o / (K * K), col = o % (K * K);
+      const float4 v = *reinterpret_cast<const float4*>(s_rows + (w * MG_WAVE + r) * RS + col);
+      *reinterpret_cast<float4*>(a.prod + an_idx(g, th.grp * AN_GROUP + 2 * w + r / AN_RUN, col,
+                                                 K * K, blk0 + r % AN_RUN)) = v;
+    }
+  } else if (th.ok) {
     st<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk), Pf);
-  st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
+  }
+  if (th.ok) st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
+  if (g.n_chunks <= AN_GROUP_MIN) return;  // uniform
+  __syncthreads();
+  if (!th.live || th.j >= K) return;
+  float m[K], l[K];  // column j and offset of the maps composed so far (chunk c0's)
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    m[i] = s_rows[th.b * RS + i * K + th.j];
+    l[i] = s_rows[th.b * RS + K * K + i];
+  }
+  for (int s = 1; s < th.cnt; ++s) {
+    const float* row = s_rows + (s * AN_RUN + th.b) * RS;
+    float P[K * K], L[K];
+#pragma unroll
+    for (int k = 0; k < K * K; k += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(row + k);
+      P[k] = v.x;
+      P[k + 1] = v.y;
+      P[k + 2] = v.z;
+      P[k + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) L[i] = row[K * K + i];
+    float nm[K], nl[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float am = 0.f, al = L[i];
+#pragma unroll
+      for (int q = 0; q < K; ++q) {
+        am = fmaf(P[i * K + q], m[q], am);
+        al = fmaf(P[i * K + q], l[q], al);
+      }
+      nm[i] = am;
+      nl[i] = al;
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      m[i] = nm[i];
+      l[i] = nl[i];
+    }
+  }
+  float* out = a.gprod + an_idx(g, th.grp, 0, K * K, th.blk);
+#pragma unroll
+  for (int i = 0; i < K; ++i) out[i * K + th.j] = m[i];
+  if (th.j == 0) st<K>(a.gsum + an_idx(g, th.grp, 0, K, th.blk), l);
 }
 
 // ---- forward pass 2: states at chunk boundaries, h_{c+1} = P_c h_c + L_c -------
@@ -860,83 +976,13 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_bwd_scan(AnArgs a, AnGe
   st<H>(a.dh0 + blk * K + H * p, y);  // the adjoint leaving chunk 0 is dL/dh0
 }
 
-// ---- two-level walk: group maps and the chunk states inside each group ---------
+// ---- two-level walk: the chunk states inside each group ------------------------
 // Forward group map over chunks c0 .. c1 (applied in order): h -> Pg h + Lg.
 // Backward group map over the same chunks applied from c1 down to c0:
-// y -> Qg y + lg with Qg = P_c0^T ... P_c1^T.  K lanes per (block, group): lane j
-// carries column j of the group's linear part (and, redundantly, its offset), so
-// a chunk costs each lane two k x k matrix-vector products; the next chunk's map
-// is loaded while the current one is applied.  `gp`, `gl` are [group][block][K*K]
-// and [group][block][K].
-template <int K, bool BWD>
-__global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_compose(AnArgs a, AnGeom g,
-                                                                       float* gp, float* gl,
-                                                                       int n_groups) {
-  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
-  const int j = (int)(gt % K);
-  const int64_t gb = gt / K;
-  const int64_t blk = gb % g.NB;
-  const int grp = (int)(gb / g.NB);
-  if (grp >= n_groups) return;
-  const int c0 = grp * AN_GROUP, c1 = min(c0 + AN_GROUP, g.n_chunks) - 1;
-  float m[K], l[K];
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-    m[i] = (i == j) ? 1.f : 0.f;
-    l[i] = 0.f;
-  }
-  struct Op {
-    float P[K * K], L[K];
-  };
-  auto fetch = [&](Op& o, int s) {
-    s = min(s, c1 - c0);  // clamped reads past the group's end are unused
-    const int c = BWD ? c1 - s : c0 + s;
-    ld<K * K>(o.P, a.prod + an_idx(g, c, 0, K * K, blk));
-    ld<K>(o.L, a.lsum + an_idx(g, c, 0, K, blk));
-  };
-  auto apply = [&](const Op& o) {
-    // forward: column <- P column, l <- P l + L;  backward: with P^T
-    float nm[K], nl[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      float am = 0.f, al = o.L[i];
-#pragma unroll
-      for (int q = 0; q < K; ++q) {
-        const float pe = BWD ? o.P[q * K + i] : o.P[i * K + q];
-        am = fmaf(pe, m[q], am);
-        al = fmaf(pe, l[q], al);
-      }
-      nm[i] = am;
-      nl[i] = al;
-    }
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      m[i] = nm[i];
-      l[i] = nl[i];
-    }
-  };
-  Op A, B;
-  fetch(A, 0);
-  const int cnt = c1 - c0 + 1;
-  int s = 0;
-  for (; s + 2 <= cnt; s += 2) {
-    fetch(B, s + 1);
-    apply(A);
-    fetch(A, s + 2);
-    apply(B);
-  }
-  if (s < cnt) apply(A);
-  // The group walk reads these as it reads chunk maps: forward P rows, backward P
-  // columns, so the backward map is stored transposed (Qg^T = P_c1 ... P_c0).
-  float* out = gp + an_idx(g, grp, 0, K * K, blk);
-  if (BWD) {
-    st<K>(out + j * K, m);  // row j of Qg^T is column j of Qg
-  } else {
-#pragma unroll
-    for (int i = 0; i < K; ++i) out[i * K + j] = m[i];
-  }
-  if (j == 0) st<K>(gl + an_idx(g, grp, 0, K, blk), l);
-}
+// y -> Qg y + lg with Qg = P_c0^T ... P_c1^T = Pg^T.  The forward reduce pass
+// composes Pg and Lg, angle_group_offsets the backward's lg; Pg is stored row-major
+// ([group][block][K*K]) after the chunk products and read by both directions, the
+// backward walk reading its columns as it reads a chunk product's.
 
 // Chunk-entry states (forward) / adjoints (backward) of every chunk of a group
 // from the group's entry value `gb` [group][block][K].  K lanes per (block,
@@ -985,6 +1031,51 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_fill(AnArgs a, An
     for (int q = 0; q < K; ++q) acc = fmaf(P[s][q], __shfl(h, base + q), acc);
     h = acc;
   }
+}
+
+// Backward group offsets lg of the maps y -> Qg y + lg (chunks applied from c1 down
+// to c0) from the chunk maps y -> P_c^T y + Lb_c: K lanes per (block, group), lane i
+// owning coordinate i, with all of the group's columns i of P_c and offsets loaded up
+// front; a chunk step is one partner read per coordinate and K multiply-adds.  The
+// linear parts Qg = Pg^T are the forward's group maps, which the walk reads as they
+// are.
+template <int K>
+__global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_offsets(AnArgs a, AnGeom g,
+                                                                       int n_groups) {
+  const int64_t gt = (int64_t)blockIdx.x * AN_WALK_THREADS + threadIdx.x;
+  const int i = (int)(gt % K);
+  const int64_t gbk = gt / K;
+  const int64_t blk = gbk % g.NB;
+  const int grp = (int)(gbk / g.NB);
+  const bool ok = grp < n_groups;  // every lane stays for the partner reads
+  const int lane = threadIdx.x & (MG_WAVE - 1), base = lane - i;
+  const int c0 = ok ? grp * AN_GROUP : 0;
+  const int c1 = ok ? min(c0 + AN_GROUP, g.n_chunks) - 1 : 0;
+  const int cnt = c1 - c0 + 1;
+  float P[AN_GROUP][K], L[AN_GROUP];
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    const int c = c1 - min(s, cnt - 1);
+    const float* pc = a.prod + an_idx(g, c, 0, K * K, blk);
+    if (ok) {
+#pragma unroll
+      for (int q = 0; q < K; ++q) P[s][q] = pc[q * K + i];
+      L[s] = a.lsum[an_idx(g, c, i, K, blk)];
+    } else {
+#pragma unroll
+      for (int q = 0; q < K; ++q) P[s][q] = 0.f;
+      L[s] = 0.f;
+    }
+  }
+  float y = 0.f;
+#pragma unroll
+  for (int s = 0; s < AN_GROUP; ++s) {
+    float acc = L[s];
+#pragma unroll
+    for (int q = 0; q < K; ++q) acc = fmaf(P[s][q], __shfl(y, base + q), acc);
+    y = s < cnt ? acc : y;
+  }
+  if (ok) a.gsum[an_idx(g, grp, i, K, blk)] = y;
 }
 
 // Group walk and fill in one launch, for at most AN_WALKFILL_GROUPS groups: each
@@ -1159,27 +1250,30 @@ AnGeom an_geom(int64_t B, int64_t T, int64_t n) {
   g.n_tiles = (int)((n + MG_WAVE - 1) / MG_WAVE);
   g.n_lg = (int)(B * g.n_tiles);
   g.n_chunks = (int)((T + AN_CHUNK - 1) / AN_CHUNK);
+  g.n_run = (int)((g.NB + AN_RUN - 1) / AN_RUN);
+  g.n_groups = (g.n_chunks + AN_GROUP - 1) / AN_GROUP;
   return g;
 }
 
-// Workspace: chunk offsets and chunk-entry states, K floats each per (chunk, block).
-int an_groups(const AnGeom& g) { return (g.n_chunks + AN_GROUP - 1) / AN_GROUP; }
+bool an_two_level(const AnGeom& g) { return g.n_chunks > AN_GROUP_MIN; }
 
-// Header, chunk offsets and chunk-entry values ([chunk][block][k] each), then the
-// two-level walk's group maps ([group][block][k*k] and [group][block][k]) and
-// group-entry values.
+// Workspace: header, chunk offsets and chunk-entry values ([chunk][block][k] each),
+// then the two-level walk's group offsets and group-entry values ([group][block][k]
+// each).
 size_t an_ws_bytes(int64_t B, int64_t T, int64_t n, int k) {
   const AnGeom g = an_geom(B, T, n);
   const size_t one = mg_align_up((size_t)g.n_chunks * k * g.NB * sizeof(float), 256);
-  const size_t gv = mg_align_up((size_t)an_groups(g) * k * g.NB * sizeof(float), 256);
-  const size_t gm = mg_align_up((size_t)an_groups(g) * k * k * g.NB * sizeof(float), 256);
-  return MG_HEADER_BYTES + 2 * one + gm + 2 * gv;
+  const size_t gv = mg_align_up((size_t)g.n_groups * k * g.NB * sizeof(float), 256);
+  return MG_HEADER_BYTES + 2 * one + 2 * gv;
 }
 
-// Chunk products saved by the forward for the backward: K*K floats per (chunk, block).
+// Saved by the forward for the backward: the chunk products, K*K floats per
+// (chunk, block), and with the two-level walk the group maps, K*K floats per
+// (group, block).
 size_t an_state_bytes(int64_t B, int64_t T, int64_t n, int k) {
   const AnGeom g = an_geom(B, T, n);
-  return (size_t)g.n_chunks * k * k * g.NB * sizeof(float);
+  const int64_t maps = g.n_chunks + (an_two_level(g) ? g.n_groups : 0);
+  return (size_t)maps * k * k * g.NB * sizeof(float);
 }
 
 template <int K, int SCHED, bool HS, bool HD, bool BWD>
@@ -1190,36 +1284,38 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
   const size_t one = mg_align_up((size_t)g.n_chunks * K * g.NB * sizeof(float), 256);
   a.lsum = (float*)((char*)ws + MG_HEADER_BYTES);
   a.bound = (float*)((char*)ws + MG_HEADER_BYTES + one);
+  const int ng = g.n_groups;
+  const size_t gv = mg_align_up((size_t)ng * K * g.NB * sizeof(float), 256);
+  a.gsum = (float*)((char*)ws + MG_HEADER_BYTES + 2 * one);
+  float* gb = (float*)((char*)ws + MG_HEADER_BYTES + 2 * one + gv);
+  a.gprod = a.prod + (size_t)g.n_chunks * K * K * g.NB;  // after the chunk products
   const int64_t waves = (int64_t)g.n_lg * g.n_chunks;
   const dim3 grid((unsigned)((waves + AN_WAVES - 1) / AN_WAVES)), block(MG_WAVE * AN_WAVES);
+  const dim3 rgrid((unsigned)((int64_t)g.n_run * ng));
   const dim3 sgrid((unsigned)((g.NB * 2 + AN_WALK_THREADS - 1) / AN_WALK_THREADS)),
       sblock(AN_WALK_THREADS);
-  // Boundary walk: direct over the chunks, or over groups of AN_GROUP chunks.
+  // Boundary walk: direct over the chunks, or over the groups of AN_GROUP chunks
+  // whose maps the reduce pass composed.
   auto walk = [&]() {
-    if (g.n_chunks <= AN_GROUP_MIN) {
+    if (!an_two_level(g)) {
       if (BWD) hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, a, g);
       else hipLaunchKernelGGL((angle_fwd_scan<K>), sgrid, sblock, 0, stream, a, g);
       return;
     }
-    const int ng = an_groups(g);
-    const size_t gv = mg_align_up((size_t)ng * K * g.NB * sizeof(float), 256);
-    const size_t gm = mg_align_up((size_t)ng * K * K * g.NB * sizeof(float), 256);
-    char* base = (char*)ws + MG_HEADER_BYTES + 2 * one;
-    float* gp = (float*)base;
-    float* gl = (float*)(base + gm);
-    float* gb = (float*)(base + gm + gv);
+    const float* gp = a.gprod;
+    const float* gl = a.gsum;
     const dim3 cgrid((unsigned)((g.NB * ng * K + AN_WALK_THREADS - 1) / AN_WALK_THREADS));
-    hipLaunchKernelGGL((angle_group_compose<K, BWD>), cgrid, sblock, 0, stream, a, g, gp, gl, ng);
+    if (BWD) hipLaunchKernelGGL((angle_group_offsets<K>), cgrid, sblock, 0, stream, a, g, ng);
     if (ng <= AN_WALKFILL_GROUPS) {
-      hipLaunchKernelGGL((angle_group_walk_fill<K, BWD>), cgrid, sblock, 0, stream, a, g,
-                         (const float*)gp, (const float*)gl, ng);
+      hipLaunchKernelGGL((angle_group_walk_fill<K, BWD>), cgrid, sblock, 0, stream, a, g, gp, gl,
+                         ng);
       return;
     }
     // The walk kernels over the group maps: chunks -> groups.
     AnArgs ag = a;
     AnGeom gg = g;
-    ag.prod = gp;
-    ag.lsum = gl;
+    ag.prod = a.gprod;
+    ag.lsum = a.gsum;
     ag.bound = gb;
     gg.n_chunks = ng;
     if (BWD) hipLaunchKernelGGL((angle_bwd_scan<K>), sgrid, sblock, 0, stream, ag, gg);
@@ -1232,7 +1328,7 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
     walk();
     hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   } else {
-    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), rgrid, block, 0, stream, a, g);
     walk();
     hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   }
@@ -1270,7 +1366,8 @@ bool an_args_ok(int64_t B, int64_t T, int64_t n, int k, int sched, int rounds) {
 
 bool an_geometry_ok(int64_t B, int64_t T, int64_t n) {
   const AnGeom g = an_geom(B, T, n);
-  return (int64_t)g.n_lg * g.n_chunks < (1ll << 31) - AN_WAVES && g.NB * 8 < (1ll << 31);
+  return (int64_t)g.n_lg * g.n_chunks < (1ll << 31) - AN_WAVES &&
+         (int64_t)g.n_run * g.n_groups < (1ll << 31) && g.NB * 8 < (1ll << 31);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

@@ -820,7 +820,8 @@ class _AngleScanFn(torch.autograd.Function):
         th, sc, gm, b32, h032 = _as_f32(theta, scale, gamma, b, h0)
         Bn, T, n, k = b32.shape
         h = torch.empty_like(b32)
-        # Chunk products P_c, saved for the backward (whose chunk maps are P_c^T).
+        # Chunk products P_c (and, past 16 chunks, the group products), saved for the
+        # backward, whose chunk and group maps are their transposes.
         prod = torch.empty(max(_size("mg_angle_scan_state_bytes", Bn, T, n, k), 16) // 4,
                            dtype=torch.float32, device=b32.device)
         ws = _workspace(_size("mg_angle_scan_workspace_bytes", Bn, T, n, k), b32.device)

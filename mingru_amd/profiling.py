@@ -49,7 +49,8 @@ ENTRIES = {
     "C3": [("mg_affine_scan_fwd", r"\baffine_fwd_kernel<2, 1,"),
            ("mg_affine_scan_bwd", r"\baffine_bwd_kernel<2, 1,")],
     "C4": [("mg_angle_scan_fwd", r"\bangle_fwd_\w+<|\bangle_group_\w+<\d+, false>"),
-           ("mg_angle_scan_bwd", r"\bangle_bwd_\w+<|\bangle_group_\w+<\d+, true>")],
+           ("mg_angle_scan_bwd",
+            r"\bangle_bwd_\w+<|\bangle_group_\w+<\d+, true>|\bangle_group_offsets<")],
     "C5": [("mg_delta_fwd", r"\bdwb_fwd_\w+<false>"), ("mg_delta_bwd", r"\bdwb_bwd_\w+<false>")],
     "C5d": [("mg_delta_gated_fwd", r"\bdwb_fwd_\w+<true>"),
             ("mg_delta_gated_bwd", r"\bdwb_bwd_\w+<true>")],

@@ -57,8 +57,11 @@ def test_workspace_queries(lib):
     assert lib.mg_log_scan_state_bytes(0, 13, 5) == 0
     assert lib.mg_affine_scan_workspace_bytes(16, 4096, 256, 2, 1) >= 256
     assert lib.mg_angle_scan_workspace_bytes(8, 2048, 64, 8) >= 256
-    # angle chunk products: 8x8 floats per (block, 16-token chunk)
-    assert lib.mg_angle_scan_state_bytes(8, 2048, 64, 8) == 128 * 64 * 8 * 64 * 4
+    # angle chunk products: 8x8 floats per (block, 16-token chunk), then, past 16
+    # chunks (the two-level walk), 8x8 floats per (block, group of 8 chunks)
+    assert lib.mg_angle_scan_state_bytes(8, 2048, 64, 8) == (128 + 16) * 64 * 8 * 64 * 4
+    assert lib.mg_angle_scan_state_bytes(2, 256, 3, 4) == 16 * 6 * 16 * 4
+    assert lib.mg_angle_scan_state_bytes(2, 257, 3, 4) == (17 + 3) * 6 * 16 * 4
     # delta: six padded 64 x 64 fp32 matrices per (batch, head, chunk)
     assert lib.mg_delta_workspace_bytes(8, 8, 8192, 1, 64, 64, 64) == 6 * 64 * 128 * 64 * 64 * 4
     assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 64 * 128 * 64 * 64 * 4

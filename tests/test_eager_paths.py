@@ -121,10 +121,11 @@ def test_profile_entry_patterns_split_angle_walk_kernels():
 
     fwd, bwd = (p for _, p in profiling.ENTRIES["C4"])
     for name in ("angle_fwd_reduce<8, 1, false, true>", "angle_fwd_scan<8>",
-                 "angle_group_compose<8, false>", "angle_group_fill<8, false>"):
+                 "angle_group_walk_fill<8, false>", "angle_group_fill<8, false>"):
         assert re.search(fwd, name) and not re.search(bwd, name), name
     for name in ("angle_bwd_final<8, 1, false, true>", "angle_bwd_scan<8>",
-                 "angle_group_compose<8, true>", "angle_group_fill<8, true>"):
+                 "angle_group_walk_fill<8, true>", "angle_group_fill<8, true>",
+                 "angle_group_offsets<8>"):
         assert re.search(bwd, name) and not re.search(fwd, name), name
 
 
