@@ -210,7 +210,8 @@ def test_delta_gated_bf16_matches_oracle(cuda, case):
 
 def test_delta_gated_bf16_c5_heads(cuda):
     """The C5d workload in bf16 (B=8, H=8, T=8192, d=64, chunk 64): two heads at full
-    length against the oracle."""
+    length against the oracle, from the first and the second half of the 64 (batch,
+    head) pairs."""
     from mingru_amd import workloads as wl
 
     print("[gpu] delta gated bf16 C5 heads", flush=True)
@@ -219,14 +220,14 @@ def test_delta_gated_bf16_c5_heads(cuda):
     lg, H0 = inp["log_gamma"], inp["H0"]
     dy, dHT = inp["grad_y"].to(torch.bfloat16), inp["grad_HT"]
     y, HT, grads = _run((Q, K, V, beta, lg, H0), dy, dHT, inp["chunk_size"], cuda)
-    sel = (slice(5, 6), slice(1, 3))
-    sub = [_np(t[sel]) for t in (Q, K, V, beta, lg, H0)]
-    ry, rHT = orc.delta_gated_sequential(*sub)
-    assert _rel(y[sel], ry) <= BF16_REL
-    assert _rel(HT[sel], rHT) <= BF16_REL
-    rg = orc.delta_gated_sequential_bwd(*sub, _np(dy[sel]), _np(dHT[sel]))
-    for name, gk, gr in zip(("dQ", "dK", "dV", "dbeta", "dlog_gamma", "dH0"), grads, rg):
-        assert _rel(gk[sel], gr) <= BF16_REL, f"{name} rel err {_rel(gk[sel], gr):.3e}"
+    for sel in ((slice(1, 2), slice(6, 7)), (slice(5, 6), slice(1, 2))):  # pairs 14 and 41
+        sub = [_np(t[sel]) for t in (Q, K, V, beta, lg, H0)]
+        ry, rHT = orc.delta_gated_sequential(*sub)
+        assert _rel(y[sel], ry) <= BF16_REL
+        assert _rel(HT[sel], rHT) <= BF16_REL
+        rg = orc.delta_gated_sequential_bwd(*sub, _np(dy[sel]), _np(dHT[sel]))
+        for name, gk, gr in zip(("dQ", "dK", "dV", "dbeta", "dlog_gamma", "dH0"), grads, rg):
+            assert _rel(gk[sel], gr) <= BF16_REL, f"{name} rel err {_rel(gk[sel], gr):.3e}"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
