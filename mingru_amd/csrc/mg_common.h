@@ -32,10 +32,14 @@
 // launches carry older tags and never validate, so stale contents are
 // harmless.  The epoch lives on the device, so graph replays advance it too.
 // Launches that may overlap (different streams) need different workspaces.
+// The elementwise scans run the persistent form (mg_persistent): resident
+// workgroups take tickets until the work runs out.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <mutex>
 
 #define MG_WAVE 64
 #define MG_HEADER_BYTES 256
@@ -87,6 +91,87 @@ __device__ __forceinline__ MgTicket mg_take_ticket(unsigned* header) {
   }
   __syncthreads();
   return MgTicket{s_ticket, s_epoch};
+}
+
+// Persistent form of the protocol: a 1-D grid of at most as many workgroups as
+// the chip holds at once, and `chunks` tickets of work.  Thread 0 of every
+// workgroup reads the epoch once, then takes tickets from that epoch's counter
+// until one lies past the work; so each workgroup ends on exactly one such ticket
+// and a launch hands out chunks + gridDim.x tickets in all.  The holder of the
+// final one -- taken after every workgroup has read the epoch -- publishes the new
+// epoch, and the holder of ticket 0 resets the other counter, as above.  A ticket
+// past the final one can only come from a workspace that broke the protocol: it
+// is counted as an error and, lying past the work, ends its workgroup.
+__device__ __forceinline__ unsigned mg_next_ticket(unsigned* header, unsigned epoch,
+                                                   unsigned chunks) {
+  const unsigned t = __hip_atomic_fetch_add(header + MG_H_TICKET0 + (epoch & 1u), 1u,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0u)  // the previous launch, which used the other counter, has completed
+    __hip_atomic_store(header + MG_H_TICKET0 + ((epoch + 1u) & 1u), 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned last = chunks + gridDim.x - 1u;
+  if (t == last)
+    __hip_atomic_store(header + MG_H_EPOCH, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else if (t > last)
+    mg_count_error(header);
+  return t;
+}
+
+// Runs body(ticket, epoch) over this workgroup's tickets below `chunks`.  The next
+// ticket's atomic is issued before the current body, so its round trip overlaps
+// the body's work instead of delaying the next chunk's first loads.  Tickets stay
+// monotone in time, so every predecessor of a chunk is held by a running
+// workgroup, as in the one-ticket form.
+template <typename Body>
+__device__ __forceinline__ void mg_persistent(unsigned* header, unsigned chunks, Body&& body) {
+  __shared__ unsigned s_ticket, s_epoch;
+  if (threadIdx.x == 0) {
+    const unsigned e =
+        __hip_atomic_load(header + MG_H_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    s_ticket = mg_next_ticket(header, e, chunks);
+    s_epoch = e;
+  }
+  __syncthreads();
+  unsigned t = s_ticket;
+  const unsigned e = s_epoch;
+  while (t < chunks) {
+    unsigned next = 0u;
+    if (threadIdx.x == 0) next = mg_next_ticket(header, e, chunks);
+    body(t, e);
+    __syncthreads();  // every thread has read s_ticket and finished the body
+    if (threadIdx.x == 0) s_ticket = next;
+    __syncthreads();
+    t = s_ticket;
+  }
+}
+
+// Workgroups of kernel `k` (blocks of `threads`) the current device holds at once,
+// the grid of a persistent launch.  Cached per (kernel, device, block) in a fixed
+// table: no allocation, so allocation-free entry points may call it.
+inline unsigned mg_resident(const void* k, int threads) {
+  struct Entry {
+    const void* k;
+    int dev, threads;
+    unsigned n;
+  };
+  constexpr int CAP = 256;
+  static Entry cache[CAP];
+  static int used = 0;
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == k && cache[i].dev == dev && cache[i].threads == threads) return cache[i].n;
+  int per = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, threads, 0) != hipSuccess || per < 1)
+    per = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 1;
+  const unsigned n = (unsigned)per * (unsigned)cus;
+  if (used < CAP) cache[used++] = Entry{k, dev, threads, n};
+  return n;
 }
 
 __device__ __forceinline__ void mg_slot_put(mg_slot_t* p, float v, unsigned epoch) {

@@ -463,21 +463,15 @@ struct EwThread {
   bool col_ok;
 };
 
-template <int VEC, int TSUB, int WAVES, bool REVERSE, int PH = EW_LOOKBACK>
-__device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header) {
+// The thread's chunk, lane group and columns for ticket `ticket` of the launch:
+// the (lane group, chunk) pair ticket % n_lg, ticket / n_lg (chunks from the end
+// for a REVERSE scan).
+template <int VEC, bool REVERSE>
+__device__ __forceinline__ EwThread ew_thread_at(const EwGeom& g, unsigned ticket,
+                                                 unsigned epoch) {
   EwThread th;
-  unsigned ticket;
-  if constexpr (PH == EW_LOOKBACK) {
-    const MgTicket tk = mg_take_ticket(header);
-    th.valid = tk.ticket < gridDim.x;
-    ticket = th.valid ? tk.ticket : 0u;
-    th.epoch = tk.epoch;
-  } else {
-    // No workgroup waits on another: the workgroup index is the chunk order.
-    th.valid = true;
-    ticket = blockIdx.x;
-    th.epoch = 0u;
-  }
+  th.valid = true;
+  th.epoch = epoch;
   th.lane = threadIdx.x & (MG_WAVE - 1);
   th.w = threadIdx.x / MG_WAVE;
   int k = (int)(ticket / (unsigned)g.n_lg);
@@ -490,6 +484,18 @@ __device__ __forceinline__ EwThread ew_thread(const EwGeom& g, unsigned* header)
   return th;
 }
 
+// Runs body(ticket, epoch) for the chunks of this workgroup: with the look-back
+// (PH = EW_LOOKBACK) a persistent workgroup takes tickets until they run out
+// (mg_persistent); the two-launch forms take one chunk per workgroup, in
+// workgroup order, since no workgroup waits on another.
+template <int PH, typename Body>
+__device__ __forceinline__ void ew_chunks(const EwGeom& g, unsigned* header, Body&& body) {
+  if constexpr (PH == EW_LOOKBACK)
+    mg_persistent(header, (unsigned)g.n_lg * (unsigned)g.n_chunks, body);
+  else
+    body(blockIdx.x, 0u);
+}
+
 // ---------------------------------------------------------------------------
 // Forward of linear_scan: a, b -> A (running product), Bc (zero-start solution).
 // ---------------------------------------------------------------------------
@@ -499,62 +505,63 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
 
-  float av[TSUB][VEC], bv[TSUB][VEC];
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      load_vec<VEC, NT>(av[s], x0 + (th.bb * T + t) * D + th.col);
-      load_vec<VEC, NT>(bv[s], x1 + (th.bb * T + t) * D + th.col);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        av[s][v] = 1.f;
-        bv[s][v] = 0.f;
-      }
-    }
-  }
-
-  Aff<1> loc[VEC], seed[VEC], carry[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    loc[v] = aff_identity<1>();
+    float av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
-      loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
-      loc[v].p *= av[s][v];
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        load_vec<VEC, NT>(av[s], x0 + (th.bb * T + t) * D + th.col);
+        load_vec<VEC, NT>(bv[s], x1 + (th.bb * T + t) * D + th.col);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          av[s][v] = 1.f;
+          bv[s][v] = 0.f;
+        }
+      }
     }
-    seed[v] = aff_identity<1>();
-  }
-  ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                          incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
 
-  float P[VEC], L[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    P[v] = carry[v].p;
-    L[v] = carry[v].l[0];
-  }
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
+    Aff<1> loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      L[v] = fmaf(av[s][v], L[v], bv[s][v]);
-      P[v] *= av[s][v];
+      loc[v] = aff_identity<1>();
+#pragma unroll
+      for (int s = 0; s < TSUB; ++s) {
+        loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
+        loc[v].p *= av[s][v];
+      }
+      seed[v] = aff_identity<1>();
     }
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      store_vec<VEC>(out0 + off, P);
-      store_vec<VEC>(out1 + off, L);
+    ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                            incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+
+    float P[VEC], L[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      P[v] = carry[v].p;
+      L[v] = carry[v].l[0];
     }
-  }
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        L[v] = fmaf(av[s][v], L[v], bv[s][v]);
+        P[v] *= av[s][v];
+      }
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        store_vec<VEC>(out0 + off, P);
+        store_vec<VEC>(out1 + off, L);
+      }
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -569,93 +576,94 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
 
-  float av[TSUB][VEC], bv[TSUB][VEC], xa[TSUB][VEC], xb[TSUB][VEC];
-  float Ap[VEC], Bp[VEC];
+    float av[TSUB][VEC], bv[TSUB][VEC], xa[TSUB][VEC], xb[TSUB][VEC];
+    float Ap[VEC], Bp[VEC];
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      load_vec<VEC, NT>(av[s], a + off);
-      if constexpr (PH != EW_REDUCE) load_vec<VEC>(bv[s], b + off);
-      load_vec<VEC, NT>(xa[s], gA + off);
-      load_vec<VEC, NT>(xb[s], gB + off);
+    for (int s = 0; s < TSUB; ++s) {
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        load_vec<VEC, NT>(av[s], a + off);
+        if constexpr (PH != EW_REDUCE) load_vec<VEC>(bv[s], b + off);
+        load_vec<VEC, NT>(xa[s], gA + off);
+        load_vec<VEC, NT>(xb[s], gB + off);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          av[s][v] = 1.f;
+          bv[s][v] = 0.f;
+          xa[s][v] = 0.f;
+          xb[s][v] = 0.f;
+        }
+      }
+    }
+    if (th.col_ok && t0 > 0 && t0 <= T) {
+      const int64_t off = (th.bb * T + t0 - 1) * D + th.col;
+      load_vec<VEC>(Ap, A + off);
+      load_vec<VEC>(Bp, Bc + off);
     } else {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        av[s][v] = 1.f;
-        bv[s][v] = 0.f;
-        xa[s][v] = 0.f;
-        xb[s][v] = 0.f;
+        Ap[v] = 1.f;
+        Bp[v] = 0.f;
       }
     }
-  }
-  if (th.col_ok && t0 > 0 && t0 <= T) {
-    const int64_t off = (th.bb * T + t0 - 1) * D + th.col;
-    load_vec<VEC>(Ap, A + off);
-    load_vec<VEC>(Bp, Bc + off);
-  } else {
+
+    Aff<2> loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      Ap[v] = 1.f;
-      Bp[v] = 0.f;
-    }
-  }
-
-  Aff<2> loc[VEC], seed[VEC], carry[VEC];
+      loc[v] = aff_identity<2>();
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    loc[v] = aff_identity<2>();
+      for (int s = TSUB - 1; s >= 0; --s) {
+        const float al = av[s][v];
+        loc[v].l[0] = al * (xa[s][v] + loc[v].l[0]);
+        loc[v].l[1] = al * (xb[s][v] + loc[v].l[1]);
+        loc[v].p *= al;
+      }
+      seed[v] = aff_identity<2>();
+    }
+    ew_carry<Aff<2>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                           incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+
+    float ya[VEC], yb[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      ya[v] = carry[v].l[0];
+      yb[v] = carry[v].l[1];
+    }
 #pragma unroll
     for (int s = TSUB - 1; s >= 0; --s) {
-      const float al = av[s][v];
-      loc[v].l[0] = al * (xa[s][v] + loc[v].l[0]);
-      loc[v].l[1] = al * (xb[s][v] + loc[v].l[1]);
-      loc[v].p *= al;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        xa[s][v] += ya[v];
+        xb[s][v] += yb[v];
+        ya[v] = av[s][v] * xa[s][v];
+        yb[v] = av[s][v] * xb[s][v];
+      }
     }
-    seed[v] = aff_identity<2>();
-  }
-  ew_carry<Aff<2>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                         incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
-
-  float ya[VEC], yb[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    ya[v] = carry[v].l[0];
-    yb[v] = carry[v].l[1];
-  }
+    for (int s = 0; s < TSUB; ++s) {
+      float d_a[VEC];
 #pragma unroll
-  for (int s = TSUB - 1; s >= 0; --s) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      xa[s][v] += ya[v];
-      xb[s][v] += yb[v];
-      ya[v] = av[s][v] * xa[s][v];
-      yb[v] = av[s][v] * xb[s][v];
+      for (int v = 0; v < VEC; ++v) {
+        d_a[v] = fmaf(xa[s][v], Ap[v], xb[s][v] * Bp[v]);
+        Bp[v] = fmaf(av[s][v], Bp[v], bv[s][v]);
+        Ap[v] *= av[s][v];
+      }
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        store_vec<VEC>(da + off, d_a);
+        store_vec<VEC>(db + off, xb[s]);
+      }
     }
-  }
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    float d_a[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      d_a[v] = fmaf(xa[s][v], Ap[v], xb[s][v] * Bp[v]);
-      Bp[v] = fmaf(av[s][v], Bp[v], bv[s][v]);
-      Ap[v] *= av[s][v];
-    }
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      store_vec<VEC>(da + off, d_a);
-      store_vec<VEC>(db + off, xb[s]);
-    }
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -690,75 +698,76 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
   constexpr bool NT = PH != EW_REDUCE;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
 
-  Xf av[TSUB][VEC], bv[TSUB][VEC];
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
-      load_xf_exp<VEC, NT>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        av[s][v] = Xf{1.f, 0.f};
-        bv[s][v] = xf_zero();
-      }
-    }
-  }
-
-  XAff loc[VEC], seed[VEC], carry[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    Xf P{1.f, 0.f}, L = xf_zero();
+    Xf av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
-      L = xf_fma(av[s][v], L, bv[s][v]);
-      P = xf_mul(P, av[s][v]);
-    }
-    loc[v] = XAff{xf_norm(P), xf_norm(L)};
-    seed[v] = XAff::identity();
-  }
-  if (th.c == 0 && th.w == 0 && th.col_ok) {
-    Xf h0[VEC];
-    load_xf_exp<VEC>(h0, lv + (th.bb * (T + 1)) * D + th.col);
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
+        load_xf_exp<VEC, NT>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+      } else {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) seed[v].l = h0[v];
-  }
-  ew_carry<XAff, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                        incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
+        for (int v = 0; v < VEC; ++v) {
+          av[s][v] = Xf{1.f, 0.f};
+          bv[s][v] = xf_zero();
+        }
+      }
+    }
 
-  Xf L[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) L[v] = carry[v].l;
-  if (hstate != nullptr && th.col_ok && t0 < T) {
-    const int64_t nsub = (T + TSUB - 1) / TSUB;
-    float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
-    float ss[VEC], se[VEC];
+    XAff loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      ss[v] = L[v].s;
-      se[v] = L[v].e;
-    }
-    store_vec<VEC>(st, ss);
-    store_vec<VEC>(st + D, se);
-  }
+      Xf P{1.f, 0.f}, L = xf_zero();
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    float out[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      L[v] = xf_fma(av[s][v], L[v], bv[s][v]);
-      out[v] = xf_to_float(L[v]);
+      for (int s = 0; s < TSUB; ++s) {
+        L = xf_fma(av[s][v], L, bv[s][v]);
+        P = xf_mul(P, av[s][v]);
+      }
+      loc[v] = XAff{xf_norm(P), xf_norm(L)};
+      seed[v] = XAff::identity();
     }
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, out);
-  }
+    if (th.c == 0 && th.w == 0 && th.col_ok) {
+      Xf h0[VEC];
+      load_xf_exp<VEC>(h0, lv + (th.bb * (T + 1)) * D + th.col);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) seed[v].l = h0[v];
+    }
+    ew_carry<XAff, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                          incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+
+    Xf L[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) L[v] = carry[v].l;
+    if (hstate != nullptr && th.col_ok && t0 < T) {
+      const int64_t nsub = (T + TSUB - 1) / TSUB;
+      float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
+      float ss[VEC], se[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        ss[v] = L[v].s;
+        se[v] = L[v].e;
+      }
+      store_vec<VEC>(st, ss);
+      store_vec<VEC>(st + D, se);
+    }
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      float out[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        L[v] = xf_fma(av[s][v], L[v], bv[s][v]);
+        out[v] = xf_to_float(L[v]);
+      }
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, out);
+    }
+  });
 }
 
 template <int VEC, int WAVES, int PH = EW_LOOKBACK>
@@ -769,107 +778,108 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
   constexpr bool NT = PH != EW_REDUCE;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
 
-  // a as Xf; lv and gh raw until needed.
-  Xf av[TSUB][VEC];
-  float lvr[TSUB][VEC], gr[TSUB][VEC];
+    // a as Xf; lv and gh raw until needed.
+    Xf av[TSUB][VEC];
+    float lvr[TSUB][VEC], gr[TSUB][VEC];
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
-      if constexpr (PH != EW_REDUCE) load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
-      load_vec<VEC, NT>(gr[s], gh + (th.bb * T + t) * D + th.col);
-    } else {
+    for (int s = 0; s < TSUB; ++s) {
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
+        if constexpr (PH != EW_REDUCE) load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+        load_vec<VEC, NT>(gr[s], gh + (th.bb * T + t) * D + th.col);
+      } else {
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        av[s][v] = Xf{1.f, 0.f};
-        lvr[s][v] = -INFINITY;
-        gr[s][v] = 0.f;
+        for (int v = 0; v < VEC; ++v) {
+          av[s][v] = Xf{1.f, 0.f};
+          lvr[s][v] = -INFINITY;
+          gr[s][v] = 0.f;
+        }
       }
     }
-  }
-  // An fp32 value as Xf without normalising: only an exact zero needs exponent -inf.
-  auto raw = [](float x) { return Xf{x, x == 0.f ? -INFINITY : 0.f}; };
+    // An fp32 value as Xf without normalising: only an exact zero needs exponent -inf.
+    auto raw = [](float x) { return Xf{x, x == 0.f ? -INFINITY : 0.f}; };
 
-  XAff loc[VEC], seed[VEC], carry[VEC];
+    XAff loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    Xf P{1.f, 0.f}, L = xf_zero();
+    for (int v = 0; v < VEC; ++v) {
+      Xf P{1.f, 0.f}, L = xf_zero();
+#pragma unroll
+      for (int s = TSUB - 1; s >= 0; --s) {
+        L = xf_mul(av[s][v], xf_add(raw(gr[s][v]), L));
+        P = xf_mul(P, av[s][v]);
+      }
+      loc[v] = XAff{xf_norm(P), xf_norm(L)};
+      seed[v] = XAff::identity();
+    }
+    ew_carry<XAff, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                         incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+
+    // Total adjoint x_s of every step; y ends as a_{t0} x_{t0}.
+    Xf x[TSUB][VEC], y[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) y[v] = carry[v].l;
 #pragma unroll
     for (int s = TSUB - 1; s >= 0; --s) {
-      L = xf_mul(av[s][v], xf_add(raw(gr[s][v]), L));
-      P = xf_mul(P, av[s][v]);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        x[s][v] = xf_add(raw(gr[s][v]), y[v]);
+        y[v] = xf_mul(av[s][v], x[s][v]);
+      }
     }
-    loc[v] = XAff{xf_norm(P), xf_norm(L)};
-    seed[v] = XAff::identity();
-  }
-  ew_carry<XAff, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                       incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
 
-  // Total adjoint x_s of every step; y ends as a_{t0} x_{t0}.
-  Xf x[TSUB][VEC], y[VEC];
+    // h_{t0-1}: e^{lv_0} at the sequence start, else the forward's record.
+    Xf hp[VEC];
+    const bool first_sub = (t0 == 0);
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l;
+    for (int v = 0; v < VEC; ++v) hp[v] = xf_zero();
+    if (th.col_ok && t0 < T) {
+      if (first_sub) {
+        load_xf_exp<VEC>(hp, lv + (th.bb * (T + 1)) * D + th.col);
+      } else if (hstate != nullptr) {
+        const int64_t nsub = (T + TSUB - 1) / TSUB;
+        const float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
+        float ss[VEC], se[VEC];
+        load_vec<VEC>(ss, st);
+        load_vec<VEC>(se, st + D);
 #pragma unroll
-  for (int s = TSUB - 1; s >= 0; --s) {
+        for (int v = 0; v < VEC; ++v) hp[v] = Xf{ss[v], se[v]};
+      } else {
+        float hv[VEC];
+        load_vec<VEC>(hv, h + (th.bb * T + t0 - 1) * D + th.col);
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      x[s][v] = xf_add(raw(gr[s][v]), y[v]);
-      y[v] = xf_mul(av[s][v], x[s][v]);
+        for (int v = 0; v < VEC; ++v) hp[v] = xf_from(hv[v]);
+      }
     }
-  }
-
-  // h_{t0-1}: e^{lv_0} at the sequence start, else the forward's record.
-  Xf hp[VEC];
-  const bool first_sub = (t0 == 0);
+    if (first_sub && th.col_ok) {
+      float d0[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) hp[v] = xf_zero();
-  if (th.col_ok && t0 < T) {
-    if (first_sub) {
-      load_xf_exp<VEC>(hp, lv + (th.bb * (T + 1)) * D + th.col);
-    } else if (hstate != nullptr) {
-      const int64_t nsub = (T + TSUB - 1) / TSUB;
-      const float* st = hstate + ((th.bb * nsub + t0 / TSUB) * 2) * D + th.col;
-      float ss[VEC], se[VEC];
-      load_vec<VEC>(ss, st);
-      load_vec<VEC>(se, st + D);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) hp[v] = Xf{ss[v], se[v]};
-    } else {
-      float hv[VEC];
-      load_vec<VEC>(hv, h + (th.bb * T + t0 - 1) * D + th.col);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) hp[v] = xf_from(hv[v]);
+      for (int v = 0; v < VEC; ++v) d0[v] = xf_to_float(xf_mul(y[v], hp[v]));
+      store_vec<VEC>(dlv + (th.bb * (T + 1)) * D + th.col, d0);
     }
-  }
-  if (first_sub && th.col_ok) {
-    float d0[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) d0[v] = xf_to_float(xf_mul(y[v], hp[v]));
-    store_vec<VEC>(dlv + (th.bb * (T + 1)) * D + th.col, d0);
-  }
+    for (int s = 0; s < TSUB; ++s) {
+      float d_c[VEC], d_v[VEC];
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    float d_c[VEC], d_v[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const Xf b = lvr[s][v] == -INFINITY ? xf_zero() : xf_exp(lvr[s][v]);
-      d_c[v] = xf_to_float(xf_mul(xf_mul(x[s][v], av[s][v]), hp[v]));
-      d_v[v] = xf_to_float(xf_mul(x[s][v], b));
-      hp[v] = xf_fma(av[s][v], hp[v], b);
+      for (int v = 0; v < VEC; ++v) {
+        const Xf b = lvr[s][v] == -INFINITY ? xf_zero() : xf_exp(lvr[s][v]);
+        d_c[v] = xf_to_float(xf_mul(xf_mul(x[s][v], av[s][v]), hp[v]));
+        d_v[v] = xf_to_float(xf_mul(x[s][v], b));
+        hp[v] = xf_fma(av[s][v], hp[v], b);
+      }
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        store_vec<VEC>(dlc + (th.bb * T + t) * D + th.col, d_c);
+        store_vec<VEC>(dlv + (th.bb * (T + 1) + t + 1) * D + th.col, d_v);
+      }
     }
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      store_vec<VEC>(dlc + (th.bb * T + t) * D + th.col, d_c);
-      store_vec<VEC>(dlv + (th.bb * (T + 1) + t + 1) * D + th.col, d_v);
-    }
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -898,62 +908,63 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  EwThread th = ew_thread<VEC, TSUB, WAVES, false, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
 
-  float av[TSUB][VEC], bv[TSUB][VEC];
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      float x0[VEC], x1[VEC], x2[VEC];
-      load_vec<VEC, NT>(x0, p0 + off);
-      load_vec<VEC, NT>(x1, p1 + off);
-      if constexpr (gate_inputs<G>() == 3) load_vec<VEC, NT>(x2, p2 + off);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v)
-        gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        av[s][v] = 1.f;
-        bv[s][v] = 0.f;
-      }
-    }
-  }
-  Aff<1> loc[VEC], seed[VEC], carry[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    loc[v] = aff_identity<1>();
+    float av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
-      loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
-      loc[v].p *= av[s][v];
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        float x0[VEC], x1[VEC], x2[VEC];
+        load_vec<VEC, NT>(x0, p0 + off);
+        load_vec<VEC, NT>(x1, p1 + off);
+        if constexpr (gate_inputs<G>() == 3) load_vec<VEC, NT>(x2, p2 + off);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+          gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          av[s][v] = 1.f;
+          bv[s][v] = 0.f;
+        }
+      }
     }
-    seed[v] = aff_identity<1>();
-  }
-  if (th.c == 0 && th.w == 0 && th.col_ok) {
-    float x[VEC];
-    load_vec<VEC>(x, h0 + th.bb * D + th.col);
+    Aff<1> loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) seed[v].l[0] = G == GATE_MINGRU ? expf(x[v]) : x[v];
-  }
-  ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                          incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
-  float L[VEC];
+    for (int v = 0; v < VEC; ++v) {
+      loc[v] = aff_identity<1>();
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) L[v] = carry[v].l[0];
+      for (int s = 0; s < TSUB; ++s) {
+        loc[v].l[0] = fmaf(av[s][v], loc[v].l[0], bv[s][v]);
+        loc[v].p *= av[s][v];
+      }
+      seed[v] = aff_identity<1>();
+    }
+    if (th.c == 0 && th.w == 0 && th.col_ok) {
+      float x[VEC];
+      load_vec<VEC>(x, h0 + th.bb * D + th.col);
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
+      for (int v = 0; v < VEC; ++v) seed[v].l[0] = G == GATE_MINGRU ? expf(x[v]) : x[v];
+    }
+    ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                            incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+    float L[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) L[v] = fmaf(av[s][v], L[v], bv[s][v]);
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, L);
-  }
+    for (int v = 0; v < VEC; ++v) L[v] = carry[v].l[0];
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) L[v] = fmaf(av[s][v], L[v], bv[s][v]);
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) store_vec<VEC>(h + (th.bb * T + t) * D + th.col, L);
+    }
+  });
 }
 
 // Backward: x_t = dL/dh_t in total (reverse scan of g_t with the a's), then
@@ -967,139 +978,140 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     float* __restrict__ d0, float* __restrict__ d1, float* __restrict__ d2,
     float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
-  EwThread th = ew_thread<VEC, TSUB, WAVES, true, PH>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, D = g.D;
-  constexpr bool MIN = G == GATE_MINGRU;
-  constexpr bool NT = PH != EW_REDUCE;
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+    EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, D = g.D;
+    constexpr bool MIN = G == GATE_MINGRU;
+    constexpr bool NT = PH != EW_REDUCE;
 
-  float ua[TSUB][VEC], ub[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
+    float ua[TSUB][VEC], ub[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
 #pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      float x0[VEC];
-      load_vec<VEC, NT>(x0, p0 + off);
-      load_vec<VEC, NT>(x[s], gh + off);
-      if constexpr (MIN) {
-        if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p1 + off);
+    for (int s = 0; s < TSUB; ++s) {
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        float x0[VEC];
+        load_vec<VEC, NT>(x0, p0 + off);
+        load_vec<VEC, NT>(x[s], gh + off);
+        if constexpr (MIN) {
+          if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p1 + off);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          ua[s][v] = mg_sigmoid(-x0[v]);  // a
-          ub[s][v] = mg_sigmoid(x0[v]);   // z
+          for (int v = 0; v < VEC; ++v) {
+            ua[s][v] = mg_sigmoid(-x0[v]);  // a
+            ub[s][v] = mg_sigmoid(x0[v]);   // z
+          }
+        } else {
+          float x1[VEC];
+          load_vec<VEC, NT>(x1, p1 + off);
+          if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p2 + off);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            ua[s][v] = mg_sigmoid(x1[v]);  // sigmoid(z)
+            ub[s][v] = mg_tanh(x0[v]);     // tanh(s)
+          }
         }
       } else {
-        float x1[VEC];
-        load_vec<VEC, NT>(x1, p1 + off);
-        if constexpr (PH != EW_REDUCE) load_vec<VEC>(hv[s], p2 + off);
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
-          ua[s][v] = mg_sigmoid(x1[v]);  // sigmoid(z)
-          ub[s][v] = mg_tanh(x0[v]);     // tanh(s)
+          ua[s][v] = 0.f;  // a = 0 closes the adjoint chain past T
+          ub[s][v] = 0.f;
+          hv[s][v] = 0.f;
+          x[s][v] = 0.f;
         }
       }
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        ua[s][v] = 0.f;  // a = 0 closes the adjoint chain past T
-        ub[s][v] = 0.f;
-        hv[s][v] = 0.f;
-        x[s][v] = 0.f;
-      }
     }
-  }
-  auto coef_a = [&](int s, int v) {
-    if constexpr (MIN) return ua[s][v];
-    else if constexpr (G == GATE_SIGNED_COUPLED) return (1.f - ua[s][v]) * ub[s][v];
-    else return ub[s][v];
-  };
-  const bool first_sub = (t0 == 0);
-  float hprev[VEC];
-  if (th.col_ok && t0 <= T) {
-    if (first_sub) {
-      load_vec<VEC>(hprev, h0 + th.bb * D + th.col);
-      if constexpr (MIN) {
+    auto coef_a = [&](int s, int v) {
+      if constexpr (MIN) return ua[s][v];
+      else if constexpr (G == GATE_SIGNED_COUPLED) return (1.f - ua[s][v]) * ub[s][v];
+      else return ub[s][v];
+    };
+    const bool first_sub = (t0 == 0);
+    float hprev[VEC];
+    if (th.col_ok && t0 <= T) {
+      if (first_sub) {
+        load_vec<VEC>(hprev, h0 + th.bb * D + th.col);
+        if constexpr (MIN) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) hprev[v] = expf(hprev[v]);
+          for (int v = 0; v < VEC; ++v) hprev[v] = expf(hprev[v]);
+        }
+      } else {
+        load_vec<VEC>(hprev, h + (th.bb * T + t0 - 1) * D + th.col);
       }
     } else {
-      load_vec<VEC>(hprev, h + (th.bb * T + t0 - 1) * D + th.col);
-    }
-  } else {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) hprev[v] = 0.f;
-  }
+      for (int v = 0; v < VEC; ++v) hprev[v] = 0.f;
+    }
 
-  Aff<1> loc[VEC], seed[VEC], carry[VEC];
+    Aff<1> loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    loc[v] = aff_identity<1>();
+    for (int v = 0; v < VEC; ++v) {
+      loc[v] = aff_identity<1>();
+#pragma unroll
+      for (int s = TSUB - 1; s >= 0; --s) {
+        const float a = coef_a(s, v);
+        loc[v].l[0] = a * (x[s][v] + loc[v].l[0]);
+        loc[v].p *= a;
+      }
+      seed[v] = aff_identity<1>();
+    }
+    ew_carry<Aff<1>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                           incl_data, carry);
+    if constexpr (PH == EW_REDUCE) return;
+    float y[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
 #pragma unroll
     for (int s = TSUB - 1; s >= 0; --s) {
-      const float a = coef_a(s, v);
-      loc[v].l[0] = a * (x[s][v] + loc[v].l[0]);
-      loc[v].p *= a;
-    }
-    seed[v] = aff_identity<1>();
-  }
-  ew_carry<Aff<1>, VEC, WAVES, true, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
-                                         incl_data, carry);
-  if constexpr (PH == EW_REDUCE) return;
-  float y[VEC];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) y[v] = carry[v].l[0];
-#pragma unroll
-  for (int s = TSUB - 1; s >= 0; --s) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      x[s][v] += y[v];
-      y[v] = coef_a(s, v) * x[s][v];
-    }
-  }
-  if (first_sub && th.col_ok) {
-    // dL/dh0 = a_1 x_1; the MinGRU input is log h0: times h0.
-    if constexpr (MIN) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) y[v] *= hprev[v];
-    }
-    store_vec<VEC>(dh0 + th.bb * D + th.col, y);
-  }
-#pragma unroll
-  for (int s = 0; s < TSUB; ++s) {
-    float o0[VEC], o1[VEC], o2[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const float xv = x[s][v], da = xv * hprev[v];  // dL/da_t
-      float a, b;
-      if constexpr (MIN) {
-        // a = sigmoid(-k): da/dk = -a z;  b = z g(hpre): db/dk = z a g, db/dhpre = z g'.
-        const float hp = hv[s][v], am = ua[s][v], zk = ub[s][v];
-        const float gv = hp >= 0.f ? hp + 0.5f : mg_sigmoid(hp);
-        const float gp = hp >= 0.f ? 1.f : gv * (1.f - gv);
-        a = am;
-        b = zk * gv;
-        o0[v] = (xv * gv - da) * am * zk;
-        o1[v] = xv * zk * gp;
-      } else {
-        const float sg = ua[s][v], tv = ub[s][v], dsg = sg * (1.f - sg);
-        a = G == GATE_SIGNED_COUPLED ? (1.f - sg) * tv : tv;
-        b = sg * hv[s][v];
-        o0[v] = da * (G == GATE_SIGNED_COUPLED ? (1.f - sg) : 1.f) * (1.f - tv * tv);
-        o1[v] = xv * hv[s][v] * dsg - (G == GATE_SIGNED_COUPLED ? da * tv * dsg : 0.f);
-        o2[v] = xv * sg;
+      for (int v = 0; v < VEC; ++v) {
+        x[s][v] += y[v];
+        y[v] = coef_a(s, v) * x[s][v];
       }
-      hprev[v] = fmaf(a, hprev[v], b);
     }
-    const int64_t t = t0 + s;
-    if (th.col_ok && t < T) {
-      const int64_t off = (th.bb * T + t) * D + th.col;
-      store_vec<VEC>(d0 + off, o0);
-      store_vec<VEC>(d1 + off, o1);
-      if constexpr (!MIN) store_vec<VEC>(d2 + off, o2);
+    if (first_sub && th.col_ok) {
+      // dL/dh0 = a_1 x_1; the MinGRU input is log h0: times h0.
+      if constexpr (MIN) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) y[v] *= hprev[v];
+      }
+      store_vec<VEC>(dh0 + th.bb * D + th.col, y);
     }
-  }
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      float o0[VEC], o1[VEC], o2[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float xv = x[s][v], da = xv * hprev[v];  // dL/da_t
+        float a, b;
+        if constexpr (MIN) {
+          // a = sigmoid(-k): da/dk = -a z;  b = z g(hpre): db/dk = z a g, db/dhpre = z g'.
+          const float hp = hv[s][v], am = ua[s][v], zk = ub[s][v];
+          const float gv = hp >= 0.f ? hp + 0.5f : mg_sigmoid(hp);
+          const float gp = hp >= 0.f ? 1.f : gv * (1.f - gv);
+          a = am;
+          b = zk * gv;
+          o0[v] = (xv * gv - da) * am * zk;
+          o1[v] = xv * zk * gp;
+        } else {
+          const float sg = ua[s][v], tv = ub[s][v], dsg = sg * (1.f - sg);
+          a = G == GATE_SIGNED_COUPLED ? (1.f - sg) * tv : tv;
+          b = sg * hv[s][v];
+          o0[v] = da * (G == GATE_SIGNED_COUPLED ? (1.f - sg) : 1.f) * (1.f - tv * tv);
+          o1[v] = xv * hv[s][v] * dsg - (G == GATE_SIGNED_COUPLED ? da * tv * dsg : 0.f);
+          o2[v] = xv * sg;
+        }
+        hprev[v] = fmaf(a, hprev[v], b);
+      }
+      const int64_t t = t0 + s;
+      if (th.col_ok && t < T) {
+        const int64_t off = (th.bb * T + t) * D + th.col;
+        store_vec<VEC>(d0 + off, o0);
+        store_vec<VEC>(d1 + off, o1);
+        if constexpr (!MIN) store_vec<VEC>(d2 + off, o2);
+      }
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -1165,11 +1177,14 @@ bool geometry_ok(int64_t B, int64_t T, int64_t D) {
 }
 
 template <typename Kernel, typename... Args>
-int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, Args... args) {
+int ew_launch(Kernel k, const EwPlan& p, void* ws, hipStream_t stream, bool persistent,
+              Args... args) {
   unsigned* header = (unsigned*)ws;
   mg_slot_t* agg = (mg_slot_t*)((char*)ws + p.agg_off);
   mg_slot_t* incl = (mg_slot_t*)((char*)ws + p.incl_off);
-  const unsigned grid = (unsigned)p.g.n_lg * (unsigned)p.g.n_chunks;
+  const unsigned chunks = (unsigned)p.g.n_lg * (unsigned)p.g.n_chunks;
+  const unsigned grid =
+      persistent ? std::min(chunks, mg_resident((const void*)k, MG_WAVE * p.waves)) : chunks;
   hipLaunchKernelGGL(k, dim3(grid), dim3(MG_WAVE * p.waves), 0, stream, args..., p.g, header,
                      agg, incl);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
@@ -1187,9 +1202,9 @@ bool ew_two_launch(const EwPlan& p, int64_t B, int64_t T, int64_t D, int arrays)
 template <typename K0, typename K1, typename K2, typename... Args>
 int ew_run(bool two, K0 lookback, K1 reduce, K2 fin, const EwPlan& p, void* ws,
            hipStream_t stream, Args... args) {
-  if (!two) return ew_launch(lookback, p, ws, stream, args...);
-  const int rc = ew_launch(reduce, p, ws, stream, args...);
-  return rc != MG_OK ? rc : ew_launch(fin, p, ws, stream, args...);
+  if (!two) return ew_launch(lookback, p, ws, stream, true, args...);
+  const int rc = ew_launch(reduce, p, ws, stream, false, args...);
+  return rc != MG_OK ? rc : ew_launch(fin, p, ws, stream, false, args...);
 }
 
 size_t ew_ws_bytes(int64_t B, int64_t T, int64_t D) {
