@@ -256,6 +256,27 @@ __device__ __forceinline__ AfThread af_thread(const AfGeom& g, unsigned* header)
   return th;
 }
 
+// The thread's chunk, lane group and plane for ticket `ticket` of a persistent
+// look-back launch (mg_persistent): the (lane group, chunk) pair ticket % n_lg,
+// ticket / n_lg (chunks from the end for the REVERSE backward).
+template <bool REVERSE>
+__device__ __forceinline__ AfThread af_thread_at(const AfGeom& g, unsigned ticket,
+                                                 unsigned epoch) {
+  AfThread th;
+  th.valid = true;
+  th.epoch = epoch;
+  th.lane = threadIdx.x & (MG_WAVE - 1);
+  th.w = threadIdx.x / MG_WAVE;
+  int kk = (int)(ticket / (unsigned)g.n_lg);
+  th.lg = (int)(ticket - (unsigned)kk * (unsigned)g.n_lg);
+  th.c = REVERSE ? g.n_chunks - 1 - kk : kk;
+  th.bb = th.lg / g.n_tiles;
+  const int tile = th.lg - th.bb * g.n_tiles;
+  th.plane = (int64_t)tile * MG_WAVE + th.lane;
+  th.ok = th.plane < g.n;
+  return th;
+}
+
 // 8x8 and 16x16 blocks run on the matrix cores (scan_affine_mfma.hip).
 size_t affine_mfma_workspace_bytes(int64_t B, int64_t T, int64_t n, int k);
 bool affine_mfma_geometry_ok(int64_t B, int64_t T, int64_t n, int k);

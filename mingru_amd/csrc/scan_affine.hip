@@ -176,221 +176,223 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
   constexpr bool HOLD = af_hold<K, V>();
   constexpr int HS = HOLD ? TSUB : 1;
   constexpr int W = K + V;  // adjoint state: [XA | XB]
-  AfThread th = af_thread<true>(g, header);
-  if (!th.valid) return;
-  const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-  const int64_t T = g.T, n = g.n;
-  auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
-  auto offB = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * V); };
+  mg_persistent(header, (unsigned)g.n_lg * (unsigned)g.n_chunks,
+                [&](unsigned ticket, unsigned epoch) {
+    AfThread th = af_thread_at<true>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    const int64_t T = g.T, n = g.n;
+    auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
+    auto offB = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * V); };
 
-  float ha[HS][K * K], hb[HS][K * V], hga[HS][K * K], hgb[HS][K * V];
-  auto fetch = [&](int s, float* a, float* b, float* ga, float* gb, bool need_b) {
-    const int64_t t = t0 + s;
-    if (th.ok && t < T) {
-      ld<K * K, HOLD>(a, A + offA(t));
-      if (need_b) ld<K * V, HOLD>(b, Bm + offB(t));
-      ld<K * K, HOLD>(ga, GA + offA(t));
-      ld<K * V, HOLD>(gb, GB + offB(t));
-    } else {
+    float ha[HS][K * K], hb[HS][K * V], hga[HS][K * K], hgb[HS][K * V];
+    auto fetch = [&](int s, float* a, float* b, float* ga, float* gb, bool need_b) {
+      const int64_t t = t0 + s;
+      if (th.ok && t < T) {
+        ld<K * K, HOLD>(a, A + offA(t));
+        if (need_b) ld<K * V, HOLD>(b, Bm + offB(t));
+        ld<K * K, HOLD>(ga, GA + offA(t));
+        ld<K * V, HOLD>(gb, GB + offB(t));
+      } else {
 #pragma unroll
-      for (int i = 0; i < K * K; ++i) {
-        a[i] = (i / K == i % K) ? 1.f : 0.f;
-        ga[i] = 0.f;
+        for (int i = 0; i < K * K; ++i) {
+          a[i] = (i / K == i % K) ? 1.f : 0.f;
+          ga[i] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < K * V; ++i) {
+          b[i] = 0.f;
+          gb[i] = 0.f;
+        }
       }
-#pragma unroll
-      for (int i = 0; i < K * V; ++i) {
-        b[i] = 0.f;
-        gb[i] = 0.f;
-      }
-    }
-  };
-  if constexpr (HOLD) {
-#pragma unroll
-    for (int s = 0; s < TSUB; ++s) fetch(s, ha[s], hb[s], hga[s], hgb[s], true);
-  }
-
-  // Local reverse aggregate: Y -> A_t^T (G_t + Y), composed from the end.
-  AffM<K, W> loc, carry;
-  affm_identity(loc);
-#pragma unroll
-  for (int s = TSUB - 1; s >= 0; --s) {
-    float a[K * K], b[K * V], ga[K * K], gb[K * V];
+    };
     if constexpr (HOLD) {
 #pragma unroll
-      for (int i = 0; i < K * K; ++i) { a[i] = ha[s][i]; ga[i] = hga[s][i]; }
-#pragma unroll
-      for (int i = 0; i < K * V; ++i) { b[i] = hb[s][i]; gb[i] = hgb[s][i]; }
-    } else {
-      fetch(s, a, b, ga, gb, false);
+      for (int s = 0; s < TSUB; ++s) fetch(s, ha[s], hb[s], hga[s], hgb[s], true);
     }
-    AffM<K, W> nx;
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-#pragma unroll
-      for (int j = 0; j < K; ++j) {
-        float acc = 0.f;
-#pragma unroll
-        for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], loc.P[m][j], acc);
-        nx.P[i][j] = acc;
-      }
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        float acc = 0.f;
-#pragma unroll
-        for (int m = 0; m < K; ++m) {
-          const float gmj = j < K ? ga[m * K + j] : gb[m * V + (j - K)];
-          acc = fmaf(a[m * K + i], gmj + loc.L[m][j], acc);
-        }
-        nx.L[i][j] = acc;
-      }
-    }
-    loc = nx;
-  }
-  AffM<K, W> seed;
-  affm_identity(seed);
-  af_carry<K, W, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
 
-  // Y entering the sub-chunk from the right (Y_T = 0 seed applied).
-  float Y[K][W];
-#pragma unroll
-  for (int i = 0; i < K; ++i)
-#pragma unroll
-    for (int j = 0; j < W; ++j) Y[i][j] = carry.L[i][j];
-
-  if constexpr (HOLD) {
-    // Reverse sweep: X_t = G_t + Y; Y <- A_t^T X_t; keep X_t in place of G_t.
+    // Local reverse aggregate: Y -> A_t^T (G_t + Y), composed from the end.
+    AffM<K, W> loc, carry;
+    affm_identity(loc);
 #pragma unroll
     for (int s = TSUB - 1; s >= 0; --s) {
-      float X[K][W];
+      float a[K * K], b[K * V], ga[K * K], gb[K * V];
+      if constexpr (HOLD) {
 #pragma unroll
-      for (int i = 0; i < K; ++i)
+        for (int i = 0; i < K * K; ++i) { a[i] = ha[s][i]; ga[i] = hga[s][i]; }
 #pragma unroll
-        for (int j = 0; j < W; ++j)
-          X[i][j] = (j < K ? hga[s][i * K + j] : hgb[s][i * V + (j - K)]) + Y[i][j];
-#pragma unroll
-      for (int i = 0; i < K; ++i)
-#pragma unroll
-        for (int j = 0; j < W; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][m * K + i], X[m][j], acc);
-          Y[i][j] = acc;
-        }
-#pragma unroll
-      for (int i = 0; i < K; ++i)
-#pragma unroll
-        for (int j = 0; j < W; ++j) {
-          if (j < K) hga[s][i * K + j] = X[i][j];
-          else hgb[s][i * V + (j - K)] = X[i][j];
-        }
-    }
-    // Forward sweep: recompute (Abar_{t-1}, Bbar_{t-1}) from the saved boundary.
-    float Sa[K * K], Sb[K * V];
-    if (th.ok && t0 > 0 && t0 <= T) {
-      ld<K * K>(Sa, Abar + offA(t0 - 1));
-      ld<K * V>(Sb, Bbar + offB(t0 - 1));
-    } else {
-#pragma unroll
-      for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
-#pragma unroll
-      for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < TSUB; ++s) {
-      float d[K * K];
-#pragma unroll
-      for (int i = 0; i < K; ++i)
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(hga[s][i * K + m], Sa[j * K + m], acc);
-#pragma unroll
-          for (int m = 0; m < V; ++m) acc = fmaf(hgb[s][i * V + m], Sb[j * V + m], acc);
-          d[i * K + j] = acc;
-        }
-      float na[K * K], nb[K * V];
+        for (int i = 0; i < K * V; ++i) { b[i] = hb[s][i]; gb[i] = hgb[s][i]; }
+      } else {
+        fetch(s, a, b, ga, gb, false);
+      }
+      AffM<K, W> nx;
 #pragma unroll
       for (int i = 0; i < K; ++i) {
 #pragma unroll
         for (int j = 0; j < K; ++j) {
           float acc = 0.f;
 #pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sa[m * K + j], acc);
-          na[i * K + j] = acc;
+          for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], loc.P[m][j], acc);
+          nx.P[i][j] = acc;
         }
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-          float acc = hb[s][i * V + j];
+        for (int j = 0; j < W; ++j) {
+          float acc = 0.f;
 #pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sb[m * V + j], acc);
-          nb[i * V + j] = acc;
+          for (int m = 0; m < K; ++m) {
+            const float gmj = j < K ? ga[m * K + j] : gb[m * V + (j - K)];
+            acc = fmaf(a[m * K + i], gmj + loc.L[m][j], acc);
+          }
+          nx.L[i][j] = acc;
         }
       }
-#pragma unroll
-      for (int i = 0; i < K * K; ++i) Sa[i] = na[i];
-#pragma unroll
-      for (int i = 0; i < K * V; ++i) Sb[i] = nb[i];
-      const int64_t t = t0 + s;
-      if (th.ok && t < T) {
-        st<K * K, true>(dA + offA(t), d);
-        st<K * V, true>(dB + offB(t), hgb[s]);
-      }
+      loc = nx;
     }
-  } else {
-    // Single reverse sweep reading the saved forward outputs.
-    for (int s = TSUB - 1; s >= 0; --s) {
-      const int64_t t = t0 + s;
-      if (!(th.ok && t < T)) continue;
-      float a[K * K], ga[K * K], gb[K * V], b_unused[1];
-      (void)b_unused;
-      ld<K * K>(a, A + offA(t));
-      ld<K * K>(ga, GA + offA(t));
-      ld<K * V>(gb, GB + offB(t));
+    AffM<K, W> seed;
+    affm_identity(seed);
+    af_carry<K, W, WAVES, true>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data, incl_data, carry);
+
+    // Y entering the sub-chunk from the right (Y_T = 0 seed applied).
+    float Y[K][W];
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int j = 0; j < W; ++j) Y[i][j] = carry.L[i][j];
+
+    if constexpr (HOLD) {
+      // Reverse sweep: X_t = G_t + Y; Y <- A_t^T X_t; keep X_t in place of G_t.
+#pragma unroll
+      for (int s = TSUB - 1; s >= 0; --s) {
+        float X[K][W];
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+          for (int j = 0; j < W; ++j)
+            X[i][j] = (j < K ? hga[s][i * K + j] : hgb[s][i * V + (j - K)]) + Y[i][j];
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < K; ++m) acc = fmaf(ha[s][m * K + i], X[m][j], acc);
+            Y[i][j] = acc;
+          }
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            if (j < K) hga[s][i * K + j] = X[i][j];
+            else hgb[s][i * V + (j - K)] = X[i][j];
+          }
+      }
+      // Forward sweep: recompute (Abar_{t-1}, Bbar_{t-1}) from the saved boundary.
       float Sa[K * K], Sb[K * V];
-      if (t > 0) {
-        ld<K * K>(Sa, Abar + offA(t - 1));
-        ld<K * V>(Sb, Bbar + offB(t - 1));
+      if (th.ok && t0 > 0 && t0 <= T) {
+        ld<K * K>(Sa, Abar + offA(t0 - 1));
+        ld<K * V>(Sb, Bbar + offB(t0 - 1));
       } else {
 #pragma unroll
         for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
 #pragma unroll
         for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
       }
-      float X[K][W];
 #pragma unroll
-      for (int i = 0; i < K; ++i)
+      for (int s = 0; s < TSUB; ++s) {
+        float d[K * K];
 #pragma unroll
-        for (int j = 0; j < W; ++j)
-          X[i][j] = (j < K ? ga[i * K + j] : gb[i * V + (j - K)]) + Y[i][j];
-      float d[K * K], xb[K * V];
+        for (int i = 0; i < K; ++i)
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
+          for (int j = 0; j < K; ++j) {
+            float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < K; ++j) {
-          float acc = 0.f;
+            for (int m = 0; m < K; ++m) acc = fmaf(hga[s][i * K + m], Sa[j * K + m], acc);
 #pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(X[i][m], Sa[j * K + m], acc);
+            for (int m = 0; m < V; ++m) acc = fmaf(hgb[s][i * V + m], Sb[j * V + m], acc);
+            d[i * K + j] = acc;
+          }
+        float na[K * K], nb[K * V];
 #pragma unroll
-          for (int m = 0; m < V; ++m) acc = fmaf(X[i][K + m], Sb[j * V + m], acc);
-          d[i * K + j] = acc;
+        for (int i = 0; i < K; ++i) {
+#pragma unroll
+          for (int j = 0; j < K; ++j) {
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sa[m * K + j], acc);
+            na[i * K + j] = acc;
+          }
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            float acc = hb[s][i * V + j];
+#pragma unroll
+            for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sb[m * V + j], acc);
+            nb[i * V + j] = acc;
+          }
         }
 #pragma unroll
-        for (int j = 0; j < V; ++j) xb[i * V + j] = X[i][K + j];
+        for (int i = 0; i < K * K; ++i) Sa[i] = na[i];
+#pragma unroll
+        for (int i = 0; i < K * V; ++i) Sb[i] = nb[i];
+        const int64_t t = t0 + s;
+        if (th.ok && t < T) {
+          st<K * K, true>(dA + offA(t), d);
+          st<K * V, true>(dB + offB(t), hgb[s]);
+        }
       }
-      st<K * K, true>(dA + offA(t), d);
-      st<K * V, true>(dB + offB(t), xb);
+    } else {
+      // Single reverse sweep reading the saved forward outputs.
+      for (int s = TSUB - 1; s >= 0; --s) {
+        const int64_t t = t0 + s;
+        if (!(th.ok && t < T)) continue;
+        float a[K * K], ga[K * K], gb[K * V], b_unused[1];
+        (void)b_unused;
+        ld<K * K>(a, A + offA(t));
+        ld<K * K>(ga, GA + offA(t));
+        ld<K * V>(gb, GB + offB(t));
+        float Sa[K * K], Sb[K * V];
+        if (t > 0) {
+          ld<K * K>(Sa, Abar + offA(t - 1));
+          ld<K * V>(Sb, Bbar + offB(t - 1));
+        } else {
 #pragma unroll
-      for (int i = 0; i < K; ++i)
+          for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], X[m][j], acc);
-          Y[i][j] = acc;
+          for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
         }
+        float X[K][W];
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+          for (int j = 0; j < W; ++j)
+            X[i][j] = (j < K ? ga[i * K + j] : gb[i * V + (j - K)]) + Y[i][j];
+        float d[K * K], xb[K * V];
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+#pragma unroll
+          for (int j = 0; j < K; ++j) {
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < K; ++m) acc = fmaf(X[i][m], Sa[j * K + m], acc);
+#pragma unroll
+            for (int m = 0; m < V; ++m) acc = fmaf(X[i][K + m], Sb[j * V + m], acc);
+            d[i * K + j] = acc;
+          }
+#pragma unroll
+          for (int j = 0; j < V; ++j) xb[i * V + j] = X[i][K + j];
+        }
+        st<K * K, true>(dA + offA(t), d);
+        st<K * V, true>(dB + offB(t), xb);
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < K; ++m) acc = fmaf(a[m * K + i], X[m][j], acc);
+            Y[i][j] = acc;
+          }
+      }
     }
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -462,8 +464,10 @@ int af_launch_bwd(const float* A, const float* Bm, const float* Abar, const floa
   AfPlan p = af_plan(B, T, n, WV, TS, K * K + K * (K + V));
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   unsigned* header = (unsigned*)ws;
-  hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, WV>),
-                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * WV), 0,
+  const unsigned chunks = (unsigned)(p.g.n_lg * p.g.n_chunks);
+  const unsigned grid =
+      std::min(chunks, mg_resident((const void*)&affine_bwd_kernel<K, V, TS, WV>, MG_WAVE * WV));
+  hipLaunchKernelGGL((affine_bwd_kernel<K, V, TS, WV>), dim3(grid), dim3(MG_WAVE * WV), 0,
                      stream, A, Bm, Abar, Bbar, GA, GB, dA, dB, p.g, header,
                      (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
