@@ -39,7 +39,7 @@ namespace {
 
 // Chunk = WAVES * TSUB time steps per workgroup.
 constexpr int EW_WAVES_FWD = 8;
-constexpr int EW_TSUB_FWD = 16;
+constexpr int EW_TSUB_FWD = 8;
 constexpr int EW_WAVES_BWD = 8;
 constexpr int EW_TSUB_BWD = 8;
 // Fused gate backward: four arrays per step stay live (sigmoid, tanh, hpre,

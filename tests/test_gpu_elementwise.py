@@ -51,11 +51,11 @@ LINEAR_SHAPES = [
     # the launch picks 4 columns per lane here, 2 at D=128 below, 1 for the small shapes
     (8, 2048, 512),
     (32, 1024, 128),
-    # launch forms (128-step forward and 64-step backward chunks; at most 32 chunks and
-    # 32 MB of inputs run as two launches): both directions two-launch, forward
-    # two-launch with a look-back backward, both look-back
+    # launch forms (64-step chunks both ways; at most 32 chunks and 32 MB of inputs run
+    # as two launches): both directions two-launch; forward two-launch with a look-back
+    # backward (its four input arrays pass 32 MB); both look-back
     (2, 2048, 64),
-    (2, 4096, 64),
+    (2, 2048, 640),
     (2, 4097, 64),
 ]
 

@@ -31,7 +31,7 @@ def test_epoch_advances_and_results_repeat(cuda):
     print("[gpu] workspace epochs", flush=True)
     lib = _native.load()
     g = torch.Generator().manual_seed(5)
-    B, T, D = 3, 4225, 136  # 34 chunks per sequence: the look-back launch (tickets, epochs)
+    B, T, D = 3, 4225, 136  # 67 chunks per sequence: the look-back launch (tickets, epochs)
     a = torch.tanh(torch.randn(B, T, D, generator=g)).to(cuda)
     b = torch.randn(B, T, D, generator=g).to(cuda)
     nbytes = lib.mg_linear_scan_workspace_bytes(B, T, D)
@@ -113,7 +113,7 @@ def test_broken_workspace_is_reported_not_silent(cuda, monkeypatch):
     MINGRU_HIP_CHECK=1, as a LookbackError.  The workspace is private to this test."""
     print("[gpu] broken workspace reporting", flush=True)
     lib = _native.load()
-    B, T, D = 2, 4225, 64  # 34 chunks per sequence: the look-back launch, which takes tickets
+    B, T, D = 2, 4225, 64  # 67 chunks per sequence: the look-back launch, which takes tickets
     a = torch.rand(B, T, D, device=cuda)
     b = torch.randn(B, T, D, device=cuda)
     nbytes = lib.mg_linear_scan_workspace_bytes(B, T, D)
