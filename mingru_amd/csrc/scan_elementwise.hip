@@ -505,12 +505,12 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     float* __restrict__ out1, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
-    EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
+  using Rows = float[TSUB][VEC];
+  const int64_t T = g.T, D = g.D;
+  // The thread's TSUB rows of a and b for ticket `ticket` (identity past the end).
+  auto load = [&](unsigned ticket, Rows& av, Rows& bv) {
+    const EwThread th = ew_thread_at<VEC, false>(g, ticket, 0u);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
-    const int64_t T = g.T, D = g.D;
-
-    float av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
       const int64_t t = t0 + s;
@@ -525,7 +525,12 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
         }
       }
     }
-
+  };
+  // The chunk from its rows: local aggregates, then `mid` (run by every thread),
+  // then the carry and the outputs.
+  auto finish = [&](unsigned ticket, unsigned epoch, const Rows& av, const Rows& bv, auto&& mid) {
+    const EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     Aff<1> loc[VEC], seed[VEC], carry[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
@@ -537,6 +542,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
       }
       seed[v] = aff_identity<1>();
     }
+    mid();
     ew_carry<Aff<1>, VEC, WAVES, false, PH>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
                                             incl_data, carry);
     if constexpr (PH == EW_REDUCE) return;
@@ -561,7 +567,46 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
         store_vec<VEC>(out1 + off, L);
       }
     }
-  });
+  };
+  if constexpr (PH != EW_LOOKBACK) {
+    Rows av, bv;
+    load(blockIdx.x, av, bv);
+    finish(blockIdx.x, 0u, av, bv, [] {});
+  } else {
+    // Persistent workgroups (mg_persistent's protocol) with two row buffers: the
+    // next ticket is shared once this chunk's local aggregates are formed, and its
+    // rows load while this chunk's carry and outputs run.
+    __shared__ unsigned s_ticket, s_epoch;
+    const unsigned chunks = (unsigned)g.n_lg * (unsigned)g.n_chunks;
+    if (threadIdx.x == 0) {
+      const unsigned e0 =
+          __hip_atomic_load(header + MG_H_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+      s_ticket = mg_next_ticket(header, e0, chunks);
+      s_epoch = e0;
+    }
+    __syncthreads();
+    unsigned t = s_ticket;
+    const unsigned e = s_epoch;
+    Rows a0, b0, a1, b1;
+    if (t < chunks) load(t, a0, b0);
+    auto step = [&](unsigned tk, const Rows& av, const Rows& bv, Rows& nav, Rows& nbv) {
+      unsigned next = 0u;
+      if (threadIdx.x == 0) next = mg_next_ticket(header, e, chunks);
+      unsigned tn = 0u;
+      finish(tk, e, av, bv, [&] {
+        if (threadIdx.x == 0) s_ticket = next;
+        __syncthreads();
+        tn = s_ticket;
+        if (tn < chunks) load(tn, nav, nbv);
+      });
+      return tn;
+    };
+    while (t < chunks) {
+      t = step(t, a0, b0, a1, b1);
+      if (t >= chunks) break;
+      t = step(t, a1, b1, a0, b0);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
