@@ -59,7 +59,7 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
  * MG_ERR_TOO_LARGE (4) without touching the device.  Every call on one GPU
  * shares the array: calls must be ordered on one stream; calls that can
  * overlap on one GPU race.  Allocates nothing, never synchronises. */
-#define MG_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define MG_NOALLOC_SCRATCH_BYTES (64u << 20)
 int mg_linear_scan_fwd_noalloc(const float* a, const float* b, float* A, float* Bc, int64_t B,
                                int64_t T, int64_t D, mg_stream_t stream);
 

@@ -1318,7 +1318,7 @@ int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const flo
 // In host code `scratch` names a host-side stand-in, never the device memory:
 // every host use goes through the address hipGetSymbolAddress returns for the
 // current device, which is looked up once per device and cached.
-constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;  // == MG_NOALLOC_SCRATCH_BYTES
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;  // == MG_NOALLOC_SCRATCH_BYTES
 static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 constexpr int NOALLOC_MAX_DEVICES = 64;

@@ -59,6 +59,28 @@ def test_noalloc_matches_workspace_entry_point(cuda):
         assert np.max(np.abs(B1[:1].double().cpu().numpy() - rB)) <= FWD_TOL
 
 
+def test_noalloc_accepts_the_headline_shape(cuda):
+    """The headline linear_scan shape (B=16, T=4096, D=1024: 2^26 elements) fits the static
+    array and gives the workspace entry point's results."""
+    B, T, D = 16, 4096, 1024
+    print(f"[gpu] mg_linear_scan_fwd_noalloc B={B} T={T} D={D}", flush=True)
+    lib = _native.load()
+    g = torch.Generator(device=cuda).manual_seed(3)
+    a = torch.tanh(2 * torch.randn(B, T, D, generator=g, device=cuda))
+    b = torch.randn(B, T, D, generator=g, device=cuda)
+    A0, B0 = torch.empty_like(a), torch.empty_like(a)
+    A1, B1 = torch.full_like(a, float("nan")), torch.full_like(a, float("nan"))
+    nbytes = lib.mg_linear_scan_workspace_bytes(B, T, D)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+    assert lib.mg_linear_scan_fwd(_p(a), _p(b), _p(A0), _p(B0), B, T, D, _p(ws), nbytes,
+                                  _stream()) == 0
+    assert lib.mg_linear_scan_fwd_noalloc(_p(a), _p(b), _p(A1), _p(B1), B, T, D,
+                                          _stream()) == 0
+    torch.cuda.synchronize()
+    assert float((A1 - A0).abs().max()) <= FWD_TOL
+    assert float((B1 - B0).abs().max()) <= FWD_TOL
+
+
 def test_noalloc_rejects_problems_beyond_the_scratch(cuda):
     """B*T*D = 2^28 needs more look-back slots than the static array holds: status 4,
     nothing launched (the pointers are never dereferenced)."""
