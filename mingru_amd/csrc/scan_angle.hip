@@ -362,7 +362,10 @@ struct LexTok {
 // current token's body and in the same basic block, so they overlap it.  A
 // conditional prefetch into a buffer copied at the loop's end let the compiler
 // sink the loads down to the copy, next to their first use.
-template <typename Tok, typename Load, typename Body>
+// FENCED keeps the scheduler from moving work across the prefetches, which bounds
+// the registers of a body as large as the forward reduce pass's (without it some of
+// its instances spill).
+template <typename Tok, bool FENCED = false, typename Load, typename Body>
 __device__ __forceinline__ void token_pairs(int64_t first, int count, int dir, Load&& load,
                                             Body&& body) {
   Tok A, B;
@@ -372,8 +375,10 @@ __device__ __forceinline__ void token_pairs(int64_t first, int count, int dir, L
   for (; i + 2 <= count; i += 2) {
     const int64_t t = first + (int64_t)i * dir;
     load(B, t + dir);
+    if constexpr (FENCED) __builtin_amdgcn_sched_barrier(0);
     body(A, t);
     load(A, i + 2 < count ? t + 2 * dir : last);
+    if constexpr (FENCED) __builtin_amdgcn_sched_barrier(0);
     body(B, t + dir);
   }
   if (i < count) body(A, first + (int64_t)i * dir);
@@ -406,13 +411,18 @@ __device__ __forceinline__ AnThread an_thread(const AnGeom& g) {
 }
 
 // Forward reduce pass: one workgroup per (run of AN_RUN consecutive blocks, group of
-// AN_GROUP consecutive chunks); thread 32 j + b holds chunk j of the group for block
-// b of the run, so wave w holds chunks 2w and 2w + 1 (a token row of 32 consecutive
-// blocks per chunk, 3.5 KB of angles at k = 8) and the workgroup holds every chunk
-// map of its blocks' group, which it composes into the group maps of the two-level
-// walk through LDS.
+// AN_GROUP consecutive chunks).  Thread 32 j + b of each half of the workgroup holds
+// chunk j of the group for block b of the run -- the first half the chunk's first
+// AN_CHUNK / 2 tokens, the second half the rest -- so wave w of a half holds chunks
+// 2w and 2w + 1 (a token row of 32 consecutive blocks per chunk, 3.5 KB of angles at
+// k = 8).  The two halves' maps are composed into the chunk maps through LDS, and
+// the workgroup then holds every chunk map of its blocks' group, which it composes
+// into the group maps of the two-level walk.  One thread per (block, chunk) gave
+// one wave per SIMD at C4, too few to keep the rotations' VALU work issuing.
 constexpr int AN_RUN = 32;
-static_assert(AN_RUN * AN_GROUP == MG_WAVE * AN_WAVES, "a workgroup is one group of chunks");
+constexpr int AN_HALF = MG_WAVE * AN_WAVES;  // threads per half of a reduce workgroup
+constexpr int AN_RED_THREADS = 2 * AN_HALF;
+static_assert(AN_RUN * AN_GROUP == AN_HALF, "a workgroup half is one group of chunks");
 
 struct AnRThread {
   int64_t bb, plane, blk;
@@ -422,12 +432,13 @@ struct AnRThread {
   bool full;              // every lane of the wave is ok (wave-uniform)
 };
 
-__device__ __forceinline__ AnRThread an_rthread(const AnGeom& g) {
+// The reduce thread q = 32 j + b of a workgroup half (q < AN_HALF).
+__device__ __forceinline__ AnRThread an_rthread(const AnGeom& g, int q) {
   AnRThread th;
   const int run = (int)(blockIdx.x % (unsigned)g.n_run);
   th.grp = (int)(blockIdx.x / (unsigned)g.n_run);
-  th.j = threadIdx.x / AN_RUN;
-  th.b = threadIdx.x % AN_RUN;
+  th.j = q / AN_RUN;
+  th.b = q % AN_RUN;
   th.blk = (int64_t)run * AN_RUN + th.b;
   th.c = th.grp * AN_GROUP + th.j;
   th.cnt = min(AN_GROUP, g.n_chunks - th.grp * AN_GROUP);
@@ -483,51 +494,58 @@ __device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const 
 }
 
 // ---- forward pass 1: chunk aggregates h -> P_c h + L_c ------------------------
-// With the two-level walk the workgroup then composes its group maps h -> Pg h + Lg
-// over chunks c0 .. c1: thread (j < K, b) carries column j of block b's Pg (and,
-// redundantly, its Lg) through the group's chunk maps read back from LDS.
+// Each half of the workgroup pushes [P | L] through its half of the chunk's tokens;
+// the pair compose (P2 P1, P2 L1 + L2) is split between the pair's two threads by
+// columns of P and rows of L.  With the two-level walk the workgroup then composes
+// its group maps h -> Pg h + Lg over chunks c0 .. c1: thread (j < K, b) carries
+// column j of block b's Pg (and, redundantly, its Lg) through the group's chunk
+// maps read back from LDS.
 template <int K, int SCHED, bool HS, bool HD>
-__global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, AnGeom g) {
+__global__ __launch_bounds__(AN_RED_THREADS) void angle_fwd_reduce(AnArgs a, AnGeom g) {
+  static_assert(K % 2 == 0, "the pair compose splits the columns of P in two");
   mg_sincos_setup();
-  const AnRThread th = an_rthread(g);
-  // Push [P | L] through the chunk's transitions.
+  const int q = threadIdx.x % AN_HALF, half = threadIdx.x / AN_HALF;
+  const AnRThread th = an_rthread(g, q);
+  // Push [P | L] through this half's tokens.
   float X[K][K + 1];
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
-    for (int q = 0; q <= K; ++q) X[i][q] = (i == q) ? 1.f : 0.f;
+    for (int c = 0; c <= K; ++c) X[i][c] = (i == c) ? 1.f : 0.f;
   // The decay is a scalar per token, so it commutes with the rotations: P's K
-  // columns take the chunk's product of decays once at the end, and only the
+  // columns take the product of the half's decays once at the end, and only the
   // offset column, which receives b_t every token, is decayed token by token.
   float gprod = 1.f;
   if (th.ok) {
-    const int64_t t0 = (int64_t)th.c * AN_CHUNK;
-    const int64_t te = min(t0 + AN_CHUNK, g.T);
-    if constexpr (SCHED == SCHED_LEX) {
-      using Tok = LexTok<K, HS, HD>;
-      token_pairs<Tok>(
-          t0, (int)(te - t0), 1,
-          [&](Tok& k, int64_t t) {
-            k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
-          },
-          [&](const Tok& cur, int64_t) {
-            apply_M_lex<K, HS, false, K + 1>(X, cur.ang, cur.d, 1.f);
-            if (HD) gprod *= cur.gm;
+    const int64_t t0 = (int64_t)th.c * AN_CHUNK + half * (AN_CHUNK / 2);
+    const int64_t te = min(t0 + AN_CHUNK / 2, g.T);
+    if (t0 < te) {
+      if constexpr (SCHED == SCHED_LEX) {
+        using Tok = LexTok<K, HS, HD>;
+        token_pairs<Tok, true>(
+            t0, (int)(te - t0), 1,
+            [&](Tok& k, int64_t t) {
+              k.template load<false>(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+            },
+            [&](const Tok& cur, int64_t) {
+              apply_M_lex<K, HS, false, K + 1>(X, cur.ang, cur.d, 1.f);
+              if (HD) gprod *= cur.gm;
 #pragma unroll
-            for (int i = 0; i < K; ++i)
-              X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
-          });
-    } else {
-      for (int64_t t = t0; t < te; ++t) {
-        const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-        const float d = HS ? a.scale[lane_tok] : 1.f;
-        const float gm = HD ? a.gamma[lane_tok] : 1.f;
-        apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
-        if (HD) gprod *= gm;
-        float bt[K];
-        ld<K>(bt, a.b + lane_tok * K);
+              for (int i = 0; i < K; ++i)
+                X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
+            });
+      } else {
+        for (int64_t t = t0; t < te; ++t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          const float d = HS ? a.scale[lane_tok] : 1.f;
+          const float gm = HD ? a.gamma[lane_tok] : 1.f;
+          apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
+          if (HD) gprod *= gm;
+          float bt[K];
+          ld<K>(bt, a.b + lane_tok * K);
 #pragma unroll
-        for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+          for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+        }
       }
     }
   }
@@ -535,47 +553,108 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
 #pragma unroll
     for (int i = 0; i < K; ++i)
 #pragma unroll
-      for (int q = 0; q < K; ++q) X[i][q] *= gprod;
+      for (int c = 0; c < K; ++c) X[i][c] *= gprod;
   }
-  float Pf[K * K], Lf[K];
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-#pragma unroll
-    for (int j = 0; j < K; ++j) Pf[i * K + j] = X[i][j];
-    Lf[i] = X[i][K];
-  }
-  // The threads' [P | L] rows pass through LDS (row = thread): the chunk products
-  // leave as whole lines (a wave's rows are two chunks of 32 consecutive blocks,
-  // consecutive in memory) and the group compose reads them back.
+  // Rows of LDS: thread t's half map [P | L] in row t; the chunk maps then replace
+  // the first half's rows (row q = 32 j + b: chunk j of block b).
   constexpr int RS = an_row_stride<K>();
-  __shared__ __attribute__((aligned(16))) float s_rows[MG_WAVE * AN_WAVES * RS];
+  __shared__ __attribute__((aligned(16))) float s_rows[AN_RED_THREADS * RS];
   const int lane = threadIdx.x & (MG_WAVE - 1), w = threadIdx.x / MG_WAVE;
-  if (th.ok) {
+  {
+    float* row = s_rows + threadIdx.x * RS;
+    float Pf[K * K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+#pragma unroll
+      for (int c = 0; c < K; ++c) Pf[i * K + c] = X[i][c];
+      row[K * K + i] = X[i][K];
+    }
 #pragma unroll
     for (int k = 0; k < K * K; k += 4)
-      *reinterpret_cast<float4*>(s_rows + threadIdx.x * RS + k) =
-          make_float4(Pf[k], Pf[k + 1], Pf[k + 2], Pf[k + 3]);
-#pragma unroll
-    for (int i = 0; i < K; ++i) s_rows[threadIdx.x * RS + K * K + i] = Lf[i];
+      *reinterpret_cast<float4*>(row + k) = make_float4(Pf[k], Pf[k + 1], Pf[k + 2], Pf[k + 3]);
   }
-  wave_sync();
+  __syncthreads();
+  // Pair compose for chunk q: this thread forms columns H half .. of P = P2 P1 and
+  // rows H half .. of L = P2 L1 + L2 (H = K / 2).
+  constexpr int H = K / 2;
+  float Pn[K][H], Ln[H];
+  {
+    const float* r1 = s_rows + q * RS;             // first half of the chunk
+    const float* r2 = s_rows + (AN_HALF + q) * RS;  // second half
+    float p1[K][H], l1[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+      for (int c = 0; c < H; ++c) p1[k][c] = r1[k * K + H * half + c];
+      l1[k] = r1[K * K + k];
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      float p2[K];
+      if constexpr (K % 4 == 0) {
+#pragma unroll
+        for (int k = 0; k < K; k += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(r2 + i * K + k);
+          p2[k] = v.x;
+          p2[k + 1] = v.y;
+          p2[k + 2] = v.z;
+          p2[k + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k) p2[k] = r2[i * K + k];
+      }
+#pragma unroll
+      for (int c = 0; c < H; ++c) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc = fmaf(p2[k], p1[k][c], acc);
+        Pn[i][c] = acc;
+      }
+      if (i / H == half) {
+        float acc = r2[K * K + i];
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc = fmaf(p2[k], l1[k], acc);
+        Ln[i % H] = acc;
+      }
+    }
+  }
+  __syncthreads();  // every pair has read both halves' rows
+  {
+    float* row = s_rows + q * RS;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int c = 0; c < H; ++c) row[i * K + H * half + c] = Pn[i][c];
+#pragma unroll
+    for (int i = 0; i < H; ++i) row[K * K + H * half + i] = Ln[i];
+  }
+  __syncthreads();
+  if (half) return;  // the first half stores the chunk maps and composes the groups
   if (th.full) {
-    // Piece q: floats 4 (64 q + lane) .. of the wave's 64 rows; the rows of one
+    // Piece p: floats 4 (64 p + lane) .. of the wave's 64 rows; the rows of one
     // piece are consecutive blocks of one chunk.
     const int64_t blk0 = th.blk - th.b;
 #pragma unroll
-    for (int q = 0; q < K * K / 4; ++q) {
-      const int o = (q * MG_WAVE + lane) * 4, r = o / (K * K), col = o % (K * K);
+    for (int p = 0; p < K * K / 4; ++p) {
+      const int o = (p * MG_WAVE + lane) * 4, r = o / (K * K), col = o % (K * K);
       const float4 v = *reinterpret_cast<const float4*>(s_rows + (w * MG_WAVE + r) * RS + col);
       *reinterpret_cast<float4*>(a.prod + an_idx(g, th.grp * AN_GROUP + 2 * w + r / AN_RUN, col,
                                                  K * K, blk0 + r % AN_RUN)) = v;
     }
   } else if (th.ok) {
+    float Pf[K * K];
+#pragma unroll
+    for (int k = 0; k < K * K; ++k) Pf[k] = s_rows[q * RS + k];
     st<K * K>(a.prod + an_idx(g, th.c, 0, K * K, th.blk), Pf);
   }
-  if (th.ok) st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
+  if (th.ok) {
+    float Lf[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) Lf[i] = s_rows[q * RS + K * K + i];
+    st<K>(a.lsum + an_idx(g, th.c, 0, K, th.blk), Lf);
+  }
   if (g.n_chunks <= AN_GROUP_MIN) return;  // uniform
-  __syncthreads();
   if (!th.live || th.j >= K) return;
   float m[K], l[K];  // column j and offset of the maps composed so far (chunk c0's)
 #pragma unroll
@@ -601,9 +680,9 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_reduce(AnArgs a, 
     for (int i = 0; i < K; ++i) {
       float am = 0.f, al = L[i];
 #pragma unroll
-      for (int q = 0; q < K; ++q) {
-        am = fmaf(P[i * K + q], m[q], am);
-        al = fmaf(P[i * K + q], l[q], al);
+      for (int c = 0; c < K; ++c) {
+        am = fmaf(P[i * K + c], m[c], am);
+        al = fmaf(P[i * K + c], l[c], al);
       }
       nm[i] = am;
       nl[i] = al;
@@ -1328,7 +1407,8 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
     walk();
     hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   } else {
-    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), rgrid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), rgrid, dim3(AN_RED_THREADS), 0, stream,
+                       a, g);
     walk();
     hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
   }
