@@ -32,9 +32,9 @@
 // launches carry older tags and never validate, so stale contents are
 // harmless.  The epoch lives on the device, so graph replays advance it too.
 // Launches that may overlap (different streams) need different workspaces.
-// The elementwise scans and the thread-per-plane block-matrix backward run the
-// persistent form (mg_persistent): resident workgroups take tickets until the
-// work runs out.
+// The elementwise scans, the thread-per-plane block-matrix backward and its
+// forward for small held inputs run the persistent form (mg_persistent's
+// protocol): resident workgroups take tickets until the work runs out.
 #pragma once
 
 #include <hip/hip_runtime.h>

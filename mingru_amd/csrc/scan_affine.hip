@@ -31,10 +31,13 @@ using namespace mg;
 // Chunk shape by block size and direction: waves per workgroup x steps per
 // wave.  Longer chunks mean fewer hops in the look-back chain, whose per-hop
 // latency (slot round trips that bypass the L2) bounds the 2x2 scans at long T;
-// the shapes were chosen by timing on MI355X at B=16, T=4096, n=256.
+// the shapes were chosen by timing on MI355X at B=16, T=4096, n=256.  The 2x2
+// forward takes 8 waves since its small held inputs run persistent workgroups with
+// two input buffers (16 waves cap a lane at 128 VGPRs, and the second buffer
+// spilled there).
 template <int K, bool BWD>
 constexpr int af_waves() {
-  return K == 2 ? (BWD ? 8 : 16) : 4;
+  return K == 2 ? 8 : 4;
 }
 
 template <int K, bool BWD>
@@ -52,15 +55,137 @@ constexpr bool af_hold() {
   return K == 1 || K * (K + V) <= 8;
 }
 
+// Whether the forward runs persistent workgroups with two input buffers: held
+// inputs small enough to double (at most 64 floats per buffer).
+template <int K, int V>
+constexpr bool af_fwd_persistent() {
+  return af_hold<K, V>() && K * (K + V) * af_tsub<K, false>() <= 64;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
+// Forward with the chunk's inputs held in registers, in persistent workgroups
+// (mg_persistent's protocol) with two input buffers: the next ticket is shared
+// once this chunk's local aggregate is formed, and its inputs load while this
+// chunk's carry and outputs run.
+template <int K, int V, int TSUB, int WAVES>
+__device__ __forceinline__ void affine_fwd_held(const float* __restrict__ A,
+                                                const float* __restrict__ Bm,
+                                                float* __restrict__ Abar, float* __restrict__ Bbar,
+                                                const AfGeom& g, unsigned* header,
+                                                mg_slot_t* agg_data, mg_slot_t* incl_data) {
+  using RA = float[TSUB][K * K];
+  using RB = float[TSUB][K * V];
+  const int64_t T = g.T, n = g.n;
+  // The thread's TSUB steps of (A_t, B_t) for ticket `ticket` (identity past the end).
+  auto load = [&](unsigned ticket, RA& ha, RB& hb) {
+    const AfThread th = af_thread_at<false>(g, ticket, 0u);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      const int64_t t = t0 + s;
+      if (th.ok && t < T) {
+        const int64_t row = (th.bb * T + t) * n + th.plane;
+        ld<K * K, true>(ha[s], A + row * (K * K));
+        ld<K * V, true>(hb[s], Bm + row * (K * V));
+      } else {
+#pragma unroll
+        for (int i = 0; i < K * K; ++i) ha[s][i] = (i / K == i % K) ? 1.f : 0.f;
+#pragma unroll
+        for (int i = 0; i < K * V; ++i) hb[s][i] = 0.f;
+      }
+    }
+  };
+  // Applies step s to x: x <- A_s x + B_s (offset columns only when OFF).
+  auto step = [&](const RA& ha, const RB& hb, int s, AffM<K, V>& x) {
+    AffM<K, V> nx;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], x.P[m][j], acc);
+        nx.P[i][j] = acc;
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float acc = hb[s][i * V + j];
+#pragma unroll
+        for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], x.L[m][j], acc);
+        nx.L[i][j] = acc;
+      }
+    }
+    x = nx;
+  };
+  // The chunk from its inputs: local aggregate, then `mid` (run by every thread),
+  // then the carry and the outputs.
+  auto finish = [&](unsigned ticket, unsigned epoch, const RA& ha, const RB& hb, auto&& mid) {
+    const AfThread th = af_thread_at<false>(g, ticket, epoch);
+    const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
+    AffM<K, V> loc, carry, seed;
+    affm_identity(loc);
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) step(ha, hb, s, loc);
+    affm_identity(seed);
+    mid();
+    af_carry<K, V, WAVES, false>(loc, seed, g, th.lg, th.c, header, th.epoch, agg_data,
+                                 incl_data, carry);
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      step(ha, hb, s, carry);
+      const int64_t t = t0 + s;
+      if (th.ok && t < T) {
+        const int64_t row = (th.bb * T + t) * n + th.plane;
+        st<K * K, true>(Abar + row * (K * K), &carry.P[0][0]);
+        st<K * V, true>(Bbar + row * (K * V), &carry.L[0][0]);
+      }
+    }
+  };
+  __shared__ unsigned s_ticket, s_epoch;
+  const unsigned chunks = (unsigned)g.n_lg * (unsigned)g.n_chunks;
+  if (threadIdx.x == 0) {
+    const unsigned e0 =
+        __hip_atomic_load(header + MG_H_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    s_ticket = mg_next_ticket(header, e0, chunks);
+    s_epoch = e0;
+  }
+  __syncthreads();
+  unsigned t = s_ticket;
+  const unsigned e = s_epoch;
+  RA a0, a1;
+  RB b0, b1;
+  if (t < chunks) load(t, a0, b0);
+  auto chunk = [&](unsigned tk, const RA& ha, const RB& hb, RA& nha, RB& nhb) {
+    unsigned next = 0u;
+    if (threadIdx.x == 0) next = mg_next_ticket(header, e, chunks);
+    unsigned tn = 0u;
+    finish(tk, e, ha, hb, [&] {
+      if (threadIdx.x == 0) s_ticket = next;
+      __syncthreads();
+      tn = s_ticket;
+      if (tn < chunks) load(tn, nha, nhb);
+    });
+    return tn;
+  };
+  while (t < chunks) {
+    t = chunk(t, a0, b0, a1, b1);
+    if (t >= chunks) break;
+    t = chunk(t, a1, b1, a0, b0);
+  }
+}
+
 template <int K, int V, int TSUB, int WAVES>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_fwd_kernel(
     const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ Abar,
     float* __restrict__ Bbar, AfGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
   constexpr bool HOLD = af_hold<K, V>();
+  if constexpr (af_fwd_persistent<K, V>()) {
+    affine_fwd_held<K, V, TSUB, WAVES>(A, Bm, Abar, Bbar, g, header, agg_data, incl_data);
+    return;
+  }
   constexpr int HS = HOLD ? TSUB : 1;
   AfThread th = af_thread<false>(g, header);
   if (!th.valid) return;
@@ -449,8 +574,13 @@ int af_launch_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int
   AfPlan p = af_plan(B, T, n, WV, TS, K * K + K * V);
   if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
   unsigned* header = (unsigned*)ws;
-  hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, WV>),
-                     dim3((unsigned)(p.g.n_lg * p.g.n_chunks)), dim3(MG_WAVE * WV), 0,
+  // Small held inputs run persistent workgroups; the others one workgroup per chunk.
+  const unsigned chunks = (unsigned)(p.g.n_lg * p.g.n_chunks);
+  const unsigned grid =
+      af_fwd_persistent<K, V>()
+          ? std::min(chunks, mg_resident((const void*)&affine_fwd_kernel<K, V, TS, WV>, MG_WAVE * WV))
+          : chunks;
+  hipLaunchKernelGGL((affine_fwd_kernel<K, V, TS, WV>), dim3(grid), dim3(MG_WAVE * WV), 0,
                      stream, A, Bm, Abar, Bbar, p.g, header,
                      (mg_slot_t*)((char*)ws + p.agg_off), (mg_slot_t*)((char*)ws + p.incl_off));
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
