@@ -44,7 +44,8 @@ size_t mg_linear_scan_workspace_bytes(int64_t B, int64_t T, int64_t D);
 /* a, b -> A (running product), Bc (zero-start solution). */
 int mg_linear_scan_fwd(const float* a, const float* b, float* A, float* Bc, int64_t B, int64_t T,
                        int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);
-/* Grads gA, gB of (A, Bc) -> da, db.  A, Bc are the forward outputs. */
+/* Grads gA, gB of (A, Bc) -> da, db.  A, Bc are the forward outputs; the kernels
+ * read Bc and the row of A before each sub-chunk, not b (kept for the interface). */
 int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,
                        const float* gA, const float* gB, float* da, float* db, int64_t B,
                        int64_t T, int64_t D, void* ws, size_t ws_bytes, mg_stream_t stream);

@@ -610,9 +610,11 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Backward of linear_scan.  Inputs a, b, saved A, Bc and grads gA, gB;
-// outputs da, db.  Adjoint: x_t = g_t + a_{t+1} x_{t+1} for both streams;
-// da_t = xA_t A_{t-1} + xB_t Bc_{t-1}, db_t = xB_t.
+// Backward of linear_scan.  Inputs a, saved A, Bc and grads gA, gB (b is not
+// read); outputs da, db.  Adjoint: x_t = g_t + a_{t+1} x_{t+1} for both streams;
+// da_t = xA_t A_{t-1} + xB_t Bc_{t-1}, db_t = xB_t.  Bc_{t-1} is read per step
+// (the saved rows shifted by one, as many bytes as b's); A_{t-1} follows from the
+// row before the wave's first step, times a.
 // ---------------------------------------------------------------------------
 template <int VEC, int TSUB, int WAVES, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
@@ -626,37 +628,40 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
 
-    float av[TSUB][VEC], bv[TSUB][VEC], xa[TSUB][VEC], xb[TSUB][VEC];
-    float Ap[VEC], Bp[VEC];
+    // bp[s] = Bc_{t0+s-1} (zero before the sequence start).
+    float av[TSUB][VEC], bp[TSUB][VEC], xa[TSUB][VEC], xb[TSUB][VEC];
+    float Ap[VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
       const int64_t t = t0 + s;
       if (th.col_ok && t < T) {
         const int64_t off = (th.bb * T + t) * D + th.col;
         load_vec<VEC, NT>(av[s], a + off);
-        if constexpr (PH != EW_REDUCE) load_vec<VEC>(bv[s], b + off);
+        if constexpr (PH != EW_REDUCE) {
+          if (t > 0) {
+            load_vec<VEC>(bp[s], Bc + off - D);
+          } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) bp[s][v] = 0.f;
+          }
+        }
         load_vec<VEC, NT>(xa[s], gA + off);
         load_vec<VEC, NT>(xb[s], gB + off);
       } else {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           av[s][v] = 1.f;
-          bv[s][v] = 0.f;
+          bp[s][v] = 0.f;
           xa[s][v] = 0.f;
           xb[s][v] = 0.f;
         }
       }
     }
     if (th.col_ok && t0 > 0 && t0 <= T) {
-      const int64_t off = (th.bb * T + t0 - 1) * D + th.col;
-      load_vec<VEC>(Ap, A + off);
-      load_vec<VEC>(Bp, Bc + off);
+      load_vec<VEC>(Ap, A + (th.bb * T + t0 - 1) * D + th.col);
     } else {
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        Ap[v] = 1.f;
-        Bp[v] = 0.f;
-      }
+      for (int v = 0; v < VEC; ++v) Ap[v] = 1.f;
     }
 
     Aff<2> loc[VEC], seed[VEC], carry[VEC];
@@ -697,8 +702,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
       float d_a[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        d_a[v] = fmaf(xa[s][v], Ap[v], xb[s][v] * Bp[v]);
-        Bp[v] = fmaf(av[s][v], Bp[v], bv[s][v]);
+        d_a[v] = fmaf(xa[s][v], Ap[v], xb[s][v] * bp[s][v]);
         Ap[v] *= av[s][v];
       }
       const int64_t t = t0 + s;
