@@ -142,7 +142,8 @@ size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, in
 int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,
                        int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,
                        mg_stream_t stream);
-/* Grads of (Abar, Bbar) -> dA, dBm.  Abar, Bbar are the forward outputs. */
+/* Grads of (Abar, Bbar) -> dA, dBm.  Abar, Bbar are the forward outputs; the kernels
+ * read them, not Bm (kept for the interface). */
 int mg_affine_scan_bwd(const float* A, const float* Bm, const float* Abar, const float* Bbar,
                        const float* gAbar, const float* gBbar, float* dA, float* dBm, int64_t B,
                        int64_t T, int64_t n, int k, int v, void* ws, size_t ws_bytes,

@@ -309,12 +309,21 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
     auto offA = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * K); };
     auto offB = [&](int64_t t) { return ((th.bb * T + t) * n + th.plane) * (K * V); };
 
+    // hb[s] holds the saved Bbar_{t-1} (zero at t = 0): the final pass's forward
+    // sweep reads it instead of rebuilding it from B, so only Abar needs a seed row.
     float ha[HS][K * K], hb[HS][K * V], hga[HS][K * K], hgb[HS][K * V];
-    auto fetch = [&](int s, float* a, float* b, float* ga, float* gb, bool need_b) {
+    auto fetch = [&](int s, float* a, float* bprev, float* ga, float* gb, bool need_b) {
       const int64_t t = t0 + s;
       if (th.ok && t < T) {
         ld<K * K, HOLD>(a, A + offA(t));
-        if (need_b) ld<K * V, HOLD>(b, Bm + offB(t));
+        if (need_b) {
+          if (t > 0) {
+            ld<K * V, HOLD>(bprev, Bbar + offB(t - 1));
+          } else {
+#pragma unroll
+            for (int i = 0; i < K * V; ++i) bprev[i] = 0.f;
+          }
+        }
         ld<K * K, HOLD>(ga, GA + offA(t));
         ld<K * V, HOLD>(gb, GB + offB(t));
       } else {
@@ -325,7 +334,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
         }
 #pragma unroll
         for (int i = 0; i < K * V; ++i) {
-          b[i] = 0.f;
+          bprev[i] = 0.f;
           gb[i] = 0.f;
         }
       }
@@ -410,16 +419,14 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
             else hgb[s][i * V + (j - K)] = X[i][j];
           }
       }
-      // Forward sweep: recompute (Abar_{t-1}, Bbar_{t-1}) from the saved boundary.
-      float Sa[K * K], Sb[K * V];
+      // Forward sweep: recompute Abar_{t-1} from the saved boundary row; Bbar_{t-1}
+      // is held.
+      float Sa[K * K];
       if (th.ok && t0 > 0 && t0 <= T) {
         ld<K * K>(Sa, Abar + offA(t0 - 1));
-        ld<K * V>(Sb, Bbar + offB(t0 - 1));
       } else {
 #pragma unroll
         for (int i = 0; i < K * K; ++i) Sa[i] = (i / K == i % K) ? 1.f : 0.f;
-#pragma unroll
-        for (int i = 0; i < K * V; ++i) Sb[i] = 0.f;
       }
 #pragma unroll
       for (int s = 0; s < TSUB; ++s) {
@@ -432,12 +439,12 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
 #pragma unroll
             for (int m = 0; m < K; ++m) acc = fmaf(hga[s][i * K + m], Sa[j * K + m], acc);
 #pragma unroll
-            for (int m = 0; m < V; ++m) acc = fmaf(hgb[s][i * V + m], Sb[j * V + m], acc);
+            for (int m = 0; m < V; ++m) acc = fmaf(hgb[s][i * V + m], hb[s][j * V + m], acc);
             d[i * K + j] = acc;
           }
-        float na[K * K], nb[K * V];
+        float na[K * K];
 #pragma unroll
-        for (int i = 0; i < K; ++i) {
+        for (int i = 0; i < K; ++i)
 #pragma unroll
           for (int j = 0; j < K; ++j) {
             float acc = 0.f;
@@ -446,17 +453,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void affine_bwd_kernel(
             na[i * K + j] = acc;
           }
 #pragma unroll
-          for (int j = 0; j < V; ++j) {
-            float acc = hb[s][i * V + j];
-#pragma unroll
-            for (int m = 0; m < K; ++m) acc = fmaf(ha[s][i * K + m], Sb[m * V + j], acc);
-            nb[i * V + j] = acc;
-          }
-        }
-#pragma unroll
         for (int i = 0; i < K * K; ++i) Sa[i] = na[i];
-#pragma unroll
-        for (int i = 0; i < K * V; ++i) Sb[i] = nb[i];
         const int64_t t = t0 + s;
         if (th.ok && t < T) {
           st<K * K, true>(dA + offA(t), d);
