@@ -97,7 +97,7 @@ __device__ __forceinline__ void affine_fwd_held(const float* __restrict__ A,
       }
     }
   };
-  // Applies step s to x: x <- A_s x + B_s (offset columns only when OFF).
+  // Applies step s to x: x <- A_s x + B_s.
   auto step = [&](const RA& ha, const RB& hb, int s, AffM<K, V>& x) {
     AffM<K, V> nx;
 #pragma unroll
