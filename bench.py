@@ -252,7 +252,12 @@ def make_step(key, torch, wl, dev):
                 Abar, Bc = mg.matrix_scan(A, b0)
                 return torch.autograd.grad((Abar, Bc), (A, b0), (gA, gB))
 
-            cpu = None
+            def cpu(bs):
+                Ac = inp["A"][:bs].clone().requires_grad_(True)
+                bc = torch.zeros(inp["Bm"][:bs].shape[:-1]).requires_grad_(True)
+                Abar, Bc = mg.matrix_scan(Ac, bc)
+                torch.autograd.grad((Abar, Bc), (Ac, bc),
+                                    (inp["grad_Abar"][:bs], inp["grad_Bbar"][:bs, ..., 0]))
         return step, cpu, wl.C3["B"]
     if key == "C4":
         from mingru_amd import hip_scans

@@ -19,7 +19,8 @@
  *     synchronises;
  *   - the return value is a status: 0 ok, 1 invalid argument / outside the
  *     envelope, 2 kernel launch failed, 3 workspace too small, 4 problem too
- *     large for a fixed static scratch, 5 a HIP runtime call failed.
+ *     large for a fixed static scratch, 5 a HIP runtime call failed, 6 a
+ *     one-time device set-up was asked for while `stream` was being captured.
  *
  * Each declaration cites the reference interface it replaces
  * (chris-santiago/minGRU, paths relative to the repository root).
@@ -55,14 +56,21 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * look-back workspace is a static device array of MG_NOALLOC_SCRATCH_BYTES per
  * GPU, held from the library's first call on that GPU until the process ends
- * and zero-filled once by that call (on `stream`).  Problems whose forward
- * workspace exceeds it (about B*T*D > 2^27 elements) return
- * MG_ERR_TOO_LARGE (4) without touching the device.  Every call on one GPU
- * shares the array: calls must be ordered on one stream; calls that can
- * overlap on one GPU race.  Allocates nothing, never synchronises. */
+ * and zero-filled once by that call (on `stream`).  That first call on a GPU
+ * must not be made under stream capture (it returns 6 and does nothing); later
+ * calls may be captured.  Problems whose forward workspace exceeds the array
+ * (about B*T*D > 2^27 elements) return MG_ERR_TOO_LARGE (4) without touching
+ * the device.  Every call on one GPU shares the array: calls must be ordered on
+ * one stream; calls that can overlap on one GPU race.  Allocates nothing, never
+ * synchronises. */
 #define MG_NOALLOC_SCRATCH_BYTES (64u << 20)
 int mg_linear_scan_fwd_noalloc(const float* a, const float* b, float* A, float* Bc, int64_t B,
                                int64_t T, int64_t D, mg_stream_t stream);
+/* Failed look-back waits recorded by mg_linear_scan_fwd_noalloc on the current
+ * GPU since its static array was zeroed (as mg_scan_workspace_errors reports for
+ * a caller workspace); 0 when the entry point has not run on this GPU.  No
+ * counterpart in the reference.  Synchronises `stream`, allocates nothing. */
+int mg_linear_scan_noalloc_errors(unsigned* count, mg_stream_t stream);
 
 /* ---- fused SignedMinGRU gates + linear_scan, (B, T, D) -----------------------
  * No reference kernel fuses these: replaces the mixer's coefficient code and
@@ -136,7 +144,8 @@ int mg_scan_workspace_errors(const void* ws, unsigned* count, mg_stream_t stream
  * Replaces affine_scan_fwd / affine_scan_bwd (src/mingru/triton_scans.py:
  * 1293-1316, 1359-1390; kernels :630-700, :824-959) behind
  * SCAN_IMPLS["matrix_scan"] / ["matrix_affine_scan"] (:2492-2563).
- * k in {1,2,4,8}, v in {1,2,4,8,16}; pointers 16-byte aligned. */
+ * k, v in {1,2,4,8,16} (k <= 4 one plane per thread, k = 8 and 16 on the
+ * matrix cores); pointers 16-byte aligned. */
 size_t mg_affine_scan_workspace_bytes(int64_t B, int64_t T, int64_t n, int k, int v);
 /* A (B,T,n,k,k), Bm (B,T,n,k,v) -> Abar = A_t..A_1, Bbar (zero-start solution). */
 int mg_affine_scan_fwd(const float* A, const float* Bm, float* Abar, float* Bbar, int64_t B,

@@ -21,6 +21,7 @@ MG_STATUS = {
     3: "workspace too small",
     4: "problem too large for the static scratch",
     5: "HIP runtime call failed",
+    6: "one-time device set-up requested under stream capture",
 }
 
 _P = ctypes.c_void_p
@@ -34,6 +35,7 @@ _SIGNATURES = {
     "mg_linear_scan_fwd": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mg_linear_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _P, _SZ, _P]),
     "mg_linear_scan_fwd_noalloc": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "mg_linear_scan_noalloc_errors": (_I32, [ctypes.POINTER(ctypes.c_uint), _P]),
     "mg_signed_gate_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "mg_signed_gate_scan_fwd": (_I32, [_P] * 5 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),
     "mg_signed_gate_scan_bwd": (_I32, [_P] * 10 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),

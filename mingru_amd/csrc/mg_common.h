@@ -53,6 +53,7 @@
 #define MG_ERR_WORKSPACE 3
 #define MG_ERR_TOO_LARGE 4  // problem needs more than a fixed static scratch holds
 #define MG_ERR_RUNTIME 5    // a HIP runtime call (not a launch) failed
+#define MG_ERR_CAPTURE 6    // a one-time device set-up was asked for under stream capture
 
 typedef unsigned long long mg_slot_t;
 

@@ -30,6 +30,7 @@
 #include "mg_gates.h"
 
 #include <initializer_list>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1328,9 +1329,8 @@ static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 constexpr int NOALLOC_MAX_DEVICES = 64;
 
 struct NoallocDevice {
-  std::once_flag once;
-  void* ptr = nullptr;
-  int status = MG_ERR_RUNTIME;
+  std::mutex mu;                     // serialises the one-time set-up
+  std::atomic<void*> ptr{nullptr};   // device address of `scratch`, once set up
 };
 NoallocDevice g_noalloc[NOALLOC_MAX_DEVICES];
 
@@ -1340,32 +1340,40 @@ __global__ void zero_fill_kernel(uint4* __restrict__ p, size_t n16) {
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// The current device's scratch address, set up on the first call per device:
+int noalloc_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= NOALLOC_MAX_DEVICES)
+    return MG_ERR_RUNTIME;
+  return MG_OK;
+}
+
+// The current device's scratch address, set up by the first call per device:
 // the symbol lookup, then one zero fill on `stream` (the look-back workspace
 // protocol starts from zeroed memory; later calls ordered on a stream after it
-// reuse the contents unchanged).
+// reuse the contents unchanged).  The set-up is refused while `stream` is being
+// captured: a captured fill would not run at capture time and would run again
+// on every replay.
 int noalloc_scratch(hipStream_t stream, void** out) {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
-    return MG_ERR_RUNTIME;
+  if (noalloc_device(&dev) != MG_OK) return MG_ERR_RUNTIME;
   NoallocDevice& d = g_noalloc[dev];
-  std::call_once(d.once, [&] {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
-      d.status = MG_ERR_RUNTIME;
-      return;
+  void* p = d.ptr.load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(d.mu);
+    p = d.ptr.load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return MG_ERR_RUNTIME;
+      if (cs != hipStreamCaptureStatusNone) return MG_ERR_CAPTURE;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+        return MG_ERR_RUNTIME;
+      hipLaunchKernelGGL(zero_fill_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)p,
+                         NOALLOC_SCRATCH_BYTES / 16);
+      if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
+      d.ptr.store(p, std::memory_order_release);
     }
-    hipLaunchKernelGGL(zero_fill_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)p,
-                       NOALLOC_SCRATCH_BYTES / 16);
-    if (hipGetLastError() != hipSuccess) {
-      d.status = MG_ERR_LAUNCH;
-      return;
-    }
-    d.ptr = p;
-    d.status = MG_OK;
-  });
-  *out = d.ptr;
-  return d.status;
+  }
+  *out = p;
+  return MG_OK;
 }
 
 template <int G>
@@ -1453,6 +1461,18 @@ int mg_scan_workspace_errors(const void* ws, unsigned* count, hipStream_t stream
   if (hipStreamSynchronize(stream) != hipSuccess) return MG_ERR_RUNTIME;
   *count = v;
   return MG_OK;
+}
+
+int mg_linear_scan_noalloc_errors(unsigned* count, hipStream_t stream) {
+  if (!count) return MG_ERR_ARG;
+  int dev = -1;
+  if (noalloc_device(&dev) != MG_OK) return MG_ERR_RUNTIME;
+  const void* p = g_noalloc[dev].ptr.load(std::memory_order_acquire);
+  if (p == nullptr) {  // never set up on this device: nothing has run
+    *count = 0;
+    return MG_OK;
+  }
+  return mg_scan_workspace_errors(p, count, stream);
 }
 
 int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const float* Bc,

@@ -152,6 +152,8 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 # request replaces the buffer with a new zero-filled one (the old one returns to
 # torch's caching allocator, ordered after the work already queued on the stream).
 _scan_ws: dict = {}
+# Failed look-back waits recorded by workspaces since replaced by larger ones.
+_retired_errors = [0]
 
 
 def _scan_workspace(nbytes: int, device) -> torch.Tensor:
@@ -160,6 +162,10 @@ def _scan_workspace(nbytes: int, device) -> torch.Tensor:
     key = (idx, raw)
     ws = _scan_ws.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            # Keep the count of waits the outgoing workspace saw give up (one stream sync,
+            # only when a workspace grows).
+            _retired_errors[0] += _ws_error_count(ws)
         ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
         _scan_ws[key] = ws
     return ws
@@ -184,7 +190,7 @@ def workspace_errors() -> int:
     workspace header and the kernel finishes with a partial carry, so a nonzero
     count means some result was wrong.  Synchronises each workspace's stream.
     """
-    return sum(_ws_error_count(ws) for ws in list(_scan_ws.values()))
+    return _retired_errors[0] + sum(_ws_error_count(ws) for ws in list(_scan_ws.values()))
 
 
 def _check_workspace(ws: torch.Tensor, t: torch.Tensor) -> None:
@@ -746,12 +752,15 @@ def _tables_cover_all_angles(perm, p2p, half: int) -> bool:
 
 
 def _device_tables(perm, sgn, p2p, k: int, half: int, device):
-    """Validated int32/fp32 copies of the plane tables on ``device`` (cached per tensor)."""
-    key = (perm._version, sgn.data_ptr(), sgn._version, p2p.data_ptr(), p2p._version, k, half,
-           str(device))
+    """Validated int32/fp32 copies of the plane tables on ``device``, cached while the
+    same three tensor objects (held by weak reference) are passed unmodified: a new
+    ``sgn`` or ``p2p`` object, even at a reused address, or an in-place change to any
+    of the three (its ``_version``) validates and copies again."""
+    key = (perm._version, sgn._version, p2p._version, k, half, str(device))
     hit = _table_cache.get(id(perm))
-    if hit is not None and hit[0]() is perm and hit[1] == key:
-        return hit[2]
+    if (hit is not None and hit[0]() is perm and hit[1]() is sgn and hit[2]() is p2p
+            and hit[3] == key):
+        return hit[4]
     pc = perm.detach().to("cpu", torch.int64)
     sc = sgn.detach().to("cpu", torch.float64)
     qc = p2p.detach().to("cpu", torch.int64)
@@ -763,7 +772,7 @@ def _device_tables(perm, sgn, p2p, k: int, half: int, device):
     if len(_table_cache) > 256:
         for dead in [i for i, v in _table_cache.items() if v[0]() is None]:
             del _table_cache[dead]
-    _table_cache[id(perm)] = (weakref.ref(perm), key, tables)
+    _table_cache[id(perm)] = (weakref.ref(perm), weakref.ref(sgn), weakref.ref(p2p), key, tables)
     return tables
 
 

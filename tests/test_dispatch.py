@@ -655,3 +655,24 @@ def test_plane_table_angle_cover():
     assert not hip_scans._tables_cover_all_angles(perm, p2p, 5)  # angle 4 unused
     perm, sgn, p2p = _random_tables(4, 3, 2, seed=2, inactive=True)
     assert not hip_scans._tables_cover_all_angles(perm.long(), p2p.long(), 2)
+
+
+def test_plane_table_cache_sees_new_sgn_and_p2p_objects():
+    """The validated-table cache must not serve stale tables when the same ``perm`` object
+    comes back with new ``sgn``/``p2p`` tensors (fresh objects start at ``_version`` 0 and
+    may reuse an address), nor after an in-place change to any of the three."""
+    perm, sgn, p2p = hip_scans._brick_tables(8, 2)
+    t1 = hip_scans._device_tables(perm, sgn, p2p, 8, 4, torch.device("cpu"))
+    assert hip_scans._device_tables(perm, sgn, p2p, 8, 4, torch.device("cpu")) is t1
+    # same perm object, new p2p contents (each plane driven by another angle)
+    p2p_new = (3 - p2p).to(p2p.dtype)
+    t2 = hip_scans._device_tables(perm, sgn, p2p_new, 8, 4, torch.device("cpu"))
+    assert torch.equal(t2[2].long(), p2p_new.long())
+    # same perm object, new sgn (every plane's sign flipped)
+    sgn_new = -sgn
+    t3 = hip_scans._device_tables(perm, sgn_new, p2p_new, 8, 4, torch.device("cpu"))
+    assert torch.equal(t3[1], sgn_new.float())
+    # in-place change of the cached sgn object
+    sgn_new.neg_()
+    t4 = hip_scans._device_tables(perm, sgn_new, p2p_new, 8, 4, torch.device("cpu"))
+    assert torch.equal(t4[1], sgn_new.float())
