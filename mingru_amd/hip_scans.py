@@ -154,6 +154,11 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 _scan_ws: dict = {}
 # Failed look-back waits recorded by workspaces since replaced by larger ones.
 _retired_errors = [0]
+# Workspaces created under HIP graph capture.  Their zero fill is itself captured,
+# so it runs before the scan at every replay and not at capture time: such a
+# workspace serves only the captured calls (never later eager calls on the stream),
+# and stays alive as long as the process, since the graph may replay at any time.
+_capture_ws: list = []
 
 
 def _scan_workspace(nbytes: int, device) -> torch.Tensor:
@@ -161,14 +166,18 @@ def _scan_workspace(nbytes: int, device) -> torch.Tensor:
     raw = _raw_stream(idx) if _raw_stream is not None else torch.cuda.current_stream(idx).cuda_stream
     key = (idx, raw)
     ws = _scan_ws.get(key)
-    if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            # Keep the count of waits the outgoing workspace saw give up (one stream sync,
-            # only when a workspace grows).
-            _retired_errors[0] += _ws_error_count(ws)
-        ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
-        _scan_ws[key] = ws
-    return ws
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    fresh = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+    if torch.cuda.is_current_stream_capturing():
+        _capture_ws.append(fresh)
+        return fresh
+    if ws is not None:
+        # Keep the count of waits the outgoing workspace saw give up (one stream sync,
+        # only when a workspace grows).
+        _retired_errors[0] += _ws_error_count(ws)
+    _scan_ws[key] = fresh
+    return fresh
 
 
 class LookbackError(RuntimeError):
@@ -190,7 +199,8 @@ def workspace_errors() -> int:
     workspace header and the kernel finishes with a partial carry, so a nonzero
     count means some result was wrong.  Synchronises each workspace's stream.
     """
-    return _retired_errors[0] + sum(_ws_error_count(ws) for ws in list(_scan_ws.values()))
+    live = list(_scan_ws.values()) + list(_capture_ws)
+    return _retired_errors[0] + sum(_ws_error_count(ws) for ws in live)
 
 
 def _check_workspace(ws: torch.Tensor, t: torch.Tensor) -> None:
