@@ -39,6 +39,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  scan_elementwise.hip issues its header atomics from one
+# thread; LLVM's atomic optimizer would turn each into a wave reduction that waits
+# for the atomic's result at once, ahead of the chunk loads it should overlap.
+EXTRA_FLAGS = {
+    "scan_elementwise.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -71,7 +79,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     for src in sources:
         obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
         objs.append(obj)
-        cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-c", src, "-o", obj]
+        extra = EXTRA_FLAGS.get(os.path.basename(src), [])
+        cmd = [hipcc, *HIPCC_FLAGS, *extra, "-I", CSRC, "-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

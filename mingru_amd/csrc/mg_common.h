@@ -25,6 +25,9 @@
 //   [MG_H_TICKET0], [MG_H_TICKET1]  ticket counters, used by alternate epochs
 //   [MG_H_ERROR]                    spin-limit overflows (diagnostic)
 //   [MG_H_EPOCH]                    epoch of the last completed launch
+//   [4], [5]                        one 64-bit {count, epoch} word of the
+//                                   elementwise scans' one-launch aggregate form
+//                                   (scan_elementwise.hip, EW_AGG)
 // Every workgroup reads the epoch (previous + 1, never 0 on a zeroed
 // workspace), takes its ticket from the counter of the epoch's parity, and the
 // workgroup holding ticket 0 resets the other counter for the next launch.

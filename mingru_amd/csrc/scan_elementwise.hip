@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace {
 
@@ -65,7 +66,12 @@ constexpr int64_t EW_FILL_WGS = 256;
 // the first launch filled with them, and EW_TWO_LAUNCH_BYTES keeps them there.
 // At B=4, T=1024, D=256 a sequence is 16 chunks, and the look-back walks them
 // one round trip after another.
-enum : int { EW_LOOKBACK = 0, EW_REDUCE = 1, EW_FINAL = 2 };
+// EW_AGG does both in one launch when the whole grid fits on the chip at once:
+// every workgroup publishes its chunk aggregate (tagged with the launch's epoch,
+// before it waits on anything), then folds its predecessors' published
+// aggregates -- all loaded at once, never an inclusive prefix, so there is no
+// chain of workgroups waiting one after another -- and recomputes its chunk.
+enum : int { EW_LOOKBACK = 0, EW_REDUCE = 1, EW_FINAL = 2, EW_AGG = 3 };
 constexpr int EW_FINAL_MAX_CHUNKS = 32;
 constexpr int64_t EW_TWO_LAUNCH_BYTES = (int64_t)32 << 20;  // input bytes of both launches
 
@@ -288,6 +294,43 @@ __device__ __forceinline__ void agg_load(const mg_slot_t* base, const EwGeom& g,
       x[v].set(f, __uint_as_float((unsigned)p[f * TILE + v * MG_WAVE]));
 }
 
+// The launch tag of an EW_AGG workgroup, in LDS: thread 0 takes it (ew_agg_begin)
+// at the start of the kernel and writes it here just before the first barrier of
+// ew_carry, so its round trip overlaps the chunk's input loads.
+__device__ __forceinline__ unsigned& ew_agg_epoch() {
+  __shared__ unsigned s_epoch;
+  return s_epoch;
+}
+
+// Workspace protocol of an EW_AGG launch: one 64-bit header word {low: count,
+// high: epoch}.  Every workgroup adds 1 (one atomic round trip, with no other
+// access waiting on it); the old value's epoch e is the launch's, and the
+// workgroup that finds count == grid - 1 -- every other workgroup of the launch
+// has added by then -- stores {0, e + 1} for the next launch.  Tags are
+// (e + 1) | 2^31: never 0 (the two-launch form's stored aggregates) and apart from
+// the look-back launches' epochs (MG_H_EPOCH, far below 2^31), whose slots share
+// the region.  A workgroup's chunk is its workgroup index, since every workgroup
+// of the grid is resident.  Returns the tag in thread 0 (0 elsewhere).
+constexpr int EW_H_AGG = 4;  // header words 4, 5 (8-byte aligned)
+__device__ __forceinline__ unsigned long long ew_agg_begin(unsigned* header) {
+  if (threadIdx.x != 0) return 0ull;
+  return __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(header + EW_H_AGG), 1ull,
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0, at the first barrier: the launch tag from ew_agg_begin's word, and the
+// hand-over to the next launch by the workgroup that added last.
+__device__ __forceinline__ unsigned ew_agg_tag(unsigned* header, unsigned long long old) {
+  const unsigned count = (unsigned)old, e = (unsigned)(old >> 32);
+  if (count == gridDim.x - 1u)
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(header + EW_H_AGG),
+                       (unsigned long long)(e + 1u) << 32, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  else if (count >= gridDim.x)
+    mg_count_error(header);
+  return (e + 1u) | 0x80000000u;
+}
+
 // Intra-workgroup combine + the carry from earlier chunks: decoupled look-back
 // (PH = EW_LOOKBACK) or the stored aggregates of the two-launch form (PH =
 // EW_FINAL; PH = EW_REDUCE only stores this chunk's aggregate and leaves
@@ -298,14 +341,14 @@ __device__ __forceinline__ void agg_load(const mg_slot_t* base, const EwGeom& g,
 template <typename Map, int VEC, int WAVES, bool REVERSE, int PH = EW_LOOKBACK>
 __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed)[VEC],
                                          const EwGeom& g, int lg, int c, unsigned* header,
-                                         unsigned epoch, mg_slot_t* agg_data,
+                                         unsigned long long epoch, mg_slot_t* agg_data,
                                          mg_slot_t* incl_data, Map (&carry)[VEC]) {
   constexpr int TILE = MG_WAVE * VEC;
   constexpr int NF = Map::NF;
   constexpr int PER = EW_FINAL_MAX_CHUNKS / WAVES;  // predecessors per wave (EW_FINAL)
   static_assert(EW_FINAL_MAX_CHUNKS % WAVES == 0, "predecessors split evenly over the waves");
   __shared__ float s_agg[WAVES][NF][TILE];
-  __shared__ float s_carry[PH == EW_FINAL ? WAVES : 1][NF][TILE];
+  __shared__ float s_carry[PH == EW_FINAL || PH == EW_AGG ? WAVES : 1][NF][TILE];
   const int lane = threadIdx.x & (MG_WAVE - 1);
   const int w = threadIdx.x / MG_WAVE;
   const int first = REVERSE ? g.n_chunks - 1 : 0;
@@ -314,6 +357,64 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
   for (int v = 0; v < VEC; ++v)
 #pragma unroll
     for (int f = 0; f < NF; ++f) s_agg[w][f][v * MG_WAVE + lane] = loc[v].get(f);
+  if constexpr (PH == EW_AGG) {
+    if (threadIdx.x == 0) ew_agg_epoch() = ew_agg_tag(header, epoch);  // thread 0's word
+    __syncthreads();  // every wave's aggregate, and the tag, are in LDS
+    const unsigned ep = ew_agg_epoch();
+    if (w == 0) {  // publish this chunk's aggregate (the first chunk's with the seed)
+      Map G[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        G[v] = c == first ? seed[v] : Map::identity();
+        for (int j = 0; j < WAVES; ++j) {
+          const int jj = REVERSE ? WAVES - 1 - j : j;
+          Map a;
+#pragma unroll
+          for (int f = 0; f < NF; ++f) a.set(f, s_agg[jj][f][v * MG_WAVE + lane]);
+          G[v] = compose(G[v], a);
+        }
+      }
+      lb_put<Map, VEC>(agg_data, g, lg, c, lane, G, ep);
+    }
+    // Wave w folds predecessors w*PER .. w*PER+PER-1 in application order, every
+    // slot polled at once and the missing ones again until all have arrived.
+    const int npred = REVERSE ? g.n_chunks - 1 - c : c;
+    Map X[PER][VEC];
+    bool ok[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int k = w * PER + i;
+      ok[i] = k >= npred ||
+              lb_try<Map, VEC>(agg_data, g, lg, REVERSE ? g.n_chunks - 1 - k : k, lane, X[i], ep);
+    }
+    for (unsigned spins = 0;;) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) all &= ok[i];
+      if (all) break;
+      if (++spins >= MG_SPIN_LIMIT) {
+        mg_count_error(header);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int k = w * PER + i;
+        if (!ok[i])
+          ok[i] = lb_try<Map, VEC>(agg_data, g, lg, REVERSE ? g.n_chunks - 1 - k : k, lane, X[i],
+                                   ep);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      Map part = (w == 0 && c == first) ? seed[v] : Map::identity();
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (w * PER + i < npred) part = compose(part, X[i][v]);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) s_carry[w][f][v * MG_WAVE + lane] = part.get(f);
+    }
+  }
   if constexpr (PH == EW_FINAL) {
     // Wave w folds predecessors w*PER .. w*PER+PER-1 in application order
     // (forward: chunks 0, 1, ...; reverse: chunks n-1, n-2, ...), all its loads
@@ -375,7 +476,7 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
     }
   }
 
-  if constexpr (PH == EW_FINAL) {
+  if constexpr (PH == EW_FINAL || PH == EW_AGG) {
     // The partials in order; the first chunk's stored aggregate carries the seed.
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
@@ -458,7 +559,7 @@ __device__ __forceinline__ void ew_carry(const Map (&loc)[VEC], const Map (&seed
 
 struct EwThread {
   int lane, w, c, lg, bb;
-  unsigned epoch;
+  unsigned long long epoch;  // the look-back epoch; EW_AGG: ew_agg_begin's word (thread 0)
   bool valid;  // false only for a ticket beyond the grid (workspace protocol broken)
   int64_t col;
   bool col_ok;
@@ -469,7 +570,7 @@ struct EwThread {
 // for a REVERSE scan).
 template <int VEC, bool REVERSE>
 __device__ __forceinline__ EwThread ew_thread_at(const EwGeom& g, unsigned ticket,
-                                                 unsigned epoch) {
+                                                 unsigned long long epoch) {
   EwThread th;
   th.valid = true;
   th.epoch = epoch;
@@ -491,10 +592,11 @@ __device__ __forceinline__ EwThread ew_thread_at(const EwGeom& g, unsigned ticke
 // workgroup order, since no workgroup waits on another.
 template <int PH, typename Body>
 __device__ __forceinline__ void ew_chunks(const EwGeom& g, unsigned* header, Body&& body) {
-  if constexpr (PH == EW_LOOKBACK)
+  if constexpr (PH == EW_LOOKBACK) {
     mg_persistent(header, (unsigned)g.n_lg * (unsigned)g.n_chunks, body);
-  else
-    body(blockIdx.x, 0u);
+  } else {
+    body(blockIdx.x, PH == EW_AGG ? ew_agg_begin(header) : 0ull);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -529,7 +631,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
   };
   // The chunk from its rows: local aggregates, then `mid` (run by every thread),
   // then the carry and the outputs.
-  auto finish = [&](unsigned ticket, unsigned epoch, const Rows& av, const Rows& bv, auto&& mid) {
+  auto finish = [&](unsigned ticket, unsigned long long epoch, const Rows& av, const Rows& bv, auto&& mid) {
     const EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     Aff<1> loc[VEC], seed[VEC], carry[VEC];
@@ -570,9 +672,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void ew_fwd_kernel(
     }
   };
   if constexpr (PH != EW_LOOKBACK) {
+    const unsigned long long tag = PH == EW_AGG ? ew_agg_begin(header) : 0ull;
     Rows av, bv;
     load(blockIdx.x, av, bv);
-    finish(blockIdx.x, 0u, av, bv, [] {});
+    finish(blockIdx.x, tag, av, bv, [] {});
   } else {
     // Persistent workgroups (mg_persistent's protocol) with two row buffers: the
     // next ticket is shared once this chunk's local aggregates are formed, and its
@@ -624,7 +727,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
@@ -748,24 +851,36 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_fwd_kernel(
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
 
-    Xf av[TSUB][VEC], bv[TSUB][VEC];
+    // Every raw load first, then the exponentials: with each step's exponentials
+    // next to its loads the compiler waited for them step by step.
+    float ra[TSUB][VEC], rb[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
       const int64_t t = t0 + s;
       if (th.col_ok && t < T) {
-        load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
-        load_xf_exp<VEC, NT>(bv[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
+        load_vec<VEC, NT>(ra[s], lc + (th.bb * T + t) * D + th.col);
+        load_vec<VEC, NT>(rb[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
       } else {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
-          av[s][v] = Xf{1.f, 0.f};
-          bv[s][v] = xf_zero();
+          ra[s][v] = 0.f;  // unused: the step is past the end
+          rb[s][v] = 0.f;
         }
+      }
+    }
+    Xf av[TSUB][VEC], bv[TSUB][VEC];
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      const bool ok = th.col_ok && t0 + s < T;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        av[s][v] = ok ? xf_exp(ra[s][v]) : Xf{1.f, 0.f};
+        bv[s][v] = ok ? xf_exp(rb[s][v]) : xf_zero();
       }
     }
 
@@ -828,29 +943,36 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void log_bwd_kernel(
     mg_slot_t* incl_data) {
   constexpr int TSUB = LOG_TSUB;
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
 
     // a as Xf; lv and gh raw until needed.
-    Xf av[TSUB][VEC];
-    float lvr[TSUB][VEC], gr[TSUB][VEC];
+    float ra[TSUB][VEC], lvr[TSUB][VEC], gr[TSUB][VEC];
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
       const int64_t t = t0 + s;
       if (th.col_ok && t < T) {
-        load_xf_exp<VEC, NT>(av[s], lc + (th.bb * T + t) * D + th.col);
+        load_vec<VEC, NT>(ra[s], lc + (th.bb * T + t) * D + th.col);
         if constexpr (PH != EW_REDUCE) load_vec<VEC>(lvr[s], lv + (th.bb * (T + 1) + t + 1) * D + th.col);
         load_vec<VEC, NT>(gr[s], gh + (th.bb * T + t) * D + th.col);
       } else {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
-          av[s][v] = Xf{1.f, 0.f};
+          ra[s][v] = 0.f;  // unused: the step is past the end
           lvr[s][v] = -INFINITY;
           gr[s][v] = 0.f;
         }
       }
+    }
+    // The exponentials after every load is issued (as in the forward).
+    Xf av[TSUB][VEC];
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) {
+      const bool ok = th.col_ok && t0 + s < T;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) av[s][v] = ok ? xf_exp(ra[s][v]) : Xf{1.f, 0.f};
     }
     // An fp32 value as Xf without normalising: only an exact zero needs exponent -inf.
     auto raw = [](float x) { return Xf{x, x == 0.f ? -INFINITY : 0.f}; };
@@ -958,7 +1080,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
@@ -1028,7 +1150,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     float* __restrict__ d0, float* __restrict__ d1, float* __restrict__ d2,
     float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned epoch) {
+  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
@@ -1248,11 +1370,24 @@ bool ew_two_launch(const EwPlan& p, int64_t B, int64_t T, int64_t D, int arrays)
          B * T * D * (int64_t)sizeof(float) * arrays <= EW_TWO_LAUNCH_BYTES;
 }
 
-// One look-back launch, or the reduce and final launches over the same grid.
-template <typename K0, typename K1, typename K2, typename... Args>
-int ew_run(bool two, K0 lookback, K1 reduce, K2 fin, const EwPlan& p, void* ws,
+// One look-back launch, or for a small problem one EW_AGG launch when its whole
+// grid is resident at once (so the workgroups it waits on are running), else the
+// reduce and final launches over the same grid.
+// MINGRU_HIP_EW_FORM=two keeps a small problem on the two-launch form even where
+// EW_AGG fits (the tests use it to cover both forms); unset, or any other value,
+// leaves the choice to the residency check.
+bool ew_force_two() {
+  const char* v = getenv("MINGRU_HIP_EW_FORM");
+  return v && v[0] == 't' && v[1] == 'w' && v[2] == 'o' && v[3] == 0;
+}
+
+template <typename K0, typename K1, typename K2, typename K3, typename... Args>
+int ew_run(bool two, K0 lookback, K1 reduce, K2 fin, K3 agg, const EwPlan& p, void* ws,
            hipStream_t stream, Args... args) {
   if (!two) return ew_launch(lookback, p, ws, stream, true, args...);
+  const unsigned chunks = (unsigned)p.g.n_lg * (unsigned)p.g.n_chunks;
+  if (!ew_force_two() && chunks <= mg_resident((const void*)agg, MG_WAVE * p.waves))
+    return ew_launch(agg, p, ws, stream, false, args...);
   const int rc = ew_launch(reduce, p, ws, stream, false, args...);
   return rc != MG_OK ? rc : ew_launch(fin, p, ws, stream, false, args...);
 }
@@ -1311,7 +1446,8 @@ int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const flo
     return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>()),
                   gate_fwd_kernel<V, TS, EW_WAVES_FWD, G>,
                   gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_REDUCE>,
-                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_FINAL>, p, ws, stream, p0, p1, p2, h0,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_FINAL>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_AGG>, p, ws, stream, p0, p1, p2, h0,
                   h);
   });
 }
@@ -1390,7 +1526,8 @@ int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const flo
     return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>() + 1),
                   gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G>,
                   gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_REDUCE>,
-                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_FINAL>, p, ws, stream,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_FINAL>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_AGG>, p, ws, stream,
                   p0, p1, p2, h0, h, gh, d0, d1, d2, dh0);
   });
 }
@@ -1406,7 +1543,8 @@ int linear_fwd_launch(const float* a, const float* b, float* A, float* Bc, int64
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, 2), ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD>,
                   ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_REDUCE>,
-                  ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_FINAL>, p, ws, stream, a, b, A,
+                  ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_FINAL>,
+                  ew_fwd_kernel<V, EW_TSUB_FWD, EW_WAVES_FWD, EW_AGG>, p, ws, stream, a, b, A,
                   Bc);
   });
 }
@@ -1490,7 +1628,8 @@ int mg_linear_scan_bwd(const float* a, const float* b, const float* A, const flo
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, 4), linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD>,
                   linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_REDUCE>,
-                  linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_FINAL>, p, ws, stream, a, b,
+                  linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_FINAL>,
+                  linear_bwd_kernel<V, EW_TSUB_BWD, EW_WAVES_BWD, EW_AGG>, p, ws, stream, a, b,
                   A, Bc, gA, gB, da, db);
   });
 }
@@ -1554,6 +1693,7 @@ int mg_log_scan_fwd(const float* lc, const float* lv, float* h, float* hstate, i
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, 2), log_fwd_kernel<V, LOG_WAVES>,
                   log_fwd_kernel<V, LOG_WAVES, EW_REDUCE>, log_fwd_kernel<V, LOG_WAVES, EW_FINAL>,
+                  log_fwd_kernel<V, LOG_WAVES, EW_AGG>,
                   p, ws, stream, lc, lv, h, hstate);
   };
   return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});
@@ -1570,6 +1710,7 @@ int mg_log_scan_bwd(const float* lc, const float* lv, const float* h, const floa
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, 3), log_bwd_kernel<V, LOG_WAVES>,
                   log_bwd_kernel<V, LOG_WAVES, EW_REDUCE>, log_bwd_kernel<V, LOG_WAVES, EW_FINAL>,
+                  log_bwd_kernel<V, LOG_WAVES, EW_AGG>,
                   p, ws, stream, lc, lv, h, hstate, gh, dlc, dlv);
   };
   return vec == 2 ? run(std::integral_constant<int, 2>{}) : run(std::integral_constant<int, 1>{});

@@ -321,3 +321,35 @@ def test_parallel_scan_log_backward_without_state_record(cuda):
     for dlc, dlv in grads:
         assert _maxerr(dlc, rdlc) <= GRAD_TOL and _maxerr(dlv, rdlv) <= GRAD_TOL
     assert int(ws[8:12].view(torch.int32).item()) == 0
+
+
+# Small problems (at most 32 chunks per sequence and 32 MB of inputs) run as one launch
+# whose workgroups publish their chunk aggregates and fold their predecessors' (when the
+# whole grid is resident, as at these shapes), or as two launches (aggregates, then the
+# fold).  MINGRU_HIP_EW_FORM=two forces the second form, so both are checked here.
+SMALL_FORM_SHAPES = [(4, 1024, 256), (2, 2048, 64), (2, 777, 136), (3, 64, 64), (1, 5, 3)]
+
+
+@pytest.mark.parametrize("form", ["auto", "two"])
+@pytest.mark.parametrize("shape", SMALL_FORM_SHAPES)
+def test_small_problem_launch_forms(cuda, shape, form, monkeypatch):
+    B, T, D = shape
+    print(f"[gpu] launch form {form}: linear_scan + parallel_scan_log shape={shape}", flush=True)
+    monkeypatch.setenv("MINGRU_HIP_EW_FORM", form)
+    g = torch.Generator().manual_seed(5 + T + D)
+    a = torch.tanh(2 * torch.randn(B, T, D, generator=g))
+    b = torch.randn(B, T, D, generator=g)
+    gA = torch.randn(B, T, D, generator=g)
+    gB = torch.randn(B, T, D, generator=g)
+    A, Bc, da, db = _run_linear(a, b, gA, gB, cuda)
+    rA, rB = orc.linear_scan(a.numpy(), b.numpy())
+    rda, rdb = orc.linear_scan_bwd(a.numpy(), b.numpy(), gA.numpy(), gB.numpy())
+    assert _maxerr(A, rA) <= FWD_TOL and _maxerr(Bc, rB) <= FWD_TOL
+    assert _maxerr(da, rda) <= GRAD_TOL and _maxerr(db, rdb) <= GRAD_TOL
+    inp = wl.c1_inputs(B, T, D)
+    lc, lv, gh = inp["log_coeffs"], inp["log_values"], inp["grad_h"]
+    h, dlc, dlv = _run_log(lc, lv, gh, cuda)
+    rh = orc.parallel_scan_log(lc.numpy(), lv.numpy())
+    rdlc, rdlv = orc.parallel_scan_log_bwd(lc.numpy(), lv.numpy(), gh.numpy())
+    assert _maxerr(h, rh) <= FWD_TOL
+    assert _maxerr(dlc, rdlc) <= GRAD_TOL and _maxerr(dlv, rdlv) <= GRAD_TOL

@@ -120,3 +120,11 @@ def test_mingru_with_decay_keeps_the_unfused_scan(cuda, monkeypatch):
     y = m(x, delta_t=dt)
     assert "MinGRUGateScanFn" not in type(y.grad_fn).__name__
     assert torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("case", [(2, 777, 136, 2.0), (4, 1024, 256, 1.0), (2, 1024, 64, 1.0)])
+def test_small_problem_two_launch_form(cuda, case, monkeypatch):
+    """The same parity on the two-launch form (MINGRU_HIP_EW_FORM=two); by default these
+    shapes run as one launch whose workgroups fold their predecessors' aggregates."""
+    monkeypatch.setenv("MINGRU_HIP_EW_FORM", "two")
+    test_mingru_gate_scan_matches_fp64(cuda, case)
