@@ -89,6 +89,39 @@ int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, c
                             float* dh0, int64_t B, int64_t T, int64_t D, int coupled, void* ws,
                             size_t ws_bytes, mg_stream_t stream);
 
+/* ---- time decay of the fused gate scans ---------------------------------------------
+ * No reference kernel: the decay-active forms of the two fused gate scans, replacing
+ * the mixers' eager decay (DecayMixin._decay_gamma folded into a,
+ * src/mingru/min_gru.py:1807-1813 for SignedMinGRU, and MinGRU's log coefficient
+ * minus lam dt, :1383-1393).  The coefficient a is multiplied by
+ * gamma = exp(-lam[d] dt[b, t]) in the kernel: dt (B, T) is the normalised delta_t,
+ * lam (D) the per-channel rate (a fixed rate repeated).  The backward also writes,
+ * where the pointer is not NULL, row-wise partial sums of
+ *   dlam: mg_gate_decay_dlam_rows(B, T, D) rows of D floats (dL/dlam = their sum),
+ *   ddt:  mg_gate_decay_ddt_rows(B, T, D) rows of B*T floats (dL/ddt = their sum);
+ * every row is written.  Workspace as the matching undecayed entry point. */
+int mg_signed_gate_scan_decay_fwd(const float* s, const float* z, const float* hpre,
+                                  const float* h0, const float* dt, const float* lam, float* h,
+                                  int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                                  size_t ws_bytes, mg_stream_t stream);
+int mg_signed_gate_scan_decay_bwd(const float* s, const float* z, const float* hpre,
+                                  const float* h0, const float* dt, const float* lam,
+                                  const float* h, const float* gh, float* ds, float* dz,
+                                  float* dhpre, float* dh0, float* dlam, float* ddt, int64_t B,
+                                  int64_t T, int64_t D, int coupled, void* ws, size_t ws_bytes,
+                                  mg_stream_t stream);
+int mg_mingru_gate_scan_decay_fwd(const float* k, const float* hpre, const float* log_h0,
+                                  const float* dt, const float* lam, float* h, int64_t B,
+                                  int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                                  mg_stream_t stream);
+int mg_mingru_gate_scan_decay_bwd(const float* k, const float* hpre, const float* log_h0,
+                                  const float* dt, const float* lam, const float* h,
+                                  const float* gh, float* dk, float* dhpre, float* dlog_h0,
+                                  float* dlam, float* ddt, int64_t B, int64_t T, int64_t D,
+                                  void* ws, size_t ws_bytes, mg_stream_t stream);
+int64_t mg_gate_decay_dlam_rows(int64_t B, int64_t T, int64_t D);
+int64_t mg_gate_decay_ddt_rows(int64_t B, int64_t T, int64_t D);
+
 /* ---- fused MinGRU gates + parallel_scan_log, (B, T, D) -------------------------
  * No reference kernel fuses these: replaces MinGRU.forward's coefficient code and
  * its scan call (src/mingru/min_gru.py:1366-1397): log(1 - z) = -softplus(k),

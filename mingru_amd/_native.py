@@ -39,6 +39,12 @@ _SIGNATURES = {
     "mg_signed_gate_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "mg_signed_gate_scan_fwd": (_I32, [_P] * 5 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),
     "mg_signed_gate_scan_bwd": (_I32, [_P] * 10 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),
+    "mg_signed_gate_scan_decay_fwd": (_I32, [_P] * 7 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),
+    "mg_signed_gate_scan_decay_bwd": (_I32, [_P] * 14 + [_I64, _I64, _I64, _I32, _P, _SZ, _P]),
+    "mg_mingru_gate_scan_decay_fwd": (_I32, [_P] * 6 + [_I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_mingru_gate_scan_decay_bwd": (_I32, [_P] * 12 + [_I64, _I64, _I64, _P, _SZ, _P]),
+    "mg_gate_decay_dlam_rows": (_I64, [_I64, _I64, _I64]),
+    "mg_gate_decay_ddt_rows": (_I64, [_I64, _I64, _I64]),
     "mg_mingru_gate_scan_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "mg_mingru_gate_scan_fwd": (_I32, [_P] * 4 + [_I64, _I64, _I64, _P, _SZ, _P]),
     "mg_mingru_gate_scan_bwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _P, _SZ, _P]),

@@ -1074,16 +1074,40 @@ constexpr int gate_inputs() {
   return G == GATE_MINGRU ? 2 : 3;
 }
 
-template <int VEC, int TSUB, int WAVES, int G, int PH = EW_LOOKBACK>
+// Time decay of the fused gate scans (DEC): the coefficient a is multiplied by
+// gamma = exp(-lam[d] dt[b, t]) (the mixers' DecayMixin, reference
+// src/mingru/min_gru.py:1807-1813 for SignedMinGRU; MinGRU's log-space form
+// log a - lam dt, :1383-1393, is the same factor).  dt (B, T) is already
+// normalised by the caller, lam (D) holds the per-channel rate (a fixed rate
+// broadcast).  The backward writes, when asked, deterministic partial sums of
+//   dL/dlam[d]  = -sum_{b,t} dt a dL/da      into dlam [B * chunks][D] (one row per
+//                                            (batch row, 32-step backward chunk)),
+//   dL/ddt[b,t] = -sum_d lam a dL/da         into ddt [ceil(D / 64)][B][T] (one row
+//                                            per tile of 64 columns),
+// with a the decayed coefficient; the caller sums the rows.
+struct GateDecay {
+  const float* dt;
+  const float* lam;
+  float* dlam;  // backward; may be null
+  float* ddt;   // backward; may be null
+};
+
+constexpr float GATE_LOG2E = 1.44269504088896341f;
+
+template <int VEC, int TSUB, int WAVES, int G, bool DEC, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
-    const float* __restrict__ h0, float* __restrict__ h, EwGeom g, unsigned* header,
-    mg_slot_t* agg_data, mg_slot_t* incl_data) {
+    const float* __restrict__ h0, float* __restrict__ h, GateDecay dec, EwGeom g,
+    unsigned* header, mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
   ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
+    float nlam[VEC];  // -lam log2(e) per column
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      nlam[v] = DEC && th.col_ok && th.col + v < D ? -GATE_LOG2E * dec.lam[th.col + v] : 0.f;
 
     float av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
@@ -1095,9 +1119,12 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
         load_vec<VEC, NT>(x0, p0 + off);
         load_vec<VEC, NT>(x1, p1 + off);
         if constexpr (gate_inputs<G>() == 3) load_vec<VEC, NT>(x2, p2 + off);
+        const float dtv = DEC ? dec.dt[th.bb * T + t] : 0.f;
 #pragma unroll
-        for (int v = 0; v < VEC; ++v)
+        for (int v = 0; v < VEC; ++v) {
           gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
+          if constexpr (DEC) av[s][v] *= __builtin_amdgcn_exp2f(nlam[v] * dtv);
+        }
       } else {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
@@ -1143,19 +1170,31 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
 // da = x h_{t-1}, db = x, dh0 = a_1 x_1, through the gate derivatives.  Per step
 // the kernel keeps the adjoint and three gate values:
 //   signed: sigmoid(z), tanh(s), hpre;   MinGRU: sigmoid(-k), sigmoid(k), hpre.
-template <int VEC, int TSUB, int WAVES, int G, int PH = EW_LOOKBACK>
+template <int VEC, int TSUB, int WAVES, int G, bool DEC, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
     const float* __restrict__ h0, const float* __restrict__ h, const float* __restrict__ gh,
     float* __restrict__ d0, float* __restrict__ d1, float* __restrict__ d2,
-    float* __restrict__ dh0, EwGeom g, unsigned* header, mg_slot_t* agg_data,
+    float* __restrict__ dh0, GateDecay dec, EwGeom g, unsigned* header, mg_slot_t* agg_data,
     mg_slot_t* incl_data) {
+  // dL/dlam partials of the workgroup's waves (DEC with dlam).
+  __shared__ float s_dlam[DEC ? WAVES : 1][DEC ? MG_WAVE * VEC : 1];
   ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
     EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
     constexpr bool MIN = G == GATE_MINGRU;
     constexpr bool NT = PH != EW_REDUCE;
+    // Decay: -lam log2(e) per column and dt per step (one value per wave and step).
+    float nlam[VEC], dts[TSUB];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      nlam[v] = DEC && th.col_ok && th.col + v < D ? -GATE_LOG2E * dec.lam[th.col + v] : 0.f;
+#pragma unroll
+    for (int s = 0; s < TSUB; ++s) dts[s] = DEC && t0 + s < T ? dec.dt[th.bb * T + t0 + s] : 0.f;
+    auto gam = [&](int s, int v) {
+      return DEC ? __builtin_amdgcn_exp2f(nlam[v] * dts[s]) : 1.f;
+    };
 
     float ua[TSUB][VEC], ub[TSUB][VEC], hv[TSUB][VEC], x[TSUB][VEC];
 #pragma unroll
@@ -1193,11 +1232,12 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
         }
       }
     }
-    auto coef_a = [&](int s, int v) {
+    auto coef_a0 = [&](int s, int v) {  // the coefficient before decay
       if constexpr (MIN) return ua[s][v];
       else if constexpr (G == GATE_SIGNED_COUPLED) return (1.f - ua[s][v]) * ub[s][v];
       else return ub[s][v];
     };
+    auto coef_a = [&](int s, int v) { return DEC ? coef_a0(s, v) * gam(s, v) : coef_a0(s, v); };
     const bool first_sub = (t0 == 0);
     float hprev[VEC];
     if (th.col_ok && t0 <= T) {
@@ -1249,12 +1289,19 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
       }
       store_vec<VEC>(dh0 + th.bb * D + th.col, y);
     }
+    // Decay: dL/dlam accumulated over this wave's steps, per column.
+    float dl[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) dl[v] = 0.f;
 #pragma unroll
     for (int s = 0; s < TSUB; ++s) {
       float o0[VEC], o1[VEC], o2[VEC];
+      float cdt = 0.f;  // this lane's share of dL/ddt at this step
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        const float xv = x[s][v], da = xv * hprev[v];  // dL/da_t
+        // dL/da_t of the decayed coefficient, and (da) of the coefficient before decay.
+        const float xv = x[s][v], dae = xv * hprev[v];
+        const float gm = gam(s, v), da = DEC ? dae * gm : dae;
         float a, b;
         if constexpr (MIN) {
           // a = sigmoid(-k): da/dk = -a z;  b = z g(hpre): db/dk = z a g, db/dhpre = z g'.
@@ -1273,14 +1320,51 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
           o1[v] = xv * hv[s][v] * dsg - (G == GATE_SIGNED_COUPLED ? da * tv * dsg : 0.f);
           o2[v] = xv * sg;
         }
+        if constexpr (DEC) {
+          a *= gm;
+          const float w = a * dae;  // (decayed a) dL/da; zero past the end and on idle columns
+          dl[v] = fmaf(-dts[s], w, dl[v]);
+          cdt = fmaf(nlam[v], w, cdt);  // -lam log2(e) a dL/da
+        }
         hprev[v] = fmaf(a, hprev[v], b);
       }
       const int64_t t = t0 + s;
+      if constexpr (DEC) {
+        if (dec.ddt != nullptr) {
+          // Sum over each 64-column tile: the 64 / VEC lanes that hold it.
+#pragma unroll
+          for (int m = 1; m < MG_WAVE / VEC; m *= 2) cdt += __shfl_xor(cdt, m);
+          const int64_t tile = th.col / MG_WAVE;
+          if ((th.lane & (MG_WAVE / VEC - 1)) == 0 && th.col < D && t < T)
+            dec.ddt[(tile * (int64_t)(g.n_lg / g.n_tiles) + th.bb) * T + t] =
+                cdt * 0.693147180559945309f;  // undo the log2(e) of nlam
+        }
+      }
       if (th.col_ok && t < T) {
         const int64_t off = (th.bb * T + t) * D + th.col;
         store_vec<VEC>(d0 + off, o0);
         store_vec<VEC>(d1 + off, o1);
         if constexpr (!MIN) store_vec<VEC>(d2 + off, o2);
+      }
+    }
+    if constexpr (DEC) {
+      if (dec.dlam != nullptr) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) s_dlam[th.w][th.lane * VEC + v] = dl[v];
+        __syncthreads();
+        if (th.w == 0 && th.col_ok) {
+          float acc[VEC];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            acc[v] = 0.f;
+            for (int j = 0; j < WAVES; ++j) acc[v] += s_dlam[j][th.lane * VEC + v];
+          }
+          float* row = dec.dlam + ((int64_t)th.bb * g.n_chunks + th.c) * D + th.col;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v)
+            if (th.col + v < D) row[v] = acc[v];
+        }
+        __syncthreads();  // s_dlam is free for the workgroup's next chunk
       }
     }
   });
@@ -1432,9 +1516,9 @@ bool all_aligned16(std::initializer_list<const void*> ps) {
   return true;
 }
 
-template <int G>
+template <int G, bool DEC>
 int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const float* h0, float* h,
-                    int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    GateDecay dec, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
                     hipStream_t stream) {
   const bool v4 = D % 4 == 0 && all_aligned16({p0, p1, p2, h0, h});
   const int vec = ew_vec(B, T, D, v4, EW_WAVES_FWD * EW_TSUB_FWD);
@@ -1444,11 +1528,11 @@ int gate_fwd_launch(const float* p0, const float* p1, const float* p2, const flo
     EwPlan p = ew_plan(B, T, D, V, TS, EW_WAVES_FWD, 1);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>()),
-                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G>,
-                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_REDUCE>,
-                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_FINAL>,
-                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, EW_AGG>, p, ws, stream, p0, p1, p2, h0,
-                  h);
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, DEC>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, DEC, EW_REDUCE>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, DEC, EW_FINAL>,
+                  gate_fwd_kernel<V, TS, EW_WAVES_FWD, G, DEC, EW_AGG>, p, ws, stream, p0, p1, p2,
+                  h0, h, dec);
   });
 }
 
@@ -1512,10 +1596,10 @@ int noalloc_scratch(hipStream_t stream, void** out) {
   return MG_OK;
 }
 
-template <int G>
+template <int G, bool DEC>
 int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const float* h0,
                     const float* h, const float* gh, float* d0, float* d1, float* d2, float* dh0,
-                    int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                    GateDecay dec, int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
                     hipStream_t stream) {
   const bool v4 = D % 4 == 0 && all_aligned16({p0, p1, p2, h0, h, gh, d0, d1, d2, dh0});
   const int vec = ew_vec(B, T, D, v4, GATE_WAVES_BWD * GATE_TSUB_BWD);
@@ -1524,11 +1608,11 @@ int gate_bwd_launch(const float* p0, const float* p1, const float* p2, const flo
     EwPlan p = ew_plan(B, T, D, V, GATE_TSUB_BWD, GATE_WAVES_BWD, 1);
     if (ws_bytes < p.total) return MG_ERR_WORKSPACE;
     return ew_run(ew_two_launch(p, B, T, D, gate_inputs<G>() + 1),
-                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G>,
-                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_REDUCE>,
-                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_FINAL>,
-                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, EW_AGG>, p, ws, stream,
-                  p0, p1, p2, h0, h, gh, d0, d1, d2, dh0);
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, DEC>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, DEC, EW_REDUCE>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, DEC, EW_FINAL>,
+                  gate_bwd_kernel<V, GATE_TSUB_BWD, GATE_WAVES_BWD, G, DEC, EW_AGG>, p, ws, stream,
+                  p0, p1, p2, h0, h, gh, d0, d1, d2, dh0, dec);
   });
 }
 
@@ -1643,9 +1727,11 @@ int mg_signed_gate_scan_fwd(const float* s, const float* z, const float* hpre, c
                             size_t ws_bytes, hipStream_t stream) {
   if (!s || !z || !hpre || !h0 || !h || !ws || !geometry_ok(B, T, D) || (coupled & ~1))
     return MG_ERR_ARG;
-  return coupled ? gate_fwd_launch<GATE_SIGNED_COUPLED>(s, z, hpre, h0, h, B, T, D, ws, ws_bytes,
-                                                        stream)
-                 : gate_fwd_launch<GATE_SIGNED>(s, z, hpre, h0, h, B, T, D, ws, ws_bytes, stream);
+  const GateDecay nd{};
+  return coupled ? gate_fwd_launch<GATE_SIGNED_COUPLED, false>(s, z, hpre, h0, h, nd, B, T, D, ws,
+                                                               ws_bytes, stream)
+                 : gate_fwd_launch<GATE_SIGNED, false>(s, z, hpre, h0, h, nd, B, T, D, ws,
+                                                       ws_bytes, stream);
 }
 
 int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, const float* h0,
@@ -1655,10 +1741,43 @@ int mg_signed_gate_scan_bwd(const float* s, const float* z, const float* hpre, c
   if (!s || !z || !hpre || !h0 || !h || !gh || !ds || !dz || !dhpre || !dh0 || !ws ||
       !geometry_ok(B, T, D) || (coupled & ~1))
     return MG_ERR_ARG;
-  return coupled ? gate_bwd_launch<GATE_SIGNED_COUPLED>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0,
-                                                        B, T, D, ws, ws_bytes, stream)
-                 : gate_bwd_launch<GATE_SIGNED>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0, B, T,
-                                                D, ws, ws_bytes, stream);
+  const GateDecay nd{};
+  return coupled ? gate_bwd_launch<GATE_SIGNED_COUPLED, false>(s, z, hpre, h0, h, gh, ds, dz,
+                                                               dhpre, dh0, nd, B, T, D, ws,
+                                                               ws_bytes, stream)
+                 : gate_bwd_launch<GATE_SIGNED, false>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0,
+                                                       nd, B, T, D, ws, ws_bytes, stream);
+}
+
+int mg_signed_gate_scan_decay_fwd(const float* s, const float* z, const float* hpre,
+                                  const float* h0, const float* dt, const float* lam, float* h,
+                                  int64_t B, int64_t T, int64_t D, int coupled, void* ws,
+                                  size_t ws_bytes, hipStream_t stream) {
+  if (!s || !z || !hpre || !h0 || !dt || !lam || !h || !ws || !geometry_ok(B, T, D) ||
+      (coupled & ~1))
+    return MG_ERR_ARG;
+  const GateDecay dec{dt, lam, nullptr, nullptr};
+  return coupled ? gate_fwd_launch<GATE_SIGNED_COUPLED, true>(s, z, hpre, h0, h, dec, B, T, D, ws,
+                                                              ws_bytes, stream)
+                 : gate_fwd_launch<GATE_SIGNED, true>(s, z, hpre, h0, h, dec, B, T, D, ws,
+                                                      ws_bytes, stream);
+}
+
+int mg_signed_gate_scan_decay_bwd(const float* s, const float* z, const float* hpre,
+                                  const float* h0, const float* dt, const float* lam,
+                                  const float* h, const float* gh, float* ds, float* dz,
+                                  float* dhpre, float* dh0, float* dlam, float* ddt, int64_t B,
+                                  int64_t T, int64_t D, int coupled, void* ws, size_t ws_bytes,
+                                  hipStream_t stream) {
+  if (!s || !z || !hpre || !h0 || !dt || !lam || !h || !gh || !ds || !dz || !dhpre || !dh0 ||
+      !ws || !geometry_ok(B, T, D) || (coupled & ~1))
+    return MG_ERR_ARG;
+  const GateDecay dec{dt, lam, dlam, ddt};
+  return coupled ? gate_bwd_launch<GATE_SIGNED_COUPLED, true>(s, z, hpre, h0, h, gh, ds, dz,
+                                                              dhpre, dh0, dec, B, T, D, ws,
+                                                              ws_bytes, stream)
+                 : gate_bwd_launch<GATE_SIGNED, true>(s, z, hpre, h0, h, gh, ds, dz, dhpre, dh0,
+                                                      dec, B, T, D, ws, ws_bytes, stream);
 }
 
 size_t mg_mingru_gate_scan_workspace_bytes(int64_t B, int64_t T, int64_t D) {
@@ -1669,7 +1788,8 @@ int mg_mingru_gate_scan_fwd(const float* k, const float* hpre, const float* log_
                             int64_t B, int64_t T, int64_t D, void* ws, size_t ws_bytes,
                             hipStream_t stream) {
   if (!k || !hpre || !log_h0 || !h || !ws || !geometry_ok(B, T, D)) return MG_ERR_ARG;
-  return gate_fwd_launch<GATE_MINGRU>(k, hpre, nullptr, log_h0, h, B, T, D, ws, ws_bytes, stream);
+  return gate_fwd_launch<GATE_MINGRU, false>(k, hpre, nullptr, log_h0, h, GateDecay{}, B, T, D,
+                                             ws, ws_bytes, stream);
 }
 
 int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_h0,
@@ -1679,8 +1799,42 @@ int mg_mingru_gate_scan_bwd(const float* k, const float* hpre, const float* log_
   if (!k || !hpre || !log_h0 || !h || !gh || !dk || !dhpre || !dlog_h0 || !ws ||
       !geometry_ok(B, T, D))
     return MG_ERR_ARG;
-  return gate_bwd_launch<GATE_MINGRU>(k, hpre, nullptr, log_h0, h, gh, dk, dhpre, nullptr,
-                                      dlog_h0, B, T, D, ws, ws_bytes, stream);
+  return gate_bwd_launch<GATE_MINGRU, false>(k, hpre, nullptr, log_h0, h, gh, dk, dhpre, nullptr,
+                                             dlog_h0, GateDecay{}, B, T, D, ws, ws_bytes, stream);
+}
+
+int mg_mingru_gate_scan_decay_fwd(const float* k, const float* hpre, const float* log_h0,
+                                  const float* dt, const float* lam, float* h, int64_t B,
+                                  int64_t T, int64_t D, void* ws, size_t ws_bytes,
+                                  hipStream_t stream) {
+  if (!k || !hpre || !log_h0 || !dt || !lam || !h || !ws || !geometry_ok(B, T, D))
+    return MG_ERR_ARG;
+  return gate_fwd_launch<GATE_MINGRU, true>(k, hpre, nullptr, log_h0, h,
+                                            GateDecay{dt, lam, nullptr, nullptr}, B, T, D, ws,
+                                            ws_bytes, stream);
+}
+
+int mg_mingru_gate_scan_decay_bwd(const float* k, const float* hpre, const float* log_h0,
+                                  const float* dt, const float* lam, const float* h,
+                                  const float* gh, float* dk, float* dhpre, float* dlog_h0,
+                                  float* dlam, float* ddt, int64_t B, int64_t T, int64_t D,
+                                  void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!k || !hpre || !log_h0 || !dt || !lam || !h || !gh || !dk || !dhpre || !dlog_h0 || !ws ||
+      !geometry_ok(B, T, D))
+    return MG_ERR_ARG;
+  return gate_bwd_launch<GATE_MINGRU, true>(k, hpre, nullptr, log_h0, h, gh, dk, dhpre, nullptr,
+                                            dlog_h0, GateDecay{dt, lam, dlam, ddt}, B, T, D, ws,
+                                            ws_bytes, stream);
+}
+
+int64_t mg_gate_decay_dlam_rows(int64_t B, int64_t T, int64_t D) {
+  if (B <= 0 || T <= 0 || D <= 0) return 0;
+  return B * ((T + GATE_WAVES_BWD * GATE_TSUB_BWD - 1) / (GATE_WAVES_BWD * GATE_TSUB_BWD));
+}
+
+int64_t mg_gate_decay_ddt_rows(int64_t B, int64_t T, int64_t D) {
+  if (B <= 0 || T <= 0 || D <= 0) return 0;
+  return (D + MG_WAVE - 1) / MG_WAVE;
 }
 
 int mg_log_scan_fwd(const float* lc, const float* lv, float* h, float* hstate, int64_t B,

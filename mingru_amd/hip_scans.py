@@ -375,48 +375,104 @@ def _linear_scan_impl(a: torch.Tensor, b: torch.Tensor):
 # ---------------------------------------------------------------------------
 
 
+def _decay_partials(dims, need_lam: bool, need_dt: bool, device):
+    """Partial-sum buffers of the decay gradients (the kernel writes every row; the
+    caller sums them), or None where the gradient is not needed."""
+    Bn, T, D = dims
+    dlam = (torch.empty(_lib().mg_gate_decay_dlam_rows(Bn, T, D), D, dtype=torch.float32,
+                        device=device) if need_lam else None)
+    ddt = (torch.empty(_lib().mg_gate_decay_ddt_rows(Bn, T, D), Bn, T, dtype=torch.float32,
+                       device=device) if need_dt else None)
+    return dlam, ddt
+
+
+def _decay_args(dt, lam, like: torch.Tensor):
+    """fp32 contiguous ``dt`` (B, T) and ``lam`` (D,) for the decay kernels."""
+    Bn, T, D = like.shape
+    dt32 = dt.to(torch.float32).contiguous()
+    lam32 = lam.to(torch.float32).expand(D).contiguous()
+    return dt32, lam32
+
+
 class _SignedGateScanFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, s, z, hpre, h0, coupled):
+    def forward(ctx, s, z, hpre, h0, dt, lam, coupled):
         out_dtype = s.dtype
         s32, z32, hp32, h032 = _as_f32(s, z, hpre, h0)
         Bn, T, D = s32.shape
         h = torch.empty_like(s32)
         ws = _scan_workspace(_size("mg_signed_gate_scan_workspace_bytes", Bn, T, D), s32.device)
-        _call("mg_signed_gate_scan_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
-              Bn, T, D, int(coupled), _ptr(ws), ws.numel(), _stream(s32))
+        if dt is None:
+            _call("mg_signed_gate_scan_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032),
+                  _ptr(h), Bn, T, D, int(coupled), _ptr(ws), ws.numel(), _stream(s32))
+            dt32 = lam32 = None
+        else:
+            dt32, lam32 = _decay_args(dt, lam, s32)
+            _call("mg_signed_gate_scan_decay_fwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032),
+                  _ptr(dt32), _ptr(lam32), _ptr(h), Bn, T, D, int(coupled), _ptr(ws),
+                  ws.numel(), _stream(s32))
         _check_workspace(ws, s32)
-        ctx.save_for_backward(s32, z32, hp32, h032, h)
+        ctx.save_for_backward(s32, z32, hp32, h032, h, dt32, lam32)
         ctx.coupled = bool(coupled)
-        ctx.out_dtype = out_dtype
+        ctx.dtypes = (out_dtype, None if dt is None else dt.dtype,
+                      None if lam is None else lam.dtype)
         return h if out_dtype == torch.float32 else h.to(out_dtype)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gh):
-        s32, z32, hp32, h032, h = ctx.saved_tensors
+        s32, z32, hp32, h032, h, dt32, lam32 = ctx.saved_tensors
         Bn, T, D = s32.shape
         (gh32,) = _as_f32(gh)
         ds, dz, dhp = (torch.empty_like(s32) for _ in range(3))
         dh0 = torch.empty_like(h032)
         ws = _scan_workspace(_size("mg_signed_gate_scan_workspace_bytes", Bn, T, D), s32.device)
-        _call("mg_signed_gate_scan_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032), _ptr(h),
-              _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, D, int(ctx.coupled),
-              _ptr(ws), ws.numel(), _stream(s32))
+        od, dtd, lamd = ctx.dtypes
+        if dt32 is None:
+            _call("mg_signed_gate_scan_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032),
+                  _ptr(h), _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, D,
+                  int(ctx.coupled), _ptr(ws), ws.numel(), _stream(s32))
+            _check_workspace(ws, s32)
+            return ds.to(od), dz.to(od), dhp.to(od), dh0.to(od), None, None, None
+        need = ctx.needs_input_grad
+        dlam, ddt = _decay_partials((Bn, T, D), need[5], need[4], s32.device)
+        _call("mg_signed_gate_scan_decay_bwd", _ptr(s32), _ptr(z32), _ptr(hp32), _ptr(h032),
+              _ptr(dt32), _ptr(lam32), _ptr(h), _ptr(gh32), _ptr(ds), _ptr(dz), _ptr(dhp),
+              _ptr(dh0), _ptr(dlam), _ptr(ddt), Bn, T, D, int(ctx.coupled), _ptr(ws),
+              ws.numel(), _stream(s32))
         _check_workspace(ws, s32)
-        od = ctx.out_dtype
-        return ds.to(od), dz.to(od), dhp.to(od), dh0.to(od), None
+        g_dt = ddt.sum(0).to(dtd) if ddt is not None else None
+        g_lam = dlam.sum(0).to(lamd) if dlam is not None else None
+        return ds.to(od), dz.to(od), dhp.to(od), dh0.to(od), g_dt, g_lam, None
+
+
+def _check_decay(what: str, like: torch.Tensor, dt, lam) -> None:
+    if (dt is None) != (lam is None):
+        raise ScanFallback(f"{what}: dt and lam must be given together")
+    if dt is None:
+        return
+    Bn, T, D = like.shape
+    if tuple(dt.shape) != (Bn, T) or not (lam.ndim == 0 or tuple(lam.shape) in ((1,), (D,))):
+        raise ScanFallback(
+            f"{what} decay (dt={tuple(dt.shape)}, lam={tuple(lam.shape)}) outside the HIP "
+            f"envelope: need dt (B, T) and lam () or (D,)"
+        )
+    _same_device(like, dt, lam)
 
 
 def signed_gate_scan_impl(s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor,
-                          h0: torch.Tensor, *, coupled: bool):
+                          h0: torch.Tensor, *, coupled: bool, dt: torch.Tensor | None = None,
+                          lam: torch.Tensor | None = None):
     """Fused SignedMinGRU coefficients + ``linear_scan``: ``h`` (B, T, D).
 
     No reference kernel fuses these; the arithmetic is the mixer's
     (``src/mingru/min_gru.py:1788-1857``): ``a = tanh(s)`` (times
     ``1 - sigmoid(z)`` when ``coupled``), ``b = sigmoid(z) * hpre`` and
     ``h = A * h0 + Bc`` with ``(A, Bc) = linear_scan(a, b)``, for pre-activations
-    ``s, z, hpre`` (B, T, D) and ``h0`` (B, 1, D).  Differentiable in all four.
+    ``s, z, hpre`` (B, T, D) and ``h0`` (B, 1, D).  With time decay (the module's
+    ``delta_t``, reference ``:1807-1813``) ``a`` is multiplied by
+    ``exp(-lam * dt)`` inside the kernel, for the normalised ``dt`` (B, T) and the
+    rate ``lam`` (a scalar, or (D,) per channel).  Differentiable in every input.
     """
     if (
         s.ndim != 3
@@ -430,9 +486,11 @@ def signed_gate_scan_impl(s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor,
             "and a (B, 1, D) h0"
         )
     _same_device(s, z, hpre, h0)
+    _check_decay("signed gate scan", s, dt, lam)
     if s.numel() == 0:
         return s.new_empty(s.shape)
-    return _funnel("signed gate scan", _SignedGateScanFn.apply, s, z, hpre, h0, bool(coupled))
+    return _funnel("signed gate scan", _SignedGateScanFn.apply, s, z, hpre, h0, dt, lam,
+                   bool(coupled))
 
 
 # ---------------------------------------------------------------------------
@@ -442,37 +500,56 @@ def signed_gate_scan_impl(s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor,
 
 class _MinGRUGateScanFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, k, hpre, log_h0):
+    def forward(ctx, k, hpre, log_h0, dt, lam):
         out_dtype = k.dtype
         k32, hp32, lh032 = _as_f32(k, hpre, log_h0)
         Bn, T, D = k32.shape
         h = torch.empty_like(k32)
         ws = _scan_workspace(_size("mg_mingru_gate_scan_workspace_bytes", Bn, T, D), k32.device)
-        _call("mg_mingru_gate_scan_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
-              Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
+        if dt is None:
+            _call("mg_mingru_gate_scan_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
+                  Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
+            dt32 = lam32 = None
+        else:
+            dt32, lam32 = _decay_args(dt, lam, k32)
+            _call("mg_mingru_gate_scan_decay_fwd", _ptr(k32), _ptr(hp32), _ptr(lh032),
+                  _ptr(dt32), _ptr(lam32), _ptr(h), Bn, T, D, _ptr(ws), ws.numel(),
+                  _stream(k32))
         _check_workspace(ws, k32)
-        ctx.save_for_backward(k32, hp32, lh032, h)
-        ctx.out_dtype = out_dtype
+        ctx.save_for_backward(k32, hp32, lh032, h, dt32, lam32)
+        ctx.dtypes = (out_dtype, None if dt is None else dt.dtype,
+                      None if lam is None else lam.dtype)
         return h if out_dtype == torch.float32 else h.to(out_dtype)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gh):
-        k32, hp32, lh032, h = ctx.saved_tensors
+        k32, hp32, lh032, h, dt32, lam32 = ctx.saved_tensors
         Bn, T, D = k32.shape
         (gh32,) = _as_f32(gh)
         dk, dhp = torch.empty_like(k32), torch.empty_like(k32)
         dlh0 = torch.empty_like(lh032)
         ws = _scan_workspace(_size("mg_mingru_gate_scan_workspace_bytes", Bn, T, D), k32.device)
-        _call("mg_mingru_gate_scan_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
-              _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), Bn, T, D,
-              _ptr(ws), ws.numel(), _stream(k32))
+        od, dtd, lamd = ctx.dtypes
+        if dt32 is None:
+            _call("mg_mingru_gate_scan_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(h),
+                  _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), Bn, T, D,
+                  _ptr(ws), ws.numel(), _stream(k32))
+            _check_workspace(ws, k32)
+            return dk.to(od), dhp.to(od), dlh0.to(od), None, None
+        need = ctx.needs_input_grad
+        dlam, ddt = _decay_partials((Bn, T, D), need[4], need[3], k32.device)
+        _call("mg_mingru_gate_scan_decay_bwd", _ptr(k32), _ptr(hp32), _ptr(lh032), _ptr(dt32),
+              _ptr(lam32), _ptr(h), _ptr(gh32), _ptr(dk), _ptr(dhp), _ptr(dlh0), _ptr(dlam),
+              _ptr(ddt), Bn, T, D, _ptr(ws), ws.numel(), _stream(k32))
         _check_workspace(ws, k32)
-        od = ctx.out_dtype
-        return dk.to(od), dhp.to(od), dlh0.to(od)
+        g_dt = ddt.sum(0).to(dtd) if ddt is not None else None
+        g_lam = dlam.sum(0).to(lamd) if dlam is not None else None
+        return dk.to(od), dhp.to(od), dlh0.to(od), g_dt, g_lam
 
 
-def mingru_gate_scan_impl(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor):
+def mingru_gate_scan_impl(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor,
+                          dt: torch.Tensor | None = None, lam: torch.Tensor | None = None):
     """Fused MinGRU coefficients + ``parallel_scan_log``: ``h`` (B, T, D).
 
     No reference kernel fuses these; the arithmetic is the mixer's
@@ -481,8 +558,11 @@ def mingru_gate_scan_impl(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Ten
     ``h = exp(parallel_scan_log(log(1 - z), [log_h0, log z + log h~]))``, run as
     the equivalent linear recurrence ``h_t = sigmoid(-k) h_{t-1} +
     sigmoid(k) g(hpre)`` from ``h_0 = exp(log_h0)`` (all terms positive).
-    ``k, hpre`` are (B, T, D) pre-activations, ``log_h0`` is (B, 1, D).
-    Differentiable in all three.
+    ``k, hpre`` are (B, T, D) pre-activations, ``log_h0`` is (B, 1, D).  With
+    time decay the log coefficient gains ``-lam * dt`` (reference ``:1383-1393``):
+    the kernel multiplies ``sigmoid(-k)`` by ``exp(-lam * dt)`` for the normalised
+    ``dt`` (B, T) and the rate ``lam`` (a scalar, or (D,)).  Differentiable in every
+    input.
     """
     if k.ndim != 3 or hpre.shape != k.shape or tuple(log_h0.shape) != (k.shape[0], 1, k.shape[2]):
         raise ScanFallback(
@@ -491,9 +571,10 @@ def mingru_gate_scan_impl(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Ten
             "pre-activations and a (B, 1, D) log_h0"
         )
     _same_device(k, hpre, log_h0)
+    _check_decay("MinGRU gate scan", k, dt, lam)
     if k.numel() == 0:
         return k.new_empty(k.shape)
-    return _funnel("MinGRU gate scan", _MinGRUGateScanFn.apply, k, hpre, log_h0)
+    return _funnel("MinGRU gate scan", _MinGRUGateScanFn.apply, k, hpre, log_h0, dt, lam)
 
 
 # ---------------------------------------------------------------------------

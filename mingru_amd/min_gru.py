@@ -221,15 +221,18 @@ def _dispatch_angle_scan(
 
 
 def _dispatch_signed_gate_scan(
-    s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor, h0: torch.Tensor, *, coupled: bool
+    s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor, h0: torch.Tensor, *, coupled: bool,
+    dt: torch.Tensor | None = None, lam: torch.Tensor | None = None,
 ):
     """Run SignedMinGRU's coefficients and scan as one fused kernel, or return ``None``.
 
     The reference has no fused path here; its mixer computes ``a, b`` eagerly
     and calls ``linear_scan`` (``src/mingru/min_gru.py:1788-1857``), which is
-    what ``None`` falls back to.  Mode handling follows the other fast paths:
-    ``eager`` and CPU ``auto`` return ``None`` silently, ``auto`` warns once
-    on a decline, the forcing mode raises.  Returns ``h`` ``(B, T, D)``.
+    what ``None`` falls back to.  With time decay, ``dt`` (B, T) and the rate
+    ``lam`` give ``a * exp(-lam * dt)`` (``:1807-1813``) inside the kernel.  Mode
+    handling follows the other fast paths: ``eager`` and CPU ``auto`` return
+    ``None`` silently, ``auto`` warns once on a decline, the forcing mode raises.
+    Returns ``h`` ``(B, T, D)``.
     """
     mode = _resolve_scan_mode(s.is_cuda)
     if mode is None:
@@ -241,7 +244,9 @@ def _dispatch_signed_gate_scan(
             raise backend.ScanFallback(str(status))
         if not hasattr(backend, "signed_gate_scan_impl"):
             raise backend.ScanFallback("no fused SignedMinGRU gate kernel registered")
-        return backend.signed_gate_scan_impl(s, z, hpre, h0, coupled=coupled)
+        if dt is None:
+            return backend.signed_gate_scan_impl(s, z, hpre, h0, coupled=coupled)
+        return backend.signed_gate_scan_impl(s, z, hpre, h0, coupled=coupled, dt=dt, lam=lam)
 
     result, reason = _resolve_native_dispatch(mode, "the fused SignedMinGRU gate path", _call)
     if reason is None:
@@ -257,14 +262,16 @@ def _dispatch_signed_gate_scan(
     return None
 
 
-def _dispatch_mingru_gate_scan(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor):
+def _dispatch_mingru_gate_scan(k: torch.Tensor, hpre: torch.Tensor, log_h0: torch.Tensor,
+                               dt: torch.Tensor | None = None, lam: torch.Tensor | None = None):
     """Run MinGRU's log-space coefficients and scan as one fused kernel, or return ``None``.
 
     The reference has no fused path here; its mixer forms ``-softplus(k)``,
     ``-softplus(-k) + log_g(hpre)`` eagerly and calls ``parallel_scan_log``
     (``src/mingru/min_gru.py:1366-1397``), which is what ``None`` falls back
-    to.  Mode handling as for ``_dispatch_signed_gate_scan``.  Returns ``h``
-    ``(B, T, D)``.
+    to.  With time decay the log coefficient gains ``-lam * dt`` (``:1383-1393``)
+    inside the kernel.  Mode handling as for ``_dispatch_signed_gate_scan``.
+    Returns ``h`` ``(B, T, D)``.
     """
     mode = _resolve_scan_mode(k.is_cuda)
     if mode is None:
@@ -276,7 +283,9 @@ def _dispatch_mingru_gate_scan(k: torch.Tensor, hpre: torch.Tensor, log_h0: torc
             raise backend.ScanFallback(str(status))
         if not hasattr(backend, "mingru_gate_scan_impl"):
             raise backend.ScanFallback("no fused MinGRU gate kernel registered")
-        return backend.mingru_gate_scan_impl(k, hpre, log_h0)
+        if dt is None:
+            return backend.mingru_gate_scan_impl(k, hpre, log_h0)
+        return backend.mingru_gate_scan_impl(k, hpre, log_h0, dt, lam)
 
     result, reason = _resolve_native_dispatch(mode, "the fused MinGRU gate path", _call)
     if reason is None:
@@ -754,11 +763,14 @@ class MinGRU(DecayMixin, nn.Module):
         k = self.linear_z(x)
         dt = self._prepare_decay(delta_t, canonical_ndim=2)
         h_pre = self.linear_h(x)
+        # Coefficients (with the decay, if any) and scan in one kernel where the native
+        # backend takes it.
         if dt is None:
-            # Coefficients and scan in one kernel where the native backend takes it.
             h = _dispatch_mingru_gate_scan(k, h_pre, log_h_0)
-            if h is not None:
-                return h
+        else:
+            h = _dispatch_mingru_gate_scan(k, h_pre, log_h_0, dt, self._decay_lambda())
+        if h is not None:
+            return h
         log_z = -F.softplus(-k)
         log_coeffs = -F.softplus(k)
         if dt is not None:
@@ -840,11 +852,15 @@ class SignedMinGRU(DecayMixin, nn.Module):
             )
         dt = self._prepare_decay(delta_t, canonical_ndim=2)
         z_pre, h_pre, s_pre = self.linear_z(x), self.linear_h(x), self.linear_s(x)
+        # GPU fast path: gates (with the decay, if any), scan and h = A h0 + Bc in one
+        # fused kernel.
         if dt is None:
-            # GPU fast path: gates, scan and h = A h0 + Bc in one fused kernel.
             h = _dispatch_signed_gate_scan(s_pre, z_pre, h_pre, h_0, coupled=self.coupled)
-            if h is not None:
-                return h
+        else:
+            h = _dispatch_signed_gate_scan(s_pre, z_pre, h_pre, h_0, coupled=self.coupled,
+                                           dt=dt, lam=self._decay_lambda())
+        if h is not None:
+            return h
         a, b = self._coeffs_from(z_pre, h_pre, s_pre, dt)
         A, Bc = linear_scan(a, b)
         return A * h_0 + Bc

@@ -20,7 +20,7 @@ def _declared():
     names = []
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names += re.findall(r"^\s*(?:int|size_t)\s+(mg_\w+)\s*\(", text, flags=re.M)
+        names += re.findall(r"^\s*(?:int|size_t|int64_t)\s+(mg_\w+)\s*\(", text, flags=re.M)
     return sorted(set(names))
 
 

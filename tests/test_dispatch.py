@@ -357,13 +357,39 @@ def test_signed_gate_seam_hands_preactivations_to_backend(monkeypatch):
     assert torch.equal(y, torch.full((2, 9, 6), 7.0))
 
 
-def test_signed_gate_seam_skips_fusion_under_decay(monkeypatch):
-    """With decay the coefficients carry gamma(dt): no fused call, the scan seam runs."""
+def test_signed_gate_seam_fuses_the_decay(monkeypatch):
+    """With decay the fused call carries the normalised dt and the rate lambda; the
+    eager coefficients and the scan seam do not run."""
+    seen = {}
+
+    def fake_gate(s, z, hpre, h0, *, coupled, dt=None, lam=None):
+        seen.update(dt=dt, lam=lam, coupled=coupled)
+        return torch.full(s.shape, 3.0)
+
+    def fake_linear(a, b):
+        raise AssertionError("the scan seam must not run when the fused path takes decay")
+
+    _fake_backend(monkeypatch, signed_gate_scan_impl=fake_gate,
+                  SCAN_IMPLS={"linear_scan": fake_linear})
+    m = SignedMinGRU(4, 5, decay="fixed", decay_rate=0.7)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    dt = torch.rand(2, 6)
+    dt[0, 1] = float("nan")
+    y = m(torch.randn(2, 6, 4), delta_t=dt)
+    assert torch.equal(y, torch.full((2, 6, 5), 3.0))
+    assert seen["coupled"] is False
+    assert torch.equal(seen["dt"], dt.nan_to_num(0.0))  # normalised by the module
+    assert float(seen["lam"]) == pytest.approx(0.7)
+
+
+def test_signed_gate_decay_decline_raises_in_forcing_mode(monkeypatch):
+    """A declined fused call under decay raises in the forcing mode, naming the reason
+    (auto would fall back to the eager coefficients and the scan seam)."""
     calls = []
 
     def fake_gate(*args, **kwargs):
         calls.append("gate")
-        raise AssertionError("fused path must not run under decay")
+        raise sys.modules[BACKEND].ScanFallback("declined by the fake backend")
 
     def fake_linear(a, b):
         calls.append("linear_scan")
@@ -373,8 +399,26 @@ def test_signed_gate_seam_skips_fusion_under_decay(monkeypatch):
                   SCAN_IMPLS={"linear_scan": fake_linear})
     m = SignedMinGRU(4, 5, decay="fixed")
     monkeypatch.setenv("MINGRU_SCAN", "hip")
-    m(torch.randn(2, 6, 4), delta_t=torch.rand(2, 6))
-    assert calls == ["linear_scan"]
+    with pytest.raises(RuntimeError, match="declined by the fake backend"):
+        m(torch.randn(2, 6, 4), delta_t=torch.rand(2, 6))
+    assert calls == ["gate"]
+
+
+def test_mingru_gate_seam_fuses_the_decay(monkeypatch):
+    seen = {}
+
+    def fake_gate(k, hpre, log_h0, dt=None, lam=None):
+        seen.update(dt=dt, lam=lam)
+        return torch.full(k.shape, 2.0)
+
+    _fake_backend(monkeypatch, mingru_gate_scan_impl=fake_gate)
+    m = MinGRU(4, 5, decay="learnable", decay_rate=0.5)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    dt = torch.rand(2, 6)
+    y = m(torch.randn(2, 6, 4), delta_t=dt)
+    assert torch.equal(y, torch.full((2, 6, 5), 2.0))
+    assert torch.equal(seen["dt"], dt)
+    assert seen["lam"].shape == (5,) and torch.allclose(seen["lam"], torch.full((5,), 0.5))
 
 
 def _seq_bc(a, b):
@@ -419,27 +463,6 @@ def test_mingru_gate_seam_hands_preactivations_to_backend(monkeypatch):
     assert seen["k"] == seen["hpre"] == (2, 9, 6)
     assert torch.allclose(seen["log_h0"], torch.full((2, 1, 6), 0.5).log())
     assert torch.equal(y, torch.full((2, 9, 6), 3.0))
-
-
-def test_mingru_gate_seam_skips_fusion_under_decay(monkeypatch):
-    """With decay log(1 - z) carries -lambda dt: no fused call, the parallel_scan_log
-    seam runs instead."""
-    calls = []
-
-    def fake_gate(*args, **kwargs):
-        calls.append("gate")
-        raise AssertionError("fused path must not run under decay")
-
-    def fake_log(lc, lv):
-        calls.append("parallel_scan_log")
-        return torch.zeros_like(lc)
-
-    _fake_backend(monkeypatch, mingru_gate_scan_impl=fake_gate,
-                  SCAN_IMPLS={"parallel_scan_log": fake_log})
-    m = MinGRU(4, 5, decay="fixed")
-    monkeypatch.setenv("MINGRU_SCAN", "hip")
-    m(torch.randn(2, 6, 4), delta_t=torch.rand(2, 6))
-    assert calls == ["parallel_scan_log"]
 
 
 def test_mingru_gate_auto_fallback_warns_once_and_runs_eager(monkeypatch):

@@ -99,18 +99,94 @@ def test_signed_mingru_module_runs_fused_and_matches_fp64(cuda, coupled, monkeyp
         assert err <= GRAD_TOL, f"{name} grad max abs err {err:.3e}"
 
 
-def test_signed_mingru_with_decay_keeps_the_unfused_scan(cuda, monkeypatch):
-    """Decay multiplies a by gamma(dt): the module computes the coefficients eagerly
-    and runs the HIP linear_scan instead of the fused kernel."""
-    print("[gpu] SignedMinGRU decay path", flush=True)
+def _ref_decay(s, z, hp, h0, dt, lam, coupled):
+    """The mixer's decay-active coefficients (a times exp(-lam dt)) and the sequential
+    recurrence, differentiable in every input."""
+    sg, th = torch.sigmoid(z), torch.tanh(s)
+    a = ((1 - sg) * th if coupled else th) * torch.exp(-lam * dt.unsqueeze(-1))
+    b = sg * hp
+    h, out = h0[:, 0], []
+    for t in range(s.shape[1]):
+        h = a[:, t] * h + b[:, t]
+        out.append(h)
+    return torch.stack(out, 1)
+
+
+DECAY_CASES = [
+    # B, T, D, coupled, per-channel rate
+    (2, 777, 136, False, True),
+    (3, 300, 70, True, False),  # a scalar rate; 70 columns: a partial 64-column tile
+    (4, 1024, 256, True, True),
+    (2, 3000, 512, False, True),  # the look-back launch
+    (1, 1, 8, False, True),
+]
+
+
+@pytest.mark.parametrize("case", DECAY_CASES)
+def test_signed_gate_scan_decay_matches_fp64(cuda, case):
+    """The decay-active fused kernel against float64 autograd: h and the gradients of
+    s, z, hpre, h0, dt and lam (dt with a saturating gap and zeros)."""
+    B, T, D, coupled, per_channel = case
+    print(f"[gpu] signed gate scan with decay case={case}", flush=True)
+    g = torch.Generator().manual_seed(41 + T + D)
+    s, z, hp = (torch.randn(B, T, D, generator=g) for _ in range(3))
+    h0 = torch.randn(B, 1, D, generator=g)
+    dt = torch.rand(B, T, generator=g) * 2
+    dt[:, T // 2] = 0.0
+    if T > 2:
+        dt[0, 1] = 60.0  # gamma underflows to zero there
+    lam = (torch.rand(D, generator=g) + 0.1) if per_channel else torch.tensor(0.8)
+    gh = torch.randn(B, T, D, generator=g)
+    ins = [t.to(cuda).requires_grad_(True) for t in (s, z, hp, h0, dt, lam)]
+    h = hip_scans.signed_gate_scan_impl(*ins[:4], coupled=coupled, dt=ins[4], lam=ins[5])
+    assert "SignedGateScanFn" in type(h.grad_fn).__name__, "HIP path did not run"
+    h.backward(gh.to(cuda))
+    torch.cuda.synchronize()
+    refs = [t.double().requires_grad_(True) for t in (s, z, hp, h0, dt, lam)]
+    hr = _ref_decay(*refs, coupled)
+    hr.backward(gh.double())
+    assert (h.detach().double().cpu() - hr.detach()).abs().max().item() <= FWD_TOL
+    for name, x, xr in zip(("ds", "dz", "dhpre", "dh0", "ddt", "dlam"), ins, refs):
+        scale = max(1.0, xr.grad.abs().max().item()) if name in ("ddt", "dlam") else 1.0
+        err = (x.grad.double().cpu() - xr.grad).abs().max().item() / scale
+        assert err <= GRAD_TOL, f"{name} max abs err {err:.3e} (scale {scale:.3g})"
+
+
+@pytest.mark.parametrize("decay", ["fixed", "learnable"])
+@pytest.mark.parametrize("coupled", [False, True])
+def test_signed_mingru_decay_module_runs_fused_and_matches_fp64(cuda, decay, coupled,
+                                                                monkeypatch):
+    """With decay the module runs the fused kernel; output, input, delta_t and parameter
+    gradients (the learnable rate's rho included) match the float64 eager module."""
+    print(f"[gpu] SignedMinGRU module decay={decay} coupled={coupled}", flush=True)
+    torch.manual_seed(11)
+    m = SignedMinGRU(24, 48, coupled=coupled, learnable_h0=True, decay=decay, decay_rate=0.6)
+    m_ref = copy.deepcopy(m).double()
+    x = torch.randn(3, 200, 24)
+    dt = torch.rand(3, 200) * 3
+    dt[1, 7] = float("nan")  # normalised to 0 by the module
+    gy = torch.randn(3, 200, 48)
     monkeypatch.setenv("MINGRU_SCAN", "hip")
-    torch.manual_seed(3)
-    m = SignedMinGRU(8, 16, decay="fixed").to(cuda)
-    x = torch.randn(2, 50, 8, device=cuda)
-    dt = torch.rand(2, 50, device=cuda)
-    y = m(x, delta_t=dt)
-    assert "SignedGateScanFn" not in type(y.grad_fn).__name__
-    assert torch.isfinite(y).all()
+    mg = m.to(cuda)
+    xg = x.to(cuda).requires_grad_(True)
+    dtg = dt.to(cuda).requires_grad_(True)
+    y = mg(xg, delta_t=dtg)
+    assert "SignedGateScanFn" in type(y.grad_fn).__name__, "fused path did not run"
+    y.backward(gy.to(cuda))
+    torch.cuda.synchronize()
+    monkeypatch.setenv("MINGRU_SCAN", "eager")
+    xr = x.double().requires_grad_(True)
+    dtr = dt.double().requires_grad_(True)
+    yr = m_ref(xr, delta_t=dtr)
+    yr.backward(gy.double())
+    assert (y.detach().double().cpu() - yr.detach()).abs().max().item() <= FWD_TOL
+    assert (xg.grad.double().cpu() - xr.grad).abs().max().item() <= GRAD_TOL
+    sc = max(1.0, dtr.grad.abs().max().item())
+    assert (dtg.grad.double().cpu() - dtr.grad).abs().max().item() / sc <= GRAD_TOL
+    for (name, p), (_, pr) in zip(mg.named_parameters(), m_ref.named_parameters()):
+        sc = max(1.0, pr.grad.abs().max().item())
+        err = (p.grad.double().cpu() - pr.grad).abs().max().item() / sc
+        assert err <= GRAD_TOL, f"{name} grad max abs err {err:.3e} (scale {sc:.3g})"
 
 
 @pytest.mark.parametrize("case", [(2, 777, 136, False), (4, 1024, 256, True), (2, 1024, 64, False)])
