@@ -116,6 +116,16 @@ def build_ops(torch, wl):
     ops["C2g"] = Op("C2g", "C2g SignedMinGRU fused gates + linear_scan fwd+bwd (C2 shape)",
                     c["B"] * c["T"], "mg_signed_gate_scan_fwd", "mg_signed_gate_scan_bwd",
                     4 * N * 4, 7 * N * 4)
+    # C2gd: C2g with time decay, a = exp(-lam dt) tanh(s) formed in the kernel; dt (B,T)
+    # and lam (D) add B*T + D floats, and the backward writes dL/dlam and dL/ddt partial
+    # rows (B*chunks*D + ceil(D/64)*B*T floats).
+    c = wl.C2
+    bt = c["B"] * c["T"]
+    part = (c["B"] * -(-c["T"] // 32) * c["D"] + -(-c["D"] // 64) * bt) * 4
+    ops["C2gd"] = Op("C2gd", "C2gd SignedMinGRU fused gates with time decay + linear_scan "
+                     "fwd+bwd (C2 shape)", bt, "mg_signed_gate_scan_decay_fwd",
+                     "mg_signed_gate_scan_decay_bwd", 4 * N * 4 + (bt + c["D"]) * 4,
+                     7 * N * 4 + (bt + c["D"]) * 4 + part)
     # C1: parallel_scan_log
     c = wl.C1
     N = c["B"] * c["T"] * c["D"]
@@ -141,6 +151,18 @@ def build_ops(torch, wl):
     ops["C4"] = Op("C4", "C4 GivensMinGRU angle-fused (28 lexicographic rotations) fwd+bwd",
                    c["B"] * c["T"], "mg_angle_scan_fwd", "mg_angle_scan_bwd",
                    180 * L + h0b, 328 * L + 2 * h0b)
+    # C4g: GivensMinGRU's brick-wall scan (k=8, 3 rounds) at the C4 shape with the heads
+    # b = sigmoid(z) * hpre formed in the kernel and decay.  Per block-token: forward reads
+    # theta (12 floats), gamma, z, hpre (8 each) and writes h; backward reads theta, gamma,
+    # z, hpre, h, dL/dh and writes dtheta, dgamma, dz, dhpre.
+    c = wl.C4
+    L = c["B"] * c["T"] * c["n"]
+    h0b = c["B"] * c["n"] * c["k"] * 4
+    ops["C4g"] = Op("C4g", "C4g GivensMinGRU brick-wall (k=8, 3 rounds) with the gated heads "
+                    "in the kernel, decay, fwd+bwd (C4 shape)", c["B"] * c["T"],
+                    "mg_angle_scan_gated_fwd", "mg_angle_scan_gated_bwd",
+                    (12 + 1 + 8 + 8 + 8) * 4 * L + h0b, (12 + 1 + 8 + 8 + 8 + 8 + 12 + 1 + 8 + 8)
+                    * 4 * L + 2 * h0b)
     # C5: DeltaMinGRU chunked-WY, bf16 inputs.  FLOP floor: per (b, h) and chunk of
     # C tokens, six C x C x d products and one triangular solve (C^3), i.e.
     # 6 * 2 C^3 + C^3 = 13 C^3 at C = d = 64; the backward is counted as 2x the
@@ -197,6 +219,35 @@ def make_step(key, torch, wl, dev):
             return torch.autograd.grad(h, xs, gh)
 
         return step, None, wl.C2["B"]
+    if key == "C2gd":
+        from mingru_amd.min_gru import _dispatch_signed_gate_scan
+
+        inp = wl.c2gd_inputs(**wl.C2)
+        xs = [inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre")]
+        h0 = inp["h0"].to(dev)
+        dt, lam = inp["dt"].to(dev), inp["lam"].to(dev).requires_grad_(True)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = _dispatch_signed_gate_scan(*xs, h0, coupled=False, dt=dt, lam=lam)
+            return torch.autograd.grad(h, xs + [lam], gh)
+
+        return step, None, wl.C2["B"]
+    if key == "C4g":
+        from mingru_amd import hip_scans
+
+        inp = wl.c4g_inputs(**wl.C4)
+        th, gm, z, hp, h0 = (inp[k].to(dev).requires_grad_(True)
+                             for k in ("theta", "gamma", "z", "hpre", "h0"))
+        meta = [t.to(dev) for t in hip_scans._brick_tables(wl.C4["k"], 3)]
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            h = hip_scans.angle_gated_scan_impl(th, None, gm, z, hp, h0, *meta, has_scale=0,
+                                                has_decay=1)
+            return torch.autograd.grad(h, (th, gm, z, hp, h0), gh)
+
+        return step, None, wl.C4["B"]
     if key == "C1g":
         from mingru_amd.min_gru import _dispatch_mingru_gate_scan
 
@@ -330,8 +381,10 @@ def make_step(key, torch, wl, dev):
 def gate_unfused_gpu_ms(key, torch, wl, dev, steps):
     """The unfused mixer path that a fused gate op replaces, fwd+bwd, ms per step over
     `steps` steps.  C2g: SignedMinGRU's eager gates on the GPU, the HIP linear_scan,
-    then h = A * h0 + Bc.  C1g: MinGRU's eager log-space gates, the concatenation
-    with log h0 and the HIP parallel_scan_log."""
+    then h = A * h0 + Bc; C2gd the same with the decay exp(-lam dt) applied eagerly.
+    C1g: MinGRU's eager log-space gates, the concatenation with log h0 and the HIP
+    parallel_scan_log.  C4g: GivensMinGRU's eager b = sigmoid(z) * hpre and the HIP
+    angle scan."""
     import torch.nn.functional as F
 
     import mingru_amd as mg
@@ -347,6 +400,31 @@ def gate_unfused_gpu_ms(key, torch, wl, dev, steps):
             sg = torch.sigmoid(z)
             A, Bc = mg.linear_scan(torch.tanh(s), sg * hp)
             torch.autograd.grad(A * h0 + Bc, (s, z, hp), gh)
+    elif key == "C2gd":
+        inp = wl.c2gd_inputs(**wl.C2)
+        s, z, hp = (inp[k].to(dev).requires_grad_(True) for k in ("s", "z", "hpre"))
+        h0 = inp["h0"].to(dev)
+        dt, lam = inp["dt"].to(dev), inp["lam"].to(dev).requires_grad_(True)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            a = torch.exp(-lam * dt.unsqueeze(-1)) * torch.tanh(s)
+            A, Bc = mg.linear_scan(a, torch.sigmoid(z) * hp)
+            torch.autograd.grad(A * h0 + Bc, (s, z, hp, lam), gh)
+    elif key == "C4g":
+        from mingru_amd import hip_scans
+
+        inp = wl.c4g_inputs(**wl.C4)
+        th, gm, z, hp, h0 = (inp[k].to(dev).requires_grad_(True)
+                             for k in ("theta", "gamma", "z", "hpre", "h0"))
+        meta = [t.to(dev) for t in hip_scans._brick_tables(wl.C4["k"], 3)]
+        ones = torch.ones(gm.shape, device=dev)
+        gh = inp["grad_h"].to(dev)
+
+        def step():
+            b = torch.sigmoid(z) * hp
+            h = hip_scans.angle_scan_impl(th, ones, gm, b, h0, *meta, has_scale=0, has_decay=1)
+            torch.autograd.grad(h, (th, gm, z, hp, h0), gh)
     else:
         inp = wl.c1g_inputs(**wl.C1)
         k, hp = (inp[n].to(dev).requires_grad_(True) for n in ("k", "hpre"))
@@ -691,7 +769,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C2g", "C1", "C1g", "C3", "C3m", "C4", "C5", "C5d"]
+    order = ["C2", "C2g", "C2gd", "C1", "C1g", "C3", "C3m", "C4", "C4g", "C5", "C5d"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -717,11 +795,12 @@ def main():
         if "graph_ms_per_step" in res:
             print(f"#   replayed from a HIP graph: {res['graph_ms_per_step']:.3f} ms/step, "
                   f"{res['graph_tokens_per_s']:.4g} tok/s", file=sys.stderr, flush=True)
-        if key in ("C2g", "C1g") and not args.no_eager:
+        if key in ("C2g", "C2gd", "C1g", "C4g") and not args.no_eager:
             uf = gate_unfused_gpu_ms(key, torch, wl, dev, args.steps)
             res["unfused_ms_per_step"] = uf
             res["speedup_vs_unfused"] = uf / res["ms_per_step"]
-            scan = "linear_scan + A*h0+Bc" if key == "C2g" else "parallel_scan_log"
+            scan = {"C2g": "linear_scan + A*h0+Bc", "C2gd": "linear_scan + A*h0+Bc",
+                    "C1g": "parallel_scan_log", "C4g": "angle scan"}[key]
             print(f"#   unfused (eager gates + HIP {scan}): {uf:.3f} ms/step "
                   f"({res['speedup_vs_unfused']:.2f}x the fused time)", file=sys.stderr,
                   flush=True)
@@ -788,8 +867,9 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator, BASELINE.json workload shapes)",
         "config": {"workload": op.workload, **{"C1": wl.C1, "C1g": wl.C1, "C2": wl.C2, "C2g": wl.C2,
-                                               "C3": wl.C3, "C3m": wl.C3, "C4": wl.C4,
-                                               "C5": wl.C5, "C5d": wl.C5}.get(head_key, {})},
+                                               "C2gd": wl.C2, "C3": wl.C3, "C3m": wl.C3,
+                                               "C4": wl.C4, "C4g": wl.C4, "C5": wl.C5,
+                                               "C5d": wl.C5}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "achieved_TBs": head["achieved_TBs"],

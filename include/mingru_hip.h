@@ -216,6 +216,26 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
                       int64_t n, int k, int sched, int rounds, int flags, void* ws,
                       size_t ws_bytes, mg_stream_t stream);
 
+/* ---- angle-fused scan with the mixers' gated prologue (brick-wall schedules) --------
+ * No reference kernel fuses these: the same scan as mg_angle_scan_fwd/bwd with
+ * sched 0 (brick-wall rounds, k in {2,4,8}), but with the heads of RotationMinGRU /
+ * GivensMinGRU formed inside the kernel instead of by eager ops
+ * (src/mingru/min_gru.py:2261-2262, 2719): b = sigmoid(z) * hpre from z, hpre
+ * (B,T,n,k), and, when flags bit 0 is set, the scale tanh(u) from u (B,T,n).  The
+ * backward writes dz, dhpre in place of db and du in place of dscale.  flags: bit 0
+ * scale, bit 1 decay (gamma (B,T,n) as in mg_angle_scan_fwd).  State and workspace
+ * sizes as mg_angle_scan_state_bytes / mg_angle_scan_workspace_bytes. */
+int mg_angle_scan_gated_fwd(const float* theta, const float* u, const float* gamma,
+                            const float* z, const float* hpre, const float* h0, float* h,
+                            float* chunk_prod, int64_t B, int64_t T, int64_t n, int k, int rounds,
+                            int flags, void* ws, size_t ws_bytes, mg_stream_t stream);
+int mg_angle_scan_gated_bwd(const float* theta, const float* u, const float* gamma,
+                            const float* z, const float* hpre, const float* h0, const float* h,
+                            const float* chunk_prod, const float* gh, float* dtheta, float* du,
+                            float* dgamma, float* dz, float* dhpre, float* dh0, int64_t B,
+                            int64_t T, int64_t n, int k, int rounds, int flags, void* ws,
+                            size_t ws_bytes, mg_stream_t stream);
+
 /* ---- angle-fused scan driven by run-time plane tables -------------------------
  * Replaces the same reference kernels as mg_angle_scan_fwd/bwd
  * (src/mingru/triton_scans.py:1039-1291, angle_scan_impl :1743-1812), taking

@@ -65,6 +65,10 @@ _SIGNATURES = {
     "mg_angle_scan_bwd": (
         _I32, [_P] * 12 + [_I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     ),
+    "mg_angle_scan_gated_fwd": (_I32, [_P] * 8 + [_I64, _I64, _I64, _I32, _I32, _I32, _P, _SZ, _P]),
+    "mg_angle_scan_gated_bwd": (
+        _I32, [_P] * 15 + [_I64, _I64, _I64, _I32, _I32, _I32, _P, _SZ, _P],
+    ),
     "mg_angle_scan_tables_state_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
     "mg_angle_scan_tables_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
     "mg_angle_scan_tables_fwd": (

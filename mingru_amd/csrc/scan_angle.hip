@@ -40,6 +40,7 @@
 // reverse time.  Its chunk maps are y -> P_c^T y + Lb_c: the linear part is
 // the saved forward product transposed, so pass 1 only sweeps one column.
 #include "mg_affm.h"
+#include "mg_gates.h"
 #include "mg_sincos.h"
 
 #include <algorithm>
@@ -50,6 +51,8 @@ namespace {
 using namespace mg;
 
 enum : int { SCHED_BRICK = 0, SCHED_LEX = 1 };
+// flags: bit 0 scale, bit 1 decay, bit 2 the gated prologue (mg_angle_scan_gated_*).
+constexpr int AN_FLAG_GATED = 4;
 
 // Reduce-then-scan over chunks of AN_CHUNK tokens: pass 1 builds every chunk's
 // affine map in parallel (one lane per (block, chunk)), pass 2 walks the chunk
@@ -328,9 +331,57 @@ struct AnArgs {
   // the chunk products) and group offsets [group][block][K] of the pass's direction.
   float* gprod;
   float* gsum;
+  // Gated prologue (GP, brick-wall kernels): `b` holds z and `hpre` the candidate, so
+  // b_t = sigmoid(z) hpre; `scale` holds u, so the scale is tanh(u).  The backward
+  // then writes dL/dz to `out`, dL/dhpre to `dhpre` and dL/du to `dscale`.
+  const float* hpre;
+  float* dhpre;
   int rounds;
   int na;  // angles per token
 };
+
+// The per-token scale and input of the brick-wall kernels, plain or through the gated
+// prologue (the RotationMinGRU / GivensMinGRU heads, reference src/mingru/min_gru.py:
+// 2261-2262, 2719: scale = tanh(linear_u x), b = sigmoid(linear_z x) * linear_h x).
+template <bool GP>
+__device__ __forceinline__ float an_scale(const AnArgs& a, int64_t lane_tok) {
+  return GP ? mg_tanh(a.scale[lane_tok]) : a.scale[lane_tok];
+}
+
+template <int K, bool GP>
+__device__ __forceinline__ void an_input(const AnArgs& a, int64_t lane_tok, float (&bt)[K]) {
+  if constexpr (GP) {
+    float zz[K], hp[K];
+    ld<K>(zz, a.b + lane_tok * K);
+    ld<K>(hp, a.hpre + lane_tok * K);
+#pragma unroll
+    for (int i = 0; i < K; ++i) bt[i] = mg_sigmoid(zz[i]) * hp[i];
+  } else {
+    ld<K>(bt, a.b + lane_tok * K);
+  }
+}
+
+// db_t = dL/dh_t (the token's adjoint) stored, or through the gated prologue dL/dz
+// and dL/dhpre.
+template <int K, bool GP>
+__device__ __forceinline__ void an_store_db(const AnArgs& a, int64_t lane_tok,
+                                            const float (&gt)[K]) {
+  if constexpr (GP) {
+    float zz[K], hp[K], dz[K], dh[K];
+    ld<K>(zz, a.b + lane_tok * K);
+    ld<K>(hp, a.hpre + lane_tok * K);
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float sg = mg_sigmoid(zz[i]);
+      dh[i] = gt[i] * sg;
+      dz[i] = dh[i] * hp[i] * (1.f - sg);
+    }
+    st<K>(a.out + lane_tok * K, dz);
+    st<K>(a.dhpre + lane_tok * K, dh);
+  } else {
+    st<K>(a.out + lane_tok * K, gt);
+  }
+}
 
 // Per-token inputs of the lexicographic kernels, loaded one token ahead: at one
 // wave per SIMD nothing else hides a load issued only when it is needed.
@@ -501,7 +552,7 @@ __device__ __forceinline__ void wave_rows_store(float* __restrict__ dst0, const 
 // its group maps h -> Pg h + Lg over chunks c0 .. c1: thread (j < K, b) carries
 // column j of block b's Pg (and, redundantly, its Lg) through the group's chunk
 // maps read back from LDS.
-template <int K, int SCHED, bool HS, bool HD>
+template <int K, int SCHED, bool HS, bool HD, bool GP = false>
 __global__ __launch_bounds__(AN_RED_THREADS) void angle_fwd_reduce(AnArgs a, AnGeom g) {
   static_assert(K % 2 == 0, "the pair compose splits the columns of P in two");
   mg_sincos_setup();
@@ -538,12 +589,12 @@ __global__ __launch_bounds__(AN_RED_THREADS) void angle_fwd_reduce(AnArgs a, AnG
       } else {
         for (int64_t t = t0; t < te; ++t) {
           const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-          const float d = HS ? a.scale[lane_tok] : 1.f;
+          const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
           const float gm = HD ? a.gamma[lane_tok] : 1.f;
           apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
           if (HD) gprod *= gm;
           float bt[K];
-          ld<K>(bt, a.b + lane_tok * K);
+          an_input<K, GP>(a, lane_tok, bt);
 #pragma unroll
           for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
         }
@@ -774,7 +825,7 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_fwd_scan(AnArgs a, AnGe
 }
 
 // ---- forward pass 3: every token's state from its chunk-entry state ------------
-template <int K, int SCHED, bool HS, bool HD>
+template <int K, int SCHED, bool HS, bool HD, bool GP = false>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, AnGeom g) {
   mg_sincos_setup();
   const AnThread th = an_thread(g);
@@ -809,11 +860,11 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, A
   } else {
     for (int64_t t = t0; t < te; ++t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? a.scale[lane_tok] : 1.f;
+      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       apply_M<K, SCHED, HS, HD, 1>(v, a.theta + lane_tok * a.na, a.rounds, d, gm);
       float bt[K];
-      ld<K>(bt, a.b + lane_tok * K);
+      an_input<K, GP>(a, lane_tok, bt);
 #pragma unroll
       for (int i = 0; i < K; ++i) {
         v[i][0] += bt[i];
@@ -948,7 +999,7 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
 // with y_in the adjoint flowing in from the right, P_c the forward chunk
 // product (saved by the forward) and Lb_c this pass's zero-start reverse sweep
 // x <- M_t^T (x + g_t).
-template <int K, int SCHED, bool HS, bool HD>
+template <int K, int SCHED, bool HS, bool HD, bool GP = false>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, AnGeom g) {
   mg_sincos_setup();
   const AnThread th = an_thread(g);
@@ -973,7 +1024,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, 
   } else {
     for (int64_t t = te - 1; t >= t0; --t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? a.scale[lane_tok] : 1.f;
+      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       float gt[K];
       ld<K>(gt, a.gh + lane_tok * K);
@@ -1245,7 +1296,7 @@ __global__ __launch_bounds__(AN_WALK_THREADS) void angle_group_walk_fill(AnArgs 
 }
 
 // ---- backward pass 3: every token's gradients from its chunk-entry adjoint ------
-template <int K, int SCHED, bool HS, bool HD>
+template <int K, int SCHED, bool HS, bool HD, bool GP = false>
 __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, AnGeom g) {
   mg_sincos_setup();
   const AnThread th = an_thread(g);
@@ -1297,7 +1348,7 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, A
   } else {
     for (int64_t t = te - 1; t >= t0; --t) {
       const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? a.scale[lane_tok] : 1.f;
+      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
       const float gm = HD ? a.gamma[lane_tok] : 1.f;
       float gt[K], hp[K];
       ld<K>(gt, a.gh + lane_tok * K);
@@ -1308,11 +1359,11 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, A
         y[i][0] += gt[i];
         gt[i] = y[i][0];
       }
-      st<K>(a.out + lane_tok * K, gt);  // db_t = dL/dh_t
+      an_store_db<K, GP>(a, lane_tok, gt);  // db_t = dL/dh_t (or dz, dhpre)
       float dd = 0.f, dg = 0.f;
       token_grad<K, SCHED, HS, HD>(y, hp, a.theta + lane_tok * a.na, a.dtheta + lane_tok * a.na,
                                    a.rounds, d, gm, dd, dg);
-      if (HS) a.dscale[lane_tok] = dd;
+      if (HS) a.dscale[lane_tok] = GP ? dd * (1.f - d * d) : dd;  // GP: dL/du, d = tanh(u)
       if (HD) a.dgamma[lane_tok] = dg;
     }
   }
@@ -1356,7 +1407,7 @@ size_t an_state_bytes(int64_t B, int64_t T, int64_t n, int k) {
   return (size_t)maps * k * k * g.NB * sizeof(float);
 }
 
-template <int K, int SCHED, bool HS, bool HD, bool BWD>
+template <int K, int SCHED, bool HS, bool HD, bool BWD, bool GP = false>
 int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_bytes,
               hipStream_t stream) {
   const AnGeom g = an_geom(B, T, n);
@@ -1404,14 +1455,14 @@ int an_launch(AnArgs a, int64_t B, int64_t T, int64_t n, void* ws, size_t ws_byt
                        (const float*)gb, ng);
   };
   if (BWD) {
-    hipLaunchKernelGGL((angle_bwd_reduce<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_bwd_reduce<K, SCHED, HS, HD, GP>), grid, block, 0, stream, a, g);
     walk();
-    hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_bwd_final<K, SCHED, HS, HD, GP>), grid, block, 0, stream, a, g);
   } else {
-    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD>), rgrid, dim3(AN_RED_THREADS), 0, stream,
+    hipLaunchKernelGGL((angle_fwd_reduce<K, SCHED, HS, HD, GP>), rgrid, dim3(AN_RED_THREADS), 0, stream,
                        a, g);
     walk();
-    hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD>), grid, block, 0, stream, a, g);
+    hipLaunchKernelGGL((angle_fwd_final<K, SCHED, HS, HD, GP>), grid, block, 0, stream, a, g);
   }
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
@@ -1420,6 +1471,25 @@ template <bool BWD>
 int an_dispatch(const AnArgs& a, int64_t B, int64_t T, int64_t n, int k, int sched, int flags,
                 void* ws, size_t ws_bytes, hipStream_t stream) {
   const bool hs = flags & 1, hd = flags & 2;
+  if (flags & AN_FLAG_GATED) {  // the gated prologue: brick-wall schedules only
+#define MG_AN_GCASE(KK)                                                                         \
+  if (k == KK && sched == SCHED_BRICK) {                                                        \
+    if (hs && hd)                                                                               \
+      return an_launch<KK, SCHED_BRICK, true, true, BWD, true>(a, B, T, n, ws, ws_bytes, stream); \
+    if (hs)                                                                                     \
+      return an_launch<KK, SCHED_BRICK, true, false, BWD, true>(a, B, T, n, ws, ws_bytes,        \
+                                                                stream);                        \
+    if (hd)                                                                                     \
+      return an_launch<KK, SCHED_BRICK, false, true, BWD, true>(a, B, T, n, ws, ws_bytes,        \
+                                                                stream);                        \
+    return an_launch<KK, SCHED_BRICK, false, false, BWD, true>(a, B, T, n, ws, ws_bytes, stream); \
+  }
+    MG_AN_GCASE(2)
+    MG_AN_GCASE(4)
+    MG_AN_GCASE(8)
+#undef MG_AN_GCASE
+    return MG_ERR_ARG;
+  }
 #define MG_AN_CASE(KK, SS)                                                                     \
   if (k == KK && sched == SS) {                                                                \
     if (hs && hd) return an_launch<KK, SS, true, true, BWD>(a, B, T, n, ws, ws_bytes, stream);   \
@@ -1471,7 +1541,7 @@ int mg_angle_scan_fwd(const float* theta, const float* scale, const float* gamma
                       const float* h0, float* h, float* chunk_prod, int64_t B, int64_t T,
                       int64_t n, int k, int sched, int rounds, int flags, void* ws,
                       size_t ws_bytes, hipStream_t stream) {
-  if (!theta || !b || !h0 || !h || !chunk_prod || !ws ||
+  if (!theta || !b || !h0 || !h || !chunk_prod || !ws || (flags & ~3) ||
       !an_args_ok(B, T, n, k, sched, rounds) || !an_geometry_ok(B, T, n))
     return MG_ERR_ARG;
   if (((flags & 1) && !scale) || ((flags & 2) && !gamma)) return MG_ERR_ARG;
@@ -1495,7 +1565,7 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
                       int64_t n, int k, int sched, int rounds, int flags, void* ws,
                       size_t ws_bytes, hipStream_t stream) {
   if (!theta || !h0 || !h || !chunk_prod || !gh || !dtheta || !db || !dh0 || !ws ||
-      !an_args_ok(B, T, n, k, sched, rounds) || !an_geometry_ok(B, T, n))
+      (flags & ~3) || !an_args_ok(B, T, n, k, sched, rounds) || !an_geometry_ok(B, T, n))
     return MG_ERR_ARG;
   if (((flags & 1) && (!scale || !dscale)) || ((flags & 2) && (!gamma || !dgamma)))
     return MG_ERR_ARG;
@@ -1518,6 +1588,68 @@ int mg_angle_scan_bwd(const float* theta, const float* scale, const float* gamma
   a.rounds = rounds;
   a.na = sched == SCHED_LEX ? k * (k - 1) / 2 : rounds * (k / 2);
   return an_dispatch<true>(a, B, T, n, k, sched, flags, ws, ws_bytes, stream);
+}
+
+int mg_angle_scan_gated_fwd(const float* theta, const float* u, const float* gamma,
+                            const float* z, const float* hpre, const float* h0, float* h,
+                            float* chunk_prod, int64_t B, int64_t T, int64_t n, int k, int rounds,
+                            int flags, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (!theta || !z || !hpre || !h0 || !h || !chunk_prod || !ws || (flags & ~3) ||
+      !an_args_ok(B, T, n, k, SCHED_BRICK, rounds) || !an_geometry_ok(B, T, n))
+    return MG_ERR_ARG;
+  if (((flags & 1) && !u) || ((flags & 2) && !gamma)) return MG_ERR_ARG;
+  if (!aligned16(theta) || !aligned16(z) || !aligned16(hpre) || !aligned16(h0) || !aligned16(h))
+    return MG_ERR_ARG;
+  AnArgs a{};
+  a.theta = theta;
+  a.scale = u;
+  a.gamma = gamma;
+  a.b = z;
+  a.hpre = hpre;
+  a.h0 = h0;
+  a.out = h;
+  a.prod = chunk_prod;
+  a.rounds = rounds;
+  a.na = rounds * (k / 2);
+  return an_dispatch<false>(a, B, T, n, k, SCHED_BRICK, flags | AN_FLAG_GATED, ws, ws_bytes,
+                            stream);
+}
+
+int mg_angle_scan_gated_bwd(const float* theta, const float* u, const float* gamma,
+                            const float* z, const float* hpre, const float* h0, const float* h,
+                            const float* chunk_prod, const float* gh, float* dtheta, float* du,
+                            float* dgamma, float* dz, float* dhpre, float* dh0, int64_t B,
+                            int64_t T, int64_t n, int k, int rounds, int flags, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
+  if (!theta || !z || !hpre || !h0 || !h || !chunk_prod || !gh || !dtheta || !dz || !dhpre ||
+      !dh0 || !ws || (flags & ~3) || !an_args_ok(B, T, n, k, SCHED_BRICK, rounds) ||
+      !an_geometry_ok(B, T, n))
+    return MG_ERR_ARG;
+  if (((flags & 1) && (!u || !du)) || ((flags & 2) && (!gamma || !dgamma))) return MG_ERR_ARG;
+  if (!aligned16(theta) || !aligned16(z) || !aligned16(hpre) || !aligned16(h0) ||
+      !aligned16(h) || !aligned16(gh) || !aligned16(dtheta) || !aligned16(dz) ||
+      !aligned16(dhpre) || !aligned16(dh0))
+    return MG_ERR_ARG;
+  AnArgs a{};
+  a.theta = theta;
+  a.scale = u;
+  a.gamma = gamma;
+  a.b = z;
+  a.hpre = hpre;
+  a.h0 = h0;
+  a.h = h;
+  a.gh = gh;
+  a.out = dz;
+  a.dhpre = dhpre;
+  a.dtheta = dtheta;
+  a.dscale = du;
+  a.dgamma = dgamma;
+  a.dh0 = dh0;
+  a.prod = const_cast<float*>(chunk_prod);
+  a.rounds = rounds;
+  a.na = rounds * (k / 2);
+  return an_dispatch<true>(a, B, T, n, k, SCHED_BRICK, flags | AN_FLAG_GATED, ws, ws_bytes,
+                           stream);
 }
 
 }  // extern "C"

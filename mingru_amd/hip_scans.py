@@ -1013,6 +1013,98 @@ def angle_scan_impl(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale: in
                    flags)
 
 
+class _AngleGatedFn(torch.autograd.Function):
+    """The brick-wall angle scan with the mixers' heads formed in the kernel: b =
+    sigmoid(z) * hpre and, with a scale, tanh(u)."""
+
+    @staticmethod
+    def forward(ctx, theta, u, gamma, z, hpre, h0, rounds, flags):
+        out_dtype = z.dtype
+        th, z32, hp32, h032 = _as_f32(theta, z, hpre, h0)
+        u32 = _as_f32(u)[0] if u is not None else None
+        gm = _as_f32(gamma)[0] if gamma is not None else None
+        Bn, T, n, k = z32.shape
+        h = torch.empty_like(z32)
+        prod = torch.empty(max(_size("mg_angle_scan_state_bytes", Bn, T, n, k), 16) // 4,
+                           dtype=torch.float32, device=z32.device)
+        ws = _workspace(_size("mg_angle_scan_workspace_bytes", Bn, T, n, k), z32.device)
+        _call("mg_angle_scan_gated_fwd", _ptr(th), _ptr(u32), _ptr(gm), _ptr(z32), _ptr(hp32),
+              _ptr(h032), _ptr(h), _ptr(prod), Bn, T, n, k, rounds, flags, _ptr(ws), ws.numel(),
+              _stream(z32))
+        ctx.save_for_backward(th, u32, gm, z32, hp32, h032, h, prod)
+        ctx.meta = (rounds, flags, out_dtype, theta.dtype,
+                    None if u is None else u.dtype, None if gamma is None else gamma.dtype,
+                    hpre.dtype, h0.dtype)
+        return h if out_dtype == torch.float32 else h.to(out_dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gh):
+        th, u32, gm, z32, hp32, h032, h, prod = ctx.saved_tensors
+        rounds, flags, out_dtype, tdt, udt, gdt, hdt, h0dt = ctx.meta
+        Bn, T, n, k = h.shape
+        (gh32,) = _as_f32(gh)
+        dth = torch.empty_like(th)
+        du = torch.empty_like(u32) if u32 is not None else None
+        dgm = torch.empty_like(gm) if gm is not None else None
+        dz, dhp = torch.empty_like(z32), torch.empty_like(hp32)
+        dh0 = torch.empty_like(h032)
+        ws = _workspace(_size("mg_angle_scan_workspace_bytes", Bn, T, n, k), h.device)
+        _call("mg_angle_scan_gated_bwd", _ptr(th), _ptr(u32), _ptr(gm), _ptr(z32), _ptr(hp32),
+              _ptr(h032), _ptr(h), _ptr(prod), _ptr(gh32), _ptr(dth), _ptr(du), _ptr(dgm),
+              _ptr(dz), _ptr(dhp), _ptr(dh0), Bn, T, n, k, rounds, flags, _ptr(ws), ws.numel(),
+              _stream(h))
+        return (dth.to(tdt), None if du is None else du.to(udt),
+                None if dgm is None else dgm.to(gdt), dz.to(out_dtype), dhp.to(hdt),
+                dh0.to(h0dt), None, None)
+
+
+def angle_gated_scan_impl(theta, u, gamma, z, hpre, h0, perm, sgn, p2p, *, has_scale: int,
+                          has_decay: int):
+    """The angle-fused scan with RotationMinGRU's / GivensMinGRU's heads formed in the
+    kernel; returns ``h`` ``(B, T, n, k)``.
+
+    No reference kernel fuses the heads: the reference computes ``scale =
+    tanh(linear_u x)`` and ``b = sigmoid(linear_z x) * linear_h x`` eagerly
+    (``src/mingru/min_gru.py:2261-2262, 2719``) and hands them to the angle scan.
+    Here ``u`` ``(B, T, n)`` (used when ``has_scale``), ``z`` and ``hpre``
+    ``(B, T, n, k)`` go to the kernel instead; ``theta``, ``gamma`` (when
+    ``has_decay``), ``h0`` and the plane tables as for ``angle_scan_impl``.  Only
+    the compiled brick-wall schedules (k in {2, 4, 8}) take this form; anything
+    else raises ``ScanFallback`` and the caller runs the heads eagerly.
+    """
+    if theta.ndim != 5 or z.ndim != 4:
+        raise ScanFallback("gated angle scan: need 5-D theta and 4-D z")
+    Bn, T, n, R, half = theta.shape
+    k = z.shape[-1]
+    if (
+        k not in _ANGLE_K
+        or R > _ANGLE_MAX_ROT
+        or tuple(z.shape[:3]) != (Bn, T, n)
+        or hpre.shape != z.shape
+        or tuple(h0.shape) != (Bn, n, k)
+        or (has_scale and (u is None or tuple(u.shape) != (Bn, T, n)))
+        or (has_decay and (gamma is None or tuple(gamma.shape) != (Bn, T, n)))
+        or tuple(perm.shape) != (R, k)
+    ):
+        raise ScanFallback(
+            f"gated angle scan (theta={tuple(theta.shape)}, z={tuple(z.shape)}, "
+            f"hpre={tuple(hpre.shape)}, h0={tuple(h0.shape)}) outside the envelope: need "
+            f"k in {sorted(_ANGLE_K)}, at most {_ANGLE_MAX_ROT} rounds and shapes agreeing on "
+            "(B, T, n, R, k)"
+        )
+    sched, rounds = _classify_schedule(perm, sgn, p2p, k, R, half)
+    if sched != 0:
+        raise ScanFallback("gated angle scan: only the brick-wall schedule takes the fused heads")
+    _same_device(theta, z, hpre, h0, *[t for t in (u, gamma) if t is not None])
+    flags = (1 if has_scale else 0) | (2 if has_decay else 0)
+    if T == 0:
+        return z.new_empty(z.shape)
+    return _funnel("angle-fused (gated heads)", _AngleGatedFn.apply, theta,
+                   u if has_scale else None, gamma if has_decay else None, z, hpre, h0, rounds,
+                   flags)
+
+
 # ---------------------------------------------------------------------------
 # DeltaMinGRU chunked-WY
 # ---------------------------------------------------------------------------

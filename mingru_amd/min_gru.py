@@ -220,6 +220,33 @@ def _dispatch_angle_scan(
     return None
 
 
+def _dispatch_angle_gated_scan(theta, u, gamma, z, hpre, h0, perm, sgn, p2p, *, has_scale: int,
+                               has_decay: int):
+    """Run the angle-fused scan with the mixer's heads (``b = sigmoid(z) * hpre``,
+    ``scale = tanh(u)``) formed in the kernel, or return ``None``.
+
+    No reference counterpart: the reference forms the heads eagerly
+    (``src/mingru/min_gru.py:2261-2262, 2719``) and calls ``_dispatch_angle_scan``
+    (``:353-439``), which is what ``None`` leads to.  Any decline (a schedule the
+    fused heads do not cover, a missing backend) returns ``None`` silently in every
+    mode: the caller's ``_dispatch_angle_scan`` then applies the mode's rules.
+    """
+    mode = _resolve_scan_mode(theta.is_cuda)
+    if mode is None:
+        return None
+    try:
+        from mingru_amd import hip_scans as backend
+    except ImportError:
+        return None
+    if not hasattr(backend, "angle_gated_scan_impl") or backend.available() is not True:
+        return None
+    try:
+        return backend.angle_gated_scan_impl(theta, u, gamma, z, hpre, h0, perm, sgn, p2p,
+                                             has_scale=has_scale, has_decay=has_decay)
+    except backend.ScanFallback:
+        return None
+
+
 def _dispatch_signed_gate_scan(
     s: torch.Tensor, z: torch.Tensor, hpre: torch.Tensor, h0: torch.Tensor, *, coupled: bool,
     dt: torch.Tensor | None = None, lam: torch.Tensor | None = None,
@@ -995,8 +1022,19 @@ class RotationMinGRU(DecayMixin, nn.Module):
         if not _angle_scan_should_try(x.is_cuda):
             return None
         B, T, _ = x.shape
-        theta, scale, gamma, b = self._angle_heads(x, dt)
+        n = self.n_blocks
         perm, sgn, p2p = self._angle_plane_meta(x.device)
+        # The heads' nonlinearities in the kernel: angle (snapped here), tanh(u) scale,
+        # sigmoid(z) * h~ input.
+        gamma = self._decay_gamma(dt).expand(B, T, n) if dt is not None else None
+        h = _dispatch_angle_gated_scan(
+            self._angle(x).view(B, T, n, 1, 1), self.linear_u(x), gamma,
+            self.linear_z(x).view(B, T, n, 2), self.linear_h(x).view(B, T, n, 2), h0_blocks,
+            perm, sgn, p2p, has_scale=1, has_decay=1 if dt is not None else 0,
+        )
+        if h is not None:
+            return h.reshape(B, T, self.hidden_size)
+        theta, scale, gamma, b = self._angle_heads(x, dt)
         h = _dispatch_angle_scan(
             theta, scale, gamma, b, h0_blocks, perm, sgn, p2p,
             has_scale=1, has_decay=1 if dt is not None else 0,
@@ -1144,8 +1182,18 @@ class GivensMinGRU(DecayMixin, nn.Module):
         if not _angle_scan_should_try(x.is_cuda):
             return None
         B, T, _ = x.shape
-        theta, scale, gamma, b = self._angle_heads(x, dt)
+        n, k, R = self.n_blocks, self.k, self.rounds
         perm, sgn, p2p = self._angle_plane_meta(x.device)
+        # The sigmoid(z) * h~ input formed in the kernel (brick-wall k <= 8).
+        gamma = self._decay_gamma(dt).expand(B, T, n) if dt is not None else None
+        h = _dispatch_angle_gated_scan(
+            self.linear_theta(x).view(B, T, n, R, k // 2), None, gamma,
+            self.linear_z(x).view(B, T, n, k), self.linear_h(x).view(B, T, n, k), h0_blocks,
+            perm, sgn, p2p, has_scale=0, has_decay=1 if dt is not None else 0,
+        )
+        if h is not None:
+            return h.reshape(B, T, self.hidden_size)
+        theta, scale, gamma, b = self._angle_heads(x, dt)
         h = _dispatch_angle_scan(
             theta, scale, gamma, b, h0_blocks, perm, sgn, p2p,
             has_scale=0, has_decay=1 if dt is not None else 0,

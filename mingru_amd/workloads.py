@@ -125,6 +125,31 @@ def c4_inputs(B=8, T=2048, n=64, k=8):
                 sgn=sgn, p2p=p2p, grad_h=gh)
 
 
+def c4g_inputs(B=8, T=2048, n=64, k=8, rounds=3):
+    """GivensMinGRU's brick-wall heads at the C4 shape (its default 3 rounds): angles
+    ``0.5 N(0,1)`` (B, T, n, rounds, k/2), ``gamma = sigmoid(N)``, the gate and candidate
+    pre-activations ``z, hpre ~ N(0,1)`` (B, T, n, k) (so ``b = sigmoid(z) * hpre``),
+    ``h0 ~ N``, upstream ``dL/dh ~ N``."""
+    g = _gen(1014)
+    theta = 0.5 * torch.randn(B, T, n, rounds, k // 2, generator=g)
+    gamma = torch.sigmoid(torch.randn(B, T, n, generator=g))
+    z = torch.randn(B, T, n, k, generator=g)
+    hpre = torch.randn(B, T, n, k, generator=g)
+    h0 = torch.randn(B, n, k, generator=g)
+    gh = torch.randn(B, T, n, k, generator=_gen(2014))
+    return dict(theta=theta, gamma=gamma, z=z, hpre=hpre, h0=h0, grad_h=gh)
+
+
+def c2gd_inputs(B=16, T=4096, D=1024):
+    """C2g's pre-activations plus time decay: ``dt ~ U(0, 2)`` (B, T) and a per-channel
+    rate ``lam ~ U(0.1, 1.1)`` (D,)."""
+    inp = c2g_inputs(B, T, D)
+    g = _gen(1013)
+    inp["dt"] = 2.0 * torch.rand(B, T, generator=g)
+    inp["lam"] = 0.1 + torch.rand(D, generator=g)
+    return inp
+
+
 def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
     """Delta-rule heads on the kernel layouts, bf16 inputs, ``H0 = 0``."""
     g = _gen(1005)

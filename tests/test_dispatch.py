@@ -699,3 +699,51 @@ def test_plane_table_cache_sees_new_sgn_and_p2p_objects():
     sgn_new.neg_()
     t4 = hip_scans._device_tables(perm, sgn_new, p2p_new, 8, 4, torch.device("cpu"))
     assert torch.equal(t4[1], sgn_new.float())
+
+
+def test_rotation_gated_heads_reach_backend(monkeypatch):
+    """RotationMinGRU's fast path hands the snapped angle (B, T, n, 1, 1), u (B, T, n),
+    and z, h~ (B, T, n, 2) pre-activations to the gated-heads kernel; its result is the
+    module's output."""
+    seen = {}
+
+    def fake_gated(theta, u, gamma, z, hpre, h0, perm, sgn, p2p, *, has_scale, has_decay):
+        seen.update(theta=tuple(theta.shape), u=tuple(u.shape), z=tuple(z.shape),
+                    hpre=tuple(hpre.shape), gamma=gamma, has_scale=has_scale,
+                    has_decay=has_decay)
+        return torch.full(z.shape, 4.0)
+
+    def fake_plain(*args, **kwargs):
+        raise AssertionError("the plain angle kernel must not run when the gated one does")
+
+    _fake_backend(monkeypatch, angle_gated_scan_impl=fake_gated, angle_scan_impl=fake_plain)
+    m = mg.RotationMinGRU(5, 6)
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    y = m(torch.randn(2, 7, 5))
+    assert torch.equal(y, torch.full((2, 7, 6), 4.0))
+    assert seen == {"theta": (2, 7, 3, 1, 1), "u": (2, 7, 3), "z": (2, 7, 3, 2),
+                    "hpre": (2, 7, 3, 2), "gamma": None, "has_scale": 1, "has_decay": 0}
+
+
+def test_givens_gated_heads_decline_runs_the_plain_kernel(monkeypatch):
+    """A declined gated call is silent: the plain angle seam then runs with eager heads,
+    under its own mode rules."""
+    calls = []
+
+    def fake_gated(*args, **kwargs):
+        calls.append("gated")
+        raise sys.modules[BACKEND].ScanFallback("schedule not covered")
+
+    def fake_plain(theta, scale, gamma, b, h0, perm, sgn, p2p, *, has_scale, has_decay):
+        calls.append("plain")
+        assert tuple(b.shape) == (2, 7, 2, 8) and has_decay == 1
+        return torch.zeros(b.shape)
+
+    _fake_backend(monkeypatch, angle_gated_scan_impl=fake_gated, angle_scan_impl=fake_plain)
+    m = GivensMinGRU(6, 16, block_size=8, decay="fixed")
+    monkeypatch.setenv("MINGRU_SCAN", "hip")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        y = m(torch.randn(2, 7, 6), delta_t=torch.rand(2, 7))
+    assert calls == ["gated", "plain"]
+    assert torch.equal(y, torch.zeros(2, 7, 16))

@@ -218,11 +218,27 @@ def test_c4_norm_preserved_full_size(cuda):
     assert drift <= 1e-4
 
 
-def _module_vs_fp64(cuda, layer, x, monkeypatch, dt=None):
+def _graph_has(t, name, depth=4):
+    """Whether an autograd node named ``name`` lies within ``depth`` steps of ``t``."""
+    frontier = [t.grad_fn]
+    for _ in range(depth):
+        nxt = []
+        for f in frontier:
+            if f is None:
+                continue
+            if name in type(f).__name__:
+                return True
+            nxt += [g for g, _ in f.next_functions]
+        frontier = nxt
+    return False
+
+
+def _module_vs_fp64(cuda, layer, x, monkeypatch, dt=None, kernel=None):
     """A mixer under MINGRU_SCAN=hip on the GPU (fp32) against a float64 copy of it on
     the CPU eager path: output within 1e-4 and the input and parameter gradients within
     1e-3, each relative to max(1, max |ref|) (the undecayed rotation state grows to
-    |h| ~ 10 over a sequence)."""
+    |h| ~ 10 over a sequence).  ``kernel`` names the autograd node the GPU forward must
+    have run (the gated-heads kernel or the plain one)."""
     import copy
 
     ref = copy.deepcopy(layer).double()
@@ -235,6 +251,8 @@ def _module_vs_fp64(cuda, layer, x, monkeypatch, dt=None):
     lg = layer.to(cuda)
     xg = x.to(cuda).requires_grad_(True)
     y = lg(xg, delta_t=None if dt is None else dt.to(cuda))
+    if kernel is not None:
+        assert _graph_has(y, kernel), f"{kernel} did not run"
     y.square().sum().backward()
     torch.cuda.synchronize()
 
@@ -250,17 +268,83 @@ def _module_vs_fp64(cuda, layer, x, monkeypatch, dt=None):
 
 def test_givens_module_matches_eager(cuda, monkeypatch):
     torch.manual_seed(0)
-    _module_vs_fp64(cuda, mg.GivensMinGRU(16, 64), torch.randn(3, 64, 16), monkeypatch)
+    _module_vs_fp64(cuda, mg.GivensMinGRU(16, 64), torch.randn(3, 64, 16), monkeypatch,
+                    kernel="AngleGatedFn")
 
 
 def test_givens_module_decay_matches_eager(cuda, monkeypatch):
     torch.manual_seed(1)
     layer = mg.GivensMinGRU(16, 32, decay="learnable")
-    _module_vs_fp64(cuda, layer, torch.randn(2, 40, 16), monkeypatch, dt=torch.rand(2, 40))
+    _module_vs_fp64(cuda, layer, torch.randn(2, 40, 16), monkeypatch, dt=torch.rand(2, 40),
+                    kernel="AngleGatedFn")
+
+
+@pytest.mark.parametrize("k, rounds", [(2, 1), (4, 5)])
+def test_givens_module_small_blocks_gated_heads(cuda, monkeypatch, k, rounds):
+    """Block sizes 2 and 4 on the gated-heads kernel, one with decay."""
+    torch.manual_seed(5 + k)
+    layer = mg.GivensMinGRU(12, 24, block_size=k, rounds=rounds,
+                            decay="fixed" if k == 4 else None)
+    dt = torch.rand(2, 300) if k == 4 else None
+    _module_vs_fp64(cuda, layer, torch.randn(2, 300, 12), monkeypatch, dt=dt,
+                    kernel="AngleGatedFn")
+
+
+def test_givens_module_block16_keeps_the_table_kernel(cuda, monkeypatch):
+    """k = 16 runs on the run-time-table kernel, with the heads formed eagerly."""
+    torch.manual_seed(6)
+    _module_vs_fp64(cuda, mg.GivensMinGRU(12, 32, block_size=16), torch.randn(2, 50, 12),
+                    monkeypatch, kernel="AngleTablesFn")
 
 
 @pytest.mark.parametrize("snap", [None, (2, 3, 4, 6)], ids=["nosnap", "default_snap"])
 def test_rotation_module_matches_eager(cuda, monkeypatch, snap):
     torch.manual_seed(2)
     _module_vs_fp64(cuda, mg.RotationMinGRU(16, 32, snap=snap), torch.randn(3, 64, 16),
-                    monkeypatch)
+                    monkeypatch, kernel="AngleGatedFn")
+
+
+@pytest.mark.parametrize("decay", ["fixed", "learnable"])
+def test_rotation_module_decay_matches_eager(cuda, monkeypatch, decay):
+    torch.manual_seed(3)
+    layer = mg.RotationMinGRU(16, 32, decay=decay)
+    _module_vs_fp64(cuda, layer, torch.randn(2, 500, 16), monkeypatch,
+                    dt=torch.rand(2, 500) * 2, kernel="AngleGatedFn")
+
+
+@pytest.mark.parametrize("has_decay", [0, 1])
+def test_gated_heads_match_the_plain_kernel_full_size(cuda, has_decay):
+    """At the C4 size (B=8, T=2048, 64 blocks of 8, brick-wall rounds as GivensMinGRU):
+    the gated-heads kernel against the plain kernel fed sigmoid(z) * hpre computed by
+    torch, forward and every gradient (through torch's autograd for the plain path)."""
+    B, T, n, k, R = 8, 2048, 64, 8, 3
+    print(f"[gpu] gated heads vs plain kernel, C4 size, has_decay={has_decay}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(9)
+    theta = (0.5 * torch.randn(B, T, n, R, k // 2, device=cuda, generator=g))
+    z = torch.randn(B, T, n, k, device=cuda, generator=g)
+    hp = torch.randn(B, T, n, k, device=cuda, generator=g)
+    gamma = torch.sigmoid(torch.randn(B, T, n, device=cuda, generator=g))
+    h0 = torch.randn(B, n, k, device=cuda, generator=g)
+    gh = torch.randn(B, T, n, k, device=cuda, generator=g)
+    perm, sgn, p2p = (t.to(cuda) for t in hip_scans._brick_tables(k, R))
+    a = [t.clone().requires_grad_(True) for t in (theta, z, hp, gamma, h0)]
+    h1 = hip_scans.angle_gated_scan_impl(a[0], None, a[3], a[1], a[2], a[4], perm, sgn, p2p,
+                                         has_scale=0, has_decay=has_decay)
+    assert "AngleGatedFn" in type(h1.grad_fn).__name__
+    h1.backward(gh)
+    b_ = [t.clone().requires_grad_(True) for t in (theta, z, hp, gamma, h0)]
+    bb = torch.sigmoid(b_[1]) * b_[2]
+    ones = torch.ones(B, T, n, device=cuda)
+    h2 = hip_scans.angle_scan_impl(b_[0], ones, b_[3], bb, b_[4], perm, sgn, p2p, has_scale=0,
+                                   has_decay=has_decay)
+    h2.backward(gh)
+    torch.cuda.synchronize()
+    # The two differ only in how sigmoid(z) is evaluated (the kernel's exp2/rcp against
+    # torch's), about 1e-7 relative per token; without decay |h| grows to ~25 over the
+    # sequence, so the bar is relative to the largest magnitude.
+    assert (h1 - h2).abs().max().item() / max(1.0, h2.abs().max().item()) <= 1e-5
+    for name, x, y in zip(("theta", "z", "hpre", "gamma", "h0"), a, b_):
+        if name == "gamma" and not has_decay:
+            continue
+        err = (x.grad - y.grad).abs().max().item() / max(1.0, y.grad.abs().max().item())
+        assert err <= 1e-5, f"d{name} {err:.2e}"
