@@ -182,6 +182,15 @@ def build_ops(torch, wl):
                     c["B"] * c["T"], "mg_delta_gated_fwd", "mg_delta_gated_bwd",
                     4 * bt + bt // c["d"] + lgb, 7 * bt + 2 * bt // c["d"] + 2 * lgb, f_fwd,
                     2 * f_fwd)
+    # C5dp: C5d with nh = 2 micro-steps per token (DeltaProduct), bf16: K, V, beta carry
+    # two micro-steps per token; the kernels tile 32 tokens (64 micro-steps) per chunk.
+    # FLOP floor as C5's per 64-micro-step tile (twice the tiles of C5).
+    nh = 2
+    bk = bt * nh  # one bf16 (B,H,T,nh,d) tensor
+    ops["C5dp"] = Op("C5dp", "C5dp DeltaMinGRU decay-gated DeltaProduct nh=2 fwd+bwd (C5 shape, "
+                     "bf16 in)", c["B"] * c["T"], "mg_delta_gated_fwd", "mg_delta_gated_bwd",
+                     2 * bt + 2 * bk + bk // c["d"] + lgb,
+                     3 * bt + 4 * bk + 2 * bk // c["d"] + 2 * lgb, nh * f_fwd, 2 * nh * f_fwd)
     return ops
 
 
@@ -360,10 +369,10 @@ def make_step(key, torch, wl, dev):
                                               inp["grad_HT"][:bs]))
 
         return step, cpu, wl.C5["B"]
-    if key == "C5d":
+    if key in ("C5d", "C5dp"):
         from mingru_amd import hip_scans
 
-        inp = wl.c5d_inputs(**wl.C5)
+        inp = wl.c5d_inputs(**wl.C5, nh=2 if key == "C5dp" else 1)
         names = ("Q", "K", "V", "beta", "log_gamma", "H0")
         xs = [inp[k].to(dev).requires_grad_(True) for k in names]
         gy = inp["grad_y"].to(dev).to(inp["Q"].dtype)
@@ -470,6 +479,26 @@ def delta_eager_gpu_ms(torch, wl, dev, reps=3):
         ts.append((time.perf_counter() - t0) * 1e3)
     ts.sort()
     return ts[len(ts) // 2]
+
+
+def delta_gated_fp32_kernels_ms(torch, wl, dev, steps, nh=1):
+    """The decay-gated workload with fp32 inputs, i.e. on the fp32-operand gated kernels,
+    fwd+bwd; ms per step over `steps` steps."""
+    from mingru_amd import hip_scans
+
+    inp = wl.c5d_inputs(**wl.C5, nh=nh)
+    names = ("Q", "K", "V", "beta", "log_gamma", "H0")
+    xs = [inp[k].to(dev).float().requires_grad_(True) for k in names]
+    gy = inp["grad_y"].to(dev)
+    gH = inp["grad_HT"].to(dev)
+
+    def step():
+        y, HT = hip_scans.delta_gated_scan_impl(*xs, chunk_size=inp["chunk_size"])
+        torch.autograd.grad((y, HT), xs, (gy, gH))
+
+    for _ in range(2):
+        step()
+    return _timed(step, steps, torch)
 
 
 def delta_gated_eager_gpu_ms(torch, wl, dev, reps=3):
@@ -769,7 +798,7 @@ def main():
     os.environ["MINGRU_SCAN"] = "hip"
     dev = torch.device("cuda:0")
     ops = build_ops(torch, wl)
-    order = ["C2", "C2g", "C2gd", "C1", "C1g", "C3", "C3m", "C4", "C4g", "C5", "C5d"]
+    order = ["C2", "C2g", "C2gd", "C1", "C1g", "C3", "C3m", "C4", "C4g", "C5", "C5d", "C5dp"]
     if args.only:
         order = [k for k in order if k in args.only.split(",")]
     results = {}
@@ -803,6 +832,15 @@ def main():
                     "C1g": "parallel_scan_log", "C4g": "angle scan"}[key]
             print(f"#   unfused (eager gates + HIP {scan}): {uf:.3f} ms/step "
                   f"({res['speedup_vs_unfused']:.2f}x the fused time)", file=sys.stderr,
+                  flush=True)
+        if key == "C5dp" and not args.no_eager:
+            # The same workload on the fp32-operand gated kernels (what bf16 DeltaProduct
+            # inputs ran on before the bf16 kernels took nh > 1).
+            f32 = delta_gated_fp32_kernels_ms(torch, wl, dev, args.steps, nh=2)
+            res["fp32_kernels_ms_per_step"] = f32
+            res["speedup_vs_fp32_kernels"] = f32 / res["ms_per_step"]
+            print(f"#   fp32-operand gated kernels: {f32:.3f} ms/step "
+                  f"({res['speedup_vs_fp32_kernels']:.2f}x the bf16 time)", file=sys.stderr,
                   flush=True)
         if key in ("C5", "C5d") and not args.no_eager:
             eg = (delta_eager_gpu_ms if key == "C5" else delta_gated_eager_gpu_ms)(torch, wl, dev)
@@ -869,7 +907,7 @@ def main():
         "config": {"workload": op.workload, **{"C1": wl.C1, "C1g": wl.C1, "C2": wl.C2, "C2g": wl.C2,
                                                "C2gd": wl.C2, "C3": wl.C3, "C3m": wl.C3,
                                                "C4": wl.C4, "C4g": wl.C4, "C5": wl.C5,
-                                               "C5d": wl.C5}.get(head_key, {})},
+                                               "C5d": wl.C5, "C5dp": wl.C5}.get(head_key, {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "achieved_TBs": head["achieved_TBs"],

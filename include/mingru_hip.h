@@ -296,7 +296,7 @@ int mg_delta_bwd(const void* Q, const void* K, const void* V, const void* beta,
  * (DeltaMinGRU._forward_chunked_gated, src/mingru/min_gru.py:3257-3448, guarded by
  * _delta_decay_dispatch_guard :612-668) and its autograd backward.  Per token t the
  * state decays by gamma_t = exp(log_gamma[b,h,t]) before the token's nh micro-steps.
- * Layouts and dtype tag as mg_delta_fwd (dtype 1 = bf16 requires nh = 1), plus
+ * Layouts and dtype tag as mg_delta_fwd (dtype 1 = bf16, any nh), plus
  * log_gamma / dlog_gamma (B,H,T) fp32.  `Hbound` takes mg_delta_state_bytes; `ws`
  * mg_delta_gated_workspace_bytes (forward and backward). */
 size_t mg_delta_gated_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,

@@ -29,9 +29,8 @@
 // added in a fixed order.
 //
 // These kernels mirror delta_wy.hip (fp32 operands on v_mfma_f32_16x16x4_f32) and
-// serve fp32 inputs and nh > 1; bf16 inputs with nh = 1 run the gated
-// instantiations of the bf16-MFMA kernels (delta_wy_bf16.hip), chosen by the
-// dtype tag of the entry points.  The per-chunk decay vectors (a beta, ptok, p,
+// serve fp32 inputs; bf16 inputs (any nh) run the gated instantiations of the
+// bf16-MFMA kernels (mg_delta_bf16.h), chosen by the dtype tag of the entry points.  The per-chunk decay vectors (a beta, ptok, p,
 // PC) travel in a small vector region after the workspace matrices.
 #include "mg_delta_bf16.h"
 
@@ -731,7 +730,7 @@ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// bf16 inputs (nh = 1): the gated instantiations of the bf16-MFMA kernels
+// bf16 inputs: the gated instantiations of the bf16-MFMA kernels
 // ---------------------------------------------------------------------------
 namespace mgd {
 
@@ -758,7 +757,6 @@ int dw_bwd_bf16_gated(const void* Q, const void* K, const void* V, const void* b
                       const float* lg, const float* Hb, const void* dy, const float* dHT, void* dQ,
                       void* dK, void* dV, void* dbeta, float* dlg, float* dH0, int64_t BH,
                       const DwGeom& g, void* ws, size_t ws_bytes, hipStream_t stream) {
-  if (g.nh != 1) return MG_ERR_ARG;  // the gated gradients are token-level
   const size_t mb = dw_mat_bytes(BH, g);
   if (ws_bytes < 6 * mb + (size_t)BH * g.nc * VECN * sizeof(float)) return MG_ERR_WORKSPACE;
   float* Um = (float*)ws;
@@ -804,7 +802,6 @@ int mg_delta_gated_fwd(const void* Q, const void* K, const void* V, const void* 
   if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
   if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
   if (dtype == 1) {
-    if (nh != 1) return MG_ERR_ARG;
     return dw_fwd_bf16_gated(Q, K, V, beta, log_gamma, H0, y, HT, Hbound, BH, g, ws, ws_bytes,
                              stream);
   }
@@ -839,7 +836,6 @@ int mg_delta_gated_bwd(const void* Q, const void* K, const void* V, const void* 
   if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return MG_ERR_ARG;
   if (!al16(ws) || !al16(Hbound)) return MG_ERR_ARG;
   if (dtype == 1) {
-    if (nh != 1) return MG_ERR_ARG;
     return dw_bwd_bf16_gated(Q, K, V, beta, log_gamma, Hbound, dy, dHT, dQ, dK, dV, dbeta,
                              dlog_gamma, dH0, BH, g, ws, ws_bytes, stream);
   }

@@ -440,7 +440,7 @@ int dwb_bwd_prep_launch(bool gated, const void* Q, const void* K, const void* V,
                         float* G0m, float* Apm, float* bpm, float* vm, int64_t BH,
                         const DwGeom& g, hipStream_t stream);
 
-// Decay-gated forms (delta_gated.hip), bf16 inputs and nh = 1: lg / dlg are the
+// Decay-gated forms (delta_gated.hip), bf16 inputs: lg / dlg are the
 // per-token log decay and its gradient, fp32 (B*H, T); the workspace adds a
 // vector region of VECN floats per chunk after the matrices.
 int dw_fwd_bf16_gated(const void* Q, const void* K, const void* V, const void* beta,

@@ -509,7 +509,7 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
   __syncthreads();
   if constexpr (GATED) {
     decay_tables<NTB>(sl, sE);
-    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
+    decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
     __syncthreads();
   }
   floatx4 pp[2];
@@ -525,9 +525,10 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED) {  // nh = 1: micro-rows are tokens
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
-          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * sE[row * LD + col] : 0.f;
+        if constexpr (GATED) {  // spans between the tokens of micro-rows (tau = m / nh)
+          const int tc = col / g.nh;
+          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + tc] : 0.f;
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + tc] : 0.f;
         } else {
           kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
           pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
@@ -728,8 +729,8 @@ __device__ __forceinline__ void smm(floatx4 (&acc)[2], const FragOff& F, const u
 //   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32, fragment-major) for the
 //      reverse chain.
 // GATED: L and P weighted by the span factors, R = V - diag(p) K Hc,
-// E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E.
-// The gated forms assume nh = 1 (the entry points check it).
+// E = T^T diag(a beta) K, b' = Q^T diag(ptok) dy - (p K)^T G0, A' = -(p K)^T E, with
+// the span weights between the tokens tau(m) = m / nh of the micro-rows.
 //
 // The products run in dependency order so that few 64 x 64 operands are live at
 // once, and LDS stays under 80 KB (two workgroups per CU):
@@ -802,11 +803,13 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
   }
   __syncthreads();
   // ---- A: L, then T = (I + L)^-1 in place ----
-  float ew[2][4];  // gated: E[row][col] at the wave's fragment positions (nh = 1)
+  // gated: the span weights at the wave's fragment positions, of L (micro-rows row, col:
+  // E[tau(row)][tau(col)]) and of P (token row, micro-row col: E[row][tau(col)]).
+  float ew[2][4], ewp[2][4];
   if constexpr (GATED) {
     float* sE = reinterpret_cast<float*>(&sR1);  // span table, row stride DN
     decay_tables<NTB, DN>(sl, sE);
-    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt);
+    decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
     write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);  // wave 0's own values
     __syncthreads();
 #pragma unroll
@@ -814,7 +817,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = C0 + 16 * jj + r;
-        ew[jj][i] = col <= row ? sE[row * DN + col] : 0.f;
+        ew[jj][i] = col < row ? sE[(row / g.nh) * DN + col / g.nh] : 0.f;
+        ewp[jj][i] = col < (row + 1) * g.nh ? sE[row * DN + col / g.nh] : 0.f;
       }
   }
   {
@@ -875,8 +879,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED)  // nh = 1: micro-rows are tokens
-          pp[jj][i] = col <= row ? pp[jj][i] * sb[col] * ew[jj][i] : 0.f;
+        if constexpr (GATED)
+          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * ewp[jj][i] : 0.f;
         else
           pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
       }
@@ -989,7 +993,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 // Q and dy enter the products as A fragments straight from memory; the split
 // operands rotate through three 16 KB regions, so LDS stays under 80 KB (two
 // workgroups per CU).  D2 is symmetrised in registers from dT and dT^T = -U G^T.
-// GATED (nh = 1, decay tables in mg_delta.h): the products are weighted as in
+// GATED (decay tables in mg_delta.h): the products are weighted as in
 // the forward -- dS = (dy U^T) beta_col E_read, D2 = (-G U^T) beta E_mm (both
 // triangles), dQ = diag(ptok) dy Hc^T + dS K, dK = -diag(p) G Hc^T + dS^T Q + D2 K
 // + diag(a beta) U dHn^T, dbeta's U (K dHn) term times a -- and the span
@@ -1061,7 +1065,7 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
   __syncthreads();
   if constexpr (GATED) {
     decay_tables<NTB>(sl, sEg);
-    decay_vectors(sl, sb, ch, 1, sLc, sp, sab, spt, sa);
+    decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt, sa);
   }
   {
     // U and Hc are fetched while G forms, and staged once E and dHn^T are free.
@@ -1095,7 +1099,9 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
   __syncthreads();
   BPair &sG = sR[0], &sU = sR[1], &sHc = sR[2];
   floatx4 ds2[2], d2[2], dq[2], dk[2];
-  floatx4 f2[2];  // gated: span gradients F at the wave's (t, t') positions
+  // gated: span gradients at the wave's positions: f1 of the (token t, micro-row m)
+  // products, f2 of the (micro-row m, micro-row j) ones.
+  floatx4 f1[2], f2[2];
   {
     floatx4 s2[2], dp2[2];
     zero2(s2);
@@ -1111,10 +1117,10 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
         const int t = R0 + 4 * gg + i, m = cj + r;
         const bool rd = m < (t + 1) * g.nh;
         if constexpr (GATED) {
-          const float er = rd ? sEg[t * LD + m] : 0.f;
+          const float er = rd ? sEg[t * LD + m / g.nh] : 0.f;
           ds2[jj][i] = dp2[jj][i] * sb[m] * er;
           db[i] = dp2[jj][i] * s2[jj][i] * er;
-          f2[jj][i] = db[i] * sb[m];
+          f1[jj][i] = db[i] * sb[m];
         } else {
           ds2[jj][i] = rd ? dp2[jj][i] * sb[m] : 0.f;
           db[i] = rd ? dp2[jj][i] * s2[jj][i] : 0.f;
@@ -1139,10 +1145,11 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       for (int i = 0; i < 4; ++i) {
         const int m = R0 + 4 * gg + i, j = cj + r;
         if constexpr (GATED) {
-          const float elo = j < m ? sEg[m * LD + j] : 0.f, ehi = m < j ? sEg[j * LD + m] : 0.f;
+          const int tm = m / g.nh, tj = j / g.nh;
+          const float elo = j < m ? sEg[tm * LD + tj] : 0.f, ehi = m < j ? sEg[tj * LD + tm] : 0.f;
           d2[jj][i] = j < m ? dt2[jj][i] * sb[j] * elo : dtt2[jj][i] * sb[m] * ehi;
           db[i] = dt2[jj][i] * kk2[jj][i] * elo;
-          f2[jj][i] += db[i] * sb[j];
+          f2[jj][i] = db[i] * sb[j];
         } else {
           d2[jj][i] = j < m ? dt2[jj][i] * sb[j] : (m < j ? dtt2[jj][i] * sb[m] : 0.f);
           db[i] = j < m ? dt2[jj][i] * kk2[jj][i] : 0.f;
@@ -1241,32 +1248,77 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
     stf(dbeta, row0 + m, acc);
   }
   if constexpr (GATED) {
-    // Token-level F (t' < t) into U's buffer, plus the carry term on row Ct - 1;
-    // f[t] in sdec's l slot.
-    float* sF = reinterpret_cast<float*>(&sR[1]);  // 64 x 64, stride DN
+    // Token-level F[t][t'] (t' < t) and f[t] (in sdec's l slot).  With one micro-step
+    // per token the micro-rows are the tokens: F is the wave's f1 + f2 plus the carry
+    // term on row Ct - 1.  With nh > 1 the (t, m) and (m, j) span gradients go to two
+    // tables and are summed over the micro-rows of each token pair:
+    //   F[t][t'] = sum_j f1[t][t' nh + j] + sum_{a,b} f2[t nh + a][t' nh + b]
+    //              (+ sum_j a beta rowsum terms of t' nh + j on row Ct - 1),
+    // and the p terms of f over the micro-rows of each token.
+    float pcs = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
+    for (int q = 0; q < WB; ++q) pcs += sred[q];
+    float* sF;
+    if (g.nh == 1) {
+      sF = reinterpret_cast<float*>(&sR[1]);  // 64 x 64, stride DN
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = R0 + 4 * gg + i, tp = C0 + 16 * jj + r;
-        sF[t * DN + tp] = (tp < t && t < ch.Ct) ? f2[jj][i] : 0.f;
-      }
-    __syncthreads();
-    if (threadIdx.x < DN) {
-      const int t = threadIdx.x;
-      if (t < ch.Ct - 1)
-        sF[(ch.Ct - 1) * DN + t] += sab[t] * (sdb[8][t] + sdb[9][t]);
-      float f = 0.f;
-      if (t < ch.Ct) {
-        f = sfp[t] + sfp[DN + t] + sfp[2 * DN + t] + sfp[3 * DN + t];
-        if (t == ch.Ct - 1) {
-          float pcs = 0.f;
+      for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int q = 0; q < WB; ++q) pcs += sred[q];
-          f = fmaf(expf(sLc[t]), pcs, f);
+        for (int i = 0; i < 4; ++i) {
+          const int t = R0 + 4 * gg + i, tp = C0 + 16 * jj + r;
+          sF[t * DN + tp] = (tp < t && t < ch.Ct) ? f1[jj][i] + f2[jj][i] : 0.f;
         }
+      __syncthreads();
+      if (threadIdx.x < DN) {
+        const int t = threadIdx.x;
+        if (t < ch.Ct - 1)
+          sF[(ch.Ct - 1) * DN + t] += sab[t] * (sdb[8][t] + sdb[9][t]);
+        float f = 0.f;
+        if (t < ch.Ct) {
+          f = sfp[t] + sfp[DN + t] + sfp[2 * DN + t] + sfp[3 * DN + t];
+          if (t == ch.Ct - 1) f = fmaf(expf(sLc[t]), pcs, f);
+        }
+        sl[t] = f;
       }
-      sl[t] = f;
+    } else {
+      const int nh = g.nh;
+      float* sA = reinterpret_cast<float*>(&sR[1]);  // f1 at (t; m)
+      float* sB = reinterpret_cast<float*>(&sR[2]);  // f2 at (m; j)
+      sF = reinterpret_cast<float*>(&sR[0]);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = R0 + 4 * gg + i, col = C0 + 16 * jj + r;
+          sA[row * DN + col] = f1[jj][i];
+          sB[row * DN + col] = f2[jj][i];
+        }
+      __syncthreads();
+      for (int e = threadIdx.x; e < DN * DN; e += NTB) {
+        const int t = e >> 6, tp = e & 63;
+        float v = 0.f;
+        if (t < ch.Ct && tp < t) {
+          for (int j = 0; j < nh; ++j) v += sA[t * DN + tp * nh + j];
+          for (int a = 0; a < nh; ++a)
+            for (int b = 0; b < nh; ++b) v += sB[(t * nh + a) * DN + tp * nh + b];
+          if (t == ch.Ct - 1)
+            for (int j = 0; j < nh; ++j) {
+              const int m = tp * nh + j;
+              v = fmaf(sab[m], sdb[8][m] + sdb[9][m], v);
+            }
+        }
+        sF[e] = v;
+      }
+      if (threadIdx.x < DN) {
+        const int t = threadIdx.x;
+        float f = 0.f;
+        if (t < ch.Ct) {
+          f = sfp[t] + sfp[DN + t];
+          for (int a = 0; a < nh; ++a) f += sfp[2 * DN + t * nh + a] + sfp[3 * DN + t * nh + a];
+          if (t == ch.Ct - 1) f = fmaf(expf(sLc[t]), pcs, f);
+        }
+        sl[t] = f;
+      }
     }
     __syncthreads();
     // dl_s = sum_{t >= s} (f[t] + sum_{t' < s} F[t][t']): wave-level prefix scans of

@@ -1265,9 +1265,9 @@ def delta_scan_impl(Q, K, V, beta, H0, *, chunk_size: int):
 class _DeltaGatedScanFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, beta, log_gamma, H0, chunk_size):
-        # bf16 inputs with nh = 1 read natively (bf16 MFMA); everything else in fp32.
+        # bf16 inputs read natively (bf16 MFMA, any nh); everything else in fp32.
         nh = K.shape[3]
-        cdt = _delta_compute_dtype(Q, K, V, beta) if nh == 1 else torch.float32
+        cdt = _delta_compute_dtype(Q, K, V, beta)
         q, k, v, bt = (_contig(t, cdt) for t in (Q, K, V, beta))
         lg, h0 = _contig(log_gamma, torch.float32), _contig(H0, torch.float32)
         Bn, nhd, T, d_k = q.shape
@@ -1317,9 +1317,9 @@ def delta_gated_scan_impl(Q, K, V, beta, log_gamma, H0, *, chunk_size: int):
     (``_forward_chunked_gated``, ``src/mingru/min_gru.py:3257-3448``).  Layouts
     as ``delta_scan_impl`` plus ``log_gamma`` ``(B, n_heads, T)``, the per-token
     log decay applied to the state before the token's micro-steps.  bf16 Q, K, V,
-    beta with ``nh = 1`` run the bf16-MFMA kernels (fp32 state); other inputs and
-    ``nh > 1`` run in fp32 (half inputs are upcast).  ``y`` comes back in Q's dtype
-    and ``H_T`` in H0's.  Differentiable in all six tensors.
+    beta run the bf16-MFMA kernels (fp32 state) for any ``nh``; other inputs run in
+    fp32 (half inputs are upcast).  ``y`` comes back in Q's dtype and ``H_T`` in H0's.
+    Differentiable in all six tensors.
     """
     _delta_validate_envelope(Q, K, V, beta, H0, chunk_size)
     if tuple(log_gamma.shape) != tuple(Q.shape[:3]):

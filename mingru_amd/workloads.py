@@ -150,13 +150,15 @@ def c2gd_inputs(B=16, T=4096, D=1024):
     return inp
 
 
-def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
-    """Delta-rule heads on the kernel layouts, bf16 inputs, ``H0 = 0``."""
+def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16, nh=1):
+    """Delta-rule heads on the kernel layouts, bf16 inputs, ``H0 = 0``; ``nh``
+    micro-steps per token (DeltaProduct) give K, V (B, H, T, nh, d) and beta
+    (B, H, T, nh)."""
     g = _gen(1005)
     q = torch.randn(B, H, T, d, generator=g)
-    k = F.normalize(torch.randn(B, H, T, 1, d, generator=g), dim=-1)
-    v = torch.randn(B, H, T, 1, d, generator=g)
-    beta = torch.sigmoid(torch.randn(B, H, T, 1, generator=g))
+    k = F.normalize(torch.randn(B, H, T, nh, d, generator=g), dim=-1)
+    v = torch.randn(B, H, T, nh, d, generator=g)
+    beta = torch.sigmoid(torch.randn(B, H, T, nh, generator=g))
     g2 = _gen(2005)
     dy = torch.randn(B, H, T, d, generator=g2)
     dHT = torch.randn(B, H, d, d, generator=g2)
@@ -164,10 +166,10 @@ def c5_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
                 H0=torch.zeros(B, H, d, d), chunk_size=chunk, grad_y=dy, grad_HT=dHT)
 
 
-def c5d_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16):
+def c5d_inputs(B=8, H=8, T=8192, d=64, chunk=64, dtype=torch.bfloat16, nh=1):
     """C5 heads (bf16, as C5) with per-token decay for the gated delta kernels:
     ``log gamma = -0.5 U(0, 1)`` per (head, token) in fp32, the span a fixed decay
     rate of 0.5 gives over unit-scale gaps."""
-    inp = c5_inputs(B, H, T, d, chunk, dtype=dtype)
+    inp = c5_inputs(B, H, T, d, chunk, dtype=dtype, nh=nh)
     inp["log_gamma"] = -0.5 * torch.rand(B, H, T, generator=_gen(1015))
     return inp

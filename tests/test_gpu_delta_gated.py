@@ -164,7 +164,7 @@ def _graph_nodes(fn, seen=None):
         stack.extend(n for n, _ in f.next_functions)
 
 
-# bf16 Q, K, V, beta with nh = 1 run the gated bf16-MFMA kernels.  Bars as for the
+# bf16 Q, K, V, beta run the gated bf16-MFMA kernels (any nh).  Bars as for the
 # ungated bf16 path: bf16 outputs (y, dQ, dK, dV, dbeta) within 2e-2 of the largest
 # reference magnitude (the oracle sees the same bf16-rounded inputs); the fp32
 # outputs (H_T, dH0, dlog_gamma) within 1e-4 of it.
@@ -172,14 +172,23 @@ BF16_REL = 2e-2
 SPLIT_REL = 1e-4
 
 BF16_CASES = [
-    # B, H, T, dk, dv, chunk, log-gamma kind
-    (1, 1, 1, 4, 4, 4, "mod"),
-    (2, 2, 100, 16, 16, 16, "mod"),
-    (1, 3, 128, 64, 64, 64, "mod"),
-    (2, 1, 130, 32, 48, 32, "spikes"),
-    (1, 2, 300, 64, 64, 64, "weak"),
-    (2, 2, 200, 64, 64, 64, "spikes"),
-    (1, 2, 70, 24, 40, 20, "zero"),
+    # B, H, T, nh, dk, dv, chunk, log-gamma kind
+    (1, 1, 1, 1, 4, 4, 4, "mod"),
+    (2, 2, 100, 1, 16, 16, 16, "mod"),
+    (1, 3, 128, 1, 64, 64, 64, "mod"),
+    (2, 1, 130, 1, 32, 48, 32, "spikes"),
+    (1, 2, 300, 1, 64, 64, 64, "weak"),
+    (2, 2, 200, 1, 64, 64, 64, "spikes"),
+    (1, 2, 70, 1, 24, 40, 20, "zero"),
+    # DeltaProduct: nh micro-steps per token on the bf16 kernels, the decay applied
+    # once per token before them; 64 micro-steps per kernel tile (nh = 2 at chunk 64
+    # runs 32-token tiles), ragged last tiles, saturating gaps.
+    (2, 2, 150, 2, 64, 64, 32, "mod"),
+    (1, 2, 200, 2, 64, 64, 64, "spikes"),
+    (2, 1, 97, 3, 32, 48, 21, "weak"),
+    (1, 3, 64, 3, 16, 16, 8, "spikes"),
+    (1, 1, 1, 2, 8, 8, 4, "mod"),
+    (1, 2, 40, 4, 64, 64, 16, "zero"),
 ]
 
 
@@ -190,13 +199,15 @@ def _rel(got, ref):
 
 @pytest.mark.parametrize("case", BF16_CASES)
 def test_delta_gated_bf16_matches_oracle(cuda, case):
-    B, H, T, dk, dv, C, kind = case
+    B, H, T, nh, dk, dv, C, kind = case
     print(f"[gpu] delta gated bf16 case={case}", flush=True)
-    Q, K, V, beta, lg, H0, dy, dHT = _inputs(B, H, T, 1, dk, dv, seed=41 + T, lg_kind=kind)
+    Q, K, V, beta, lg, H0, dy, dHT = _inputs(B, H, T, nh, dk, dv, seed=41 + T + nh, lg_kind=kind)
     Q, K, V, beta, dy = (t.to(torch.bfloat16) for t in (Q, K, V, beta, dy))
     y, HT, grads = _run((Q, K, V, beta, lg, H0), dy, dHT, C, cuda)
     assert y.dtype == torch.bfloat16 and grads[0].dtype == torch.bfloat16
     assert grads[4].dtype == torch.float32
+    # The bf16 kernels ran: y is the op's own bf16 output (an fp32 compute would end in
+    # a cast, whose graph node _run's check on y.grad_fn would have rejected).
     ref = [_np(t) for t in (Q, K, V, beta, lg, H0)]
     ry, rHT = orc.delta_gated_sequential(*ref)
     assert _rel(y, ry) <= BF16_REL
