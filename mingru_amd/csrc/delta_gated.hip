@@ -439,13 +439,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_chain(const float* __restrict__ K,
 }
 
 // Row sums over the 16 lanes of a lane group (the 16 columns of a tile).
-__device__ __forceinline__ float rowsum16(float p) {
-  p += __shfl_xor(p, 1);
-  p += __shfl_xor(p, 2);
-  p += __shfl_xor(p, 4);
-  p += __shfl_xor(p, 8);
-  return p;
-}
+__device__ __forceinline__ float rowsum16(float p) { return mg_group_sum<16>(p); }
 
 __global__ __launch_bounds__(NT) void dg_bwd_grads(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ beta,
@@ -499,9 +493,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
   decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
   // PC term: <dHn, Hc>, with dHn in this thread's tile registers and Hc in sH.
   {
-    float part = tn.dot(sH);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+    const float part = mg_group_sum<64>(tn.dot(sH));
     if (lane == 0) sred[w] = part;
   }
   __syncthreads();

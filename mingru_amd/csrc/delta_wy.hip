@@ -502,12 +502,7 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
       a[i] += sb[m] * bu[i];
       if (m < ch.M && d < g.dk) stf(dK, (row0 + m) * g.dk + d, a[i]);
       // row sum over the 16 columns of this tile
-      float p = sU[m * LD + 16 * J + r] * x[i];
-      p += __shfl_xor(p, 1);
-      p += __shfl_xor(p, 2);
-      p += __shfl_xor(p, 4);
-      p += __shfl_xor(p, 8);
-      rowp[i] += p;
+      rowp[i] += mg_group_sum<16>(sU[m * LD + 16 * J + r] * x[i]);
     }
   }
   if (r == 0) {

@@ -66,6 +66,13 @@ __device__ __forceinline__ void mg_count_error(unsigned* header) {
   __hip_atomic_fetch_add(header + MG_H_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A value every lane of the wave holds (an LDS word all lanes read, a wave index),
+// marked as such: the compiler keeps it and what is derived from it in scalar
+// registers.
+__device__ __forceinline__ unsigned mg_uniform(unsigned x) {
+  return (unsigned)__builtin_amdgcn_readfirstlane((int)x);
+}
+
 struct MgTicket {
   unsigned ticket;  // dispatch-ordered index of this workgroup within the launch
   unsigned epoch;   // tag of every slot this launch publishes
@@ -127,7 +134,13 @@ __device__ __forceinline__ unsigned mg_next_ticket(unsigned* header, unsigned ep
 // the body's work instead of delaying the next chunk's first loads.  Tickets stay
 // monotone in time, so every predecessor of a chunk is held by a running
 // workgroup, as in the one-ticket form.
-template <typename Body>
+// UNIFORM marks the ticket and epoch, which every lane reads from the same LDS
+// words, as wave-uniform (mg_uniform), so that what the body derives from them
+// (chunk, lane group, row bases) stays in scalar registers.  It is a per-kernel
+// choice: it frees vector registers where a kernel is at the cap (the linear
+// backward: 38 spilled registers -> 5), and it was slower by 1-2% in kernels that
+// are not.
+template <bool UNIFORM = false, typename Body>
 __device__ __forceinline__ void mg_persistent(unsigned* header, unsigned chunks, Body&& body) {
   __shared__ unsigned s_ticket, s_epoch;
   if (threadIdx.x == 0) {
@@ -137,8 +150,8 @@ __device__ __forceinline__ void mg_persistent(unsigned* header, unsigned chunks,
     s_epoch = e;
   }
   __syncthreads();
-  unsigned t = s_ticket;
-  const unsigned e = s_epoch;
+  unsigned t = UNIFORM ? mg_uniform(s_ticket) : s_ticket;
+  const unsigned e = UNIFORM ? mg_uniform(s_epoch) : s_epoch;
   while (t < chunks) {
     unsigned next = 0u;
     if (threadIdx.x == 0) next = mg_next_ticket(header, e, chunks);
@@ -146,7 +159,7 @@ __device__ __forceinline__ void mg_persistent(unsigned* header, unsigned chunks,
     __syncthreads();  // every thread has read s_ticket and finished the body
     if (threadIdx.x == 0) s_ticket = next;
     __syncthreads();
-    t = s_ticket;
+    t = UNIFORM ? mg_uniform(s_ticket) : s_ticket;
   }
 }
 
@@ -222,3 +235,45 @@ __device__ __forceinline__ float mg_ld_stream(const float* p) { return __builtin
 __device__ __forceinline__ void mg_st_stream(float* p, float x) { __builtin_nontemporal_store(x, p); }
 
 static inline size_t mg_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// x of the lane N places further along this lane's DPP row of 16 lanes, cyclically
+// (DPP row_ror:N, a VALU operand modifier: no LDS crossbar round trip).
+template <int N>
+__device__ __forceinline__ float mg_row_ror(float x) {
+  static_assert(N >= 1 && N <= 15, "row_ror takes 1..15");
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// x + x of lane ^ 16 (S = 16) or lane ^ 32 (S = 32), in every lane, by gfx950's
+// v_permlane16_swap / v_permlane32_swap of x with itself: one copy ends up with the
+// lower rows (halves) of each pair, the other with the upper ones, so their sum is
+// the pair's sum in every lane, whichever copy the builtin returns first.
+template <int S>
+__device__ __forceinline__ float mg_pair_sum(float x) {
+  static_assert(S == 16 || S == 32, "row pairs (16) or wave halves (32)");
+  const unsigned u = __float_as_uint(x);
+  if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// Sum of x over each group of N consecutive lanes (N = 16, 32 or 64), in every lane
+// of the group; the whole wave must be active.  Rotations by 8, 4, 2, 1 within a
+// row leave every lane of it the row's total; wider groups add the other rows'
+// totals by lane swaps.  No LDS crossbar is used, and the association is fixed, so
+// results are reproducible.
+template <int N>
+__device__ __forceinline__ float mg_group_sum(float x) {
+  static_assert(N == 16 || N == 32 || N == 64, "groups of 16, 32 or 64 lanes");
+  x += mg_row_ror<8>(x);
+  x += mg_row_ror<4>(x);
+  x += mg_row_ror<2>(x);
+  x += mg_row_ror<1>(x);
+  if constexpr (N >= 32) x = mg_pair_sum<16>(x);
+  if constexpr (N >= 64) x = mg_pair_sum<32>(x);
+  return x;
+}

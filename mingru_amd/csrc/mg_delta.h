@@ -314,9 +314,7 @@ __device__ __forceinline__ void build_L(const float* sK, const float* sb, float*
 // written to s[col]; every (slot, column) is written by exactly one lane, so the
 // final reduction order is fixed and the result bitwise reproducible.
 __device__ __forceinline__ void put_colsum(floatx4 v, float* s, int col) {
-  float p = v[0] + v[1] + v[2] + v[3];
-  p += __shfl_xor(p, 16);
-  p += __shfl_xor(p, 32);
+  const float p = mg_pair_sum<32>(mg_pair_sum<16>(v[0] + v[1] + v[2] + v[3]));
   if (lane_id() < 16) s[col] = p;
 }
 

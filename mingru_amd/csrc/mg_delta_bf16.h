@@ -188,9 +188,7 @@ __device__ __forceinline__ void zero2(floatx4 (&acc)[2]) { acc[0] = acc[1] = zer
 // Column sums of the wave's tile jj (over its 16 rows) into s[col]: each
 // (slot, column) is written by one lane, so reductions stay in a fixed order.
 __device__ __forceinline__ void colsum16(floatx4 v, float* s, int col) {
-  float p = v[0] + v[1] + v[2] + v[3];
-  p += __shfl_xor(p, 16);
-  p += __shfl_xor(p, 32);
+  const float p = mg_pair_sum<32>(mg_pair_sum<16>(v[0] + v[1] + v[2] + v[3]));
   if (lane_id() < 16) s[col] = p;
 }
 
@@ -1083,8 +1081,7 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       for (int v = 0; v < 2; ++v)
         part += tn2.f[v].x * th.f[v].x + tn2.f[v].y * th.f[v].y + tn2.f[v].z * th.f[v].z +
                 tn2.f[v].w * th.f[v].w;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+      part = mg_group_sum<64>(part);
       if (lane == 0) sred[wave_id()] = part;
     }
     __syncthreads();
@@ -1176,13 +1173,8 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
         a = fmaf(bget(sQt, d, row), dq[jj][i], a);
         b = fmaf(bget(sK, row, d), dk[jj][i], b);
       }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        a += __shfl_xor(a, o);
-        b += __shfl_xor(b, o);
-      }
-      fq[i] = a;
-      fpv[i] = b;
+      fq[i] = mg_group_sum<16>(a);  // over the 16 lanes r of this row group
+      fpv[i] = mg_group_sum<16>(b);
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         dq[jj][i] *= spt[row];
@@ -1226,11 +1218,8 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       const float sc = GATED ? sab[m] : sb[m];
       dk[0][i] += sc * bu2[0][i];
       dk[1][i] += sc * bu2[1][i];
-      rowp[i] = bget(sK, m, C0 + r) * bu2[0][i] + bget(sK, m, C0 + 16 + r) * bu2[1][i];
-      rowp[i] += __shfl_xor(rowp[i], 1);
-      rowp[i] += __shfl_xor(rowp[i], 2);
-      rowp[i] += __shfl_xor(rowp[i], 4);
-      rowp[i] += __shfl_xor(rowp[i], 8);
+      rowp[i] = mg_group_sum<16>(bget(sK, m, C0 + r) * bu2[0][i] +
+                                 bget(sK, m, C0 + 16 + r) * bu2[1][i]);
     }
     store_block_bf16(dK + row0 * g.dk, g.dk, dk, R0, C0, ch.M, g.dk);
     if (r == 0) {

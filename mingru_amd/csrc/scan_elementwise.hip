@@ -568,14 +568,15 @@ struct EwThread {
 // The thread's chunk, lane group and columns for ticket `ticket` of the launch:
 // the (lane group, chunk) pair ticket % n_lg, ticket / n_lg (chunks from the end
 // for a REVERSE scan).
-template <int VEC, bool REVERSE>
+// UNI: the wave index is marked wave-uniform as well (see mg_persistent's UNIFORM).
+template <int VEC, bool REVERSE, bool UNI = false>
 __device__ __forceinline__ EwThread ew_thread_at(const EwGeom& g, unsigned ticket,
                                                  unsigned long long epoch) {
   EwThread th;
   th.valid = true;
   th.epoch = epoch;
   th.lane = threadIdx.x & (MG_WAVE - 1);
-  th.w = threadIdx.x / MG_WAVE;
+  th.w = UNI ? (int)mg_uniform(threadIdx.x / MG_WAVE) : (int)(threadIdx.x / MG_WAVE);
   int k = (int)(ticket / (unsigned)g.n_lg);
   th.lg = (int)(ticket - (unsigned)k * (unsigned)g.n_lg);
   th.c = REVERSE ? g.n_chunks - 1 - k : k;
@@ -590,10 +591,10 @@ __device__ __forceinline__ EwThread ew_thread_at(const EwGeom& g, unsigned ticke
 // (PH = EW_LOOKBACK) a persistent workgroup takes tickets until they run out
 // (mg_persistent); the two-launch forms take one chunk per workgroup, in
 // workgroup order, since no workgroup waits on another.
-template <int PH, typename Body>
+template <int PH, bool UNI = false, typename Body>
 __device__ __forceinline__ void ew_chunks(const EwGeom& g, unsigned* header, Body&& body) {
   if constexpr (PH == EW_LOOKBACK) {
-    mg_persistent(header, (unsigned)g.n_lg * (unsigned)g.n_chunks, body);
+    mg_persistent<UNI>(header, (unsigned)g.n_lg * (unsigned)g.n_chunks, body);
   } else {
     body(blockIdx.x, PH == EW_AGG ? ew_agg_begin(header) : 0ull);
   }
@@ -727,8 +728,9 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void linear_bwd_kernel(
     float* __restrict__ da, float* __restrict__ db, EwGeom g, unsigned* header,
     mg_slot_t* agg_data, mg_slot_t* incl_data) {
   constexpr bool NT = PH != EW_REDUCE;
-  ew_chunks<PH>(g, header, [&](unsigned ticket, unsigned long long epoch) {
-    EwThread th = ew_thread_at<VEC, true>(g, ticket, epoch);
+  // Uniform tickets: without them this kernel spills 38 registers at the cap.
+  ew_chunks<PH, true>(g, header, [&](unsigned ticket, unsigned long long epoch) {
+    EwThread th = ew_thread_at<VEC, true, true>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
 
@@ -1332,8 +1334,7 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
       if constexpr (DEC) {
         if (dec.ddt != nullptr) {
           // Sum over each 64-column tile: the 64 / VEC lanes that hold it.
-#pragma unroll
-          for (int m = 1; m < MG_WAVE / VEC; m *= 2) cdt += __shfl_xor(cdt, m);
+          cdt = mg_group_sum<MG_WAVE / VEC>(cdt);
           const int64_t tile = th.col / MG_WAVE;
           if ((th.lane & (MG_WAVE / VEC - 1)) == 0 && th.col < D && t < T)
             dec.ddt[(tile * (int64_t)(g.n_lg / g.n_tiles) + th.bb) * T + t] =

@@ -18,7 +18,8 @@ Usage (on the directories the rocprofv3 runs wrote)::
   kernel (average per dispatch).
 * ``--valu``: a ``--pmc`` directory with ``SQ_INSTS_VALU``; adds each call's VALU issue
   floor (``valu`` lines, read by ``bench.py``).
-* ``--bench``: the JSON line ``bench.py`` printed, for the HIP-event timings.
+* ``--bench``: the JSON line an unprofiled ``bench.py`` run printed, for the HIP-event
+  timings and the step time (rocprofv3's own tracing adds to the step).
 
 Kernels are attributed to C-ABI entry points by name (``ENTRIES``), independent of
 tile-size template arguments; an entry point with no matching dispatch is an error,
@@ -40,20 +41,29 @@ import statistics
 ENTRIES = {
     "C2": [("mg_linear_scan_fwd", r"\bew_fwd_kernel<"),
            ("mg_linear_scan_bwd", r"\blinear_bwd_kernel<")],
-    # gate kernels: <columns per lane, steps per wave, waves, gate kind[, launch form]>
-    "C2g": [("mg_signed_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, [01](, \d)?>"),
-            ("mg_signed_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, [01](, \d)?>")],
-    "C1g": [("mg_mingru_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, 2(, \d)?>"),
-            ("mg_mingru_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, 2(, \d)?>")],
+    # gate kernels: <columns per lane, steps per wave, waves, gate kind, decay[, launch form]>
+    "C2g": [("mg_signed_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, [01], false(, \d)?>"),
+            ("mg_signed_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, [01], false(, \d)?>")],
+    "C2gd": [("mg_signed_gate_scan_decay_fwd",
+              r"\bgate_fwd_kernel<\d+, \d+, \d+, [01], true(, \d)?>"),
+             ("mg_signed_gate_scan_decay_bwd",
+              r"\bgate_bwd_kernel<\d+, \d+, \d+, [01], true(, \d)?>")],
+    "C1g": [("mg_mingru_gate_scan_fwd", r"\bgate_fwd_kernel<\d+, \d+, \d+, 2, false(, \d)?>"),
+            ("mg_mingru_gate_scan_bwd", r"\bgate_bwd_kernel<\d+, \d+, \d+, 2, false(, \d)?>")],
     "C1": [("mg_log_scan_fwd", r"\blog_fwd_kernel<"), ("mg_log_scan_bwd", r"\blog_bwd_kernel<")],
     "C3": [("mg_affine_scan_fwd", r"\baffine_fwd_kernel<2, 1,"),
            ("mg_affine_scan_bwd", r"\baffine_bwd_kernel<2, 1,")],
     "C4": [("mg_angle_scan_fwd", r"\bangle_fwd_\w+<|\bangle_group_\w+<\d+, false>"),
            ("mg_angle_scan_bwd",
             r"\bangle_bwd_\w+<|\bangle_group_\w+<\d+, true>|\bangle_group_offsets<")],
+    # brick-wall schedule with the gated heads: pass kernels <K, schedule, scale, decay, gated>
+    "C4g": [("mg_angle_scan_gated_fwd", r"\bangle_fwd_\w+<"),
+            ("mg_angle_scan_gated_bwd", r"\bangle_bwd_\w+<")],
     "C5": [("mg_delta_fwd", r"\bdwb_fwd_\w+<false>"), ("mg_delta_bwd", r"\bdwb_bwd_\w+<false>")],
     "C5d": [("mg_delta_gated_fwd", r"\bdwb_fwd_\w+<true>"),
             ("mg_delta_gated_bwd", r"\bdwb_bwd_\w+<true>")],
+    "C5dp": [("mg_delta_gated_fwd", r"\bdwb_fwd_\w+<true>"),
+             ("mg_delta_gated_bwd", r"\bdwb_bwd_\w+<true>")],
 }
 
 COPY_PROBE_BYTES = 1 << 30  # bench.py --copy-probe: one 1 GiB device-to-device copy
@@ -194,6 +204,8 @@ def summarize(args) -> str:
     for name, calls, avg, lo, hi, pct in kernel_stats(args.stats):
         L.append(f"| `{name}` | {calls} | {avg:.2f} | {lo:.2f} | {hi:.2f} | {pct:.1f}% |")
     L += ["", "## HIP-event timing in `bench.py` (per C-ABI call)", "",
+          "From an unprofiled `bench.py` run (the first command above), not from the rocprofv3 "
+          "runs.", "",
           "| entry point | avg µs | algorithmic bytes | achieved GB/s |", "|---|---:|---:|---:|"]
     for e, k in ops.get("kernels", {}).items():
         L.append(f"| `{e}` | {k['avg_us']:.1f} | {k['algorithmic_bytes']:,} | "

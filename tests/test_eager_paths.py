@@ -107,17 +107,21 @@ def test_profile_summary_attributes_traffic(tmp_path):
 
 def test_profile_entry_patterns_split_angle_walk_kernels():
     """The angle scan's walk kernels are attributed by their direction argument, and the
-    gate kernels by their gate kind whatever their launch form."""
+    gate kernels by their gate kind and decay flag whatever their launch form."""
     import re
 
     sfwd, sbwd = (p for _, p in profiling.ENTRIES["C2g"])
+    dfwd, dbwd = (p for _, p in profiling.ENTRIES["C2gd"])
     mfwd, mbwd = (p for _, p in profiling.ENTRIES["C1g"])
-    for name, pat, others in (("gate_fwd_kernel<4, 16, 8, 0>", sfwd, (sbwd, mfwd, mbwd)),
-                              ("gate_fwd_kernel<4, 16, 8, 1, 2>", sfwd, (sbwd, mfwd, mbwd)),
-                              ("gate_bwd_kernel<1, 4, 8, 0, 1>", sbwd, (sfwd, mfwd, mbwd)),
-                              ("gate_fwd_kernel<1, 8, 8, 2, 1>", mfwd, (sfwd, sbwd, mbwd)),
-                              ("gate_bwd_kernel<4, 4, 8, 2>", mbwd, (sfwd, sbwd, mfwd))):
-        assert re.search(pat, name) and not any(re.search(o, name) for o in others), name
+    pats = (sfwd, sbwd, dfwd, dbwd, mfwd, mbwd)
+    for name, pat in (("gate_fwd_kernel<4, 16, 8, 0, false>", sfwd),
+                      ("gate_fwd_kernel<4, 16, 8, 1, false, 2>", sfwd),
+                      ("gate_bwd_kernel<1, 4, 8, 0, false, 1>", sbwd),
+                      ("gate_fwd_kernel<4, 16, 8, 1, true, 3>", dfwd),
+                      ("gate_bwd_kernel<2, 4, 8, 0, true>", dbwd),
+                      ("gate_fwd_kernel<1, 8, 8, 2, false, 1>", mfwd),
+                      ("gate_bwd_kernel<4, 4, 8, 2, false>", mbwd)):
+        assert [bool(re.search(p, name)) for p in pats] == [p is pat for p in pats], name
 
     fwd, bwd = (p for _, p in profiling.ENTRIES["C4"])
     for name in ("angle_fwd_reduce<8, 1, false, true>", "angle_fwd_scan<8>",
