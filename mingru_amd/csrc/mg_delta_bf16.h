@@ -100,15 +100,32 @@ __device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (
 
 // Accumulator tile (lane (g, r) holds rows R0+4g..R0+4g+3 of column C0+r) into
 // a split BMat, either as (row = tile row, k = tile column) or transposed
-// (row = tile column, k = tile row; four consecutive k per lane).
+// (row = tile column, k = tile row).
 __device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) put_split1(m, R0 + 4 * g + i, C0 + r, a[i]);
 }
+// Transposed: lane (g, r) holds k = R0+4g..R0+4g+3 of row C0+r, half of a 16-byte
+// chunk.  The lane rows g and g^1 (lanes 16 apart) swap halves with
+// v_permlane16_swap: afterwards an even-g lane holds the chunk's 8 hi values and the
+// odd-g lane beside it the 8 lo values, so each lane makes one 16-byte store, and a
+// group of 8 lanes stores 8 consecutive rows, which the swizzle puts in 8 distinct
+// bank groups.  (Four 8-byte stores per lane pair of 16 rows put two rows on each
+// bank group.)  The whole wave must be active; R0 is a multiple of 8.
 __device__ __forceinline__ void acc_put_t(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
-  put_split4(m, C0 + r, R0 + 4 * g, a[0], a[1], a[2], a[3]);
+  u16 h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bf_split(a[i], h[i], l[i]);
+  const unsigned hx = h[0] | ((unsigned)h[1] << 16), hy = h[2] | ((unsigned)h[3] << 16);
+  const unsigned lx = l[0] | ((unsigned)l[1] << 16), ly = l[2] | ((unsigned)l[3] << 16);
+  // [0]: even lane rows keep their own (hi) words and odd ones receive the even
+  // partner's lo words; [1]: even rows receive the odd partner's hi words, odd rows
+  // keep their own lo words.
+  const auto sx = __builtin_amdgcn_permlane16_swap(hx, lx, false, false);
+  const auto sy = __builtin_amdgcn_permlane16_swap(hy, ly, false, false);
+  m[g & 1].v[bpos(C0 + r, (R0 >> 3) + (g >> 1))] = make_uint4(sx[0], sy[0], sx[1], sy[1]);
 }
 
 __device__ __forceinline__ bf16x8 bneg(bf16x8 x) {
