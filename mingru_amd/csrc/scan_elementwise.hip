@@ -1096,6 +1096,34 @@ struct GateDecay {
 
 constexpr float GATE_LOG2E = 1.44269504088896341f;
 
+// -lam log2(e) for the thread's VEC columns: one vector load where all of them exist
+// and the address allows it (a caller's pointer may have any alignment).
+template <int VEC>
+__device__ __forceinline__ void decay_rates(float (&nlam)[VEC], const float* lam, int64_t col,
+                                            int64_t D) {
+  if (col + VEC <= D && ((uintptr_t)(lam + col) & (sizeof(float) * VEC - 1)) == 0) {
+    load_vec<VEC, false>(nlam, lam + col);
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) nlam[v] = col + v < D ? lam[col + v] : 0.f;
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) nlam[v] *= -GATE_LOG2E;
+}
+
+// dt[row + s] for a wave's TSUB steps (0 from step n on), the same in every lane:
+// lane s loads step s, and each step's value is read back from its lane, one
+// vector load per wave instead of one per step.
+template <int TSUB>
+__device__ __forceinline__ void decay_gaps(float (&dts)[TSUB], const float* dt, int64_t row,
+                                           int64_t n, int lane) {
+  static_assert(TSUB <= MG_WAVE, "one lane per step");
+  const float mine = lane < TSUB && lane < n ? dt[row + lane] : 0.f;
+#pragma unroll
+  for (int s = 0; s < TSUB; ++s)
+    dts[s] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), s));
+}
+
 template <int VEC, int TSUB, int WAVES, int G, bool DEC, int PH = EW_LOOKBACK>
 __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     const float* __restrict__ p0, const float* __restrict__ p1, const float* __restrict__ p2,
@@ -1106,10 +1134,11 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
     EwThread th = ew_thread_at<VEC, false>(g, ticket, epoch);
     const int64_t t0 = (int64_t)th.c * (WAVES * TSUB) + th.w * TSUB;
     const int64_t T = g.T, D = g.D;
-    float nlam[VEC];  // -lam log2(e) per column
-#pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      nlam[v] = DEC && th.col_ok && th.col + v < D ? -GATE_LOG2E * dec.lam[th.col + v] : 0.f;
+    float nlam[VEC], dts[TSUB];  // -lam log2(e) per column, dt per step
+    if constexpr (DEC) {
+      decay_rates<VEC>(nlam, dec.lam, th.col, D);
+      decay_gaps<TSUB>(dts, dec.dt, th.bb * T + t0, T - t0, th.lane);
+    }
 
     float av[TSUB][VEC], bv[TSUB][VEC];
 #pragma unroll
@@ -1121,11 +1150,10 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_fwd_kernel(
         load_vec<VEC, NT>(x0, p0 + off);
         load_vec<VEC, NT>(x1, p1 + off);
         if constexpr (gate_inputs<G>() == 3) load_vec<VEC, NT>(x2, p2 + off);
-        const float dtv = DEC ? dec.dt[th.bb * T + t] : 0.f;
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           gate_coeffs<G>(x0[v], x1[v], gate_inputs<G>() == 3 ? x2[v] : 0.f, av[s][v], bv[s][v]);
-          if constexpr (DEC) av[s][v] *= __builtin_amdgcn_exp2f(nlam[v] * dtv);
+          if constexpr (DEC) av[s][v] *= __builtin_amdgcn_exp2f(nlam[v] * dts[s]);
         }
       } else {
 #pragma unroll
@@ -1189,11 +1217,15 @@ __global__ __launch_bounds__(MG_WAVE* WAVES) void gate_bwd_kernel(
     constexpr bool NT = PH != EW_REDUCE;
     // Decay: -lam log2(e) per column and dt per step (one value per wave and step).
     float nlam[VEC], dts[TSUB];
+    if constexpr (DEC) {
+      decay_rates<VEC>(nlam, dec.lam, th.col, D);
+      decay_gaps<TSUB>(dts, dec.dt, th.bb * T + t0, T - t0, th.lane);
+    } else {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      nlam[v] = DEC && th.col_ok && th.col + v < D ? -GATE_LOG2E * dec.lam[th.col + v] : 0.f;
+      for (int v = 0; v < VEC; ++v) nlam[v] = 0.f;
 #pragma unroll
-    for (int s = 0; s < TSUB; ++s) dts[s] = DEC && t0 + s < T ? dec.dt[th.bb * T + t0 + s] : 0.f;
+      for (int s = 0; s < TSUB; ++s) dts[s] = 0.f;
+    }
     auto gam = [&](int s, int v) {
       return DEC ? __builtin_amdgcn_exp2f(nlam[v] * dts[s]) : 1.f;
     };
