@@ -383,6 +383,36 @@ __device__ __forceinline__ void an_store_db(const AnArgs& a, int64_t lane_tok,
   }
 }
 
+// an_input and an_store_db with the token's z, hpre (gated) or b already in registers.
+template <int K, bool GP>
+__device__ __forceinline__ void an_input_reg(const float (&v)[K], const float (&hq)[GP ? K : 1],
+                                             float (&bt)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    if constexpr (GP) bt[i] = mg_sigmoid(v[i]) * hq[i];
+    else bt[i] = v[i];
+  }
+}
+
+template <int K, bool GP>
+__device__ __forceinline__ void an_store_db_reg(const AnArgs& a, int64_t lane_tok,
+                                                const float (&gt)[K], const float (&zz)[GP ? K : 1],
+                                                const float (&hp)[GP ? K : 1]) {
+  if constexpr (GP) {
+    float dz[K], dh[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float sg = mg_sigmoid(zz[i]);
+      dh[i] = gt[i] * sg;
+      dz[i] = dh[i] * hp[i] * (1.f - sg);
+    }
+    st<K>(a.out + lane_tok * K, dz);
+    st<K>(a.dhpre + lane_tok * K, dh);
+  } else {
+    st<K>(a.out + lane_tok * K, gt);
+  }
+}
+
 // Per-token inputs of the lexicographic kernels, loaded one token ahead: at one
 // wave per SIMD nothing else hides a load issued only when it is needed.
 template <int K, bool HS, bool HD>
@@ -406,6 +436,87 @@ struct LexTok {
     }
   }
 };
+
+// Per-token inputs of the brick-wall kernels with R rounds fixed at compile time (the
+// mixers' R = 3, and RotationMinGRU's R = 1), loaded one token ahead as LexTok's are;
+// other round counts take the per-token loop.  v: b_t, or z_t under the gated
+// prologue (forward), or g_t (backward); hq: the gated prologue's hpre_t; zb: z_t in
+// the gated backward final pass; hp: h_{t-1} (backward final pass).
+template <int K, int R, bool HS, bool HD, bool HQ, bool ZB, bool HP>
+struct BrickTok {
+  static constexpr int H = K / 2;
+  float ang[R][H];
+  float v[K];
+  float hq[HQ ? K : 1];
+  float zb[ZB ? K : 1];
+  float hp[HP ? K : 1];
+  float d, gm;  // the scale input (u under the gated prologue) and the decay
+
+  __device__ __forceinline__ void load(const AnArgs& a, const float* vec, int64_t lane_tok,
+                                       int64_t t, int64_t n, int64_t blk) {
+    const float* th = a.theta + lane_tok * (R * H);
+#pragma unroll
+    for (int r = 0; r < R; ++r) ld<H>(ang[r], th + r * H);
+    ld<K>(v, vec + lane_tok * K);
+    if constexpr (HQ) ld<K>(hq, a.hpre + lane_tok * K);
+    if constexpr (ZB) ld<K>(zb, a.b + lane_tok * K);
+    d = HS ? a.scale[lane_tok] : 1.f;
+    gm = HD ? a.gamma[lane_tok] : 1.f;
+    if constexpr (HP) {
+      if (t > 0) ld<K>(hp, a.h + lane_tok * K - n * K);
+      else ld<K>(hp, a.h0 + blk * K);
+    }
+  }
+};
+
+// The R brick-wall rounds of a token with its angles in registers: rounds 0 .. R-1,
+// or (TRANSPOSE) their transposes from R-1 down to 0.
+template <int K, int NC, bool TRANSPOSE, int R>
+__device__ __forceinline__ void brick_rounds_reg(float (&X)[K][NC], const float (&ang)[R][K / 2]) {
+  constexpr int H = K / 2;
+  static_for(
+      [&](auto rc) {
+        constexpr int r = TRANSPOSE ? R - 1 - decltype(rc)::value : decltype(rc)::value;
+        float cs[H], sn[H];
+#pragma unroll
+        for (int m = 0; m < H; ++m) mg_sincos(ang[r][m], sn[m], cs[m]);
+        brick_planes<K, NC, TRANSPOSE, r & 1>(X, cs, sn, std::make_integer_sequence<int, H>{});
+      },
+      std::make_index_sequence<R>{});
+}
+
+// X <- M_t X and X <- M_t^T X (apply_M / apply_Mt) with the angles in registers.
+template <int K, int R, bool HS, bool HD, int NC>
+__device__ __forceinline__ void apply_M_brick(float (&X)[K][NC], const float (&ang)[R][K / 2],
+                                              float d, float gm) {
+  if (HS) {
+#pragma unroll
+    for (int q = 0; q < NC; ++q) X[1][q] *= d;
+  }
+  brick_rounds_reg<K, NC, false, R>(X, ang);
+  if (HD) {
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int q = 0; q < NC; ++q) X[i][q] *= gm;
+  }
+}
+
+template <int K, int R, bool HS, bool HD, int NC>
+__device__ __forceinline__ void apply_Mt_brick(float (&X)[K][NC], const float (&ang)[R][K / 2],
+                                               float d, float gm) {
+  if (HD) {
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+      for (int q = 0; q < NC; ++q) X[i][q] *= gm;
+  }
+  brick_rounds_reg<K, NC, true, R>(X, ang);
+  if (HS) {
+#pragma unroll
+    for (int q = 0; q < NC; ++q) X[1][q] *= d;
+  }
+}
 
 // Runs body(tok, t) over `count` tokens t = first, first + dir, ..., each token's
 // inputs loaded one token ahead into two alternating buffers.  The next token's
@@ -587,17 +698,40 @@ __global__ __launch_bounds__(AN_RED_THREADS) void angle_fwd_reduce(AnArgs a, AnG
                 X[i][K] = HD ? fmaf(cur.gm, X[i][K], cur.v[i]) : X[i][K] + cur.v[i];
             });
       } else {
-        for (int64_t t = t0; t < te; ++t) {
-          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-          const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
-          const float gm = HD ? a.gamma[lane_tok] : 1.f;
-          apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
-          if (HD) gprod *= gm;
-          float bt[K];
-          an_input<K, GP>(a, lane_tok, bt);
+        brick_dispatch(a.rounds, [&](auto rc) {
+          constexpr int R = decltype(rc)::value;
+          if constexpr (R > 0) {
+            using Tok = BrickTok<K, R, HS, HD, GP, false, false>;
+            token_pairs<Tok>(
+                t0, (int)(te - t0), 1,
+                [&](Tok& k, int64_t t) {
+                  k.load(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+                },
+                [&](const Tok& cur, int64_t) {
+                  const float d = HS ? (GP ? mg_tanh(cur.d) : cur.d) : 1.f;
+                  apply_M_brick<K, R, HS, false, K + 1>(X, cur.ang, d, 1.f);
+                  if (HD) gprod *= cur.gm;
+                  float bt[K];
+                  an_input_reg<K, GP>(cur.v, cur.hq, bt);
 #pragma unroll
-          for (int i = 0; i < K; ++i) X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
-        }
+                  for (int i = 0; i < K; ++i)
+                    X[i][K] = HD ? fmaf(cur.gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+                });
+          } else {
+            for (int64_t t = t0; t < te; ++t) {
+              const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+              const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
+              const float gm = HD ? a.gamma[lane_tok] : 1.f;
+              apply_M<K, SCHED, HS, false, K + 1>(X, a.theta + lane_tok * a.na, a.rounds, d, 1.f);
+              if (HD) gprod *= gm;
+              float bt[K];
+              an_input<K, GP>(a, lane_tok, bt);
+#pragma unroll
+              for (int i = 0; i < K; ++i)
+                X[i][K] = HD ? fmaf(gm, X[i][K], bt[i]) : X[i][K] + bt[i];
+            }
+          }
+        });
       }
     }
   }
@@ -858,20 +992,45 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_fwd_final(AnArgs a, A
           st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
         });
   } else {
-    for (int64_t t = t0; t < te; ++t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
-      const float gm = HD ? a.gamma[lane_tok] : 1.f;
-      apply_M<K, SCHED, HS, HD, 1>(v, a.theta + lane_tok * a.na, a.rounds, d, gm);
-      float bt[K];
-      an_input<K, GP>(a, lane_tok, bt);
+    brick_dispatch(a.rounds, [&](auto rc) {
+      constexpr int R = decltype(rc)::value;
+      if constexpr (R > 0) {
+        using Tok = BrickTok<K, R, HS, HD, GP, false, false>;
+        token_pairs<Tok>(
+            t0, (int)(te - t0), 1,
+            [&](Tok& k, int64_t t) {
+              k.load(a, a.b, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+            },
+            [&](const Tok& cur, int64_t t) {
+              const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+              const float d = HS ? (GP ? mg_tanh(cur.d) : cur.d) : 1.f;
+              apply_M_brick<K, R, HS, HD, 1>(v, cur.ang, d, cur.gm);
+              float bt[K];
+              an_input_reg<K, GP>(cur.v, cur.hq, bt);
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        v[i][0] += bt[i];
-        bt[i] = v[i][0];
+              for (int i = 0; i < K; ++i) {
+                v[i][0] += bt[i];
+                bt[i] = v[i][0];
+              }
+              st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
+            });
+      } else {
+        for (int64_t t = t0; t < te; ++t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
+          const float gm = HD ? a.gamma[lane_tok] : 1.f;
+          apply_M<K, SCHED, HS, HD, 1>(v, a.theta + lane_tok * a.na, a.rounds, d, gm);
+          float bt[K];
+          an_input<K, GP>(a, lane_tok, bt);
+#pragma unroll
+          for (int i = 0; i < K; ++i) {
+            v[i][0] += bt[i];
+            bt[i] = v[i][0];
+          }
+          st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
+        }
       }
-      st<K>(a.out + lane_tok * K, bt);  // k floats per lane: L2 merges the rows
-    }
+    });
   }
 }
 
@@ -994,6 +1153,67 @@ __device__ __forceinline__ void token_grad(float (&x)[K][1], const float (&hp)[K
   }
 }
 
+// token_grad for the brick-wall schedule with the R rounds' angles in registers: each
+// angle's sin and cos are evaluated once for both sweeps, and dtheta is returned in gr
+// (round-major, as the angles are stored).
+template <int K, int R, bool HS, bool HD>
+__device__ __forceinline__ void token_grad_brick(float (&x)[K][1], const float (&hp)[K],
+                                                 const float (&ang)[R][K / 2],
+                                                 float (&gr)[R * (K / 2)], float d, float gm,
+                                                 float& dd, float& dg) {
+  constexpr int H = K / 2;
+  float v[K][1];
+#pragma unroll
+  for (int i = 0; i < K; ++i) v[i][0] = hp[i];
+  if (HS) v[1][0] *= d;
+  float cs[R][H], sn[R][H];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < H; ++m) mg_sincos(ang[r][m], sn[r][m], cs[r][m]);
+  static_for(
+      [&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        brick_planes<K, 1, false, r & 1>(v, cs[r], sn[r], std::make_integer_sequence<int, H>{});
+      },
+      std::make_index_sequence<R>{});
+  if (HD) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) acc = fmaf(x[i][0], v[i][0], acc);
+    dg = acc;
+#pragma unroll
+    for (int i = 0; i < K; ++i) x[i][0] *= gm;
+  }
+  static_for(
+      [&](auto rc) {
+        constexpr int r = R - 1 - decltype(rc)::value;
+        static_for(
+            [&](auto mc) {
+              constexpr int m = decltype(mc)::value;
+              constexpr int I = 2 * m + (r & 1), J = (I + 1) % K;
+              gr[r * H + m] = rot_grad<K, I, J>(v, x, cs[r][m], sn[r][m]);
+            },
+            std::make_index_sequence<H>{});
+      },
+      std::make_index_sequence<R>{});
+  if (HS) {
+    dd = x[1][0] * hp[1];
+    x[1][0] *= d;
+  }
+}
+
+// Runs f with the brick-wall round count as a compile-time constant where a
+// prefetching token loop exists for it (the mixers' 3 rounds, RotationMinGRU's 1),
+// else with 0 (the per-token loop that reads any number of rounds).
+constexpr int AN_BRICK_TOK_RMAX = 3;
+template <typename F>
+__device__ __forceinline__ void brick_dispatch(int rounds, F&& f) {
+  if (rounds == 3) f(std::integral_constant<int, 3>{});
+  else if (rounds == 1) f(std::integral_constant<int, 1>{});
+  else f(std::integral_constant<int, 0>{});
+}
+
 // ---- backward pass 1: adjoint offsets of each chunk ---------------------------
 // The adjoint flowing out of chunk c to the left is y_out = P_c^T y_in + Lb_c,
 // with y_in the adjoint flowing in from the right, P_c the forward chunk
@@ -1022,16 +1242,34 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_reduce(AnArgs a, 
           apply_Mt_lex<K, HS, HD, 1>(x, cur.ang, cur.d, cur.gm);
         });
   } else {
-    for (int64_t t = te - 1; t >= t0; --t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
-      const float gm = HD ? a.gamma[lane_tok] : 1.f;
-      float gt[K];
-      ld<K>(gt, a.gh + lane_tok * K);
+    brick_dispatch(a.rounds, [&](auto rc) {
+      constexpr int R = decltype(rc)::value;
+      if constexpr (R > 0) {
+        using Tok = BrickTok<K, R, HS, HD, false, false, false>;
+        token_pairs<Tok>(
+            te - 1, (int)(te - t0), -1,
+            [&](Tok& k, int64_t t) {
+              k.load(a, a.gh, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+            },
+            [&](const Tok& cur, int64_t) {
+              const float d = HS ? (GP ? mg_tanh(cur.d) : cur.d) : 1.f;
 #pragma unroll
-      for (int i = 0; i < K; ++i) x[i][0] += gt[i];
-      apply_Mt<K, SCHED, HS, HD, 1>(x, a.theta + lane_tok * a.na, a.rounds, d, gm);
-    }
+              for (int i = 0; i < K; ++i) x[i][0] += cur.v[i];
+              apply_Mt_brick<K, R, HS, HD, 1>(x, cur.ang, d, cur.gm);
+            });
+      } else {
+        for (int64_t t = te - 1; t >= t0; --t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
+          const float gm = HD ? a.gamma[lane_tok] : 1.f;
+          float gt[K];
+          ld<K>(gt, a.gh + lane_tok * K);
+#pragma unroll
+          for (int i = 0; i < K; ++i) x[i][0] += gt[i];
+          apply_Mt<K, SCHED, HS, HD, 1>(x, a.theta + lane_tok * a.na, a.rounds, d, gm);
+        }
+      }
+    });
   }
   float xf[K];
 #pragma unroll
@@ -1346,26 +1584,67 @@ __global__ __launch_bounds__(MG_WAVE* AN_WAVES) void angle_bwd_final(AnArgs a, A
           if (HD) a.dgamma[lane_tok] = dg;
         });
   } else {
-    for (int64_t t = te - 1; t >= t0; --t) {
-      const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
-      const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
-      const float gm = HD ? a.gamma[lane_tok] : 1.f;
-      float gt[K], hp[K];
-      ld<K>(gt, a.gh + lane_tok * K);
-      if (t > 0) ld<K>(hp, a.h + lane_tok * K - g.n * K);
-      else ld<K>(hp, a.h0 + th.blk * K);
+    // dtheta rows of the prefetching form (R K/2 floats per lane) leave through LDS as
+    // whole lines when they are whole 16-byte pieces and the wave is complete.
+    constexpr int BR = AN_BRICK_TOK_RMAX * (K / 2);
+    __shared__ __attribute__((aligned(16))) float s_brows[AN_WAVES][MG_WAVE * BR];
+    const int lane = threadIdx.x & (MG_WAVE - 1);
+    const bool whole = __builtin_amdgcn_read_exec() == ~0ull;
+    float* rows = s_brows[threadIdx.x / MG_WAVE];
+    brick_dispatch(a.rounds, [&](auto rc) {
+      constexpr int R = decltype(rc)::value;
+      if constexpr (R > 0) {
+        constexpr int NA = R * (K / 2);
+        using Tok = BrickTok<K, R, HS, HD, GP, GP, true>;
+        token_pairs<Tok>(
+            te - 1, (int)(te - t0), -1,
+            [&](Tok& k, int64_t t) {
+              k.load(a, a.gh, (th.bb * g.T + t) * g.n + th.plane, t, g.n, th.blk);
+            },
+            [&](const Tok& cur, int64_t t) {
+              const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+              const float d = HS ? (GP ? mg_tanh(cur.d) : cur.d) : 1.f;
+              float gt[K];
 #pragma unroll
-      for (int i = 0; i < K; ++i) {
-        y[i][0] += gt[i];
-        gt[i] = y[i][0];
+              for (int i = 0; i < K; ++i) {
+                y[i][0] += cur.v[i];
+                gt[i] = y[i][0];
+              }
+              an_store_db_reg<K, GP>(a, lane_tok, gt, cur.zb, cur.hq);  // db_t (or dz, dhpre)
+              float dd = 0.f, dg = 0.f, gr[NA];
+              token_grad_brick<K, R, HS, HD>(y, cur.hp, cur.ang, gr, d, cur.gm, dd, dg);
+              if constexpr (NA % 4 == 0) {
+                if (whole) wave_rows_store<NA>(a.dtheta + (lane_tok - lane) * NA, gr, rows, lane);
+                else st<NA>(a.dtheta + lane_tok * NA, gr);
+              } else {
+                st<NA>(a.dtheta + lane_tok * NA, gr);  // partial-line rows: the L2 merges them
+              }
+              if (HS) a.dscale[lane_tok] = GP ? dd * (1.f - d * d) : dd;  // GP: dL/du, d = tanh(u)
+              if (HD) a.dgamma[lane_tok] = dg;
+            });
+      } else {
+        for (int64_t t = te - 1; t >= t0; --t) {
+          const int64_t lane_tok = (th.bb * g.T + t) * g.n + th.plane;
+          const float d = HS ? an_scale<GP>(a, lane_tok) : 1.f;
+          const float gm = HD ? a.gamma[lane_tok] : 1.f;
+          float gt[K], hp[K];
+          ld<K>(gt, a.gh + lane_tok * K);
+          if (t > 0) ld<K>(hp, a.h + lane_tok * K - g.n * K);
+          else ld<K>(hp, a.h0 + th.blk * K);
+#pragma unroll
+          for (int i = 0; i < K; ++i) {
+            y[i][0] += gt[i];
+            gt[i] = y[i][0];
+          }
+          an_store_db<K, GP>(a, lane_tok, gt);  // db_t = dL/dh_t (or dz, dhpre)
+          float dd = 0.f, dg = 0.f;
+          token_grad<K, SCHED, HS, HD>(y, hp, a.theta + lane_tok * a.na,
+                                       a.dtheta + lane_tok * a.na, a.rounds, d, gm, dd, dg);
+          if (HS) a.dscale[lane_tok] = GP ? dd * (1.f - d * d) : dd;  // GP: dL/du, d = tanh(u)
+          if (HD) a.dgamma[lane_tok] = dg;
+        }
       }
-      an_store_db<K, GP>(a, lane_tok, gt);  // db_t = dL/dh_t (or dz, dhpre)
-      float dd = 0.f, dg = 0.f;
-      token_grad<K, SCHED, HS, HD>(y, hp, a.theta + lane_tok * a.na, a.dtheta + lane_tok * a.na,
-                                   a.rounds, d, gm, dd, dg);
-      if (HS) a.dscale[lane_tok] = GP ? dd * (1.f - d * d) : dd;  // GP: dL/du, d = tanh(u)
-      if (HD) a.dgamma[lane_tok] = dg;
-    }
+    });
   }
 }
 
