@@ -688,14 +688,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     float acc = 0.f;
     for (int rr = 0; rr < DN / (NT / 64); ++rr) {
       const int t = (DN / (NT / 64)) * w + rr;
-      float x = sQ[t * LD + lane];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(x, d);
-        if (lane >= d) x += y;
-      }
-      float ex = __shfl_up(x, 1);
-      if (lane == 0) ex = 0.f;
+      const float ex = mg_wave_prev(mg_wave_prefix_sum(sQ[t * LD + lane]));
       if (t >= lane && t < ch.Ct) acc += sfv[3][t] + ex;
     }
     sdl[w][lane] = acc;

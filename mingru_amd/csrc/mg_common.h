@@ -277,3 +277,40 @@ __device__ __forceinline__ float mg_group_sum(float x) {
   if constexpr (N >= 64) x = mg_pair_sum<32>(x);
   return x;
 }
+
+// DPP move with the lanes whose source lies outside the pattern's range receiving 0.
+template <int CTRL>
+__device__ __forceinline__ float mg_dpp0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Inclusive prefix (lane l: x[0] + ... + x[l]) and suffix (x[l] + ... + x[63]) sums
+// over the wave without the LDS crossbar: Hillis-Steele steps of 1, 2, 4 and 8 lanes
+// within each 16-lane row (DPP row_shr / row_shl), then the other rows' totals read
+// with v_readlane.  Each lane's sum holds only its own range's terms (no difference of
+// running sums).  The whole wave must be active.
+__device__ __forceinline__ float mg_wave_prefix_sum(float x) {
+  x += mg_dpp0<0x111>(x);  // row_shr:1
+  x += mg_dpp0<0x112>(x);
+  x += mg_dpp0<0x114>(x);
+  x += mg_dpp0<0x118>(x);
+  const int row = (threadIdx.x & (MG_WAVE - 1)) >> 4;
+  const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 15));
+  const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 31));
+  const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 47));
+  return x + ((row > 0 ? t0 : 0.f) + ((row > 1 ? t1 : 0.f) + (row > 2 ? t2 : 0.f)));
+}
+__device__ __forceinline__ float mg_wave_suffix_sum(float x) {
+  x += mg_dpp0<0x101>(x);  // row_shl:1
+  x += mg_dpp0<0x102>(x);
+  x += mg_dpp0<0x104>(x);
+  x += mg_dpp0<0x108>(x);
+  const int row = (threadIdx.x & (MG_WAVE - 1)) >> 4;
+  const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return x + ((row < 1 ? t1 : 0.f) + ((row < 2 ? t2 : 0.f) + (row < 3 ? t3 : 0.f)));
+}
+// x of lane l + 1 (0 in lane 63) and of lane l - 1 (0 in lane 0): DPP wave_shl / wave_shr.
+__device__ __forceinline__ float mg_wave_next(float x) { return mg_dpp0<0x130>(x); }
+__device__ __forceinline__ float mg_wave_prev(float x) { return mg_dpp0<0x138>(x); }

@@ -341,14 +341,7 @@ __device__ __forceinline__ void decay_tables(const float* sl, float* sE) {
   const float lv = sl[lane];
   for (int rr = 0; rr < ROWS; ++rr) {
     const int t = ROWS * w + rr;
-    float x = lane <= t ? lv : 0.f;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_down(x, d);
-      if (lane + d < 64) x += y;
-    }
-    float ex = __shfl_down(x, 1);
-    if (lane == 63) ex = 0.f;
+    const float ex = mg_wave_next(mg_wave_suffix_sum(lane <= t ? lv : 0.f));
     sE[t * LDE + lane] = lane <= t ? expf(ex) : 0.f;
   }
 }
@@ -365,15 +358,8 @@ __device__ __forceinline__ void decay_vectors(const float* sl, const float* sb, 
   if (wave_id() != 0) return;
   const int lane = lane_id();
   const float lv = sl[lane];
-  float pre = lv, suf = lane < ch.Ct ? lv : 0.f;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float y = __shfl_up(pre, d), z = __shfl_down(suf, d);
-    if (lane >= d) pre += y;
-    if (lane + d < 64) suf += z;
-  }
-  float carry = __shfl_down(suf, 1);  // sum over (lane, Ct - 1]
-  if (lane == 63) carry = 0.f;
+  const float pre = mg_wave_prefix_sum(lv);
+  const float carry = mg_wave_next(mg_wave_suffix_sum(lane < ch.Ct ? lv : 0.f));  // (lane, Ct-1]
   sLc[lane] = pre;
   if (spt) spt[lane] = lane < ch.Ct ? expf(pre) : 0.f;
   const int tau = lane / nh;

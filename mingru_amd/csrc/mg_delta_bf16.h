@@ -1335,14 +1335,7 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       float acc = 0.f;
       for (int rr = 0; rr < ROWS; ++rr) {
         const int t = ROWS * w + rr;
-        float x = sF[t * DN + lane];
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const float y = __shfl_up(x, d);
-          if (lane >= d) x += y;
-        }
-        float ex = __shfl_up(x, 1);
-        if (lane == 0) ex = 0.f;
+        const float ex = mg_wave_prev(mg_wave_prefix_sum(sF[t * DN + lane]));
         if (t >= lane && t < ch.Ct) acc += sl[t] + ex;
       }
       sdl[w * DN + lane] = acc;
