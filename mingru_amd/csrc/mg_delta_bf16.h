@@ -33,6 +33,7 @@ using namespace mgd;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16;
 
 // ---- bf16 operand matrices in LDS ------------------------------------------------
@@ -55,7 +56,23 @@ __device__ __forceinline__ float bget(const BMat& m, int r, int k) {
 
 __device__ __forceinline__ u16 bf_bits(float x) { return __builtin_bit_cast(u16, (__bf16)x); }
 __device__ __forceinline__ float bf_val(u16 h) { return __uint_as_float((unsigned)h << 16); }
-// x = hi + lo to about 16 significant bits (both round to nearest even).
+// x = hi + lo to about 16 significant bits (both round to nearest even), for two
+// values at once: hp packs hi(x0) | hi(x1) << 16, lp the lo halves.  Both his come
+// from one packed conversion and are widened in place (a shift for the low half, a
+// mask for the high one), and both remainders go through one packed conversion:
+// six VALU per pair, where splitting each value on its own and packing the halves
+// afterwards took eleven (the pair's conversions are also half as many).  The empty asm statements keep the packed words opaque:
+// without them the compiler rewrites their uses as per-value conversions again.
+__device__ __forceinline__ void bf_split2(float x0, float x1, unsigned& hp, unsigned& lp) {
+  const bf16x2 h = {(__bf16)x0, (__bf16)x1};
+  hp = __builtin_bit_cast(unsigned, h);
+  asm("" : "+v"(hp));
+  const float r0 = x0 - __uint_as_float(hp << 16);
+  const float r1 = x1 - __uint_as_float(hp & 0xffff0000u);
+  const bf16x2 l = {(__bf16)r0, (__bf16)r1};
+  lp = __builtin_bit_cast(unsigned, l);
+  asm("" : "+v"(lp));
+}
 __device__ __forceinline__ void bf_split(float x, u16& hi, u16& lo) {
   hi = bf_bits(x);
   lo = bf_bits(x - bf_val(hi));
@@ -64,36 +81,30 @@ __device__ __forceinline__ void bf_split(float x, u16& hi, u16& lo) {
 // Split pair (hi, lo) of an fp32 matrix.
 typedef BMat BPair[2];
 
-__device__ __forceinline__ void put_split1(BPair& m, int r, int k, float x) {
-  u16 hi, lo;
-  bf_split(x, hi, lo);
-  *belem(m[0], r, k) = hi;
-  *belem(m[1], r, k) = lo;
+// Two single elements, (r0, k0) = x0 and (r1, k1) = x1, split as a pair.
+__device__ __forceinline__ void put_split1x2(BPair& m, int r0, int k0, float x0, int r1, int k1,
+                                             float x1) {
+  unsigned hp, lp;
+  bf_split2(x0, x1, hp, lp);
+  *belem(m[0], r0, k0) = (u16)hp;
+  *belem(m[1], r0, k0) = (u16)lp;
+  *belem(m[0], r1, k1) = (u16)(hp >> 16);
+  *belem(m[1], r1, k1) = (u16)(lp >> 16);
 }
 // Four consecutive k (k % 4 == 0): one 8-byte write per half.
 __device__ __forceinline__ void put_split4(BPair& m, int r, int k, float x0, float x1, float x2,
                                            float x3) {
-  u16 h[4], l[4];
-  bf_split(x0, h[0], l[0]);
-  bf_split(x1, h[1], l[1]);
-  bf_split(x2, h[2], l[2]);
-  bf_split(x3, h[3], l[3]);
-  *reinterpret_cast<uint2*>(belem(m[0], r, k)) =
-      make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
-  *reinterpret_cast<uint2*>(belem(m[1], r, k)) =
-      make_uint2(l[0] | ((unsigned)l[1] << 16), l[2] | ((unsigned)l[3] << 16));
+  unsigned h01, l01, h23, l23;
+  bf_split2(x0, x1, h01, l01);
+  bf_split2(x2, x3, h23, l23);
+  *reinterpret_cast<uint2*>(belem(m[0], r, k)) = make_uint2(h01, h23);
+  *reinterpret_cast<uint2*>(belem(m[1], r, k)) = make_uint2(l01, l23);
 }
 // Eight consecutive k (one chunk q): one 16-byte write per half.
 __device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (&x)[8]) {
   unsigned h[4], l[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    u16 h0, l0, h1, l1;
-    bf_split(x[2 * p], h0, l0);
-    bf_split(x[2 * p + 1], h1, l1);
-    h[p] = h0 | ((unsigned)h1 << 16);
-    l[p] = l0 | ((unsigned)l1 << 16);
-  }
+  for (int p = 0; p < 4; ++p) bf_split2(x[2 * p], x[2 * p + 1], h[p], l[p]);
   m[0].v[bpos(r, q)] = make_uint4(h[0], h[1], h[2], h[3]);
   m[1].v[bpos(r, q)] = make_uint4(l[0], l[1], l[2], l[3]);
 }
@@ -103,8 +114,8 @@ __device__ __forceinline__ void put_split8(BPair& m, int r, int q, const float (
 // (row = tile column, k = tile row).
 __device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) put_split1(m, R0 + 4 * g + i, C0 + r, a[i]);
+  put_split1x2(m, R0 + 4 * g, C0 + r, a[0], R0 + 4 * g + 1, C0 + r, a[1]);
+  put_split1x2(m, R0 + 4 * g + 2, C0 + r, a[2], R0 + 4 * g + 3, C0 + r, a[3]);
 }
 // Transposed: lane (g, r) holds k = R0+4g..R0+4g+3 of row C0+r, half of a 16-byte
 // chunk.  The lane rows g and g^1 (lanes 16 apart) swap halves with
@@ -115,11 +126,9 @@ __device__ __forceinline__ void acc_put(BPair& m, floatx4 a, int R0, int C0) {
 // bank group.)  The whole wave must be active; R0 is a multiple of 8.
 __device__ __forceinline__ void acc_put_t(BPair& m, floatx4 a, int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
-  u16 h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) bf_split(a[i], h[i], l[i]);
-  const unsigned hx = h[0] | ((unsigned)h[1] << 16), hy = h[2] | ((unsigned)h[3] << 16);
-  const unsigned lx = l[0] | ((unsigned)l[1] << 16), ly = l[2] | ((unsigned)l[3] << 16);
+  unsigned hx, lx, hy, ly;
+  bf_split2(a[0], a[1], hx, lx);
+  bf_split2(a[2], a[3], hy, ly);
   // [0]: even lane rows keep their own (hi) words and odd ones receive the even
   // partner's lo words; [1]: even rows receive the odd partner's hi words, odd rows
   // keep their own lo words.
@@ -273,10 +282,8 @@ struct FTile {
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
-      put_split1(m, c0 + 0, row, f[v].x);
-      put_split1(m, c0 + 1, row, f[v].y);
-      put_split1(m, c0 + 2, row, f[v].z);
-      put_split1(m, c0 + 3, row, f[v].w);
+      put_split1x2(m, c0 + 0, row, f[v].x, c0 + 1, row, f[v].y);
+      put_split1x2(m, c0 + 2, row, f[v].z, c0 + 3, row, f[v].w);
     }
   }
 };
@@ -325,10 +332,8 @@ struct FTileF {
     for (int v = 0; v < 2; ++v) {
       int d0, j;
       coords(v, d0, j);
-      put_split1(m, d0 + 0, j, f[v].x);
-      put_split1(m, d0 + 1, j, f[v].y);
-      put_split1(m, d0 + 2, j, f[v].z);
-      put_split1(m, d0 + 3, j, f[v].w);
+      put_split1x2(m, d0 + 0, j, f[v].x, d0 + 1, j, f[v].y);
+      put_split1x2(m, d0 + 2, j, f[v].z, d0 + 3, j, f[v].w);
     }
   }
   // transposed: (row = column, k = row), four consecutive k per entry
@@ -405,6 +410,9 @@ constexpr int SPLIT_LO = DN * DN;  // u16 offset of the lo half
 __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2], int R0, int C0) {
   const int lane = lane_id(), r = lane & 15, g = lane >> 4;
   u16* p = dst + (R0 + 4 * g) * DN + C0 + r;
+  // Value by value: splitting the pairs (tile 0, tile 1) of each row and storing
+  // their high halves with global_store_short_d16_hi took the forward preparation
+  // kernel from 199 to 212 us at C5.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -667,13 +675,7 @@ __device__ __forceinline__ void rmm(floatx4 (&acc)[2], const FragOff& F, const u
 __device__ __forceinline__ void split_frag(const float (&x)[8], uint4& hi, uint4& lo) {
   unsigned h[4], l[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    u16 h0, l0, h1, l1;
-    bf_split(x[2 * p], h0, l0);
-    bf_split(x[2 * p + 1], h1, l1);
-    h[p] = h0 | ((unsigned)h1 << 16);
-    l[p] = l0 | ((unsigned)l1 << 16);
-  }
+  for (int p = 0; p < 4; ++p) bf_split2(x[2 * p], x[2 * p + 1], h[p], l[p]);
   hi = make_uint4(h[0], h[1], h[2], h[3]);
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
