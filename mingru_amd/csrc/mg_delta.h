@@ -33,6 +33,15 @@ __device__ __forceinline__ float ldf(const float* p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float ldf(const uint16_t* p, int64_t i) {
   return __uint_as_float((unsigned)p[i] << 16);
 }
+// ok ? p[i] : 0 with the load issued whether or not ok holds (from element 0, which
+// every caller's buffer has, when it does not): written as a conditional load, the
+// compiler gives each load a branch of its own and waits for it there, so a lane's
+// loads run one after another instead of all in flight at once.
+template <typename T>
+__device__ __forceinline__ float ldf_or0(const T* p, int64_t i, bool ok) {
+  const float v = ldf(p, ok ? i : 0);
+  return ok ? v : 0.f;
+}
 __device__ __forceinline__ uint16_t f2bf(float v) {
   unsigned u = __float_as_uint(v);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);

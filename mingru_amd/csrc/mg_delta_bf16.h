@@ -320,10 +320,10 @@ struct FTileF {
       int d0, j;
       coords(v, d0, j);
       const bool c = j < cols;
-      f[v] = make_float4(c && d0 + 0 < rows ? src[(d0 + 0) * DN + j] : 0.f,
-                         c && d0 + 1 < rows ? src[(d0 + 1) * DN + j] : 0.f,
-                         c && d0 + 2 < rows ? src[(d0 + 2) * DN + j] : 0.f,
-                         c && d0 + 3 < rows ? src[(d0 + 3) * DN + j] : 0.f);
+      f[v] = make_float4(ldf_or0(src, (d0 + 0) * DN + j, c && d0 + 0 < rows),
+                         ldf_or0(src, (d0 + 1) * DN + j, c && d0 + 1 < rows),
+                         ldf_or0(src, (d0 + 2) * DN + j, c && d0 + 2 < rows),
+                         ldf_or0(src, (d0 + 3) * DN + j, c && d0 + 3 < rows));
     }
   }
   // (row, k = column)
@@ -516,7 +516,7 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = R0 + 4 * gg + i, d = C0 + 16 * jj + r;
-        qv[jj][i] = (t < ch.Ct && d < g.dk) ? ldf(Q, (trow0 + t) * g.dk + d) : 0.f;
+        qv[jj][i] = ldf_or0(Q, (trow0 + t) * g.dk + d, t < ch.Ct && d < g.dk);
       }
     const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
     tk.put(sK);
@@ -798,7 +798,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = R0 + 4 * gg + i, j = C0 + 16 * jj + r;
-      vpre[jj][i] = (m < ch.M && j < g.dv) ? ldf(V, (row0 + m) * g.dv + j) : 0.f;
+      vpre[jj][i] = ldf_or0(V, (row0 + m) * g.dv + j, m < ch.M && j < g.dv);
     }
   uint4 qf[2];
   load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
