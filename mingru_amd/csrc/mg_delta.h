@@ -391,9 +391,13 @@ __device__ __forceinline__ void write_vectors(float* vv, const float* sLc, const
   }
 }
 
+// l of token (thread index mod 64) of chunk ch: every wave of a larger workgroup
+// loads the same values, so a kernel can store them without a branch on the thread
+// index (inside such a branch the compiler issues the load last and waits for it).
 __device__ __forceinline__ float ld_l(const float* lg, int64_t bh, const DwGeom& g,
                                       const Chunk& ch) {
-  return threadIdx.x < ch.Ct ? lg[bh * g.T + ch.t0 + threadIdx.x] : 0.f;
+  const int t = threadIdx.x & (DN - 1);
+  return ldf_or0(lg, bh * g.T + ch.t0 + t, t < ch.Ct);
 }
 
 

@@ -227,8 +227,11 @@ struct BTile {
   __device__ __forceinline__ void load(const u16* src, int rows, int cols, int64_t ldg) {
     const int idx = threadIdx.x, row = idx >> 3, c0 = (idx & 7) * 8;
     if (cols == DN && ldg == DN && (((uintptr_t)src) & 15u) == 0) {
-      q = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + c0)
-                     : make_uint4(0u, 0u, 0u, 0u);
+      // Loaded whether or not the row is in the block (row 0 when it is not), so the
+      // compiler keeps the load out of a branch that would wait for it.
+      const unsigned off = (unsigned)((row < rows ? row : 0) * DN + c0);
+      const uint4 v = *reinterpret_cast<const uint4*>(src + off);
+      q = row < rows ? v : make_uint4(0u, 0u, 0u, 0u);
     } else {
       u16 e[8];
 #pragma unroll
@@ -253,28 +256,35 @@ struct BTile {
 
 // fp32 block (rows x cols) of a padded 64 x 64 workspace matrix: thread idx holds
 // rows (idx + 512 v) / 16, columns 4 ((idx + 512 v) % 16) + 0..3, v = 0, 1; zero
-// outside the block.
+// outside the block.  Every row of a padded matrix is in the buffer, so the loads
+// are unconditional and the block's bounds are applied when the tile is put: masking
+// at the load made the wave wait for it there, before the loads that follow it were
+// issued.
 struct FTile {
   float4 f[2];
+  int rows, cols;  // the block (wave-uniform)
 
-  __device__ __forceinline__ void load(const float* src, int rows, int cols) {
+  __device__ __forceinline__ void load(const float* src, int rows_, int cols_) {
+    rows = rows_;
+    cols = cols_;
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
-      float4 x = row < rows ? *reinterpret_cast<const float4*>(src + row * DN + c0)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (c0 + 0 >= cols) x.x = 0.f;
-      if (c0 + 1 >= cols) x.y = 0.f;
-      if (c0 + 2 >= cols) x.z = 0.f;
-      if (c0 + 3 >= cols) x.w = 0.f;
-      f[v] = x;
+      const unsigned off = (threadIdx.x + v * NTB) * 4u;  // row idx / 16, columns 4 (idx % 16)
+      f[v] = *reinterpret_cast<const float4*>(src + off);
     }
+  }
+  __device__ __forceinline__ float4 val(int v) const {
+    const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
+    const int nc = row < rows ? cols - c0 : 0;  // components inside: min(nc, 4)
+    return make_float4(nc > 0 ? f[v].x : 0.f, nc > 1 ? f[v].y : 0.f, nc > 2 ? f[v].z : 0.f,
+                       nc > 3 ? f[v].w : 0.f);
   }
   __device__ __forceinline__ void put_split(BPair& m) const {
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       const int idx = threadIdx.x + v * NTB;
-      put_split4(m, idx >> 4, (idx & 15) * 4, f[v].x, f[v].y, f[v].z, f[v].w);
+      const float4 x = val(v);
+      put_split4(m, idx >> 4, (idx & 15) * 4, x.x, x.y, x.z, x.w);
     }
   }
   // transposed: (row = column, k = row)
@@ -282,8 +292,9 @@ struct FTile {
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
       const int idx = threadIdx.x + v * NTB, row = idx >> 4, c0 = (idx & 15) * 4;
-      put_split1x2(m, c0 + 0, row, f[v].x, c0 + 1, row, f[v].y);
-      put_split1x2(m, c0 + 2, row, f[v].z, c0 + 3, row, f[v].w);
+      const float4 x = val(v);
+      put_split1x2(m, c0 + 0, row, x.x, c0 + 1, row, x.y);
+      put_split1x2(m, c0 + 2, row, x.z, c0 + 3, row, x.w);
     }
   }
 };
@@ -294,24 +305,19 @@ struct FTile {
 // L % 16 -- with one contiguous 16-byte load; zero outside the block.
 struct FTileF {
   float4 f[2];
+  int rows, cols;  // the block (wave-uniform); load_rowmajor applies it itself
 
   __device__ static __forceinline__ void coords(int v, int& d0, int& j) {
     const int e = threadIdx.x + v * NTB, t = e >> 6, L = e & 63;
     d0 = 16 * (t >> 2) + 4 * (L >> 4);
     j = 16 * (t & 3) + (L & 15);
   }
-  __device__ __forceinline__ void load(const float* src, int rows, int cols) {
+  __device__ __forceinline__ void load(const float* src, int rows_, int cols_) {
+    rows = rows_;
+    cols = cols_;
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      int d0, j;
-      coords(v, d0, j);
-      float4 x = *reinterpret_cast<const float4*>(src + (threadIdx.x + v * NTB) * 4);
-      if (j >= cols || d0 + 0 >= rows) x.x = 0.f;
-      if (j >= cols || d0 + 1 >= rows) x.y = 0.f;
-      if (j >= cols || d0 + 2 >= rows) x.z = 0.f;
-      if (j >= cols || d0 + 3 >= rows) x.w = 0.f;
-      f[v] = x;
-    }
+    for (int v = 0; v < 2; ++v)  // raw loads; the bounds are applied when used (as in FTile)
+      f[v] = *reinterpret_cast<const float4*>(src + (threadIdx.x + v * NTB) * 4u);
   }
   // The same entries of a row-major matrix (row stride DN): four rows of one column.
   __device__ __forceinline__ void load_rowmajor(const float* src, int rows, int cols) {
@@ -325,6 +331,15 @@ struct FTileF {
                          ldf_or0(src, (d0 + 2) * DN + j, c && d0 + 2 < rows),
                          ldf_or0(src, (d0 + 3) * DN + j, c && d0 + 3 < rows));
     }
+    this->rows = DN;  // already applied
+    this->cols = DN;
+  }
+  __device__ __forceinline__ float4 val(int v) const {
+    int d0, j;
+    coords(v, d0, j);
+    const int nr = j < cols ? rows - d0 : 0;  // components inside: min(nr, 4)
+    return make_float4(nr > 0 ? f[v].x : 0.f, nr > 1 ? f[v].y : 0.f, nr > 2 ? f[v].z : 0.f,
+                       nr > 3 ? f[v].w : 0.f);
   }
   // (row, k = column)
   __device__ __forceinline__ void put_split(BPair& m) const {
@@ -332,8 +347,9 @@ struct FTileF {
     for (int v = 0; v < 2; ++v) {
       int d0, j;
       coords(v, d0, j);
-      put_split1x2(m, d0 + 0, j, f[v].x, d0 + 1, j, f[v].y);
-      put_split1x2(m, d0 + 2, j, f[v].z, d0 + 3, j, f[v].w);
+      const float4 x = val(v);
+      put_split1x2(m, d0 + 0, j, x.x, d0 + 1, j, x.y);
+      put_split1x2(m, d0 + 2, j, x.z, d0 + 3, j, x.w);
     }
   }
   // transposed: (row = column, k = row), four consecutive k per entry
@@ -342,7 +358,8 @@ struct FTileF {
     for (int v = 0; v < 2; ++v) {
       int d0, j;
       coords(v, d0, j);
-      put_split4(m, j, d0, f[v].x, f[v].y, f[v].z, f[v].w);
+      const float4 x = val(v);
+      put_split4(m, j, d0, x.x, x.y, x.z, x.w);
     }
   }
 };
@@ -518,15 +535,15 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
         const int t = R0 + 4 * gg + i, d = C0 + 16 * jj + r;
         qv[jj][i] = ldf_or0(Q, (trow0 + t) * g.dk + d, t < ch.Ct && d < g.dk);
       }
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.put(sK);
     tk.put_t(sKt);
     tv.put_t(sVt);
     tq.put(sQ);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
     if constexpr (GATED) {
       const float lv = ld_l(lg, bh, g, ch);
-      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+      sl[threadIdx.x & (DN - 1)] = lv;
     }
   }
   __syncthreads();
@@ -808,14 +825,14 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
     td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
     th.load(Hb + mat, g.dk, g.dv);
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.put(sK);
     tq.put_t(sQt);
     td.put_t(sDyt);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
     if constexpr (GATED) {
       const float lv = ld_l(lg, bh, g, ch);
-      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+      sl[threadIdx.x & (DN - 1)] = lv;
     }
   }
   __syncthreads();
@@ -1066,17 +1083,17 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
     const uint4 elo = *reinterpret_cast<const uint4*>(es + SPLIT_LO + erow * DN + 8 * eq);
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) gacc[jj] = acc_load_ws(G0m + mat + R0 * DN + C0 + 16 * jj);
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.put(sK);
     tk.put_t(sKt);
     tq.put_t(sQt);
     sR[0][0].v[bpos(erow, eq)] = ehi;
     sR[0][1].v[bpos(erow, eq)] = elo;
     tn.put_split_t(sR[1]);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
     if constexpr (GATED) {
       const float lv = ld_l(lg, bh, g, ch);
-      if (threadIdx.x < DN) sl[threadIdx.x] = lv;
+      sl[threadIdx.x & (DN - 1)] = lv;
     }
   }
   __syncthreads();
@@ -1097,9 +1114,10 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       tn2.load_rowmajor(dHn + mat, g.dk, g.dv);
       float part = 0.f;
 #pragma unroll
-      for (int v = 0; v < 2; ++v)
-        part += tn2.f[v].x * th.f[v].x + tn2.f[v].y * th.f[v].y + tn2.f[v].z * th.f[v].z +
-                tn2.f[v].w * th.f[v].w;
+      for (int v = 0; v < 2; ++v) {
+        const float4 a = tn2.val(v), b = th.val(v);
+        part += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+      }
       part = mg_group_sum<64>(part);
       if (lane == 0) sred[wave_id()] = part;
     }
