@@ -78,14 +78,12 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
   tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
   tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
   tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
-  const float bv = threadIdx.x < ch.M ? beta[row0 + threadIdx.x] : 0.f;
+  const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
   const float lv = ld_l(lg, bh, g, ch);
   tk.store(sK);
   tv.store(sV);
-  if (threadIdx.x < DN) {
-    sb[threadIdx.x] = bv;
-    sl[threadIdx.x] = lv;
-  }
+  sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
+  sl[threadIdx.x & (DN - 1)] = lv;
   __syncthreads();
   decay_tables<NT>(sl, sE);
   decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab);
@@ -187,7 +185,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_chain(const float* __restrict__ Q,
     const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
-    abv = threadIdx.x < DN ? vv[V_AB + threadIdx.x] : 0.f;
+    abv = vv[V_AB + (threadIdx.x & (DN - 1))];  // every wave loads the same 64 values
     pcv = vv[V_PC];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ptv[i] = vv[V_PT + 16 * w + 4 * gg + i];
@@ -202,7 +200,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_chain(const float* __restrict__ Q,
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     tk.store(sK[buf]);
     tq.store(sQ[buf]);
-    if (threadIdx.x < DN) sab[buf][threadIdx.x] = abv;
+    sab[buf][threadIdx.x & (DN - 1)] = abv;  // and stores them: no branch to wait in
     float wc[16], pc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -273,17 +271,15 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
     th.load(Hb + mat, g.dk, g.dv, DN);
     tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
     td.load(dy + (bh * g.T + ch.t0) * g.dv, ch.Ct, g.dv, g.dv);
-    const float bv = threadIdx.x < ch.M ? beta[row0 + threadIdx.x] : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     const float lv = ld_l(lg, bh, g, ch);
     tk.store(sK);
     tv.store(sV);
     th.store(sX);
     tq.store(sQ);
     td.store(sD);
-    if (threadIdx.x < DN) {
-      sb[threadIdx.x] = bv;
-      sl[threadIdx.x] = lv;
-    }
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
+    sl[threadIdx.x & (DN - 1)] = lv;
   }
   __syncthreads();
   decay_tables<NT>(sl, sE);
@@ -396,7 +392,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_chain(const float* __restrict__ K,
     load16g(ea, Em + mat + (16 * w + r) * DN + 16 * gg);
     g0 = acc_load_ws(G0m + mat + 16 * w * DN + col0);
     qd0 = acc_load_ws(QdYm + mat + 16 * w * DN + col0);
-    pv = threadIdx.x < DN ? vv[V_P + threadIdx.x] : 0.f;
+    pv = vv[V_P + (threadIdx.x & (DN - 1))];  // every wave loads the same 64 values
     pcv = vv[V_PC];
   };
   fetch(g.nc - 1);
@@ -404,7 +400,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_chain(const float* __restrict__ K,
     const int buf = c & 1;
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     tk.store(sK[buf]);
-    if (threadIdx.x < DN) sp[buf][threadIdx.x] = pv;
+    sp[buf][threadIdx.x & (DN - 1)] = pv;  // and stores them: no branch to wait in
     float ec[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) ec[i] = ea[i];
@@ -475,7 +471,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     tg.load(Gm + mat, ch.M, g.dv, DN);
     th.load(Hb + mat, g.dk, g.dv, DN);
     tn.load(dHn + mat, g.dk, g.dv, DN);
-    const float bv = threadIdx.x < ch.M ? beta[row0 + threadIdx.x] : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     const float lv = ld_l(lg, bh, g, ch);
     tk.store(sK);
     tq.store(sQ);
@@ -483,10 +479,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
     tu.store(sU);
     tg.store(sG);
     th.store(sH);
-    if (threadIdx.x < DN) {
-      sb[threadIdx.x] = bv;
-      sl[threadIdx.x] = lv;
-    }
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
+    sl[threadIdx.x & (DN - 1)] = lv;
   }
   __syncthreads();
   decay_tables<NT>(sl, sE);

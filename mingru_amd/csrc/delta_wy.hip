@@ -59,10 +59,10 @@ __global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, cons
   tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
   tv.load(V + row0 * g.dv, ch.M, g.dv, g.dv);
   tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
-  const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+  const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
   tk.store(sK);
   tv.store(sV);
-  if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+  sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
   __syncthreads();
   build_L(sK, sb, sL);
   __syncthreads();
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(NT) void dw_fwd_chain(const TI* __restrict__ Q, con
     const int64_t row0 = (bh * g.T + ch.t0) * g.nh;
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
-    bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     load16(wa, Wm + mat + (16 * w + r) * DN + 16 * gg);
     load16(pa, Pm + mat + (16 * w + r) * DN + 16 * gg);
     u0 = acc_load_ws(U0m + mat + 16 * w * DN + col0);
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(NT) void dw_fwd_chain(const TI* __restrict__ Q, con
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     tk.store(sK[buf]);
     tq.store(sQ[buf]);
-    if (threadIdx.x < DN) sb[buf][threadIdx.x] = bv;
+    sb[buf][threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values
     float wc[16], pc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -238,13 +238,13 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
     th.load(Hb + mat, g.dk, g.dv, DN);
     tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
     td.load(dy + (bh * g.T + ch.t0) * g.dv, ch.Ct, g.dv, g.dv);
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.store(sK);
     tv.store(sV);
     th.store(sX);
     tq.store(sQ);
     td.store(sD);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
   }
   __syncthreads();
   build_L(sK, sb, sL);
@@ -410,14 +410,14 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
     tg.load(Gm + mat, ch.M, g.dv, DN);
     th.load(Hb + mat, g.dk, g.dv, DN);
     tn.load(dHn + mat, g.dk, g.dv, DN);
-    const float bv = threadIdx.x < ch.M ? ldf(beta, row0 + threadIdx.x) : 0.f;
+    const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.store(sK);
     tq.store(sQ);
     td.store(sD);
     tu.store(sU);
     tg.store(sG);
     th.store(sH);
-    if (threadIdx.x < DN) sb[threadIdx.x] = bv;
+    sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
   }
   __syncthreads();
   // S = Q K^T, dP = dy U^T (rows = tokens of block w, cols = micro-rows of block J).

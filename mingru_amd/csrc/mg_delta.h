@@ -132,6 +132,9 @@ __device__ __forceinline__ float tof(uint16_t x) { return __uint_as_float((unsig
 // matrix, written later to a 64 x 64 LDS matrix (stride LD) with zeros outside
 // the block.  Each thread holds 16 elements; every load is issued before any LDS
 // store, and full-width, 16-byte aligned blocks move as 16-byte vectors.
+// Sixteen zero bytes in global memory (never written).
+static __device__ uint4 mg_zero16 = {0u, 0u, 0u, 0u};
+
 template <typename TI>
 struct Tile {
   static constexpr int EPV = 16 / sizeof(TI);  // elements per 16-byte vector
@@ -147,8 +150,11 @@ struct Tile {
       for (int v = 0; v < NV; ++v) {
         const int idx = threadIdx.x + v * NT;
         const int row = idx / VPR, col = (idx % VPR) * EPV;
-        q[v] = row < rows ? *reinterpret_cast<const uint4*>(src + (int64_t)row * DN + col)
-                          : make_uint4(0u, 0u, 0u, 0u);
+        // Rows outside the block read a zero vector instead of being skipped: a
+        // conditional load (or a select on its value) gets a branch of its own that
+        // waits for it, so the thread's loads would not all be in flight at once.
+        q[v] = *(row < rows ? reinterpret_cast<const uint4*>(src + (int64_t)row * DN + col)
+                            : &mg_zero16);
       }
     } else {
       TI* e = reinterpret_cast<TI*>(q);
@@ -156,7 +162,9 @@ struct Tile {
       for (int k = 0; k < 16; ++k) {
         const int idx = threadIdx.x + k * NT;
         const int row = idx >> 6, col = idx & 63;
-        e[k] = (row < rows && col < cols) ? src[(int64_t)row * ldg + col] : TI(0);
+        const bool ok = row < rows && col < cols;
+        const TI x = src[ok ? (int64_t)row * ldg + col : 0];
+        e[k] = ok ? x : TI(0);
       }
     }
   }
