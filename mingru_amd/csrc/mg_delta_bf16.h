@@ -420,8 +420,9 @@ __device__ __forceinline__ floatx4 load_tile_frag(const float* src, int rb, int 
 }
 
 // Split workspace matrix: a 64 x 64 row-major bf16 hi half followed by the lo
-// half (the 16 KB of one padded fp32 matrix slot).  Read back by the chains as
-// MFMA A fragments straight from memory.
+// half (the 16 KB of one padded fp32 matrix slot).  E is kept in this form for
+// the gradient kernel's row reads; the chains' operands use the fragment order
+// below.
 constexpr int SPLIT_LO = DN * DN;  // u16 offset of the lo half
 
 __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2], int R0, int C0) {
@@ -440,6 +441,37 @@ __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2
       p[SPLIT_LO + i * DN + 16 * jj] = lo;
     }
   }
+}
+
+// Split workspace matrix in A-fragment order: a hi half and a lo half of 4096
+// bf16 each, laid out so that the MFMA A fragment of rows 16 rb..16 rb + 15 and
+// k 32 s..32 s + 31 is 1 KB of consecutive memory, lane l's eight values at
+// ((rb * 2 + s) * 64 + l) * 8.  Element (row, k) sits at
+// ((row / 16 * 2 + k / 32) * 64 + 16 * (k / 8 % 4) + row % 16) * 8 + k % 8.  The
+// chains read their operands back with one 16-byte load per fragment and half,
+// and a wave's load covers 1 KB without gaps (the row-major form read 16 bytes
+// from each of 64 rows).
+// The wave's 16 x 32 accumulator block (rows 16 rb, columns 32 ch) into a split
+// workspace matrix in fragment order.  The block is exactly the A fragment
+// (rb, s = ch), so the wave puts it into its own block of an LDS pair `st`,
+// reads back each lane's eight hi and eight lo values and stores each with one
+// 16-byte write (writing the accumulator's values one by one to their fragment
+// slots made the forward preparation kernel 15 us slower at C5).  Only this wave
+// touches its block of `st`, and one wave's LDS operations complete in order; the
+// empty asm statements keep the compiler from moving one lane's LDS write past
+// another lane's read of it (a previous call's reads included).
+__device__ __forceinline__ void store_block_splitfrag(BPair& st, const floatx4 (&v)[2],
+                                                      const FragOff& F, u16* dst) {
+  asm volatile("" ::: "memory");
+  acc_put(st, v[0], 16 * F.rb, 32 * F.ch);
+  acc_put(st, v[1], 16 * F.rb, 32 * F.ch + 16);
+  asm volatile("" ::: "memory");
+  const unsigned a = F.ch ? F.a[1] : F.a[0];
+  const uint4 hi = __builtin_bit_cast(uint4, frag_at(st[0], a));
+  const uint4 lo = __builtin_bit_cast(uint4, frag_at(st[1], a));
+  const unsigned off = ((unsigned)(F.rb * 2 + F.ch) * 64u + lane_id()) * 8u;
+  *reinterpret_cast<uint4*>(dst + off) = hi;
+  *reinterpret_cast<uint4*>(dst + SPLIT_LO + off) = lo;
 }
 
 // Split operands from a 64 x 64 fp32 LDS matrix (row stride LD), one chunk of 8
@@ -642,10 +674,13 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
     }
     bmm<true, false>(b2, F, sM1, &sVt);  // B = M1 V
     bmm<true, false>(pu, F, sM2, &sVt);  // Pu = M2 V
-    store_block_split(reinterpret_cast<u16*>(Ao + mat), a2, R0, C0);
     store_block_frag(Bo + mat, b2, R0, C0);
-    store_block_split(reinterpret_cast<u16*>(Qeo + mat), qe, R0, C0);
     store_block_frag(Puo + mat, pu, R0, C0);
+    // A and Qe leave through T^T's pair, free since M1 and M2 were formed (gated:
+    // it holds (p K)^T, which every wave has read once past the barrier).
+    if constexpr (GATED) __syncthreads();
+    store_block_splitfrag(sTt, a2, F, reinterpret_cast<u16*>(Ao + mat));
+    store_block_splitfrag(sTt, qe, F, reinterpret_cast<u16*>(Qeo + mat));
   }
 }
 
@@ -1010,8 +1045,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
         }
       }
     }
-    store_block_split(reinterpret_cast<u16*>(Apo + mat), a2, R0, C0);
     store_block_frag(bpo + mat, qd, R0, C0);
+    store_block_splitfrag(sQD, a2, F, reinterpret_cast<u16*>(Apo + mat));  // Q^T, dy^T are free
   }
 }
 
@@ -1421,14 +1456,16 @@ __device__ __forceinline__ void amm2(floatx4& acc0, const uint4 (&ah0)[2], const
   }
 }
 
-// A fragments of a split workspace matrix: row `row`, chunks g and 4 + g.
+// A fragments of a fragment-ordered split workspace matrix: rows 16 rb..16 rb + 15,
+// k halves s = 0, 1.
 __device__ __forceinline__ void load_split_frag(uint4 (&hi)[2], uint4 (&lo)[2], const u16* m,
-                                                int row) {
-  const int g = lane_id() >> 4;
+                                                int rb) {
+  const unsigned lane = lane_id();
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    hi[s] = *reinterpret_cast<const uint4*>(m + row * DN + 8 * (4 * s + g));
-    lo[s] = *reinterpret_cast<const uint4*>(m + SPLIT_LO + row * DN + 8 * (4 * s + g));
+    const unsigned off = ((unsigned)(rb * 2 + s) * 64u + lane) * 8u;
+    hi[s] = *reinterpret_cast<const uint4*>(m + off);
+    lo[s] = *reinterpret_cast<const uint4*>(m + SPLIT_LO + off);
   }
 }
 
@@ -1464,8 +1501,8 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
   }
   auto fetch = [&](FwdOps& o, int c) {
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Am + mat), 16 * w + r);
-    load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), 16 * w + r);
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Am + mat), w);
+    load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), w);
     o.b = load_tile_frag(Bm + mat, w, col0 >> 4);
     o.pu = load_tile_frag(Pum + mat, w, col0 >> 4);
     if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
@@ -1543,7 +1580,7 @@ __global__ __launch_bounds__(NT) void dwb_bwd_chain(const float* __restrict__ dH
   }
   auto fetch = [&](BwdOps& o, int c) {
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
-    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), 16 * w + r);
+    load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), w);
     o.b = load_tile_frag(bpm + mat, w, col0 >> 4);
     if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
   };
