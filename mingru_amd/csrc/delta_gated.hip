@@ -186,7 +186,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_chain(const float* __restrict__ Q,
     tk.load(K + row0 * g.dk, ch.M, g.dk, g.dk);
     tq.load(Q + (bh * g.T + ch.t0) * g.dk, ch.Ct, g.dk, g.dk);
     abv = vv[V_AB + (threadIdx.x & (DN - 1))];  // every wave loads the same 64 values
-    pcv = vv[V_PC];
+    pcv = ld_uniform_v(vv + V_PC);
 #pragma unroll
     for (int i = 0; i < 4; ++i) ptv[i] = vv[V_PT + 16 * w + 4 * gg + i];
     load16g(wa, Wm + mat + (16 * w + r) * DN + 16 * gg);
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_chain(const float* __restrict__ K,
     g0 = acc_load_ws(G0m + mat + 16 * w * DN + col0);
     qd0 = acc_load_ws(QdYm + mat + 16 * w * DN + col0);
     pv = vv[V_P + (threadIdx.x & (DN - 1))];  // every wave loads the same 64 values
-    pcv = vv[V_PC];
+    pcv = ld_uniform_v(vv + V_PC);
   };
   fetch(g.nc - 1);
   for (int c = g.nc - 1; c >= 0; --c) {

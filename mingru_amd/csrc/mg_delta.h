@@ -42,6 +42,15 @@ __device__ __forceinline__ float ldf_or0(const T* p, int64_t i, bool ok) {
   const float v = ldf(p, ok ? i : 0);
   return ok ? v : 0.f;
 }
+// p[0] for a workgroup-uniform p, read with a vector load.  The compiler issues a
+// uniform load as a scalar load, and scalar loads are counted together with LDS
+// operations: a loop that prefetches one and then waits for its LDS writes before
+// a barrier waits for the whole memory round trip of the prefetch as well.
+__device__ __forceinline__ float ld_uniform_v(const float* p) {
+  unsigned z = 0;
+  asm volatile("" : "+v"(z));  // an index the compiler cannot prove uniform
+  return p[z];
+}
 __device__ __forceinline__ uint16_t f2bf(float v) {
   unsigned u = __float_as_uint(v);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);

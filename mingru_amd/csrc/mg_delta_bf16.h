@@ -1505,7 +1505,7 @@ __global__ __launch_bounds__(NT) void dwb_fwd_chain(const float* __restrict__ H0
     load_split_frag(o.qh, o.ql, reinterpret_cast<const u16*>(Qem + mat), w);
     o.b = load_tile_frag(Bm + mat, w, col0 >> 4);
     o.pu = load_tile_frag(Pum + mat, w, col0 >> 4);
-    if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
+    if constexpr (GATED) o.pc = ld_uniform_v(vm + ((size_t)bh * g.nc + c) * VECN + V_PC);
   };
   // Chunk c + 2 is fetched while chunk c computes: three operand buffers in a
   // ring, the loop unrolled by three so the buffers never move.  The fetch is
@@ -1582,7 +1582,7 @@ __global__ __launch_bounds__(NT) void dwb_bwd_chain(const float* __restrict__ dH
     const size_t mat = ((size_t)bh * g.nc + c) * MAT;
     load_split_frag(o.ah, o.al, reinterpret_cast<const u16*>(Apm + mat), w);
     o.b = load_tile_frag(bpm + mat, w, col0 >> 4);
-    if constexpr (GATED) o.pc = vm[((size_t)bh * g.nc + c) * VECN + V_PC];
+    if constexpr (GATED) o.pc = ld_uniform_v(vm + ((size_t)bh * g.nc + c) * VECN + V_PC);
   };
   // Chunk c - 2 is fetched while chunk c computes (ring of three buffers).
   auto step = [&](const BwdOps& cur, BwdOps& fill, int c) {
