@@ -13,12 +13,13 @@ int dwb_bwd_prep_launch(bool gated, const void* Q, const void* K, const void* V,
   const dim3 pgrid(g.nc, (unsigned)BH);
   const u16 *q = (const u16*)Q, *k = (const u16*)K, *v = (const u16*)V, *b = (const u16*)beta,
             *d = (const u16*)dy;
+  const float* Tin = dw_inv_slots(Hb, BH, g);
   if (gated)
-    hipLaunchKernelGGL(dwb_bwd_prep<true>, pgrid, dim3(NTB), 0, stream, q, k, v, b, lg, d, Hb, Um,
-                       Em, G0m, Apm, bpm, vm, g);
+    hipLaunchKernelGGL(dwb_bwd_prep<true>, pgrid, dim3(NTB), 0, stream, q, k, v, b, lg, d, Hb, Tin,
+                       Um, Em, G0m, Apm, bpm, vm, g);
   else
     hipLaunchKernelGGL(dwb_bwd_prep<false>, pgrid, dim3(NTB), 0, stream, q, k, v, b, nullptr, d,
-                       Hb, Um, Em, G0m, Apm, bpm, nullptr, g);
+                       Hb, Tin, Um, Em, G0m, Apm, bpm, nullptr, g);
   return hipGetLastError() == hipSuccess ? MG_OK : MG_ERR_LAUNCH;
 }
 

@@ -725,7 +725,7 @@ int dw_fwd_bf16_gated(const void* Q, const void* K, const void* V, const void* b
   float* vm = (float*)((char*)ws + 4 * mb);
   hipLaunchKernelGGL(dwb_fwd_prep<true>, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream,
                      (const u16*)Q, (const u16*)K, (const u16*)V, (const u16*)beta, lg, Am, Bm,
-                     Qem, Pum, vm, g);
+                     Qem, Pum, vm, dw_inv_slots(Hb, BH, g), g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dwb_fwd_chain<true>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, H0, Am, Bm,
                      Qem, Pum, vm, (u16*)y, HT, Hb, g, BH);

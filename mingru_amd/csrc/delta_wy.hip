@@ -589,7 +589,7 @@ size_t mg_delta_state_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int
   DwGeom g;
   int64_t BH;
   if (!dw_geom(B, H, T, nh, dk, dv, chunk, g, BH)) return 0;
-  return dw_mat_bytes(BH, g);
+  return dw_state_bytes(BH, g);
 }
 
 int mg_delta_fwd(const void* Q, const void* K, const void* V, const void* beta, const float* H0,

@@ -32,7 +32,7 @@ int dw_fwd_bf16(const void* Q, const void* K, const void* V, const void* beta, c
   float* Pum = (float*)((char*)ws + 3 * mb);
   hipLaunchKernelGGL(dwb_fwd_prep<false>, dim3(g.nc, (unsigned)BH), dim3(NTB), 0, stream,
                      (const u16*)Q, (const u16*)K, (const u16*)V, (const u16*)beta, nullptr, Am,
-                     Bm, Qem, Pum, nullptr, g);
+                     Bm, Qem, Pum, nullptr, dw_inv_slots(Hb, BH, g), g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dwb_fwd_chain<false>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, H0, Am,
                      Bm, Qem, Pum, nullptr, (u16*)y, HT, Hb, g, BH);

@@ -436,6 +436,17 @@ inline bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int
 }
 
 inline size_t dw_mat_bytes(int64_t BH, const DwGeom& g) { return (size_t)BH * g.nc * MAT * sizeof(float); }
+// The saved state buffer (Hbound): one padded matrix slot per (head, chunk) for the
+// chunk-entry states, then one for each chunk's T^T = ((I + L)^-1)^T, which the bf16
+// forward preparation kernel writes for the backward preparation kernel (the fp32
+// kernels leave the second half unused).
+inline size_t dw_state_bytes(int64_t BH, const DwGeom& g) { return 2 * dw_mat_bytes(BH, g); }
+inline float* dw_inv_slots(float* Hb, int64_t BH, const DwGeom& g) {
+  return Hb + (size_t)BH * g.nc * MAT;
+}
+inline const float* dw_inv_slots(const float* Hb, int64_t BH, const DwGeom& g) {
+  return Hb + (size_t)BH * g.nc * MAT;
+}
 
 // bf16-input entry points (delta_wy_bf16.hip).  Q, K, V, beta, y, dy and the
 // input gradients are bf16 (uint16_t storage); states and workspaces are fp32.

@@ -451,6 +451,15 @@ __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2
 // chains read their operands back with one 16-byte load per fragment and half,
 // and a wave's load covers 1 KB without gaps (the row-major form read 16 bytes
 // from each of 64 rows).
+// T^T = ((I + L)^-1)^T is upper triangular: of its 8-float row chunks (row, q) only
+// those with q >= row / 8 can be nonzero, 288 of 512.  They are kept packed, row by
+// row, in the first 9 KB of the chunk's matrix slot; this is the packed index of
+// chunk (row, q), q >= row / 8.
+__device__ __forceinline__ int tri_chunk(int row, int q) {
+  const int a = row >> 3;
+  return 8 * (8 * a - a * (a - 1) / 2) + (row & 7) * (8 - a) + (q - a);
+}
+
 // The wave's 16 x 32 accumulator block (rows 16 rb, columns 32 ch) into a split
 // workspace matrix in fragment order.  The block is exactly the A fragment
 // (rb, s = ch), so the wave puts it into its own block of an LDS pair `st`,
@@ -507,7 +516,8 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked),
 //   P = (Q K^T) * beta_col * read, M1 = (beta K)^T T, M2 = P T;
 //   A = -M1 K, B = M1 V, Qe = Q - M2 K, Pu = M2 V
-//   -> A, Qe (split bf16 pairs), B, Pu (fp32, fragment-major) in the workspace.
+//   -> A, Qe (split bf16 pairs), B, Pu (fp32, fragment-major) in the workspace, and
+//      T^T (fp32, row-major) to To for the backward.
 // (W = T K and U0 = T V never materialise: A = -K^T diag(beta) W = -M1 K, etc.)
 // LDS stays under 80 KB, so two workgroups share a CU.
 // GATED (per-token decay, decay tables in mg_delta.h): L and P are weighted by
@@ -524,7 +534,8 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
                                                     float* __restrict__ Ao, float* __restrict__ Bo,
                                                     float* __restrict__ Qeo,
                                                     float* __restrict__ Puo,
-                                                    float* __restrict__ vo, DwGeom g) {
+                                                    float* __restrict__ vo,
+                                                    float* __restrict__ To, DwGeom g) {
   __shared__ BMat sKt, sVt;                    // K^T, V^T as (col; m)
   __shared__ BMat sX[2];                       // K, Q; then P split; then M2 split
   __shared__ uint4 sLraw[(DN * LD + 3) / 4];   // L (fp32); then T^T split
@@ -620,6 +631,13 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = sT[(8 * q + e) * LD + row];
     put_split8(sTt, row, q, x);  // (m; m') = T[m'][m]
+    // T^T's nonzero chunks, packed, for the backward preparation kernel, which
+    // would otherwise form L and invert it again.
+    if (q >= row >> 3) {
+      float4* t = reinterpret_cast<float4*>(To + mat + 8 * tri_chunk(row, q));
+      t[0] = make_float4(x[0], x[1], x[2], x[3]);
+      t[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
   }
   __syncthreads();  // sT is free
   {
@@ -792,7 +810,7 @@ __device__ __forceinline__ void smm(floatx4 (&acc)[2], const FragOff& F, const u
 // ---------------------------------------------------------------------------
 // backward, preparation kernel: one workgroup per (chunk, head)
 // ---------------------------------------------------------------------------
-//   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked)
+//   T = (I + L)^-1, L = strict(K K^T) * beta_col: read as the forward formed it
 //   R = V - K Hc, U = T R, P = (Q K^T) * beta_col * read, D1 = P^T dy
 //   E = T^T diag(beta) K, G0 = T^T D1, QdY = Q^T dy
 //   -> U, G0 (fp32), E (split) for the gradients; A' (split), b' (fp32, fragment-major) for the
@@ -803,8 +821,8 @@ __device__ __forceinline__ void smm(floatx4 (&acc)[2], const FragOff& F, const u
 //
 // The products run in dependency order so that few 64 x 64 operands are live at
 // once, and LDS stays under 80 KB (two workgroups per CU):
-//   A  L (fp32), then T = (I + L)^-1 in place; the inverse's workspace and the
-//      gated span table sit in split regions that are still free;
+//   A  T^T (fp32) from the forward, written into LDS as T; the gated span table
+//      sits in a split region that is still free;
 //   B  Hc^T (split) -> R = V - K Hc, V read per element from memory -> R^T (split);
 //   C  U = T R;
 //   D  P = Q K^T with Q as register fragments -> P^T (split); Q^T dy; D1 = P^T dy;
@@ -817,14 +835,14 @@ template <bool GATED>
 __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     const u16* __restrict__ Q, const u16* __restrict__ K, const u16* __restrict__ V,
     const u16* __restrict__ beta, const float* __restrict__ lg, const u16* __restrict__ dy,
-    const float* __restrict__ Hb, float* __restrict__ Uo, float* __restrict__ Eo,
-    float* __restrict__ G0o, float* __restrict__ Apo, float* __restrict__ bpo,
-    float* __restrict__ vo, DwGeom g) {
+    const float* __restrict__ Hb, const float* __restrict__ Tin, float* __restrict__ Uo,
+    float* __restrict__ Eo, float* __restrict__ G0o, float* __restrict__ Apo,
+    float* __restrict__ bpo, float* __restrict__ vo, DwGeom g) {
   __shared__ BMat sK;        // K as (m; d), exact
   __shared__ BMat sQD[2];    // Q^T as (d; t), dy^T as (j; t), exact
   __shared__ BPair sR1;      // [gated span table] -> Hc^T -> P^T -> G0^T
-  __shared__ BPair sR2;      // inverse workspace -> R^T -> D1^T -> E^T
-  __shared__ float sT[DN * LD];  // L, then T (in place)
+  __shared__ BPair sR2;      // R^T -> D1^T -> E^T
+  __shared__ float sT[DN * LD];  // T, as the forward preparation kernel formed it
   __shared__ float sb[DN];
   __shared__ float sdec[GATED ? 5 * DN : 1];  // l, Lc, p, a beta, ptok
   float *sl = sdec, *sLc = sdec + DN, *sp = sdec + 2 * DN, *sab = sdec + 3 * DN,
@@ -860,10 +878,28 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     tq.load(Q + trow0 * g.dk, ch.Ct, g.dk, g.dk);
     td.load(dy + trow0 * g.dv, ch.Ct, g.dv, g.dv);
     th.load(Hb + mat, g.dk, g.dv);
+    // T^T row tr, columns 8 tc..8 tc + 7, written back transposed (row stride LD:
+    // the 64 lanes of a wave write 64 distinct banks).  The forward stores only the
+    // packed chunks that can be nonzero; the others read a zero vector.
+    const int tr = threadIdx.x >> 3, tc = threadIdx.x & 7;
+    const bool tnz = tc >= tr >> 3;
+    const float4* tsrc =
+        reinterpret_cast<const float4*>(Tin + mat + 8 * tri_chunk(tr, tnz ? tc : tr >> 3));
+    const float4 t0 = *(tnz ? tsrc : reinterpret_cast<const float4*>(&mg_zero16));
+    const float4 t1 = *(tnz ? tsrc + 1 : reinterpret_cast<const float4*>(&mg_zero16));
     const float bv = ldf_or0(beta, row0 + (threadIdx.x & (DN - 1)), (threadIdx.x & (DN - 1)) < ch.M);
     tk.put(sK);
     tq.put_t(sQt);
     td.put_t(sDyt);
+    float* tcol = sT + 8 * tc * LD + tr;
+    tcol[0] = t0.x;
+    tcol[LD] = t0.y;
+    tcol[2 * LD] = t0.z;
+    tcol[3 * LD] = t0.w;
+    tcol[4 * LD] = t1.x;
+    tcol[5 * LD] = t1.y;
+    tcol[6 * LD] = t1.z;
+    tcol[7 * LD] = t1.w;
     sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
     if constexpr (GATED) {
       const float lv = ld_l(lg, bh, g, ch);
@@ -871,10 +907,10 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     }
   }
   __syncthreads();
-  // ---- A: L, then T = (I + L)^-1 in place ----
-  // gated: the span weights at the wave's fragment positions, of L (micro-rows row, col:
-  // E[tau(row)][tau(col)]) and of P (token row, micro-row col: E[row][tau(col)]).
-  float ew[2][4], ewp[2][4];
+  // ---- A: T = (I + L)^-1 is in sT (formed by the forward preparation kernel) ----
+  // gated: the span weights of P at the wave's fragment positions (token row,
+  // micro-row col: E[row][tau(col)]).
+  float ewp[2][4];
   if constexpr (GATED) {
     float* sE = reinterpret_cast<float*>(&sR1);  // span table, row stride DN
     decay_tables<NTB, DN>(sl, sE);
@@ -886,27 +922,10 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = C0 + 16 * jj + r;
-        ew[jj][i] = col < row ? sE[(row / g.nh) * DN + col / g.nh] : 0.f;
         ewp[jj][i] = col < (row + 1) * g.nh ? sE[row * DN + col / g.nh] : 0.f;
       }
+    __syncthreads();  // the span table is read: Hc^T takes its region
   }
-  {
-    floatx4 kk[2];
-    zero2(kk);
-    bmm<false, false>(kk, F, &sK, &sK);  // K K^T
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int cj = C0 + 16 * jj;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = R0 + 4 * gg + i, col = cj + r;
-        kk[jj][i] = col < row ? kk[jj][i] * sb[col] * (GATED ? ew[jj][i] : 1.f) : 0.f;
-      }
-      acc_store_lds(kk[jj], sT + R0 * LD + cj, LD);
-    }
-  }
-  __syncthreads();  // L complete (and, gated, the span table read)
-  unit_lower_inverse(sT, sT, reinterpret_cast<float*>(&sR2));  // ends with a barrier
   // ---- B: R = V - K Hc (gated: V - diag(p) K Hc) -> R^T ----
   th.put_split_t(sR1);  // Hc^T as (j; d)
   __syncthreads();

@@ -64,7 +64,9 @@ def test_workspace_queries(lib):
     assert lib.mg_angle_scan_state_bytes(2, 257, 3, 4) == (17 + 3) * 6 * 16 * 4
     # delta: six padded 64 x 64 fp32 matrices per (batch, head, chunk)
     assert lib.mg_delta_workspace_bytes(8, 8, 8192, 1, 64, 64, 64) == 6 * 64 * 128 * 64 * 64 * 4
-    assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 64 * 128 * 64 * 64 * 4
+    # saved state: two padded matrices per (batch, head, chunk) -- the chunk-entry
+    # state and the chunk's inverse (I + L)^-1 kept for the backward
+    assert lib.mg_delta_state_bytes(8, 8, 8192, 1, 64, 64, 64) == 2 * 64 * 128 * 64 * 64 * 4
     # outside the envelope: the minimum / zero answer, never a crash
     assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 32, 1) == 256
     assert lib.mg_affine_scan_workspace_bytes(1, 8, 1, 16, 3) == 256
