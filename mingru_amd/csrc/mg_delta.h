@@ -327,10 +327,14 @@ __device__ __forceinline__ void build_L(const float* sK, const float* sb, float*
   mma_row4<64>(acc, sK + 16 * w * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
+    // The masked value is formed first and the mask picks a local: a conditional
+    // whose arm computes becomes a branch, with the LDS read of sb moved into it.
+    const float bc = sb[16 * J + r];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * w + 4 * g + i, col = 16 * J + r;
-      sL[row * LD + col] = col < row ? acc[J][i] * sb[col] : 0.f;
+      const float v = acc[J][i] * bc;
+      sL[row * LD + col] = col < row ? v : 0.f;
     }
   }
 }

@@ -605,17 +605,25 @@ __global__ __launch_bounds__(NTB) void dwb_fwd_prep(const u16* __restrict__ Q,
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
+      // Masked values are formed before the masks pick them, and each mask picks
+      // between a local and zero: a conditional whose arm computes (or reads LDS)
+      // becomes a branch, the LDS read is moved into it and waited for there, one
+      // read at a time.  Every index is in range.
+      const float bc = sb[cj + r];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
+        float kv, pv;
         if constexpr (GATED) {  // spans between the tokens of micro-rows (tau = m / nh)
           const int tc = col / g.nh;
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] * sE[(row / g.nh) * LD + tc] : 0.f;
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * sE[row * LD + tc] : 0.f;
+          kv = kk[jj][i] * bc * sE[(row / g.nh) * LD + tc];
+          pv = pp[jj][i] * bc * sE[row * LD + tc];
         } else {
-          kk[jj][i] = col < row ? kk[jj][i] * sb[col] : 0.f;
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+          kv = kk[jj][i] * bc;
+          pv = pp[jj][i] * bc;
         }
+        kk[jj][i] = col < row ? kv : 0.f;
+        pp[jj][i] = col < (row + 1) * g.nh ? pv : 0.f;
       }
       acc_store_lds(kk[jj], sL + R0 * LD + cj, LD);
     }
@@ -922,7 +930,8 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = C0 + 16 * jj + r;
-        ewp[jj][i] = col < (row + 1) * g.nh ? sE[row * DN + col / g.nh] : 0.f;
+        const float e = sE[row * DN + col / g.nh];  // read first, then picked
+        ewp[jj][i] = col < (row + 1) * g.nh ? e : 0.f;
       }
     __syncthreads();  // the span table is read: Hc^T takes its region
   }
@@ -964,13 +973,12 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
+      const float bc = sb[cj + r];  // masked value formed first, then picked
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = R0 + 4 * gg + i, col = cj + r;
-        if constexpr (GATED)
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] * ewp[jj][i] : 0.f;
-        else
-          pp[jj][i] = col < (row + 1) * g.nh ? pp[jj][i] * sb[col] : 0.f;
+        const float pv = GATED ? pp[jj][i] * bc * ewp[jj][i] : pp[jj][i] * bc;
+        pp[jj][i] = col < (row + 1) * g.nh ? pv : 0.f;
       }
       acc_put_t(sR1, pp[jj], R0, cj);  // P^T as (m; t)
     }
@@ -1199,19 +1207,26 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
+      // Masked values are formed before the masks pick them, and each mask picks
+      // between a local and zero: a conditional whose arm computes (or reads LDS)
+      // becomes a branch, the LDS read is moved into it and waited for there, one
+      // read at a time.  Every index is in range.
+      const float bm = sb[cj + r];
       floatx4 db;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = R0 + 4 * gg + i, m = cj + r;
         const bool rd = m < (t + 1) * g.nh;
         if constexpr (GATED) {
-          const float er = rd ? sEg[t * LD + m / g.nh] : 0.f;
-          ds2[jj][i] = dp2[jj][i] * sb[m] * er;
+          const float e = sEg[t * LD + m / g.nh];
+          const float er = rd ? e : 0.f;
+          ds2[jj][i] = dp2[jj][i] * bm * er;
           db[i] = dp2[jj][i] * s2[jj][i] * er;
-          f1[jj][i] = db[i] * sb[m];
+          f1[jj][i] = db[i] * bm;
         } else {
-          ds2[jj][i] = rd ? dp2[jj][i] * sb[m] : 0.f;
-          db[i] = rd ? dp2[jj][i] * s2[jj][i] : 0.f;
+          const float dv = dp2[jj][i] * bm, bv = dp2[jj][i] * s2[jj][i];
+          ds2[jj][i] = rd ? dv : 0.f;
+          db[i] = rd ? bv : 0.f;
         }
       }
       colsum16(db, sdb[F.rb], cj + r);
@@ -1228,19 +1243,27 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int cj = C0 + 16 * jj;
+      const float bj = sb[cj + r];  // masked values formed first, then picked
       floatx4 db;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = R0 + 4 * gg + i, j = cj + r;
+        const float bmi = sb[m];
         if constexpr (GATED) {
           const int tm = m / g.nh, tj = j / g.nh;
-          const float elo = j < m ? sEg[tm * LD + tj] : 0.f, ehi = m < j ? sEg[tj * LD + tm] : 0.f;
-          d2[jj][i] = j < m ? dt2[jj][i] * sb[j] * elo : dtt2[jj][i] * sb[m] * ehi;
+          const float e0 = sEg[tm * LD + tj], e1 = sEg[tj * LD + tm];
+          const float elo = j < m ? e0 : 0.f, ehi = m < j ? e1 : 0.f;
+          const float lo = dt2[jj][i] * bj * elo, hi = dtt2[jj][i] * bmi * ehi;
+          d2[jj][i] = j < m ? lo : hi;  // locals: a select
           db[i] = dt2[jj][i] * kk2[jj][i] * elo;
-          f2[jj][i] = db[i] * sb[j];
+          f2[jj][i] = db[i] * bj;
         } else {
-          d2[jj][i] = j < m ? dt2[jj][i] * sb[j] : (m < j ? dtt2[jj][i] * sb[m] : 0.f);
-          db[i] = j < m ? dt2[jj][i] * kk2[jj][i] : 0.f;
+          // Nested: the compiler keeps branches here (one LDS read waits in one), which
+          // costs less than the 10 spilled registers of the branch-free form.
+          const float lo = dt2[jj][i] * bj, hi = dtt2[jj][i] * bmi;
+          const float dd = dt2[jj][i] * kk2[jj][i];
+          d2[jj][i] = j < m ? lo : (m < j ? hi : 0.f);
+          db[i] = j < m ? dd : 0.f;
         }
       }
       colsum16(db, sdb[4 + F.rb], cj + r);
