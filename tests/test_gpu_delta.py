@@ -125,6 +125,31 @@ def test_delta_bf16_matches_oracle(cuda, case):
         assert err <= bar, f"{name} rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_delta_interleaved_calls(cuda, dtype):
+    """Two forwards before either backward (as two layers' forwards run before their
+    backwards): each backward must read its own forward's saved state -- the chunk-entry
+    states and, for bf16, the chunk inverses -- while the second forward and the first
+    backward have rewritten the shared workspace.  Bitwise equal to separate runs."""
+    B, H, T, nh, dk, dv, C = 2, 2, 200, 1, 64, 64, 64
+    print(f"[gpu] delta interleaved calls dtype={dtype}", flush=True)
+    xa = _inputs(B, H, T, nh, dk, dv, seed=31, dtype=dtype)
+    xb = _inputs(B, H, T, nh, dk, dv, seed=32, dtype=dtype)
+    ref = [_run(*x, C, cuda) for x in (xa, xb)]
+    leaves, outs = [], []
+    for x in (xa, xb):
+        ts = [t.to(cuda).requires_grad_(True) for t in x[:5]]
+        leaves.append(ts)
+        outs.append(hip_scans.delta_scan_impl(*ts, chunk_size=C))
+    for (y, HT), x in zip(outs[::-1], (xb, xa)):  # second call's backward first
+        torch.autograd.backward([y, HT], [x[5].to(cuda), x[6].to(cuda)])
+    torch.cuda.synchronize()
+    for (y, HT), ts, (ry, rHT, rg) in zip(outs, leaves, ref):
+        assert torch.equal(y, ry) and torch.equal(HT, rHT)
+        for g, rgk in zip((t.grad for t in ts), rg):
+            assert torch.equal(g, rgk)
+
+
 def test_delta_c5_full_size(cuda):
     """C5 (B=8, H=8, T=8192, d=64, chunk 64, bf16): two heads at full length vs the
     oracle, from the first and the second half of the 64 (batch, head) pairs."""

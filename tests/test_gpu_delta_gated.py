@@ -219,6 +219,33 @@ def test_delta_gated_bf16_matches_oracle(cuda, case):
         assert _rel(gk, gr) <= bar, f"{name} rel err {_rel(gk, gr):.3e}"
 
 
+@pytest.mark.parametrize("nh", [1, 2])
+def test_delta_gated_bf16_interleaved_calls(cuda, nh):
+    """Two gated bf16 forwards before either backward: each backward reads its own
+    forward's saved chunk states and chunk inverses while the shared workspace has been
+    rewritten in between.  Bitwise equal to separate runs."""
+    B, H, T, dk, dv, C = 2, 2, 150, 64, 64, 64 // nh
+    print(f"[gpu] delta gated bf16 interleaved calls nh={nh}", flush=True)
+    xs = []
+    for seed in (51, 52):
+        Q, K, V, beta, lg, H0, dy, dHT = _inputs(B, H, T, nh, dk, dv, seed=seed, lg_kind="mod")
+        Q, K, V, beta, dy = (t.to(torch.bfloat16) for t in (Q, K, V, beta, dy))
+        xs.append(((Q, K, V, beta, lg, H0), dy, dHT))
+    ref = [_run(ins, dy, dHT, C, cuda) for ins, dy, dHT in xs]
+    leaves, outs = [], []
+    for ins, _, _ in xs:
+        ts = [t.to(cuda).requires_grad_(True) for t in ins]
+        leaves.append(ts)
+        outs.append(hip_scans.delta_gated_scan_impl(*ts, chunk_size=C))
+    for (y, HT), (_, dy, dHT) in zip(outs[::-1], xs[::-1]):  # second call's backward first
+        torch.autograd.backward([y, HT], [dy.to(cuda), dHT.to(cuda)])
+    torch.cuda.synchronize()
+    for (y, HT), ts, (ry, rHT, rg) in zip(outs, leaves, ref):
+        assert torch.equal(y, ry) and torch.equal(HT, rHT)
+        for g, rgk in zip((t.grad for t in ts), rg):
+            assert torch.equal(g, rgk)
+
+
 def test_delta_gated_bf16_c5_heads(cuda):
     """The C5d workload in bf16 (B=8, H=8, T=8192, d=64, chunk 64): two heads at full
     length against the oracle, from the first and the second half of the 64 (batch,
