@@ -50,8 +50,10 @@ __device__ __forceinline__ void build_L_gated(const float* sK, const float* sb, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * w + 4 * g + i, col = 16 * J + r;
-      sL[row * LD + col] =
-          col < row ? acc[J][i] * sb[col] * sE[(row / nh) * LD + col / nh] : 0.f;
+      // formed first, then picked: a masked arm that reads LDS becomes a branch that
+      // waits for the read on its own
+      const float v = acc[J][i] * sb[col] * sE[(row / nh) * LD + col / nh];
+      sL[row * LD + col] = col < row ? v : 0.f;
     }
   }
 }
@@ -105,7 +107,8 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-        sp4[J][i] = (m < (t + 1) * g.nh) ? sp4[J][i] * sb[m] * sE[t * LD + m / g.nh] : 0.f;
+        const float v = sp4[J][i] * sb[m] * sE[t * LD + m / g.nh];  // formed first, then picked
+        sp4[J][i] = (m < (t + 1) * g.nh) ? v : 0.f;
       }
       acc_store_ws(sp4[J], Po + mat + 16 * w * DN + 16 * J);
     }
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_chain(const float* __restrict__ Q,
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 16 * w + 4 * gg + i;
-    h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
+    h[i] = ldf_or0(H0, (bh * g.dk + d) * g.dv + col, d < g.dk && col < g.dv);
   }
   Tile<float> tk, tq;
   float abv, pcv, wa[16], pa[16];
@@ -317,7 +320,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-        sp4[J][i] = (m < (t + 1) * g.nh) ? sp4[J][i] * sb[m] * sE[t * LD + m / g.nh] : 0.f;
+        const float v = sp4[J][i] * sb[m] * sE[t * LD + m / g.nh];  // formed first, then picked
+        sp4[J][i] = (m < (t + 1) * g.nh) ? v : 0.f;
       }
       acc_store_lds(sp4[J], sL + 16 * w * LD + 16 * J, LD);
     }
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_chain(const float* __restrict__ K,
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 16 * w + 4 * gg + i;
-    h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
+    h[i] = ldf_or0(dHT, (bh * g.dk + d) * g.dv + col, d < g.dk && col < g.dv);
   }
   Tile<float> tk;
   float ea[16], pv, pcv;
@@ -507,7 +511,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
         const bool rd = m < (t + 1) * g.nh;
-        const float er = rd ? sE[t * LD + m / g.nh] : 0.f;
+        const float e = sE[t * LD + m / g.nh];  // read first, then picked
+        const float er = rd ? e : 0.f;
         ds[i] = dp[i] * sb[m] * er;
         db[i] = dp[i] * s[i] * er;
         fr[i] = db[i] * sb[m];
@@ -588,7 +593,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 16 * w + 4 * gg + i, j = 16 * J + r;
-        const float em = j < m ? sE[(m / g.nh) * LD + j / g.nh] : 0.f;
+        const float e = sE[(m / g.nh) * LD + j / g.nh];  // read first, then picked
+        const float em = j < m ? e : 0.f;
         dkk[i] = dt[i] * sb[j] * em;
         db[i] = dt[i] * kk[i] * em;
         ft[i] = db[i] * sb[j];
@@ -627,7 +633,8 @@ __global__ __launch_bounds__(NT) void dg_bwd_grads(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 16 * w + 4 * gg + i;
-        sdb[8][m] = m < ch.M ? sE[(ch.Ct - 1) * LD + m / g.nh] * rowp[i] : 0.f;
+        const float v = sE[(ch.Ct - 1) * LD + m / g.nh] * rowp[i];  // formed first, then picked
+        sdb[8][m] = m < ch.M ? v : 0.f;
         sfv[2][m] = sab[m] * rowp[i];
       }
     }

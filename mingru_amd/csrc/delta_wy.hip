@@ -93,7 +93,8 @@ __global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, cons
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-        sp[J][i] = (m < (t + 1) * g.nh) ? sp[J][i] * sb[m] : 0.f;
+        const float v = sp[J][i] * sb[m];  // formed first: the mask then picks a local
+        sp[J][i] = (m < (t + 1) * g.nh) ? v : 0.f;
       }
       acc_store_ws(sp[J], Po + mat + 16 * w * DN + 16 * J);
     }
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(NT) void dw_fwd_chain(const TI* __restrict__ Q, con
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 16 * w + 4 * gg + i;
-    h[i] = (d < g.dk && col < g.dv) ? H0[(bh * g.dk + d) * g.dv + col] : 0.f;
+    h[i] = ldf_or0(H0, (bh * g.dk + d) * g.dv + col, d < g.dk && col < g.dv);
   }
   // Operands of chunk c + 1 are fetched into registers while chunk c computes.
   Tile<TI> tk, tq;
@@ -273,7 +274,8 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
-        sp[J][i] = (m < (t + 1) * g.nh) ? sp[J][i] * sb[m] : 0.f;
+        const float v = sp[J][i] * sb[m];  // formed first: the mask then picks a local
+        sp[J][i] = (m < (t + 1) * g.nh) ? v : 0.f;
       }
       acc_store_lds(sp[J], sL + 16 * w * LD + 16 * J, LD);
     }
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(NT) void dw_bwd_chain(const TI* __restrict__ K,
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 16 * w + 4 * gg + i;
-    h[i] = (d < g.dk && col < g.dv) ? dHT[(bh * g.dk + d) * g.dv + col] : 0.f;
+    h[i] = ldf_or0(dHT, (bh * g.dk + d) * g.dv + col, d < g.dk && col < g.dv);
   }
   Tile<TI> tk;
   float ea[16];
@@ -434,8 +436,9 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * w + 4 * gg + i, m = 16 * J + r;
       const bool rd = m < (t + 1) * g.nh;
-      ds[i] = rd ? dp[i] * sb[m] : 0.f;
-      db[i] = rd ? dp[i] * s[i] : 0.f;
+      const float dv = dp[i] * sb[m], bv = dp[i] * s[i];  // formed first, then picked
+      ds[i] = rd ? dv : 0.f;
+      db[i] = rd ? bv : 0.f;
     }
     acc_store_lds(ds, sX + 16 * w * LD + 16 * J, LD);
     put_colsum(db, sdb[w], 16 * J + r);
@@ -475,8 +478,9 @@ __global__ __launch_bounds__(NT) void dw_bwd_grads(
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * w + 4 * gg + i, j = 16 * J + r;
       const bool st = j < m;
-      dkk[i] = st ? dt[i] * sb[j] : 0.f;
-      db[i] = st ? dt[i] * kk[i] : 0.f;
+      const float kv = dt[i] * sb[j], bv = dt[i] * kk[i];  // formed first, then picked
+      dkk[i] = st ? kv : 0.f;
+      db[i] = st ? bv : 0.f;
     }
     acc_store_lds(dkk, sX + 16 * w * LD + 16 * J, LD);
     put_colsum(db, sdb[4 + w], 16 * J + r);
