@@ -68,7 +68,7 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
                                                   const float* __restrict__ lg,
                                                   float* __restrict__ Wo, float* __restrict__ U0o,
                                                   float* __restrict__ Po, float* __restrict__ vo,
-                                                  DwGeom g) {
+                                                  float* __restrict__ To, DwGeom g) {
   __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD], sE[DN * LD];
   __shared__ float sY[2 * 32 * LDS16];
   __shared__ float sb[DN], sl[DN], sLc[DN], sp[DN], sab[DN];
@@ -92,12 +92,13 @@ __global__ __launch_bounds__(NT) void dg_fwd_prep(const float* __restrict__ Q,
   __syncthreads();
   build_L_gated(sK, sb, sE, g.nh, sL);
   __syncthreads();
-  unit_lower_inverse(sL, sT, sY);
+  unit_lower_inverse(sL, sT, sY);  // ends with a barrier
   tq.store(sL);  // sL is free: Q goes there for P
   write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
+  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  store_inv_packed<NT>(To + mat, sT);  // for the backward preparation kernel
   __syncthreads();
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
-  const size_t mat = ((size_t)bh * g.nc + c) * MAT;
   {
     floatx4 sp4[4];
     zero_row4(sp4);
@@ -256,11 +257,11 @@ __global__ __launch_bounds__(NT) void dg_fwd_chain(const float* __restrict__ Q,
 __global__ __launch_bounds__(NT) void dg_bwd_prep(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ beta, const float* __restrict__ lg, const float* __restrict__ dy,
-    const float* __restrict__ Hb, float* __restrict__ Uo, float* __restrict__ Eo,
-    float* __restrict__ G0o, float* __restrict__ QdYo, float* __restrict__ vo, DwGeom g) {
+    const float* __restrict__ Hb, const float* __restrict__ Tin, float* __restrict__ Uo,
+    float* __restrict__ Eo, float* __restrict__ G0o, float* __restrict__ QdYo,
+    float* __restrict__ vo, DwGeom g) {
   __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD], sX[DN * LD];
   __shared__ float sQ[DN * LD], sD[DN * LD], sE[DN * LD];
-  __shared__ float sY[2 * 32 * LDS16];
   __shared__ float sb[DN], sl[DN], sLc[DN], sp[DN], sab[DN], spt[DN];
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
@@ -283,12 +284,11 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
     td.store(sD);
     sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
     sl[threadIdx.x & (DN - 1)] = lv;
+    load_inv_packed<NT>(sT, Tin + mat);  // T = (I + L)^-1 as the forward formed it
   }
   __syncthreads();
   decay_tables<NT>(sl, sE);
   decay_vectors(sl, sb, ch, g.nh, sLc, sp, sab, spt);
-  __syncthreads();
-  build_L_gated(sK, sb, sE, g.nh, sL);
   __syncthreads();
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   // R = V - diag(p) K Hc in place in sV (tile (w, J) read and written by wave w only).
@@ -306,8 +306,7 @@ __global__ __launch_bounds__(NT) void dg_bwd_prep(
   }
   write_vectors(vo + ((size_t)bh * g.nc + c) * VECN, sLc, sp, sab, ch);
   __syncthreads();
-  unit_lower_inverse(sL, sT, sY);
-  // U = Tm^-1 R; P = (Q K^T) * beta_col * E_read into sL (free now).
+  // U = Tm^-1 R; P = (Q K^T) * beta_col * E_read into sL (free).
   {
     floatx4 u[4], sp4[4];
     zero_row4(u);
@@ -801,7 +800,7 @@ int mg_delta_gated_fwd(const void* Q, const void* K, const void* V, const void* 
   const float *q = (const float*)Q, *k = (const float*)K, *v = (const float*)V,
               *b = (const float*)beta;
   hipLaunchKernelGGL(dg_fwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, q, k, v, b,
-                     log_gamma, Wm, U0m, Pm, vm, g);
+                     log_gamma, Wm, U0m, Pm, vm, dw_inv_slots(Hbound, BH, g), g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dg_fwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, q, k, H0, Wm,
                      U0m, Pm, vm, (float*)y, HT, Hbound, g, BH);
@@ -838,7 +837,7 @@ int mg_delta_gated_bwd(const void* Q, const void* K, const void* V, const void* 
   const float *q = (const float*)Q, *k = (const float*)K, *v = (const float*)V,
               *b = (const float*)beta, *d = (const float*)dy;
   hipLaunchKernelGGL(dg_bwd_prep, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream, q, k, v, b,
-                     log_gamma, d, Hbound, Um, Em, G0m, QdYm, vm, g);
+                     log_gamma, d, Hbound, dw_inv_slots(Hbound, BH, g), Um, Em, G0m, QdYm, vm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dg_bwd_chain, dim3(chain_grid(BH, g)), dim3(NT), 0, stream, k, dHT, Em, G0m,
                      QdYm, vm, Gm, dHn, dH0, g, BH);

@@ -47,7 +47,8 @@ template <typename TI>
 __global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, const TI* __restrict__ K,
                                                   const TI* __restrict__ V, const TI* __restrict__ beta,
                                                   float* __restrict__ Wo, float* __restrict__ U0o,
-                                                  float* __restrict__ Po, DwGeom g) {
+                                                  float* __restrict__ Po, float* __restrict__ To,
+                                                  DwGeom g) {
   __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD];
   __shared__ float sY[2 * 32 * LDS16];
   __shared__ float sb[DN];
@@ -66,11 +67,12 @@ __global__ __launch_bounds__(NT) void dw_fwd_prep(const TI* __restrict__ Q, cons
   __syncthreads();
   build_L(sK, sb, sL);
   __syncthreads();
-  unit_lower_inverse(sL, sT, sY);
+  unit_lower_inverse(sL, sT, sY);  // ends with a barrier
   // sL is free: Q goes there for P.
   tq.store(sL);
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   const size_t mat = ((size_t)bh * g.nc + c) * MAT;
+  store_inv_packed<NT>(To + mat, sT);  // for the backward preparation kernel
   {
     floatx4 wa[4], ua[4];
     zero_row4(wa);
@@ -219,12 +221,12 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
                                                   const TI* __restrict__ V, const TI* __restrict__ beta,
                                                   const TI* __restrict__ dy,
                                                   const float* __restrict__ Hb,
+                                                  const float* __restrict__ Tin,
                                                   float* __restrict__ Uo, float* __restrict__ Eo,
                                                   float* __restrict__ G0o, float* __restrict__ QdYo,
                                                   DwGeom g) {
   __shared__ float sK[DN * LD], sV[DN * LD], sL[DN * LD], sT[DN * LD], sX[DN * LD];
   __shared__ float sQ[DN * LD], sD[DN * LD];
-  __shared__ float sY[2 * 32 * LDS16];
   __shared__ float sb[DN];
   const int c = blockIdx.x;
   const int64_t bh = blockIdx.y;
@@ -246,9 +248,9 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
     tq.store(sQ);
     td.store(sD);
     sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
+    load_inv_packed<NT>(sT, Tin + mat);  // T = (I + L)^-1 as the forward formed it
   }
   __syncthreads();
-  build_L(sK, sb, sL);
   const int w = wave_id(), lane = lane_id(), r = lane & 15, gg = lane >> 4;
   // R = V - K Hc in place in sV (tile (w, J) read and written by wave w only).
   {
@@ -260,8 +262,7 @@ __global__ __launch_bounds__(NT) void dw_bwd_prep(const TI* __restrict__ Q, cons
     for (int J = 0; J < 4; ++J) acc_store_lds(acc[J], sV + 16 * w * LD + 16 * J, LD);
   }
   __syncthreads();
-  unit_lower_inverse(sL, sT, sY);
-  // U = Tm^-1 R; P = (Q K^T) * beta_col * read into sL (free now).
+  // U = Tm^-1 R; P = (Q K^T) * beta_col * read into sL (free).
   {
     floatx4 u[4], sp[4];
     zero_row4(u);
@@ -541,7 +542,8 @@ int dw_fwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* U0m = (float*)((char*)ws + mb);
   float* Pm = (float*)((char*)ws + 2 * mb);
   hipLaunchKernelGGL(dw_fwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
-                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm, g);
+                     (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, Wm, U0m, Pm,
+                     dw_inv_slots(Hb, BH, g), g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dw_fwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)beta, H0, Wm, U0m, Pm, (TI*)y, HT, Hb,
@@ -564,7 +566,7 @@ int dw_bwd(const void* Q, const void* K, const void* V, const void* beta, const 
   float* dHn = (float*)((char*)ws + 5 * mb);
   hipLaunchKernelGGL(dw_bwd_prep<TI>, dim3(g.nc, (unsigned)BH), dim3(NT), 0, stream,
                      (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)beta, (const TI*)dy, Hb,
-                     Um, Em, G0m, QdYm, g);
+                     dw_inv_slots(Hb, BH, g), Um, Em, G0m, QdYm, g);
   if (hipGetLastError() != hipSuccess) return MG_ERR_LAUNCH;
   hipLaunchKernelGGL(dw_bwd_chain<TI>, dim3(chain_grid(BH, g)), dim3(NT), 0, stream,
                      (const TI*)K, dHT, Em, G0m, QdYm, Gm, dHn, dH0, g, BH);

@@ -319,6 +319,55 @@ __device__ __forceinline__ void unit_lower_inverse(const float* sL, float* sT, f
   __syncthreads();
 }
 
+// T^T = ((I + L)^-1)^T is upper triangular: of its 8-float row chunks (row, q) only
+// those with q >= row / 8 can be nonzero, 288 of 512.  They are kept packed, row by
+// row, in the first 9 KB of the chunk's matrix slot; this is the packed index of
+// chunk (row, q), q >= row / 8.
+__device__ __forceinline__ int tri_chunk(int row, int q) {
+  const int a = row >> 3;
+  return 8 * (8 * a - a * (a - 1) / 2) + (row & 7) * (8 - a) + (q - a);
+}
+
+// T^T's possibly nonzero chunks from the fp32 T in LDS (row stride LD) to a packed slot,
+// and back into LDS as T with the zero chunks filled in (NTH threads, each taking chunks
+// i = tid, tid + NTH, ... of the 512 (row, q)).  The fp32 kernels' backward preparation
+// reads the inverse its forward formed instead of forming L and inverting it again.
+template <int NTH>
+__device__ __forceinline__ void store_inv_packed(float* To, const float* sT) {
+#pragma unroll
+  for (int i = threadIdx.x; i < DN * 8; i += NTH) {
+    const int row = i >> 3, q = i & 7;
+    if (q >= row >> 3) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sT[(8 * q + e) * LD + row];
+      float4* t = reinterpret_cast<float4*>(To + 8 * tri_chunk(row, q));
+      t[0] = make_float4(x[0], x[1], x[2], x[3]);
+      t[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
+  }
+}
+template <int NTH>
+__device__ __forceinline__ void load_inv_packed(float* sT, const float* Tin) {
+#pragma unroll
+  for (int i = threadIdx.x; i < DN * 8; i += NTH) {
+    const int row = i >> 3, q = i & 7;
+    const bool nz = q >= row >> 3;  // zero chunks read a zero vector (no branch)
+    const float4* src = reinterpret_cast<const float4*>(Tin + 8 * tri_chunk(row, nz ? q : row >> 3));
+    const float4 a = *(nz ? src : reinterpret_cast<const float4*>(&mg_zero16));
+    const float4 b = *(nz ? src + 1 : reinterpret_cast<const float4*>(&mg_zero16));
+    float* col = sT + 8 * q * LD + row;
+    col[0] = a.x;
+    col[LD] = a.y;
+    col[2 * LD] = a.z;
+    col[3 * LD] = a.w;
+    col[4 * LD] = b.x;
+    col[5 * LD] = b.y;
+    col[6 * LD] = b.z;
+    col[7 * LD] = b.w;
+  }
+}
+
 // L = strict_lower(K K^T) * beta_col into sL; wave w builds block-row w.
 __device__ __forceinline__ void build_L(const float* sK, const float* sb, float* sL) {
   const int w = wave_id(), lane = lane_id(), r = lane & 15, g = lane >> 4;
@@ -441,9 +490,8 @@ inline bool dw_geom(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int
 
 inline size_t dw_mat_bytes(int64_t BH, const DwGeom& g) { return (size_t)BH * g.nc * MAT * sizeof(float); }
 // The saved state buffer (Hbound): one padded matrix slot per (head, chunk) for the
-// chunk-entry states, then one for each chunk's T^T = ((I + L)^-1)^T, which the bf16
-// forward preparation kernel writes for the backward preparation kernel (the fp32
-// kernels leave the second half unused).
+// chunk-entry states, then one for each chunk's T^T = ((I + L)^-1)^T, which the forward
+// preparation kernels write (packed, tri_chunk) for the backward preparation kernels.
 inline size_t dw_state_bytes(int64_t BH, const DwGeom& g) { return 2 * dw_mat_bytes(BH, g); }
 inline float* dw_inv_slots(float* Hb, int64_t BH, const DwGeom& g) {
   return Hb + (size_t)BH * g.nc * MAT;

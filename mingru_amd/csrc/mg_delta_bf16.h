@@ -451,15 +451,6 @@ __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2
 // chains read their operands back with one 16-byte load per fragment and half,
 // and a wave's load covers 1 KB without gaps (the row-major form read 16 bytes
 // from each of 64 rows).
-// T^T = ((I + L)^-1)^T is upper triangular: of its 8-float row chunks (row, q) only
-// those with q >= row / 8 can be nonzero, 288 of 512.  They are kept packed, row by
-// row, in the first 9 KB of the chunk's matrix slot; this is the packed index of
-// chunk (row, q), q >= row / 8.
-__device__ __forceinline__ int tri_chunk(int row, int q) {
-  const int a = row >> 3;
-  return 8 * (8 * a - a * (a - 1) / 2) + (row & 7) * (8 - a) + (q - a);
-}
-
 // The wave's 16 x 32 accumulator block (rows 16 rb, columns 32 ch) into a split
 // workspace matrix in fragment order.  The block is exactly the A fragment
 // (rb, s = ch), so the wave puts it into its own block of an LDS pair `st`,
