@@ -274,10 +274,10 @@ int mg_angle_scan_tables_bwd(const float* theta, const float* scale, const float
  * y (B,H,T,dv), all of element type `dtype` (0 = fp32, 1 = bf16);
  * H0 / HT / dHT / dH0 (B,H,dk,dv) fp32.  Envelope: 1 <= dk, dv <= 64,
  * chunk >= 1, nh * chunk <= 64.
- * `Hbound` (mg_delta_state_bytes) receives the chunk-entry states and, for bf16,
- * each chunk's inverse (I + L)^-1 in a layout private to the library (it differs
- * between dtypes) and is read back only by mg_delta_bwd with the same shape and
- * dtype; `ws` needs mg_delta_workspace_bytes. */
+ * `Hbound` (mg_delta_state_bytes) receives the chunk-entry states and each chunk's
+ * inverse (I + L)^-1 in a layout private to the library (it differs between dtypes)
+ * and is read back only by mg_delta_bwd with the same shape and dtype; `ws` needs
+ * mg_delta_workspace_bytes. */
 size_t mg_delta_workspace_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv,
                                 int chunk);
 size_t mg_delta_state_bytes(int64_t B, int64_t H, int64_t T, int nh, int dk, int dv, int chunk);
