@@ -451,9 +451,10 @@ __device__ __forceinline__ void store_block_split(u16* dst, const floatx4 (&v)[2
 // chains read their operands back with one 16-byte load per fragment and half,
 // and a wave's load covers 1 KB without gaps (the row-major form read 16 bytes
 // from each of 64 rows).
-// The wave's 16 x 32 accumulator block (rows 16 rb, columns 32 ch) into a split
-// workspace matrix in fragment order.  The block is exactly the A fragment
-// (rb, s = ch), so the wave puts it into its own block of an LDS pair `st`,
+//
+// store_block_splitfrag writes the wave's 16 x 32 accumulator block (rows 16 rb,
+// columns 32 ch) in that order.  The block is exactly the A fragment (rb, s = ch),
+// so the wave puts it into its own block of an LDS pair `st`,
 // reads back each lane's eight hi and eight lo values and stores each with one
 // 16-byte write (writing the accumulator's values one by one to their fragment
 // slots made the forward preparation kernel 15 us slower at C5).  Only this wave
@@ -507,8 +508,9 @@ __device__ __forceinline__ void stage_split(BPair& m, BPair& mt, BPair& mts, con
 //   L = strict(K K^T) * beta_col, T = (I + L)^-1 (fp32, blocked),
 //   P = (Q K^T) * beta_col * read, M1 = (beta K)^T T, M2 = P T;
 //   A = -M1 K, B = M1 V, Qe = Q - M2 K, Pu = M2 V
-//   -> A, Qe (split bf16 pairs), B, Pu (fp32, fragment-major) in the workspace, and
-//      T^T (fp32, row-major) to To for the backward.
+//   -> A, Qe (split bf16 pairs, A-fragment order), B, Pu (fp32, fragment-major) in the
+//      workspace, and T^T's nonzero row chunks (fp32, packed: tri_chunk) to To for the
+//      backward.
 // (W = T K and U0 = T V never materialise: A = -K^T diag(beta) W = -M1 K, etc.)
 // LDS stays under 80 KB, so two workgroups share a CU.
 // GATED (per-token decay, decay tables in mg_delta.h): L and P are weighted by
