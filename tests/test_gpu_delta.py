@@ -150,6 +150,66 @@ def test_delta_interleaved_calls(cuda, dtype):
             assert torch.equal(g, rgk)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("gated", [False, True])
+def test_delta_c_abi_buffers_stay_in_bounds(cuda, dtype, gated):
+    """Through the C ABI with buffers of exactly the reported sizes plus a canary tail:
+    the saved state (chunk-entry states and the packed chunk inverses) and the workspace
+    are written only inside mg_delta_state_bytes / the workspace size, and the results
+    equal the autograd wrapper's bitwise.  Ragged last chunk (T = 130, chunk 64)."""
+    import ctypes
+
+    from mingru_amd import _native
+
+    B, H, T, nh, dk, dv, C = 1, 2, 130, 1, 64, 64, 64
+    print(f"[gpu] delta C ABI buffer bounds dtype={dtype} gated={gated}", flush=True)
+    lib = _native.load()
+    Q, K, V, beta, H0, dy, dHT = (t.to(cuda).contiguous()
+                                  for t in _inputs(B, H, T, nh, dk, dv, seed=61, dtype=dtype))
+    lg = (-0.5 * torch.rand(B, H, T, generator=torch.Generator().manual_seed(62))).to(cuda)
+    tag = 1 if dtype == torch.bfloat16 else 0
+    dims = (B, H, T, nh, dk, dv, C)
+    canary = 4096  # floats after each buffer
+    pattern = 1234.5
+    nstate = lib.mg_delta_state_bytes(*dims) // 4
+    wsb = (lib.mg_delta_gated_workspace_bytes if gated else lib.mg_delta_workspace_bytes)(*dims)
+    Hb = torch.full((nstate + canary,), pattern, device=cuda)
+    ws = torch.full((wsb // 4 + canary,), pattern, device=cuda)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    y = torch.empty(B, H, T, dv, dtype=dtype, device=cuda)
+    HT = torch.empty(B, H, dk, dv, device=cuda)
+    dQ, dK, dV, dbeta = (torch.empty_like(t) for t in (Q, K, V, beta))
+    dH0 = torch.empty_like(H0)
+    if gated:
+        dlg = torch.empty_like(lg)
+        assert lib.mg_delta_gated_fwd(p(Q), p(K), p(V), p(beta), p(lg), p(H0), p(y), p(HT), p(Hb),
+                                      *dims, tag, p(ws), wsb, stream) == 0
+        assert lib.mg_delta_gated_bwd(p(Q), p(K), p(V), p(beta), p(lg), p(Hb), p(dy), p(dHT),
+                                      p(dQ), p(dK), p(dV), p(dbeta), p(dlg), p(dH0), *dims, tag,
+                                      p(ws), wsb, stream) == 0
+    else:
+        assert lib.mg_delta_fwd(p(Q), p(K), p(V), p(beta), p(H0), p(y), p(HT), p(Hb), *dims, tag,
+                                p(ws), wsb, stream) == 0
+        assert lib.mg_delta_bwd(p(Q), p(K), p(V), p(beta), p(Hb), p(dy), p(dHT), p(dQ), p(dK),
+                                p(dV), p(dbeta), p(dH0), *dims, tag, p(ws), wsb, stream) == 0
+    torch.cuda.synchronize()
+    assert bool((Hb[nstate:] == pattern).all()), "saved state written past mg_delta_state_bytes"
+    assert bool((ws[wsb // 4:] == pattern).all()), "workspace written past its size"
+    ts = [t.clone().requires_grad_(True) for t in ((Q, K, V, beta, lg, H0) if gated
+                                                   else (Q, K, V, beta, H0))]
+    if gated:
+        ry, rHT = hip_scans.delta_gated_scan_impl(*ts, chunk_size=C)
+    else:
+        ry, rHT = hip_scans.delta_scan_impl(*ts, chunk_size=C)
+    torch.autograd.backward([ry, rHT], [dy, dHT])
+    torch.cuda.synchronize()
+    assert torch.equal(y, ry) and torch.equal(HT, rHT)
+    mine = (dQ, dK, dV, dbeta, dlg, dH0) if gated else (dQ, dK, dV, dbeta, dH0)
+    for g, t in zip(mine, ts):
+        assert torch.equal(g, t.grad)
+
+
 def test_delta_c5_full_size(cuda):
     """C5 (B=8, H=8, T=8192, d=64, chunk 64, bf16): two heads at full length vs the
     oracle, from the first and the second half of the 64 (batch, head) pairs."""
