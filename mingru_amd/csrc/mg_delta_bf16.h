@@ -1100,8 +1100,14 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
     const float* __restrict__ G0m, u16* __restrict__ dQ, u16* __restrict__ dK,
     u16* __restrict__ dV, u16* __restrict__ dbeta, float* __restrict__ dlg, DwGeom g) {
   __shared__ BMat sK, sKt, sQt;  // exact inputs
-  // Split regions: [E, dHn^T] -> [G, U, Hc] -> [dS, U, dS^T] -> [D2, U, dHn].
-  __shared__ BPair sR[3];
+  // Split regions: [E, dHn^T] -> [G, U, Hc] -> [dS, U, dS^T] -> [D2, U, dHn].  The gated
+  // form runs one workgroup per CU anyway (registers), so it takes three more regions and
+  // no result overwrites an operand that other waves may still read: regions
+  // 0, 1 = E, dHn^T -> dS, dS^T and 3, 4, 5 = G, U, Hc -> D2, U, dHn, which drops the
+  // three barriers that only waited for those reads.
+  __shared__ BPair sR[GATED ? 6 : 3];
+  constexpr int RG = GATED ? 3 : 0, RU = GATED ? 4 : 1, RH = GATED ? 5 : 2;
+  constexpr int RDS = 0, RDST = GATED ? 1 : 2, RD2 = RG, RDHN = RH;
   __shared__ float sb[DN];
   // dbeta partials: [0..3] read-term column sums per row block, [4..7] strict-term
   // column sums per row block, [8..9] row sums of K * (U dHn^T) per column half.
@@ -1176,17 +1182,17 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       part = mg_group_sum<64>(part);
       if (lane == 0) sred[wave_id()] = part;
     }
-    __syncthreads();
-    acc_put(sR[0], gacc[0], R0, C0);  // G as (m; j)
-    acc_put(sR[0], gacc[1], R0, C0 + 16);
-    tu.put_split(sR[1]);              // U as (m; j)
-    th.put_split(sR[2]);              // Hc as (d; j)
+    if constexpr (!GATED) __syncthreads();  // E and dHn^T are read
+    acc_put(sR[RG], gacc[0], R0, C0);  // G as (m; j)
+    acc_put(sR[RG], gacc[1], R0, C0 + 16);
+    tu.put_split(sR[RU]);              // U as (m; j)
+    th.put_split(sR[RH]);              // Hc as (d; j)
   }
   uint4 qf[2], yf[2];  // Q and dy fragments of the wave's rows t
   load_in_frag(qf, Q + trow0 * g.dk, g.dk, R0 + r, ch.Ct, g.dk);
   load_in_frag(yf, dy + trow0 * g.dv, g.dv, R0 + r, ch.Ct, g.dv);
   __syncthreads();
-  BPair &sG = sR[0], &sU = sR[1], &sHc = sR[2];
+  BPair &sG = sR[RG], &sU = sR[RU], &sHc = sR[RH];
   floatx4 ds2[2], d2[2], dq[2], dk[2];
   // gated: span gradients at the wave's positions: f1 of the (token t, micro-row m)
   // products, f2 of the (micro-row m, micro-row j) ones.
@@ -1297,27 +1303,27 @@ __global__ __launch_bounds__(NTB, GATED ? 2 : 4) void dwb_bwd_grads(
       }
     }
   }
-  __syncthreads();  // G and Hc are free
-  acc_put(sR[0], ds2[0], R0, C0);  // dS as (t; m)
-  acc_put(sR[0], ds2[1], R0, C0 + 16);
-  acc_put_t(sR[2], ds2[0], R0, C0);  // dS^T as (m; t)
-  acc_put_t(sR[2], ds2[1], R0, C0 + 16);
+  if constexpr (!GATED) __syncthreads();  // G and Hc are free
+  acc_put(sR[RDS], ds2[0], R0, C0);  // dS as (t; m)
+  acc_put(sR[RDS], ds2[1], R0, C0 + 16);
+  acc_put_t(sR[RDST], ds2[0], R0, C0);  // dS^T as (m; t)
+  acc_put_t(sR[RDST], ds2[1], R0, C0 + 16);
   __syncthreads();
   FTile tn;  // dHn again (an L2 hit), fetched while the dS products run
   tn.load(dHn + mat, g.dk, g.dv);
-  bmm<true, false>(dq, F, sR[0], &sKt);  // + dS K
-  bmm<true, false>(dk, F, sR[2], &sQt);  // + dS^T Q
+  bmm<true, false>(dq, F, sR[RDS], &sKt);  // + dS K
+  bmm<true, false>(dk, F, sR[RDST], &sQt);  // + dS^T Q
   store_block_bf16(dQ + trow0 * g.dk, g.dk, dq, R0, C0, ch.Ct, g.dk);
-  __syncthreads();  // dS and dS^T are free
-  acc_put_t(sR[0], d2[0], R0, C0);  // D2 (symmetric)
-  acc_put_t(sR[0], d2[1], R0, C0 + 16);
-  tn.put_split(sR[2]);  // dHn as (d; j)
+  if constexpr (!GATED) __syncthreads();  // dS and dS^T are free
+  acc_put_t(sR[RD2], d2[0], R0, C0);  // D2 (symmetric)
+  acc_put_t(sR[RD2], d2[1], R0, C0 + 16);
+  tn.put_split(sR[RDHN]);  // dHn as (d; j)
   __syncthreads();
   {
     floatx4 bu2[2];
     zero2(bu2);
-    bmm<true, false>(dk, F, sR[0], &sKt);  // + D2 K
-    bmm<true, true>(bu2, F, sU, sR[2]);    // U dHn^T
+    bmm<true, false>(dk, F, sR[RD2], &sKt);  // + D2 K
+    bmm<true, true>(bu2, F, sU, sR[RDHN]);   // U dHn^T
     float rowp[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
