@@ -902,6 +902,7 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     tcol[6 * LD] = t1.z;
     tcol[7 * LD] = t1.w;
     sb[threadIdx.x & (DN - 1)] = bv;  // every wave stores the same values (no branch)
+    if constexpr (!GATED) th.put_split_t(sR1);  // Hc^T as (j; d): sR1 is free from the start
     if constexpr (GATED) {
       const float lv = ld_l(lg, bh, g, ch);
       sl[threadIdx.x & (DN - 1)] = lv;
@@ -929,8 +930,10 @@ __global__ __launch_bounds__(NTB) void dwb_bwd_prep(
     __syncthreads();  // the span table is read: Hc^T takes its region
   }
   // ---- B: R = V - K Hc (gated: V - diag(p) K Hc) -> R^T ----
-  th.put_split_t(sR1);  // Hc^T as (j; d)
-  __syncthreads();
+  if constexpr (GATED) {  // the span table held sR1 until now
+    th.put_split_t(sR1);  // Hc^T as (j; d)
+    __syncthreads();
+  }
   {
     floatx4 rr[2];
     zero2(rr);
